@@ -1,0 +1,369 @@
+"""ctypes access to the CPU checker (liboracle.so) and the compiled reference
+(oracle/_ref/libref_*.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py.  The product package never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int)
+
+
+class OrQMat(C.Structure):
+    _fields_ = [("fmt", C.c_int), ("O", C.c_int), ("I", C.c_int), ("gs", C.c_int),
+                ("rb", C.c_int), ("ng", C.c_int), ("f", f32p), ("s", f32p),
+                ("q", C.c_void_p)]
+
+
+class OrLayer(C.Structure):
+    _fields_ = [("H", C.c_int), ("E", C.c_int), ("K", C.c_int), ("I", C.c_int),
+                ("I_sh", C.c_int), ("router", OrQMat), ("shared_gate", OrQMat),
+                ("shared_up", OrQMat), ("shared_down", OrQMat),
+                ("shared_scale", OrQMat), ("gate", C.POINTER(OrQMat)),
+                ("up", C.POINTER(OrQMat)), ("down", C.POINTER(OrQMat))]
+
+
+class OrTrace(C.Structure):
+    _fields_ = [("logits", f32p), ("idx", i32p), ("weight", f32p),
+                ("shared", f32p), ("sgate", f32p)]
+
+
+def ptr(a: np.ndarray | None, typ=C.c_void_p):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return C.cast(a.ctypes.data, typ)
+
+
+def build(ref: bool = False) -> None:
+    """Compile liboracle.so (and _ref when the reference tree is present)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    if ref and os.path.isdir("/root/reference/c"):
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+def _declare(lib, prefix: str):
+    P = prefix
+    for name, res, args in [
+        ("dot_q8f", C.c_float, [C.c_void_p, f32p, C.c_int]),
+        ("qrow_i8", C.c_float, [f32p, C.c_void_p, C.c_int]),
+        ("dot_i8i8", C.c_int32, [C.c_void_p, C.c_void_p, C.c_int]),
+        ("dot_q4_group", C.c_float, [C.c_void_p, f32p, C.c_int]),
+        ("dot_q3_group", C.c_float, [C.c_void_p, f32p, C.c_int]),
+        ("expf", C.c_float, [C.c_float]),
+        ("siluf", C.c_float, [C.c_float]),
+        ("qmat_mul", None, [f32p, f32p, C.POINTER(OrQMat), C.c_int]),
+        ("qmat_mul_batch", None, [f32p, f32p, C.c_int, C.c_int, C.POINTER(OrQMat), C.c_int]),
+        ("router_topk", None, [f32p, C.c_int, C.c_int, i32p, f32p]),
+        ("mlp_one", None, [f32p, f32p, C.POINTER(OrQMat), C.POINTER(OrQMat),
+                            C.POINTER(OrQMat), C.c_int]),
+    ]:
+        fn = getattr(lib, P + name)
+        fn.restype = res
+        fn.argtypes = args
+    dotname = "ref_dot" if P == "ref_" else "or_dot_f32"
+    getattr(lib, dotname).restype = C.c_float
+    getattr(lib, dotname).argtypes = [f32p, f32p, C.c_int]
+
+
+class Oracle:
+    """The restatement (liboracle.so)."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build()
+        self.lib = C.CDLL(path)
+        L = self.lib
+        _declare(L, "or_")
+        L.or_sigmoidf.restype = C.c_float
+        L.or_sigmoidf.argtypes = [C.c_float]
+        L.or_q3_value.restype = C.c_int
+        L.or_q3_value.argtypes = [C.c_void_p, C.c_int]
+        L.or_qmat_dot_row.restype = C.c_float
+        L.or_qmat_dot_row.argtypes = [C.POINTER(OrQMat), C.c_int, f32p]
+        L.or_mlp_batch.restype = None
+        L.or_mlp_batch.argtypes = [f32p, f32p, C.c_int, C.c_int, C.POINTER(OrQMat),
+                                   C.POINTER(OrQMat), C.POINTER(OrQMat), C.c_int]
+        L.or_moe_forward.restype = None
+        L.or_moe_forward.argtypes = [C.POINTER(OrLayer), f32p, f32p, C.POINTER(OrTrace)]
+        L.or_moe_prefill_grouped.restype = None
+        L.or_moe_prefill_grouped.argtypes = [C.POINTER(OrLayer), f32p, C.c_int, f32p,
+                                             C.POINTER(OrTrace)]
+        L.or_bucket.restype = C.c_int
+        L.or_bucket.argtypes = [i32p, C.c_int, C.c_int, C.c_int, i32p, i32p, i32p]
+        L.or_synth_router.restype = None
+        L.or_synth_router.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, f32p, f32p]
+        L.or_synth_shared_q8.restype = None
+        L.or_synth_shared_q8.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int,
+                                         C.c_void_p, f32p, C.c_void_p, f32p,
+                                         C.c_void_p, f32p]
+        L.or_synth_expert.restype = None
+        L.or_synth_expert.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.c_int, C.c_void_p, f32p, C.c_void_p,
+                                      f32p, C.c_void_p, f32p]
+        L.or_synth_x.restype = None
+        L.or_synth_x.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, f32p]
+        L.or_synth_bytes.restype = None
+        L.or_synth_bytes.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int,
+                                     C.c_void_p, C.c_uint64]
+        L.or_set_threads.restype = None
+        L.or_set_threads.argtypes = [C.c_int]
+        L.or_get_threads.restype = C.c_int
+        L.or_get_threads.argtypes = []
+
+    # -- building blocks ------------------------------------------------------
+    def dot(self, a, b):
+        return self.lib.or_dot_f32(ptr(a, f32p), ptr(b, f32p), a.size)
+
+    def router_topk(self, logit: np.ndarray, K: int):
+        idx = np.zeros(K, np.int32)
+        w = np.zeros(K, np.float32)
+        self.lib.or_router_topk(ptr(logit, f32p), logit.size, K, ptr(idx, i32p), ptr(w, f32p))
+        return idx, w
+
+    def qmat_mul(self, x: np.ndarray, m: "HostQMat", allow_idot: int = 1):
+        y = np.zeros(m.O, np.float32)
+        self.lib.or_qmat_mul(ptr(y, f32p), ptr(x, f32p), C.byref(m.st), allow_idot)
+        return y
+
+    def qmat_mul_batch(self, x: np.ndarray, m: "HostQMat", allow_idot: int = 1):
+        B, ldx = x.shape
+        y = np.zeros((B, m.O), np.float32)
+        self.lib.or_qmat_mul_batch(ptr(y, f32p), ptr(x, f32p), B, ldx, C.byref(m.st), allow_idot)
+        return y
+
+    def qrow_i8(self, x: np.ndarray):
+        q = np.zeros(x.size, np.int8)
+        s = self.lib.or_qrow_i8(ptr(x, f32p), ptr(q), x.size)
+        return q, np.float32(s)
+
+    def bucket(self, idx: np.ndarray, E: int):
+        T, K = idx.shape
+        idx = np.ascontiguousarray(idx, np.int32)
+        off = np.zeros(E + 1, np.int32)
+        tok = np.zeros(T * K, np.int32)
+        slot = np.zeros(T * K, np.int32)
+        n = self.lib.or_bucket(ptr(idx, i32p), T, K, E, ptr(off, i32p), ptr(tok, i32p),
+                               ptr(slot, i32p))
+        return off, tok[:n], slot[:n]
+
+    def moe_forward(self, layer: "HostLayer", x: np.ndarray, trace: bool = False):
+        H, E, K = layer.H, layer.E, layer.K
+        out = np.zeros(H, np.float32)
+        tr = None
+        if trace:
+            t = dict(logits=np.zeros(E, np.float32), idx=np.zeros(K, np.int32),
+                     weight=np.zeros(K, np.float32), shared=np.zeros(H, np.float32),
+                     sgate=np.zeros(1, np.float32))
+            tr = OrTrace(ptr(t["logits"], f32p), ptr(t["idx"], i32p), ptr(t["weight"], f32p),
+                         ptr(t["shared"], f32p), ptr(t["sgate"], f32p))
+        self.lib.or_moe_forward(C.byref(layer.st), ptr(x, f32p), ptr(out, f32p),
+                                C.byref(tr) if tr is not None else None)
+        return (out, t) if trace else out
+
+    def moe_prefill(self, layer: "HostLayer", x: np.ndarray, trace: bool = False):
+        T, H = x.shape
+        E, K = layer.E, layer.K
+        out = np.zeros((T, H), np.float32)
+        tr = None
+        if trace:
+            t = dict(logits=np.zeros((T, E), np.float32), idx=np.zeros((T, K), np.int32),
+                     weight=np.zeros((T, K), np.float32), shared=np.zeros((T, H), np.float32),
+                     sgate=np.zeros(T, np.float32))
+            tr = OrTrace(ptr(t["logits"], f32p), ptr(t["idx"], i32p), ptr(t["weight"], f32p),
+                         ptr(t["shared"], f32p), ptr(t["sgate"], f32p))
+        self.lib.or_moe_prefill_grouped(C.byref(layer.st), ptr(x, f32p), T, ptr(out, f32p),
+                                        C.byref(tr) if tr is not None else None)
+        return (out, t) if trace else out
+
+    def synth_x(self, seed: int, layer: int, step: int, H: int):
+        x = np.zeros(H, np.float32)
+        self.lib.or_synth_x(seed, layer, step, H, ptr(x, f32p))
+        return x
+
+    def set_threads(self, n: int):
+        self.lib.or_set_threads(n)
+
+
+def ref_lib_candidates():
+    """Compiled-reference builds, best match for this host first."""
+    flags = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("flags"):
+                    flags = line
+                    break
+    except OSError:
+        pass
+    names = []
+    if "avx512f" in flags and "avx512bw" in flags and "avx512_vnni" in flags:
+        names += ["libref_native.so", "libref_v4.so"]
+    if "avx2" in flags and " fma" in flags:
+        names += ["libref_v3.so"]
+    return [os.path.join(REF_DIR, n) for n in names if os.path.exists(os.path.join(REF_DIR, n))]
+
+
+class Reference:
+    """The reference's own CPU MoE code compiled in place (oracle/_ref)."""
+
+    def __init__(self, path: str | None = None):
+        if path is None:
+            cands = ref_lib_candidates()
+            if not cands:
+                raise FileNotFoundError("oracle/_ref has no build usable on this CPU")
+            path = cands[0]
+        self.path = path
+        self.lib = C.CDLL(path)
+        L = self.lib
+        _declare(L, "ref_")
+        L.ref_layer_create.restype = C.c_void_p
+        L.ref_layer_create.argtypes = [C.POINTER(OrLayer)]
+        L.ref_layer_destroy.restype = None
+        L.ref_layer_destroy.argtypes = [C.c_void_p]
+        L.ref_moe_forward.restype = None
+        L.ref_moe_forward.argtypes = [C.c_void_p, f32p, f32p]
+        L.ref_moe_prefill_grouped.restype = None
+        L.ref_moe_prefill_grouped.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        L.ref_set_threads.restype = None
+        L.ref_set_threads.argtypes = [C.c_int]
+        L.ref_omp_threads.restype = C.c_int
+
+    def dot(self, a, b):
+        return self.lib.ref_dot(ptr(a, f32p), ptr(b, f32p), a.size)
+
+    def router_topk(self, logit: np.ndarray, K: int):
+        idx = np.zeros(K, np.int32)
+        w = np.zeros(K, np.float32)
+        self.lib.ref_router_topk(ptr(logit, f32p), logit.size, K, ptr(idx, i32p), ptr(w, f32p))
+        return idx, w
+
+    def qmat_mul(self, x, m: "HostQMat", allow_idot: int = 1):
+        y = np.zeros(m.O, np.float32)
+        self.lib.ref_qmat_mul(ptr(y, f32p), ptr(x, f32p), C.byref(m.st), allow_idot)
+        return y
+
+    def qmat_mul_batch(self, x, m: "HostQMat", allow_idot: int = 1):
+        B, ldx = x.shape
+        y = np.zeros((B, m.O), np.float32)
+        self.lib.ref_qmat_mul_batch(ptr(y, f32p), ptr(x, f32p), B, ldx, C.byref(m.st),
+                                    allow_idot)
+        return y
+
+    def qrow_i8(self, x: np.ndarray):
+        q = np.zeros(x.size, np.int8)
+        s = self.lib.ref_qrow_i8(ptr(x, f32p), ptr(q), x.size)
+        return q, np.float32(s)
+
+    def layer(self, host_layer: "HostLayer"):
+        return RefLayer(self, host_layer)
+
+    def set_threads(self, n: int):
+        self.lib.ref_set_threads(n)
+
+
+class RefLayer:
+    def __init__(self, ref: Reference, hl: "HostLayer"):
+        self.ref = ref
+        self.hl = hl
+        self.h = ref.lib.ref_layer_create(C.byref(hl.st))
+
+    def forward(self, x: np.ndarray):
+        out = np.zeros(self.hl.H, np.float32)
+        self.ref.lib.ref_moe_forward(self.h, ptr(x, f32p), ptr(out, f32p))
+        return out
+
+    def prefill(self, x: np.ndarray):
+        T = x.shape[0]
+        out = np.zeros((T, self.hl.H), np.float32)
+        self.ref.lib.ref_moe_prefill_grouped(self.h, ptr(x, f32p), T, ptr(out, f32p))
+        return out
+
+    def __del__(self):
+        try:
+            self.ref.lib.ref_layer_destroy(self.h)
+        except Exception:
+            pass
+
+
+# -- host-side layer containers ------------------------------------------------
+
+def row_bytes(fmt: int, cols: int, gs: int) -> int:
+    """Container row bytes: int4 ng*gs/2, int3 ng*gs*3/8, int8 cols
+    (c/qwen.c:2242-2254)."""
+    if fmt == 1:
+        return cols
+    ng = (cols + gs - 1) // gs
+    return ng * gs // 2 if fmt == 4 else ng * gs * 3 // 8
+
+
+class HostQMat:
+    """Owns numpy buffers and the matching OrQMat struct."""
+
+    def __init__(self, fmt: int, O: int, I: int, gs: int = 0, q=None, s=None, f=None):
+        self.fmt, self.O, self.I, self.gs = fmt, O, I, gs
+        self.ng = (I + gs - 1) // gs if fmt in (3, 4) else 0
+        self.rb = row_bytes(fmt, I, gs) if fmt in (1, 3, 4) else 0
+        self.q, self.s, self.f = q, s, f
+        self.st = OrQMat(fmt, O, I, gs, self.rb, self.ng,
+                         ptr(f, f32p) if f is not None else None,
+                         ptr(s, f32p) if s is not None else None,
+                         ptr(q) if q is not None else None)
+
+
+class HostLayer:
+    """One synthetic MoE layer materialised on the host from sw_synth.h."""
+
+    def __init__(self, oracle: Oracle, seed: int, layer: int, H: int, E: int, K: int,
+                 I: int, I_sh: int, fmt: int, gs: int = 128, router=None):
+        self.H, self.E, self.K, self.I, self.I_sh, self.fmt, self.gs = H, E, K, I, I_sh, fmt, gs
+        L = oracle.lib
+        self.router_w = np.zeros((E, H), np.float32)
+        self.shared_gate_row = np.zeros(H, np.float32)
+        L.or_synth_router(seed, layer, E, H, ptr(self.router_w, f32p),
+                          ptr(self.shared_gate_row, f32p))
+        if router is not None:
+            self.router_w[...] = router
+        sg_q = np.zeros((I_sh, H), np.int8); sg_s = np.zeros(I_sh, np.float32)
+        su_q = np.zeros((I_sh, H), np.int8); su_s = np.zeros(I_sh, np.float32)
+        sd_q = np.zeros((H, I_sh), np.int8); sd_s = np.zeros(H, np.float32)
+        L.or_synth_shared_q8(seed, layer, H, I_sh, ptr(sg_q), ptr(sg_s, f32p), ptr(su_q),
+                             ptr(su_s, f32p), ptr(sd_q), ptr(sd_s, f32p))
+        self.router = HostQMat(0, E, H, f=self.router_w)
+        self.shared_scale = HostQMat(0, 1, H, f=self.shared_gate_row)
+        self.shared_gate = HostQMat(1, I_sh, H, q=sg_q, s=sg_s)
+        self.shared_up = HostQMat(1, I_sh, H, q=su_q, s=su_s)
+        self.shared_down = HostQMat(1, H, I_sh, q=sd_q, s=sd_s)
+        rbh, rbi = row_bytes(fmt, H, gs), row_bytes(fmt, I, gs)
+        ngh, ngi = (H + gs - 1) // gs, (I + gs - 1) // gs
+        self.gq = np.zeros((E, I, rbh), np.uint8); self.gsc = np.zeros((E, I, ngh), np.float32)
+        self.uq = np.zeros((E, I, rbh), np.uint8); self.usc = np.zeros((E, I, ngh), np.float32)
+        self.dq = np.zeros((E, H, rbi), np.uint8); self.dsc = np.zeros((E, H, ngi), np.float32)
+        for e in range(E):
+            L.or_synth_expert(seed, layer, e, fmt, H, I, gs, ptr(self.gq[e]),
+                              ptr(self.gsc[e], f32p), ptr(self.uq[e]), ptr(self.usc[e], f32p),
+                              ptr(self.dq[e]), ptr(self.dsc[e], f32p))
+        self.gate = [HostQMat(fmt, I, H, gs, q=self.gq[e], s=self.gsc[e]) for e in range(E)]
+        self.up = [HostQMat(fmt, I, H, gs, q=self.uq[e], s=self.usc[e]) for e in range(E)]
+        self.down = [HostQMat(fmt, H, I, gs, q=self.dq[e], s=self.dsc[e]) for e in range(E)]
+        self._g = (OrQMat * E)(*[m.st for m in self.gate])
+        self._u = (OrQMat * E)(*[m.st for m in self.up])
+        self._d = (OrQMat * E)(*[m.st for m in self.down])
+        self.st = OrLayer(H, E, K, I, I_sh, self.router.st, self.shared_gate.st,
+                          self.shared_up.st, self.shared_down.st, self.shared_scale.st,
+                          self._g, self._u, self._d)
+
+    def set_router_column(self, col: int, values: np.ndarray):
+        """Overwrite one router column in place (the Zipf bias feature)."""
+        self.router_w[:, col] = values
