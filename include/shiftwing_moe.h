@@ -1,0 +1,288 @@
+/* shiftwing MoE path for MI355X (gfx950): the C ABI.
+ *
+ * Part 1 keeps the reference backend's MoE-path entry points with identical
+ * prototypes, so c/qwen.c links against this library instead of
+ * backend_cuda.o unchanged (reference: /root/reference/c/backend_cuda.h; line
+ * numbers cited per entry point).  Conventions are the reference's
+ * (c/backend_cuda.cu:47-70): every call returns 0 on success and -1 on
+ * failure with a message in a thread-local buffer read by
+ * coli_cuda_last_error(); tensors are device pointers owned by the caller;
+ * every call is stream-ordered on the context's one stream and only
+ * coli_cuda_sync() (and profile_snapshot) blocks the host; the caller
+ * serialises calls on one context.
+ *
+ * Part 2 adds the device-resident MoE step that has no counterpart in the
+ * reference backend: a registered HBM-resident layer (router, int8 shared
+ * expert, all routed experts), device routing with the reference's exact
+ * top-k, device token->expert bucketing, and the fused layer step with no
+ * per-call host pointer tables and no batch/route limits.
+ */
+#ifndef SHIFTWING_MOE_H
+#define SHIFTWING_MOE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ColiCuda ColiCuda; /* backend_cuda.h:10 */
+
+/* ---- Part 1: reference backend entry points (c/backend_cuda.h) ---------- */
+
+const char *coli_cuda_last_error(void);                 /* backend_cuda.h:13 */
+int coli_cuda_create(ColiCuda **out, int device);         /* :14 */
+void coli_cuda_destroy(ColiCuda *ctx);                    /* :15 */
+const char *coli_cuda_device_name(const ColiCuda *ctx);   /* :16 */
+int coli_cuda_compute_capability(const ColiCuda *ctx, int *major,
+                                 int *minor);             /* :17 */
+int coli_cuda_device_limits(const ColiCuda *ctx, int *sm_count,
+                            int *shared_per_block);       /* :18-19 */
+int coli_cuda_async_alloc_enabled(const ColiCuda *ctx);   /* :20 */
+int coli_cuda_memory_info(ColiCuda *ctx, size_t *free_bytes,
+                          size_t *total_bytes);           /* :21-22 */
+int coli_cuda_malloc(ColiCuda *ctx, void **ptr, size_t bytes);        /* :24 */
+void coli_cuda_free(ColiCuda *ctx, void *ptr);                        /* :25 */
+int coli_cuda_malloc_host(ColiCuda *ctx, void **ptr, size_t bytes);   /* :26 */
+void coli_cuda_free_host(ColiCuda *ctx, void *ptr);                   /* :27 */
+int coli_cuda_host_register(ColiCuda *ctx, void *ptr, size_t bytes);  /* :28 */
+void coli_cuda_host_unregister(ColiCuda *ctx, void *ptr);             /* :29 */
+int coli_cuda_upload(ColiCuda *ctx, void *dst, const void *src,
+                     size_t bytes);                                   /* :30 */
+int coli_cuda_download(ColiCuda *ctx, void *dst, const void *src,
+                       size_t bytes);                                 /* :31 */
+int coli_cuda_copy(ColiCuda *ctx, void *dst, const void *src,
+                   size_t bytes);                                     /* :32 */
+int coli_cuda_memset(ColiCuda *ctx, void *dst, int value, size_t bytes); /* :33 */
+int coli_cuda_sync(ColiCuda *ctx);                                    /* :34 */
+void coli_cuda_profile_reset(ColiCuda *ctx);                          /* :35 */
+int coli_cuda_profile_snapshot(ColiCuda *ctx, unsigned long long *transactions,
+                               double stage_ms[8]);                   /* :38-40 */
+
+int coli_cuda_rmsnorm_zero(ColiCuda *ctx, float *y, const float *x,
+                           const float *w, int n, float eps);         /* :46-47 */
+int coli_cuda_rmsnorm_zero_batch(ColiCuda *ctx, float *y, const float *x,
+                                 const float *w, int batch, int n,
+                                 float eps);                          /* :48-49 */
+int coli_cuda_f32_gemm(ColiCuda *ctx, float *y, const float *x,
+                       const float *w, int batch, int rows, int cols); /* :50-51 */
+int coli_cuda_sigmoid(ColiCuda *ctx, float *y, const float *x, int n); /* :52 */
+int coli_cuda_silu_mul(ColiCuda *ctx, float *y, const float *gate,
+                       const float *up, int n);                       /* :53-54 */
+int coli_cuda_axpy(ColiCuda *ctx, float *y, const float *x, float scale,
+                   int n);                                            /* :55 */
+int coli_cuda_sigmoid_axpy(ColiCuda *ctx, float *y, const float *x,
+                           const float *logit, int n);                /* :56-57 */
+int coli_cuda_f32_to_f16(ColiCuda *ctx, unsigned short *y, const float *x,
+                         int n);                                      /* :58-59 */
+int coli_cuda_q8_gemv(ColiCuda *ctx, float *y, const float *x,
+                      const signed char *q, const float *scales, int rows,
+                      int cols, int row_bytes);                       /* :60-62 */
+int coli_cuda_q8_gemm(ColiCuda *ctx, float *y, const float *x, int batch,
+                      const signed char *q, const float *scales, int rows,
+                      int cols, int row_bytes);                       /* :63-65 */
+int coli_cuda_q4_gemv(ColiCuda *ctx, float *y, const float *x,
+                      const unsigned char *q, const float *scales, int rows,
+                      int cols, int group_size, int row_bytes,
+                      int groups_per_row);                            /* :66-69 */
+int coli_cuda_q4_gemm(ColiCuda *ctx, float *y, const float *x, int batch,
+                      const unsigned char *q, const float *scales, int rows,
+                      int cols, int group_size, int row_bytes,
+                      int groups_per_row);                            /* :70-73 */
+int coli_cuda_q4_gemv_f16(ColiCuda *ctx, float *y, const unsigned short *x,
+                          const unsigned char *q, const float *scales,
+                          int rows, int cols, int group_size, int row_bytes,
+                          int groups_per_row);                        /* :74-77 */
+int coli_cuda_q3_gemv(ColiCuda *ctx, float *y, const float *x,
+                      const unsigned char *q, const float *scales, int rows,
+                      int cols, int group_size, int row_bytes,
+                      int groups_per_row);                            /* :78-81 */
+int coli_cuda_q3_gemv_f16(ColiCuda *ctx, float *y, const unsigned short *x,
+                          const unsigned char *q, const float *scales,
+                          int rows, int cols, int group_size, int row_bytes,
+                          int groups_per_row);                        /* :82-86 */
+int coli_cuda_grouped_q4_mlp_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int experts, int hidden, int intermediate,
+    int group_size, int hidden_row_bytes, int hidden_groups,
+    int down_row_bytes, int down_groups);                            /* :87-94 */
+int coli_cuda_grouped_q3_mlp_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int experts, int hidden, int intermediate,
+    int group_size, int hidden_row_bytes, int hidden_groups,
+    int down_row_bytes, int down_groups);                            /* :95-102 */
+int coli_cuda_grouped_q4_mlp_batch_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int batch, int experts_per_token, int hidden,
+    int intermediate, int group_size, int hidden_row_bytes,
+    int hidden_groups, int down_row_bytes, int down_groups);         /* :103-110 */
+int coli_cuda_grouped_q3_mlp_batch_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int batch, int experts_per_token, int hidden,
+    int intermediate, int group_size, int hidden_row_bytes,
+    int hidden_groups, int down_row_bytes, int down_groups);         /* :111-118 */
+int coli_cuda_shared_q4_mlp_batch_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *gate_q, const float *gate_s,
+    const unsigned char *up_q, const float *up_s,
+    const unsigned char *down_q, const float *down_s,
+    const unsigned char *scale_q, const float *scale_s,
+    int batch, int hidden, int intermediate, int group_size,
+    int hidden_row_bytes, int hidden_groups, int down_row_bytes,
+    int down_groups, int scale_row_bytes, int scale_groups);         /* :119-127 */
+int coli_cuda_shared_q8_mlp_batch(
+    ColiCuda *ctx, float *y, const float *x, const float *scale,
+    const signed char *gate_q, const float *gate_s, int gate_row_bytes,
+    const signed char *up_q, const float *up_s, int up_row_bytes,
+    const signed char *down_q, const float *down_s, int down_row_bytes,
+    int batch, int hidden, int intermediate);                        /* :128-133 */
+int coli_cuda_shared_q8_mlp_batch_device_scale(
+    ColiCuda *ctx, float *y, const float *x, const float *device_scale,
+    const signed char *gate_q, const float *gate_s, int gate_row_bytes,
+    const signed char *up_q, const float *up_s, int up_row_bytes,
+    const signed char *down_q, const float *down_s, int down_row_bytes,
+    int batch, int hidden, int intermediate);                        /* :134-139 */
+int coli_cuda_shared_q4_mlp_f16(
+    ColiCuda *ctx, float *y, const unsigned short *x,
+    const unsigned char *gate_q, const float *gate_s,
+    const unsigned char *up_q, const float *up_s,
+    const unsigned char *down_q, const float *down_s,
+    const unsigned char *scale_q, const float *scale_s,
+    int hidden, int intermediate, int group_size, int hidden_row_bytes,
+    int hidden_groups, int down_row_bytes, int down_groups,
+    int scale_row_bytes, int scale_groups);                          /* :140-148 */
+
+/* ---- Part 2: device-resident MoE step (no reference counterpart) -------- */
+
+/* fp32-activation variants of the grouped calls above (same arguments with
+ * x as float*).  The reference only has fp16-activation grouped kernels; its
+ * CPU path is fp32, which these match within tolerance. */
+int coli_cuda_grouped_q4_mlp(
+    ColiCuda *ctx, float *y, const float *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int experts, int hidden, int intermediate,
+    int group_size, int hidden_row_bytes, int hidden_groups,
+    int down_row_bytes, int down_groups);
+int coli_cuda_grouped_q3_mlp(
+    ColiCuda *ctx, float *y, const float *x,
+    const unsigned char *const *gate_q, const float *const *gate_s,
+    const unsigned char *const *up_q, const float *const *up_s,
+    const unsigned char *const *down_q, const float *const *down_s,
+    const float *route_weight, int experts, int hidden, int intermediate,
+    int group_size, int hidden_row_bytes, int hidden_groups,
+    int down_row_bytes, int down_groups);
+
+/* Bit-exact IDOT int8 GEMM (c/qwen.c:1696-1705, 1765-1768, 3313-3319):
+ * per token xq = qrow_i8(x) (amax/127, 1/s, lrintf), then
+ * y[b,o] = ((float)sum_i q[o,i]*xq[b,i] * scales[o]) * sx[b]. */
+int coli_cuda_idot_q8_gemm(ColiCuda *ctx, float *y, const float *x, int batch,
+                           const signed char *q, const float *scales,
+                           int rows, int cols, int row_bytes);
+
+/* router_topk (c/qwen.c:3421-3426) on device logits, bit-exact:
+ * logits [tokens x experts] -> idx / weight [tokens x topk]. */
+int coli_cuda_router_topk(ColiCuda *ctx, const float *logits, int tokens,
+                          int experts, int topk, int *idx, float *weight);
+
+/* Token->expert bucketing in the reference's grouped-prefill order
+ * (c/qwen.c:4168, 3956-3968): experts ascending, tokens ascending.
+ * idx [tokens x topk] -> offsets [experts+1], token [tokens*topk],
+ * slot [tokens*topk] (the route index k).  Entries past offsets[experts]
+ * are left untouched. */
+int coli_cuda_moe_bucket(ColiCuda *ctx, const int *idx, int tokens, int topk,
+                         int experts, int *offsets, int *token, int *slot);
+
+typedef struct ColiMoeLayer ColiMoeLayer;
+
+typedef struct {
+    int hidden;              /* H */
+    int experts;             /* E */
+    int topk;                /* K */
+    int intermediate;        /* routed expert I */
+    int shared_intermediate; /* shared expert I */
+    int expert_format;       /* 4 = grouped int4, 3 = packed int3 triplets */
+    int group_size;          /* routed-expert quant group (128) */
+} ColiMoeShape;
+
+/* Allocate an HBM-resident layer (all experts).  Requires hidden,
+ * intermediate and shared_intermediate to be multiples of 16, group_size 128
+ * and topk <= 32. */
+int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out,
+                               const ColiMoeShape *shape);
+void coli_cuda_moe_layer_destroy(ColiCuda *ctx, ColiMoeLayer *layer);
+/* Device bytes held by the layer. */
+size_t coli_cuda_moe_layer_bytes(const ColiMoeLayer *layer);
+
+/* Load weights from device buffers in the container layouts of c/qwen.c
+ * (QMat, c/qwen.c:68-81): router f32 [E x H] and shared gate row f32 [H];
+ * shared expert int8 rows (row_bytes = cols) with one f32 scale per row;
+ * routed expert codes [rows x row_bytes] with f32 scales [rows x groups].
+ * Routed experts are repacked on the device into the MFMA tile layout. */
+int coli_cuda_moe_layer_set_router(ColiCuda *ctx, ColiMoeLayer *layer,
+                                   const float *router,
+                                   const float *shared_gate);
+int coli_cuda_moe_layer_set_shared_q8(ColiCuda *ctx, ColiMoeLayer *layer,
+                                      const signed char *gate_q,
+                                      const float *gate_s,
+                                      const signed char *up_q,
+                                      const float *up_s,
+                                      const signed char *down_q,
+                                      const float *down_s);
+int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *layer,
+                                   int expert, const unsigned char *gate_q,
+                                   const float *gate_s,
+                                   const unsigned char *up_q,
+                                   const float *up_s,
+                                   const unsigned char *down_q,
+                                   const float *down_s);
+/* Generate the whole layer on the device from the counter hash of
+ * shiftwing_amd/csrc/sw_synth.h (identical bytes to the host generator). */
+int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *layer,
+                                   unsigned long long seed, int layer_index);
+/* Device pointer to the layer's router [E x H] (for in-place edits). */
+float *coli_cuda_moe_layer_router(ColiMoeLayer *layer);
+
+/* The MoE step for `tokens` activation rows: y[t] = sum_k w[t,k] *
+ * expert_{idx[t,k]}(x[t]) + sigmoid(gate . x[t]) * shared(x[t]).
+ * x, y: device [tokens x H] f32.  route_idx / route_weight: optional device
+ * outputs [tokens x K].  Routing is bit-exact with router_topk over the
+ * reference's fp32 router logits; the shared expert uses IDOT. */
+int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *layer, float *y,
+                          const float *x, int tokens, int *route_idx,
+                          float *route_weight);
+
+/* Router only: idx / weight [tokens x K]; logits (optional, [tokens x E])
+ * receives the fp32 logits of the reference's serial dot when the exact path
+ * ran for that token, NaN otherwise. */
+int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *layer, const float *x,
+                        int tokens, int *idx, float *weight);
+
+/* Routing statistics since the layer was created: tokens routed, tokens that
+ * needed the exact serial-chain fallback. */
+int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *layer,
+                              unsigned long long *tokens,
+                              unsigned long long *exact_fallbacks);
+
+/* Router policy: 0 = certified fast path with exact fallback (default),
+ * 1 = always run the exact serial chain. */
+int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -292,6 +292,16 @@ float or_sigmoidf(float x) {
 }
 float or_siluf(float x) { return x * or_sigmoidf(x); }
 
+/* Batch forms of the above for exhaustive device comparisons. */
+void or_sigmoid_batch(const float *x, float *y, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) y[i] = or_sigmoidf(x[i]);
+}
+void or_expf_batch(const float *x, float *y, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 /* router_topk, qwen.c:3421-3426: softmax over all E (serial denominator in
  * expert order), K rounds of argmax with strict '>' (lowest index wins a
  * tie), then renormalisation of the K picked probabilities. */

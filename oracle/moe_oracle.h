@@ -66,6 +66,8 @@ void or_qmat_mul_batch(float *y, const float *x, int B, int ldx,
 float or_expf(float x);
 float or_sigmoidf(float x);
 float or_siluf(float x);
+void or_sigmoid_batch(const float *x, float *y, int64_t n);
+void or_expf_batch(const float *x, float *y, int64_t n);
 void or_router_topk(const float *logit, int E, int K, int *idx, float *weight);
 void or_mlp_one(float *out, const float *x, const or_qmat *gate,
                 const or_qmat *up, const or_qmat *down, int I);

@@ -117,6 +117,11 @@ class Oracle:
         L.or_synth_bytes.restype = None
         L.or_synth_bytes.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int,
                                      C.c_void_p, C.c_uint64]
+        for nm in ("or_sigmoid_batch", "or_expf_batch"):
+            getattr(L, nm).restype = None
+            getattr(L, nm).argtypes = [f32p, f32p, C.c_int64]
+        L.or_siluf.restype = C.c_float
+        L.or_siluf.argtypes = [C.c_float]
         L.or_set_threads.restype = None
         L.or_set_threads.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
@@ -194,6 +199,14 @@ class Oracle:
 
     def set_threads(self, n: int):
         self.lib.or_set_threads(n)
+
+    def sigmoid_batch(self, x: np.ndarray) -> np.ndarray:
+        y = np.empty_like(x)
+        self.lib.or_sigmoid_batch(ptr(x, f32p), ptr(y, f32p), x.size)
+        return y
+
+    def host_layer(self, seed, layer, H, E, K, I, I_sh, fmt, gs=128):
+        return HostLayer(self, seed, layer, H, E, K, I, I_sh, fmt, gs)
 
 
 def ref_lib_candidates():

@@ -1,0 +1,1217 @@
+// HBM-resident MoE layer step for gfx950 (the coli_cuda_moe_* entry points).
+//
+// What it computes is the reference's CPU MoE step (c/qwen.c): moe_forward
+// 3717-3739 for one token and moe_prefill_grouped 4141-4206 for many, with
+// router_topk 3421-3426, the int8 IDOT shared expert 1696-1705/1765-1768 and
+// grouped int4 / int3 routed experts 1706-1754.
+//
+// Device layout (set at registration, see tile_* below).  Routed expert
+// matrices are repacked into MFMA tiles: a tile is 16 rows x one 128-wide
+// quant group; lane l of a wave owns row (l%16) and the 32 codes at group
+// positions kb*16+[0,16) and 64+kb*16+[0,16), kb = l/16.  Those 32 codes are
+// stored as 16 bytes (int4: byte m of word i holds codes 8i+m (low nibble)
+// and 8i+4+m (high nibble)) or 12 bytes (int3: two 2-bit planes L0, L1 and a
+// high-bit plane H).  One coalesced 1 KB / 768 B wave load fetches a tile.
+// Per-(row, group) f32 scales are stored in the same tile order.
+//
+// Arithmetic.  Routed experts run on v_mfma_i32_16x16x64_i8: the activation
+// is split per 128-group into two int8 digits, x ~= A*q1 + B*q2 (A =
+// amax/127, B = A/254), the codes are unpacked to int8 bytes, and exact int32
+// group dots are scaled once per group in fp32.  The shared expert's int8
+// dots are exact int32 on the same MFMA (IDOT, bit-identical to the CPU).
+// Routing is bit-exact: a certified fp64 pass proves the top-k order of the
+// reference's serial fp32 router dot, and tokens it cannot certify run the
+// serial chain itself.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "sw_backend.h"
+#include "sw_device.h"
+#include "sw_synth.h"
+
+using namespace sw;
+
+namespace {
+
+constexpr int kTileRows = 16;
+constexpr int kGroup = 128;
+constexpr int kMaxTopK = 32;
+constexpr int kMaxTokensPerItem = 8;   // routed MFMA B columns: 8 tokens x 2 digits
+constexpr int kSharedTokens = 16;      // shared IDOT B columns: 16 tokens
+constexpr int kMaxTokens = 2048;       // per call (bucketing LDS bitmap)
+
+inline int tile_bytes_per_lane(int fmt) { return fmt == 4 ? 16 : 12; }
+
+}  // namespace
+
+struct ColiMoeLayer {
+  ColiMoeShape sh;
+  int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
+  size_t gate_codes, down_codes; // bytes of one gate (= up) / down tiled matrix
+  size_t gate_scales, down_scales;
+  size_t expert_codes, expert_scales;  // per expert
+  float *router;                 // [E][H]
+  float *sgate_row;              // [H]
+  signed char *sh_gq, *sh_uq, *sh_dq;  // row-major int8
+  float *sh_gs, *sh_us, *sh_ds;
+  unsigned char *codes;          // [E][gate|up|down] tiled
+  float *scales;                 // [E][gate|up|down] tiled
+  unsigned long long *stats;     // device [2]: tokens, exact fallbacks
+  int router_mode;
+  size_t bytes;
+  void *alloc[16];
+  int nalloc;
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// tile addressing
+// ---------------------------------------------------------------------------
+// group-relative k of lane slot s (0..31) for k-slice kb
+__host__ __device__ inline int slot_k(int s, int kb) { return s < 16 ? kb * 16 + s : 64 + kb * 16 + (s - 16); }
+
+__device__ inline int container_code(const unsigned char *row, int k, int cols, int fmt) {
+  if (k >= cols) return fmt == 4 ? 8 : 4;  // zero value
+  if (fmt == 4) {
+    unsigned char b = row[k >> 1];
+    return (k & 1) ? (b >> 4) : (b & 15);
+  }
+  int bit = 3 * k, byte = bit >> 3, shift = bit & 7;
+  unsigned w = row[byte];
+  if (shift > 5) w |= (unsigned)row[byte + 1] << 8;
+  return (int)((w >> shift) & 7u);
+}
+
+// one thread per (row tile, group, lane): container codes -> tile bytes
+__global__ void k_repack_codes(unsigned char *dst, const unsigned char *src, int rows, int cols, int rb,
+                               int ng, int fmt) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long total = (long long)(rows / kTileRows) * ng * 64;
+  if (tid >= total) return;
+  int lane = (int)(tid & 63);
+  long long tg = tid >> 6;  // rt * ng + g
+  int g = (int)(tg % ng);
+  int rt = (int)(tg / ng);
+  int r = rt * kTileRows + (lane & 15), kb = lane >> 4;
+  const unsigned char *row = src + (size_t)r * rb;
+  int code[32];
+#pragma unroll
+  for (int s = 0; s < 32; s++) code[s] = container_code(row, g * kGroup + slot_k(s, kb), cols, fmt);
+  if (fmt == 4) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int m = 0; m < 4; m++) v |= (uint32_t)(code[8 * i + m] | (code[8 * i + 4 + m] << 4)) << (8 * m);
+      w[i] = v;
+    }
+    uint32_t *d = (uint32_t *)(dst + tid * 16);
+    d[0] = w[0];
+    d[1] = w[1];
+    d[2] = w[2];
+    d[3] = w[3];
+  } else {
+    uint32_t L[2] = {0, 0}, H = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        int c = code[4 * j + m];
+        L[j >> 2] |= (uint32_t)(c & 3) << (8 * m + 2 * (j & 3));
+        H |= (uint32_t)((c >> 2) & 1) << (8 * m + j);
+      }
+    uint32_t *d = (uint32_t *)(dst + tid * 12);
+    d[0] = L[0];
+    d[1] = L[1];
+    d[2] = H;
+  }
+}
+
+// scales [rows][ng] -> [rt][g][16]
+__global__ void k_repack_scales(float *dst, const float *src, int rows, int ng) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long total = (long long)rows * ng;
+  if (tid >= total) return;
+  int r = (int)(tid & 15);
+  long long tg = tid >> 4;
+  int g = (int)(tg % ng);
+  int rt = (int)(tg / ng);
+  dst[tid] = src[(size_t)(rt * kTileRows + r) * ng + g];
+}
+
+// ---------------------------------------------------------------------------
+// synthetic weights (sw_synth.h), generated in place
+// ---------------------------------------------------------------------------
+__global__ void k_synth_bytes(unsigned char *dst, size_t n, uint64_t key) {
+  size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t i = w * 8;
+  if (i >= n) return;
+  uint64_t h = sw_word(key, w);
+  if (i + 8 <= n && ((((uintptr_t)dst) & 7) == 0)) {
+    *(uint64_t *)(dst + i) = h;
+  } else {
+    for (int b = 0; b < 8 && i + b < n; b++) dst[i + b] = (unsigned char)(h >> (8 * b));
+  }
+}
+__global__ void k_synth_i8(signed char *dst, size_t n, uint64_t key) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = sw_i8(key, i);
+}
+__global__ void k_synth_normal(float *dst, size_t n, uint64_t key, float sigma, int absolute) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = absolute ? sw_abs_normal_sigma(key, i, sigma) : sw_normal_sigma(key, i, sigma);
+}
+// tiled scales straight from the hash at their container index
+__global__ void k_synth_scales_tiled(float *dst, int rows, int ng, uint64_t key) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= (long long)rows * ng) return;
+  int r = (int)(tid & 15);
+  long long tg = tid >> 4;
+  int g = (int)(tg % ng);
+  int rt = (int)(tg / ng);
+  dst[tid] = sw_abs_normal_sigma(key, (uint64_t)(rt * kTileRows + r) * ng + g, 0.01f);
+}
+
+inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+// ---------------------------------------------------------------------------
+// activation digits: v (len n, zero-padded to ng*128) ->
+//   d1, d2 int8 [ng*128], gp[g] = {A, B, Q1, Q2} with v ~= A*d1 + B*d2 and
+//   Q = sum of the digits of the group.  One block; waves loop over groups.
+// ---------------------------------------------------------------------------
+__device__ void quantize_digits(const float *v, int n, int ng, signed char *d1, signed char *d2, float4 *gp) {
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int g = wave; g < ng; g += nw) {
+    int i0 = g * kGroup + 2 * lane;
+    float a = i0 < n ? v[i0] : 0.0f;
+    float b = i0 + 1 < n ? v[i0 + 1] : 0.0f;
+    float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
+    float A = amax / 127.0f;
+    float B = A / 254.0f;
+    int qa1 = 0, qa2 = 0, qb1 = 0, qb2 = 0;
+    if (amax > 0.0f) {
+      float invA = 127.0f / amax, invB = 254.0f / A;
+      qa1 = (int)fminf(fmaxf(__builtin_rintf(a * invA), -127.0f), 127.0f);
+      qb1 = (int)fminf(fmaxf(__builtin_rintf(b * invA), -127.0f), 127.0f);
+      float ra = __builtin_fmaf(-(float)qa1, A, a);
+      float rb = __builtin_fmaf(-(float)qb1, A, b);
+      qa2 = (int)fminf(fmaxf(__builtin_rintf(ra * invB), -127.0f), 127.0f);
+      qb2 = (int)fminf(fmaxf(__builtin_rintf(rb * invB), -127.0f), 127.0f);
+    }
+    d1[i0] = (signed char)qa1;
+    d1[i0 + 1] = (signed char)qb1;
+    d2[i0] = (signed char)qa2;
+    d2[i0 + 1] = (signed char)qb2;
+    int Q1 = wave_sum_i(qa1 + qb1), Q2 = wave_sum_i(qa2 + qb2);
+    if (lane == 0) gp[g] = make_float4(A, B, __int_as_float(Q1), __int_as_float(Q2));
+  }
+}
+
+// qrow_i8 (c/qwen.c:1696) by one block: returns s, writes q
+__device__ float qrow_i8_block(const float *x, int n, signed char *q, float *red) {
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, fabsf(x[i]));
+  m = wave_max(m);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float a = 0.0f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) a = fmaxf(a, red[i]);
+  float s = a / 127.0f;
+  if (s < 1e-12f) s = 1e-12f;
+  float inv = 1.0f / s;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) q[i] = (signed char)__builtin_rintf(x[i] * inv);
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// per-call workspace carved from one scratch buffer
+// ---------------------------------------------------------------------------
+struct Work {
+  int T, H, E, K, I, Ish, ngh, ngi, Hp, Ip;
+  // prep
+  signed char *xq; float *sx;
+  signed char *xd1, *xd2; float4 *xgp;
+  // router
+  double2 *lb; float *sgate; int *certified; float *logits;
+  int *idx; float *w;
+  // bucket
+  int *offsets, *btok, *bslot, *pos; int4 *items; int *nitems;
+  // shared
+  float *hsh; signed char *hq; float *shx; float *shout;
+  // routed
+  float *hroute; signed char *hd1, *hd2; float4 *hgp; float *rout;
+  size_t bytes;
+};
+
+size_t carve(Work &w, char *base) {
+  size_t off = 0;
+  auto take = [&](size_t n) -> char * {
+    off = (off + 255) & ~(size_t)255;
+    char *p = base ? base + off : nullptr;
+    off += n;
+    return p;
+  };
+  int T = w.T, R = w.T * w.K;
+  w.xq = (signed char *)take((size_t)T * w.H);
+  w.sx = (float *)take((size_t)T * 4);
+  w.xd1 = (signed char *)take((size_t)T * w.Hp);
+  w.xd2 = (signed char *)take((size_t)T * w.Hp);
+  w.xgp = (float4 *)take((size_t)T * w.ngh * 16);
+  w.lb = (double2 *)take((size_t)T * (w.E + 1) * 16);
+  w.sgate = (float *)take((size_t)T * 4);
+  w.certified = (int *)take((size_t)T * 4);
+  w.logits = (float *)take((size_t)T * w.E * 4);
+  w.idx = (int *)take((size_t)R * 4);
+  w.w = (float *)take((size_t)R * 4);
+  w.offsets = (int *)take((size_t)(w.E + 1) * 4);
+  w.btok = (int *)take((size_t)R * 4);
+  w.bslot = (int *)take((size_t)R * 4);
+  w.pos = (int *)take((size_t)R * 4);
+  w.items = (int4 *)take((size_t)(R + w.E) * 16);
+  w.nitems = (int *)take(16);
+  w.hsh = (float *)take((size_t)T * w.Ish * 4);
+  w.hq = (signed char *)take((size_t)T * w.Ish);
+  w.shx = (float *)take((size_t)T * 4);
+  w.shout = (float *)take((size_t)T * w.H * 4);
+  w.hroute = (float *)take((size_t)R * w.I * 4);
+  w.hd1 = (signed char *)take((size_t)R * w.Ip);
+  w.hd2 = (signed char *)take((size_t)R * w.Ip);
+  w.hgp = (float4 *)take((size_t)R * w.ngi * 16);
+  w.rout = (float *)take((size_t)R * w.H * 4);
+  w.bytes = off + 256;
+  return w.bytes;
+}
+
+// ---------------------------------------------------------------------------
+// 1. activation prep: IDOT quantisation + routed digits; grid T, 256 threads
+// ---------------------------------------------------------------------------
+__global__ void k_prep_x(Work w, const float *x) {
+  __shared__ float red[16];
+  int t = blockIdx.x;
+  const float *xt = x + (size_t)t * w.H;
+  float s = qrow_i8_block(xt, w.H, w.xq + (size_t)t * w.H, red);
+  if (threadIdx.x == 0) w.sx[t] = s;
+  quantize_digits(xt, w.H, w.ngh, w.xd1 + (size_t)t * w.Hp, w.xd2 + (size_t)t * w.Hp, w.xgp + (size_t)t * w.ngh);
+}
+
+// ---------------------------------------------------------------------------
+// 2. router: per (token, expert) the fp64 logit L and a rigorous bound B on
+// |fl32 serial dot - L| (c/qwen.c:1674 evaluated as s = rn(s + rn(x*w)),
+// tail FMA).  Each step's rounding is at most u*|partial| (u = 2^-24), each
+// product's at most u*|x*w|, so |err| <= u*(sum|x w| + sum_k |S_k|)*(1+uH).
+// Lane j owns the contiguous chunk j of the row; the prefix sums S_k are the
+// chunk offset O_j plus the local prefix, bounded by |O_j| + |local|.
+// Row E is the shared-expert gate row.  grid (ceil((E+1)/4), T), 256 threads.
+// ---------------------------------------------------------------------------
+__global__ void k_router_bounds(Work w, const float *x, const float *router, const float *sgate_row) {
+  int lane = threadIdx.x & 63;
+  int e = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
+  if (e > w.E) return;
+  const float *row = e < w.E ? router + (size_t)e * w.H : sgate_row;
+  const float *xt = x + (size_t)t * w.H;
+  int chunk = (w.H + 63) / 64;
+  int i0 = lane * chunk, i1 = min(i0 + chunk, w.H);
+  double lp = 0.0, pa = 0.0, aa = 0.0;
+  for (int i = i0; i < i1; i++) {
+    double xd = (double)xt[i], wd = (double)row[i];
+    lp = __builtin_fma(xd, wd, lp);
+    aa = __builtin_fma(fabs(xd), fabs(wd), aa);
+    pa += fabs(lp);
+  }
+  double off = wave_exclusive_scan(lp, lane);
+  double L = wave_sum(lp);
+  double Pb = wave_sum((double)(i1 > i0 ? i1 - i0 : 0) * fabs(off) + pa);
+  double A = wave_sum(aa);
+  if (lane == 0) {
+    const double u = 0x1p-24;
+    double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+    w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, B);
+    if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
+  }
+}
+
+// block argmax over (value, index): largest value, lowest index on ties
+struct VI {
+  double v;
+  int i;
+};
+__device__ inline VI vi_better(VI a, VI b) {
+  if (b.i < 0) return a;
+  if (a.i < 0) return b;
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+__device__ VI block_argmax(VI x, VI *red) {
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    VI y;
+    y.v = __shfl_xor(x.v, o, 64);
+    y.i = __shfl_xor(x.i, o, 64);
+    x = vi_better(x, y);
+  }
+  __syncthreads();
+  if (lane == 0) red[wave] = x;
+  __syncthreads();
+  VI r = red[0];
+  for (int i = 1; i < nw; i++) r = vi_better(r, red[i]);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// 3. certify: the top-k order (and the k|k+1 boundary) of the fp32 logits is
+// fixed if the bound intervals of adjacent candidates are disjoint with a
+// margin that also covers the rounding of (l - max), expf and the division,
+// so router_topk on the true fp32 logits picks exactly these indices.
+// grid T, 512 threads.
+// ---------------------------------------------------------------------------
+__global__ void k_certify(Work w, int mode, unsigned long long *stats) {
+  __shared__ VI red[16];
+  __shared__ int cand[kMaxTopK + 1];
+  __shared__ unsigned char chosen[4096];
+  int t = blockIdx.x;
+  const double2 *lb = w.lb + (size_t)t * (w.E + 1);
+  for (int e = threadIdx.x; e < w.E; e += blockDim.x) chosen[e] = 0;
+  __syncthreads();
+  int nc = min(w.K + 1, w.E);
+  for (int r = 0; r < nc; r++) {
+    VI best = {0.0, -1};
+    for (int e = threadIdx.x; e < w.E; e += blockDim.x)
+      if (!chosen[e]) best = vi_better(best, VI{lb[e].x, e});
+    best = block_argmax(best, red);
+    if (threadIdx.x == 0) {
+      cand[r] = best.i;
+      chosen[best.i] = 1;
+    }
+    __syncthreads();
+  }
+  // largest upper bound among experts outside the top-k
+  VI up = {0.0, -1};
+  for (int e = threadIdx.x; e < w.E; e += blockDim.x) {
+    bool in_top = false;
+    for (int r = 0; r < w.K && r < nc; r++) in_top |= cand[r] == e;
+    if (!in_top) up = vi_better(up, VI{lb[e].x + lb[e].y, e});
+  }
+  up = block_argmax(up, red);
+  if (threadIdx.x == 0) {
+    double mx = lb[cand[0]].x;
+    bool ok = mode == 0 && w.K <= w.E;
+    for (int r = 0; ok && r + 1 < w.K; r++) {
+      double2 a = lb[cand[r]], b = lb[cand[r + 1]];
+      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
+      ok = (a.x - a.y) - (b.x + b.y) > margin;
+    }
+    if (ok && up.i >= 0) {
+      double2 a = lb[cand[w.K - 1]];
+      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(up.v) + 2.0 * fabs(mx));
+      ok = (a.x - a.y) - up.v > margin;
+    }
+    if (ok) ok = (lb[cand[w.K - 1]].x - lb[cand[w.K - 1]].y) - (mx + lb[cand[0]].y) > -80.0;
+    w.certified[t] = ok ? 1 : 0;
+    if (ok) {
+      double p[kMaxTopK], den = 0.0;
+      for (int r = 0; r < w.K; r++) {
+        p[r] = exp(lb[cand[r]].x - mx);
+        den += p[r];
+      }
+      for (int r = 0; r < w.K; r++) {
+        w.idx[(size_t)t * w.K + r] = cand[r];
+        w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
+      }
+    }
+    atomicAdd(&stats[0], 1ull);
+    if (!ok) atomicAdd(&stats[1], 1ull);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. exact fallback: the reference's fp32 serial dot for every expert of an
+// uncertified token (one lane per expert; blocks of 64 experts).
+// grid (ceil(E/64), T), 64 threads.
+// ---------------------------------------------------------------------------
+__global__ void k_exact_logits(Work w, const float *x, const float *router) {
+  int t = blockIdx.y;
+  if (w.certified[t]) return;
+  int e = blockIdx.x * 64 + threadIdx.x;
+  if (e >= w.E) return;
+  const float *xt = x + (size_t)t * w.H;
+  const float *row = router + (size_t)e * w.H;
+  int m = (w.H / 8) * 8;
+  float s = 0.0f;
+  int i = 0;
+  for (; i + 4 <= m; i += 4) {
+    float4 wv = *(const float4 *)(row + i);
+    float4 xv = *(const float4 *)(xt + i);
+    s = __fadd_rn(s, __fmul_rn(xv.x, wv.x));
+    s = __fadd_rn(s, __fmul_rn(xv.y, wv.y));
+    s = __fadd_rn(s, __fmul_rn(xv.z, wv.z));
+    s = __fadd_rn(s, __fmul_rn(xv.w, wv.w));
+  }
+  for (; i < m; i++) s = __fadd_rn(s, __fmul_rn(xt[i], row[i]));
+  for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+  w.logits[(size_t)t * w.E + e] = s;
+}
+
+// router_topk (c/qwen.c:3421-3426) on fp32 logits, bit-exact: serial max and
+// denominator in expert order, glibc expf, K argmax rounds with strict '>'
+// (lowest index on ties, -1 if nothing beats -1), serial renormalisation.
+// One block per token; `skip` (may be null) marks certified tokens.
+__device__ void topk_exact_block(const float *logit, int E, int K, int *idx, float *weight, float *prob,
+                                 VI *red) {
+  __shared__ float s_mx, s_den;
+  if (threadIdx.x == 0) {
+    float mx = -__builtin_huge_valf();
+    for (int e = 0; e < E; e++)
+      if (logit[e] > mx) mx = logit[e];
+    s_mx = mx;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) prob[e] = expf_glibc(logit[e] - s_mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float den = 0.0f;
+    for (int e = 0; e < E; e++) den += prob[e];
+    s_den = den;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) prob[e] = prob[e] / s_den;
+  __syncthreads();
+  __shared__ int s_idx[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
+  for (int j = 0; j < K; j++) {
+    VI best = {-1.0, -1};
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      bool used = false;
+      for (int p = 0; p < j; p++) used |= s_idx[p] == e;
+      float pv = prob[e];
+      if (!used && pv > -1.0f) best = vi_better(best, VI{(double)pv, e});
+    }
+    best = block_argmax(best, red);
+    if (threadIdx.x == 0) {
+      s_idx[j] = best.i;
+      s_w[j] = best.i >= 0 ? (float)best.v : -1.0f;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float topden = 0.0f;
+    for (int j = 0; j < K; j++) topden += s_w[j];
+    for (int j = 0; j < K; j++) {
+      idx[j] = s_idx[j];
+      weight[j] = s_w[j] / topden;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ void k_topk_exact(Work w) {
+  __shared__ VI red[16];
+  __shared__ float prob[4096];
+  int t = blockIdx.x;
+  if (w.certified[t]) return;
+  topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
+                   prob, red);
+}
+
+__global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx, float *weight) {
+  __shared__ VI red[16];
+  __shared__ float prob[4096];
+  int t = blockIdx.x;
+  topk_exact_block(logits + (size_t)t * E, E, K, idx + (size_t)t * K, weight + (size_t)t * K, prob, red);
+}
+
+// ---------------------------------------------------------------------------
+// 5. bucketing (c/qwen.c:4168 expert order, 3956-3968 token order): a stable
+// counting sort through per-expert token bitmaps.  Also emits the routed work
+// items {expert, first CSR entry, count <= 8} and pos[t*K+k] (CSR entry of
+// route (t,k)).  One block of 1024 threads; T <= 2048, E <= 512.
+// ---------------------------------------------------------------------------
+__device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
+                             int *pos, int4 *items, int *nitems, unsigned *bits, int *cnt, int *iofs) {
+  int words = (T + 31) / 32;
+  for (int i = threadIdx.x; i < E * words; i += blockDim.x) bits[i] = 0;
+  __syncthreads();
+  for (int r = threadIdx.x; r < T * K; r += blockDim.x) {
+    int e = idx[r];
+    if (e >= 0 && e < E) atomicOr(&bits[e * words + r / K / 32], 1u << ((r / K) & 31));
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int c = 0;
+    for (int q = 0; q < words; q++) c += __popc(bits[e * words + q]);
+    cnt[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0, ia = 0;
+    for (int e = 0; e < E; e++) {
+      offsets[e] = acc;
+      iofs[e] = ia;
+      acc += cnt[e];
+      ia += (cnt[e] + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+    }
+    offsets[E] = acc;
+    iofs[E] = ia;
+    *nitems = ia;
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < T * K; r += blockDim.x) {
+    int e = idx[r], t = r / K, k = r % K;
+    if (e < 0 || e >= E) {
+      pos[r] = -1;
+      continue;
+    }
+    // the reference's gather takes the first matching k of a token
+    bool first = true;
+    for (int k2 = 0; k2 < k; k2++) first &= idx[t * K + k2] != e;
+    if (!first) {
+      pos[r] = -1;
+      continue;
+    }
+    const unsigned *b = bits + e * words;
+    int rank = 0;
+    for (int q = 0; q < t / 32; q++) rank += __popc(b[q]);
+    rank += __popc(b[t / 32] & ((1u << (t & 31)) - 1u));
+    int p = offsets[e] + rank;
+    btok[p] = t;
+    bslot[p] = k;
+    pos[r] = p;
+  }
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int n = cnt[e];
+    for (int i = 0, it = iofs[e]; i < n; i += kMaxTokensPerItem, it++)
+      items[it] = make_int4(e, offsets[e] + i, min(kMaxTokensPerItem, n - i), 0);
+  }
+}
+
+__global__ void k_bucket(Work w) {
+  extern __shared__ unsigned smem[];
+  int words = (w.T + 31) / 32;
+  unsigned *bits = smem;
+  int *cnt = (int *)(smem + w.E * words);
+  int *iofs = cnt + w.E;
+  bucket_block(w.idx, w.T, w.K, w.E, w.offsets, w.btok, w.bslot, w.pos, w.items, w.nitems, bits, cnt, iofs);
+}
+
+__global__ void k_bucket_only(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
+                              int *pos, int4 *items, int *nitems) {
+  extern __shared__ unsigned smem[];
+  int words = (T + 31) / 32;
+  unsigned *bits = smem;
+  int *cnt = (int *)(smem + E * words);
+  int *iofs = cnt + E;
+  bucket_block(idx, T, K, E, offsets, btok, bslot, pos, items, nitems, bits, cnt, iofs);
+}
+
+// ---------------------------------------------------------------------------
+// routed tile GEMV on int8 MFMA.  For row tile rt and groups [g0, g1) of a
+// tiled matrix, accumulates into acc[i] (rows 4*kb+i) the group-scaled dots
+// with up to 8 token activations given as digit arrays.  Valid results sit in
+// lanes with odd column c = lane%16: token c/2.
+// ---------------------------------------------------------------------------
+template <int FMT>
+__device__ __forceinline__ void unpack_tile(const unsigned char *tp, v4i &a0, v4i &a1) {
+  if (FMT == 4) {
+    uint4 q = *(const uint4 *)tp;
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    uint32_t d[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      d[2 * i] = w[i] & 0x0F0F0F0Fu;
+      d[2 * i + 1] = (w[i] >> 4) & 0x0F0F0F0Fu;
+    }
+    a0 = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    a1 = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+  } else {
+    const uint32_t *p = (const uint32_t *)tp;
+    uint32_t L0 = p[0], L1 = p[1], H = p[2];
+    uint32_t d[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t L = j < 4 ? L0 : L1;
+      uint32_t lo = (L >> (2 * (j & 3))) & 0x03030303u;
+      uint32_t hi = j <= 2 ? (H << (2 - j)) : (H >> (j - 2));
+      d[j] = lo | (hi & 0x04040404u);
+    }
+    a0 = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    a1 = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+  }
+}
+
+struct TokDigits {
+  const signed char *d1[kMaxTokensPerItem];  // per token digit arrays (group-major)
+  const signed char *d2[kMaxTokensPerItem];
+  const float4 *gp[kMaxTokensPerItem];
+};
+
+template <int FMT>
+__device__ __forceinline__ void tile_gemv(const unsigned char *codes, const float *scales, int rt, int ng, int g0,
+                                          int g1, const signed char *dsrc, const float4 *gpsrc, float acc[4],
+                                          int lane) {
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+  const int kb = lane >> 4;
+  for (int g = g0; g < g1; g++) {
+    v4i a0, a1;
+    unpack_tile<FMT>(codes + ((size_t)(rt * ng + g) * 64 + lane) * BPL, a0, a1);
+    v4i b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
+    float dsc = 0.0f;
+    int Q = 0;
+    if (dsrc) {
+      b0 = *(const v4i *)(dsrc + g * kGroup + kb * 16);
+      b1 = *(const v4i *)(dsrc + g * kGroup + 64 + kb * 16);
+    }
+    if (gpsrc) {
+      float4 p = gpsrc[g];
+      bool second = lane & 1;
+      dsc = second ? p.y : p.x;
+      Q = __float_as_int(second ? p.w : p.z);
+    }
+    v4i c = {0, 0, 0, 0};
+    c = mfma_i8(a0, b0, c);
+    c = mfma_i8(a1, b1, c);
+    float4 sc = *(const float4 *)(scales + (size_t)(rt * ng + g) * kTileRows + 4 * kb);
+    float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float f = (float)(c[i] - OFF * Q) * dsc;
+      float tsum = f + dpp_row_shr1(f);
+      acc[i] = __builtin_fmaf(tsum, scv[i], acc[i]);
+    }
+  }
+}
+
+// B-operand source for lane column c: token c/2's digit array (c%2), or null
+__device__ inline void lane_digit_src(int lane, int cnt, const signed char *const *d1s, const signed char *const *d2s,
+                                      const float4 *const *gps, const signed char *&dsrc, const float4 *&gp) {
+  int c = lane & 15, tt = c >> 1;
+  dsrc = nullptr;
+  gp = nullptr;
+  if (tt < cnt) {
+    dsrc = (c & 1) ? d2s[tt] : d1s[tt];
+    gp = gps[tt];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 6. shared expert gate/up, IDOT on MFMA: exact int32 dots for 16 rows x up
+// to 16 tokens, k split over the block's waves, then h = silu(g)*u with the
+// reference's rounding.  grid (Ish/16, ceil(T/16)), 512 threads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void idot_tile(const signed char *W, int ld, int row0, int kc0, int kc1,
+                                          const signed char *xq, int xld, int t0, int T, v4i &c, int lane) {
+  const int r = lane & 15, kb = lane >> 4;
+  const signed char *arow = W + (size_t)(row0 + r) * ld + kb * 16;
+  int tok = t0 + r;  // B column = lane%16 = token
+  const signed char *brow = tok < T ? xq + (size_t)tok * xld + kb * 16 : nullptr;
+  for (int kc = kc0; kc < kc1; kc++) {
+    v4i a = *(const v4i *)(arow + kc * 64);
+    v4i b = {0, 0, 0, 0};
+    if (brow) b = *(const v4i *)(brow + kc * 64);
+    c = mfma_i8(a, b, c);
+  }
+}
+
+__global__ void k_shared_swiglu(Work w, const signed char *gq, const float *gs, const signed char *uq,
+                                const float *us) {
+  __shared__ int part[8][2][256];
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int rt = blockIdx.x, t0 = blockIdx.y * kSharedTokens;
+  int nk = w.H / 64;
+  int per = (nk + nw - 1) / nw, kc0 = wave * per, kc1 = min(nk, kc0 + per);
+  v4i cg = {0, 0, 0, 0}, cu = {0, 0, 0, 0};
+  if (kc0 < kc1) {
+    idot_tile(gq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cg, lane);
+    idot_tile(uq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cu, lane);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    part[wave][0][lane * 4 + i] = cg[i];
+    part[wave][1][lane * 4 + i] = cu[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int kb = lane >> 4, tok = t0 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int dg = 0, du = 0;
+      for (int v = 0; v < nw; v++) {
+        dg += part[v][0][lane * 4 + i];
+        du += part[v][1][lane * 4 + i];
+      }
+      int row = rt * kTileRows + 4 * kb + i;
+      if (tok < w.T) {
+        float sx = w.sx[tok];
+        float g = (float)dg * gs[row] * sx;
+        float u = (float)du * us[row] * sx;
+        w.hsh[(size_t)tok * w.Ish + row] = silu_ref(g) * u;
+      }
+    }
+  }
+}
+
+// qrow_i8 of the shared hidden rows + digits of the routed hidden rows
+__global__ void k_prep_hidden(Work w) {
+  __shared__ float red[16];
+  int b = blockIdx.x;
+  if (b < w.T) {
+    float s = qrow_i8_block(w.hsh + (size_t)b * w.Ish, w.Ish, w.hq + (size_t)b * w.Ish, red);
+    if (threadIdx.x == 0) w.shx[b] = s;
+    return;
+  }
+  int p = b - w.T;
+  if (p >= w.offsets[w.E]) return;
+  quantize_digits(w.hroute + (size_t)p * w.I, w.I, w.ngi, w.hd1 + (size_t)p * w.Ip, w.hd2 + (size_t)p * w.Ip,
+                  w.hgp + (size_t)p * w.ngi);
+}
+
+// ---------------------------------------------------------------------------
+// 7. routed gate/up: item = (expert, <=8 tokens); 4 waves split the H groups,
+// then h = silu(g)*u per token.  grid (I/16, min(items bound, 1024)), 256 thr.
+// ---------------------------------------------------------------------------
+template <int FMT>
+__global__ void k_expert_gateup(Work w, const unsigned char *codes, const float *scales, size_t expert_codes,
+                                size_t expert_scales, size_t gate_codes, size_t gate_scales) {
+  __shared__ float part[4][2][64][4];
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int rt = blockIdx.x;
+  int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
+    int4 item = w.items[it];
+    int e = item.x, p0 = item.y, cnt = item.z;
+    const signed char *d1s[kMaxTokensPerItem], *d2s[kMaxTokensPerItem];
+    const float4 *gps[kMaxTokensPerItem];
+    for (int j = 0; j < kMaxTokensPerItem; j++) {
+      int tok = j < cnt ? w.btok[p0 + j] : 0;
+      d1s[j] = w.xd1 + (size_t)tok * w.Hp;
+      d2s[j] = w.xd2 + (size_t)tok * w.Hp;
+      gps[j] = w.xgp + (size_t)tok * w.ngh;
+    }
+    const signed char *dsrc;
+    const float4 *gp;
+    lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
+    const unsigned char *ce = codes + (size_t)e * expert_codes;
+    const float *se = scales + (size_t)e * expert_scales;
+    int per = (w.ngh + 3) / 4, g0 = wave * per, g1 = min(w.ngh, g0 + per);
+    float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
+    if (g0 < g1) {
+      tile_gemv<FMT>(ce, se, rt, w.ngh, g0, g1, dsrc, gp, ag, lane);
+      tile_gemv<FMT>(ce + gate_codes, se + gate_scales, rt, w.ngh, g0, g1, dsrc, gp, au, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      part[wave][0][lane][i] = ag[i];
+      part[wave][1][lane][i] = au[i];
+    }
+    __syncthreads();
+    if (wave == 0 && (lane & 1) && ((lane & 15) >> 1) < cnt) {
+      int tt = (lane & 15) >> 1, kb = lane >> 4;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float g = part[0][0][lane][i], u = part[0][1][lane][i];
+        for (int v = 1; v < 4; v++) {
+          g += part[v][0][lane][i];
+          u += part[v][1][lane][i];
+        }
+        int row = rt * kTileRows + 4 * kb + i;
+        w.hroute[(size_t)(p0 + tt) * w.I + row] = silu_ref(g) * u;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 8. down: routed items -> rout[p][row]; shared token chunks (IDOT) ->
+// shout[t][row].  grid (H/16, n_item_slots + ceil(T/16)), 64 threads.
+// ---------------------------------------------------------------------------
+template <int FMT>
+__global__ void k_down(Work w, const unsigned char *codes, const float *scales, size_t expert_codes,
+                       size_t expert_scales, size_t down_codes_off, size_t down_scales_off, int item_slots,
+                       const signed char *dq, const float *ds) {
+  int lane = threadIdx.x;
+  int rt = blockIdx.x;
+  int kb = lane >> 4;
+  if ((int)blockIdx.y >= item_slots) {
+    int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens;
+    v4i c = {0, 0, 0, 0};
+    idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
+    int tok = t0 + (lane & 15);
+    if (tok < w.T) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        int row = rt * kTileRows + 4 * kb + i;
+        w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+      }
+    }
+    return;
+  }
+  int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += item_slots) {
+    int4 item = w.items[it];
+    int e = item.x, p0 = item.y, cnt = item.z;
+    const signed char *d1s[kMaxTokensPerItem], *d2s[kMaxTokensPerItem];
+    const float4 *gps[kMaxTokensPerItem];
+    for (int j = 0; j < kMaxTokensPerItem; j++) {
+      int p = p0 + (j < cnt ? j : 0);
+      d1s[j] = w.hd1 + (size_t)p * w.Ip;
+      d2s[j] = w.hd2 + (size_t)p * w.Ip;
+      gps[j] = w.hgp + (size_t)p * w.ngi;
+    }
+    const signed char *dsrc;
+    const float4 *gp;
+    lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
+    float acc[4] = {0, 0, 0, 0};
+    tile_gemv<FMT>(codes + (size_t)e * expert_codes + down_codes_off,
+                   scales + (size_t)e * expert_scales + down_scales_off, rt, w.ngi, 0, w.ngi, dsrc, gp, acc, lane);
+    if ((lane & 1) && ((lane & 15) >> 1) < cnt) {
+      int tt = (lane & 15) >> 1;
+#pragma unroll
+      for (int i = 0; i < 4; i++) w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + i] = acc[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 9. combine.  One token (moe_forward 3734-3737): out = fma chain over k of
+// tmp_k * w_k, then fma(shared, sg).  Many tokens (moe_prefill_grouped
+// 4151-4152, 3977, 4203): shared *= sg, routed = tmp*w, out = sum_k routed +
+// shared.  grid (ceil(H/256), T), 256 threads.
+// ---------------------------------------------------------------------------
+__global__ void k_combine(Work w, float *y, int *route_idx, float *route_weight) {
+  int h = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (h < w.H) {
+    float sg = w.sgate[t];
+    float sh = w.shout[(size_t)t * w.H + h];
+    float out = 0.0f;
+    if (w.T == 1) {
+      for (int k = 0; k < w.K; k++) {
+        int p = w.pos[(size_t)t * w.K + k];
+        float v = p >= 0 ? w.rout[(size_t)p * w.H + h] : 0.0f;
+        out = __builtin_fmaf(v, w.w[(size_t)t * w.K + k], out);
+      }
+      out = __builtin_fmaf(sh, sg, out);
+    } else {
+      float shs = sh * sg;
+      for (int k = 0; k < w.K; k++) {
+        int p = w.pos[(size_t)t * w.K + k];
+        float v = p >= 0 ? w.rout[(size_t)p * w.H + h] : 0.0f;
+        float r = v * w.w[(size_t)t * w.K + k];
+        out = out + r;
+      }
+      out = out + shs;
+    }
+    y[(size_t)t * w.H + h] = out;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < w.K) {
+    size_t r = (size_t)t * w.K + threadIdx.x;
+    if (route_idx) route_idx[r] = w.idx[r];
+    if (route_weight) route_weight[r] = w.w[r];
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+static int layer_alloc(ColiMoeLayer *L, void **p, size_t bytes, const char *what) {
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return fail_hip(what, e);
+  L->alloc[L->nalloc++] = *p;
+  L->bytes += bytes;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, const ColiMoeShape *s) {
+  if (!ctx || !out || !s) return fail_arg("coli_cuda_moe_layer_create: null argument");
+  *out = nullptr;
+  if (s->hidden <= 0 || s->experts <= 0 || s->topk <= 0 || s->intermediate <= 0 ||
+      s->shared_intermediate <= 0 || s->hidden % 64 || s->intermediate % 16 || s->shared_intermediate % 64 ||
+      s->topk > kMaxTopK || s->topk > s->experts || s->experts > 4096 || s->group_size != kGroup ||
+      (s->expert_format != 3 && s->expert_format != 4))
+    return fail_arg("coli_cuda_moe_layer_create: unsupported shape (H%%64, I%%16, I_sh%%64, "
+                    "group_size 128, format 3|4, topk<=32, experts<=4096)");
+  ColiMoeLayer *L = (ColiMoeLayer *)calloc(1, sizeof(ColiMoeLayer));
+  if (!L) return fail_arg("out of memory creating MoE layer");
+  L->sh = *s;
+  int H = s->hidden, I = s->intermediate, E = s->experts, Ish = s->shared_intermediate;
+  int bpl = tile_bytes_per_lane(s->expert_format);
+  L->ngh = (H + kGroup - 1) / kGroup;
+  L->ngi = (I + kGroup - 1) / kGroup;
+  L->gate_codes = (size_t)(I / kTileRows) * L->ngh * 64 * bpl;
+  L->down_codes = (size_t)(H / kTileRows) * L->ngi * 64 * bpl;
+  L->gate_scales = (size_t)I * L->ngh;
+  L->down_scales = (size_t)H * L->ngi;
+  L->expert_codes = 2 * L->gate_codes + L->down_codes;
+  L->expert_scales = 2 * L->gate_scales + L->down_scales;
+  int rc = layer_alloc(L, (void **)&L->router, (size_t)E * H * 4, "router allocation") ||
+           layer_alloc(L, (void **)&L->sgate_row, (size_t)H * 4, "shared gate allocation") ||
+           layer_alloc(L, (void **)&L->sh_gq, (size_t)Ish * H, "shared gate allocation") ||
+           layer_alloc(L, (void **)&L->sh_uq, (size_t)Ish * H, "shared up allocation") ||
+           layer_alloc(L, (void **)&L->sh_dq, (size_t)H * Ish, "shared down allocation") ||
+           layer_alloc(L, (void **)&L->sh_gs, (size_t)Ish * 4, "shared scale allocation") ||
+           layer_alloc(L, (void **)&L->sh_us, (size_t)Ish * 4, "shared scale allocation") ||
+           layer_alloc(L, (void **)&L->sh_ds, (size_t)H * 4, "shared scale allocation") ||
+           layer_alloc(L, (void **)&L->codes, (size_t)E * L->expert_codes, "expert code allocation") ||
+           layer_alloc(L, (void **)&L->scales, (size_t)E * L->expert_scales * 4, "expert scale allocation") ||
+           layer_alloc(L, (void **)&L->stats, 64, "router stats allocation");
+  if (rc) {
+    coli_cuda_moe_layer_destroy(ctx, L);
+    return -1;
+  }
+  hipMemsetAsync(L->stats, 0, 64, ctx->stream);
+  *out = L;
+  return launch_status("coli_cuda_moe_layer_create");
+}
+
+extern "C" void coli_cuda_moe_layer_destroy(ColiCuda *ctx, ColiMoeLayer *L) {
+  if (!L) return;
+  if (ctx) hipStreamSynchronize(ctx->stream);
+  for (int i = 0; i < L->nalloc; i++) hipFree(L->alloc[i]);
+  free(L);
+}
+
+extern "C" size_t coli_cuda_moe_layer_bytes(const ColiMoeLayer *L) { return L ? L->bytes : 0; }
+
+extern "C" float *coli_cuda_moe_layer_router(ColiMoeLayer *L) { return L ? L->router : nullptr; }
+
+extern "C" int coli_cuda_moe_set_router_mode(ColiMoeLayer *L, int mode) {
+  if (!L || (mode != 0 && mode != 1)) return fail_arg("coli_cuda_moe_set_router_mode: invalid argument");
+  L->router_mode = mode;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_layer_set_router(ColiCuda *ctx, ColiMoeLayer *L, const float *router,
+                                              const float *shared_gate) {
+  if (!ctx || !L || !router || !shared_gate) return fail_arg("coli_cuda_moe_layer_set_router: null argument");
+  hipMemcpyAsync(L->router, router, (size_t)L->sh.experts * L->sh.hidden * 4, hipMemcpyDeviceToDevice,
+                 ctx->stream);
+  hipMemcpyAsync(L->sgate_row, shared_gate, (size_t)L->sh.hidden * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  return launch_status("coli_cuda_moe_layer_set_router");
+}
+
+extern "C" int coli_cuda_moe_layer_set_shared_q8(ColiCuda *ctx, ColiMoeLayer *L, const signed char *gq,
+                                                 const float *gs, const signed char *uq, const float *us,
+                                                 const signed char *dq, const float *ds) {
+  if (!ctx || !L || !gq || !gs || !uq || !us || !dq || !ds)
+    return fail_arg("coli_cuda_moe_layer_set_shared_q8: null argument");
+  size_t H = L->sh.hidden, I = L->sh.shared_intermediate;
+  hipStream_t st = ctx->stream;
+  hipMemcpyAsync(L->sh_gq, gq, I * H, hipMemcpyDeviceToDevice, st);
+  hipMemcpyAsync(L->sh_uq, uq, I * H, hipMemcpyDeviceToDevice, st);
+  hipMemcpyAsync(L->sh_dq, dq, H * I, hipMemcpyDeviceToDevice, st);
+  hipMemcpyAsync(L->sh_gs, gs, I * 4, hipMemcpyDeviceToDevice, st);
+  hipMemcpyAsync(L->sh_us, us, I * 4, hipMemcpyDeviceToDevice, st);
+  hipMemcpyAsync(L->sh_ds, ds, H * 4, hipMemcpyDeviceToDevice, st);
+  return launch_status("coli_cuda_moe_layer_set_shared_q8");
+}
+
+static int repack_matrix(ColiCuda *ctx, unsigned char *dst_codes, float *dst_scales, const unsigned char *q,
+                         const float *s, int rows, int cols, int fmt) {
+  int ng = (cols + kGroup - 1) / kGroup;
+  int rb = fmt == 4 ? ng * kGroup / 2 : ng * kGroup * 3 / 8;
+  size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
+  k_repack_codes<<<blocks_for(lanes, 256), 256, 0, ctx->stream>>>(dst_codes, q, rows, cols, rb, ng, fmt);
+  size_t ns = (size_t)rows * ng;
+  k_repack_scales<<<blocks_for(ns, 256), 256, 0, ctx->stream>>>(dst_scales, s, rows, ng);
+  return launch_status("expert repack");
+}
+
+extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, int expert,
+                                              const unsigned char *gq, const float *gs, const unsigned char *uq,
+                                              const float *us, const unsigned char *dq, const float *ds) {
+  if (!ctx || !L || !gq || !gs || !uq || !us || !dq || !ds)
+    return fail_arg("coli_cuda_moe_layer_set_expert: null argument");
+  if (expert < 0 || expert >= L->sh.experts)
+    return fail_arg("coli_cuda_moe_layer_set_expert: expert %d outside [0,%d)", expert, L->sh.experts);
+  int H = L->sh.hidden, I = L->sh.intermediate, fmt = L->sh.expert_format;
+  unsigned char *c = L->codes + (size_t)expert * L->expert_codes;
+  float *sc = L->scales + (size_t)expert * L->expert_scales;
+  if (repack_matrix(ctx, c, sc, gq, gs, I, H, fmt) ||
+      repack_matrix(ctx, c + L->gate_codes, sc + L->gate_scales, uq, us, I, H, fmt) ||
+      repack_matrix(ctx, c + 2 * L->gate_codes, sc + 2 * L->gate_scales, dq, ds, H, I, fmt))
+    return -1;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long seed,
+                                              int layer_index) {
+  if (!ctx || !L) return fail_arg("coli_cuda_moe_layer_synthesize: null argument");
+  int H = L->sh.hidden, I = L->sh.intermediate, E = L->sh.experts, Ish = L->sh.shared_intermediate;
+  int fmt = L->sh.expert_format;
+  uint32_t li = (uint32_t)layer_index;
+  hipStream_t st = ctx->stream;
+  size_t n;
+  n = (size_t)E * H;
+  k_synth_normal<<<blocks_for(n, 256), 256, 0, st>>>(L->router, n, sw_key(seed, li, 0, SW_T_ROUTER), 0.02f, 0);
+  k_synth_normal<<<blocks_for(H, 256), 256, 0, st>>>(L->sgate_row, H, sw_key(seed, li, 0, SW_T_SHARED_GATE),
+                                                     0.02f, 0);
+  n = (size_t)Ish * H;
+  k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_gq, n, sw_key(seed, li, 0, SW_T_SH_GATE_Q));
+  k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_uq, n, sw_key(seed, li, 0, SW_T_SH_UP_Q));
+  k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_dq, n, sw_key(seed, li, 0, SW_T_SH_DOWN_Q));
+  k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_gs, Ish, sw_key(seed, li, 0, SW_T_SH_GATE_S), 0.01f, 1);
+  k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_us, Ish, sw_key(seed, li, 0, SW_T_SH_UP_S), 0.01f, 1);
+  k_synth_normal<<<blocks_for(H, 256), 256, 0, st>>>(L->sh_ds, H, sw_key(seed, li, 0, SW_T_SH_DOWN_S), 0.01f, 1);
+  // routed experts: container bytes into scratch, repacked per matrix
+  int rbh = fmt == 4 ? L->ngh * kGroup / 2 : L->ngh * kGroup * 3 / 8;
+  int rbi = fmt == 4 ? L->ngi * kGroup / 2 : L->ngi * kGroup * 3 / 8;
+  size_t need = (size_t)I * rbh > (size_t)H * rbi ? (size_t)I * rbh : (size_t)H * rbi;
+  if (ensure_scratch(ctx, kScrSetup, need, "synthesis scratch")) return -1;
+  unsigned char *tmp = (unsigned char *)ctx->scratch[kScrSetup];
+  for (int e = 0; e < E; e++) {
+    unsigned char *c = L->codes + (size_t)e * L->expert_codes;
+    float *sc = L->scales + (size_t)e * L->expert_scales;
+    const int tq[3] = {SW_T_GATE_Q, SW_T_UP_Q, SW_T_DOWN_Q}, ts[3] = {SW_T_GATE_S, SW_T_UP_S, SW_T_DOWN_S};
+    for (int m = 0; m < 3; m++) {
+      int rows = m < 2 ? I : H, cols = m < 2 ? H : I, rb = m < 2 ? rbh : rbi, ng = m < 2 ? L->ngh : L->ngi;
+      size_t nb = (size_t)rows * rb;
+      k_synth_bytes<<<blocks_for((nb + 7) / 8, 256), 256, 0, st>>>(tmp, nb, sw_key(seed, li, (uint32_t)e, tq[m]));
+      size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
+      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(c + m * L->gate_codes, tmp, rows, cols, rb, ng, fmt);
+      k_synth_scales_tiled<<<blocks_for((size_t)rows * ng, 256), 256, 0, st>>>(
+          sc + m * L->gate_scales, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
+    }
+  }
+  return launch_status("coli_cuda_moe_layer_synthesize");
+}
+
+static Work make_work(const ColiMoeLayer *L, int T) {
+  Work w;
+  memset(&w, 0, sizeof(w));
+  w.T = T;
+  w.H = L->sh.hidden;
+  w.E = L->sh.experts;
+  w.K = L->sh.topk;
+  w.I = L->sh.intermediate;
+  w.Ish = L->sh.shared_intermediate;
+  w.ngh = L->ngh;
+  w.ngi = L->ngi;
+  w.Hp = w.ngh * kGroup;
+  w.Ip = w.ngi * kGroup;
+  return w;
+}
+
+// dynamic LDS above 64 KiB must be enabled per kernel (gfx950: 160 KiB/CU)
+static int set_lds(const void *fn, size_t bytes) {
+  if (bytes > 160 * 1024) return fail_arg("MoE bucketing needs %zu bytes of LDS (> 160 KiB)", bytes);
+  if (bytes <= 64 * 1024) return 0;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  return e == hipSuccess ? 0 : fail_hip("hipFuncSetAttribute", e);
+}
+
+static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
+  hipStream_t st = ctx->stream;
+  k_prep_x<<<w.T, 256, 0, st>>>(w, x);
+  k_router_bounds<<<dim3((w.E + 1 + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router, L->sgate_row);
+  k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
+  k_exact_logits<<<dim3((w.E + 63) / 64, w.T), 64, 0, st>>>(w, x, L->router);
+  k_topk_exact<<<w.T, 512, 0, st>>>(w);
+  return launch_status("MoE routing kernels");
+}
+
+static int prepare(ColiCuda *ctx, ColiMoeLayer *L, int T, Work &w) {
+  if (T <= 0 || T > kMaxTokens) return fail_arg("MoE step: tokens %d outside [1,%d]", T, kMaxTokens);
+  w = make_work(L, T);
+  size_t bytes = carve(w, nullptr);
+  if (ensure_scratch(ctx, kScrXPrep, bytes, "MoE workspace allocation")) return -1;
+  carve(w, (char *)ctx->scratch[kScrXPrep]);
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *L, const float *x, int tokens, int *idx,
+                                   float *weight) {
+  if (!ctx || !L || !x || !idx || !weight) return fail_arg("coli_cuda_moe_route: null argument");
+  Work w;
+  if (prepare(ctx, L, tokens, w)) return -1;
+  if (route_launch(ctx, L, w, x)) return -1;
+  hipMemcpyAsync(idx, w.idx, (size_t)tokens * w.K * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  hipMemcpyAsync(weight, w.w, (size_t)tokens * w.K * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  return launch_status("coli_cuda_moe_route");
+}
+
+extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int tokens,
+                                     int *route_idx, float *route_weight) {
+  if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
+  Work w;
+  if (prepare(ctx, L, tokens, w)) return -1;
+  hipStream_t st = ctx->stream;
+  int T = tokens;
+  if (route_launch(ctx, L, w, x)) return -1;
+  size_t bucket_lds = (size_t)w.E * ((T + 31) / 32) * 4 + (size_t)(2 * w.E + 1) * 4;
+  if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
+  k_bucket<<<1, 1024, bucket_lds, st>>>(w);
+  k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedTokens - 1) / kSharedTokens), 512, 0, st>>>(
+      w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+  int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+  int slots = item_bound < T * w.K ? item_bound : T * w.K;
+  if (slots > 1024) slots = 1024;
+  if (L->sh.expert_format == 4)
+    k_expert_gateup<4><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->codes, L->scales, L->expert_codes,
+                                                                    L->expert_scales, L->gate_codes,
+                                                                    L->gate_scales);
+  else
+    k_expert_gateup<3><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->codes, L->scales, L->expert_codes,
+                                                                    L->expert_scales, L->gate_codes,
+                                                                    L->gate_scales);
+  k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
+  int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
+  if (L->sh.expert_format == 4)
+    k_down<4><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
+        w, L->codes, L->scales, L->expert_codes, L->expert_scales, 2 * L->gate_codes, 2 * L->gate_scales, slots,
+        L->sh_dq, L->sh_ds);
+  else
+    k_down<3><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
+        w, L->codes, L->scales, L->expert_codes, L->expert_scales, 2 * L->gate_codes, 2 * L->gate_scales, slots,
+        L->sh_dq, L->sh_ds);
+  k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
+  return launch_status("coli_cuda_moe_forward");
+}
+
+extern "C" int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long *tokens,
+                                         unsigned long long *fallbacks) {
+  if (!ctx || !L || !tokens || !fallbacks) return fail_arg("coli_cuda_moe_route_stats: null argument");
+  unsigned long long s[2];
+  hipError_t e = hipMemcpyAsync(s, L->stats, sizeof(s), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return fail_hip("coli_cuda_moe_route_stats", e);
+  *tokens = s[0];
+  *fallbacks = s[1];
+  return 0;
+}
+
+extern "C" int coli_cuda_router_topk(ColiCuda *ctx, const float *logits, int tokens, int experts, int topk,
+                                     int *idx, float *weight) {
+  if (!ctx || !logits || !idx || !weight || tokens <= 0 || experts <= 0 || experts > 4096 || topk <= 0 ||
+      topk > kMaxTopK)
+    return fail_arg("coli_cuda_router_topk: invalid argument");
+  k_router_topk_logits<<<tokens, 512, 0, ctx->stream>>>(logits, experts, topk, idx, weight);
+  return launch_status("coli_cuda_router_topk");
+}
+
+extern "C" int coli_cuda_moe_bucket(ColiCuda *ctx, const int *idx, int tokens, int topk, int experts, int *offsets,
+                                    int *token, int *slot) {
+  if (!ctx || !idx || !offsets || !token || !slot || tokens <= 0 || tokens > kMaxTokens || topk <= 0 ||
+      experts <= 0 || experts > 512)
+    return fail_arg("coli_cuda_moe_bucket: invalid argument (tokens<=%d, experts<=512)", kMaxTokens);
+  size_t R = (size_t)tokens * topk;
+  size_t need = R * 4 + (R + experts) * 16 + 256;
+  if (ensure_scratch(ctx, kScrRoutes, need, "bucket scratch")) return -1;
+  char *b = (char *)ctx->scratch[kScrRoutes];
+  int *pos = (int *)b;
+  int4 *items = (int4 *)(b + ((R * 4 + 15) & ~(size_t)15));
+  int *nitems = (int *)(b + need - 64);
+  size_t lds = (size_t)experts * ((tokens + 31) / 32) * 4 + (size_t)(2 * experts + 1) * 4;
+  if (set_lds((const void *)k_bucket_only, lds)) return -1;
+  k_bucket_only<<<1, 1024, lds, ctx->stream>>>(idx, tokens, topk, experts, offsets, token, slot, pos, items,
+                                                nitems);
+  return launch_status("coli_cuda_moe_bucket");
+}

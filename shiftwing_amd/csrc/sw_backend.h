@@ -1,0 +1,57 @@
+// Internal: the context object behind the C ABI and its error / scratch
+// helpers.  Semantics follow c/backend_cuda.cu:47-177 (thread-local error
+// text, 0/-1 returns, one non-blocking stream per context, backend-owned
+// scratch grown on demand and freed by coli_cuda_destroy).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "shiftwing_moe.h"
+
+namespace sw {
+
+enum Scratch {
+  kScrSetup = 0,   // per-call pointer tables / route maps (legacy grouped calls)
+  kScrHidden,      // routed hidden activations
+  kScrRouteOut,    // per-route down outputs (legacy batch)
+  kScrGate,        // shared / misc fp32 vectors
+  kScrUp,
+  kScrWeight,
+  kScrXPrep,       // activation digits (fast path)
+  kScrRouter,      // router logit bounds (fast path)
+  kScrRoutes,      // idx / weights / buckets (fast path)
+  kScrShared,      // shared expert int32 partials + h (fast path)
+  kScrCount
+};
+
+}  // namespace sw
+
+struct ColiCuda {
+  int device;
+  int major, minor;
+  int sm_count;
+  int shared_per_block;
+  int async_alloc;
+  char name[256];
+  hipStream_t stream;
+  void *scratch[sw::kScrCount];
+  size_t scratch_cap[sw::kScrCount];
+  // stage profiling (CUDA_PROFILE_STAGES=1), c/backend_cuda.cu:118-131
+  int profile_stages, profile_pending, profile_shared_marked, profile_download_marked;
+  hipEvent_t profile_event[9];
+  double profile_ms[8];
+  unsigned long long profile_transactions;
+};
+
+namespace sw {
+
+int fail_hip(const char *where, hipError_t e);
+int fail_arg(const char *fmt, ...);
+int launch_status(const char *where);
+// Grow-only scratch owned by the context (released by coli_cuda_destroy).
+int ensure_scratch(ColiCuda *ctx, Scratch which, size_t bytes, const char *where);
+
+}  // namespace sw

@@ -1,0 +1,131 @@
+// Device helpers shared by the gfx950 kernels: bit-exact replicas of the host
+// arithmetic the reference relies on, wave64 reductions and the int8 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sw {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// expf, bit-identical to glibc 2.35's expf (the libm the reference links) on
+// every non-positive float -- the whole domain of router_topk's softmax
+// (logit - max <= 0) and of sigmoidf_stable (expf(-|x|)), c/qwen.c:307, 3423.
+//
+// Method: the published table-driven scheme of ARM optimized-routines that
+// glibc uses for expf (sysdeps/ieee754/flt-32/e_expf.c): x*N/ln2 = k + r with
+// N = 32, 2^(k/N) from a 32-entry table of correctly rounded 2^(i/32), and a
+// cubic in r evaluated in double, rounded to float once.  The table is
+// bits(2^(i/32)) - (i << 47); the coefficients are the published minimax
+// values.  glibc's x86-64 build with FMA (the ifunc chosen on every FMA host)
+// fuses the reduction r = x*N/ln2 - k; that variant is restated here with
+// explicit fma and was checked equal to host expf on all 2^31 non-positive
+// floats.
+// ---------------------------------------------------------------------------
+__device__ __constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL,
+    0x3fef9301d0125b51ULL, 0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL,
+    0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL, 0x3fef06fe0a31b715ULL,
+    0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL,
+    0x3feea47eb03a5585ULL, 0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL,
+    0x3feea11473eb0187ULL, 0x3feea589994cce13ULL, 0x3feeace5422aa0dbULL,
+    0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL,
+    0x3fef3720dcef9069ULL, 0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL,
+    0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float expf_glibc(float x) {
+  // Special cases first (glibc: NaN propagates, overflow -> inf,
+  // x < -0x1.9fe368p6 underflows to +0).
+  if (!(x == x)) return x + x;
+  if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
+  if (x < -0x1.9fe368p6f) return 0.0f;
+  constexpr double kN = 32.0;
+  constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN;
+  constexpr double kShift = 0x1.8p+52;
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / kN / kN / kN;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / kN / kN;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / kN;
+  double xd = (double)x;
+  double kd = __builtin_fma(kInvLn2N, xd, kShift);
+  uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+  kd -= kShift;
+  double r = __builtin_fma(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki & 31];
+  t += ki << (52 - 5);
+  double s = __builtin_bit_cast(double, t);
+  double z = __builtin_fma(kC0, r, kC1);
+  double r2 = r * r;
+  double y = __builtin_fma(kC2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// sigmoidf_stable / siluf, c/qwen.c:307-308, bit-exact with glibc expf.
+__device__ __forceinline__ float sigmoid_ref(float x) {
+  if (x >= 0.0f) {
+    float z = expf_glibc(-x);
+    return 1.0f / (1.0f + z);
+  }
+  float z = expf_glibc(x);
+  return z / (1.0f + z);
+}
+__device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+// exclusive prefix sum over the wave (lane order)
+__device__ __forceinline__ double wave_exclusive_scan(double v, int lane) {
+  double inc = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    double n = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += n;
+  }
+  return inc - v;
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA: C[16x16] += A[16x64] * B[64x16], exact int32.
+// Lane l supplies A row (l%16), B column (l%16), both for the k-slice (l/16)
+// (16 bytes each); C lane l holds rows 4*(l/16)+i, column l%16.
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Row shift within each 16-lane row: lane l receives lane l-1 (lane 0 of the
+// row receives 0).
+__device__ __forceinline__ float dpp_row_shr1(float v) {
+  int r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xF, 0xF, false);
+  return __builtin_bit_cast(float, r);
+}
+
+}  // namespace sw

@@ -1,0 +1,116 @@
+"""The fused MoE step (coli_cuda_moe_forward) against the reference CPU layer.
+
+Golden fixtures hold the compiled reference's outputs (moe_forward per token,
+moe_prefill_grouped for the token block) for synthetic layers that both sides
+regenerate from the seed; the oracle (C restatement) covers random seeds.
+Contract: router indices bit-exact; outputs within max-abs 1e-3 x RMS."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, assert_close_rms
+
+pytestmark = pytest.mark.gpu
+
+LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3"]
+
+
+def _load(name):
+    g = np.load(os.path.join(GOLDEN, f"layer_{name}.npz"))
+    H, E, K, I, Ish, fmt, gs, seed, layer, T = (int(v) for v in g["cfg"])
+    return g, dict(H=H, E=E, K=K, I=I, Ish=Ish, fmt=fmt, gs=gs, seed=seed, layer=layer, T=T)
+
+
+def _device_layer(be, c):
+    from shiftwing_amd import MoeLayer
+    L = MoeLayer(be, c["H"], c["E"], c["K"], c["I"], c["Ish"], c["fmt"], c["gs"])
+    L.synthesize(c["seed"], c["layer"])
+    return L
+
+
+def _pad_ok(c):
+    return c["H"] % 64 == 0 and c["I"] % 16 == 0 and c["Ish"] % 64 == 0
+
+
+@pytest.mark.parametrize("name", LAYERS)
+def test_decode_matches_reference(be, name):
+    g, c = _load(name)
+    if not _pad_ok(c):
+        pytest.skip("shape outside the fused path's tiling (H%64, I%16, I_sh%64)")
+    L = _device_layer(be, c)
+    for t in range(c["T"]):
+        print(f"[{name}] decode token {t}", flush=True)
+        y, idx, w = L.forward_host(g["x"][t])
+        assert np.array_equal(idx[0], g["idx"][t]), (t, idx[0], g["idx"][t])
+        assert np.max(np.abs(w[0] - g["weight"][t])) <= 1e-4
+        assert_close_rms(y[0], g["decode"][t], 1e-3, f"{name} decode t={t}")
+
+
+@pytest.mark.parametrize("name", LAYERS)
+def test_prefill_matches_reference(be, name):
+    g, c = _load(name)
+    if not _pad_ok(c):
+        pytest.skip("shape outside the fused path's tiling")
+    L = _device_layer(be, c)
+    print(f"[{name}] prefill T={c['T']}", flush=True)
+    y, idx, w = L.forward_host(g["x"])
+    assert np.array_equal(idx, g["idx"])
+    assert_close_rms(y, g["prefill"], 1e-3, f"{name} prefill")
+
+
+def test_exact_router_mode_bitexact_weights(be, oracle):
+    """Router mode 1 runs the serial fp32 chain for every token: indices and
+    weights equal router_topk over the reference's logits bit for bit."""
+    g, c = _load("s35_q4")
+    L = _device_layer(be, c)
+    L.set_router_mode(1)
+    for t in range(c["T"]):
+        y, idx, w = L.forward_host(g["x"][t])
+        assert np.array_equal(idx[0], g["idx"][t])
+        assert np.array_equal(w[0].view(np.uint32), g["weight"][t].view(np.uint32))
+        assert_close_rms(y[0], g["decode"][t], 1e-3, "exact-router decode")
+    tok, fb = L.route_stats()
+    assert tok == c["T"] and fb == c["T"]
+
+
+def test_upload_path_equals_device_synthesis(be, oracle):
+    """Weights uploaded in the container layout (set_router / set_shared_q8 /
+    set_expert, repacked on device) give the same result as device synthesis."""
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish, fmt = 256, 16, 4, 128, 128, 3
+    hl = oracle.host_layer(21, 2, H, E, K, I, Ish, fmt)
+    A = MoeLayer(be, H, E, K, I, Ish, fmt)
+    A.synthesize(21, 2)
+    B = MoeLayer(be, H, E, K, I, Ish, fmt)
+    keep = [be.upload(hl.router_w), be.upload(hl.shared_gate_row)]
+    B.set_router(*keep)
+    sh = [be.upload(a) for a in (hl.shared_gate.q, hl.shared_gate.s, hl.shared_up.q, hl.shared_up.s,
+                                 hl.shared_down.q, hl.shared_down.s)]
+    B.set_shared_q8(*sh)
+    for e in range(E):
+        bufs = [be.upload(a) for a in (hl.gq[e], hl.gsc[e], hl.uq[e], hl.usc[e], hl.dq[e], hl.dsc[e])]
+        B.set_expert(e, *bufs)
+        be.sync()
+    x = np.stack([oracle.synth_x(21, 2, t, H) for t in range(3)])
+    ya, ia, _ = A.forward_host(x)
+    yb, ib, _ = B.forward_host(x)
+    assert np.array_equal(ia, ib)
+    assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32))
+    want = oracle.moe_prefill(hl, x)
+    assert_close_rms(ya, want, 1e-3, "upload path vs oracle")
+
+
+@pytest.mark.parametrize("seed", [101, 202, 303])
+def test_random_seeds_vs_oracle_s35(be, oracle, seed):
+    H, E, K, I, Ish, fmt = 2048, 256, 8, 512, 512, 4
+    hl = oracle.host_layer(seed, 5, H, E, K, I, Ish, fmt)
+    from shiftwing_amd import MoeLayer
+    L = MoeLayer(be, H, E, K, I, Ish, fmt)
+    L.synthesize(seed, 5)
+    for t in range(4):
+        x = oracle.synth_x(seed, 5, t, H)
+        want, tr = oracle.moe_forward(hl, x, trace=True)
+        y, idx, w = L.forward_host(x)
+        assert np.array_equal(idx[0], tr["idx"])
+        assert_close_rms(y[0], want, 1e-3, f"seed {seed} t {t}")
