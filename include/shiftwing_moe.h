@@ -265,9 +265,7 @@ int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *layer, float *y,
                           const float *x, int tokens, int *route_idx,
                           float *route_weight);
 
-/* Router only: idx / weight [tokens x K]; logits (optional, [tokens x E])
- * receives the fp32 logits of the reference's serial dot when the exact path
- * ran for that token, NaN otherwise. */
+/* Router only: idx / weight [tokens x K] (device). */
 int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *layer, const float *x,
                         int tokens, int *idx, float *weight);
 
@@ -280,6 +278,31 @@ int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *layer,
 /* Router policy: 0 = certified fast path with exact fallback (default),
  * 1 = always run the exact serial chain. */
 int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
+
+/* n_layers MoE steps in order on the context stream: layer l reads
+ * x + l*x_layer_stride and writes y + l*y_layer_stride (floats).  Strict
+ * decode order: layer l+1 starts after layer l's output is written. */
+int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers,
+                                 int n_layers, float *y, const float *x,
+                                 int tokens, size_t x_layer_stride,
+                                 size_t y_layer_stride);
+
+/* rows x cols synthetic activations ~N(0,1) (sw_synth.h), row r keyed by
+ * (seed, layer, step0 + r): identical to the host generator. */
+int coli_cuda_synth_activations(ColiCuda *ctx, float *x, int rows, int cols,
+                                unsigned long long seed, int layer, int step0);
+
+/* Stream timer on the context stream (HIP events). */
+int coli_cuda_timer_start(ColiCuda *ctx);
+int coli_cuda_timer_stop(ColiCuda *ctx, float *ms);
+
+/* Per-stage device timing of the MoE step (HIP events between the step's
+ * kernels).  Stages: 0 activation prep + router + top-k, 1 bucketing,
+ * 2 shared gate/up, 3 routed gate/up, 4 hidden prep, 5 down (routed +
+ * shared), 6 combine.  Accumulated over calls until reset. */
+int coli_cuda_moe_stage_timing(ColiCuda *ctx, int enable);
+int coli_cuda_moe_stage_times(ColiCuda *ctx, double ms[8],
+                              unsigned long long *calls);
 
 #ifdef __cplusplus
 }

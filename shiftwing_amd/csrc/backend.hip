@@ -140,6 +140,10 @@ extern "C" void coli_cuda_destroy(ColiCuda *ctx) {
             ctx->profile_ms[6], ctx->profile_ms[7]);
   for (int i = 0; i < 9; i++)
     if (ctx->profile_event[i]) hipEventDestroy(ctx->profile_event[i]);
+  for (int i = 0; i < 2; i++)
+    if (ctx->timer_event[i]) hipEventDestroy(ctx->timer_event[i]);
+  for (int i = 0; i < 8; i++)
+    if (ctx->moe_event[i]) hipEventDestroy(ctx->moe_event[i]);
   hipStreamDestroy(ctx->stream);
   free(ctx);
 }
@@ -280,6 +284,25 @@ extern "C" int coli_cuda_profile_snapshot(ColiCuda *ctx, unsigned long long *tra
   *transactions = ctx->profile_transactions;
   memcpy(stage_ms, ctx->profile_ms, 8 * sizeof(double));
   return 0;
+}
+
+extern "C" int coli_cuda_timer_start(ColiCuda *ctx) {
+  if (!ctx) return fail_arg("coli_cuda_timer_start: null context");
+  for (int i = 0; i < 2; i++)
+    if (!ctx->timer_event[i]) {
+      hipError_t e = hipEventCreate(&ctx->timer_event[i]);
+      if (e != hipSuccess) return fail_hip("hipEventCreate", e);
+    }
+  hipError_t e = hipEventRecord(ctx->timer_event[0], ctx->stream);
+  return e == hipSuccess ? 0 : fail_hip("hipEventRecord", e);
+}
+
+extern "C" int coli_cuda_timer_stop(ColiCuda *ctx, float *ms) {
+  if (!ctx || !ms || !ctx->timer_event[0]) return fail_arg("coli_cuda_timer_stop: timer not started");
+  hipError_t e = hipEventRecord(ctx->timer_event[1], ctx->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(ctx->timer_event[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->timer_event[0], ctx->timer_event[1]);
+  return e == hipSuccess ? 0 : fail_hip("coli_cuda_timer_stop", e);
 }
 
 // ---------------------------------------------------------------------------

@@ -31,6 +31,7 @@
 #include "sw_backend.h"
 #include "sw_device.h"
 #include "sw_synth.h"
+#include "sw_moe_layer.h"
 
 using namespace sw;
 
@@ -47,24 +48,7 @@ inline int tile_bytes_per_lane(int fmt) { return fmt == 4 ? 16 : 12; }
 
 }  // namespace
 
-struct ColiMoeLayer {
-  ColiMoeShape sh;
-  int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
-  size_t gate_codes, down_codes; // bytes of one gate (= up) / down tiled matrix
-  size_t gate_scales, down_scales;
-  size_t expert_codes, expert_scales;  // per expert
-  float *router;                 // [E][H]
-  float *sgate_row;              // [H]
-  signed char *sh_gq, *sh_uq, *sh_dq;  // row-major int8
-  float *sh_gs, *sh_us, *sh_ds;
-  unsigned char *codes;          // [E][gate|up|down] tiled
-  float *scales;                 // [E][gate|up|down] tiled
-  unsigned long long *stats;     // device [2]: tokens, exact fallbacks
-  int router_mode;
-  size_t bytes;
-  void *alloc[16];
-  int nalloc;
-};
+
 
 namespace {
 
@@ -179,6 +163,12 @@ __global__ void k_synth_scales_tiled(float *dst, int rows, int ng, uint64_t key)
 }
 
 inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+// capture-safe clear (a kernel, not a memset node)
+__global__ void k_zero_u32(unsigned *p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
 
 // ---------------------------------------------------------------------------
 // activation digits: v (len n, zero-padded to ng*128) ->
@@ -963,11 +953,14 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
            layer_alloc(L, (void **)&L->codes, (size_t)E * L->expert_codes, "expert code allocation") ||
            layer_alloc(L, (void **)&L->scales, (size_t)E * L->expert_scales * 4, "expert scale allocation") ||
            layer_alloc(L, (void **)&L->stats, 64, "router stats allocation");
+  L->sync_words = decode_sync_words(*s);
+  rc = rc || layer_alloc(L, (void **)&L->sync, L->sync_words * 4, "decode counter allocation");
   if (rc) {
     coli_cuda_moe_layer_destroy(ctx, L);
     return -1;
   }
-  hipMemsetAsync(L->stats, 0, 64, ctx->stream);
+  k_zero_u32<<<blocks_for(16, 256), 256, 0, ctx->stream>>>((unsigned *)L->stats, 16);
+  k_zero_u32<<<blocks_for(L->sync_words, 256), 256, 0, ctx->stream>>>(L->sync, L->sync_words);
   *out = L;
   return launch_status("coli_cuda_moe_layer_create");
 }
@@ -1138,19 +1131,40 @@ extern "C" int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *L, const float *
   return launch_status("coli_cuda_moe_route");
 }
 
+// stage marks (coli_cuda_moe_stage_timing): event i closes stage i-1
+static inline void mark(ColiCuda *ctx, int i) {
+  if (ctx->moe_timing) hipEventRecord(ctx->moe_event[i], ctx->stream);
+}
+
+static void stage_accumulate(ColiCuda *ctx) {
+  if (!ctx->moe_timing) return;
+  hipEventSynchronize(ctx->moe_event[7]);
+  for (int i = 0; i < 7; i++) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ctx->moe_event[i], ctx->moe_event[i + 1]) == hipSuccess) ctx->moe_ms[i] += ms;
+  }
+  ctx->moe_calls++;
+}
+
 extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int tokens,
                                      int *route_idx, float *route_weight) {
   if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
+  if (tokens == 1 && !ctx->moe_timing && !getenv("SW_MOE_GENERIC"))
+    return decode_step(ctx, L, y, x, route_idx, route_weight);
   Work w;
   if (prepare(ctx, L, tokens, w)) return -1;
   hipStream_t st = ctx->stream;
   int T = tokens;
+  mark(ctx, 0);
   if (route_launch(ctx, L, w, x)) return -1;
+  mark(ctx, 1);
   size_t bucket_lds = (size_t)w.E * ((T + 31) / 32) * 4 + (size_t)(2 * w.E + 1) * 4;
   if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
   k_bucket<<<1, 1024, bucket_lds, st>>>(w);
+  mark(ctx, 2);
   k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedTokens - 1) / kSharedTokens), 512, 0, st>>>(
       w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+  mark(ctx, 3);
   int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
@@ -1162,7 +1176,9 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     k_expert_gateup<3><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->codes, L->scales, L->expert_codes,
                                                                     L->expert_scales, L->gate_codes,
                                                                     L->gate_scales);
+  mark(ctx, 4);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
+  mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
   if (L->sh.expert_format == 4)
     k_down<4><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
@@ -1172,8 +1188,59 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     k_down<3><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
         w, L->codes, L->scales, L->expert_codes, L->expert_scales, 2 * L->gate_codes, 2 * L->gate_scales, slots,
         L->sh_dq, L->sh_ds);
+  mark(ctx, 6);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
-  return launch_status("coli_cuda_moe_forward");
+  mark(ctx, 7);
+  int rc = launch_status("coli_cuda_moe_forward");
+  stage_accumulate(ctx);
+  return rc;
+}
+
+extern "C" int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers, int n_layers, float *y,
+                                            const float *x, int tokens, size_t xs, size_t ys) {
+  if (!ctx || !layers || !y || !x || n_layers <= 0)
+    return fail_arg("coli_cuda_moe_forward_layers: invalid argument");
+  for (int l = 0; l < n_layers; l++)
+    if (coli_cuda_moe_forward(ctx, layers[l], y + (size_t)l * ys, x + (size_t)l * xs, tokens, nullptr, nullptr))
+      return -1;
+  return 0;
+}
+
+__global__ static void k_synth_x(float *x, int rows, int cols, uint64_t seed, uint32_t layer, int step0) {
+  int r = blockIdx.y;
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= cols || r >= rows) return;
+  x[(size_t)r * cols + i] = sw_normal(sw_key(seed, layer, (uint32_t)(step0 + r), SW_T_X), (uint64_t)i);
+}
+
+extern "C" int coli_cuda_synth_activations(ColiCuda *ctx, float *x, int rows, int cols, unsigned long long seed,
+                                           int layer, int step0) {
+  if (!ctx || !x || rows <= 0 || cols <= 0 || rows > 65535)
+    return fail_arg("coli_cuda_synth_activations: invalid argument");
+  k_synth_x<<<dim3((cols + 255) / 256, rows), 256, 0, ctx->stream>>>(x, rows, cols, seed, (uint32_t)layer, step0);
+  return launch_status("coli_cuda_synth_activations");
+}
+
+extern "C" int coli_cuda_moe_stage_timing(ColiCuda *ctx, int enable) {
+  if (!ctx) return fail_arg("coli_cuda_moe_stage_timing: null context");
+  if (enable) {
+    for (int i = 0; i < 8; i++)
+      if (!ctx->moe_event[i]) {
+        hipError_t e = hipEventCreate(&ctx->moe_event[i]);
+        if (e != hipSuccess) return fail_hip("hipEventCreate", e);
+      }
+    memset(ctx->moe_ms, 0, sizeof(ctx->moe_ms));
+    ctx->moe_calls = 0;
+  }
+  ctx->moe_timing = enable ? 1 : 0;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_stage_times(ColiCuda *ctx, double ms[8], unsigned long long *calls) {
+  if (!ctx || !ms || !calls) return fail_arg("coli_cuda_moe_stage_times: null argument");
+  memcpy(ms, ctx->moe_ms, sizeof(ctx->moe_ms));
+  *calls = ctx->moe_calls;
+  return 0;
 }
 
 extern "C" int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long *tokens,

@@ -44,6 +44,12 @@ struct ColiCuda {
   hipEvent_t profile_event[9];
   double profile_ms[8];
   unsigned long long profile_transactions;
+  // stream timer and MoE stage timing
+  hipEvent_t timer_event[2];
+  int moe_timing;
+  hipEvent_t moe_event[8];
+  double moe_ms[8];
+  unsigned long long moe_calls;
 };
 
 namespace sw {

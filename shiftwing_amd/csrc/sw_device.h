@@ -116,9 +116,96 @@ __device__ __forceinline__ double wave_exclusive_scan(double v, int lane) {
 // (16 bytes each); C lane l holds rows 4*(l/16)+i, column l%16.
 // ---------------------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// DPP wave64 all-reductions: four intra-row steps (quad_perm 1032, 2301,
+// row_half_mirror, row_mirror) leave each 16-lane row's total in every lane
+// of the row; row_bcast15 / row_bcast31 fold the rows into lane 63, which is
+// read back as a wave-uniform value.  No LDS traffic, ~6 VALU ops.
+// ---------------------------------------------------------------------------
+#define SW_DPP_I(old, v, ctrl, rm, bc) __builtin_amdgcn_update_dpp((old), (v), (ctrl), (rm), 0xF, (bc))
+#define SW_DPP_F(old, v, ctrl, rm, bc) \
+  __builtin_bit_cast(float, SW_DPP_I(__builtin_bit_cast(int, (float)(old)), __builtin_bit_cast(int, (v)), ctrl, rm, bc))
+
+__device__ __forceinline__ float readlane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += SW_DPP_F(0.0f, v, 0xB1, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x4E, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x141, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x140, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x142, 0xA, false);
+  v += SW_DPP_F(0.0f, v, 0x143, 0xC, false);
+  return readlane63(v);
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  const float ninf = -__builtin_huge_valf();
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0xB1, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x4E, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x141, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x140, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x142, 0xA, false));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x143, 0xC, false));
+  return readlane63(v);
+}
+
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += SW_DPP_I(0, v, 0xB1, 0xF, true);
+  v += SW_DPP_I(0, v, 0x4E, 0xF, true);
+  v += SW_DPP_I(0, v, 0x141, 0xF, true);
+  v += SW_DPP_I(0, v, 0x140, 0xF, true);
+  v += SW_DPP_I(0, v, 0x142, 0xA, false);
+  v += SW_DPP_I(0, v, 0x143, 0xC, false);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+#define SW_DPP_D_STEP(v, ctrl, rm, bc)                                              \
+  {                                                                                 \
+    int lo_ = SW_DPP_I(0, (int)__double2loint(v), ctrl, rm, bc);                   \
+    int hi_ = SW_DPP_I(0, (int)__double2hiint(v), ctrl, rm, bc);                   \
+    v += __hiloint2double(hi_, lo_);                                                \
+  }
+
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+  SW_DPP_D_STEP(v, 0xB1, 0xF, true);
+  SW_DPP_D_STEP(v, 0x4E, 0xF, true);
+  SW_DPP_D_STEP(v, 0x141, 0xF, true);
+  SW_DPP_D_STEP(v, 0x140, 0xF, true);
+  SW_DPP_D_STEP(v, 0x142, 0xA, false);
+  SW_DPP_D_STEP(v, 0x143, 0xC, false);
+  int lo = __builtin_amdgcn_readlane((int)__double2loint(v), 63);
+  int hi = __builtin_amdgcn_readlane((int)__double2hiint(v), 63);
+  return __hiloint2double(hi, lo);
+}
+
+// largest 64-bit key over the wave (keys encode value and index)
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#define SW_U64_STEP(ctrl, rm, bc)                                                           \
+  {                                                                                         \
+    unsigned lo_ = (unsigned)SW_DPP_I(0, (int)(unsigned)k, ctrl, rm, bc);                  \
+    unsigned hi_ = (unsigned)SW_DPP_I(0, (int)(unsigned)(k >> 32), ctrl, rm, bc);          \
+    unsigned long long o_ = ((unsigned long long)hi_ << 32) | lo_;                          \
+    k = o_ > k ? o_ : k;                                                                    \
+  }
+  SW_U64_STEP(0xB1, 0xF, true);
+  SW_U64_STEP(0x4E, 0xF, true);
+  SW_U64_STEP(0x141, 0xF, true);
+  SW_U64_STEP(0x140, 0xF, true);
+  SW_U64_STEP(0x142, 0xA, false);
+  SW_U64_STEP(0x143, 0xC, false);
+#undef SW_U64_STEP
+  unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)k, 63);
+  unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(k >> 32), 63);
+  return ((unsigned long long)hi << 32) | lo;
 }
 
 // Row shift within each 16-lane row: lane l receives lane l-1 (lane 0 of the

@@ -1,0 +1,39 @@
+// Internal: the HBM-resident layer object behind ColiMoeLayer and the
+// decode-step entry shared by moe.hip and moe_decode.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "shiftwing_moe.h"
+
+struct ColiMoeLayer {
+  ColiMoeShape sh;
+  int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
+  size_t gate_codes, down_codes; // bytes of one gate (= up) / down tiled matrix
+  size_t gate_scales, down_scales;
+  size_t expert_codes, expert_scales;  // per expert
+  float *router;                 // [E][H]
+  float *sgate_row;              // [H]
+  signed char *sh_gq, *sh_uq, *sh_dq;  // row-major int8
+  float *sh_gs, *sh_us, *sh_ds;
+  unsigned char *codes;          // [E][gate|up|down] tiled
+  float *scales;                 // [E][gate|up|down] tiled
+  unsigned long long *stats;     // device [2]: tokens, exact fallbacks
+  // decode-step fan-in counters and int32 accumulators, owned by the layer
+  // (zeroed at creation and returned to zero by every step), so a context
+  // serving layers of different shapes never sees another layer's state
+  unsigned *sync;
+  size_t sync_words;
+  int router_mode;
+  size_t bytes;
+  void *alloc[16];
+  int nalloc;
+};
+
+namespace sw {
+// words of ColiMoeLayer::sync for a layer shape
+size_t decode_sync_words(const ColiMoeShape &s);
+// One decoded token through one layer (three kernels); see moe_decode.hip.
+int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight);
+}  // namespace sw

@@ -114,3 +114,20 @@ def test_random_seeds_vs_oracle_s35(be, oracle, seed):
         y, idx, w = L.forward_host(x)
         assert np.array_equal(idx[0], tr["idx"])
         assert_close_rms(y[0], want, 1e-3, f"seed {seed} t {t}")
+
+
+def test_shapes_interleaved_in_one_context(be):
+    """Layers of different shapes served by one context, in both router
+    modes, in an order that reuses the context workspace across shapes."""
+    order = ["s397_q3", "s35_q4", "small_q3", "s397_q3", "s35_q4"]
+    layers = {}
+    for i, name in enumerate(order):
+        g, c = _load(name)
+        if name not in layers:
+            layers[name] = _device_layer(be, c)
+        L = layers[name]
+        L.set_router_mode(i % 2)
+        print(f"[interleave] {name} mode {i % 2}", flush=True)
+        y, idx, w = L.forward_host(g["x"][0])
+        assert np.array_equal(idx[0], g["idx"][0]), name
+        assert_close_rms(y[0], g["decode"][0], 1e-3, f"interleaved {name}")
