@@ -43,8 +43,7 @@ WORKLOADS = {
             "(256, top-8) + int8 shared expert, 17 GB HBM-resident, batch-1 decode"),
 }
 
-STAGES = ["prep+router+topk", "bucket", "shared gate/up", "routed gate/up", "hidden prep",
-          "down (routed+shared)", "combine"]
+KERNELS = ["route", "experts", "down"]
 
 
 def row_bytes(fmt, cols, gs=128):
@@ -52,18 +51,19 @@ def row_bytes(fmt, cols, gs=128):
     return ng * gs // 2 if fmt == 4 else ng * gs * 3 // 8
 
 
-def stage_bytes(H, E, K, I, Ish, fmt):
-    """Algorithmic HBM bytes per layer step for each stage (weights + scales;
-    activations are < 0.1% and omitted)."""
+def kernel_bytes(H, E, K, I, Ish, fmt):
+    """Algorithmic HBM bytes per layer step of each decode kernel: the weights
+    and scales it must stream (activations, < 0.1%, omitted).
+      route:   router f32 [E x H] + shared gate row [H] + shared gate/up int8 [2 Ish x H]
+      experts: K routed gate/up (codes + group scales)
+      down:    K routed down (codes + group scales) + shared down int8 [H x Ish]
+               + shared row scales (gate, up, down)"""
     ngh, ngi = (H + 127) // 128, (I + 127) // 128
     gate = I * row_bytes(fmt, H) + I * ngh * 4
     down = H * row_bytes(fmt, I) + H * ngi * 4
-    b = [0] * 7
-    b[0] = E * H * 4 + H * 4                      # router f32 + shared gate row
-    b[2] = 2 * Ish * H + 2 * Ish * 4              # shared gate/up int8 + row scales
-    b[3] = K * 2 * gate                           # routed gate/up
-    b[5] = K * down + H * Ish + H * 4             # routed down + shared down
-    return b
+    return [E * H * 4 + H * 4 + 2 * Ish * H,
+            K * 2 * gate,
+            K * down + H * Ish + 2 * Ish * 4 + H * 4]
 
 
 def cpu_baseline(cfg, budget_s: float):
@@ -163,25 +163,26 @@ def main():
     ms_per_step = total_ms / args.steps
     tok_s = args.steps / (total_ms / 1e3)
 
-    # per-stage timing pass (HIP events between the step's kernels)
+    # per-kernel timing pass: HIP events on the context stream around each of
+    # the three decode kernels (the kernels' own stream)
     be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
     nst = min(args.steps, 8)
     for s in range(args.warmup, args.warmup + nst):
         run(s)
     be.sync()
-    stage_ms = (C.c_double * 8)()
+    kms = (C.c_double * 3)()
     calls = C.c_ulonglong()
-    be.check(lib.coli_cuda_moe_stage_times(be.ctx, stage_ms, C.byref(calls)))
+    be.check(lib.coli_cuda_moe_decode_times(be.ctx, kms, C.byref(calls)))
     be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 0))
-    per_call = [stage_ms[i] / max(calls.value, 1) for i in range(7)]
-    sb = stage_bytes(H, E, K, I, Ish, fmt)
-    dom = max(range(7), key=lambda i: per_call[i])
-    dom_bytes = sb[dom] if sb[dom] else sb[3]
-    achieved = dom_bytes / (per_call[dom] * 1e-3) / 1e9
-    step_bytes = sum(sb)
-    routed_fb = [L.route_stats() for L in stack]
-    tokens_routed = sum(t for t, _ in routed_fb)
-    fallbacks = sum(f for _, f in routed_fb)
+    per_call = [kms[i] / max(calls.value, 1) for i in range(3)]
+    kb = kernel_bytes(H, E, K, I, Ish, fmt)
+    dom = max(range(3), key=lambda i: per_call[i])
+    achieved = kb[dom] / (per_call[dom] * 1e-3) / 1e9
+    step_bytes = sum(kb)
+    stats = [L.route_stats_full() for L in stack]
+    tokens_routed = sum(t for t, _, _ in stats)
+    fallbacks = sum(f for _, f, _ in stats)
+    full = sum(u for _, _, u in stats)
 
     result = {
         "metric": METRIC,
@@ -206,21 +207,22 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": STAGES[dom],
+            "kernel": KERNELS[dom],
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "bytes_per_launch": dom_bytes,
+            "bytes_per_launch": kb[dom],
             "avg_launch_us": round(per_call[dom] * 1e3, 3),
         },
         "step": {
             "algorithmic_bytes_per_layer": step_bytes,
             "effective_gbs": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9, 1),
             "frac_of_peak": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "stage_us_per_layer": {STAGES[i]: round(per_call[i] * 1e3, 3) for i in range(7)},
-            "router_exact_fallbacks": f"{fallbacks}/{tokens_routed} token-layers",
+            "kernel_us_per_layer": {KERNELS[i]: round(per_call[i] * 1e3, 3) for i in range(3)},
+            "kernel_gbs": {KERNELS[i]: round(kb[i] / (per_call[i] * 1e-3) / 1e9, 1) for i in range(3)},
+            "router_not_certified": f"{fallbacks}/{tokens_routed} token-layers ({full} needed every chain)",
             "weight_generation_s": round(gen_s, 1),
         },
     }

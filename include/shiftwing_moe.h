@@ -274,6 +274,11 @@ int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *layer, const float *x,
 int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *layer,
                               unsigned long long *tokens,
                               unsigned long long *exact_fallbacks);
+/* out[0] tokens routed, out[1] tokens the bounds did not certify, out[2]
+ * tokens that needed every expert's serial chain (the rest of out[1] were
+ * settled by exact chains of the ambiguous experts only). */
+int coli_cuda_moe_route_stats_full(ColiCuda *ctx, ColiMoeLayer *layer,
+                                   unsigned long long out[3]);
 
 /* Router policy: 0 = certified fast path with exact fallback (default),
  * 1 = always run the exact serial chain. */
@@ -303,6 +308,16 @@ int coli_cuda_timer_stop(ColiCuda *ctx, float *ms);
 int coli_cuda_moe_stage_timing(ColiCuda *ctx, int enable);
 int coli_cuda_moe_stage_times(ColiCuda *ctx, double ms[8],
                               unsigned long long *calls);
+
+/* Single-token steps run the three-kernel decode path (route / experts /
+ * down); with stage timing enabled its kernels are timed separately:
+ * ms[0] route (router bounds + top-k, shared gate/up, digits), ms[1] experts
+ * (routed gate/up, shared down), ms[2] routed down + combine. */
+int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3],
+                               unsigned long long *calls);
+/* 1 (default): single-token steps take the decode kernels; 0: they take the
+ * many-token kernels (same results to the stated tolerance; for tests). */
+int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int enable);
 
 #ifdef __cplusplus
 }

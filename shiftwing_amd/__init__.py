@@ -95,6 +95,12 @@ class Backend:
     def device_name(self) -> str:
         return self.lib.coli_cuda_device_name(self.ctx).decode()
 
+    def set_decode_kernels(self, enable: bool):
+        """True (default): single-token steps take the three decode kernels;
+        False: they take the many-token kernels."""
+        self.check(self.lib.coli_cuda_moe_set_decode_kernels(self.ctx, 1 if enable else 0),
+                   "coli_cuda_moe_set_decode_kernels")
+
     def close(self):
         if self.ctx:
             self.lib.coli_cuda_destroy(self.ctx)
@@ -169,6 +175,13 @@ class MoeLayer:
         self.be.check(self.be.lib.coli_cuda_moe_route_stats(self.be.ctx, self.h, C.byref(t), C.byref(f)),
                       "coli_cuda_moe_route_stats")
         return t.value, f.value
+
+    def route_stats_full(self):
+        """(tokens, not certified by the bounds, needing every expert's chain)."""
+        out = (C.c_ulonglong * 3)()
+        self.be.check(self.be.lib.coli_cuda_moe_route_stats_full(self.be.ctx, self.h, out),
+                      "coli_cuda_moe_route_stats_full")
+        return tuple(int(v) for v in out)
 
     def forward_host(self, x: np.ndarray):
         """Convenience: host x [T,H] -> (y [T,H], idx [T,K], weight [T,K])."""

@@ -417,7 +417,10 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
       }
     }
     atomicAdd(&stats[0], 1ull);
-    if (!ok) atomicAdd(&stats[1], 1ull);
+    if (!ok) {
+      atomicAdd(&stats[1], 1ull);
+      atomicAdd(&stats[2], 1ull);  // this path always re-runs every expert's chain
+    }
   }
 }
 
@@ -1149,8 +1152,10 @@ static void stage_accumulate(ColiCuda *ctx) {
 extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int tokens,
                                      int *route_idx, float *route_weight) {
   if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
-  if (tokens == 1 && !ctx->moe_timing && !getenv("SW_MOE_GENERIC"))
-    return decode_step(ctx, L, y, x, route_idx, route_weight);
+  if (tokens == 1 && !ctx->moe_generic_only) {
+    int rc = decode_step(ctx, L, y, x, route_idx, route_weight);
+    if (rc <= 0) return rc;  // 1: shape outside the decode kernels' limits
+  }
   Work w;
   if (prepare(ctx, L, tokens, w)) return -1;
   hipStream_t st = ctx->stream;
@@ -1231,6 +1236,8 @@ extern "C" int coli_cuda_moe_stage_timing(ColiCuda *ctx, int enable) {
       }
     memset(ctx->moe_ms, 0, sizeof(ctx->moe_ms));
     ctx->moe_calls = 0;
+    memset(ctx->moe_dec_ms, 0, sizeof(ctx->moe_dec_ms));
+    ctx->moe_dec_calls = 0;
   }
   ctx->moe_timing = enable ? 1 : 0;
   return 0;
@@ -1243,15 +1250,34 @@ extern "C" int coli_cuda_moe_stage_times(ColiCuda *ctx, double ms[8], unsigned l
   return 0;
 }
 
+extern "C" int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3], unsigned long long *calls) {
+  if (!ctx || !ms || !calls) return fail_arg("coli_cuda_moe_decode_times: null argument");
+  memcpy(ms, ctx->moe_dec_ms, sizeof(ctx->moe_dec_ms));
+  *calls = ctx->moe_dec_calls;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int enable) {
+  if (!ctx || (enable != 0 && enable != 1)) return fail_arg("coli_cuda_moe_set_decode_kernels: invalid argument");
+  ctx->moe_generic_only = enable ? 0 : 1;
+  return 0;
+}
+
 extern "C" int coli_cuda_moe_route_stats(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long *tokens,
                                          unsigned long long *fallbacks) {
   if (!ctx || !L || !tokens || !fallbacks) return fail_arg("coli_cuda_moe_route_stats: null argument");
-  unsigned long long s[2];
-  hipError_t e = hipMemcpyAsync(s, L->stats, sizeof(s), hipMemcpyDeviceToHost, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  if (e != hipSuccess) return fail_hip("coli_cuda_moe_route_stats", e);
+  unsigned long long s[3];
+  if (coli_cuda_moe_route_stats_full(ctx, L, s)) return -1;
   *tokens = s[0];
   *fallbacks = s[1];
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_route_stats_full(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long out[3]) {
+  if (!ctx || !L || !out) return fail_arg("coli_cuda_moe_route_stats_full: null argument");
+  hipError_t e = hipMemcpyAsync(out, L->stats, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return fail_hip("coli_cuda_moe_route_stats_full", e);
   return 0;
 }
 

@@ -1,24 +1,31 @@
 // One decoded token through one HBM-resident MoE layer in three kernels
 // (moe_forward, c/qwen.c:3717-3739):
 //
-//   K1 route   wave tasks over all CUs: the router rows (fp64 logit + a
-//              rigorous bound on the reference's serial fp32 dot), the shared
-//              expert's gate/up int8 dots (exact int32, split over k and
-//              summed with integer atomics), and the activation digits for the
-//              routed experts.  The last workgroup to finish certifies the
-//              top-k (or runs the exact serial chain), and quantises the
-//              shared hidden vector (qrow_i8).
-//   K2 experts routed gate/up tiles for the K chosen experts (the last
-//              workgroup of each expert quantises its hidden vector) and the
-//              shared down projection.
-//   K3 down    one workgroup per 16 output rows: the K routed down tiles, then
-//              the reference's combine order (fma over k, then shared * gate).
+//   K1 route   router workgroups (four router rows each: an fp64 logit and a
+//              rigorous bound on the reference's serial fp32 dot), shared
+//              expert workgroups (gate/up int8 dots, exact int32, split over k
+//              and summed with integer atomics) and activation-digit
+//              workgroups.  The last router workgroup to finish selects the
+//              top-k: certified from the bounds, else from exact fp32 logits of
+//              the experts the bounds leave ambiguous, else (near ties) by the
+//              reference's full serial computation.  Router workgroups come
+//              first in the grid, so the selection overlaps the shared-expert
+//              streaming.
+//   K2 experts one workgroup per (route, matrix, 16 rows) of the routed gate /
+//              up tiles.  The last workgroup of a route forms its hidden vector
+//              h = silu(g) * u and quantises it to activation digits.
+//   K3 down    one workgroup per 16 output rows: one wave per route (routed
+//              down tiles) and one wave for the shared down projection, whose
+//              hidden vector every workgroup rebuilds from the integer sums;
+//              then the reference's combine order.
 //
-// The hand-offs inside a kernel use a fan-in counter (the last arriver does
-// the dependent tail; nobody spins), so the only device-wide waits are the
-// two kernel boundaries.  Counters and integer accumulators are returned to
-// zero by their last user, so consecutive calls (and graph replays) need no
-// memset.
+// Fan-in (router rows in K1, routes in K2) is one release by one thread per
+// workgroup, whose own wave wrote the published data; every other hand-off is
+// a kernel boundary.  Counters are reset by their last arriver.  The shared
+// expert's integer sums alternate between two buffers (a parity word kept on
+// the device), so the buffer one call reads is cleared by the next one.  No
+// memset, no host state: consecutive calls and graph replays need nothing.
+// Each kernel issues its weight loads before it waits for anything else.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <string.h>
@@ -33,28 +40,27 @@ using namespace sw;
 namespace {
 
 constexpr int kMaxK = 32;
-constexpr int kDecThreads = 256;  // K1 / K2 workgroup
+constexpr int kThreads = 256;       // K1 / K2 workgroup
+constexpr int kMaxAmbig = 64;       // experts the targeted exact selection can take
+constexpr int kMaxDownWaves = 10;   // K3 routed waves per workgroup (+1 shared)
+constexpr int kSegPrefetch = 16;    // router row segments (of 256) loaded ahead
 
 struct Dec {
   int H, E, K, I, Ish, ngh, ngi, Hp, Ip, KQ;
-  signed char *xd;    // [2][Hp] routed activation digits
-  float4 *xgp;        // [ngh]
-  double2 *lb;        // [E+1] fp64 logit, bound (row E: shared gate)
-  int *acc;           // [2][Ish] shared gate/up int32 partial dots
-  unsigned *rtcnt;    // [Ish/16]
-  unsigned *cnt;      // [8] fan-in counters
-  float *hsh;         // [Ish]
-  signed char *hq;    // [Ish]
-  float *misc;        // [0] shx  [1] sgate  [2] sx
-  int *idx;           // [K]
-  float *w;           // [K]
-  float *logits;      // [E] exact fallback logits
-  float *hroute;      // [K][I]
-  signed char *hd;    // [K][2][Ip]
-  float4 *hgp;        // [K][ngi]
-  unsigned *ecnt;     // [K]
-  float *shout;       // [H]
-  size_t bytes;
+  int n_router_wg, n_shared_wg;
+  signed char *xd;  // [2][Hp] routed activation digits
+  float4 *xgp;      // [ngh]
+  double2 *lb;      // [E+1] fp64 logit, bound (row E: shared gate)
+  float *misc;      // [0] sx (IDOT scale of x)  [1] shared gate
+  int *imisc;       // [0] parity of this call's integer sums
+  int *idx;         // [K]
+  float *w;         // [K]
+  float *gu;        // [K][2][I] routed gate / up outputs
+  signed char *hd;  // [K][2][Ip] routed hidden digits
+  float4 *hgp;      // [K][ngi]
+  unsigned *cnt;    // per layer: [0] router fan-in  [1] parity
+  unsigned *ecnt;   // per layer: [K] route fan-in
+  int *acc;         // per layer: [2][2][Ish] shared gate/up int32 dots
 };
 
 size_t dec_carve(Dec &d, char *base) {
@@ -68,51 +74,22 @@ size_t dec_carve(Dec &d, char *base) {
   d.xd = (signed char *)take((size_t)2 * d.Hp);
   d.xgp = (float4 *)take((size_t)d.ngh * 16);
   d.lb = (double2 *)take((size_t)(d.E + 1) * 16);
-  d.hsh = (float *)take((size_t)d.Ish * 4);
-  d.hq = (signed char *)take((size_t)d.Ish);
-  d.misc = (float *)take(64);
+  d.misc = (float *)take(32);
+  d.imisc = (int *)take(32);
   d.idx = (int *)take((size_t)kMaxK * 4);
   d.w = (float *)take((size_t)kMaxK * 4);
-  d.logits = (float *)take((size_t)d.E * 4);
-  d.hroute = (float *)take((size_t)d.K * d.I * 4);
+  d.gu = (float *)take((size_t)d.K * 2 * d.I * 4);
   d.hd = (signed char *)take((size_t)d.K * 2 * d.Ip);
   d.hgp = (float4 *)take((size_t)d.K * d.ngi * 16);
-  d.shout = (float *)take((size_t)d.H * 4);
-  d.bytes = off + 256;
-  return d.bytes;
-}
-
-// ---------------------------------------------------------------------------
-// fan-in: every thread releases its writes; returns true in all threads of the
-// last workgroup to arrive (which then acquires).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool block_last_arrival(unsigned *counter, unsigned total, unsigned *s_flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) *s_flag = (atomicAdd(counter, 1u) == total - 1) ? 1u : 0u;
-  __syncthreads();
-  bool last = *s_flag != 0;
-  if (last) __threadfence();
-  return last;
-}
-
-// same for a single wave
-__device__ __forceinline__ bool wave_last_arrival(unsigned *counter, unsigned total, int lane) {
-  __threadfence();
-  unsigned prev = 0;
-  if (lane == 0) prev = atomicAdd(counter, 1u);
-  prev = (unsigned)__builtin_amdgcn_readfirstlane((int)prev);
-  bool last = prev == total - 1;
-  if (last) __threadfence();
-  return last;
+  return off + 256;
 }
 
 // inclusive DPP prefix sum of a double over the wave (lane order)
-#define SW_DPP_D_ADD(v, ctrl, rm, bc)                                   \
-  {                                                                     \
-    int lo_ = SW_DPP_I(0, (int)__double2loint(v), ctrl, rm, bc);       \
-    int hi_ = SW_DPP_I(0, (int)__double2hiint(v), ctrl, rm, bc);       \
-    v += __hiloint2double(hi_, lo_);                                    \
+#define SW_DPP_D_ADD(v, ctrl, rm, bc)                             \
+  {                                                               \
+    int lo_ = SW_DPP_I(0, (int)__double2loint(v), ctrl, rm, bc); \
+    int hi_ = SW_DPP_I(0, (int)__double2hiint(v), ctrl, rm, bc); \
+    v += __hiloint2double(hi_, lo_);                              \
   }
 __device__ __forceinline__ double wave_inclusive_scan_dpp(double v) {
   SW_DPP_D_ADD(v, 0x111, 0xF, true);
@@ -130,6 +107,36 @@ __device__ __forceinline__ double readlane63_d(double v) {
 }
 
 // ---------------------------------------------------------------------------
+// Fan-in without release fences.  On this chip an agent-scope release fence
+// writes back the issuing XCD's whole L2; issued by hundreds of workgroups
+// they serialise into tens of microseconds.  Instead, a workgroup publishes
+// its words with returning device-scope atomics (performed at the coherence
+// point every XCD's device-scope atomics go through), waits for them to
+// return, and only then bumps the counter with another device-scope atomic.
+// The last arriver reads the published words with device-scope atomic loads,
+// served from the same coherence point.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned publish(float *p, float v) { return __float_as_uint(atomicExch(p, v)); }
+__device__ __forceinline__ unsigned publish(unsigned long long *p, unsigned long long v) {
+  unsigned long long o = atomicExch(p, v);
+  return (unsigned)o ^ (unsigned)(o >> 32);
+}
+// Every publish of this wave has returned.  dep: the xor of the lane's
+// publish results (0 for lanes that published nothing), consumed only here so
+// that all of a wave's atomics are in flight together.
+__device__ __forceinline__ void published(unsigned dep) {
+  asm volatile("" ::"v"(dep));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ float read_published(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double read_published(const double *p) {
+  unsigned long long v = __hip_atomic_load((const unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __longlong_as_double((long long)v);
+}
+
+// ---------------------------------------------------------------------------
 // Router row bound.  The reference logit is dot() (c/qwen.c:1674), evaluated
 // with gcc -O3 as s_k = rn(s_{k-1} + rn(x_k w_k)) (a tail of H%8 terms fused).
 // With exact prefix sums S_k and u = 2^-24:
@@ -138,18 +145,31 @@ __device__ __forceinline__ double readlane63_d(double v) {
 // walks the row in 256-element segments (float4 per lane, coalesced); S_k
 // comes from an fp64 lane scan plus the running carry, exact to 1e-16.
 // ---------------------------------------------------------------------------
-__device__ double2 row_bound(const float *row, const float *xs, int H, int lane) {
-  double carry = 0.0, A = 0.0, P = 0.0;
-  for (int base = 0; base < H; base += 256) {
-    int i0 = base + 4 * lane;
+struct RowSegs {
+  v4f w[kSegPrefetch];
+};
+
+__device__ __forceinline__ void row_prefetch(RowSegs &s, const float *row, int H, int base, int lane) {
+#pragma unroll
+  for (int q = 0; q < kSegPrefetch; q++) {
+    int i0 = base + 256 * q + 4 * lane;
+    s.w[q] = i0 < H ? __builtin_nontemporal_load((const v4f *)(row + i0)) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+}
+
+__device__ __forceinline__ void row_accumulate(const RowSegs &s, const float *xs, int H, int base, int lane,
+                                               double &carry, double &A, double &P) {
+#pragma unroll
+  for (int q = 0; q < kSegPrefetch; q++) {
+    if (base + 256 * q >= H) break;
+    int i0 = base + 256 * q + 4 * lane;
     double p[4] = {0.0, 0.0, 0.0, 0.0};
     if (i0 < H) {
-      v4f wv = __builtin_nontemporal_load((const v4f *)(row + i0));
       float4 xv = *(const float4 *)(xs + i0);
-      p[0] = (double)xv.x * (double)wv.x;
-      p[1] = (double)xv.y * (double)wv.y;
-      p[2] = (double)xv.z * (double)wv.z;
-      p[3] = (double)xv.w * (double)wv.w;
+      p[0] = (double)xv.x * (double)s.w[q].x;
+      p[1] = (double)xv.y * (double)s.w[q].y;
+      p[2] = (double)xv.z * (double)s.w[q].z;
+      p[3] = (double)xv.w * (double)s.w[q].w;
     }
     double q0 = p[0], q1 = q0 + p[1], q2 = q1 + p[2], q3 = q2 + p[3];
     A += fabs(p[0]) + fabs(p[1]) + fabs(p[2]) + fabs(p[3]);
@@ -158,6 +178,9 @@ __device__ double2 row_bound(const float *row, const float *xs, int H, int lane)
     if (i0 < H) P += fabs(pre + q0) + fabs(pre + q1) + fabs(pre + q2) + fabs(pre + q3);
     carry += readlane63_d(inc);
   }
+}
+
+__device__ __forceinline__ double2 row_finish(double carry, double A, double P) {
   A = wave_sum_dpp(A);
   P = wave_sum_dpp(P);
   const double u = 0x1p-24;
@@ -165,29 +188,365 @@ __device__ double2 row_bound(const float *row, const float *xs, int H, int lane)
   return make_double2(carry, B);
 }
 
+// The reference's router logit bit for bit: dot() at c/qwen.c:1674 as gcc
+// compiles it (products rounded, then added in index order; a fused tail of
+// H%8 terms).  One chain per thread; rows streamed 32 floats ahead.
+__device__ float exact_logit(const float *row, const float *xs, int H) {
+  const int m8 = (H / 8) * 8;
+  float s = 0.0f;
+  int i = 0;
+  for (; i + 32 <= m8; i += 32) {
+    v4f a[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) a[q] = *(const v4f *)(row + i + 4 * q);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      float4 xv = *(const float4 *)(xs + i + 4 * q);
+      s = s + xv.x * a[q].x;
+      s = s + xv.y * a[q].y;
+      s = s + xv.z * a[q].z;
+      s = s + xv.w * a[q].w;
+    }
+  }
+  for (; i < m8; i++) s = s + xs[i] * row[i];
+  for (; i < H; i++) s = __builtin_fmaf(xs[i], row[i], s);
+  return s;
+}
+
+// Separation that makes two logits' softmax probabilities strictly ordered
+// after the reference's fp32 rounding (l - max, expf, division).
+__device__ __forceinline__ double order_margin(double a, double b, double mx) {
+  return 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
+}
+
+
 // ---------------------------------------------------------------------------
-// K1
+// Top-k selection by the last router workgroup (all 256 threads).
+//   lds: at least 24*E + 16 bytes (bounds, then keys; reused for the exact
+//   logits).  xs: x in LDS.
+// Writes d.idx / d.w (router_topk's indices exactly; weights from the fp64
+// logits, or the reference's fp32 values on the full serial path) and the
+// shared gate.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kDecThreads) void k_dec_route(Dec d, const float *__restrict__ x,
-                                                           const float *__restrict__ router,
-                                                           const float *__restrict__ sgrow,
-                                                           const signed char *__restrict__ gq,
-                                                           const float *__restrict__ gs,
-                                                           const signed char *__restrict__ uq,
-                                                           const float *__restrict__ us, int mode,
-                                                           unsigned long long *stats) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  float *xs = (float *)smem;                           // [H]
-  signed char *xq = (signed char *)(xs + d.H);         // [H]
-  __shared__ float red[8];
-  __shared__ unsigned s_flag;
+__device__ void select_routes(const Dec &d, const float *xs, const float *router, int mode,
+                              unsigned long long *stats, unsigned char *lds) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // stage x and its IDOT quantisation (qrow_i8, c/qwen.c:1696)
+  const int E = d.E, K = d.K;
+  double2 *lb = (double2 *)lds;                                 // [E+1]
+  unsigned long long *lk = (unsigned long long *)(lb + E + 1);  // [E]
+  __shared__ int s_cand[kMaxK + 1];
+  __shared__ int s_state;  // 0 certified, 1 targeted exact, 2 full exact
+  __shared__ int s_nm;
+  __shared__ int s_m[kMaxAmbig];
+  __shared__ float s_ex[kMaxAmbig];
+  __shared__ float s_sl[kMaxAmbig];
+  __shared__ int s_se[kMaxAmbig];
+  // bounds -> LDS with device-scope loads, all issued before the first use
+  constexpr int kLbRegs = 3;
+  double bx[kLbRegs], by[kLbRegs];
+#pragma unroll
+  for (int q = 0; q < kLbRegs; q++) {
+    int e = threadIdx.x + q * kThreads;
+    e = e < E ? e : E;
+    bx[q] = read_published(&d.lb[e].x);
+    by[q] = read_published(&d.lb[e].y);
+  }
+#pragma unroll
+  for (int q = 0; q < kLbRegs; q++) {
+    int e = threadIdx.x + q * kThreads;
+    if (e <= E) {
+      lb[e] = make_double2(bx[q], by[q]);
+      if (e < E) lk[e] = ((unsigned long long)float_key((float)bx[q]) << 32) | (unsigned)(~e);
+    }
+  }
+  for (int e = threadIdx.x + kLbRegs * kThreads; e <= E; e += kThreads) {
+    double2 b = make_double2(read_published(&d.lb[e].x), read_published(&d.lb[e].y));
+    lb[e] = b;
+    if (e < E) lk[e] = ((unsigned long long)float_key((float)b.x) << 32) | (unsigned)(~e);
+  }
+  if (threadIdx.x == 0) s_nm = 0;
+  __syncthreads();
+  if (wave == 0) {
+    // top K+1 by fp64 logit (float keys, lowest index first on equal keys;
+    // near-ties fail the separation tests below).  Lane l alone clears the
+    // keys l+64i it scans, so the rounds need no LDS sync.
+    const int nc = K + 1 < E ? K + 1 : E;
+    for (int r = 0; r < nc; r++) {
+      unsigned long long best = 0;
+      for (int e = lane; e < E; e += 64) best = lk[e] > best ? lk[e] : best;
+      best = wave_max_u64(best);
+      int e = (int)(~(unsigned)best);
+      if ((e & 63) == lane) lk[e] = 0;
+      if (lane == 0) s_cand[r] = e;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // the largest upper bound outside the top K (selected keys are zero)
+    const int candK = K < E ? s_cand[K] : -1;
+    unsigned long long upk = 0;
+    for (int e = lane; e < E; e += 64)
+      if (lk[e] != 0 || e == candK) {
+        unsigned long long k2 = double_key(lb[e].x + lb[e].y);
+        upk = k2 > upk ? k2 : upk;
+      }
+    upk = wave_max_u64(upk);
+    const double mx = lb[s_cand[0]].x;
+    const double2 kth = lb[s_cand[K - 1]];
+    // adjacent candidates separated (lane r tests the pair r, r+1)
+    bool pair_ok = true;
+    if (lane + 1 < K) {
+      double2 a = lb[s_cand[lane]], b = lb[s_cand[lane + 1]];
+      pair_ok = (a.x - a.y) - (b.x + b.y) > order_margin(a.x, b.x, mx);
+    }
+    bool ok = mode == 0 && __all(pair_ok);
+    if (ok && K < E) {
+      double up = key_double(upk);
+      ok = (kth.x - kth.y) - up > order_margin(kth.x, up, mx);
+    }
+    // keep every selected probability a normal float (den <= E <= 4096)
+    if (ok) ok = (kth.x - kth.y) - (mx + lb[s_cand[0]].y) > -75.0;
+    int state = 0;
+    if (ok) {
+      double ev = lane < K ? exp(lb[s_cand[lane < K ? lane : 0]].x - mx) : 0.0;
+      double den = wave_sum_dpp(ev);
+      if (lane < K) {
+        d.idx[lane] = s_cand[lane];
+        d.w[lane] = (float)(ev / den);
+      }
+    } else if (mode != 0) {
+      state = 2;
+    } else {
+      // Every expert whose upper bound reaches the lowest lower bound among
+      // the K candidates (less a margin): the exact top K lies in this set,
+      // since anything outside it is strictly below all K candidates.
+      double theta = 1e300;
+      for (int r = 0; r < K; r++) theta = fmin(theta, lb[s_cand[r]].x - lb[s_cand[r]].y);
+      for (int e = lane; e < E; e += 64) {
+        double2 b = lb[e];
+        if (b.x + b.y >= theta - order_margin(b.x, theta, mx)) {
+          int slot = atomicAdd(&s_nm, 1);
+          if (slot < kMaxAmbig) s_m[slot] = e;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      state = s_nm <= kMaxAmbig && s_nm >= K ? 1 : 2;
+    }
+    if (lane == 0) {
+      s_state = state;
+      d.misc[1] = sigmoid_ref((float)lb[E].x);
+      atomicAdd(&stats[0], 1ull);
+      if (state != 0) atomicAdd(&stats[1], 1ull);
+    }
+  }
+  __syncthreads();
+  if (s_state == 1) {
+    const int nm = s_nm;
+    if ((int)threadIdx.x < nm) s_ex[threadIdx.x] = exact_logit(router + (size_t)s_m[threadIdx.x] * d.H, xs, d.H);
+    __syncthreads();
+    if (wave == 0) {
+      // order by (exact logit desc, index asc) = router_topk's order whenever
+      // consecutive logits are equal or separated by the margin
+      float l = lane < nm ? s_ex[lane] : -__builtin_huge_valf();
+      int e = lane < nm ? s_m[lane] : 0x7fffffff;
+      int rank = 0;
+      for (int q = 0; q < nm; q++) {
+        float lq = s_ex[q];
+        int eq = s_m[q];
+        rank += (lq > l) || (lq == l && eq < e);
+      }
+      if (lane < nm) {
+        s_sl[rank] = l;
+        s_se[rank] = e;
+      }
+      __builtin_amdgcn_wave_barrier();
+      const double mx = s_sl[0];
+      bool pair_ok = true;
+      if (lane < K && lane + 1 < nm) {
+        double a = s_sl[lane], b = s_sl[lane + 1];
+        pair_ok = a == b || a - b > order_margin(a, b, mx);
+      }
+      bool ok = __all(pair_ok) && ((double)s_sl[K - 1] - mx > -75.0);
+      if (ok) {
+        double ev = lane < K ? exp((double)s_sl[lane < K ? lane : 0] - mx) : 0.0;
+        double den = wave_sum_dpp(ev);
+        if (lane < K) {
+          d.idx[lane] = s_se[lane];
+          d.w[lane] = (float)(ev / den);
+        }
+      }
+      if (lane == 0 && !ok) s_state = 2;
+    }
+    __syncthreads();
+  }
+  if (s_state != 2) return;
+  if (threadIdx.x == 0) atomicAdd(&stats[2], 1ull);
+  // router_topk (c/qwen.c:3421-3426) on the exact logits of every expert,
+  // bit-exact: max, expf(l - max), serial denominator in expert order,
+  // division, K argmax rounds (lowest index on ties), serial renormalisation.
+  float *lgs = (float *)lk;  // [E]
+  __shared__ float s_mx, s_den;
+  for (int e = threadIdx.x; e < E; e += kThreads) lgs[e] = exact_logit(router + (size_t)e * d.H, xs, d.H);
+  __syncthreads();
+  if (wave == 0) {
+    float m = -__builtin_huge_valf();
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, lgs[e]);
+    m = wave_max_dpp(m);
+    if (lane == 0) s_mx = m;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kThreads) lgs[e] = expf_glibc(lgs[e] - s_mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float den = 0.0f;
+    for (int e = 0; e < E; e++) den += lgs[e];
+    s_den = den;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kThreads) lgs[e] = lgs[e] / s_den;
+  __syncthreads();
+  if (wave == 0) {
+    __shared__ int chosen[kMaxK];
+    __shared__ float wsel[kMaxK];
+    for (int j = 0; j < K; j++) {
+      unsigned long long best = 0;
+      for (int e = lane; e < E; e += 64) {
+        bool used = false;
+        for (int q = 0; q < j; q++) used |= chosen[q] == e;
+        float pv = lgs[e];
+        unsigned long long k2 = (((unsigned long long)float_key(pv)) << 32) | (unsigned)(~e);
+        if (!used && pv > -1.0f && k2 > best) best = k2;
+      }
+      best = wave_max_u64(best);
+      int c = best ? (int)(~(unsigned)best) : -1;
+      if (lane == 0) {
+        chosen[j] = c;
+        wsel[j] = best ? lgs[c] : -1.0f;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0) {
+      float topden = 0.0f;
+      for (int j = 0; j < K; j++) topden += wsel[j];
+      for (int j = 0; j < K; j++) {
+        d.idx[j] = chosen[j];
+        d.w[j] = wsel[j] / topden;
+      }
+    }
+  }
+}
+
+// x [H] into LDS in two steps, so that the (cached) x loads are issued before
+// a workgroup's weight loads: loads return in issue order.
+constexpr int kXRegs = 4;
+struct XRegs {
+  v4f v[kXRegs];
+};
+// (unconditional loads at clamped indices: no branch ahead of the weights)
+__device__ __forceinline__ void x_load(XRegs &xr, const float *x, int H) {
+#pragma unroll
+  for (int q = 0; q < kXRegs; q++) {
+    int i = (q * kThreads + (int)threadIdx.x) * 4;
+    xr.v[q] = *(const v4f *)(x + (i < H ? i : H - 4));
+  }
+}
+__device__ __forceinline__ void x_store(const XRegs &xr, const float *x, float *xs, int H) {
+#pragma unroll
+  for (int q = 0; q < kXRegs; q++) {
+    int i = (q * kThreads + (int)threadIdx.x) * 4;
+    if (i < H) *(v4f *)(xs + i) = xr.v[q];
+  }
+  for (int i = (kXRegs * kThreads + (int)threadIdx.x) * 4; i < H; i += kThreads * 4)
+    *(float4 *)(xs + i) = *(const float4 *)(x + i);
+}
+
+// ---------------------------------------------------------------------------
+// K1.  grid: n_router_wg | n_shared_wg | digit workgroups; 256 threads.
+// LDS: x [H] f32 | xq [H] i8 (shared rows) or bounds + keys (selection).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_dec_route(Dec d, const float *__restrict__ x,
+                                                        const float *__restrict__ router,
+                                                        const float *__restrict__ sgrow,
+                                                        const signed char *__restrict__ gq,
+                                                        const signed char *__restrict__ uq, int mode,
+                                                        unsigned long long *stats) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  if (b >= d.n_router_wg + d.n_shared_wg) {
+    // activation digits for the routed experts, one 128-group per wave
+    int g = (b - d.n_router_wg - d.n_shared_wg) * 4 + wave;
+    if (g < d.ngh) quantize_group(x, d.H, g, d.xd, d.xd + d.Hp, d.xgp, lane);
+    return;
+  }
+  float *xs = (float *)smem;
+  unsigned char *tail = smem + (((size_t)d.H * 4 + 15) & ~(size_t)15);
+  __shared__ float red[4];
+
+  if (b < d.n_router_wg) {
+    // ---- router rows: weights first, then x ----
+    const int r = b * 4 + wave;
+    const float *row = r < d.E ? router + (size_t)r * d.H : sgrow;
+    XRegs xr;
+    x_load(xr, x, d.H);
+    RowSegs rs;
+    if (r <= d.E) row_prefetch(rs, row, d.H, 0, lane);
+    x_store(xr, x, xs, d.H);
+    __syncthreads();
+    __shared__ double2 s_lb[4];
+    if (r <= d.E) {
+      double carry = 0.0, A = 0.0, P = 0.0;
+      row_accumulate(rs, xs, d.H, 0, lane, carry, A, P);
+      for (int base = 256 * kSegPrefetch; base < d.H; base += 256 * kSegPrefetch) {
+        row_prefetch(rs, row, d.H, base, lane);
+        row_accumulate(rs, xs, d.H, base, lane, carry, A, P);
+      }
+      double2 bb = row_finish(carry, A, P);
+      if (lane == 0) s_lb[wave] = bb;
+    }
+    __syncthreads();
+    // fan-in: thread 0 publishes the workgroup's rows, releases, counts
+    __shared__ unsigned s_last;
+    if (wave == 0) {
+      // lanes 0..7: one word each of the four (logit, bound) pairs
+      unsigned dep = 0;
+      const int q = lane >> 1;
+      if (lane < 8 && b * 4 + q <= d.E) {
+        double v = (lane & 1) ? s_lb[q].y : s_lb[q].x;
+        dep = publish((unsigned long long *)&d.lb[b * 4 + q] + (lane & 1), (unsigned long long)__double_as_longlong(v));
+      }
+      published(dep);
+      if (lane == 0) s_last = atomicAdd(&d.cnt[0], 1u) == (unsigned)d.n_router_wg - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0) atomicExch(&d.cnt[0], 0u);
+    select_routes(d, xs, router, mode, stats, tail);
+    return;
+  }
+
+  // ---- shared expert gate/up: 16 rows x one k-slice per wave ----
+  const int t = (b - d.n_router_wg) * 4 + wave;
+  const int n_tasks = (d.Ish / kTileRows) * d.KQ;
+  const int nk = d.H / 64;
+  int rt = 0, kc0 = 0, kc1 = 0;
+  if (t < n_tasks) {
+    rt = t / d.KQ;
+    int kq = t % d.KQ;
+    kc0 = kq * nk / d.KQ;
+    kc1 = (kq + 1) * nk / d.KQ;
+  }
+  XRegs xr;
+  x_load(xr, x, d.H);
+  const int p = (int)(d.cnt[1] & 1u);
+  RowPrefetch<8> pg, pu;
+  const int e0 = kc0 + 8 < kc1 ? kc0 + 8 : kc1;
+  rows_prefetch<8>(pg, gq, d.H, rt * kTileRows, kc0, e0, lane);
+  rows_prefetch<8>(pu, uq, d.H, rt * kTileRows, kc0, e0, lane);
+  // x and its IDOT quantisation (qrow_i8, c/qwen.c:1696)
+  x_store(xr, x, xs, d.H);
   float m = 0.0f;
-  for (int i = threadIdx.x; i < d.H; i += blockDim.x) {
-    float v = x[i];
-    xs[i] = v;
-    m = fmaxf(m, fabsf(v));
+  for (int i = threadIdx.x * 4; i < d.H; i += kThreads * 4) {
+    float4 v = *(const float4 *)(xs + i);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   }
   m = wave_max_dpp(m);
   if (lane == 0) red[wave] = m;
@@ -196,372 +555,305 @@ __global__ __launch_bounds__(kDecThreads) void k_dec_route(Dec d, const float *_
   float sx = amax / 127.0f;
   if (sx < 1e-12f) sx = 1e-12f;
   const float inv = 1.0f / sx;
-  for (int i = threadIdx.x; i < d.H; i += blockDim.x) xq[i] = (signed char)__builtin_rintf(xs[i] * inv);
+  signed char *xq = (signed char *)tail;
+  for (int i = threadIdx.x; i < d.H; i += kThreads) xq[i] = (signed char)__builtin_rintf(xs[i] * inv);
   __syncthreads();
-
-  // one task per wave: router rows, shared gate/up slices, digit groups
-  const int task = blockIdx.x * 4 + wave;
-  const int n_router = d.E + 1;
-  const int n_shared = (d.Ish / kTileRows) * d.KQ;
-  if (task < n_router) {
-    const float *row = task < d.E ? router + (size_t)task * d.H : sgrow;
-    double2 b = row_bound(row, xs, d.H, lane);
-    if (lane == 0) d.lb[task] = b;
-  } else if (task < n_router + n_shared) {
-    int t = task - n_router, rt = t / d.KQ, kq = t % d.KQ;
-    int nk = d.H / 64, per = nk / d.KQ, kc0 = kq * per, kc1 = kc0 + per;
-    v4i cg = {0, 0, 0, 0}, cu = {0, 0, 0, 0};
-    bool bvalid = (lane & 15) == 0;
-    for (int kc = kc0; kc < kc1; kc += 8) {
-      int e1 = kc + 8 < kc1 ? kc + 8 : kc1;
-      idot_tile<8>(gq, d.H, rt * kTileRows, kc, e1, xq, 0, bvalid, cg, lane);
-      idot_tile<8>(uq, d.H, rt * kTileRows, kc, e1, xq, 0, bvalid, cu, lane);
-    }
-    if ((lane & 15) == 0) {
-      int r0 = rt * kTileRows + 4 * (lane >> 4);
+  if (b == d.n_router_wg && threadIdx.x == 0) {
+    d.misc[0] = sx;
+    d.imisc[0] = p;
+  }
+  if (t >= n_tasks) return;
+  v4i cg = {0, 0, 0, 0}, cu = {0, 0, 0, 0};
+  const bool bvalid = (lane & 15) == 0;
+  rows_compute<8>(pg, kc0, e0, xq, 0, bvalid, cg, lane);
+  rows_compute<8>(pu, kc0, e0, xq, 0, bvalid, cu, lane);
+  for (int kc = e0; kc < kc1; kc += 8) {
+    int e1 = kc + 8 < kc1 ? kc + 8 : kc1;
+    idot_tile<8>(gq, d.H, rt * kTileRows, kc, e1, xq, 0, bvalid, cg, lane);
+    idot_tile<8>(uq, d.H, rt * kTileRows, kc, e1, xq, 0, bvalid, cu, lane);
+  }
+  if ((lane & 15) == 0) {
+    int *acc = d.acc + (size_t)p * 2 * d.Ish;
+    int r0 = rt * kTileRows + 4 * (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        atomicAdd(&d.acc[r0 + i], cg[i]);
-        atomicAdd(&d.acc[d.Ish + r0 + i], cu[i]);
-      }
-    }
-    if (wave_last_arrival(&d.rtcnt[rt], (unsigned)d.KQ, lane)) {
-      // h = silu(g) * u for the tile's 16 rows (c/qwen.c:3419, 1767)
-      if (lane < kTileRows) {
-        int row = rt * kTileRows + lane;
-        int dg = __hip_atomic_load(&d.acc[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int du = __hip_atomic_load(&d.acc[d.Ish + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float g = (float)dg * gs[row] * sx;
-        float u = (float)du * us[row] * sx;
-        d.hsh[row] = silu_ref(g) * u;
-        atomicExch(&d.acc[row], 0);
-        atomicExch(&d.acc[d.Ish + row], 0);
-      }
-      if (lane == 0) atomicExch(&d.rtcnt[rt], 0u);
-    }
-  } else if (task < n_router + n_shared + d.ngh) {
-    int g = task - n_router - n_shared;
-    quantize_group(xs, d.H, g, d.xd, d.xd + d.Hp, d.xgp, lane);
-  }
-
-  if (!block_last_arrival(&d.cnt[0], gridDim.x, &s_flag)) return;
-
-  // ---- last workgroup: routes, shared hidden quantisation ----
-  __shared__ int s_ok;
-  if (wave == 0) {
-    const int E = d.E, K = d.K;
-    // top K+1 by fp64 logit (float keys; ties / near-ties fail certification)
-    unsigned long long key[64];
-    int per = (E + 63) / 64;
-    for (int i = 0; i < per && i < 64; i++) {
-      int e = lane + 64 * i;
-      key[i] = e < E ? (((unsigned long long)float_key((float)d.lb[e].x) << 32) | (unsigned)(~e)) : 0ull;
-    }
-    int cand[kMaxK + 1];
-    int nc = K + 1 < E ? K + 1 : E;
-    for (int r = 0; r < nc; r++) {
-      unsigned long long best = 0;
-      for (int i = 0; i < per && i < 64; i++) best = key[i] > best ? key[i] : best;
-      best = wave_max_u64(best);
-      int e = (int)(~(unsigned)best);
-      for (int i = 0; i < per && i < 64; i++)
-        if (key[i] == best) key[i] = 0;
-      cand[r] = e;
-    }
-    // the largest upper bound outside the top K
-    unsigned long long upk = 0;
-    for (int i = 0; i < per && i < 64; i++) {
-      int e = lane + 64 * i;
-      if (e >= E) continue;
-      bool top = false;
-      for (int r = 0; r < K; r++) top |= cand[r] == e;
-      if (!top) {
-        unsigned long long k2 = double_key(d.lb[e].x + d.lb[e].y);
-        upk = k2 > upk ? k2 : upk;
-      }
-    }
-    upk = wave_max_u64(upk);
-    {
-      double mx = d.lb[cand[0]].x;
-      bool ok = mode == 0;
-      for (int r = 0; ok && r + 1 < K; r++) {
-        double2 a = d.lb[cand[r]], b = d.lb[cand[r + 1]];
-        double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
-        ok = (a.x - a.y) - (b.x + b.y) > margin;
-      }
-      if (ok && K < E) {
-        double2 a = d.lb[cand[K - 1]];
-        double up = key_double(upk);
-        double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(up) + 2.0 * fabs(mx));
-        ok = (a.x - a.y) - up > margin;
-      }
-      if (ok) ok = (d.lb[cand[K - 1]].x - d.lb[cand[K - 1]].y) - (mx + d.lb[cand[0]].y) > -80.0;
-      if (ok) {
-        double p[kMaxK], den = 0.0;
-        for (int r = 0; r < K; r++) {
-          p[r] = exp(d.lb[cand[r]].x - mx);
-          den += p[r];
-        }
-        if (lane == 0)
-          for (int r = 0; r < K; r++) {
-            d.idx[r] = cand[r];
-            d.w[r] = (float)(p[r] / den);
-          }
-      }
-      if (lane == 0) {
-        s_ok = ok;
-        d.misc[1] = sigmoid_ref((float)d.lb[E].x);
-        atomicAdd(&stats[0], 1ull);
-        if (!ok) atomicAdd(&stats[1], 1ull);
-      }
-    }
-  }
-  __syncthreads();
-  if (!s_ok) {
-    // exact serial fp32 router dot for every expert (two chains per lane),
-    // kept in LDS for the exact top-k below
-    float *lgs = (float *)(smem + ((size_t)d.H * 5 + 15) / 16 * 16);  // [E]
-    __shared__ float s_mx, s_den;
-    const int m8 = (d.H / 8) * 8;
-    for (int e0 = threadIdx.x; e0 < d.E; e0 += 2 * blockDim.x) {
-      int e1 = e0 + blockDim.x;
-      const float *r0 = router + (size_t)e0 * d.H;
-      const float *r1 = router + (size_t)(e1 < d.E ? e1 : e0) * d.H;
-      float s0 = 0.0f, s1 = 0.0f;
-      int i = 0;
-      for (; i + 4 <= m8; i += 4) {
-        float4 a = *(const float4 *)(r0 + i), b = *(const float4 *)(r1 + i);
-        float4 xv = *(const float4 *)(xs + i);
-        s0 = s0 + xv.x * a.x;
-        s1 = s1 + xv.x * b.x;
-        s0 = s0 + xv.y * a.y;
-        s1 = s1 + xv.y * b.y;
-        s0 = s0 + xv.z * a.z;
-        s1 = s1 + xv.z * b.z;
-        s0 = s0 + xv.w * a.w;
-        s1 = s1 + xv.w * b.w;
-      }
-      for (; i < m8; i++) {
-        s0 = s0 + xs[i] * r0[i];
-        s1 = s1 + xs[i] * r1[i];
-      }
-      for (; i < d.H; i++) {
-        s0 = __builtin_fmaf(xs[i], r0[i], s0);
-        s1 = __builtin_fmaf(xs[i], r1[i], s1);
-      }
-      lgs[e0] = s0;
-      if (e1 < d.E) lgs[e1] = s1;
-    }
-    __syncthreads();
-    // router_topk (c/qwen.c:3421-3426) on the exact logits, bit-exact:
-    // max, expf(l - max), serial denominator in expert order, division,
-    // K argmax rounds (lowest index on ties), serial renormalisation
-    if (wave == 0) {
-      float mx = -__builtin_huge_valf();
-      for (int e = lane; e < d.E; e += 64) mx = fmaxf(mx, lgs[e]);
-      mx = wave_max_dpp(mx);
-      if (lane == 0) s_mx = mx;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < d.E; e += blockDim.x) lgs[e] = expf_glibc(lgs[e] - s_mx);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float den = 0.0f;
-      for (int e = 0; e < d.E; e++) den += lgs[e];
-      s_den = den;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < d.E; e += blockDim.x) lgs[e] = lgs[e] / s_den;
-    __syncthreads();
-    if (wave == 0) {
-      int chosen[kMaxK];
-      float wsel[kMaxK];
-      for (int j = 0; j < d.K; j++) {
-        unsigned long long best = 0;
-        for (int e = lane; e < d.E; e += 64) {
-          bool used = false;
-          for (int q = 0; q < j; q++) used |= chosen[q] == e;
-          float pv = lgs[e];
-          unsigned long long k2 = (((unsigned long long)float_key(pv)) << 32) | (unsigned)(~e);
-          if (!used && pv > -1.0f && k2 > best) best = k2;
-        }
-        best = wave_max_u64(best);
-        chosen[j] = best ? (int)(~(unsigned)best) : -1;
-        wsel[j] = best ? lgs[chosen[j]] : -1.0f;
-      }
-      if (lane == 0) {
-        float topden = 0.0f;
-        for (int j = 0; j < d.K; j++) topden += wsel[j];
-        for (int j = 0; j < d.K; j++) {
-          d.idx[j] = chosen[j];
-          d.w[j] = wsel[j] / topden;
-        }
-      }
-    }
-  }
-  // shared hidden -> int8 (qrow_i8) for the IDOT down projection
-  __syncthreads();
-  {
-    float hm = 0.0f;
-    for (int i = threadIdx.x; i < d.Ish; i += blockDim.x) hm = fmaxf(hm, fabsf(d.hsh[i]));
-    hm = wave_max_dpp(hm);
-    __syncthreads();
-    if (lane == 0) red[wave] = hm;
-    __syncthreads();
-    float ha = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float shx = ha / 127.0f;
-    if (shx < 1e-12f) shx = 1e-12f;
-    float hinv = 1.0f / shx;
-    for (int i = threadIdx.x; i < d.Ish; i += blockDim.x)
-      d.hq[i] = (signed char)__builtin_rintf(d.hsh[i] * hinv);
-    if (threadIdx.x == 0) {
-      d.misc[0] = shx;
-      atomicExch(&d.cnt[0], 0u);
+    for (int i = 0; i < 4; i++) {
+      atomicAdd(&acc[r0 + i], cg[i]);
+      atomicAdd(&acc[d.Ish + r0 + i], cu[i]);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// K2: routed gate/up tiles + shared down.  grid K*I/16 + H/16, 256 threads
+// K2: routed gate/up.  grid K * 2 * I/16 (route, matrix, row tile), 256
+// threads; the last workgroup of each route builds its hidden digits.
 // ---------------------------------------------------------------------------
 template <int FMT>
-__global__ __launch_bounds__(kDecThreads) void k_dec_experts(Dec d, const unsigned char *__restrict__ codes,
-                                                             const float *__restrict__ scales, size_t expert_codes,
-                                                             size_t expert_scales, size_t gate_codes,
-                                                             size_t gate_scales,
-                                                             const signed char *__restrict__ dq,
-                                                             const float *__restrict__ ds) {
+__global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned char *__restrict__ codes,
+                                                          const float *__restrict__ scales, size_t expert_codes,
+                                                          size_t expert_scales, size_t gate_codes,
+                                                          size_t gate_scales) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float part[4][2][64][4];
-  __shared__ int ipart[4][64][4];
+  __shared__ float part[4][64][4];
   __shared__ __align__(16) signed char zero16[16];
-  __shared__ unsigned s_flag;
+  __shared__ unsigned s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n_route_tiles = d.I / kTileRows;
-  const int routed = d.K * n_route_tiles;
-  if ((int)blockIdx.x >= routed) {
-    // shared down: 16 rows of the int8 [H x Ish] matrix, exact int32 dots
-    int rt = blockIdx.x - routed;
-    int nk = d.Ish / 64, per = (nk + 3) / 4, kc0 = wave * per, kc1 = min(nk, kc0 + per);
-    v4i c = {0, 0, 0, 0};
-    bool bvalid = (lane & 15) == 0;
-    for (int kc = kc0; kc < kc1; kc += 8) {
-      int e1 = kc + 8 < kc1 ? kc + 8 : kc1;
-      idot_tile<8>(dq, d.Ish, rt * kTileRows, kc, e1, d.hq, 0, bvalid, c, lane);
+  const int n_rt = d.I / kTileRows;
+  const int j = blockIdx.x / (2 * n_rt), r2 = blockIdx.x % (2 * n_rt);
+  const int mat = r2 / n_rt, rt = r2 % n_rt;
+  const int e = d.idx[j];
+  if ((unsigned)e >= (unsigned)d.E) return;  // router_topk's -1: the route contributes nothing
+  const unsigned char *ce = codes + (size_t)e * expert_codes + (size_t)mat * gate_codes;
+  const float *se = scales + (size_t)e * expert_scales + (size_t)mat * gate_scales;
+  const int per = (d.ngh + 3) / 4, g0 = wave * per;
+  const int n = (d.ngh < g0 + per ? d.ngh : g0 + per) - g0;
+  signed char *dig = (signed char *)smem;            // [2][Hp]
+  float4 *gp = (float4 *)(smem + 2 * (size_t)d.Hp);  // [ngh]
+  const DigitSrc src = lane_digits(lane, 1, dig, d.Hp, gp, d.ngh, zero16);
+  // activation digits first (cached; loads return in issue order), then tiles
+  // (unconditional loads at clamped indices: no branch ahead of the tiles)
+  const int n16 = (2 * d.Hp) / 16, tid = threadIdx.x;
+  const v4i *xdv = (const v4i *)d.xd;
+  const v4i dr0 = xdv[tid < n16 ? tid : n16 - 1];
+  const v4i dr1 = xdv[tid + kThreads < n16 ? tid + kThreads : n16 - 1];
+  const float4 gr = d.xgp[tid < d.ngh ? tid : d.ngh - 1];
+  float acc[4] = {0, 0, 0, 0};
+  // every wave runs the first iteration (it holds the workgroup barrier)
+  for (int c0 = 0; c0 == 0 || c0 < n; c0 += 8) {
+    const int nn = n - c0 < 8 ? n - c0 : 8;
+    TilePrefetch<FMT, 8> t;
+    tile_prefetch<FMT, 8>(t, ce, se, rt, d.ngh, g0 + c0, nn, lane);
+    if (c0 == 0) {
+      if (tid < n16) ((v4i *)dig)[tid] = dr0;
+      if (tid + kThreads < n16) ((v4i *)dig)[tid + kThreads] = dr1;
+      for (int i = 2 * kThreads + tid; i < n16; i += kThreads) ((v4i *)dig)[i] = xdv[i];
+      if (tid < d.ngh) gp[tid] = gr;
+      for (int i = kThreads + tid; i < d.ngh; i += kThreads) gp[i] = d.xgp[i];
+      if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
+      __syncthreads();
     }
+    tile_compute<FMT, 8>(t, g0 + c0, nn, src, acc, lane);
+  }
+  digit_fold(acc);
 #pragma unroll
-    for (int i = 0; i < 4; i++) ipart[wave][lane][i] = c[i];
-    __syncthreads();
-    if (wave == 0 && (lane & 15) == 0) {
-      float shx = d.misc[0];
+  for (int i = 0; i < 4; i++) part[wave][lane][i] = acc[i];
+  __syncthreads();
+  if (wave == 0) {
+    unsigned dep = 0;
+    if ((lane & 15) == 1) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        int dot = ipart[0][lane][i] + ipart[1][lane][i] + ipart[2][lane][i] + ipart[3][lane][i];
+        float v = part[0][lane][i] + part[1][lane][i] + part[2][lane][i] + part[3][lane][i];
         int row = rt * kTileRows + 4 * (lane >> 4) + i;
-        d.shout[row] = (float)dot * ds[row] * shx;
+        dep ^= publish(&d.gu[((size_t)j * 2 + mat) * d.I + row], v);
       }
     }
-    return;
-  }
-  const int j = blockIdx.x / n_route_tiles, rt = blockIdx.x % n_route_tiles;
-  const int e = d.idx[j];
-  if ((unsigned)e >= (unsigned)d.E) return;  // no expert (router_topk's -1): contributes nothing
-  // activation digits -> LDS
-  signed char *dig = (signed char *)smem;                 // [2][Hp]
-  float4 *gp = (float4 *)(smem + 2 * (size_t)d.Hp);       // [ngh]
-  for (int i = threadIdx.x; i < (2 * d.Hp) / 16; i += blockDim.x)
-    ((int4 *)dig)[i] = ((const int4 *)d.xd)[i];
-  for (int i = threadIdx.x; i < d.ngh; i += blockDim.x) gp[i] = d.xgp[i];
-  if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
-  __syncthreads();
-  DigitSrc src = lane_digits(lane, 1, dig, d.Hp, gp, d.ngh, zero16);
-  const unsigned char *ce = codes + (size_t)e * expert_codes;
-  const float *se = scales + (size_t)e * expert_scales;
-  int per = (d.ngh + 3) / 4, g0 = wave * per, n = min(d.ngh, g0 + per) - g0;
-  float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
-  for (int c0 = 0; c0 < n; c0 += 8) {
-    int nn = n - c0 < 8 ? n - c0 : 8;
-    tile_gemv<FMT, 8>(ce, se, rt, d.ngh, g0 + c0, nn, src, ag, lane);
-    tile_gemv<FMT, 8>(ce + gate_codes, se + gate_scales, rt, d.ngh, g0 + c0, nn, src, au, lane);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    part[wave][0][lane][i] = ag[i];
-    part[wave][1][lane][i] = au[i];
+    published(dep);
+    if (lane == 0) s_last = atomicAdd(&d.ecnt[j], 1u) == 2u * n_rt - 1 ? 1u : 0u;
   }
   __syncthreads();
-  if (wave == 0 && (lane & 15) == 1) {
+  if (!s_last) return;
+  // last workgroup of route j: h = silu(g) * u (c/qwen.c:3419), then digits
+  float *hb = (float *)smem;  // [I], reuses the digit buffer
+  const float *g = d.gu + (size_t)j * 2 * d.I, *u = g + d.I;
+  for (int i0 = threadIdx.x; i0 < d.I; i0 += 4 * kThreads) {
+    float gv[4], uv[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float g = part[0][0][lane][i] + part[1][0][lane][i] + part[2][0][lane][i] + part[3][0][lane][i];
-      float u = part[0][1][lane][i] + part[1][1][lane][i] + part[2][1][lane][i] + part[3][1][lane][i];
-      int row = rt * kTileRows + 4 * (lane >> 4) + i;
-      d.hroute[(size_t)j * d.I + row] = silu_ref(g) * u;
+    for (int q = 0; q < 4; q++) {
+      int i = i0 + q * kThreads;
+      i = i < d.I ? i : d.I - 1;
+      gv[q] = read_published(g + i);
+      uv[q] = read_published(u + i);
     }
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      if (i0 + q * kThreads < d.I) hb[i0 + q * kThreads] = silu_ref(gv[q]) * uv[q];
   }
-  if (!block_last_arrival(&d.ecnt[j], (unsigned)n_route_tiles, &s_flag)) return;
-  // last tile of expert j: its hidden vector -> digits for the down projection
+  __syncthreads();
   signed char *hd = d.hd + (size_t)j * 2 * d.Ip;
-  for (int g = wave; g < d.ngi; g += 4)
-    quantize_group(d.hroute + (size_t)j * d.I, d.I, g, hd, hd + d.Ip, d.hgp + (size_t)j * d.ngi, lane);
+  for (int q = wave; q < d.ngi; q += 4) quantize_group(hb, d.I, q, hd, hd + d.Ip, d.hgp + (size_t)j * d.ngi, lane);
   if (threadIdx.x == 0) atomicExch(&d.ecnt[j], 0u);
 }
 
 // ---------------------------------------------------------------------------
-// K3: down + combine.  grid H/16, one wave per route (64*K threads)
+// K3: routed down + shared down + combine.  grid H/16; waves 0..nwr-1 take
+// routes j = wave, wave + nwr, ...; waves nwr and nwr+1 each take half of the
+// shared expert's k range: they rebuild that half of the shared hidden vector
+// from the integer sums and run its rows of the int8 down projection.
+// LDS: per routed wave digits [2][Ip] | group parameters [ngi]; then the
+// shared hidden vector h [Ish] f32 and its int8 quantisation [Ish].
 // ---------------------------------------------------------------------------
+constexpr int kShRegs = 8;  // shared hidden rows per lane loaded ahead
+
 template <int FMT>
-__global__ void k_dec_down(Dec d, const unsigned char *__restrict__ codes, const float *__restrict__ scales,
-                           size_t expert_codes, size_t expert_scales, size_t down_codes_off, size_t down_scales_off,
-                           float *__restrict__ y, int *route_idx, float *route_weight) {
+__global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
+    Dec d, const unsigned char *__restrict__ codes, const float *__restrict__ scales, size_t expert_codes,
+    size_t expert_scales, size_t down_codes_off, size_t down_scales_off, const signed char *__restrict__ dq,
+    const float *__restrict__ ds, const float *__restrict__ gs, const float *__restrict__ us,
+    float *__restrict__ y, int *route_idx, float *route_weight) {
+  extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float vals[kMaxK][kTileRows];
-  for (int i = threadIdx.x; i < kMaxK * kTileRows; i += blockDim.x) (&vals[0][0])[i] = 0.0f;
+  __shared__ int ish[2][kTileRows];
+  __shared__ float red[2];
   __shared__ __align__(16) signed char zero16[16];
-  const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6, nwr = nw - 2;
   const int rt = blockIdx.x;
+  const size_t wbytes = 2 * (size_t)d.Ip + 16 * (size_t)d.ngi;
+  float *hf = (float *)(smem + nwr * wbytes);    // [Ish]
+  signed char *hq = (signed char *)(hf + d.Ish);  // [Ish]
+  const bool routed = wave < nwr;
+  for (int i = threadIdx.x; i < kMaxK * kTileRows; i += blockDim.x) (&vals[0][0])[i] = 0.0f;
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
-  __syncthreads();
-  if (j < d.K && (unsigned)d.idx[j] < (unsigned)d.E) {
-    const int e = d.idx[j];
-    const signed char *hd = d.hd + (size_t)j * 2 * d.Ip;
-    DigitSrc src = lane_digits(lane, 1, hd, d.Ip, d.hgp + (size_t)j * d.ngi, d.ngi, zero16);
-    float acc[4] = {0, 0, 0, 0};
-    const unsigned char *ce = codes + (size_t)e * expert_codes + down_codes_off;
-    const float *se = scales + (size_t)e * expert_scales + down_scales_off;
-    for (int c0 = 0; c0 < d.ngi; c0 += 8) {
-      int nn = d.ngi - c0 < 8 ? d.ngi - c0 : 8;
-      tile_gemv<FMT, 8>(ce, se, rt, d.ngi, c0, nn, src, acc, lane);
+  const int p = d.imisc[0];
+  const float sx = d.misc[0];
+  const int nk = d.Ish / 64, sw = wave - nwr;
+  const int kc0 = routed ? 0 : sw * nk / 2, kc1 = routed ? 0 : (sw + 1) * nk / 2;
+
+  TilePrefetch<FMT, 8> t;
+  RowPrefetch<8> pd;
+  float hm = 0.0f;
+  int e = -1;
+  if (routed) {
+    // ---- route `wave`: its hidden digits (cached) first, then its tiles ----
+    signed char *dig = (signed char *)(smem + wave * wbytes);
+    float4 *gp = (float4 *)(dig + 2 * (size_t)d.Ip);
+    if (wave < d.K) e = d.idx[wave];
+    if ((unsigned)e < (unsigned)d.E) {
+      const int4 *hs = (const int4 *)(d.hd + (size_t)wave * 2 * d.Ip);
+      const int n16 = (2 * d.Ip) / 16;
+      int4 h0 = lane < n16 ? hs[lane] : int4{0, 0, 0, 0};
+      int4 h1 = lane + 64 < n16 ? hs[lane + 64] : int4{0, 0, 0, 0};
+      float4 g0 = lane < d.ngi ? d.hgp[(size_t)wave * d.ngi + lane] : make_float4(0, 0, 0, 0);
+      tile_prefetch<FMT, 8>(t, codes + (size_t)e * expert_codes + down_codes_off,
+                            scales + (size_t)e * expert_scales + down_scales_off, rt, d.ngi, 0,
+                            d.ngi < 8 ? d.ngi : 8, lane);
+      if (lane < n16) ((int4 *)dig)[lane] = h0;
+      if (lane + 64 < n16) ((int4 *)dig)[lane + 64] = h1;
+      for (int i = lane + 128; i < n16; i += 64) ((int4 *)dig)[i] = hs[i];
+      if (lane < d.ngi) gp[lane] = g0;
+      for (int i = lane + 64; i < d.ngi; i += 64) gp[i] = d.hgp[(size_t)wave * d.ngi + i];
     }
-    if ((lane & 15) == 1) {
+  } else {
+    // ---- shared half: integer sums (cached) first, then the int8 rows ----
+    const int *accp = d.acc + (size_t)p * 2 * d.Ish;
+    const int r0 = kc0 * 64, r1 = kc1 * 64;
+    int ag[kShRegs], au[kShRegs];
+    float sg[kShRegs], su[kShRegs];
 #pragma unroll
-      for (int i = 0; i < 4; i++) vals[j][4 * (lane >> 4) + i] = acc[i];
+    for (int q = 0; q < kShRegs; q++) {
+      int i = r0 + q * 64 + lane;
+      i = i < r1 ? i : (r1 > 0 ? r1 - 1 : 0);  // clamped: no branch ahead of the rows
+      ag[q] = accp[i];
+      au[q] = accp[d.Ish + i];
+      sg[q] = gs[i];
+      su[q] = us[i];
+    }
+    const int ke0 = kc0 + 8 < kc1 ? kc0 + 8 : kc1;
+    rows_prefetch<8>(pd, dq, d.Ish, rt * kTileRows, kc0, ke0, lane);
+    // h = silu(g) * u from the exact integer dots (IDOT epilogue
+    // ((float)dot * s_row) * sx, c/qwen.c:1766)
+#pragma unroll
+    for (int q = 0; q < kShRegs; q++) {
+      int i = r0 + q * 64 + lane;
+      if (i < r1) {
+        float h = silu_ref((float)ag[q] * sg[q] * sx) * ((float)au[q] * su[q] * sx);
+        hf[i] = h;
+        hm = fmaxf(hm, fabsf(h));
+      }
+    }
+    for (int i = r0 + kShRegs * 64 + lane; i < r1; i += 64) {
+      float h = silu_ref((float)accp[i] * gs[i] * sx) * ((float)accp[d.Ish + i] * us[i] * sx);
+      hf[i] = h;
+      hm = fmaxf(hm, fabsf(h));
+    }
+    hm = wave_max_dpp(hm);
+    if (lane == 0) red[sw] = hm;
+  }
+  __syncthreads();
+  // qrow_i8 scale of the whole shared hidden vector
+  float shx = fmaxf(red[0], red[1]) / 127.0f;
+  if (shx < 1e-12f) shx = 1e-12f;
+
+  if (routed) {
+    signed char *dig = (signed char *)(smem + wave * wbytes);
+    float4 *gp = (float4 *)(dig + 2 * (size_t)d.Ip);
+    const DigitSrc src = lane_digits(lane, 1, dig, d.Ip, gp, d.ngi, zero16);
+    for (int j = wave; j < d.K; j += nwr) {
+      if (j != wave) e = d.idx[j];
+      if ((unsigned)e >= (unsigned)d.E) continue;
+      const unsigned char *ce = codes + (size_t)e * expert_codes + down_codes_off;
+      const float *se = scales + (size_t)e * expert_scales + down_scales_off;
+      float acc[4] = {0, 0, 0, 0};
+      for (int c0 = 0; c0 < d.ngi; c0 += 8) {
+        const int nn = d.ngi - c0 < 8 ? d.ngi - c0 : 8;
+        if (j != wave || c0 != 0) {
+          tile_prefetch<FMT, 8>(t, ce, se, rt, d.ngi, c0, nn, lane);
+          if (c0 == 0) {
+            // a later route: its digits -> this wave's LDS (wave-local)
+            const int4 *hs = (const int4 *)(d.hd + (size_t)j * 2 * d.Ip);
+            for (int i = lane; i < (2 * d.Ip) / 16; i += 64) ((int4 *)dig)[i] = hs[i];
+            for (int i = lane; i < d.ngi; i += 64) gp[i] = d.hgp[(size_t)j * d.ngi + i];
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+        tile_compute<FMT, 8>(t, c0, nn, src, acc, lane);
+      }
+      digit_fold(acc);
+      if ((lane & 15) == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) vals[j][4 * (lane >> 4) + i] = acc[i];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else {
+    // this half's int8 hidden values (wave-local rows), then the dots
+    const float hinv = 1.0f / shx;
+    for (int i = kc0 * 64 + lane; i < kc1 * 64; i += 64) hq[i] = (signed char)__builtin_rintf(hf[i] * hinv);
+    __builtin_amdgcn_wave_barrier();
+    v4i c = {0, 0, 0, 0};
+    const bool bvalid = (lane & 15) == 0;
+    const int ke0 = kc0 + 8 < kc1 ? kc0 + 8 : kc1;
+    rows_compute<8>(pd, kc0, ke0, hq, 0, bvalid, c, lane);
+    for (int kc = ke0; kc < kc1; kc += 8) {
+      int e1 = kc + 8 < kc1 ? kc + 8 : kc1;
+      idot_tile<8>(dq, d.Ish, rt * kTileRows, kc, e1, hq, 0, bvalid, c, lane);
+    }
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) ish[sw][4 * (lane >> 4) + i] = c[i];
     }
   }
   __syncthreads();
   if (threadIdx.x < kTileRows) {
-    int row = rt * kTileRows + threadIdx.x;
+    // moe_forward's combine: fma over k in route order, then shared * gate
+    const int row = rt * kTileRows + threadIdx.x;
     float out = 0.0f;
     for (int k = 0; k < d.K; k++) out = __builtin_fmaf(vals[k][threadIdx.x], d.w[k], out);
-    out = __builtin_fmaf(d.shout[row], d.misc[1], out);
+    const float shv = (float)(ish[0][threadIdx.x] + ish[1][threadIdx.x]) * ds[row] * shx;
+    out = __builtin_fmaf(shv, d.misc[1], out);
     y[row] = out;
   }
-  if (blockIdx.x == 0 && threadIdx.x < d.K) {
+  // clear the other parity's integer sums for the next call; flip the parity
+  int *accz = d.acc + (size_t)(1 - p) * 2 * d.Ish;
+  const int n_acc = 2 * d.Ish, chunk = (n_acc + gridDim.x - 1) / gridDim.x;
+  const int z0 = blockIdx.x * chunk, z1 = z0 + chunk < n_acc ? z0 + chunk : n_acc;
+  for (int i = z0 + threadIdx.x; i < z1; i += blockDim.x) accz[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) d.cnt[1] = (unsigned)(1 - p);
+  if (blockIdx.x == 0 && (int)threadIdx.x < d.K) {
     if (route_idx) route_idx[threadIdx.x] = d.idx[threadIdx.x];
     if (route_weight) route_weight[threadIdx.x] = d.w[threadIdx.x];
   }
 }
 
-}  // namespace
-
-namespace sw {
-
-// layout of ColiMoeLayer::sync: cnt[16] | ecnt[32] | rtcnt[Ish/16] | acc[2*Ish]
-size_t decode_sync_words(const ColiMoeShape &s) {
-  return 16 + kMaxK + (size_t)(s.shared_intermediate / kTileRows) + 2 * (size_t)s.shared_intermediate;
-}
-
-int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight) {
+struct DecLaunch {
   Dec d;
+  int g1, g2, g3, t3;
+  size_t lds1, lds2, lds3;
+};
+
+// Shapes the decode kernels take; others run the many-token path.
+bool decode_plan(const ColiMoeLayer *L, DecLaunch &p) {
+  Dec &d = p.d;
   memset(&d, 0, sizeof(d));
   d.H = L->sh.hidden;
   d.E = L->sh.experts;
@@ -573,35 +865,74 @@ int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *r
   d.Hp = d.ngh * kGroup;
   d.Ip = d.ngi * kGroup;
   d.KQ = d.H >= 512 ? d.H / 512 : 1;
+  if (d.H > 16384 || d.K > kMaxK) return false;
+  d.n_router_wg = (d.E + 1 + 3) / 4;
+  d.n_shared_wg = ((d.Ish / kTileRows) * d.KQ + 3) / 4;
+  p.g1 = d.n_router_wg + d.n_shared_wg + (d.ngh + 3) / 4;
+  size_t xs_bytes = ((size_t)d.H * 4 + 15) & ~(size_t)15;
+  size_t sel = (size_t)(d.E + 1) * 16 + (size_t)d.E * 8;
+  p.lds1 = xs_bytes + (sel > (size_t)d.H ? sel : (size_t)d.H);
+  p.g2 = d.K * 2 * (d.I / kTileRows);
+  size_t l2a = 2 * (size_t)d.Hp + (size_t)d.ngh * 16, l2b = (size_t)d.I * 4;
+  p.lds2 = l2a > l2b ? l2a : l2b;
+  size_t wbytes = 2 * (size_t)d.Ip + 16 * (size_t)d.ngi;
+  int nwr = d.K < kMaxDownWaves ? d.K : kMaxDownWaves;
+  p.g3 = d.H / kTileRows;
+  p.t3 = 64 * (nwr + 2);
+  p.lds3 = nwr * wbytes + 5 * (size_t)d.Ish;
+  const size_t lim = 64 * 1024;
+  return p.lds1 <= lim && p.lds2 <= lim && p.lds3 <= lim;
+}
+
+}  // namespace
+
+namespace sw {
+
+// layout of ColiMoeLayer::sync: cnt[16] | ecnt[32] | acc[2][2*Ish]
+size_t decode_sync_words(const ColiMoeShape &s) { return 16 + kMaxK + 4 * (size_t)s.shared_intermediate; }
+
+int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight) {
+  DecLaunch p;
+  if (!decode_plan(L, p)) return 1;
+  Dec &d = p.d;
   size_t bytes = dec_carve(d, nullptr);
   if (ensure_scratch(ctx, kScrShared, bytes, "decode workspace allocation")) return -1;
   dec_carve(d, (char *)ctx->scratch[kScrShared]);
   d.cnt = L->sync;
   d.ecnt = L->sync + 16;
-  d.rtcnt = L->sync + 16 + kMaxK;
-  d.acc = (int *)(L->sync + 16 + kMaxK + d.Ish / kTileRows);
+  d.acc = (int *)(L->sync + 16 + kMaxK);
   hipStream_t st = ctx->stream;
-  int n_tasks = (d.E + 1) + (d.Ish / kTileRows) * d.KQ + d.ngh;
-  int g1 = (n_tasks + 3) / 4;
-  size_t lds1 = ((size_t)d.H * 5 + 15) / 16 * 16 + (size_t)d.E * 4;
-  k_dec_route<<<g1, kDecThreads, lds1, st>>>(d, x, L->router, L->sgate_row, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us,
-                                           L->router_mode, L->stats);
-  int g2 = d.K * (d.I / kTileRows) + d.H / kTileRows;
-  size_t lds2 = 2 * (size_t)d.Hp + (size_t)d.ngh * 16;
+  const bool timing = ctx->moe_timing != 0;
+  if (timing) (void)hipEventRecord(ctx->moe_event[0], st);
+  k_dec_route<<<p.g1, kThreads, p.lds1, st>>>(d, x, L->router, L->sgate_row, L->sh_gq, L->sh_uq, L->router_mode,
+                                              L->stats);
+  if (timing) (void)hipEventRecord(ctx->moe_event[1], st);
   if (L->sh.expert_format == 4)
-    k_dec_experts<4><<<g2, kDecThreads, lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                     L->gate_codes, L->gate_scales, L->sh_dq, L->sh_ds);
+    k_dec_experts<4><<<p.g2, kThreads, p.lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
+                                                      L->gate_codes, L->gate_scales);
   else
-    k_dec_experts<3><<<g2, kDecThreads, lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                     L->gate_codes, L->gate_scales, L->sh_dq, L->sh_ds);
-  int t3 = 64 * d.K;
+    k_dec_experts<3><<<p.g2, kThreads, p.lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
+                                                      L->gate_codes, L->gate_scales);
+  if (timing) (void)hipEventRecord(ctx->moe_event[2], st);
   if (L->sh.expert_format == 4)
-    k_dec_down<4><<<d.H / kTileRows, t3, 0, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                   2 * L->gate_codes, 2 * L->gate_scales, y, route_idx, route_weight);
+    k_dec_down<4><<<p.g3, p.t3, p.lds3, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
+                                              2 * L->gate_codes, 2 * L->gate_scales, L->sh_dq, L->sh_ds, L->sh_gs,
+                                              L->sh_us, y, route_idx, route_weight);
   else
-    k_dec_down<3><<<d.H / kTileRows, t3, 0, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                   2 * L->gate_codes, 2 * L->gate_scales, y, route_idx, route_weight);
-  return launch_status("MoE decode step");
+    k_dec_down<3><<<p.g3, p.t3, p.lds3, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
+                                              2 * L->gate_codes, 2 * L->gate_scales, L->sh_dq, L->sh_ds, L->sh_gs,
+                                              L->sh_us, y, route_idx, route_weight);
+  if (timing) (void)hipEventRecord(ctx->moe_event[3], st);
+  int rc = launch_status("MoE decode step");
+  if (timing && rc == 0) {
+    (void)hipEventSynchronize(ctx->moe_event[3]);
+    for (int i = 0; i < 3; i++) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, ctx->moe_event[i], ctx->moe_event[i + 1]) == hipSuccess) ctx->moe_dec_ms[i] += ms;
+    }
+    ctx->moe_dec_calls++;
+  }
+  return rc;
 }
 
 }  // namespace sw

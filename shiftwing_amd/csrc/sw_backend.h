@@ -50,6 +50,9 @@ struct ColiCuda {
   hipEvent_t moe_event[8];
   double moe_ms[8];
   unsigned long long moe_calls;
+  double moe_dec_ms[3];
+  unsigned long long moe_dec_calls;
+  int moe_generic_only;  // single-token steps take the many-token kernels
 };
 
 namespace sw {

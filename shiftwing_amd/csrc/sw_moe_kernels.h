@@ -123,9 +123,10 @@ __device__ __forceinline__ void tile_prefetch(TilePrefetch<FMT, NMAX> &t, const 
 
 // Group-scaled dots over the prefetched groups: per group, the two int8
 // MFMAs give exact int32 dots of the codes with both activation digits; the
-// epilogue applies the digit scales, removes the code offset (8 for int4, 4
-// for int3) through the digit sums, and accumulates scale[row, group] * dot.
-// Valid results: lanes with odd column c (token c/2), rows 4*kb+i.
+// epilogue applies the lane's digit scale, removes the code offset (8 for
+// int4, 4 for int3) through the digit sum, and accumulates
+// scale[row, group] * dot into the lane's own accumulator.  The two digit
+// columns of a token are folded once, after the last group (digit_fold).
 template <int FMT, int NMAX>
 __device__ __forceinline__ void tile_compute(const TilePrefetch<FMT, NMAX> &t, int g0, int n, const DigitSrc &ds,
                                              float acc[4], int lane) {
@@ -152,12 +153,15 @@ __device__ __forceinline__ void tile_compute(const TilePrefetch<FMT, NMAX> &t, i
       c = mfma_i8(a1, b1, c);
       const float scv[4] = {t.sc[i].x, t.sc[i].y, t.sc[i].z, t.sc[i].w};
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float f = (float)(c[r] - OFF * Q) * dsc;
-        float tsum = f + dpp_row_shr1(f);
-        acc[r] = __builtin_fmaf(tsum, scv[r], acc[r]);
-      }
+      for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf((float)(c[r] - OFF * Q) * dsc, scv[r], acc[r]);
     }
+}
+
+// Digit 1 (even column) + digit 2 (odd column): valid in lanes with odd
+// column c (token c/2), rows 4*kb+i.
+__device__ __forceinline__ void digit_fold(float acc[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = acc[r] + dpp_row_shr1(acc[r]);
 }
 
 template <int FMT, int NMAX>
@@ -198,23 +202,41 @@ __device__ __forceinline__ void quantize_group(const float *v, int n, int g, sig
 
 // Exact int32 dots of 16 int8 rows (row-major, leading dim ld) with up to 16
 // int8 activation rows (B column = lane%16 = activation row), over 64-wide
-// k chunks [kc0, kc1).  All loads issued before the MFMAs (NMAX chunks max).
+// k chunks [kc0, kc1), at most NMAX chunks per call.  The weight loads are a
+// separate step so that a caller can issue them before it has produced the
+// activations.
 template <int NMAX>
-__device__ __forceinline__ void idot_tile(const signed char *W, int ld, int row0, int kc0, int kc1,
-                                          const signed char *bsrc, int bld, bool bvalid, v4i &c, int lane) {
-  const int r = lane & 15, kb = lane >> 4;
-  const signed char *arow = W + (size_t)(row0 + r) * ld + kb * 16;
-  const signed char *brow = bsrc + (size_t)r * bld + kb * 16;
-  v4i a[NMAX], b[NMAX];
+struct RowPrefetch {
+  v4i a[NMAX];
+};
+
+template <int NMAX>
+__device__ __forceinline__ void rows_prefetch(RowPrefetch<NMAX> &p, const signed char *W, int ld, int row0, int kc0,
+                                              int kc1, int lane) {
+  const signed char *arow = W + (size_t)(row0 + (lane & 15)) * ld + (lane >> 4) * 16;
+#pragma unroll
+  for (int i = 0; i < NMAX; i++)
+    if (kc0 + i < kc1) p.a[i] = __builtin_nontemporal_load((const v4i *)(arow + (size_t)(kc0 + i) * 64));
+}
+
+template <int NMAX>
+__device__ __forceinline__ void rows_compute(const RowPrefetch<NMAX> &p, int kc0, int kc1, const signed char *bsrc,
+                                             int bld, bool bvalid, v4i &c, int lane) {
+  const signed char *brow = bsrc + (size_t)(lane & 15) * bld + (lane >> 4) * 16;
 #pragma unroll
   for (int i = 0; i < NMAX; i++)
     if (kc0 + i < kc1) {
-      a[i] = __builtin_nontemporal_load((const v4i *)(arow + (size_t)(kc0 + i) * 64));
-      b[i] = bvalid ? *(const v4i *)(brow + (size_t)(kc0 + i) * 64) : v4i{0, 0, 0, 0};
+      v4i b = bvalid ? *(const v4i *)(brow + (size_t)(kc0 + i) * 64) : v4i{0, 0, 0, 0};
+      c = mfma_i8(p.a[i], b, c);
     }
-#pragma unroll
-  for (int i = 0; i < NMAX; i++)
-    if (kc0 + i < kc1) c = mfma_i8(a[i], b[i], c);
+}
+
+template <int NMAX>
+__device__ __forceinline__ void idot_tile(const signed char *W, int ld, int row0, int kc0, int kc1,
+                                          const signed char *bsrc, int bld, bool bvalid, v4i &c, int lane) {
+  RowPrefetch<NMAX> p;
+  rows_prefetch<NMAX>(p, W, ld, row0, kc0, kc1, lane);
+  rows_compute<NMAX>(p, kc0, kc1, bsrc, bld, bvalid, c, lane);
 }
 
 // Order-preserving 32-bit key of a float (larger float -> larger key).

@@ -34,6 +34,7 @@ struct ColiMoeLayer {
 namespace sw {
 // words of ColiMoeLayer::sync for a layer shape
 size_t decode_sync_words(const ColiMoeShape &s);
-// One decoded token through one layer (three kernels); see moe_decode.hip.
+// One decoded token through one layer (three kernels).  Returns 0 on success,
+// -1 on error, 1 when the layer shape is outside the decode kernels' limits.
 int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight);
 }  // namespace sw
