@@ -1,0 +1,239 @@
+"""The oracle (oracle/moe_oracle.c, a C restatement of the reference CPU MoE
+path) pinned without a GPU.
+
+What pins it (each check chosen so that a plausible slip fails one of them):
+  * golden vectors written by the compiled reference (tests/golden/*.npz,
+    made by tests/golden/make_golden.py from c/qwen.c compiled in place):
+    router_topk, the int8/int4/int3 row dots (IDOT on and off, single and
+    batched), and whole layers (moe_forward decode, moe_prefill_grouped);
+  * the reference's own router fixture c/fixtures/router.json (indices exact,
+    weights within 2e-6 as in c/tests/test_router.c);
+  * byte-layout known answers from c/tests/test_convert_qwen.py:283-290 and
+    c/quant.h:167-209, and a brute-force fp64 dequantised dot (closed form);
+  * integer identities (IDOT dots are exact int32; bucketing is a stable
+    counting sort) and the tie rule of router_topk (lowest index first);
+  * the compiled reference itself (oracle/_ref) on fresh seeds, when built.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3"]
+
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------- router_topk
+def test_router_topk_golden_bitexact(oracle):
+    g = np.load(os.path.join(GOLDEN, "router_topk.npz"))
+    for c in range(len(g["E"])):
+        E, K = int(g["E"][c]), int(g["K"][c])
+        idx, w = oracle.router_topk(g["logits"][c, :E].copy(), K)
+        assert np.array_equal(idx, g["idx"][c, :K]), c
+        assert np.array_equal(_bits(w), _bits(g["weight"][c, :K])), c
+
+
+def test_router_topk_reference_fixture(oracle):
+    """c/fixtures/router.json: indices exact, weights within 2e-6."""
+    j = json.load(open(os.path.join(GOLDEN, "router.json")))
+    logits = np.asarray(j["logits"], np.float32)
+    K = int(j["top_k"])
+    want_i = np.asarray(j["indices"], np.int32)
+    want_w = np.asarray(j["weights"], np.float32)
+    logits = logits.reshape(-1, logits.shape[-1])
+    want_i = want_i.reshape(len(logits), -1)
+    want_w = want_w.reshape(len(logits), -1)
+    for t in range(len(logits)):
+        idx, w = oracle.router_topk(logits[t].copy(), K)
+        assert np.array_equal(idx, want_i[t])
+        assert np.max(np.abs(w - want_w[t])) <= 2e-6
+
+
+def test_router_topk_closed_forms(oracle):
+    rng = np.random.default_rng(5)
+    # distinct, well separated logits: indices are the descending sort, the
+    # weights the renormalised softmax of the top K
+    for E, K in [(16, 4), (256, 8), (512, 10)]:
+        lg = (rng.permutation(E).astype(np.float32) * 0.05).astype(np.float32)
+        idx, w = oracle.router_topk(lg.copy(), K)
+        want = np.argsort(-lg, kind="stable")[:K]
+        assert np.array_equal(idx, want)
+        p = np.exp(lg[want].astype(np.float64) - lg.max())
+        assert np.max(np.abs(w - p / p.sum())) <= 1e-6
+        assert abs(float(np.sum(w, dtype=np.float64)) - 1.0) <= 1e-6
+    # equal logits: lowest index first
+    lg = np.zeros(32, np.float32)
+    lg[[3, 17, 9]] = 2.0
+    idx, w = oracle.router_topk(lg.copy(), 5)
+    assert list(idx[:3]) == [3, 9, 17] and list(idx[3:]) == [0, 1]
+
+
+# ---------------------------------------------------------------- row dots
+def _qmat_cases():
+    g = np.load(os.path.join(GOLDEN, "qmat.npz"))
+    keys = sorted({k.rsplit("_", 1)[0] for k in g.files if k.endswith("_q")})
+    return g, keys
+
+
+def test_qmat_golden_bitexact(oracle):
+    from oracle.pyoracle import HostQMat
+    g, keys = _qmat_cases()
+    assert keys
+    for k in keys:
+        fmt, I = int(k.split("_")[0][1:]), int(k.split("_")[1][1:])
+        q, s = g[k + "_q"], g[k + "_s"]
+        m = HostQMat(fmt, q.shape[0], I, 0 if fmt == 1 else 128, q=q, s=s)
+        assert np.array_equal(_bits(oracle.qmat_mul(g[k + "_x"], m, 1)), _bits(g[k + "_y"])), k
+        assert np.array_equal(_bits(oracle.qmat_mul(g[k + "_x"], m, 0)), _bits(g[k + "_y_noidot"])), k
+        assert np.array_equal(_bits(oracle.qmat_mul_batch(g[k + "_X"], m)), _bits(g[k + "_Y"])), k
+
+
+def _dequant(fmt, q, s, I, gs=128):
+    """Brute-force dequantisation from the byte layouts (fp64)."""
+    O = q.shape[0]
+    w = np.zeros((O, I), np.float64)
+    for o in range(O):
+        for i in range(I):
+            if fmt == 1:
+                w[o, i] = float(q[o, i]) * float(s[o])
+                continue
+            if fmt == 4:
+                byte = int(q[o, i >> 1])
+                code = (byte & 15) if (i & 1) == 0 else (byte >> 4)
+                v = code - 8
+            else:
+                j, k = i // 8, i % 8
+                word = int(q[o, 3 * j]) | int(q[o, 3 * j + 1]) << 8 | int(q[o, 3 * j + 2]) << 16
+                v = ((word >> (3 * k)) & 7) - 4
+            w[o, i] = v * float(s[o, i // gs])
+    return w
+
+
+def test_qmat_matches_bruteforce_dequant(oracle):
+    """The row dots equal x . dequant(W) up to fp32 rounding: pins nibble
+    order, triplet bit order, code offsets and the per-group scale index."""
+    from oracle.pyoracle import HostQMat
+    g, keys = _qmat_cases()
+    for k in keys:
+        fmt, I = int(k.split("_")[0][1:]), int(k.split("_")[1][1:])
+        q, s, x = g[k + "_q"], g[k + "_s"], g[k + "_x"]
+        w = _dequant(fmt, q, s, I)
+        want = w @ x.astype(np.float64)
+        m = HostQMat(fmt, q.shape[0], I, 0 if fmt == 1 else 128, q=q, s=s)
+        got = oracle.qmat_mul(x, m, 0)
+        scale = np.abs(w) @ np.abs(x.astype(np.float64)) + 1e-30
+        assert np.all(np.abs(got - want) <= 1e-5 * scale), k
+
+
+def test_layout_known_answers(oracle):
+    """int3: codes [-4..3] with scale 1 pack to 88 C6 FA
+    (c/tests/test_convert_qwen.py:283-290); int4: byte 0x71 holds values
+    (1-8, 7-8) = (-7, -1), low nibble first (c/quant.h:167-209)."""
+    from oracle.pyoracle import HostQMat
+    q3 = np.zeros((1, 48), np.uint8)
+    q3[0, :3] = [0x88, 0xC6, 0xFA]
+    s3 = np.ones((1, 1), np.float32)
+    m3 = HostQMat(3, 1, 8, 128, q=q3, s=s3)
+    for i in range(8):
+        x = np.zeros(8, np.float32)
+        x[i] = 1.0
+        assert oracle.qmat_mul(x, m3, 0)[0] == float(i - 4)
+    q4 = np.zeros((1, 64), np.uint8)
+    q4[0, 0] = 0x71
+    m4 = HostQMat(4, 1, 2, 128, q=q4, s=np.ones((1, 1), np.float32))
+    assert oracle.qmat_mul(np.array([1, 0], np.float32), m4, 0)[0] == -7.0
+    assert oracle.qmat_mul(np.array([0, 1], np.float32), m4, 0)[0] == -1.0
+
+
+def test_idot_is_exact_integer_dot(oracle):
+    """IDOT: x -> (q, sx) by qrow_i8; y_o = ((float)sum q*w) * s_o * sx with an
+    exact integer sum (checked against int64)."""
+    from oracle.pyoracle import HostQMat
+    rng = np.random.default_rng(9)
+    O, I = 7, 4099
+    w = rng.integers(-127, 128, (O, I), dtype=np.int8)
+    s = np.abs(rng.standard_normal(O)).astype(np.float32) * 0.01
+    x = rng.standard_normal(I).astype(np.float32)
+    q, sx = oracle.qrow_i8(x)
+    assert q.dtype == np.int8 and np.max(np.abs(q.astype(np.int32))) <= 127
+    dot = w.astype(np.int64) @ q.astype(np.int64)
+    assert np.all(np.abs(dot) < 2 ** 31)
+    want = (dot.astype(np.float32) * s) * np.float32(sx)
+    got = oracle.qmat_mul(x, HostQMat(1, O, I, 0, q=w, s=s), 1)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+# ---------------------------------------------------------------- bucketing
+def test_bucket_is_stable_counting_sort(oracle):
+    rng = np.random.default_rng(3)
+    for T, K, E in [(1, 8, 256), (7, 4, 16), (32, 10, 512), (512, 8, 256)]:
+        idx = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        off, tok, slot = oracle.bucket(idx, E)
+        # experts ascending; within an expert tokens ascending, slot = first k
+        want_tok, want_slot, want_off = [], [], [0]
+        for e in range(E):
+            for t in range(T):
+                ks = np.nonzero(idx[t] == e)[0]
+                if len(ks):
+                    want_tok.append(t)
+                    want_slot.append(int(ks[0]))
+            want_off.append(len(want_tok))
+        assert np.array_equal(off, want_off)
+        assert np.array_equal(tok, want_tok) and np.array_equal(slot, want_slot)
+
+
+# ---------------------------------------------------------------- layers
+def _layer(oracle, name):
+    g = np.load(os.path.join(GOLDEN, f"layer_{name}.npz"))
+    H, E, K, I, Ish, fmt, gs, seed, layer, T = (int(v) for v in g["cfg"])
+    return g, oracle.host_layer(seed, layer, H, E, K, I, Ish, fmt, gs)
+
+
+@pytest.mark.parametrize("name", LAYERS)
+def test_layer_golden_bitexact(oracle, name):
+    """moe_forward per token and moe_prefill_grouped over the block, bit for
+    bit against the compiled reference (same synthetic weights by seed)."""
+    g, hl = _layer(oracle, name)
+    for t in range(len(g["x"])):
+        y, tr = oracle.moe_forward(hl, g["x"][t], trace=True)
+        assert np.array_equal(tr["idx"], g["idx"][t]), (name, t)
+        assert np.array_equal(_bits(tr["weight"]), _bits(g["weight"][t])), (name, t)
+        assert np.array_equal(_bits(tr["logits"]), _bits(g["logits"][t])), (name, t)
+        assert np.array_equal(_bits(y), _bits(g["decode"][t])), (name, t)
+    yp = oracle.moe_prefill(hl, g["x"])
+    assert np.array_equal(_bits(yp), _bits(g["prefill"])), name
+
+
+def test_decode_equals_single_token_prefill(oracle):
+    """Batched == single (c/tests/test_quant_matmul.c:72-86) at the layer
+    level: a one-token prefill block is the decode step up to the combine's
+    contraction (fma chain vs mul-then-add), here within 1e-6 x RMS."""
+    g, hl = _layer(oracle, "small_q3")
+    for t in range(3):
+        a = oracle.moe_forward(hl, g["x"][t])
+        b = oracle.moe_prefill(hl, g["x"][t:t + 1])[0]
+        assert np.max(np.abs(a - b)) <= 1e-6 * float(np.sqrt(np.mean(a.astype(np.float64) ** 2)))
+
+
+def test_oracle_matches_compiled_reference(oracle):
+    """Fresh seeds through the compiled reference (oracle/_ref, built from the
+    reference's own c/qwen.c where /root/reference is present)."""
+    from oracle.pyoracle import Reference
+    try:
+        ref = Reference()
+    except Exception as e:  # not built (no reference sources here)
+        pytest.skip(f"compiled reference not available: {e}")
+    for (H, E, K, I, Ish, fmt, seed) in [(256, 16, 4, 128, 128, 4, 71), (384, 32, 8, 257, 129, 3, 72),
+                                         (1024, 64, 6, 256, 256, 3, 73)]:
+        hl = oracle.host_layer(seed, 2, H, E, K, I, Ish, fmt)
+        rl = ref.layer(hl)
+        X = np.stack([oracle.synth_x(seed, 2, t, H) for t in range(4)])
+        for t in range(4):
+            assert np.array_equal(_bits(oracle.moe_forward(hl, X[t])), _bits(rl.forward(X[t]))), (seed, t)
+        assert np.array_equal(_bits(oracle.moe_prefill(hl, X)), _bits(rl.prefill(X))), seed
