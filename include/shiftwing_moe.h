@@ -218,9 +218,9 @@ typedef struct {
     int group_size;          /* routed-expert quant group (128) */
 } ColiMoeShape;
 
-/* Allocate an HBM-resident layer (all experts).  Requires hidden,
- * intermediate and shared_intermediate to be multiples of 16, group_size 128
- * and topk <= 32. */
+/* Allocate an HBM-resident layer (all experts).  Requires hidden % 64 == 0,
+ * intermediate % 16 == 0, shared_intermediate % 64 == 0, group_size 128,
+ * expert_format 3 or 4, topk <= 32 and experts <= 4096. */
 int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out,
                                const ColiMoeShape *shape);
 void coli_cuda_moe_layer_destroy(ColiCuda *ctx, ColiMoeLayer *layer);
