@@ -11,17 +11,17 @@
 //              reference's full serial computation.  Router workgroups come
 //              first in the grid, so the selection overlaps the shared-expert
 //              streaming.
-//   K2 experts one workgroup per (route, matrix, 16 rows) of the routed gate /
-//              up tiles.  The last workgroup of a route forms its hidden vector
-//              h = silu(g) * u and quantises it to activation digits.
-//   K3 down    one workgroup per 16 output rows: one wave per route (routed
-//              down tiles) and one wave for the shared down projection, whose
-//              hidden vector every workgroup rebuilds from the integer sums;
-//              then the reference's combine order.
+//   K2 experts one workgroup per (route, 16 rows): each wave takes a quarter
+//              of the groups of both the gate and the up tile; the workgroup
+//              writes h = silu(g) * u for its 16 rows.
+//   K3 down    one workgroup per 16 output rows: one wave per route (it
+//              quantises its route's h, 8 lanes per 128-group, while its down
+//              tiles are in flight) and two waves for the shared down
+//              projection, whose hidden vector every workgroup rebuilds from
+//              the integer sums; then the reference's combine order.
 //
-// Fan-in (router rows in K1, routes in K2) is one release by one thread per
-// workgroup, whose own wave wrote the published data; every other hand-off is
-// a kernel boundary.  Counters are reset by their last arriver.  The shared
+// Fan-in (router rows in K1) publishes with device-scope atomics; every other
+// hand-off is a kernel boundary.  Counters are reset by their last arriver.  The shared
 // expert's integer sums alternate between two buffers (a parity word kept on
 // the device), so the buffer one call reads is cleared by the next one.  No
 // memset, no host state: consecutive calls and graph replays need nothing.
@@ -55,11 +55,8 @@ struct Dec {
   int *imisc;       // [0] parity of this call's integer sums
   int *idx;         // [K]
   float *w;         // [K]
-  float *gu;        // [K][2][I] routed gate / up outputs
-  signed char *hd;  // [K][2][Ip] routed hidden digits
-  float4 *hgp;      // [K][ngi]
+  float *h;         // [K][I] routed hidden vectors silu(g) * u
   unsigned *cnt;    // per layer: [0] router fan-in  [1] parity
-  unsigned *ecnt;   // per layer: [K] route fan-in
   int *acc;         // per layer: [2][2][Ish] shared gate/up int32 dots
 };
 
@@ -78,9 +75,7 @@ size_t dec_carve(Dec &d, char *base) {
   d.imisc = (int *)take(32);
   d.idx = (int *)take((size_t)kMaxK * 4);
   d.w = (float *)take((size_t)kMaxK * 4);
-  d.gu = (float *)take((size_t)d.K * 2 * d.I * 4);
-  d.hd = (signed char *)take((size_t)d.K * 2 * d.Ip);
-  d.hgp = (float4 *)take((size_t)d.K * d.ngi * 16);
+  d.h = (float *)take((size_t)d.K * d.I * 4);
   return off + 256;
 }
 
@@ -584,8 +579,10 @@ __global__ __launch_bounds__(kThreads) void k_dec_route(Dec d, const float *__re
 }
 
 // ---------------------------------------------------------------------------
-// K2: routed gate/up.  grid K * 2 * I/16 (route, matrix, row tile), 256
-// threads; the last workgroup of each route builds its hidden digits.
+// K2: routed gate/up.  grid K * I/16 (route, row tile), 256 threads.  Wave w
+// takes groups [w*per, w*per + per) of both matrices; the tile's scales for
+// both matrices are staged in LDS, so a wave holds only codes in flight.
+// LDS: digits [2][Hp] | group parameters [ngh] | scales [2][ngh][16].
 // ---------------------------------------------------------------------------
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned char *__restrict__ codes,
@@ -593,85 +590,71 @@ __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned 
                                                           size_t expert_scales, size_t gate_codes,
                                                           size_t gate_scales) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float part[4][64][4];
+  __shared__ float part[2][4][64][4];
   __shared__ __align__(16) signed char zero16[16];
-  __shared__ unsigned s_last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
   const int n_rt = d.I / kTileRows;
-  const int j = blockIdx.x / (2 * n_rt), r2 = blockIdx.x % (2 * n_rt);
-  const int mat = r2 / n_rt, rt = r2 % n_rt;
-  const int e = d.idx[j];
-  if ((unsigned)e >= (unsigned)d.E) return;  // router_topk's -1: the route contributes nothing
-  const unsigned char *ce = codes + (size_t)e * expert_codes + (size_t)mat * gate_codes;
-  const float *se = scales + (size_t)e * expert_scales + (size_t)mat * gate_scales;
-  const int per = (d.ngh + 3) / 4, g0 = wave * per;
-  const int n = (d.ngh < g0 + per ? d.ngh : g0 + per) - g0;
-  signed char *dig = (signed char *)smem;            // [2][Hp]
-  float4 *gp = (float4 *)(smem + 2 * (size_t)d.Hp);  // [ngh]
-  const DigitSrc src = lane_digits(lane, 1, dig, d.Hp, gp, d.ngh, zero16);
-  // activation digits first (cached; loads return in issue order), then tiles
-  // (unconditional loads at clamped indices: no branch ahead of the tiles)
-  const int n16 = (2 * d.Hp) / 16, tid = threadIdx.x;
+  const int j = blockIdx.x / n_rt, rt = blockIdx.x % n_rt;
+  signed char *dig = (signed char *)smem;                         // [2][Hp]
+  float4 *gp = (float4 *)(smem + 2 * (size_t)d.Hp);               // [ngh]
+  float *scl = (float *)(gp + d.ngh);                             // [2][ngh][16]
+  // activation digits and group parameters (cached): unconditional loads at
+  // clamped indices, issued before anything that depends on the route
+  const int n16 = (2 * d.Hp) / 16;
   const v4i *xdv = (const v4i *)d.xd;
   const v4i dr0 = xdv[tid < n16 ? tid : n16 - 1];
   const v4i dr1 = xdv[tid + kThreads < n16 ? tid + kThreads : n16 - 1];
   const float4 gr = d.xgp[tid < d.ngh ? tid : d.ngh - 1];
-  float acc[4] = {0, 0, 0, 0};
+  const int e = d.idx[j];
+  if ((unsigned)e >= (unsigned)d.E) return;  // router_topk's -1: the route contributes nothing
+  const unsigned char *cg = codes + (size_t)e * expert_codes;
+  const float *sg = scales + (size_t)e * expert_scales + (size_t)rt * d.ngh * kTileRows;
+  // this row tile's scales (2 x ngh x 16 floats, contiguous per matrix)
+  const int ns4 = d.ngh * 4;  // float4 per matrix
+  const int sq = tid < 2 * ns4 ? tid : 2 * ns4 - 1;
+  const v4f sr = *(const v4f *)((sq < ns4 ? sg : sg + gate_scales) + 4 * (sq % ns4));
+  const int per = (d.ngh + 3) / 4, g0 = wave * per;
+  const int n = (d.ngh < g0 + per ? d.ngh : g0 + per) - g0;
+  const DigitSrc src = lane_digits(lane, 1, dig, d.Hp, gp, d.ngh, zero16);
+  float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
   // every wave runs the first iteration (it holds the workgroup barrier)
   for (int c0 = 0; c0 == 0 || c0 < n; c0 += 8) {
     const int nn = n - c0 < 8 ? n - c0 : 8;
-    TilePrefetch<FMT, 8> t;
-    tile_prefetch<FMT, 8>(t, ce, se, rt, d.ngh, g0 + c0, nn, lane);
+    TileCodes<FMT, 8> tg, tu;
+    tile_codes_prefetch<FMT, 8>(tg, cg, rt, d.ngh, g0 + c0, nn, lane);
+    tile_codes_prefetch<FMT, 8>(tu, cg + gate_codes, rt, d.ngh, g0 + c0, nn, lane);
     if (c0 == 0) {
       if (tid < n16) ((v4i *)dig)[tid] = dr0;
       if (tid + kThreads < n16) ((v4i *)dig)[tid + kThreads] = dr1;
       for (int i = 2 * kThreads + tid; i < n16; i += kThreads) ((v4i *)dig)[i] = xdv[i];
       if (tid < d.ngh) gp[tid] = gr;
       for (int i = kThreads + tid; i < d.ngh; i += kThreads) gp[i] = d.xgp[i];
-      if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
+      if (tid < 2 * ns4) ((v4f *)scl)[tid] = sr;
+      for (int i = kThreads + tid; i < 2 * ns4; i += kThreads)
+        ((v4f *)scl)[i] = *(const v4f *)((i < ns4 ? sg : sg + gate_scales) + 4 * (i % ns4));
+      if (tid < 4) ((int *)zero16)[tid] = 0;
       __syncthreads();
     }
-    tile_compute<FMT, 8>(t, g0 + c0, nn, src, acc, lane);
+    tile_compute_lds<FMT, 8>(tg, g0 + c0, nn, src, scl, ag, lane);
+    tile_compute_lds<FMT, 8>(tu, g0 + c0, nn, src, scl + d.ngh * kTileRows, au, lane);
   }
-  digit_fold(acc);
+  digit_fold(ag);
+  digit_fold(au);
 #pragma unroll
-  for (int i = 0; i < 4; i++) part[wave][lane][i] = acc[i];
+  for (int i = 0; i < 4; i++) {
+    part[0][wave][lane][i] = ag[i];
+    part[1][wave][lane][i] = au[i];
+  }
   __syncthreads();
-  if (wave == 0) {
-    unsigned dep = 0;
-    if ((lane & 15) == 1) {
+  if (wave == 0 && (lane & 15) == 1) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float v = part[0][lane][i] + part[1][lane][i] + part[2][lane][i] + part[3][lane][i];
-        int row = rt * kTileRows + 4 * (lane >> 4) + i;
-        dep ^= publish(&d.gu[((size_t)j * 2 + mat) * d.I + row], v);
-      }
+    for (int i = 0; i < 4; i++) {
+      float g = part[0][0][lane][i] + part[0][1][lane][i] + part[0][2][lane][i] + part[0][3][lane][i];
+      float u = part[1][0][lane][i] + part[1][1][lane][i] + part[1][2][lane][i] + part[1][3][lane][i];
+      int row = rt * kTileRows + 4 * (lane >> 4) + i;
+      d.h[(size_t)j * d.I + row] = silu_ref(g) * u;  // c/qwen.c:3419
     }
-    published(dep);
-    if (lane == 0) s_last = atomicAdd(&d.ecnt[j], 1u) == 2u * n_rt - 1 ? 1u : 0u;
   }
-  __syncthreads();
-  if (!s_last) return;
-  // last workgroup of route j: h = silu(g) * u (c/qwen.c:3419), then digits
-  float *hb = (float *)smem;  // [I], reuses the digit buffer
-  const float *g = d.gu + (size_t)j * 2 * d.I, *u = g + d.I;
-  for (int i0 = threadIdx.x; i0 < d.I; i0 += 4 * kThreads) {
-    float gv[4], uv[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      int i = i0 + q * kThreads;
-      i = i < d.I ? i : d.I - 1;
-      gv[q] = read_published(g + i);
-      uv[q] = read_published(u + i);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-      if (i0 + q * kThreads < d.I) hb[i0 + q * kThreads] = silu_ref(gv[q]) * uv[q];
-  }
-  __syncthreads();
-  signed char *hd = d.hd + (size_t)j * 2 * d.Ip;
-  for (int q = wave; q < d.ngi; q += 4) quantize_group(hb, d.I, q, hd, hd + d.Ip, d.hgp + (size_t)j * d.ngi, lane);
-  if (threadIdx.x == 0) atomicExch(&d.ecnt[j], 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -684,6 +667,31 @@ __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned 
 // ---------------------------------------------------------------------------
 constexpr int kShRegs = 8;  // shared hidden rows per lane loaded ahead
 
+// A route's hidden vector -> digits in this wave's LDS, 1024 values per pass
+// (the lane's 16 values of the first pass come loaded ahead in hv).
+__device__ __forceinline__ void route_digits(const float *hj, int I, int Ip, const v4f hv[4], signed char *dig,
+                                             float4 *gp, int lane) {
+  quantize_slice8(hv, 0, Ip, dig, dig + Ip, gp, lane);
+  for (int base = 1024; base < Ip; base += 1024) {
+    v4f w[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      int i = base + 16 * lane + 4 * q;
+      w[q] = i < I ? *(const v4f *)(hj + i) : v4f{0, 0, 0, 0};
+    }
+    quantize_slice8(w, base, Ip, dig, dig + Ip, gp, lane);
+  }
+}
+
+__device__ __forceinline__ void route_h_load(const float *hj, int I, v4f hv[4], int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    int i = 16 * lane + 4 * q;
+    hv[q] = *(const v4f *)(hj + (i < I ? i : 0));
+    if (i >= I) hv[q] = v4f{0, 0, 0, 0};
+  }
+}
+
 template <int FMT>
 __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
     Dec d, const unsigned char *__restrict__ codes, const float *__restrict__ scales, size_t expert_codes,
@@ -694,6 +702,8 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
   __shared__ float vals[kMaxK][kTileRows];
   __shared__ int ish[2][kTileRows];
   __shared__ float red[2];
+  __shared__ float cw[kMaxK + 1];     // route weights, shared gate
+  __shared__ float cds[kTileRows];    // shared down row scales
   __shared__ __align__(16) signed char zero16[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6, nwr = nw - 2;
@@ -714,27 +724,29 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
   float hm = 0.0f;
   int e = -1;
   if (routed) {
-    // ---- route `wave`: its hidden digits (cached) first, then its tiles ----
+    // ---- route `wave`: its hidden vector (cached) and expert id, then tiles
     signed char *dig = (signed char *)(smem + wave * wbytes);
     float4 *gp = (float4 *)(dig + 2 * (size_t)d.Ip);
-    if (wave < d.K) e = d.idx[wave];
-    if ((unsigned)e < (unsigned)d.E) {
-      const int4 *hs = (const int4 *)(d.hd + (size_t)wave * 2 * d.Ip);
-      const int n16 = (2 * d.Ip) / 16;
-      int4 h0 = lane < n16 ? hs[lane] : int4{0, 0, 0, 0};
-      int4 h1 = lane + 64 < n16 ? hs[lane + 64] : int4{0, 0, 0, 0};
-      float4 g0 = lane < d.ngi ? d.hgp[(size_t)wave * d.ngi + lane] : make_float4(0, 0, 0, 0);
-      tile_prefetch<FMT, 8>(t, codes + (size_t)e * expert_codes + down_codes_off,
-                            scales + (size_t)e * expert_scales + down_scales_off, rt, d.ngi, 0,
-                            d.ngi < 8 ? d.ngi : 8, lane);
-      if (lane < n16) ((int4 *)dig)[lane] = h0;
-      if (lane + 64 < n16) ((int4 *)dig)[lane + 64] = h1;
-      for (int i = lane + 128; i < n16; i += 64) ((int4 *)dig)[i] = hs[i];
-      if (lane < d.ngi) gp[lane] = g0;
-      for (int i = lane + 64; i < d.ngi; i += 64) gp[i] = d.hgp[(size_t)wave * d.ngi + i];
+    if (wave < d.K) {
+      const float *hj = d.h + (size_t)wave * d.I;
+      v4f hv[4];
+      route_h_load(hj, d.I, hv, lane);
+      e = d.idx[wave];
+      if ((unsigned)e < (unsigned)d.E) {
+        tile_prefetch<FMT, 8>(t, codes + (size_t)e * expert_codes + down_codes_off,
+                              scales + (size_t)e * expert_scales + down_scales_off, rt, d.ngi, 0,
+                              d.ngi < 8 ? d.ngi : 8, lane);
+        route_digits(hj, d.I, d.Ip, hv, dig, gp, lane);
+      }
     }
   } else {
     // ---- shared half: integer sums (cached) first, then the int8 rows ----
+    if (sw == 1) {
+      // the combine's operands, early
+      if (lane < d.K) cw[lane] = d.w[lane];
+      if (lane == 32) cw[kMaxK] = d.misc[1];
+      if (lane >= 48) cds[lane - 48] = ds[rt * kTileRows + lane - 48];
+    }
     const int *accp = d.acc + (size_t)p * 2 * d.Ish;
     const int r0 = kc0 * 64, r1 = kc1 * 64;
     int ag[kShRegs], au[kShRegs];
@@ -790,12 +802,13 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
           tile_prefetch<FMT, 8>(t, ce, se, rt, d.ngi, c0, nn, lane);
           if (c0 == 0) {
             // a later route: its digits -> this wave's LDS (wave-local)
-            const int4 *hs = (const int4 *)(d.hd + (size_t)j * 2 * d.Ip);
-            for (int i = lane; i < (2 * d.Ip) / 16; i += 64) ((int4 *)dig)[i] = hs[i];
-            for (int i = lane; i < d.ngi; i += 64) gp[i] = d.hgp[(size_t)j * d.ngi + i];
-            __builtin_amdgcn_wave_barrier();
+            const float *hj = d.h + (size_t)j * d.I;
+            v4f hv[4];
+            route_h_load(hj, d.I, hv, lane);
+            route_digits(hj, d.I, d.Ip, hv, dig, gp, lane);
           }
         }
+        __builtin_amdgcn_wave_barrier();
         tile_compute<FMT, 8>(t, c0, nn, src, acc, lane);
       }
       digit_fold(acc);
@@ -826,12 +839,11 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
   __syncthreads();
   if (threadIdx.x < kTileRows) {
     // moe_forward's combine: fma over k in route order, then shared * gate
-    const int row = rt * kTileRows + threadIdx.x;
     float out = 0.0f;
-    for (int k = 0; k < d.K; k++) out = __builtin_fmaf(vals[k][threadIdx.x], d.w[k], out);
-    const float shv = (float)(ish[0][threadIdx.x] + ish[1][threadIdx.x]) * ds[row] * shx;
-    out = __builtin_fmaf(shv, d.misc[1], out);
-    y[row] = out;
+    for (int k = 0; k < d.K; k++) out = __builtin_fmaf(vals[k][threadIdx.x], cw[k], out);
+    const float shv = (float)(ish[0][threadIdx.x] + ish[1][threadIdx.x]) * cds[threadIdx.x] * shx;
+    out = __builtin_fmaf(shv, cw[kMaxK], out);
+    y[rt * kTileRows + threadIdx.x] = out;
   }
   // clear the other parity's integer sums for the next call; flip the parity
   int *accz = d.acc + (size_t)(1 - p) * 2 * d.Ish;
@@ -841,7 +853,7 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
   if (blockIdx.x == 0 && threadIdx.x == 0) d.cnt[1] = (unsigned)(1 - p);
   if (blockIdx.x == 0 && (int)threadIdx.x < d.K) {
     if (route_idx) route_idx[threadIdx.x] = d.idx[threadIdx.x];
-    if (route_weight) route_weight[threadIdx.x] = d.w[threadIdx.x];
+    if (route_weight) route_weight[threadIdx.x] = cw[threadIdx.x];
   }
 }
 
@@ -872,9 +884,8 @@ bool decode_plan(const ColiMoeLayer *L, DecLaunch &p) {
   size_t xs_bytes = ((size_t)d.H * 4 + 15) & ~(size_t)15;
   size_t sel = (size_t)(d.E + 1) * 16 + (size_t)d.E * 8;
   p.lds1 = xs_bytes + (sel > (size_t)d.H ? sel : (size_t)d.H);
-  p.g2 = d.K * 2 * (d.I / kTileRows);
-  size_t l2a = 2 * (size_t)d.Hp + (size_t)d.ngh * 16, l2b = (size_t)d.I * 4;
-  p.lds2 = l2a > l2b ? l2a : l2b;
+  p.g2 = d.K * (d.I / kTileRows);
+  p.lds2 = 2 * (size_t)d.Hp + (size_t)d.ngh * 16 + 2 * (size_t)d.ngh * kTileRows * 4;
   size_t wbytes = 2 * (size_t)d.Ip + 16 * (size_t)d.ngi;
   int nwr = d.K < kMaxDownWaves ? d.K : kMaxDownWaves;
   p.g3 = d.H / kTileRows;
@@ -888,8 +899,8 @@ bool decode_plan(const ColiMoeLayer *L, DecLaunch &p) {
 
 namespace sw {
 
-// layout of ColiMoeLayer::sync: cnt[16] | ecnt[32] | acc[2][2*Ish]
-size_t decode_sync_words(const ColiMoeShape &s) { return 16 + kMaxK + 4 * (size_t)s.shared_intermediate; }
+// layout of ColiMoeLayer::sync: cnt[16] | acc[2][2*Ish]
+size_t decode_sync_words(const ColiMoeShape &s) { return 16 + 4 * (size_t)s.shared_intermediate; }
 
 int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight) {
   DecLaunch p;
@@ -899,8 +910,7 @@ int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *r
   if (ensure_scratch(ctx, kScrShared, bytes, "decode workspace allocation")) return -1;
   dec_carve(d, (char *)ctx->scratch[kScrShared]);
   d.cnt = L->sync;
-  d.ecnt = L->sync + 16;
-  d.acc = (int *)(L->sync + 16 + kMaxK);
+  d.acc = (int *)(L->sync + 16);
   hipStream_t st = ctx->stream;
   const bool timing = ctx->moe_timing != 0;
   if (timing) (void)hipEventRecord(ctx->moe_event[0], st);

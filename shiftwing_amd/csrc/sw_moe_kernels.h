@@ -157,6 +157,113 @@ __device__ __forceinline__ void tile_compute(const TilePrefetch<FMT, NMAX> &t, i
     }
 }
 
+// Codes only (the group scales come from LDS): 3 or 4 registers per group.
+template <int FMT, int NMAX>
+struct TileCodes {
+  TileWord<FMT> q[NMAX];
+};
+
+template <int FMT, int NMAX>
+__device__ __forceinline__ void tile_codes_prefetch(TileCodes<FMT, NMAX> &t, const unsigned char *codes, int rt,
+                                                    int ng, int g0, int n, int lane) {
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+#pragma unroll
+  for (int i = 0; i < NMAX; i++)
+    if (i < n) t.q[i] = load_tile<FMT>(codes + (((size_t)rt * ng + g0 + i) * 64 + lane) * BPL);
+}
+
+// tile_compute with the row tile's scales in LDS: sc[g][16 rows].
+template <int FMT, int NMAX>
+__device__ __forceinline__ void tile_compute_lds(const TileCodes<FMT, NMAX> &t, int g0, int n, const DigitSrc &ds,
+                                                 const float *sc, float acc[4], int lane) {
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+  const int kb = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < NMAX; i++)
+    if (i < n) {
+      int g = g0 + i;
+      v4i a0, a1;
+      unpack_tile<FMT>(t.q[i], a0, a1);
+      int off = (g * kGroup + kb * 16) & ds.mask;
+      v4i b0 = *(const v4i *)(ds.d + off);
+      v4i b1 = *(const v4i *)(ds.d + ((off + 64) & ds.mask));
+      float dsc = 0.0f;
+      int Q = 0;
+      if (ds.gp) {
+        float4 p = ds.gp[g];
+        dsc = ds.second ? p.y : p.x;
+        Q = __float_as_int(ds.second ? p.w : p.z);
+      }
+      v4i c = {0, 0, 0, 0};
+      c = mfma_i8(a0, b0, c);
+      c = mfma_i8(a1, b1, c);
+      const v4f s4 = *(const v4f *)(sc + g * kTileRows + 4 * kb);
+      const float scv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf((float)(c[r] - OFF * Q) * dsc, scv[r], acc[r]);
+    }
+}
+
+// Digits of one 1024-wide slice of v (v[base .. base+1024), zero padded)
+// with 8 lanes per 128-group: lane l owns elements base+16l .. base+16l+15.
+// Same arithmetic as quantize_group (amax of the group, A = amax/127,
+// B = A/254, two rounded digits per element, digit sums); d1 / d2 / gp are
+// indexed like quantize_group's and written below `limit` (the padded
+// length, a multiple of 128) only.  vv: the lane's 16 values, loaded ahead.
+__device__ __forceinline__ void quantize_slice8(const v4f vv[4], int base, int limit, signed char *d1,
+                                                signed char *d2, float4 *gp, int lane) {
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    v[4 * q] = vv[q].x;
+    v[4 * q + 1] = vv[q].y;
+    v[4 * q + 2] = vv[q].z;
+    v[4 * q + 3] = vv[q].w;
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+  m = fmaxf(m, __shfl_xor(m, 1, 8));
+  m = fmaxf(m, __shfl_xor(m, 2, 8));
+  m = fmaxf(m, __shfl_xor(m, 4, 8));
+  const float A = m / 127.0f;
+  const float B = A / 254.0f;
+  int q1[16], q2[16];
+  int s1 = 0, s2 = 0;
+  if (m > 0.0f) {
+    const float invA = 127.0f / m, invB = 254.0f / A;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      q1[i] = (int)fminf(fmaxf(__builtin_rintf(v[i] * invA), -127.0f), 127.0f);
+      float r = __builtin_fmaf(-(float)q1[i], A, v[i]);
+      q2[i] = (int)fminf(fmaxf(__builtin_rintf(r * invB), -127.0f), 127.0f);
+      s1 += q1[i];
+      s2 += q2[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) q1[i] = q2[i] = 0;
+  }
+  v4i p1, p2;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    p1[w] = (q1[4 * w] & 255) | (q1[4 * w + 1] & 255) << 8 | (q1[4 * w + 2] & 255) << 16 | (q1[4 * w + 3] & 255) << 24;
+    p2[w] = (q2[4 * w] & 255) | (q2[4 * w + 1] & 255) << 8 | (q2[4 * w + 2] & 255) << 16 | (q2[4 * w + 3] & 255) << 24;
+  }
+  const bool mine = base + 16 * lane < limit;
+  if (mine) {
+    *(v4i *)(d1 + base + 16 * lane) = p1;
+    *(v4i *)(d2 + base + 16 * lane) = p2;
+  }
+  s1 += __shfl_xor(s1, 1, 8);
+  s1 += __shfl_xor(s1, 2, 8);
+  s1 += __shfl_xor(s1, 4, 8);
+  s2 += __shfl_xor(s2, 1, 8);
+  s2 += __shfl_xor(s2, 2, 8);
+  s2 += __shfl_xor(s2, 4, 8);
+  if (mine && (lane & 7) == 0) gp[(base >> 7) + (lane >> 3)] = make_float4(A, B, __int_as_float(s1), __int_as_float(s2));
+}
+
 // Digit 1 (even column) + digit 2 (odd column): valid in lanes with odd
 // column c (token c/2), rows 4*kb+i.
 __device__ __forceinline__ void digit_fold(float acc[4]) {
