@@ -109,6 +109,43 @@ def cpu_baseline(cfg, budget_s: float):
             "lib": os.path.basename(ref.path) if ref is not None else "liboracle.so"}
 
 
+def copy_probe(mib: int):
+    """A plain copy of known size through coli_cuda_copy (HIP's own blit
+    kernel): the reference point that scales the HBM byte counters."""
+    from shiftwing_amd import Backend
+    be = Backend(0)
+    n = mib << 20
+    src, dst = be.alloc(n), be.alloc(n)
+    be.check(be.lib.coli_cuda_memset(be.ctx, src.p, 1, C.c_size_t(n)))
+    reps = 4
+    be.check(be.lib.coli_cuda_copy(be.ctx, dst.p, src.p, C.c_size_t(n)))
+    be.sync()
+    be.check(be.lib.coli_cuda_timer_start(be.ctx))
+    for _ in range(reps):
+        be.check(be.lib.coli_cuda_copy(be.ctx, dst.p, src.p, C.c_size_t(n)))
+    ms = C.c_float()
+    be.check(be.lib.coli_cuda_timer_stop(be.ctx, C.byref(ms)))
+    sec = ms.value / 1e3 / reps
+    print(json.dumps({"copy_bytes": n, "read_bytes": n, "write_bytes": n, "ms": round(sec * 1e3, 4),
+                      "gbs_read_plus_write": round(2 * n / sec / 1e9, 1), "launches": reps + 1}), flush=True)
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/hbm_traffic_<workload>.txt: FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by what the counter reads for a copy of known
+    size).  None when no summary covers the kernel."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 3 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(parts[2])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,11 +155,16 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (testing)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="time a plain device-to-device copy of MIB MiB (the counter calibration kernel) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the multi-GPU sharding is a design only, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     from shiftwing_amd import Backend, MoeLayer
     H, E, K, I, Ish, fmt, layers, seed, desc = WORKLOADS[args.workload]
@@ -212,7 +254,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.workload, KERNELS[dom]),
             "bytes_per_launch": kb[dom],
             "avg_launch_us": round(per_call[dom] * 1e3, 3),
         },
