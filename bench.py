@@ -130,19 +130,20 @@ def copy_probe(mib: int):
                       "gbs_read_plus_write": round(2 * n / sec / 1e9, 1), "launches": reps + 1}), flush=True)
 
 
-def measured_traffic(workload: str, kernel: str):
+def measured_traffic(workload: str, kernel: str, layers_per_launch: int):
     """HBM bytes per launch of `kernel` from the committed counter summary
     (profiles/hbm_traffic_<workload>.txt: FETCH_SIZE and WRITE_SIZE per
     dispatch, each scaled by what the counter reads for a copy of known
-    size).  None when no summary covers the kernel."""
+    size), scaled to this launch's layer count.  None when no summary covers
+    the kernel."""
     path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
             parts = line.split()
-            if len(parts) >= 3 and parts[0] == "traffic" and parts[1] == kernel:
-                return int(parts[2])
+            if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == kernel:
+                return int(round(int(parts[2]) * layers_per_launch / int(parts[3])))
     return None
 
 
@@ -155,6 +156,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (testing)")
+    ap.add_argument("--decode-kernels", type=int, default=1, choices=[1, 2],
+                    help="1: the persistent decode kernel, one launch per stack step (default); "
+                         "2: the three per-layer decode kernels")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="time a plain device-to-device copy of MIB MiB (the counter calibration kernel) and exit")
     args = ap.parse_args()
@@ -171,6 +175,7 @@ def main():
     if args.layers:
         layers = args.layers
     be = Backend(0)
+    be.set_decode_kernels(args.decode_kernels)
     lib = be.lib
     t0 = time.perf_counter()
     stack = []
@@ -205,22 +210,41 @@ def main():
     ms_per_step = total_ms / args.steps
     tok_s = args.steps / (total_ms / 1e3)
 
-    # per-kernel timing pass: HIP events on the context stream around each of
-    # the three decode kernels (the kernels' own stream)
-    be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
-    nst = min(args.steps, 8)
-    for s in range(args.warmup, args.warmup + nst):
-        run(s)
-    be.sync()
-    kms = (C.c_double * 3)()
-    calls = C.c_ulonglong()
-    be.check(lib.coli_cuda_moe_decode_times(be.ctx, kms, C.byref(calls)))
-    be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 0))
-    per_call = [kms[i] / max(calls.value, 1) for i in range(3)]
     kb = kernel_bytes(H, E, K, I, Ish, fmt)
-    dom = max(range(3), key=lambda i: per_call[i])
-    achieved = kb[dom] / (per_call[dom] * 1e-3) / 1e9
     step_bytes = sum(kb)
+    if args.decode_kernels == 1:
+        # one persistent kernel per step: HIP events on the context stream
+        # right before and after single launches give its duration
+        durs = []
+        for s in range(args.warmup, args.warmup + min(args.steps, 16)):
+            be.check(lib.coli_cuda_timer_start(be.ctx))
+            run(s)
+            m1 = C.c_float()
+            be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(m1)))
+            durs.append(m1.value)
+        launch_ms = sum(durs) / len(durs)
+        kname, launch_bytes, layers_per_launch = "k_stack", layers * step_bytes, layers
+        kernel_us = {"k_stack": round(launch_ms * 1e3, 3), "per_layer": round(launch_ms * 1e3 / layers, 3)}
+        kernel_gbs = {"k_stack": round(launch_bytes / (launch_ms * 1e-3) / 1e9, 1)}
+    else:
+        # per-kernel timing pass: HIP events on the context stream around each
+        # of the three decode kernels (the kernels' own stream)
+        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
+        nst = min(args.steps, 8)
+        for s in range(args.warmup, args.warmup + nst):
+            run(s)
+        be.sync()
+        kms = (C.c_double * 3)()
+        calls = C.c_ulonglong()
+        be.check(lib.coli_cuda_moe_decode_times(be.ctx, kms, C.byref(calls)))
+        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 0))
+        per_call = [kms[i] / max(calls.value, 1) for i in range(3)]
+        dom = max(range(3), key=lambda i: per_call[i])
+        kname, launch_bytes, layers_per_launch = KERNELS[dom], kb[dom], 1
+        launch_ms = per_call[dom]
+        kernel_us = {KERNELS[i]: round(per_call[i] * 1e3, 3) for i in range(3)}
+        kernel_gbs = {KERNELS[i]: round(kb[i] / (per_call[i] * 1e-3) / 1e9, 1) for i in range(3)}
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     stats = [L.route_stats_full() for L in stack]
     tokens_routed = sum(t for t, _, _ in stats)
     fallbacks = sum(f for _, f, _ in stats)
@@ -249,21 +273,21 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": KERNELS[dom],
+            "kernel": kname,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.workload, KERNELS[dom]),
-            "bytes_per_launch": kb[dom],
-            "avg_launch_us": round(per_call[dom] * 1e3, 3),
+            "traffic": measured_traffic(args.workload, kname, layers_per_launch),
+            "bytes_per_launch": launch_bytes,
+            "avg_launch_us": round(launch_ms * 1e3, 3),
         },
         "step": {
             "algorithmic_bytes_per_layer": step_bytes,
             "effective_gbs": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9, 1),
             "frac_of_peak": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel_us_per_layer": {KERNELS[i]: round(per_call[i] * 1e3, 3) for i in range(3)},
-            "kernel_gbs": {KERNELS[i]: round(kb[i] / (per_call[i] * 1e-3) / 1e9, 1) for i in range(3)},
+            "kernel_us": kernel_us,
+            "kernel_gbs": kernel_gbs,
             "router_not_certified": f"{fallbacks}/{tokens_routed} token-layers ({full} needed every chain)",
             "weight_generation_s": round(gen_s, 1),
         },

@@ -286,7 +286,10 @@ int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
 
 /* n_layers MoE steps in order on the context stream: layer l reads
  * x + l*x_layer_stride and writes y + l*y_layer_stride (floats).  Strict
- * decode order: layer l+1 starts after layer l's output is written. */
+ * decode order: layer l+1 starts after layer l's output is written.  With
+ * tokens == 1 and layers of one shape this is one persistent kernel that
+ * needs every compute unit of the device for the duration of the call; a
+ * call that cannot get them reports an error at the next coli_cuda_sync. */
 int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers,
                                  int n_layers, float *y, const float *x,
                                  int tokens, size_t x_layer_stride,
@@ -315,9 +318,19 @@ int coli_cuda_moe_stage_times(ColiCuda *ctx, double ms[8],
  * (routed gate/up, shared down), ms[2] routed down + combine. */
 int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3],
                                unsigned long long *calls);
-/* 1 (default): single-token steps take the decode kernels; 0: they take the
- * many-token kernels (same results to the stated tolerance; for tests). */
-int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int enable);
+/* Kernels for single-token steps: 1 (default) the persistent decode kernel
+ * (one launch for a whole coli_cuda_moe_forward_layers stack; shapes it does
+ * not take fall back to 2); 2 the three per-layer decode kernels; 0 the
+ * many-token kernels.  Same results to the stated tolerance (for tests). */
+int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode);
+/* Stage stamps of the persistent decode kernel (measurement): while set,
+ * every call writes the device wall clock (100 MHz) into the caller's device
+ * buffer at [layer][workgroup][8]: layer start, router/shared done, router
+ * barrier passed, selection done, routed gate/up done, hidden barrier passed,
+ * down done, layer barrier passed.  Workgroups = the device's CU count.
+ * trace = NULL, words = 0 switches it off. */
+int coli_cuda_moe_stack_trace(ColiCuda *ctx, unsigned long long *trace,
+                              size_t words);
 
 #ifdef __cplusplus
 }

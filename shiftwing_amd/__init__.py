@@ -95,11 +95,12 @@ class Backend:
     def device_name(self) -> str:
         return self.lib.coli_cuda_device_name(self.ctx).decode()
 
-    def set_decode_kernels(self, enable: bool):
-        """True (default): single-token steps take the three decode kernels;
-        False: they take the many-token kernels."""
-        self.check(self.lib.coli_cuda_moe_set_decode_kernels(self.ctx, 1 if enable else 0),
-                   "coli_cuda_moe_set_decode_kernels")
+    def set_decode_kernels(self, mode):
+        """Kernels for single-token steps: 1 or True (default) the persistent
+        decode kernel, 2 the three per-layer decode kernels, 0 or False the
+        many-token kernels."""
+        m = int(mode) if not isinstance(mode, bool) else (1 if mode else 0)
+        self.check(self.lib.coli_cuda_moe_set_decode_kernels(self.ctx, m), "coli_cuda_moe_set_decode_kernels")
 
     def close(self):
         if self.ctx:

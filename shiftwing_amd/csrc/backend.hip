@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include "sw_backend.h"
+#include "sw_stack.h"
 #include "sw_device.h"
 
 static thread_local char g_error[512];
@@ -130,6 +131,7 @@ extern "C" void coli_cuda_destroy(ColiCuda *ctx) {
   hipStreamSynchronize(ctx->stream);
   for (int i = 0; i < kScrCount; i++)
     if (ctx->scratch[i]) hipFree(ctx->scratch[i]);
+  stack_release(ctx);
   if (ctx->profile_transactions)
     fprintf(stderr,
             "[HIP_MOE_STAGE] transactions=%llu setup_ms=%.3f routed_hidden_ms=%.3f "
@@ -248,6 +250,7 @@ extern "C" int coli_cuda_memset(ColiCuda *ctx, void *dst, int value, size_t byte
 extern "C" int coli_cuda_sync(ColiCuda *ctx) {
   if (!ctx) return fail_arg("coli_cuda_sync: null context");
   hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e == hipSuccess && stack_check_abort(ctx)) return -1;
   if (e == hipSuccess && ctx->profile_pending && ctx->profile_download_marked) {
     for (int i = 0; i < 8; i++) {
       float ms = 0.0f;

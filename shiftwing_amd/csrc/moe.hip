@@ -32,6 +32,7 @@
 #include "sw_device.h"
 #include "sw_synth.h"
 #include "sw_moe_layer.h"
+#include "sw_stack.h"
 
 using namespace sw;
 
@@ -1153,6 +1154,11 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
                                      int *route_idx, float *route_weight) {
   if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
   if (tokens == 1 && !ctx->moe_generic_only) {
+    if (ctx->moe_decode_mode == 0) {
+      ColiMoeLayer *one[1] = {L};
+      int rc = stack_step(ctx, one, 1, y, 0, x, 0, route_idx, route_weight);
+      if (rc <= 0) return rc;  // 1: shape outside the persistent kernel's limits
+    }
     int rc = decode_step(ctx, L, y, x, route_idx, route_weight);
     if (rc <= 0) return rc;  // 1: shape outside the decode kernels' limits
   }
@@ -1206,6 +1212,12 @@ extern "C" int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *
   if (!ctx || !layers || !y || !x || n_layers <= 0)
     return fail_arg("coli_cuda_moe_forward_layers: invalid argument");
   for (int l = 0; l < n_layers; l++)
+    if (!layers[l]) return fail_arg("coli_cuda_moe_forward_layers: null layer %d", l);
+  if (tokens == 1 && !ctx->moe_generic_only && ctx->moe_decode_mode == 0) {
+    int rc = stack_step(ctx, layers, n_layers, y, ys, x, xs, nullptr, nullptr);
+    if (rc <= 0) return rc;
+  }
+  for (int l = 0; l < n_layers; l++)
     if (coli_cuda_moe_forward(ctx, layers[l], y + (size_t)l * ys, x + (size_t)l * xs, tokens, nullptr, nullptr))
       return -1;
   return 0;
@@ -1257,9 +1269,10 @@ extern "C" int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3], unsigned 
   return 0;
 }
 
-extern "C" int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int enable) {
-  if (!ctx || (enable != 0 && enable != 1)) return fail_arg("coli_cuda_moe_set_decode_kernels: invalid argument");
-  ctx->moe_generic_only = enable ? 0 : 1;
+extern "C" int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode) {
+  if (!ctx || mode < 0 || mode > 2) return fail_arg("coli_cuda_moe_set_decode_kernels: invalid argument");
+  ctx->moe_generic_only = mode == 0 ? 1 : 0;
+  ctx->moe_decode_mode = mode == 2 ? 1 : 0;
   return 0;
 }
 

@@ -24,6 +24,7 @@ enum Scratch {
   kScrRouter,      // router logit bounds (fast path)
   kScrRoutes,      // idx / weights / buckets (fast path)
   kScrShared,      // shared expert int32 partials + h (fast path)
+  kScrStack,       // persistent decode: router records, exact logits, h records
   kScrCount
 };
 
@@ -53,6 +54,21 @@ struct ColiCuda {
   double moe_dec_ms[3];
   unsigned long long moe_dec_calls;
   int moe_generic_only;  // single-token steps take the many-token kernels
+  int moe_decode_mode;   // 0 persistent stack kernel (default), 1 three-kernel decode
+  // persistent stack kernel (moe_stack.hip): counters / integer sums in two
+  // parity sets, the device layer table, the abort status
+  void *stack_sync;
+  int stack_cap_layers;
+  int stack_dirty[2], stack_dirty_acc[2];
+  unsigned long long stack_epoch;
+  void *stack_table_dev;
+  size_t stack_table_cap;
+  void *stack_table_host;
+  int stack_table_n;
+  void *stack_abort;
+  unsigned *stack_abort_host, *stack_abort_host_dev;
+  unsigned long long *stack_trace;  // optional stage stamps (coli_cuda_moe_stack_trace)
+  size_t stack_trace_words;
 };
 
 namespace sw {

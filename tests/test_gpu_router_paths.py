@@ -86,6 +86,32 @@ def test_decode_kernels_agree_with_many_token_kernels(be, oracle):
         L.close()
 
 
+@pytest.mark.parametrize("shape", [(2048, 256, 8, 512, 512, 3), (4096, 512, 10, 1024, 1024, 3),
+                                   (512, 32, 4, 256, 128, 4)])
+def test_persistent_agrees_with_three_kernel_decode(be, oracle, shape):
+    """The persistent decode kernel and the three per-layer decode kernels:
+    same indices, weights within 1e-5, outputs within the tolerance of each
+    other (they quantise the routed hidden vector per 16 and per 128 values)."""
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish, fmt = shape
+    L = MoeLayer(be, H, E, K, I, Ish, fmt)
+    L.synthesize(91, 2)
+    try:
+        for t in range(6):
+            print(f"[persistent vs three-kernel] H{H} token {t}", flush=True)
+            x = oracle.synth_x(91, 2, t, H)
+            be.set_decode_kernels(1)
+            y1, i1, w1 = L.forward_host(x)
+            be.set_decode_kernels(2)
+            y2, i2, w2 = L.forward_host(x)
+            assert np.array_equal(i1, i2), t
+            assert np.max(np.abs(w1 - w2)) <= 1e-5
+            assert_close_rms(y1[0], y2[0], 1e-3, f"persistent vs three-kernel t={t}")
+    finally:
+        be.set_decode_kernels(1)
+        L.close()
+
+
 def test_stack_forward_equals_per_layer_calls(be):
     """coli_cuda_moe_forward_layers over a stack == one forward per layer."""
     import ctypes as C
