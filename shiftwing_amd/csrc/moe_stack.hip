@@ -36,6 +36,7 @@
 // workgroup leaves, and the host reports the error at the next sync.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stdint.h>
 #include <string.h>
 
 #include "sw_backend.h"
@@ -53,7 +54,6 @@ constexpr int kW = kT / 64;      // waves per workgroup
 constexpr int kMaxK = kStackMaxK;
 constexpr int kRSlots = 3;       // router rows per workgroup held in registers
 constexpr int kNch = 2;          // 2048-float chunks per router row (H <= 4096)
-constexpr int kSPF = 4;          // shared gate/up k-chunks per lane held in registers
 constexpr int kMaxAmbig = 64;    // experts the targeted exact selection can take
 constexpr int kLine = 32;        // words between counters (one 128-byte line)
 constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h, y
@@ -90,7 +90,7 @@ struct StackArgs {
   int n;
   int H, E, K, I, Ish, fmt, ngh, ngi, Hp, nrt_i, nch;
   size_t expert_codes, expert_scales, gate_codes, gate_scales;
-  int NB, rslots, KQ, n_sh_tasks;
+  int NB, rslots, KQ, n_sh_tasks, shkc;
   const float *x;
   size_t xs;
   float *y;
@@ -153,6 +153,36 @@ __device__ __forceinline__ void published(unsigned dep) {
   asm volatile("" ::"v"(dep));
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for
+// every outstanding global load of the wave (vmcnt(0)), which would drain the
+// weight tiles kept in flight across the barrier; global ordering is made
+// explicit where it is needed (published(), the DMA waits).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Global -> LDS copies (gfx950 global_load_lds): lane i's bytes land at the
+// wave-uniform LDS address base + i * size.  Issued as inline assembly so that
+// the compiler does not drain them at the next barrier; their completion is
+// waited for explicitly (s_waitcnt vmcnt) before the LDS is read.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_b128(const void *gptr, unsigned base) {
+  base = __builtin_amdgcn_readfirstlane(base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32(const void *gptr, unsigned base) {
+  base = __builtin_amdgcn_readfirstlane(base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Field by field, so that the kernel-argument copy and the table copy are
 // never merged into one flat pointer.
@@ -289,12 +319,9 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   return d;
 }
 
-// Per-workgroup registers carried between stages.
-struct RouterRegs {
-  v4f w[kRSlots * kNch];  // router rows: slot s, chunk c -> floats 2048c + 4t
-};
-typedef RowPrefetch<kSPF> SharedRegs;
-
+// ---------------------------------------------------------------------------
+// Stage R
+// ---------------------------------------------------------------------------
 // The shared gate/up task of this workgroup: matrix m, row tile rt, k-chunks [kc0, kc1)
 struct ShTask {
   int valid, m, rt, kc0, kc1;
@@ -320,46 +347,103 @@ __device__ __forceinline__ void sh_wave_range(const ShTask &t, int wave, int &k0
   k1 = t.kc0 + (wave + 1) * n / kW;
 }
 
-// Loads that do not depend on the token: router rows and the shared task.
-// Every register is written (zero where there is nothing to load), so no
-// stale value stays live across the stages in between.
-__device__ __forceinline__ void prefetch_static(const StackArgs &a, const LayerPtrs &L, RouterRegs &rr,
-                                                SharedRegs &sr) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-#pragma unroll
-  for (int s = 0; s < kRSlots; s++) {
-    const int r = blockIdx.x + s * a.NB;
-    const bool rv = s < a.rslots && r <= a.E;
-    const float *row = r < a.E ? L.router + (size_t)r * a.H : L.sgate;
-#pragma unroll
-    for (int c = 0; c < kNch; c++) {
-      const int e0 = 2048 * c + 4 * t;
-      v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (rv && c < a.nch && e0 < a.H) v = __builtin_nontemporal_load((const v4f *)(row + e0));
-      rr.w[s * kNch + c] = v;
-    }
-  }
-  const ShTask st = sh_task(a);
-  int k0 = 0, k1 = 0;
-  if (st.valid) sh_wave_range(st, wave, k0, k1);
-  const signed char *arow = (st.m == 0 ? L.gq : L.uq) + (size_t)(st.rt * kTileRows + (lane & 15)) * a.H + (lane >> 4) * 16;
-#pragma unroll
-  for (int i = 0; i < kSPF; i++) {
-    v4i v = {0, 0, 0, 0};
-    if (st.valid && k0 + i < k1) v = __builtin_nontemporal_load((const v4i *)(arow + (size_t)(k0 + i) * 64));
-    sr.a[i] = v;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Stage R
-// ---------------------------------------------------------------------------
 struct RStageLds {
   double segT[kRSlots][kNch * 8];
   double Ap[kRSlots][kW], Pp[kRSlots][kW];
   float red[kW];
   int acc_i[kW][16];
 };
+
+// Stage R's inputs in the stage-local LDS union: this workgroup's router rows
+// [rslots][H] f32 and its shared gate/up tile [16 rows][k-chunks * 64] int8
+// (rows padded by 16 bytes against bank conflicts).  They do not depend on
+// the token, so they are copied in while the previous layer finishes.
+struct RLayout {
+  size_t rbuf, sbuf, srow, end;
+};
+__host__ __device__ inline RLayout r_layout(int rslots, int H, int shkc) {
+  RLayout r;
+  size_t o = (sizeof(RStageLds) + 255) & ~(size_t)255;
+  r.rbuf = o;
+  o += (size_t)rslots * H * 4;
+  r.srow = (size_t)shkc * 64 + 16;
+  r.sbuf = o;
+  o += (size_t)kTileRows * r.srow;
+  r.end = o;
+  return r;
+}
+
+// Stage R's inputs of the next layer travel in registers of waves 1..7
+// (wave 0 keeps no loads outstanding: it polls the grid barriers).  They are
+// loaded while the current layer waits on its router barrier and selection
+// (HBM is otherwise idle then) and written to LDS when the next layer starts.
+// Thread T = t - 64 carries the 16-byte chunks T + 448 i of the byte stream
+// [router rows of this workgroup | shared tile in 1 KB blocks: k-chunk kc,
+// then 16 rows of 64 bytes].  Every offset is found with compares, shifts and
+// masks: integer division by a runtime value costs tens of instructions.
+constexpr int kStRegs = 12;
+constexpr int kStThreads = kT - 64;
+struct StaticRegs {
+  v4u v[kStRegs];
+};
+struct StaticMap {
+  unsigned rowb, rbytes;  // bytes per router row, all router rows (at most kRSlots)
+  unsigned total;         // whole stream
+};
+__device__ __forceinline__ StaticMap static_map(const StackArgs &a) {
+  StaticMap m;
+  int nrows = 0;
+  for (int s2 = 0; s2 < a.rslots; s2++)
+    if ((int)blockIdx.x + s2 * a.NB <= a.E) nrows = s2 + 1;
+  m.rowb = (unsigned)a.H * 4u;
+  m.rbytes = (unsigned)nrows * m.rowb;
+  const ShTask st = sh_task(a);
+  m.total = m.rbytes + (st.valid ? (unsigned)(st.kc1 - st.kc0) * 1024u : 0u);
+  return m;
+}
+__device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs &L, StaticRegs &sr, int t) {
+  if (t < 64) return;
+  const StaticMap m = static_map(a);
+  const ShTask st = sh_task(a);
+  const unsigned char *sbase =
+      (const unsigned char *)((st.m == 0 ? L.gq : L.uq) + (size_t)st.rt * kTileRows * a.H + st.kc0 * 64);
+  const unsigned char *rows[kRSlots];
+#pragma unroll
+  for (int s2 = 0; s2 < kRSlots; s2++) {
+    const int r = blockIdx.x + s2 * a.NB;
+    rows[s2] = (const unsigned char *)(r < a.E ? L.router + (size_t)r * a.H : L.sgate);
+  }
+#pragma unroll
+  for (int i = 0; i < kStRegs; i++) {
+    const unsigned o = 16u * (unsigned)((t - 64) + kStThreads * i);
+    v4u v = {0u, 0u, 0u, 0u};
+    if (o < m.rbytes) {
+      const int s2 = (o >= m.rowb) + (o >= 2 * m.rowb);
+      const unsigned char *row = s2 == 0 ? rows[0] : (s2 == 1 ? rows[1] : rows[2]);
+      v = __builtin_nontemporal_load((const v4u *)(row + (o - (unsigned)s2 * m.rowb)));
+    } else if (o < m.total) {
+      const unsigned o2 = o - m.rbytes;
+      v = __builtin_nontemporal_load(
+          (const v4u *)(sbase + (size_t)((o2 >> 6) & 15) * a.H + (o2 >> 10) * 64 + (o2 & 63)));
+    }
+    sr.v[i] = v;
+  }
+}
+__device__ __forceinline__ void static_store(const StackArgs &a, const StaticRegs &sr, unsigned char *u, int t) {
+  if (t < 64) return;
+  const StaticMap m = static_map(a);
+  const RLayout rl = r_layout(a.rslots, a.H, a.shkc);
+#pragma unroll
+  for (int i = 0; i < kStRegs; i++) {
+    const unsigned o = 16u * (unsigned)((t - 64) + kStThreads * i);
+    if (o < m.rbytes) {
+      *(v4u *)(u + rl.rbuf + o) = sr.v[i];
+    } else if (o < m.total) {
+      const unsigned o2 = o - m.rbytes;
+      *(v4u *)(u + rl.sbuf + ((o2 >> 6) & 15) * (unsigned)rl.srow + (o2 >> 10) * 64 + (o2 & 63)) = sr.v[i];
+    }
+  }
+}
 
 // The exact fp32 chain of the reference's dot() for the listed slots (rows
 // b + s*NB): products rn(x*w) written to LDS by every thread, then one lane per
@@ -384,7 +468,7 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
         *(v4f *)(prod + (size_t)s * a.H + e0) = p;
       }
     }
-  __syncthreads();
+  lds_barrier();
   if (lane == 0 && wave < kRSlots && (want & (1u << wave))) {
     const float *p = prod + (size_t)wave * a.H;
     float acc = 0.0f;
@@ -399,13 +483,115 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
     }
     out[wave] = acc;
   }
-  __syncthreads();
+  lds_barrier();
+}
+
+// The x operands of one wave's groups, kept in registers for the whole G
+// stage (the wave always takes the same groups): the MFMA B operands of both
+// steps (column c = lane%16: digit c of token 0 for c < 2, zero otherwise)
+// and the group's digit scale and offset correction.
+constexpr int kGMax = 8;   // groups per wave and unit
+constexpr int kGRing = 6;  // stage G ring slots per wave
+struct XOps {
+  v4i b0[kGMax], b1[kGMax];
+  float dsc[kGMax], zq[kGMax];
+};
+template <int FMT>
+__device__ __forceinline__ void xops_load(XOps &xo, const DigitSrc &ds, int g0, int n, int lane) {
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+  const int kb = lane >> 4;
+#pragma unroll
+  for (int gi = 0; gi < kGMax; gi++) {
+    xo.b0[gi] = xo.b1[gi] = v4i{0, 0, 0, 0};
+    xo.dsc[gi] = xo.zq[gi] = 0.0f;
+    if (gi < n) {
+      const int g = g0 + gi;
+      const int off = (g * kGroup + kb * 16) & ds.mask;
+      xo.b0[gi] = *(const v4i *)(ds.d + off);
+      xo.b1[gi] = *(const v4i *)(ds.d + ((off + 64) & ds.mask));
+      if (ds.gp) {
+        const float4 p = ds.gp[g];
+        const float d = ds.second ? p.y : p.x;
+        const int Q = __float_as_int(ds.second ? p.w : p.z);
+        xo.dsc[gi] = d;
+        xo.zq[gi] = (float)(OFF * Q) * d;  // exact integer, one rounding
+      }
+    }
+  }
+}
+
+// One tile-group from a ring slot (codes, then the 16 row scales).
+template <int FMT>
+__device__ __forceinline__ void g_item(const unsigned char *slot, const v4i &b0, const v4i &b1, float dsc, float zq,
+                                       float acc[4], int lane) {
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+  TileWord<FMT> tw;
+  const unsigned char *cp = slot + lane * BPL;
+  if constexpr (FMT == 4) {
+    const v4u v = *(const v4u *)cp;
+    tw.w[0] = v.x;
+    tw.w[1] = v.y;
+    tw.w[2] = v.z;
+    tw.w[3] = v.w;
+  } else {
+    tw.w[0] = ((const unsigned *)cp)[0];
+    tw.w[1] = ((const unsigned *)cp)[1];
+    tw.w[2] = ((const unsigned *)cp)[2];
+  }
+  const v4f s4 = *(const v4f *)(slot + 64 * BPL + 16 * (lane >> 4));
+  v4i a0, a1;
+  unpack_tile<FMT>(tw, a0, a1);
+  v4i c = {0, 0, 0, 0};
+  c = mfma_i8(a0, b0, c);
+  c = mfma_i8(a1, b1, c);
+  const float scv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(__builtin_fmaf((float)c[r], dsc, -zq), scv[r], acc[r]);
+}
+
+// 16-lane row reductions by DPP (quad xor 1, quad xor 2, half-row mirror,
+// row mirror): every lane of the row ends with the row's result
+__device__ __forceinline__ float row16_max(float v) {
+  const float ninf = -__builtin_huge_valf();
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0xB1, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x4E, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x141, 0xF, true));
+  v = fmaxf(v, SW_DPP_F(ninf, v, 0x140, 0xF, true));
+  return v;
+}
+__device__ __forceinline__ int row16_sum_i(int v) {
+  v += SW_DPP_I(0, v, 0xB1, 0xF, true);
+  v += SW_DPP_I(0, v, 0x4E, 0xF, true);
+  v += SW_DPP_I(0, v, 0x141, 0xF, true);
+  v += SW_DPP_I(0, v, 0x140, 0xF, true);
+  return v;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (the immediate is encoded per case)
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+#define SW_VM(k) \
+  case k:        \
+    asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); \
+    break;
+    SW_VM(1) SW_VM(2) SW_VM(3) SW_VM(4) SW_VM(5) SW_VM(6) SW_VM(7) SW_VM(8) SW_VM(9) SW_VM(10) SW_VM(11)
+    SW_VM(12) SW_VM(13) SW_VM(14) SW_VM(15) SW_VM(16) SW_VM(17)
+#undef SW_VM
+    default:
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Stage S: selection from the published records (all workgroups identically).
 // ---------------------------------------------------------------------------
+constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
+constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
+constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
+  unsigned long long wcand[kSelRec * kW * (kMaxK + 1)];  // each wave's top K+1 keys per record round
+  unsigned long long wup[kW];                           // each wave's largest upper bound outside them
+  double theta, mxd;
   int cand[kMaxK + 1];
   int state;      // 0 certified, 1 targeted exact, 2 full exact
   int nm;
@@ -426,13 +612,13 @@ struct Routes {  // result of stage S, in static LDS
 };
 
 __device__ bool sync_barrier(const StackArgs &a, int l, int which, Routes &rt) {
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) {
     unsigned *bar = bar_of(a, l, which);
     bar_arrive(bar, a.NB);
     rt.flag = bar_wait(bar, a) ? 1 : 0;
   }
-  __syncthreads();
+  lds_barrier();
   return rt.flag != 0;
 }
 
@@ -463,9 +649,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     }
   }
 
-  RouterRegs rr;
-  SharedRegs sr;
-  prefetch_static(a0, layer_ref(a0, 0), rr, sr);
+  StaticRegs sreg;
+  static_load(a0, layer_ref(a0, 0), sreg, threadIdx.x);
 
   for (int l = 0; l < a0.n; l++) {
     // Lane indices are re-derived every layer: values hoisted out of the loop
@@ -473,7 +658,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     const StackArgs &a = a0;
     int t = (int)threadIdx.x;
     asm volatile("" : "+v"(t));
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const LayerPtrs L = layer_ref(a, l);
     const float *x = a.x + (size_t)l * a.xs;
     int *acc = a.acc + (size_t)(l * 2 + a.parity) * a.acc_stride;
@@ -487,8 +672,41 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int e0 = 2048 * c + 4 * t;
       xv[c] = (c < a.nch && e0 < a.H) ? *(const v4f *)(x + e0) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    // routed activation digits, one 128-group per wave
-    for (int g = wave; g < a.ngh; g += kW) quantize_group(x, a.H, g, S.xd, S.xd + a.Hp, S.xgp, lane);
+    // routed activation digits from the registers: a 128-group is 32 lanes x
+    // 4 values (quantize_group's arithmetic: A = amax/127, B = A/254, two
+    // rounded digits per element, digit sums)
+#pragma unroll
+    for (int c = 0; c < kNch; c++) {
+      const int e0 = 2048 * c + 4 * t;
+      if (c < a.nch) {
+        const float v[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+        float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        m = row16_max(m);
+        m = fmaxf(m, __shfl_xor(m, 16, 32));
+        const float A = m / 127.0f, B = A / 254.0f;
+        int q1[4] = {0, 0, 0, 0}, q2[4] = {0, 0, 0, 0};
+        if (m > 0.0f) {
+          const float invA = 127.0f / m, invB = 254.0f / A;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            q1[i] = (int)fminf(fmaxf(__builtin_rintf(v[i] * invA), -127.0f), 127.0f);
+            const float r = __builtin_fmaf(-(float)q1[i], A, v[i]);
+            q2[i] = (int)fminf(fmaxf(__builtin_rintf(r * invB), -127.0f), 127.0f);
+          }
+        }
+        int s1 = q1[0] + q1[1] + q1[2] + q1[3], s2 = q2[0] + q2[1] + q2[2] + q2[3];
+        s1 = row16_sum_i(s1);
+        s2 = row16_sum_i(s2);
+        s1 += __shfl_xor(s1, 16, 32);
+        s2 += __shfl_xor(s2, 16, 32);
+        if (e0 < a.Hp) {
+          *(int *)(S.xd + e0) = (q1[0] & 255) | (q1[1] & 255) << 8 | (q1[2] & 255) << 16 | (q1[3] & 255) << 24;
+          *(int *)(S.xd + a.Hp + e0) =
+              (q2[0] & 255) | (q2[1] & 255) << 8 | (q2[2] & 255) << 16 | (q2[3] & 255) << 24;
+          if ((t & 31) == 0) S.xgp[e0 >> 7] = make_float4(A, B, __int_as_float(s1), __int_as_float(s2));
+        }
+      }
+    }
     // qrow_i8 of x (c/qwen.c:1696): amax, sx = amax/127 (floor 1e-12), q = rint(x/sx)
     {
       float m = 0.0f;
@@ -498,6 +716,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       m = wave_max_dpp(m);
       if (lane == 0) R.red[wave] = m;
     }
+    // this layer's router rows and shared tile: registers -> LDS
+    static_store(a, sreg, S.u, t);
+    lds_barrier();
+    const RLayout rl = r_layout(a.rslots, a.H, a.shkc);
+    const float *rbuf = (const float *)(S.u + rl.rbuf);
     // router pass 1: segment totals and |products|
     double Aacc[kRSlots];
 #pragma unroll
@@ -511,7 +734,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             const int e0 = 2048 * c + 4 * t;
             double p0 = 0, p1 = 0, p2 = 0, p3 = 0;
             if (e0 < a.H) {
-              const v4f w = rr.w[s * kNch + c];
+              const v4f w = *(const v4f *)(rbuf + (size_t)s * a.H + e0);
               p0 = (double)xv[c].x * (double)w.x;
               p1 = (double)xv[c].y * (double)w.y;
               p2 = (double)xv[c].z * (double)w.z;
@@ -524,7 +747,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     float sx;
     {
       float amax = 0.0f;
@@ -554,11 +777,20 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int c = 0; c < kNch; c++) {
           if (c < a.nch) {
             const int e0 = 2048 * c + 4 * t;
+            // exact prefix of the segments before this wave's: a scan of the
+            // segment totals held one per lane
+            const double segv = lane < a.nch * 8 ? R.segT[s][lane] : 0.0;
+            const double segi = wave_inclusive_scan_d(segv);
+            const int sg = c * 8 + wave;
             double carry = 0.0;
-            for (int k = 0; k < c * 8 + wave; k++) carry += R.segT[s][k];
+            if (sg > 0) {
+              const int lo_ = __builtin_amdgcn_readlane((int)__double2loint(segi), sg - 1);
+              const int hi_ = __builtin_amdgcn_readlane((int)__double2hiint(segi), sg - 1);
+              carry = __hiloint2double(hi_, lo_);
+            }
             double p0 = 0, p1 = 0, p2 = 0, p3 = 0;
             if (e0 < a.H) {
-              const v4f w = rr.w[s * kNch + c];
+              const v4f w = *(const v4f *)(rbuf + (size_t)s * a.H + e0);
               p0 = (double)xv[c].x * (double)w.x;
               p1 = (double)xv[c].y * (double)w.y;
               p2 = (double)xv[c].z * (double)w.z;
@@ -580,24 +812,23 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     }
     // shared gate/up task: exact int32 dots of 16 rows with xq
     const ShTask st = sh_task(a);
-    __syncthreads();  // xq, segT, Ap/Pp complete
+    lds_barrier();  // xq, segT, Ap/Pp complete
     v4i cs = {0, 0, 0, 0};
     if (st.valid) {
       int k0, k1;
       sh_wave_range(st, wave, k0, k1);
-      const bool bvalid = (lane & 15) == 0;
-      const int ke = k0 + kSPF < k1 ? k0 + kSPF : k1;
-      rows_compute<kSPF>(sr, k0, ke, S.xq, 0, bvalid, cs, lane);
-      for (int kc = ke; kc < k1; kc += kSPF) {
-        const int e1 = kc + kSPF < k1 ? kc + kSPF : k1;
-        idot_tile<kSPF>(st.m == 0 ? L.gq : L.uq, a.H, st.rt * kTileRows, kc, e1, S.xq, 0, bvalid, cs, lane);
+      const signed char *arow = (const signed char *)(S.u + rl.sbuf) + (lane & 15) * rl.srow + (lane >> 4) * 16;
+      for (int kc = k0; kc < k1; kc++) {
+        const v4i av = *(const v4i *)(arow + (kc - st.kc0) * 64);
+        const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
+        cs = mfma_i8(av, bv, cs);
       }
       if ((lane & 15) == 0) {
 #pragma unroll
         for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       unsigned dep = 0;
       // router records of this workgroup's rows: lanes 2s (logit), 2s+1 (bound)
@@ -626,7 +857,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       published(dep);
     }
     stamp(a, l, 1);
-    if (!sync_barrier(a, l, kBarLb, rt)) return;
+    lds_barrier();
+    if (t == 0) bar_arrive(bar_of(a, l, kBarLb), a.NB);
+    if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarLb), a) ? 1 : 0;
+    lds_barrier();
+    if (!rt.flag) return;
     stamp(a, l, 2);
 
     // ======================= stage S =======================
@@ -636,31 +871,106 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       unsigned long long *lk = (unsigned long long *)(lb + a.E + 1);
       float *prod = (float *)((unsigned char *)lk + (((size_t)a.E * 8 + 15) & ~(size_t)15));  // [kRSlots][H]
       const int E = a.E, K = a.K;
-      for (int e = t; e <= E; e += kT) {
-        const double2 v = make_double2(ld_agent(&a.rec[2 * e]), ld_agent(&a.rec[2 * e + 1]));
-        lb[e] = v;
-        if (e < E) lk[e] = ((unsigned long long)float_key((float)v.x) << 32) | (unsigned)(~e);
+      // records -> LDS, and this thread's keys (experts t + i*kT) in registers;
+      // every load is issued before the first is used
+      double lx[kSelRec], ly[kSelRec];
+#pragma unroll
+      for (int i = 0; i < kSelRec; i++) {
+        const int e = t + i * kT;
+        lx[i] = ly[i] = 0.0;
+        if (e <= E) {
+          lx[i] = ld_agent(&a.rec[2 * e]);
+          ly[i] = ld_agent(&a.rec[2 * e + 1]);
+        }
+      }
+      unsigned long long key[kSelRec];
+#pragma unroll
+      for (int i = 0; i < kSelRec; i++) {
+        const int e = t + i * kT;
+        if (e <= E) lb[e] = make_double2(lx[i], ly[i]);
+        key[i] = e < E ? ((unsigned long long)float_key((float)lx[i]) << 32) | (unsigned)(~e) : 0ull;
       }
       if (t == 0) sel.nm = 0;
-      __syncthreads();
-      if (wave == 0) {
-        const int nc = K + 1 < E ? K + 1 : E;
-        for (int r = 0; r < nc; r++) {
-          unsigned long long best = 0;
-          for (int e = lane; e < E; e += 64) best = lk[e] > best ? lk[e] : best;
-          best = wave_max_u64(best);
-          const int e = (int)(~(unsigned)best);
-          if ((e & 63) == lane) lk[e] = 0;
-          if (lane == 0) sel.cand[r] = e;
+      // Each wave ranks its 64 experts of each record round among themselves
+      // (keys: fp64 logit as a float key, lowest index first on equal keys;
+      // near-ties fail the separation tests) by rotating the keys around the
+      // wave; its top K+1 go to LDS in rank order.
+      const int nc = K + 1 < E ? K + 1 : E;
+      {
+        int rank[kSelRec];
+#pragma unroll
+        for (int i = 0; i < kSelRec; i++) rank[i] = 0;
+        // rank within the wave's 64 lanes, per record round i
+#pragma unroll
+        for (int i = 0; i < kSelRec; i++) {
+          if (t + i * kT - lane >= E) continue;  // wave-uniform: no key in this round
+          unsigned lo = (unsigned)key[i], hi = (unsigned)(key[i] >> 32);
+          int rk = 0;
+          for (int sh = 1; sh < 64; sh++) {
+            // DPP wave_ror:1 -- lane l receives lane l-1 (wrapping)
+            lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)lo, 0x13C, 0xF, 0xF, false);
+            hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)hi, 0x13C, 0xF, 0xF, false);
+            const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+            rk += o > key[i];
+          }
+          rank[i] = rk;
+        }
+        // candidates of this wave: rounds merged by rank (rounds are ranked
+        // separately, so a wave's list holds up to kSelRec * (K+1) keys)
+#pragma unroll
+        for (int i = 0; i < kSelRec; i++)
+          if (key[i] && rank[i] < nc) sel.wcand[(i * kW + wave) * (kMaxK + 1) + rank[i]] = key[i];
+        // the largest upper bound among this wave's experts outside those lists
+        unsigned long long up = 0;
+#pragma unroll
+        for (int i = 0; i < kSelRec; i++)
+          if (key[i] && rank[i] >= nc) {
+            const unsigned long long k2 = double_key(lx[i] + ly[i]);
+            up = k2 > up ? k2 : up;
+          }
+        up = wave_max_u64(up);
+        if (lane == 0) sel.wup[wave] = up;
+        // lists shorter than nc (rounds with few experts) end with zero keys
+        for (int i = 0; i < kSelRec; i++) {
+          const int nkeys = E - (i * kT + wave * 64);  // keys of this wave in round i
+          if (nkeys > 0 && nkeys < nc && lane >= nkeys && lane < nc)
+            sel.wcand[(i * kW + wave) * (kMaxK + 1) + lane] = 0ull;
+          if (nkeys <= 0 && lane < nc) sel.wcand[(i * kW + wave) * (kMaxK + 1) + lane] = 0ull;
+        }
+      }
+      lds_barrier();
+      if (wave != 0) {
+        // waves 1..7: the next layer's stage R inputs, loaded while wave 0
+        // merges (the memory system is otherwise idle here)
+        if (l + 1 < a.n) static_load(a, layer_ref(a, l + 1), sreg, t);
+      } else {
+        // merge: K rounds of a tournament over the lists' heads (each list is
+        // in rank order; keys are unique, so one lane holds each round's max)
+        const int nlists = ((E + kT - 1) / kT) * kW;
+        int ptr = 0;
+        unsigned long long head = lane < nlists ? sel.wcand[lane * (kMaxK + 1)] : 0ull;
+        unsigned long long kth_key = 0;
+        for (int r = 0; r < K; r++) {
+          const unsigned long long m = wave_max_u64(head);
+          if (lane == 0) sel.cand[r] = (int)(~(unsigned)m);
+          if (head == m) {
+            ptr++;
+            head = ptr < nc ? sel.wcand[lane * (kMaxK + 1) + ptr] : 0ull;
+          }
+          kth_key = m;
         }
         __builtin_amdgcn_wave_barrier();
-        const int candK = K < E ? sel.cand[K] : -1;
-        unsigned long long upk = 0;
-        for (int e = lane; e < E; e += 64)
-          if (lk[e] != 0 || e == candK) {
-            const unsigned long long k2 = double_key(lb[e].x + lb[e].y);
+        // the largest upper bound outside the top K: the waves' leftovers, the
+        // listed keys below the K-th
+        unsigned long long upk = lane < kW ? sel.wup[lane] : 0ull;
+        for (int g = lane; g < nlists * (kMaxK + 1); g += 64) {
+          const unsigned long long k1 = (g % (kMaxK + 1)) < nc ? sel.wcand[g] : 0ull;
+          if (k1 && k1 < kth_key) {
+            const double2 v = lb[(int)(~(unsigned)k1)];
+            const unsigned long long k2 = double_key(v.x + v.y);
             upk = k2 > upk ? k2 : upk;
           }
+        }
         upk = wave_max_u64(upk);
         const double mx = lb[sel.cand[0]].x;
         const double2 kth = lb[sel.cand[K - 1]];
@@ -675,7 +985,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           ok = (kth.x - kth.y) - up > order_margin(kth.x, up, mx);
         }
         if (ok) ok = (kth.x - kth.y) - (mx + lb[sel.cand[0]].y) > -75.0;
-        int state = 0;
         if (ok) {
           const double ev = lane < K ? exp(lb[sel.cand[lane < K ? lane : 0]].x - mx) : 0.0;
           const double den = wave_sum_dpp(ev);
@@ -683,31 +992,38 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             rt.idx[lane] = sel.cand[lane];
             rt.w[lane] = (float)(ev / den);
           }
-        } else if (L.mode != 0) {
-          state = 2;
-        } else {
-          double theta = 1e300;
-          for (int r = 0; r < K; r++) theta = fmin(theta, lb[sel.cand[r]].x - lb[sel.cand[r]].y);
-          for (int e = lane; e < E; e += 64) {
-            const double2 v = lb[e];
-            if (v.x + v.y >= theta - order_margin(v.x, theta, mx)) {
-              const int slot = atomicAdd(&sel.nm, 1);
-              if (slot < kMaxAmbig) sel.m[slot] = e;
-            }
-          }
-          __builtin_amdgcn_wave_barrier();
-          state = sel.nm <= kMaxAmbig && sel.nm >= K ? 1 : 2;
         }
         if (lane == 0) {
-          sel.state = state;
+          double theta = 1e300;
+          for (int r = 0; r < K; r++) theta = fmin(theta, lb[sel.cand[r]].x - lb[sel.cand[r]].y);
+          sel.theta = theta;
+          sel.mxd = mx;
+          sel.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
           rt.sg = sigmoid_ref((float)lb[E].x);
-          if (b == 0) {
-            atomicAdd(&L.stats[0], 1ull);
-            if (state != 0) atomicAdd(&L.stats[1], 1ull);
-          }
         }
       }
-      __syncthreads();
+      lds_barrier();
+      if (sel.state == 1) {
+        // Every expert whose upper bound reaches the lowest lower bound among
+        // the K candidates (less a margin): the exact top K lies in this set,
+        // since anything outside it is strictly below all K candidates.
+        const double theta = sel.theta, mx = sel.mxd;
+#pragma unroll
+        for (int i = 0; i < kSelRec; i++) {
+          const int e = t + i * kT;
+          if (e < E && lx[i] + ly[i] >= theta - order_margin(lx[i], theta, mx)) {
+            const int slot = atomicAdd(&sel.nm, 1);
+            if (slot < kMaxAmbig) sel.m[slot] = e;
+          }
+        }
+        lds_barrier();
+        if (t == 0 && !(sel.nm <= kMaxAmbig && sel.nm >= K)) sel.state = 2;
+        lds_barrier();
+      }
+      if (b == 0 && t == 0) {
+        atomicAdd(&L.stats[0], 1ull);
+        if (sel.state != 0) atomicAdd(&L.stats[1], 1ull);
+      }
       if (sel.state == 1) {
         // exact chains of the ambiguous experts this workgroup owns
         unsigned want = 0;
@@ -759,7 +1075,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
           if (lane == 0 && !ok) sel.state = 2;
         }
-        __syncthreads();
+        lds_barrier();
       }
       if (sel.state == 2) {
         // every expert's exact chain (owners compute theirs), then router_topk
@@ -781,24 +1097,24 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (!sync_barrier(a, l, kBarEx2, rt)) return;
         float *lgs = prod;  // [E]
         for (int e = t; e < E; e += kT) lgs[e] = ld_agent(&a.ex[e]);
-        __syncthreads();
+        lds_barrier();
         if (wave == 0) {
           float m = -__builtin_huge_valf();
           for (int e = lane; e < E; e += 64) m = fmaxf(m, lgs[e]);
           m = wave_max_dpp(m);
           if (lane == 0) sel.mx = m;
         }
-        __syncthreads();
+        lds_barrier();
         for (int e = t; e < E; e += kT) lgs[e] = expf_glibc(lgs[e] - sel.mx);
-        __syncthreads();
+        lds_barrier();
         if (t == 0) {
           float den = 0.0f;
           for (int e = 0; e < E; e++) den += lgs[e];
           sel.den = den;
         }
-        __syncthreads();
+        lds_barrier();
         for (int e = t; e < E; e += kT) lgs[e] = lgs[e] / sel.den;
-        __syncthreads();
+        lds_barrier();
         if (wave == 0) {
           for (int j = 0; j < K; j++) {
             unsigned long long best = 0;
@@ -827,66 +1143,87 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             if (b == 0) atomicAdd(&L.stats[2], 1ull);
           }
         }
-        __syncthreads();
+        lds_barrier();
       }
       if (b == 0 && t < K) {
         if (a.route_idx) a.route_idx[t] = rt.idx[t];
         if (a.route_w) a.route_w[t] = rt.w[t];
       }
-      __syncthreads();  // the selection's LDS is reused below
+      lds_barrier();  // the selection's LDS is reused below
     }
     stamp(a, l, 3);
 
     // ======================= stage G =======================
     {
-      float(*red)[16] = (float(*)[16])S.u;              // [kW][16]
-      unsigned *stage = (unsigned *)(S.u + kW * 16 * 4);  // [8] packed digits
+      float(*red)[16] = (float(*)[16])S.u;                  // [2][kW][16] partials
+      unsigned *stage = (unsigned *)(S.u + 2 * kW * 16 * 4);  // [kW][8] packed digits
       const int nU = a.K * a.nrt_i;
       const int m = wave >> 2, qd = wave & 3;
       const int per = (a.ngh + 3) / 4, g0 = qd * per;
-      const int n = (a.ngh < g0 + per ? a.ngh : g0 + per) - g0;
+      const int n = (a.ngh < g0 + per ? a.ngh : g0 + per) - g0;  // this wave's groups (may be <= 0)
+      constexpr int BPL = FMT == 4 ? 16 : 12;
+      // Each wave streams its own tile-groups (its matrix, its groups, unit
+      // after unit) through a ring of kGRing slots in LDS: one tile-group's
+      // codes and row scales per slot, kGRing-1 of them in flight while one is
+      // computed.  Small in-flight amounts keep the copies from stalling the
+      // wave that issues them.
+      constexpr int kSlotG = 64 * BPL + 64;
+      unsigned char *ring = S.u + 2048 + (size_t)wave * kGRing * kSlotG;
+      const int nunits = b < nU ? (nU - 1 - b) / a.NB + 1 : 0;
+      const int nitems = n > 0 ? nunits * n : 0;
       const DigitSrc src = lane_digits(lane, 1, S.xd, a.Hp, S.xgp, a.ngh, zero16);
-      // pieces of 4 groups: piece k = (unit b + (k/2)*NB, half k%2), loaded one ahead
-      auto load_piece = [&](TilePrefetch<FMT, 4> &tp, int k) {
-        const int u = b + (k >> 1) * a.NB;
-        const int j = u / a.nrt_i, r16 = u % a.nrt_i;
-        const int e = rt.idx[j];
-        const int ga = g0 + (k & 1) * 4;
-        const int nn = n - (k & 1) * 4;
-        if ((unsigned)e < (unsigned)a.E && nn > 0)
-          tile_prefetch<FMT, 4>(tp, L.codes + (size_t)e * a.expert_codes + (size_t)m * a.gate_codes,
-                                L.scales + (size_t)e * a.expert_scales + (size_t)m * a.gate_scales, r16, a.ngh,
-                                ga, nn < 4 ? nn : 4, lane);
-      };
-      auto compute_piece = [&](const TilePrefetch<FMT, 4> &tp, int k, float acc4[4]) {
-        const int u = b + (k >> 1) * a.NB;
+      XOps xo;
+      xops_load<FMT>(xo, src, g0, n, lane);
+      // Issue cursor over this wave's items (unit iu, group gu, ring slot su);
+      // per unit one expert lookup, per item two copies with some lane active
+      // (vmcnt counts them; the waits below rely on it).  An invalid route
+      // copies the layer's first bytes instead (never read).
+      int iu = 0, gu = 0, su = 0, issued = 0;
+      const unsigned char *ucb = L.codes, *usb = (const unsigned char *)L.scales;
+      auto set_unit = [&](int i) {
+        const int u = b + i * a.NB, r16 = u % a.nrt_i;
         const int e = rt.idx[u / a.nrt_i];
-        const int ga = g0 + (k & 1) * 4;
-        const int nn = n - (k & 1) * 4;
-        if ((unsigned)e < (unsigned)a.E && nn > 0) tile_compute<FMT, 4>(tp, ga, nn < 4 ? nn : 4, src, acc4, lane);
+        const size_t tg = (size_t)r16 * a.ngh + g0;
+        const bool ok = (unsigned)e < (unsigned)a.E;
+        ucb = ok ? L.codes + (size_t)e * a.expert_codes + (size_t)m * a.gate_codes + tg * 64 * BPL : L.codes;
+        usb = (const unsigned char *)(ok ? L.scales + (size_t)e * a.expert_scales + (size_t)m * a.gate_scales +
+                                               tg * kTileRows
+                                         : L.scales);
       };
-      unsigned dep = 0;
-      auto finish_unit = [&](float acc4[4], int u) {
+      auto issue_next = [&]() {
+        const unsigned slot = lds_addr(ring + su * kSlotG);
+        if (16 * lane < 64 * BPL) dma_b128(ucb + gu * 64 * BPL + 16 * lane, slot);
+        if (16 * lane < 64) dma_b128(usb + gu * 64 + 16 * lane, slot + 64 * BPL);
+        issued++;
+        if (++su == kGRing) su = 0;
+        if (++gu == n) {
+          gu = 0;
+          if (++iu < nunits) set_unit(iu);
+        }
+      };
+      // Partials of unit i go to red[i & 1]; after one barrier, wave i % 8
+      // builds h for the unit while the others go on to the next unit (the
+      // next unit's barrier keeps red[i & 1] until the finisher is done).
+      auto finish_unit = [&](float acc4[4], int u, int i) {
         const int j = u / a.nrt_i, r16 = u % a.nrt_i;
         const int e = rt.idx[j];
+        float(*rb)[16] = red + (i & 1) * kW;
         digit_fold(acc4);
         if ((lane & 15) == 1) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) red[wave][4 * (lane >> 4) + i] = acc4[i];
+          for (int q = 0; q < 4; q++) rb[wave][4 * (lane >> 4) + q] = acc4[q];
         }
-        __syncthreads();
-        if (wave == 0 && lane < 16) {
+        lds_barrier();
+        if (wave == (i & (kW - 1)) && lane < 16) {
           const int r = lane;
-          const float gsum = red[0][r] + red[1][r] + red[2][r] + red[3][r];
-          const float usum = red[4][r] + red[5][r] + red[6][r] + red[7][r];
-          float h = silu_ref(gsum) * usum;  // c/qwen.c:3419
+          const float gsum = rb[0][r] + rb[1][r] + rb[2][r] + rb[3][r];
+          const float usum = rb[4][r] + rb[5][r] + rb[6][r] + rb[7][r];
+          // SwiGLU (c/qwen.c:3419); the routed hidden vector is quantised next,
+          // so the hardware exponential is within the tolerance
+          float h = gsum / (1.0f + __expf(-gsum)) * usum;
           if ((unsigned)e >= (unsigned)a.E || r16 * kTileRows + r >= a.I) h = 0.0f;
           // two int8 digits of this 16-value chunk: A = amax/127, B = A/254
-          float mm = fabsf(h);
-          mm = fmaxf(mm, __shfl_xor(mm, 1, 16));
-          mm = fmaxf(mm, __shfl_xor(mm, 2, 16));
-          mm = fmaxf(mm, __shfl_xor(mm, 4, 16));
-          mm = fmaxf(mm, __shfl_xor(mm, 8, 16));
+          const float mm = row16_max(fabsf(h));
           const float A = mm / 127.0f, B = A / 254.0f;
           int q1 = 0, q2 = 0;
           if (mm > 0.0f) {
@@ -895,51 +1232,60 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             const float rr2 = __builtin_fmaf(-(float)q1, A, h);
             q2 = (int)fminf(fmaxf(__builtin_rintf(rr2 * invB), -127.0f), 127.0f);
           }
-          int s1 = q1, s2 = q2;
-          s1 += __shfl_xor(s1, 1, 16);
-          s1 += __shfl_xor(s1, 2, 16);
-          s1 += __shfl_xor(s1, 4, 16);
-          s1 += __shfl_xor(s1, 8, 16);
-          s2 += __shfl_xor(s2, 1, 16);
-          s2 += __shfl_xor(s2, 2, 16);
-          s2 += __shfl_xor(s2, 4, 16);
-          s2 += __shfl_xor(s2, 8, 16);
-          ((signed char *)stage)[r] = (signed char)q1;
-          ((signed char *)stage)[16 + r] = (signed char)q2;
+          const int s1 = row16_sum_i(q1), s2 = row16_sum_i(q2);
+          signed char *stg = (signed char *)(stage + 8 * wave);
+          stg[r] = (signed char)q1;
+          stg[16 + r] = (signed char)q2;
           __builtin_amdgcn_wave_barrier();
           unsigned v = 0;
-          if (r < 8) v = stage[r];
+          if (r < 8) v = ((const unsigned *)stg)[r];
           else if (r == 8) v = __float_as_uint(A);
           else if (r == 9) v = __float_as_uint(B);
           else if (r == 10) v = (unsigned)s1;
           else if (r == 11) v = (unsigned)s2;
-          if (r < kRecWords) dep ^= pub(&a.hd[((size_t)j * a.ngi * 8 + r16) * kRecWords + r], v);
+          // a device-scope store: complete (and visible to every device-scope
+          // load) once vmcnt drains, which published() waits for before the
+          // workgroup arrives at the barrier
+          if (r < kRecWords)
+            __hip_atomic_store(&a.hd[((size_t)j * a.ngi * 8 + r16) * kRecWords + r], v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
-        __syncthreads();
       };
-      const int nunits = b < nU ? (nU - 1 - b) / a.NB + 1 : 0;
-      const int npieces = 2 * nunits;
-      TilePrefetch<FMT, 4> ta, tb;
-      float acc4[4] = {0, 0, 0, 0};
-      if (npieces > 0) load_piece(ta, 0);
-      for (int k = 0; k < npieces; k += 2) {
-        load_piece(tb, k + 1);
-        compute_piece(ta, k, acc4);
-        if (k + 2 < npieces) load_piece(ta, k + 2);
-        compute_piece(tb, k + 1, acc4);
-        finish_unit(acc4, b + (k >> 1) * a.NB);
+      if (nitems > 0) set_unit(0);
+      while (issued < kGRing - 1 && issued < nitems) issue_next();
+      int cs = 0;  // consume slot
+      for (int i = 0; i < nunits; i++) {
+        const int u = b + i * a.NB;
+        const int e = rt.idx[u / a.nrt_i];
+        const bool ok = (unsigned)e < (unsigned)a.E;
+        float acc4[4] = {0, 0, 0, 0};
+        if (n > 0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc4[i] = 0.0f;
+          for (int gi = 0; gi < kGMax; gi++)
+            if (gi < n) {
+              if (issued < nitems) issue_next();
+              const int after = issued - 1 - (i * n + gi);  // items issued after this one
+              if (after == kGRing - 1)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (kGRing - 1)) : "memory");
+              else
+                wait_vm(2 * after);
+              if (ok) g_item<FMT>(ring + cs * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
+              if (++cs == kGRing) cs = 0;
+            }
+        }
+        finish_unit(acc4, u, i);
       }
+      lds_barrier();  // the last finisher is done with its partials
       // zero records of chunks past I inside the last group (only when I % 128 != 0)
       if (b == 0 && wave == 0) {
         const int pad = a.ngi * 8 - a.nrt_i;
         for (int i = lane; i < a.K * pad * kRecWords; i += 64) {
           const int j = i / (pad * kRecWords), rem = i % (pad * kRecWords);
-          dep ^= pub(&a.hd[((size_t)j * a.ngi * 8 + a.nrt_i) * kRecWords + rem], 0u);
+          __hip_atomic_store(&a.hd[((size_t)j * a.ngi * 8 + a.nrt_i) * kRecWords + rem], 0u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      if (wave == 0) published(dep);
+      if (wave == 0) published(0);
     }
 
     // ======================= stage D (loads, then barrier h) =======================
@@ -954,44 +1300,39 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int tile0 = b, ntiles = a.H / kTileRows;
       unsigned char *dtile = S.u + dl.dtile;
       signed char *dsh = (signed char *)(S.u + dl.dsh);
-      // the tile's routed down tile-groups and shared down rows, straight into LDS
+      // the tile's routed down tile-groups and shared down rows, straight into
+      // LDS, copied by waves 1..7 (wave 0 polls the barrier meanwhile)
       auto issue_down = [&](int tile) {
-        for (int q = qa; q < qb; q++) {
+        if (wave == 0) return;
+        for (int q = wave - 1; q < nq; q += kW - 1) {
           const int j = q / a.ngi, g = q % a.ngi;
           const int e = rt.idx[j];
           if ((unsigned)e >= (unsigned)a.E) continue;
           const size_t tg = (size_t)tile * a.ngi + g;
           const unsigned char *src = L.codes + (size_t)e * a.expert_codes + 2 * a.gate_codes + (tg * 64 + lane) * BPL;
+          const unsigned slot = lds_addr(dtile + (size_t)q * kSlot);
           if constexpr (FMT == 4) {
-            __builtin_amdgcn_global_load_lds((const void *)src,
-                                             (__attribute__((address_space(3))) void *)(dtile + (size_t)q * kSlot), 16, 0, 0);
+            dma_b128(src, slot);
           } else {
             // three dword planes [3][64]: plane i holds word i of every lane's 12 bytes
 #pragma unroll
-            for (int i = 0; i < 3; i++)
-              __builtin_amdgcn_global_load_lds((const void *)(src + 4 * i),
-                                               (__attribute__((address_space(3))) void *)(dtile + (size_t)q * kSlot + 256 * i),
-                                               4, 0, 0);
+            for (int i = 0; i < 3; i++) dma_b32(src + 4 * i, slot + 256 * i);
           }
           if (lane < kTileRows)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(L.scales + (size_t)e * a.expert_scales + 2 * a.gate_scales + tg * kTileRows + lane),
-                (__attribute__((address_space(3))) void *)(dtile + (size_t)q * kSlot + 64 * BPL), 4, 0, 0);
+            dma_b32(L.scales + (size_t)e * a.expert_scales + 2 * a.gate_scales + tg * kTileRows + lane, slot + 64 * BPL);
         }
-        for (int r = wave; r < kTileRows; r += kW)
+        for (int r = wave - 1; r < kTileRows; r += kW - 1)
           for (int c0 = 0; c0 < a.Ish; c0 += 1024)
             if (c0 + 16 * lane < a.Ish)
-              __builtin_amdgcn_global_load_lds(
-                  (const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
-                  (__attribute__((address_space(3))) void *)(dsh + (size_t)r * (a.Ish + 16) + c0), 16, 0, 0);
+              dma_b128(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane,
+                       lds_addr(dsh + (size_t)r * (a.Ish + 16) + c0));
       };
-      if (tile0 < ntiles && wave != 0) issue_down(tile0);
-      __syncthreads();
+      lds_barrier();
       stamp(a, l, 4);
       if (t == 0) bar_arrive(bar_of(a, l, kBarH), a.NB);
-      if (tile0 < ntiles && wave == 0) issue_down(tile0);
+      if (tile0 < ntiles) issue_down(tile0);  // in flight across the barrier
       if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarH), a) ? 1 : 0;
-      __syncthreads();
+      lds_barrier();
       if (!rt.flag) return;
       stamp(a, l, 5);
 
@@ -1002,21 +1343,50 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       float *part = (float *)(S.u + dl.part);        // [K][kW][16]
       int *shp = (int *)(S.u + dl.shp);              // [kW][16]
       float *redm = (float *)(S.u + dl.redm);        // [kW]
-      const int nrec_words = a.K * a.ngi * 8 * kRecWords;
-      for (int i = t; i < nrec_words / 2; i += kT)
-        ((unsigned long long *)hrec)[i] = ld_agent((const unsigned long long *)a.hd + i);
+      // (every device-scope load of a batch is issued before the first is used)
+      const int n64 = a.K * a.ngi * 8 * kRecWords / 2;
+      {
+        unsigned long long hv[kHrecPT];
+#pragma unroll
+        for (int i = 0; i < kHrecPT; i++) {
+          const int j = t + i * kT;
+          hv[i] = j < n64 ? ld_agent((const unsigned long long *)a.hd + j) : 0ull;
+        }
+#pragma unroll
+        for (int i = 0; i < kHrecPT; i++) {
+          const int j = t + i * kT;
+          if (j < n64) ((unsigned long long *)hrec)[j] = hv[i];
+        }
+        for (int j = t + kHrecPT * kT; j < n64; j += kT)
+          ((unsigned long long *)hrec)[j] = ld_agent((const unsigned long long *)a.hd + j);
+      }
       for (int i = t; i < kMaxK * kW * 16; i += kT) part[i] = 0.0f;
       float hm = 0.0f;
-      for (int i = t; i < a.Ish; i += kT) {
-        const int ag = ld_agent(&acc[i]), au = ld_agent(&acc[a.Ish + i]);
-        // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
-        const float h = silu_ref((float)ag * L.gs[i] * sx) * ((float)au * L.us[i] * sx);
-        hsh[i] = h;
-        hm = fmaxf(hm, fabsf(h));
+      for (int i0 = t; i0 < a.Ish; i0 += kShPT * kT) {
+        int ag[kShPT], au[kShPT];
+        float gsv[kShPT], usv[kShPT];
+#pragma unroll
+        for (int q = 0; q < kShPT; q++) {
+          const int i = i0 + q * kT < a.Ish ? i0 + q * kT : i0;
+          ag[q] = ld_agent(&acc[i]);
+          au[q] = ld_agent(&acc[a.Ish + i]);
+          gsv[q] = L.gs[i];
+          usv[q] = L.us[i];
+        }
+#pragma unroll
+        for (int q = 0; q < kShPT; q++) {
+          const int i = i0 + q * kT;
+          if (i < a.Ish) {
+            // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
+            const float h = silu_ref((float)ag[q] * gsv[q] * sx) * ((float)au[q] * usv[q] * sx);
+            hsh[i] = h;
+            hm = fmaxf(hm, fabsf(h));
+          }
+        }
       }
       hm = wave_max_dpp(hm);
       if (lane == 0) redm[wave] = hm;
-      __syncthreads();
+      lds_barrier();
       float shx = 0.0f;
 #pragma unroll
       for (int w = 0; w < kW; w++) shx = fmaxf(shx, redm[w]);
@@ -1029,62 +1399,80 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
       for (int tile = tile0; tile < ntiles; tile += a.NB) {
         if (tile != tile0) issue_down(tile);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS loads have landed
-        __syncthreads();                                    // ... and every other wave's
+        wait_dma();     // this wave's LDS copies have landed
+        lds_barrier();  // ... and every other wave's
         constexpr int OFF = FMT == 4 ? 8 : 4;
         const int c = lane & 15, kb = lane >> 4;
         const bool lo = c < 8 && (c >> 1) == kb;
         const bool hi = c >= 8 && ((c - 8) >> 1) == kb;
         const int chb = lo ? kb : 4 + kb;
-        // routed: per tile-group two MFMAs; B column c = (chunk c>>1, digit c&1)
-        float accr[4] = {0, 0, 0, 0};
-        int jcur = -1;
-        for (int q = qa; q < qb; q++) {
-          const int j = q / a.ngi, g = q % a.ngi;
-          if (j != jcur) {
-            if (jcur >= 0) {
-#pragma unroll
-              for (int r = 0; r < 4; r++) {
-                const float v = row16_sum(accr[r]);
-                if (c == 0) part[(jcur * kW + wave) * 16 + 4 * kb + r] = v;
-                accr[r] = 0.0f;
-              }
-            }
-            jcur = j;
-          }
-          const int e = rt.idx[j];
-          if ((unsigned)e >= (unsigned)a.E) continue;
-          const unsigned char *tq = dtile + (size_t)q * kSlot;
+        // routed: per tile-group two MFMAs; B column c = (chunk c>>1, digit c&1).
+        // The next tile-group's LDS operands are read while this one computes.
+        struct DOps {
           TileWord<FMT> cw;
+          v4f s4;
+          v4i dv;
+          float dscl, zq;
+          bool valid;
+        };
+        auto load_ops = [&](DOps &o, int q, int jq, int gq) {
+          o.valid = (unsigned)rt.idx[jq] < (unsigned)a.E;
+          const unsigned char *tq = dtile + (size_t)q * kSlot;
           if constexpr (FMT == 4) {
             const v4u v = *(const v4u *)(tq + 16 * lane);
-            cw.w[0] = v.x;
-            cw.w[1] = v.y;
-            cw.w[2] = v.z;
-            cw.w[3] = v.w;
+            o.cw.w[0] = v.x;
+            o.cw.w[1] = v.y;
+            o.cw.w[2] = v.z;
+            o.cw.w[3] = v.w;
           } else {
             const unsigned *wp = (const unsigned *)tq + lane;
-            cw.w[0] = wp[0];
-            cw.w[1] = wp[64];
-            cw.w[2] = wp[128];
+            o.cw.w[0] = wp[0];
+            o.cw.w[1] = wp[64];
+            o.cw.w[2] = wp[128];
           }
-          const v4f s4 = *(const v4f *)(tq + 64 * BPL + 16 * kb);
-          v4i a0, a1;
-          unpack_tile<FMT>(cw, a0, a1);
-          const unsigned *rbase = hrec + (size_t)(j * a.ngi * 8 + g * 8) * kRecWords;
-          const v4i dv = *(const v4i *)(rbase + chb * kRecWords + (c & 1) * 4);
-          const v4i z = {0, 0, 0, 0};
-          v4i cc = {0, 0, 0, 0};
-          cc = mfma_i8(a0, lo ? dv : z, cc);
-          cc = mfma_i8(a1, hi ? dv : z, cc);
+          o.s4 = *(const v4f *)(tq + 64 * BPL + 16 * kb);
+          const unsigned *rbase = hrec + (size_t)(jq * a.ngi * 8 + gq * 8) * kRecWords;
+          o.dv = *(const v4i *)(rbase + chb * kRecWords + (c & 1) * 4);
           const unsigned *prm = rbase + (c >> 1) * kRecWords + 8;
-          const float dscl = __uint_as_float(prm[c & 1]);
-          const int Q = (int)prm[2 + (c & 1)];
-          const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          o.dscl = __uint_as_float(prm[c & 1]);
+          o.zq = (float)(OFF * (int)prm[2 + (c & 1)]) * o.dscl;
+        };
+        float accr[4] = {0, 0, 0, 0};
+        int jn = qa / a.ngi, gn = qa % a.ngi;
+        int jcur = jn;
+        DOps cur, nxt;
+        if (qa < qb) load_ops(nxt, qa, jn, gn);
+        for (int q = qa; q < qb; q++) {
+          cur = nxt;
+          const int jq = jn;
+          if (++gn == a.ngi) {
+            gn = 0;
+            ++jn;
+          }
+          if (q + 1 < qb) load_ops(nxt, q + 1, jn, gn);
+          if (jq != jcur) {
 #pragma unroll
-          for (int r = 0; r < 4; r++) accr[r] = __builtin_fmaf((float)(cc[r] - OFF * Q) * dscl, sv[r], accr[r]);
+            for (int r = 0; r < 4; r++) {
+              const float v = row16_sum(accr[r]);
+              if (c == 0) part[(jcur * kW + wave) * 16 + 4 * kb + r] = v;
+              accr[r] = 0.0f;
+            }
+            jcur = jq;
+          }
+          if (cur.valid) {
+            v4i a0, a1;
+            unpack_tile<FMT>(cur.cw, a0, a1);
+            const v4i z = {0, 0, 0, 0};
+            v4i cc = {0, 0, 0, 0};
+            cc = mfma_i8(a0, lo ? cur.dv : z, cc);
+            cc = mfma_i8(a1, hi ? cur.dv : z, cc);
+            const float sv[4] = {cur.s4.x, cur.s4.y, cur.s4.z, cur.s4.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              accr[r] = __builtin_fmaf(__builtin_fmaf((float)cc[r], cur.dscl, -cur.zq), sv[r], accr[r]);
+          }
         }
-        if (jcur >= 0) {
+        if (qa < qb) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             const float v = row16_sum(accr[r]);
@@ -1105,7 +1493,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             for (int i = 0; i < 4; i++) shp[wave * 16 + 4 * kb + i] = cd[i];
           }
         }
-        __syncthreads();
+        lds_barrier();
         if (t < kTileRows) {
           // moe_forward's combine: fma over k in route order, then shared * gate
           float out = 0.0f;
@@ -1122,20 +1510,19 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
-        __syncthreads();
+        lds_barrier();
         for (int i = t; i < kMaxK * kW * 16; i += kT) part[i] = 0.0f;
       }
-      __syncthreads();
+      lds_barrier();
     }
 
     // ======================= barrier y (next layer) =======================
     stamp(a, l, 6);
     if (l + 1 < a.n) {
-      __syncthreads();
+      lds_barrier();
       if (t == 0) bar_arrive(bar_of(a, l, kBarY), a.NB);
-      prefetch_static(a, layer_ref(a, l + 1), rr, sr);
       if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarY), a) ? 1 : 0;
-      __syncthreads();
+      lds_barrier();
       if (!rt.flag) return;
       stamp(a, l, 7);
     }
@@ -1167,22 +1554,40 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
   return r;
 }
 
+// Bytes of the stage-local LDS union: the largest of stage R's inputs,
+// the selection's arrays, stage G's ring and stage D's layout.
+static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, int fmt, int rslots, int shkc) {
+  const size_t rlay = r_layout(rslots, H, shkc).end;
+  const size_t sel = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (size_t)E * 8 + 16 +
+                     (size_t)kRSlots * H * 4;
+  const size_t dst = d_layout(K, ngi, Ish, fmt).end;
+  const int bpl = fmt == 4 ? 16 : 12;
+  const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64);
+  size_t u = rlay;
+  if (sel > u) u = sel;
+  if (dst > u) u = dst;
+  if (ring > u) u = ring;
+  return u;
+}
+
 bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   const int NB = ctx->sm_count;
   const int H = s.hidden, E = s.experts, K = s.topk, I = s.intermediate, Ish = s.shared_intermediate;
   if (H > 2048 * kNch || H % 64 || K > kMaxK || K > E || I % 16 || Ish % 64 || Ish > kStackMaxIsh) return false;
   if ((E + 1 + NB - 1) / NB > kRSlots) return false;                 // router rows in registers
+  if (E > 2 * kT) return false;                                       // selection keys in registers
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
   if (ngh > 32) return false;                                         // G: 8 groups per wave
   const int Hp = ngh * kGroup;
-  const size_t sel = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (size_t)E * 8 + 16 +
-                     (size_t)kRSlots * H * 4;
-  const size_t dst = d_layout(K, ngi, Ish, s.expert_format).end;
-  size_t u = sizeof(RStageLds);
-  if (sel > u) u = sel;
-  if (dst > u) u = dst;
-  return lds_fixed(Hp, ngh) + u <= (size_t)ctx->shared_per_block;
+  const int rslots = (E + 1 + NB - 1) / NB;
+  int KQ = NB / (2 * (Ish / kTileRows));
+  if (KQ < 1) KQ = 1;
+  if (KQ > H / 64) KQ = H / 64;
+  const int shkc = (H / 64 + KQ - 1) / KQ;
+  if ((size_t)rslots * H * 4 + (size_t)shkc * 1024 > (size_t)16 * kStRegs * kStThreads) return false;  // registers
+  const size_t u = stack_union_bytes(E, H, K, ngh, ngi, Ish, s.expert_format, rslots, shkc);
+  return lds_fixed(Hp, ngh) + u + 1024 <= (size_t)ctx->shared_per_block;
 }
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
@@ -1261,9 +1666,9 @@ int stack_check_abort(ColiCuda *ctx) {
   // clear the device state the aborted call left behind
   *ctx->stack_abort_host = 0;
   const size_t per_layer = ((size_t)kBars * kBarWords + 2 * (size_t)kStackMaxIsh) * 2 * 4;
-  hipMemsetAsync(ctx->stack_sync, 0, per_layer * ctx->stack_cap_layers, ctx->stream);
-  hipMemsetAsync(ctx->stack_abort, 0, 256, ctx->stream);
-  hipStreamSynchronize(ctx->stream);
+  (void)hipMemsetAsync(ctx->stack_sync, 0, per_layer * ctx->stack_cap_layers, ctx->stream);
+  (void)hipMemsetAsync(ctx->stack_abort, 0, 256, ctx->stream);
+  (void)hipStreamSynchronize(ctx->stream);
   ctx->stack_dirty[0] = ctx->stack_dirty[1] = 0;
   ctx->stack_dirty_acc[0] = ctx->stack_dirty_acc[1] = 0;
   return fail_arg("MoE stack step aborted: a grid barrier timed out (the kernel needs every workgroup "
@@ -1310,6 +1715,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   if (KQ > a.H / 64) KQ = a.H / 64;
   a.KQ = KQ;
   a.n_sh_tasks = nsh_rt * KQ;
+  a.shkc = (a.H / 64 + KQ - 1) / KQ;
   a.x = x;
   a.xs = xs;
   a.y = y;
@@ -1334,17 +1740,12 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.trace = (unsigned long long *)ctx->stack_trace;
   a.trace_words = ctx->stack_trace_words;
   const size_t Hp = (size_t)a.Hp;
-  const size_t sel = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(a.E + 1) * 16 + (size_t)a.E * 8 + 16 +
-                     (size_t)kRSlots * a.H * 4;
-  const size_t dst = d_layout(a.K, a.ngi, a.Ish, a.fmt).end;
-  size_t u = sizeof(RStageLds);
-  if (sel > u) u = sel;
-  if (dst > u) u = dst;
+  const size_t u = stack_union_bytes(a.E, a.H, a.K, a.ngh, a.ngi, a.Ish, a.fmt, a.rslots, a.shkc);
   size_t lds = lds_fixed((int)Hp, a.ngh) + u;
   // more than half of a CU's LDS: exactly one workgroup per CU
   const size_t one_per_cu = (size_t)ctx->shared_per_block / 2 + 1024;
   if (lds < one_per_cu) lds = one_per_cu;
-  if (lds > (size_t)ctx->shared_per_block) return 1;
+  if (lds + 1024 > (size_t)ctx->shared_per_block) return 1;
   hipError_t e;
   if (a.fmt == 4) {
     e = hipFuncSetAttribute((const void *)k_stack<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1363,11 +1764,11 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
 }
 
 void stack_release(ColiCuda *ctx) {
-  if (ctx->stack_sync) hipFree(ctx->stack_sync);
-  if (ctx->stack_table_dev) hipFree(ctx->stack_table_dev);
+  if (ctx->stack_sync) (void)hipFree(ctx->stack_sync);
+  if (ctx->stack_table_dev) (void)hipFree(ctx->stack_table_dev);
   free(ctx->stack_table_host);
-  if (ctx->stack_abort) hipFree(ctx->stack_abort);
-  if (ctx->stack_abort_host) hipHostFree(ctx->stack_abort_host);
+  if (ctx->stack_abort) (void)hipFree(ctx->stack_abort);
+  if (ctx->stack_abort_host) (void)hipHostFree(ctx->stack_abort_host);
   ctx->stack_sync = nullptr;
   ctx->stack_table_dev = nullptr;
   ctx->stack_table_host = nullptr;
