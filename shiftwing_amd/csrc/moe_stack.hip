@@ -266,6 +266,13 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += SW_DPP_F(0.0f, v, 0x140, 0xF, true);
   return v;
 }
+// Row shift left within each 16-lane row: lane l receives lane l+1 (the
+// row's last lane receives 0).
+__device__ __forceinline__ double dpp_row_shl1_d(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), 0x101, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), 0x101, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
 __device__ __forceinline__ double order_margin(double a, double b, double mx) {
   return 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
 }
@@ -375,8 +382,8 @@ __host__ __device__ inline RLayout r_layout(int rslots, int H, int shkc) {
 
 // Stage R's inputs of the next layer travel in registers of waves 1..7
 // (wave 0 keeps no loads outstanding: it polls the grid barriers).  They are
-// loaded while the current layer waits on its router barrier and selection
-// (HBM is otherwise idle then) and written to LDS when the next layer starts.
+// loaded while the current layer waits on its last grid barrier (HBM is
+// otherwise idle then) and written to LDS when the next layer starts.
 // Thread T = t - 64 carries the 16-byte chunks T + 448 i of the byte stream
 // [router rows of this workgroup | shared tile in 1 KB blocks: k-chunk kc,
 // then 16 rows of 64 bytes].  Every offset is found with compares, shifts and
@@ -589,8 +596,10 @@ constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
 constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
 constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
-  unsigned long long wcand[kSelRec * kW * (kMaxK + 1)];  // each wave's top K+1 keys per record round
-  unsigned long long wup[kW];                           // each wave's largest upper bound outside them
+  unsigned long long samp[64];  // each 64-expert list's c largest keys
+  unsigned long long mc[64];    // keys at or above the sample threshold
+  unsigned long long wup[kW];   // each wave's largest upper bound below it
+  int nmc;
   double theta, mxd;
   int cand[kMaxK + 1];
   int state;      // 0 certified, 1 targeted exact, 2 full exact
@@ -890,116 +899,136 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (e <= E) lb[e] = make_double2(lx[i], ly[i]);
         key[i] = e < E ? ((unsigned long long)float_key((float)lx[i]) << 32) | (unsigned)(~e) : 0ull;
       }
-      if (t == 0) sel.nm = 0;
-      // Each wave ranks its 64 experts of each record round among themselves
-      // (keys: fp64 logit as a float key, lowest index first on equal keys;
-      // near-ties fail the separation tests) by rotating the keys around the
-      // wave; its top K+1 go to LDS in rank order.
-      const int nc = K + 1 < E ? K + 1 : E;
-      {
-        int rank[kSelRec];
+      if (t == 0) {
+        sel.nm = 0;
+        sel.nmc = 0;
+      }
+      // Candidates by a sampled threshold.  List L holds experts [64L, 64L+64)
+      // (one wave, one record round); the c largest keys of each of the nl
+      // non-empty lists form the sample, with c chosen so that it holds at
+      // least K keys.  T0 = the sample's K-th largest key is at most the K-th
+      // largest key overall, so the top K lie among the keys >= T0: usually a
+      // few more than K, at most 64 on this path (else the full exact path).
+      const int nl = (E + 63) >> 6;
+      const int c = nl == 1 ? K : max(2, (K - 1 + nl - 2) / (nl - 1));  // nl * c <= 64
 #pragma unroll
-        for (int i = 0; i < kSelRec; i++) rank[i] = 0;
-        // rank within the wave's 64 lanes, per record round i
-#pragma unroll
-        for (int i = 0; i < kSelRec; i++) {
-          if (t + i * kT - lane >= E) continue;  // wave-uniform: no key in this round
-          unsigned lo = (unsigned)key[i], hi = (unsigned)(key[i] >> 32);
-          int rk = 0;
-          for (int sh = 1; sh < 64; sh++) {
-            // DPP wave_ror:1 -- lane l receives lane l-1 (wrapping)
-            lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)lo, 0x13C, 0xF, 0xF, false);
-            hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)hi, 0x13C, 0xF, 0xF, false);
-            const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-            rk += o > key[i];
-          }
-          rank[i] = rk;
+      for (int i = 0; i < kSelRec; i++) {
+        const int li = i * kW + wave;
+        if (li >= nl) continue;  // wave-uniform
+        unsigned long long kk = key[i];
+        for (int j = 0; j < c; j++) {
+          const unsigned long long m = wave_max_u64(kk);
+          if (lane == 0) sel.samp[li * c + j] = m;
+          if (kk == m) kk = 0ull;
         }
-        // candidates of this wave: rounds merged by rank (rounds are ranked
-        // separately, so a wave's list holds up to kSelRec * (K+1) keys)
-#pragma unroll
-        for (int i = 0; i < kSelRec; i++)
-          if (key[i] && rank[i] < nc) sel.wcand[(i * kW + wave) * (kMaxK + 1) + rank[i]] = key[i];
-        // the largest upper bound among this wave's experts outside those lists
+      }
+      {
+        // the shared expert's gate, by the thread holding record E
+        const int iE = E / kT;
+        if (t == E - iE * kT) rt.sg = sigmoid_ref((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])));
+      }
+      lds_barrier();
+      // T0, found by every wave: the sample with exactly K-1 larger ones
+      unsigned long long T0;
+      {
+        const int ns = nl * c;
+        const unsigned long long sv = lane < ns ? sel.samp[lane] : 0ull;
+        int rk = 0;
+        for (int q = 0; q < ns; q++) rk += sel.samp[q] > sv;
+        const unsigned long long bal = __ballot(sv != 0ull && rk == K - 1);
+        T0 = 1ull;  // (unreachable: the sample holds K keys) every key
+        if (bal) {
+          const int src = __ffsll((long long)bal) - 1;
+          const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)sv, src);
+          const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(sv >> 32), src);
+          T0 = ((unsigned long long)hi << 32) | lo;
+        }
+      }
+      // keys >= T0 to the candidate list; the largest upper bound of the rest
+      {
         unsigned long long up = 0;
 #pragma unroll
-        for (int i = 0; i < kSelRec; i++)
-          if (key[i] && rank[i] >= nc) {
+        for (int i = 0; i < kSelRec; i++) {
+          if (i * kT + wave * 64 >= E) continue;  // wave-uniform: no key in this round
+          const bool in = key[i] >= T0;           // key 0 (no expert) is below every T0
+          const unsigned long long bal = __ballot(in);
+          if (bal) {
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&sel.nmc, __popcll(bal));
+            base = __builtin_amdgcn_readfirstlane(base);
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+            if (in && pos < 64) sel.mc[pos] = key[i];
+          }
+          if (key[i] && !in) {
             const unsigned long long k2 = double_key(lx[i] + ly[i]);
             up = k2 > up ? k2 : up;
           }
+        }
         up = wave_max_u64(up);
         if (lane == 0) sel.wup[wave] = up;
-        // lists shorter than nc (rounds with few experts) end with zero keys
-        for (int i = 0; i < kSelRec; i++) {
-          const int nkeys = E - (i * kT + wave * 64);  // keys of this wave in round i
-          if (nkeys > 0 && nkeys < nc && lane >= nkeys && lane < nc)
-            sel.wcand[(i * kW + wave) * (kMaxK + 1) + lane] = 0ull;
-          if (nkeys <= 0 && lane < nc) sel.wcand[(i * kW + wave) * (kMaxK + 1) + lane] = 0ull;
-        }
       }
       lds_barrier();
-      if (wave != 0) {
-        // waves 1..7: the next layer's stage R inputs, loaded while wave 0
-        // merges (the memory system is otherwise idle here)
-        if (l + 1 < a.n) static_load(a, layer_ref(a, l + 1), sreg, t);
-      } else {
-        // merge: K rounds of a tournament over the lists' heads (each list is
-        // in rank order; keys are unique, so one lane holds each round's max)
-        const int nlists = ((E + kT - 1) / kT) * kW;
-        int ptr = 0;
-        unsigned long long head = lane < nlists ? sel.wcand[lane * (kMaxK + 1)] : 0ull;
-        unsigned long long kth_key = 0;
-        for (int r = 0; r < K; r++) {
-          const unsigned long long m = wave_max_u64(head);
-          if (lane == 0) sel.cand[r] = (int)(~(unsigned)m);
-          if (head == m) {
-            ptr++;
-            head = ptr < nc ? sel.wcand[lane * (kMaxK + 1) + ptr] : 0ull;
-          }
-          kth_key = m;
-        }
-        __builtin_amdgcn_wave_barrier();
-        // the largest upper bound outside the top K: the waves' leftovers, the
-        // listed keys below the K-th
-        unsigned long long upk = lane < kW ? sel.wup[lane] : 0ull;
-        for (int g = lane; g < nlists * (kMaxK + 1); g += 64) {
-          const unsigned long long k1 = (g % (kMaxK + 1)) < nc ? sel.wcand[g] : 0ull;
-          if (k1 && k1 < kth_key) {
-            const double2 v = lb[(int)(~(unsigned)k1)];
+      if (wave == 0) {
+        const int M = sel.nmc;
+        if (M > 64) {
+          if (lane == 0) sel.state = 2;
+        } else {
+          // rank of each candidate among the candidates
+          const unsigned long long ck = lane < M ? sel.mc[lane] : 0ull;
+          int rk = 0;
+          for (int q = 0; q < M; q++) rk += sel.mc[q] > ck;
+          if (lane < M && rk < K) sel.cand[rk] = (int)(~(unsigned)ck);
+          // the largest upper bound outside the top K
+          unsigned long long upk = lane < kW ? sel.wup[lane] : 0ull;
+          if (lane < M && rk >= K) {
+            const double2 v = lb[(int)(~(unsigned)ck)];
             const unsigned long long k2 = double_key(v.x + v.y);
             upk = k2 > upk ? k2 : upk;
           }
-        }
-        upk = wave_max_u64(upk);
-        const double mx = lb[sel.cand[0]].x;
-        const double2 kth = lb[sel.cand[K - 1]];
-        bool pair_ok = true;
-        if (lane + 1 < K) {
-          const double2 p = lb[sel.cand[lane]], q = lb[sel.cand[lane + 1]];
-          pair_ok = (p.x - p.y) - (q.x + q.y) > order_margin(p.x, q.x, mx);
-        }
-        bool ok = L.mode == 0 && __all(pair_ok);
-        if (ok && K < E) {
-          const double up = key_double(upk);
-          ok = (kth.x - kth.y) - up > order_margin(kth.x, up, mx);
-        }
-        if (ok) ok = (kth.x - kth.y) - (mx + lb[sel.cand[0]].y) > -75.0;
-        if (ok) {
-          const double ev = lane < K ? exp(lb[sel.cand[lane < K ? lane : 0]].x - mx) : 0.0;
-          const double den = wave_sum_dpp(ev);
-          if (lane < K) {
-            rt.idx[lane] = sel.cand[lane];
-            rt.w[lane] = (float)(ev / den);
+          upk = wave_max_u64(upk);
+          __builtin_amdgcn_wave_barrier();
+          // certification, one candidate per lane (K <= 16: lanes 0..15)
+          const int ce = sel.cand[lane < K ? lane : 0];
+          const double2 v = lb[ce];
+          const double vlo = v.x - v.y;
+          const double mx = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), 0),
+                                             __builtin_amdgcn_readlane(__double2loint(v.x), 0));
+          const double mxy = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.y), 0),
+                                              __builtin_amdgcn_readlane(__double2loint(v.y), 0));
+          const double kx = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), K - 1),
+                                             __builtin_amdgcn_readlane(__double2loint(v.x), K - 1));
+          const double klo = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), K - 1),
+                                              __builtin_amdgcn_readlane(__double2loint(vlo), K - 1));
+          // the next candidate's bounds (row shift left within lanes 0..15)
+          const double nx = dpp_row_shl1_d(v.x), ny = dpp_row_shl1_d(v.y);
+          bool pair_ok = true;
+          if (lane + 1 < K) pair_ok = vlo - (nx + ny) > order_margin(v.x, nx, mx);
+          bool ok = L.mode == 0 && __all(pair_ok);
+          if (ok && K < E) {
+            const double up = key_double(upk);
+            ok = klo - up > order_margin(kx, up, mx);
           }
-        }
-        if (lane == 0) {
-          double theta = 1e300;
-          for (int r = 0; r < K; r++) theta = fmin(theta, lb[sel.cand[r]].x - lb[sel.cand[r]].y);
-          sel.theta = theta;
-          sel.mxd = mx;
-          sel.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
-          rt.sg = sigmoid_ref((float)lb[E].x);
+          if (ok) ok = klo - (mx + mxy) > -75.0;
+          if (ok) {
+            const double ev = lane < K ? exp(v.x - mx) : 0.0;
+            const double den = wave_sum_dpp(ev);
+            if (lane < K) {
+              rt.idx[lane] = ce;
+              rt.w[lane] = (float)(ev / den);
+            }
+          } else {
+            // the lowest lower bound among the K candidates
+            double theta = 1e300;
+            for (int r = 0; r < K; r++)
+              theta = fmin(theta, __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), r),
+                                                   __builtin_amdgcn_readlane(__double2loint(vlo), r)));
+            if (lane == 0) {
+              sel.theta = theta;
+              sel.mxd = mx;
+            }
+          }
+          if (lane == 0) sel.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
         }
       }
       lds_barrier();
@@ -1521,6 +1550,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     if (l + 1 < a.n) {
       lds_barrier();
       if (t == 0) bar_arrive(bar_of(a, l, kBarY), a.NB);
+      // waves 1..7: the next layer's stage R inputs, loaded while the grid
+      // finishes this layer (the memory system is otherwise idle then)
+      static_load(a, layer_ref(a, l + 1), sreg, t);
       if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarY), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
