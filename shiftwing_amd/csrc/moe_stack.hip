@@ -181,6 +181,12 @@ __device__ __forceinline__ void dma_b32(const void *gptr, unsigned base) {
   base = __builtin_amdgcn_readfirstlane(base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gptr), "s"(base) : "memory", "m0");
 }
+// the same copy from a wave-uniform base plus a per-lane 32-bit byte offset
+__device__ __forceinline__ void dma_b128_s(const void *sbase, unsigned voff, unsigned base) {
+  base = __builtin_amdgcn_readfirstlane(base);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -1203,31 +1209,42 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const DigitSrc src = lane_digits(lane, 1, S.xd, a.Hp, S.xgp, a.ngh, zero16);
       XOps xo;
       xops_load<FMT>(xo, src, g0, n, lane);
-      // Issue cursor over this wave's items (unit iu, group gu, ring slot su);
-      // per unit one expert lookup, per item two copies with some lane active
-      // (vmcnt counts them; the waits below rely on it).  An invalid route
-      // copies the layer's first bytes instead (never read).
-      int iu = 0, gu = 0, su = 0, issued = 0;
-      const unsigned char *ucb = L.codes, *usb = (const unsigned char *)L.scales;
-      auto set_unit = [&](int i) {
-        const int u = b + i * a.NB, r16 = u % a.nrt_i;
-        const int e = rt.idx[u / a.nrt_i];
-        const size_t tg = (size_t)r16 * a.ngh + g0;
-        const bool ok = (unsigned)e < (unsigned)a.E;
-        ucb = ok ? L.codes + (size_t)e * a.expert_codes + (size_t)m * a.gate_codes + tg * 64 * BPL : L.codes;
-        usb = (const unsigned char *)(ok ? L.scales + (size_t)e * a.expert_scales + (size_t)m * a.gate_scales +
-                                               tg * kTileRows
-                                         : L.scales);
+      // This wave's unit table, one unit per lane: byte offsets of the unit's
+      // first tile-group of this wave's matrix and groups (an invalid route
+      // reads the layer's first bytes instead; its results are discarded).
+      unsigned long long tc = 0ull, ts = 0ull;
+      if (lane < nunits) {
+        const int u = b + lane * a.NB, j = u / a.nrt_i, r16 = u - j * a.nrt_i;
+        const int e = rt.idx[j];
+        if ((unsigned)e < (unsigned)a.E) {
+          const size_t tg = (size_t)r16 * a.ngh + g0;
+          tc = (size_t)e * a.expert_codes + (size_t)m * a.gate_codes + tg * 64 * BPL;
+          ts = ((size_t)e * a.expert_scales + (size_t)m * a.gate_scales + tg * kTileRows) * 4;
+        }
+      }
+      // Issue cursor (unit iu, group gu, ring slot su).  Every step issues the
+      // two copies of one tile-group; past the last item it keeps re-reading
+      // the last unit's groups (in bounds, never consumed), so that exactly
+      // kGRing-1 items are always in flight and one wait count serves all.
+      int iu = 0, gu = 0, su = 0;
+      const unsigned char *cb = (const unsigned char *)L.codes, *sbp = (const unsigned char *)L.scales;
+      auto unit_base = [&](int i) {
+        const int ii = i < nunits ? i : nunits - 1;
+        const unsigned lo_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)tc, ii);
+        const unsigned hi_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(tc >> 32), ii);
+        const unsigned lo_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)ts, ii);
+        const unsigned hi_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(ts >> 32), ii);
+        cb = (const unsigned char *)L.codes + (((unsigned long long)hi_c << 32) | lo_c);
+        sbp = (const unsigned char *)L.scales + (((unsigned long long)hi_s << 32) | lo_s);
       };
       auto issue_next = [&]() {
         const unsigned slot = lds_addr(ring + su * kSlotG);
-        if (16 * lane < 64 * BPL) dma_b128(ucb + gu * 64 * BPL + 16 * lane, slot);
-        if (16 * lane < 64) dma_b128(usb + gu * 64 + 16 * lane, slot + 64 * BPL);
-        issued++;
+        if (16 * lane < 64 * BPL) dma_b128_s(cb + gu * 64 * BPL, 16 * lane, slot);
+        if (16 * lane < 64) dma_b128_s(sbp + gu * 64, 16 * lane, slot + 64 * BPL);
         if (++su == kGRing) su = 0;
         if (++gu == n) {
           gu = 0;
-          if (++iu < nunits) set_unit(iu);
+          unit_base(++iu);
         }
       };
       // Partials of unit i go to red[i & 1]; after one barrier, wave i % 8
@@ -1280,30 +1297,31 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
                                __HIP_MEMORY_SCOPE_AGENT);
         }
       };
-      if (nitems > 0) set_unit(0);
-      while (issued < kGRing - 1 && issued < nitems) issue_next();
+      if (nitems > 0) {
+        unit_base(0);
+#pragma unroll
+        for (int k = 0; k < kGRing - 1; k++) issue_next();
+      }
       int cs = 0;  // consume slot
       for (int i = 0; i < nunits; i++) {
         const int u = b + i * a.NB;
-        const int e = rt.idx[u / a.nrt_i];
-        const bool ok = (unsigned)e < (unsigned)a.E;
         float acc4[4] = {0, 0, 0, 0};
         if (n > 0) {
 #pragma unroll
           for (int gi = 0; gi < kGMax; gi++)
             if (gi < n) {
-              if (issued < nitems) issue_next();
-              const int after = issued - 1 - (i * n + gi);  // items issued after this one
-              if (after == kGRing - 1)
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (kGRing - 1)) : "memory");
-              else
-                wait_vm(2 * after);
-              if (ok) g_item<FMT>(ring + cs * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
+              issue_next();
+              // this item's two copies are done once at most the 2(kGRing-1)
+              // issued after them are outstanding (a wave's loads complete in
+              // order; a store of finish_unit only makes the wait longer)
+              asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (kGRing - 1)) : "memory");
+              g_item<FMT>(ring + cs * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
               if (++cs == kGRing) cs = 0;
             }
         }
         finish_unit(acc4, u, i);
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the last item
       lds_barrier();  // the last finisher is done with its partials
       // zero records of chunks past I inside the last group (only when I % 128 != 0)
       if (b == 0 && wave == 0) {
@@ -1611,6 +1629,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
   if (ngh > 32) return false;                                         // G: 8 groups per wave
+  if ((K * (I / kTileRows) + NB - 1) / NB > 64) return false;         // G: one unit per lane
   const int Hp = ngh * kGroup;
   const int rslots = (E + 1 + NB - 1) / NB;
   int KQ = NB / (2 * (Ish / kTileRows));
