@@ -109,6 +109,7 @@ struct StackArgs {
   unsigned *abort_word; // device
   unsigned *abort_host; // host-mapped status
   long long spin_ticks; // wall-clock budget of one wait (100 MHz ticks)
+  unsigned tag0;        // layer 0's tag (1..255) in the exchanged words
   unsigned long long *trace;  // optional stage stamps [layer][NB][kStamps]
   size_t trace_words;
 };
@@ -235,6 +236,38 @@ __device__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) 
   }
 }
 
+// Tagged words.  A word exchanged between workgroups within a layer carries
+// the layer's tag (1..255; consecutive layers, also across calls, differ) in
+// its low byte, so a reader needs no barrier: it reads the words themselves
+// until every one shows the tag.  64-bit words are read and written whole.
+// Between calls every tagged word is zero (never a tag): each call clears
+// what it wrote once no one reads it any more, fresh scratch is cleared, and
+// so is the scratch of an aborted call.
+__device__ __forceinline__ unsigned layer_tag(const StackArgs &a, int l) {
+  return 1u + (a.tag0 - 1u + (unsigned)l) % 255u;
+}
+__device__ __forceinline__ unsigned long long with_tag(unsigned long long bits, unsigned tag) {
+  return (bits & ~0xFFull) | tag;
+}
+// spins until *p shows the tag; false on abort or time-out (then every
+// workgroup leaves through the abort word)
+__device__ bool poll_tag64(const unsigned long long *p, unsigned tag, unsigned long long &v, const StackArgs &a) {
+  const long long t0 = (long long)wall_clock64();
+  for (unsigned it = 0;; it++) {
+    v = ld_agent(p);
+    if ((unsigned)(v & 0xFFull) == tag) return true;
+    if ((it & 31) == 31) {
+      if (ld_agent(a.abort_word)) return false;
+      if ((long long)wall_clock64() - t0 > a.spin_ticks) {
+        atomicMax(a.abort_word, 1u);
+        __hip_atomic_store(a.abort_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // arrive: the workgroup's published words must have returned already
 __device__ __forceinline__ void bar_arrive(unsigned *bar, int NB) {
   const int g = blockIdx.x & 7;
@@ -290,17 +323,20 @@ struct Lds {
   signed char *xd;   // [2][Hp] routed activation digits
   float4 *xgp;       // [ngh]
   signed char *xq;   // [Hp] IDOT quantisation of x
+  signed char *hq;   // [Ish] IDOT quantisation of the shared hidden vector
   unsigned char *u;  // stage-local union
 };
-__host__ __device__ inline size_t lds_fixed(int Hp, int ngh) {
-  return (((size_t)2 * Hp + 15) & ~(size_t)15) + (size_t)ngh * 16 + (((size_t)Hp + 15) & ~(size_t)15) + 16;
+__host__ __device__ inline size_t lds_fixed(int Hp, int ngh, int Ish) {
+  return (((size_t)2 * Hp + 15) & ~(size_t)15) + (size_t)ngh * 16 + (((size_t)Hp + 15) & ~(size_t)15) +
+         (((size_t)Ish + 15) & ~(size_t)15) + 16;
 }
-__device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh) {
+__device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, int Ish) {
   Lds s;
   s.xd = (signed char *)smem;
   s.xgp = (float4 *)(smem + (((size_t)2 * Hp + 15) & ~(size_t)15));
   s.xq = (signed char *)(s.xgp + ngh);
-  s.u = smem + lds_fixed(Hp, ngh);
+  s.hq = s.xq + (((size_t)Hp + 15) & ~(size_t)15);
+  s.u = smem + lds_fixed(Hp, ngh, Ish);
   return s;
 }
 
@@ -309,7 +345,7 @@ __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh) {
 // (placed past everything stage G uses, since they are loaded before the "h"
 // barrier while stage G's buffers may still be read).
 struct DLayout {
-  size_t hrec, hsh, hq, part, shp, redm, dtile, dsh, end;
+  size_t hrec, part, shp, dtile, dsh, end;
 };
 __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   DLayout d;
@@ -321,11 +357,8 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   };
   const size_t bpl = fmt == 4 ? 16 : 12;
   d.hrec = take((size_t)K * ngi * 8 * kRecWords * 4);
-  d.hsh = take((size_t)Ish * 4);
-  d.hq = take((size_t)Ish);
   d.part = take((size_t)kMaxK * kW * 16 * 4);
   d.shp = take((size_t)kW * 16 * 4);
-  d.redm = take((size_t)kW * 4);
   d.dtile = take((size_t)K * ngi * (64 * bpl + 64));
   d.dsh = take((size_t)kTileRows * (Ish + 16));
   d.end = o;
@@ -599,12 +632,14 @@ __device__ __forceinline__ void wait_vm(int n) {
 // Stage S: selection from the published records (all workgroups identically).
 // ---------------------------------------------------------------------------
 constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
+static_assert(kStackMaxE + 1 <= kSelRec * kT, "every record has a thread in stage S");
 constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
 constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
   unsigned long long mc[64];    // keys at or above the sample threshold
   unsigned long long wup[kW];   // each wave's largest upper bound below it
+  float shm[kW];                // each wave's largest |shared hidden value|
   int nmc;
   double theta, mxd;
   int cand[kMaxK + 1];
@@ -645,10 +680,12 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ Routes rt;
   __shared__ __align__(16) signed char zero16[16];
-  __shared__ float s_misc[4];  // [0] sx of x
+  __shared__ float s_misc[4];  // [0] sx of x, [1] sx of the shared hidden vector
+  __shared__ int s_abort;      // a wait of this workgroup timed out or saw the abort word
   const int b = blockIdx.x;
-  const Lds S = lds_carve(smem, a0.Hp, a0.ngh);
+  const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_abort = 0;
 
   // clear the other parity set's counters and integer sums for the next call
   {
@@ -736,6 +773,26 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     lds_barrier();
     const RLayout rl = r_layout(a.rslots, a.H, a.shkc);
     const float *rbuf = (const float *)(S.u + rl.rbuf);
+    // qrow_i8 of x (c/qwen.c:1696): sx = amax/127 (floor 1e-12), q = rint(x/sx)
+    float sx;
+    {
+      float amax = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; w++) amax = fmaxf(amax, R.red[w]);
+      sx = amax / 127.0f;
+      if (sx < 1e-12f) sx = 1e-12f;
+      const float inv = 1.0f / sx;
+#pragma unroll
+      for (int c = 0; c < kNch; c++) {
+        const int e0 = 2048 * c + 4 * t;
+        if (c < a.nch && e0 < a.H) {
+          int q0 = (int)__builtin_rintf(xv[c].x * inv), q1 = (int)__builtin_rintf(xv[c].y * inv);
+          int q2 = (int)__builtin_rintf(xv[c].z * inv), q3 = (int)__builtin_rintf(xv[c].w * inv);
+          *(int *)(S.xq + e0) = (q0 & 255) | (q1 & 255) << 8 | (q2 & 255) << 16 | (q3 & 255) << 24;
+        }
+      }
+      if (t == 0) s_misc[0] = sx;
+    }
     // router pass 1: segment totals and |products|
     double Aacc[kRSlots];
 #pragma unroll
@@ -762,25 +819,36 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
     }
-    lds_barrier();
-    float sx;
+    lds_barrier();  // xq, segT complete
+    // shared gate/up task: exact int32 dots of 16 rows with xq; the sums go
+    // out first, so that they are in before this workgroup's records show the
+    // layer's tag (stage S reads them once it has seen every record)
+    const ShTask st = sh_task(a);
     {
-      float amax = 0.0f;
+      v4i cs = {0, 0, 0, 0};
+      if (st.valid) {
+        int k0, k1;
+        sh_wave_range(st, wave, k0, k1);
+        const signed char *arow = (const signed char *)(S.u + rl.sbuf) + (lane & 15) * rl.srow + (lane >> 4) * 16;
+        for (int kc = k0; kc < k1; kc++) {
+          const v4i av = *(const v4i *)(arow + (kc - st.kc0) * 64);
+          const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
+          cs = mfma_i8(av, bv, cs);
+        }
+        if ((lane & 15) == 0) {
 #pragma unroll
-      for (int w = 0; w < kW; w++) amax = fmaxf(amax, R.red[w]);
-      sx = amax / 127.0f;
-      if (sx < 1e-12f) sx = 1e-12f;
-      const float inv = 1.0f / sx;
-#pragma unroll
-      for (int c = 0; c < kNch; c++) {
-        const int e0 = 2048 * c + 4 * t;
-        if (c < a.nch && e0 < a.H) {
-          int q0 = (int)__builtin_rintf(xv[c].x * inv), q1 = (int)__builtin_rintf(xv[c].y * inv);
-          int q2 = (int)__builtin_rintf(xv[c].z * inv), q3 = (int)__builtin_rintf(xv[c].w * inv);
-          *(int *)(S.xq + e0) = (q0 & 255) | (q1 & 255) << 8 | (q2 & 255) << 16 | (q3 & 255) << 24;
+          for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
         }
       }
-      if (t == 0) s_misc[0] = sx;
+    }
+    lds_barrier();
+    unsigned dep_acc = 0;
+    if (wave == 0 && st.valid && lane >= 16 && lane < 32) {
+      const int r = lane - 16;
+      int v = 0;
+#pragma unroll
+      for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
+      dep_acc = (unsigned)atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], v);
     }
     // router pass 2: exact prefix sums -> sum |S_k|
 #pragma unroll
@@ -825,28 +893,12 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
     }
-    // shared gate/up task: exact int32 dots of 16 rows with xq
-    const ShTask st = sh_task(a);
-    lds_barrier();  // xq, segT, Ap/Pp complete
-    v4i cs = {0, 0, 0, 0};
-    if (st.valid) {
-      int k0, k1;
-      sh_wave_range(st, wave, k0, k1);
-      const signed char *arow = (const signed char *)(S.u + rl.sbuf) + (lane & 15) * rl.srow + (lane >> 4) * 16;
-      for (int kc = k0; kc < k1; kc++) {
-        const v4i av = *(const v4i *)(arow + (kc - st.kc0) * 64);
-        const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
-        cs = mfma_i8(av, bv, cs);
-      }
-      if ((lane & 15) == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
-      }
-    }
-    lds_barrier();
+    lds_barrier();  // Ap/Pp complete
     if (wave == 0) {
-      unsigned dep = 0;
-      // router records of this workgroup's rows: lanes 2s (logit), 2s+1 (bound)
+      published(dep_acc);
+      // router records of this workgroup's rows, lanes 2s (logit) and 2s+1
+      // (bound), tagged: the tag replaces the low 8 bits of each double, and
+      // the bound grows by more than the logit can move (2^-44 relative)
       if (lane < 2 * kRSlots) {
         const int s = lane >> 1;
         const int r = b + s * a.NB;
@@ -858,26 +910,24 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             A += R.Ap[s][w];
             P += R.Pp[s][w];
           }
-          const double B = 0x1p-24 * (A + P) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
-          dep ^= pub(&a.rec[2 * r + (lane & 1)], (lane & 1) ? B : Lg);
+          double B = 0x1p-24 * (A + P) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+          B = (B + fabs(Lg) * 0x1p-43) * (1.0 + 0x1p-40);
+          const double v = (lane & 1) ? B : Lg;
+          __hip_atomic_store((unsigned long long *)a.rec + 2 * r + (lane & 1),
+                             with_tag((unsigned long long)__double_as_longlong(v), layer_tag(a, l)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      if (st.valid && lane >= 16 && lane < 32) {
-        const int r = lane - 16;
-        int v = 0;
-#pragma unroll
-        for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
-        dep ^= (unsigned)atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], v);
-      }
-      published(dep);
     }
     stamp(a, l, 1);
-    lds_barrier();
-    if (t == 0) bar_arrive(bar_of(a, l, kBarLb), a.NB);
-    if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarLb), a) ? 1 : 0;
-    lds_barrier();
-    if (!rt.flag) return;
+    lds_barrier();  // stage R's LDS is reused below
     stamp(a, l, 2);
+
+    // stage G's waves: matrix m, groups [g0, g0+n) of x (n may be <= 0)
+    const int m = wave >> 2, qd = wave & 3;
+    const int per = (a.ngh + 3) / 4, g0 = qd * per;
+    const int n = (a.ngh < g0 + per ? a.ngh : g0 + per) - g0;
+    XOps xo;
 
     // ======================= stage S =======================
     {
@@ -888,15 +938,33 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int E = a.E, K = a.K;
       // records -> LDS, and this thread's keys (experts t + i*kT) in registers;
       // every load is issued before the first is used
+      const unsigned tag = layer_tag(a, l);
+      const unsigned long long *rec = (const unsigned long long *)a.rec;
+      unsigned long long rx[kSelRec], ry[kSelRec];
+#pragma unroll
+      for (int i = 0; i < kSelRec; i++) {
+        const int e = t + i * kT;
+        rx[i] = ry[i] = 0ull;
+        if (e <= E) {
+          rx[i] = ld_agent(rec + 2 * e);
+          ry[i] = ld_agent(rec + 2 * e + 1);
+        }
+      }
+      // stage G's activation operands from LDS while the records travel
+      xops_load<FMT>(xo, lane_digits(lane, 1, S.xd, a.Hp, S.xgp, a.ngh, zero16), g0, n, lane);
+      // records not yet tagged with this layer: read again until they are
       double lx[kSelRec], ly[kSelRec];
 #pragma unroll
       for (int i = 0; i < kSelRec; i++) {
         const int e = t + i * kT;
-        lx[i] = ly[i] = 0.0;
         if (e <= E) {
-          lx[i] = ld_agent(&a.rec[2 * e]);
-          ly[i] = ld_agent(&a.rec[2 * e + 1]);
+          bool ok = true;
+          if ((unsigned)(rx[i] & 0xFFull) != tag) ok = poll_tag64(rec + 2 * e, tag, rx[i], a);
+          if (ok && (unsigned)(ry[i] & 0xFFull) != tag) ok = poll_tag64(rec + 2 * e + 1, tag, ry[i], a);
+          if (!ok) s_abort = 1;
         }
+        lx[i] = __longlong_as_double((long long)rx[i]);
+        ly[i] = __longlong_as_double((long long)ry[i]);
       }
       unsigned long long key[kSelRec];
 #pragma unroll
@@ -934,6 +1002,28 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (t == E - iE * kT) rt.sg = sigmoid_ref((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])));
       }
       lds_barrier();
+      if (s_abort) return;
+      // Every record of this layer is in, so every workgroup's shared gate/up
+      // sums are too (each adds them before tagging its records): waves 1..7
+      // load them now and build the shared hidden vector while wave 0 selects.
+      float *hsh = prod + (size_t)kRSlots * a.H;  // [Ish]
+      int ag[kShPT], au[kShPT];
+      float gsv[kShPT], usv[kShPT];
+      auto sh_load = [&](int i0) {
+#pragma unroll
+        for (int q = 0; q < kShPT; q++) {
+          const int i = i0 + q * kStThreads;
+          ag[q] = au[q] = 0;
+          gsv[q] = usv[q] = 0.0f;
+          if (i < a.Ish) {
+            ag[q] = ld_agent(&acc[i]);
+            au[q] = ld_agent(&acc[a.Ish + i]);
+            gsv[q] = L.gs[i];
+            usv[q] = L.us[i];
+          }
+        }
+      };
+      if (wave != 0) sh_load(t - 64);
       // T0, found by every wave: the sample with exactly K-1 larger ones
       unsigned long long T0;
       {
@@ -975,7 +1065,24 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (lane == 0) sel.wup[wave] = up;
       }
       lds_barrier();
-      if (wave == 0) {
+      if (wave != 0) {
+        // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
+        float hm = 0.0f;
+        for (int i0 = t - 64; i0 < a.Ish; i0 += kShPT * kStThreads) {
+          if (i0 != t - 64) sh_load(i0);
+#pragma unroll
+          for (int q = 0; q < kShPT; q++) {
+            const int i = i0 + q * kStThreads;
+            if (i < a.Ish) {
+              const float h = silu_ref((float)ag[q] * gsv[q] * sx) * ((float)au[q] * usv[q] * sx);
+              hsh[i] = h;
+              hm = fmaxf(hm, fabsf(h));
+            }
+          }
+        }
+        hm = wave_max_dpp(hm);
+        if (lane == 0) sel.shm[wave] = hm;
+      } else {
         const int M = sel.nmc;
         if (M > 64) {
           if (lane == 0) sel.state = 2;
@@ -1017,11 +1124,13 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
           if (ok) ok = klo - (mx + mxy) > -75.0;
           if (ok) {
-            const double ev = lane < K ? exp(v.x - mx) : 0.0;
-            const double den = wave_sum_dpp(ev);
+            // softmax over the K (lanes 0..15 hold them): fp32 suffices for
+            // the weights' 1e-5 tolerance
+            const float ev = lane < K ? __expf((float)(v.x - mx)) : 0.0f;
+            const float den = row16_sum(ev);
             if (lane < K) {
               rt.idx[lane] = ce;
-              rt.w[lane] = (float)(ev / den);
+              rt.w[lane] = ev / den;
             }
           } else {
             // the lowest lower bound among the K candidates
@@ -1038,6 +1147,17 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
       lds_barrier();
+      {
+        // qrow_i8 of the shared hidden vector (stage D's shared down operand)
+        float shx = 0.0f;
+#pragma unroll
+        for (int w = 1; w < kW; w++) shx = fmaxf(shx, sel.shm[w]);
+        shx = shx / 127.0f;
+        if (shx < 1e-12f) shx = 1e-12f;
+        const float hinv = 1.0f / shx;
+        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
+        if (t == 0) s_misc[1] = shx;
+      }
       if (sel.state == 1) {
         // Every expert whose upper bound reaches the lowest lower bound among
         // the K candidates (less a margin): the exact top K lies in this set,
@@ -1101,11 +1221,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
           const bool ok = __all(pair_ok) && ((double)sel.sl[K - 1] - mx > -75.0);
           if (ok) {
-            const double ev = lane < K ? exp((double)sel.sl[lane < K ? lane : 0] - mx) : 0.0;
-            const double den = wave_sum_dpp(ev);
+            const float ev = lane < K ? __expf((float)((double)sel.sl[lane < K ? lane : 0] - mx)) : 0.0f;
+            const float den = row16_sum(ev);
             if (lane < K) {
               rt.idx[lane] = sel.se[lane];
-              rt.w[lane] = (float)(ev / den);
+              rt.w[lane] = ev / den;
             }
           }
           if (lane == 0 && !ok) sel.state = 2;
@@ -1193,9 +1313,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       float(*red)[16] = (float(*)[16])S.u;                  // [2][kW][16] partials
       unsigned *stage = (unsigned *)(S.u + 2 * kW * 16 * 4);  // [kW][8] packed digits
       const int nU = a.K * a.nrt_i;
-      const int m = wave >> 2, qd = wave & 3;
-      const int per = (a.ngh + 3) / 4, g0 = qd * per;
-      const int n = (a.ngh < g0 + per ? a.ngh : g0 + per) - g0;  // this wave's groups (may be <= 0)
       constexpr int BPL = FMT == 4 ? 16 : 12;
       // Each wave streams its own tile-groups (its matrix, its groups, unit
       // after unit) through a ring of kGRing slots in LDS: one tile-group's
@@ -1206,9 +1323,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       unsigned char *ring = S.u + 2048 + (size_t)wave * kGRing * kSlotG;
       const int nunits = b < nU ? (nU - 1 - b) / a.NB + 1 : 0;
       const int nitems = n > 0 ? nunits * n : 0;
-      const DigitSrc src = lane_digits(lane, 1, S.xd, a.Hp, S.xgp, a.ngh, zero16);
-      XOps xo;
-      xops_load<FMT>(xo, src, g0, n, lane);
       // This wave's unit table, one unit per lane: byte offsets of the unit's
       // first tile-group of this wave's matrix and groups (an invalid route
       // reads the layer's first bytes instead; its results are discarded).
@@ -1382,15 +1496,25 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       lds_barrier();
       if (!rt.flag) return;
       stamp(a, l, 5);
+      if (l == a.n - 1 && wave == 0 && lane < kRSlots) {
+        // Every workgroup has passed this call's last selection, so no one
+        // reads the records any more: clear this workgroup's, so that a later
+        // call never meets a word left by an older one (records are read
+        // only where a call writes them, and tags repeat)
+        const int r = b + lane * a.NB;
+        if (lane < a.rslots && r <= a.E) {
+          __hip_atomic_store((unsigned long long *)a.rec + 2 * r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store((unsigned long long *)a.rec + 2 * r + 1, 0ull, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
 
-      // h records of every route -> LDS; shared hidden vector -> int8
+      // h records of every route -> LDS (every load issued before the first is used)
       unsigned *hrec = (unsigned *)(S.u + dl.hrec);  // [K][ngi*8][12]
-      float *hsh = (float *)(S.u + dl.hsh);          // [Ish]
-      signed char *hq = (signed char *)(S.u + dl.hq);
       float *part = (float *)(S.u + dl.part);        // [K][kW][16]
       int *shp = (int *)(S.u + dl.shp);              // [kW][16]
-      float *redm = (float *)(S.u + dl.redm);        // [kW]
-      // (every device-scope load of a batch is issued before the first is used)
+      const signed char *hq = S.hq;
+      const float shx = s_misc[1];
       const int n64 = a.K * a.ngi * 8 * kRecWords / 2;
       {
         unsigned long long hv[kHrecPT];
@@ -1408,41 +1532,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           ((unsigned long long *)hrec)[j] = ld_agent((const unsigned long long *)a.hd + j);
       }
       for (int i = t; i < kMaxK * kW * 16; i += kT) part[i] = 0.0f;
-      float hm = 0.0f;
-      for (int i0 = t; i0 < a.Ish; i0 += kShPT * kT) {
-        int ag[kShPT], au[kShPT];
-        float gsv[kShPT], usv[kShPT];
-#pragma unroll
-        for (int q = 0; q < kShPT; q++) {
-          const int i = i0 + q * kT < a.Ish ? i0 + q * kT : i0;
-          ag[q] = ld_agent(&acc[i]);
-          au[q] = ld_agent(&acc[a.Ish + i]);
-          gsv[q] = L.gs[i];
-          usv[q] = L.us[i];
-        }
-#pragma unroll
-        for (int q = 0; q < kShPT; q++) {
-          const int i = i0 + q * kT;
-          if (i < a.Ish) {
-            // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
-            const float h = silu_ref((float)ag[q] * gsv[q] * sx) * ((float)au[q] * usv[q] * sx);
-            hsh[i] = h;
-            hm = fmaxf(hm, fabsf(h));
-          }
-        }
-      }
-      hm = wave_max_dpp(hm);
-      if (lane == 0) redm[wave] = hm;
-      lds_barrier();
-      float shx = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kW; w++) shx = fmaxf(shx, redm[w]);
-      shx = shx / 127.0f;
-      if (shx < 1e-12f) shx = 1e-12f;
-      {
-        const float hinv = 1.0f / shx;
-        for (int i = t; i < a.Ish; i += kT) hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
-      }
 
       for (int tile = tile0; tile < ntiles; tile += a.NB) {
         if (tile != tile0) issue_down(tile);
@@ -1541,15 +1630,22 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
         }
         lds_barrier();
+        // each route's total over the waves, one (route, row) per thread, into
+        // the route's first partial row
+        for (int i = t; i < a.K * 16; i += kT) {
+          const int k = i >> 4, r = i & 15;
+          float v = 0.0f;
+#pragma unroll
+          for (int w = 0; w < kW; w++) v += part[(k * kW + w) * 16 + r];
+          part[k * kW * 16 + r] = v;
+        }
+        lds_barrier();
         if (t < kTileRows) {
           // moe_forward's combine: fma over k in route order, then shared * gate
           float out = 0.0f;
-          for (int k = 0; k < a.K; k++) {
-            float v = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kW; w++) v += part[(k * kW + w) * 16 + t];
-            out = __builtin_fmaf(v, rt.w[k], out);
-          }
+          for (int k = 0; k < kMaxK; k++)
+            if (k < a.K) out = __builtin_fmaf(part[k * kW * 16 + t], rt.w[k], out);
           int dot = 0;
 #pragma unroll
           for (int w = 0; w < kW; w++) dot += shp[w * 16 + t];
@@ -1609,7 +1705,7 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
 static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, int fmt, int rslots, int shkc) {
   const size_t rlay = r_layout(rslots, H, shkc).end;
   const size_t sel = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (size_t)E * 8 + 16 +
-                     (size_t)kRSlots * H * 4;
+                     (size_t)kRSlots * H * 4 + (size_t)Ish * 4;
   const size_t dst = d_layout(K, ngi, Ish, fmt).end;
   const int bpl = fmt == 4 ? 16 : 12;
   const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64);
@@ -1620,26 +1716,42 @@ static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, 
   return u;
 }
 
+// shared gate/up tasks: 16-row tiles of both matrices, each split into KQ
+// k-ranges; every task's workgroup must also own a router record (its tagged
+// records vouch for its shared sums)
+static int stack_kq(int NB, int H, int E, int Ish) {
+  const int nsh_rt = 2 * (Ish / kTileRows);
+  if (nsh_rt == 0) return 1;
+  int KQ = NB / nsh_rt;
+  if (KQ > (E + 1) / nsh_rt) KQ = (E + 1) / nsh_rt;
+  if (KQ > H / 64) KQ = H / 64;
+  return KQ < 1 ? 1 : KQ;
+}
+
 bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   const int NB = ctx->sm_count;
   const int H = s.hidden, E = s.experts, K = s.topk, I = s.intermediate, Ish = s.shared_intermediate;
   if (H > 2048 * kNch || H % 64 || K > kMaxK || K > E || I % 16 || Ish % 64 || Ish > kStackMaxIsh) return false;
   if ((E + 1 + NB - 1) / NB > kRSlots) return false;                 // router rows in registers
-  if (E > 2 * kT) return false;                                       // selection keys in registers
+  if (E > kStackMaxE) return false;                                   // selection keys in registers
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
   if (ngh > 32) return false;                                         // G: 8 groups per wave
   if ((K * (I / kTileRows) + NB - 1) / NB > 64) return false;         // G: one unit per lane
   const int Hp = ngh * kGroup;
   const int rslots = (E + 1 + NB - 1) / NB;
-  int KQ = NB / (2 * (Ish / kTileRows));
-  if (KQ < 1) KQ = 1;
-  if (KQ > H / 64) KQ = H / 64;
+  const int KQ = stack_kq(NB, H, E, Ish);
+  if (2 * (Ish / kTileRows) * KQ > E + 1) return false;              // tasks' workgroups own records
   const int shkc = (H / 64 + KQ - 1) / KQ;
   if ((size_t)rslots * H * 4 + (size_t)shkc * 1024 > (size_t)16 * kStRegs * kStThreads) return false;  // registers
   const size_t u = stack_union_bytes(E, H, K, ngh, ngi, Ish, s.expert_format, rslots, shkc);
-  return lds_fixed(Hp, ngh) + u + 1024 <= (size_t)ctx->shared_per_block;
+  return lds_fixed(Hp, ngh, Ish) + u + 1024 <= (size_t)ctx->shared_per_block;
 }
+
+// Scratch regions at offsets that no shape changes: a tagged word must never
+// land where another shape's untagged data (exact logits) was written.
+constexpr size_t kRecRegion = ((size_t)(kStackMaxE + 1) * 16 + 255) & ~(size_t)255;  // router records
+constexpr size_t kExRegion = ((size_t)kStackMaxE * 4 + 255) & ~(size_t)255;          // exact logits
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
@@ -1660,9 +1772,15 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
     ctx->stack_dirty_acc[0] = ctx->stack_dirty_acc[1] = 0;
   }
   const int ngi = (s.intermediate + kGroup - 1) / kGroup;
-  const size_t scratch = (size_t)(s.experts + 1) * 16 + 256 + (size_t)s.experts * 4 + 256 +
-                         (size_t)s.topk * ngi * 8 * kRecWords * 4;
+  const size_t scratch = kRecRegion + kExRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
+  const void *before = ctx->scratch[kScrStack];
   if (ensure_scratch(ctx, kScrStack, scratch, "MoE stack scratch allocation")) return -1;
+  if (ctx->scratch[kScrStack] != before) {
+    // tagged words are trusted by their low byte: fresh memory starts at zero
+    // (a tag is never 0)
+    hipError_t e = hipMemsetAsync(ctx->scratch[kScrStack], 0, ctx->scratch_cap[kScrStack], ctx->stream);
+    if (e != hipSuccess) return fail_hip("MoE stack scratch clear", e);
+  }
   if (!ctx->stack_abort) {
     hipError_t e = hipMalloc(&ctx->stack_abort, 256);
     if (e == hipSuccess) e = hipMemsetAsync(ctx->stack_abort, 0, 256, ctx->stream);
@@ -1719,6 +1837,8 @@ int stack_check_abort(ColiCuda *ctx) {
   const size_t per_layer = ((size_t)kBars * kBarWords + 2 * (size_t)kStackMaxIsh) * 2 * 4;
   (void)hipMemsetAsync(ctx->stack_sync, 0, per_layer * ctx->stack_cap_layers, ctx->stream);
   (void)hipMemsetAsync(ctx->stack_abort, 0, 256, ctx->stream);
+  if (ctx->scratch[kScrStack])  // tagged words an aborted call left behind
+    (void)hipMemsetAsync(ctx->scratch[kScrStack], 0, ctx->scratch_cap[kScrStack], ctx->stream);
   (void)hipStreamSynchronize(ctx->stream);
   ctx->stack_dirty[0] = ctx->stack_dirty[1] = 0;
   ctx->stack_dirty_acc[0] = ctx->stack_dirty_acc[1] = 0;
@@ -1761,9 +1881,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.NB = ctx->sm_count;
   a.rslots = (a.E + 1 + a.NB - 1) / a.NB;
   const int nsh_rt = 2 * (a.Ish / kTileRows);
-  int KQ = a.NB / nsh_rt;
-  if (KQ < 1) KQ = 1;
-  if (KQ > a.H / 64) KQ = a.H / 64;
+  const int KQ = stack_kq(a.NB, a.H, a.E, a.Ish);
   a.KQ = KQ;
   a.n_sh_tasks = nsh_rt * KQ;
   a.shkc = (a.H / 64 + KQ - 1) / KQ;
@@ -1775,13 +1893,14 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.route_w = route_weight;
   char *scr = (char *)ctx->scratch[kScrStack];
   a.rec = (double *)scr;
-  a.ex = (float *)(scr + (((size_t)(a.E + 1) * 16 + 255) & ~(size_t)255));
-  a.hd = (unsigned *)((char *)a.ex + (((size_t)a.E * 4 + 255) & ~(size_t)255));
+  a.ex = (float *)(scr + kRecRegion);
+  a.hd = (unsigned *)(scr + kRecRegion + kExRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
   a.acc = (int *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
   a.acc_stride = acc_words;
   a.parity = (int)(ctx->stack_epoch & 1);
+  a.tag0 = 1u + (unsigned)(ctx->stack_layers_run % 255u);
   const int op = a.parity ^ 1;
   a.zero_layers = ctx->stack_dirty[op];
   a.zero_acc_words = ctx->stack_dirty_acc[op];
@@ -1792,7 +1911,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.trace_words = ctx->stack_trace_words;
   const size_t Hp = (size_t)a.Hp;
   const size_t u = stack_union_bytes(a.E, a.H, a.K, a.ngh, a.ngi, a.Ish, a.fmt, a.rslots, a.shkc);
-  size_t lds = lds_fixed((int)Hp, a.ngh) + u;
+  size_t lds = lds_fixed((int)Hp, a.ngh, a.Ish) + u;
   // more than half of a CU's LDS: exactly one workgroup per CU
   const size_t one_per_cu = (size_t)ctx->shared_per_block / 2 + 1024;
   if (lds < one_per_cu) lds = one_per_cu;
@@ -1811,6 +1930,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   ctx->stack_dirty[a.parity] = n;
   ctx->stack_dirty_acc[a.parity] = 2 * a.Ish;
   ctx->stack_epoch++;
+  ctx->stack_layers_run += (unsigned long long)n;
   return 0;
 }
 

@@ -61,6 +61,7 @@ struct ColiCuda {
   int stack_cap_layers;
   int stack_dirty[2], stack_dirty_acc[2];
   unsigned long long stack_epoch;
+  unsigned long long stack_layers_run;  // layers of every call so far (tags of exchanged words)
   void *stack_table_dev;
   size_t stack_table_cap;
   void *stack_table_host;

@@ -8,6 +8,7 @@
 
 namespace sw {
 
+constexpr int kStackMaxE = 1024;    // experts per layer
 constexpr int kStackMaxK = 16;      // routes per token
 constexpr int kStackMaxIsh = 4096;  // shared intermediate (integer-sum block size)
 
