@@ -249,23 +249,19 @@ __device__ __forceinline__ unsigned layer_tag(const StackArgs &a, int l) {
 __device__ __forceinline__ unsigned long long with_tag(unsigned long long bits, unsigned tag) {
   return (bits & ~0xFFull) | tag;
 }
-// spins until *p shows the tag; false on abort or time-out (then every
-// workgroup leaves through the abort word)
-__device__ bool poll_tag64(const unsigned long long *p, unsigned tag, unsigned long long &v, const StackArgs &a) {
-  const long long t0 = (long long)wall_clock64();
-  for (unsigned it = 0;; it++) {
-    v = ld_agent(p);
-    if ((unsigned)(v & 0xFFull) == tag) return true;
-    if ((it & 31) == 31) {
-      if (ld_agent(a.abort_word)) return false;
-      if ((long long)wall_clock64() - t0 > a.spin_ticks) {
-        atomicMax(a.abort_word, 1u);
-        __hip_atomic_store(a.abort_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        return false;
-      }
-    }
-    __builtin_amdgcn_s_sleep(1);
+__device__ __forceinline__ bool has_tag(unsigned long long v, unsigned tag) { return (unsigned)(v & 0xFFull) == tag; }
+// A reader re-reads all of its words not yet tagged at once (one memory
+// round trip per round) until every one is.  Rounds are bounded: true when
+// the wait started at t0 must end (the abort word is set, or the time is up;
+// then every workgroup leaves through the abort word).
+__device__ bool wait_expired(long long t0, const StackArgs &a) {
+  if (ld_agent(a.abort_word)) return true;
+  if ((long long)wall_clock64() - t0 > a.spin_ticks) {
+    atomicMax(a.abort_word, 1u);
+    __hip_atomic_store(a.abort_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return true;
   }
+  return false;
 }
 
 // arrive: the workgroup's published words must have returned already
@@ -953,16 +949,31 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // stage G's activation operands from LDS while the records travel
       xops_load<FMT>(xo, lane_digits(lane, 1, S.xd, a.Hp, S.xgp, a.ngh, zero16), g0, n, lane);
       // records not yet tagged with this layer: read again until they are
+      {
+        const long long t0 = (long long)wall_clock64();
+        for (unsigned it = 0;; it++) {
+          bool all = true;
+#pragma unroll
+          for (int i = 0; i < kSelRec; i++)
+            if (t + i * kT <= E) all = all && has_tag(rx[i], tag) && has_tag(ry[i], tag);
+          if (all) break;
+          if ((it & 15) == 15 && wait_expired(t0, a)) {
+            s_abort = 1;
+            break;
+          }
+#pragma unroll
+          for (int i = 0; i < kSelRec; i++) {
+            const int e = t + i * kT;
+            if (e <= E) {
+              if (!has_tag(rx[i], tag)) rx[i] = ld_agent(rec + 2 * e);
+              if (!has_tag(ry[i], tag)) ry[i] = ld_agent(rec + 2 * e + 1);
+            }
+          }
+        }
+      }
       double lx[kSelRec], ly[kSelRec];
 #pragma unroll
       for (int i = 0; i < kSelRec; i++) {
-        const int e = t + i * kT;
-        if (e <= E) {
-          bool ok = true;
-          if ((unsigned)(rx[i] & 0xFFull) != tag) ok = poll_tag64(rec + 2 * e, tag, rx[i], a);
-          if (ok && (unsigned)(ry[i] & 0xFFull) != tag) ok = poll_tag64(rec + 2 * e + 1, tag, ry[i], a);
-          if (!ok) s_abort = 1;
-        }
         lx[i] = __longlong_as_double((long long)rx[i]);
         ly[i] = __longlong_as_double((long long)ry[i]);
       }
