@@ -8,8 +8,9 @@
 //      dot, c/qwen.c:1674) for the rows this workgroup owns (row r belongs to
 //      workgroup r % NB), one shared-expert gate/up IDOT task (exact int32
 //      dots, c/qwen.c:1696-1705, summed over k-slices with integer atomics),
-//      and the activation digits of x for the routed GEMV.
-//   -- barrier "lb": every router record and shared sum is published.
+//      and the activation digits of x for the routed GEMV.  Each workgroup's
+//      shared sums go out first; its router records follow, tagged with the
+//      layer (no barrier: readers read the records until all carry the tag).
 //   S  every workgroup selects the top-k itself from the published records
 //      (router_topk, c/qwen.c:3421-3426): certified by the bounds, else by
 //      the exact fp32 chains of the ambiguous experts (computed by the rows'
@@ -27,13 +28,15 @@
 // shared gate/up tile) are loaded into registers before the "y" barrier; the
 // down tiles of the selected experts are loaded before the "h" barrier.
 //
-// Cross-workgroup data is published with returning device-scope atomics and
+// Cross-workgroup data is published with device-scope stores and atomics and
 // read with device-scope loads; barriers are two-level counters (8 groups,
 // then one top counter).  Counters and integer sums come in two parity sets:
-// a call uses set p and clears set 1-p for the next call, so no call needs a
-// memset and the host keeps no device state beyond the parity.  Every wait is
-// bounded in wall-clock time: on expiry the kernel raises an abort flag, every
-// workgroup leaves, and the host reports the error at the next sync.
+// a call uses set p and clears set 1-p for the next call.  The call state
+// (parity, dirty extents, the running layer count behind the tags) lives in
+// device memory and is advanced by the kernel itself, so no call needs a
+// memset and a captured graph replays correctly.  Every wait is bounded in
+// wall-clock time: on expiry the kernel raises an abort flag, every workgroup
+// leaves, and the host reports the error at the next sync.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -84,6 +87,15 @@ struct LayerPtrs {
   int mode;
 };
 
+// Device-side call state: [0..1] layers run by every call so far (64-bit),
+// [2] the parity set this call uses, [3..4] layers and [5..6] integer-sum
+// words the last call of each parity dirtied.
+enum { kStLayersLo = 0, kStLayersHi, kStParity, kStDirtyN0, kStDirtyN1, kStDirtyAcc0, kStDirtyAcc1, kStWords };
+struct CallState {
+  int parity;
+  unsigned tag0;  // layer 0's tag (1..255) in the exchanged words
+};
+
 struct StackArgs {
   LayerRef one;                 // n == 1
   const SW_G LayerRef *table;   // n > 1
@@ -103,13 +115,10 @@ struct StackArgs {
   int *acc;             // [layer][parity][2*Ish]
   unsigned *bars;       // [layer][parity][kBars][kBarWords]
   size_t acc_stride;    // words per (layer, parity) acc block
-  int parity;
-  int zero_layers;      // layers of the other parity to clear
-  int zero_acc_words;
+  unsigned *state;      // call state, advanced by every call (StackState)
   unsigned *abort_word; // device
   unsigned *abort_host; // host-mapped status
   long long spin_ticks; // wall-clock budget of one wait (100 MHz ticks)
-  unsigned tag0;        // layer 0's tag (1..255) in the exchanged words
   unsigned long long *trace;  // optional stage stamps [layer][NB][kStamps]
   size_t trace_words;
 };
@@ -212,8 +221,8 @@ __device__ __forceinline__ LayerPtrs layer_ref(const StackArgs &a, int l) {
   p.mode = one ? a.one.mode : a.table[l].mode;
   return p;
 }
-__device__ __forceinline__ unsigned *bar_of(const StackArgs &a, int l, int which) {
-  return a.bars + ((size_t)(l * 2 + a.parity) * kBars + which) * kBarWords;
+__device__ __forceinline__ unsigned *bar_of(const StackArgs &a, const CallState &cs, int l, int which) {
+  return a.bars + ((size_t)(l * 2 + cs.parity) * kBars + which) * kBarWords;
 }
 
 // ---------------------------------------------------------------------------
@@ -243,8 +252,8 @@ __device__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) 
 // Between calls every tagged word is zero (never a tag): each call clears
 // what it wrote once no one reads it any more, fresh scratch is cleared, and
 // so is the scratch of an aborted call.
-__device__ __forceinline__ unsigned layer_tag(const StackArgs &a, int l) {
-  return 1u + (a.tag0 - 1u + (unsigned)l) % 255u;
+__device__ __forceinline__ unsigned layer_tag(const CallState &cs, int l) {
+  return 1u + (cs.tag0 - 1u + (unsigned)l) % 255u;
 }
 __device__ __forceinline__ unsigned long long with_tag(unsigned long long bits, unsigned tag) {
   return (bits & ~0xFFull) | tag;
@@ -657,10 +666,10 @@ struct Routes {  // result of stage S, in static LDS
   int flag;      // barrier result broadcast
 };
 
-__device__ bool sync_barrier(const StackArgs &a, int l, int which, Routes &rt) {
+__device__ bool sync_barrier(const StackArgs &a, const CallState &cs, int l, int which, Routes &rt) {
   lds_barrier();
   if (threadIdx.x == 0) {
-    unsigned *bar = bar_of(a, l, which);
+    unsigned *bar = bar_of(a, cs, l, which);
     bar_arrive(bar, a.NB);
     rt.flag = bar_wait(bar, a) ? 1 : 0;
   }
@@ -683,17 +692,32 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
 
+  // The call state, read by every workgroup before any of them can pass the
+  // first grid barrier (workgroup 0 advances it after the last one).
+  CallState cs;
+  unsigned long long layers_run;
+  int zero_layers, zero_acc_words;
+  {
+    unsigned v[kStWords];
+#pragma unroll
+    for (int i = 0; i < kStWords; i++) v[i] = __builtin_amdgcn_readfirstlane(ld_agent(a0.state + i));
+    layers_run = ((unsigned long long)v[kStLayersHi] << 32) | v[kStLayersLo];
+    cs.parity = (int)(v[kStParity] & 1u);
+    cs.tag0 = 1u + (unsigned)(layers_run % 255u);
+    zero_layers = (int)v[cs.parity ? kStDirtyN0 : kStDirtyN1];
+    zero_acc_words = (int)v[cs.parity ? kStDirtyAcc0 : kStDirtyAcc1];
+  }
   // clear the other parity set's counters and integer sums for the next call
   {
     const StackArgs &a = a0;
     const int t = threadIdx.x;
-    const int op = a.parity ^ 1;
+    const int op = cs.parity ^ 1;
     const size_t bw = (size_t)kBars * kBarWords;
-    for (int l = 0; l < a.zero_layers; l++) {
+    for (int l = 0; l < zero_layers; l++) {
       unsigned *bz = a.bars + (size_t)(l * 2 + op) * bw;
       for (size_t i = (size_t)b * kT + t; i < bw; i += (size_t)a.NB * kT) bz[i] = 0u;
       int *az = a.acc + (size_t)(l * 2 + op) * a.acc_stride;
-      for (size_t i = (size_t)b * kT + t; i < (size_t)a.zero_acc_words; i += (size_t)a.NB * kT) az[i] = 0;
+      for (size_t i = (size_t)b * kT + t; i < (size_t)zero_acc_words; i += (size_t)a.NB * kT) az[i] = 0;
     }
   }
 
@@ -709,7 +733,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const LayerPtrs L = layer_ref(a, l);
     const float *x = a.x + (size_t)l * a.xs;
-    int *acc = a.acc + (size_t)(l * 2 + a.parity) * a.acc_stride;
+    int *acc = a.acc + (size_t)(l * 2 + cs.parity) * a.acc_stride;
 
     // ======================= stage R =======================
     stamp(a, l, 0);
@@ -910,7 +934,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           B = (B + fabs(Lg) * 0x1p-43) * (1.0 + 0x1p-40);
           const double v = (lane & 1) ? B : Lg;
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r + (lane & 1),
-                             with_tag((unsigned long long)__double_as_longlong(v), layer_tag(a, l)), __ATOMIC_RELAXED,
+                             with_tag((unsigned long long)__double_as_longlong(v), layer_tag(cs, l)), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
       }
@@ -934,7 +958,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int E = a.E, K = a.K;
       // records -> LDS, and this thread's keys (experts t + i*kT) in registers;
       // every load is issued before the first is used
-      const unsigned tag = layer_tag(a, l);
+      const unsigned tag = layer_tag(cs, l);
       const unsigned long long *rec = (const unsigned long long *)a.rec;
       unsigned long long rx[kSelRec], ry[kSelRec];
 #pragma unroll
@@ -1206,7 +1230,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             published(dep);
           }
         }
-        if (!sync_barrier(a, l, kBarEx1, rt)) return;
+        if (!sync_barrier(a, cs, l, kBarEx1, rt)) return;
         if (wave == 0) {
           const int nm = sel.nm;
           const float lv = lane < nm ? ld_agent(&a.ex[sel.m[lane]]) : -__builtin_huge_valf();
@@ -1260,7 +1284,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             published(dep);
           }
         }
-        if (!sync_barrier(a, l, kBarEx2, rt)) return;
+        if (!sync_barrier(a, cs, l, kBarEx2, rt)) return;
         float *lgs = prod;  // [E]
         for (int e = t; e < E; e += kT) lgs[e] = ld_agent(&a.ex[e]);
         lds_barrier();
@@ -1501,9 +1525,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       };
       lds_barrier();
       stamp(a, l, 4);
-      if (t == 0) bar_arrive(bar_of(a, l, kBarH), a.NB);
+      if (t == 0) bar_arrive(bar_of(a, cs, l, kBarH), a.NB);
       if (tile0 < ntiles) issue_down(tile0);  // in flight across the barrier
-      if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarH), a) ? 1 : 0;
+      if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
       stamp(a, l, 5);
@@ -1518,6 +1542,18 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r + 1, 0ull, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
+      if (l == a.n - 1 && b == 0 && t == 0) {
+        // every workgroup has read the call state: advance it for the next call
+        const unsigned long long nl = layers_run + (unsigned long long)a.n;
+        const int p = cs.parity;
+        __hip_atomic_store(a.state + kStLayersLo, (unsigned)nl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.state + kStLayersHi, (unsigned)(nl >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.state + (p ? kStDirtyN1 : kStDirtyN0), (unsigned)a.n, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.state + (p ? kStDirtyAcc1 : kStDirtyAcc0), (unsigned)(2 * a.Ish), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.state + kStParity, (unsigned)(p ^ 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
 
       // h records of every route -> LDS (every load issued before the first is used)
@@ -1674,11 +1710,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     stamp(a, l, 6);
     if (l + 1 < a.n) {
       lds_barrier();
-      if (t == 0) bar_arrive(bar_of(a, l, kBarY), a.NB);
+      if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
       // waves 1..7: the next layer's stage R inputs, loaded while the grid
       // finishes this layer (the memory system is otherwise idle then)
       static_load(a, layer_ref(a, l + 1), sreg, t);
-      if (t == 0) rt.flag = bar_wait(bar_of(a, l, kBarY), a) ? 1 : 0;
+      if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarY), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
       stamp(a, l, 7);
@@ -1763,6 +1799,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
 // land where another shape's untagged data (exact logits) was written.
 constexpr size_t kRecRegion = ((size_t)(kStackMaxE + 1) * 16 + 255) & ~(size_t)255;  // router records
 constexpr size_t kExRegion = ((size_t)kStackMaxE * 4 + 255) & ~(size_t)255;          // exact logits
+constexpr size_t kStateRegion = 256;                                                  // call state
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
@@ -1779,17 +1816,17 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
     if (e == hipSuccess) e = hipMemsetAsync(ctx->stack_sync, 0, per_layer * cap, ctx->stream);
     if (e != hipSuccess) return fail_hip("MoE stack counter allocation", e);
     ctx->stack_cap_layers = cap;
-    ctx->stack_dirty[0] = ctx->stack_dirty[1] = 0;
-    ctx->stack_dirty_acc[0] = ctx->stack_dirty_acc[1] = 0;
   }
   const int ngi = (s.intermediate + kGroup - 1) / kGroup;
-  const size_t scratch = kRecRegion + kExRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
+  const size_t scratch = kRecRegion + kExRegion + kStateRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
   const void *before = ctx->scratch[kScrStack];
   if (ensure_scratch(ctx, kScrStack, scratch, "MoE stack scratch allocation")) return -1;
   if (ctx->scratch[kScrStack] != before) {
     // tagged words are trusted by their low byte: fresh memory starts at zero
-    // (a tag is never 0)
+    // (a tag is never 0); a fresh call state says nothing is dirty, so the
+    // counters and integer sums are cleared with it
     hipError_t e = hipMemsetAsync(ctx->scratch[kScrStack], 0, ctx->scratch_cap[kScrStack], ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(ctx->stack_sync, 0, per_layer * ctx->stack_cap_layers, ctx->stream);
     if (e != hipSuccess) return fail_hip("MoE stack scratch clear", e);
   }
   if (!ctx->stack_abort) {
@@ -1851,8 +1888,6 @@ int stack_check_abort(ColiCuda *ctx) {
   if (ctx->scratch[kScrStack])  // tagged words an aborted call left behind
     (void)hipMemsetAsync(ctx->scratch[kScrStack], 0, ctx->scratch_cap[kScrStack], ctx->stream);
   (void)hipStreamSynchronize(ctx->stream);
-  ctx->stack_dirty[0] = ctx->stack_dirty[1] = 0;
-  ctx->stack_dirty_acc[0] = ctx->stack_dirty_acc[1] = 0;
   return fail_arg("MoE stack step aborted: a grid barrier timed out (the kernel needs every workgroup "
                   "resident; another kernel may have held compute units)");
 }
@@ -1905,16 +1940,12 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   char *scr = (char *)ctx->scratch[kScrStack];
   a.rec = (double *)scr;
   a.ex = (float *)(scr + kRecRegion);
-  a.hd = (unsigned *)(scr + kRecRegion + kExRegion);
+  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
   a.acc = (int *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
   a.acc_stride = acc_words;
-  a.parity = (int)(ctx->stack_epoch & 1);
-  a.tag0 = 1u + (unsigned)(ctx->stack_layers_run % 255u);
-  const int op = a.parity ^ 1;
-  a.zero_layers = ctx->stack_dirty[op];
-  a.zero_acc_words = ctx->stack_dirty_acc[op];
+  a.state = (unsigned *)(scr + kRecRegion + kExRegion);
   a.abort_word = (unsigned *)ctx->stack_abort;
   a.abort_host = ctx->stack_abort_host_dev;
   a.spin_ticks = 200000000LL;  // 2 s of the 100 MHz wall clock
@@ -1938,10 +1969,6 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   if (e != hipSuccess) return fail_hip("MoE stack kernel attributes", e);
   int rc = launch_status("MoE stack step");
   if (rc) return rc;
-  ctx->stack_dirty[a.parity] = n;
-  ctx->stack_dirty_acc[a.parity] = 2 * a.Ish;
-  ctx->stack_epoch++;
-  ctx->stack_layers_run += (unsigned long long)n;
   return 0;
 }
 

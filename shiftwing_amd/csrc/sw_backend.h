@@ -56,12 +56,10 @@ struct ColiCuda {
   int moe_generic_only;  // single-token steps take the many-token kernels
   int moe_decode_mode;   // 0 persistent stack kernel (default), 1 three-kernel decode
   // persistent stack kernel (moe_stack.hip): counters / integer sums in two
-  // parity sets, the device layer table, the abort status
+  // parity sets (the call state that selects them is device-side), the
+  // device layer table, the abort status
   void *stack_sync;
   int stack_cap_layers;
-  int stack_dirty[2], stack_dirty_acc[2];
-  unsigned long long stack_epoch;
-  unsigned long long stack_layers_run;  // layers of every call so far (tags of exchanged words)
   void *stack_table_dev;
   size_t stack_table_cap;
   void *stack_table_host;
