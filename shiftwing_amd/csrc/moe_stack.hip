@@ -112,6 +112,7 @@ struct StackArgs {
   double *rec;          // [E+1][2] logit, bound
   float *ex;            // [E] exact logits
   unsigned *hd;         // [K][ngi*8][kRecWords]
+  unsigned long long *spl;  // [kSplitUnits][16][2] tagged half sums of split units
   int *acc;             // [layer][parity][2*Ish]
   unsigned *bars;       // [layer][parity][kBars][kBarWords]
   size_t acc_stride;    // words per (layer, parity) acc block
@@ -350,7 +351,7 @@ __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, i
 // (placed past everything stage G uses, since they are loaded before the "h"
 // barrier while stage G's buffers may still be read).
 struct DLayout {
-  size_t hrec, part, shp, dtile, dsh, end;
+  size_t hrec, part, shp, dtile, end;
 };
 __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   DLayout d;
@@ -362,10 +363,9 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   };
   const size_t bpl = fmt == 4 ? 16 : 12;
   d.hrec = take((size_t)K * ngi * 8 * kRecWords * 4);
-  d.part = take((size_t)kMaxK * kW * 16 * 4);
+  d.part = take((size_t)kW * 16 * 4);
   d.shp = take((size_t)kW * 16 * 4);
   d.dtile = take((size_t)K * ngi * (64 * bpl + 64));
-  d.dsh = take((size_t)kTileRows * (Ish + 16));
   d.end = o;
   return d;
 }
@@ -638,7 +638,8 @@ __device__ __forceinline__ void wait_vm(int n) {
 // ---------------------------------------------------------------------------
 constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
 static_assert(kStackMaxE + 1 <= kSelRec * kT, "every record has a thread in stage S");
-constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
+constexpr int kHrecPT = 8;
+constexpr int kSplitUnits = 128;  // units of the last round that may be split in halves  // h-record words (64-bit) per thread loaded in one batch
 constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
@@ -1356,52 +1357,102 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // wave that issues them.
       constexpr int kSlotG = 64 * BPL + 64;
       unsigned char *ring = S.u + 2048 + (size_t)wave * kGRing * kSlotG;
-      const int nunits = b < nU ? (nU - 1 - b) / a.NB + 1 : 0;
-      const int nitems = n > 0 ? nunits * n : 0;
-      // This wave's unit table, one unit per lane: byte offsets of the unit's
-      // first tile-group of this wave's matrix and groups (an invalid route
-      // reads the layer's first bytes instead; its results are discarded).
+      // Units go round-robin over the workgroups.  When the last round would
+      // leave half of them idle (nU % NB <= NB/2), its units are split in two
+      // halves of every wave's groups, on workgroups 2k and 2k+1: each does
+      // its half first; 2k+1 publishes its partial sums (tagged words) and 2k
+      // adds them to its own at the end and builds the unit's record.
+      const int F = nU / a.NB, remu = nU - F * a.NB;
+      const bool split = remu > 0 && 2 * remu <= a.NB && remu <= kSplitUnits && a.ngh % 8 == 0;
+      const bool has_half = split && b < 2 * remu;
+      const int half = b & 1, hu = F * a.NB + (b >> 1);
+      const int nfull = split ? F : (b < nU ? (nU - 1 - b) / a.NB + 1 : 0);
+      const int nent = nfull + (has_half ? 1 : 0);
+      const int nh = n / 2, hlo = half ? nh : 0;  // the half: groups [hlo, hlo + nh) of the wave's
+      auto ent_unit = [&](int e_) { return has_half ? (e_ == 0 ? hu : b + (e_ - 1) * a.NB) : b + e_ * a.NB; };
+      auto ent_len = [&](int e_) { return (has_half && e_ == 0) ? nh : n; };
+      const int nitems = n > 0 ? nfull * n + (has_half ? nh : 0) : 0;
+      // This wave's unit table, one entry per lane: byte offsets of the
+      // entry's first tile-group of this wave's matrix and groups (an invalid
+      // route reads the layer's first bytes instead; its results are discarded).
       unsigned long long tc = 0ull, ts = 0ull;
-      if (lane < nunits) {
-        const int u = b + lane * a.NB, j = u / a.nrt_i, r16 = u - j * a.nrt_i;
+      if (lane < nent) {
+        const int u = ent_unit(lane), j = u / a.nrt_i, r16 = u - j * a.nrt_i;
         const int e = rt.idx[j];
         if ((unsigned)e < (unsigned)a.E) {
-          const size_t tg = (size_t)r16 * a.ngh + g0;
+          const size_t tg = (size_t)r16 * a.ngh + g0 + ((has_half && lane == 0) ? hlo : 0);
           tc = (size_t)e * a.expert_codes + (size_t)m * a.gate_codes + tg * 64 * BPL;
           ts = ((size_t)e * a.expert_scales + (size_t)m * a.gate_scales + tg * kTileRows) * 4;
         }
       }
-      // Issue cursor (unit iu, group gu, ring slot su).  Every step issues the
+      // Issue cursor (entry iu, group gu, ring slot su).  Every step issues the
       // two copies of one tile-group; past the last item it keeps re-reading
-      // the last unit's groups (in bounds, never consumed), so that exactly
+      // the last entry's groups (in bounds, never consumed), so that exactly
       // kGRing-1 items are always in flight and one wait count serves all.
-      int iu = 0, gu = 0, su = 0;
+      int iu = 0, gu = 0, su = 0, glen = ent_len(0);
       const unsigned char *cb = (const unsigned char *)L.codes, *sbp = (const unsigned char *)L.scales;
       auto unit_base = [&](int i) {
-        const int ii = i < nunits ? i : nunits - 1;
+        const int ii = i < nent ? i : nent - 1;
         const unsigned lo_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)tc, ii);
         const unsigned hi_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(tc >> 32), ii);
         const unsigned lo_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)ts, ii);
         const unsigned hi_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(ts >> 32), ii);
         cb = (const unsigned char *)L.codes + (((unsigned long long)hi_c << 32) | lo_c);
         sbp = (const unsigned char *)L.scales + (((unsigned long long)hi_s << 32) | lo_s);
+        glen = ent_len(ii);
       };
       auto issue_next = [&]() {
         const unsigned slot = lds_addr(ring + su * kSlotG);
         if (16 * lane < 64 * BPL) dma_b128_s(cb + gu * 64 * BPL, 16 * lane, slot);
         if (16 * lane < 64) dma_b128_s(sbp + gu * 64, 16 * lane, slot + 64 * BPL);
         if (++su == kGRing) su = 0;
-        if (++gu == n) {
+        if (++gu == glen) {
           gu = 0;
           unit_base(++iu);
         }
       };
-      // Partials of unit i go to red[i & 1]; after one barrier, wave i % 8
-      // builds h for the unit while the others go on to the next unit (the
-      // next unit's barrier keeps red[i & 1] until the finisher is done).
-      auto finish_unit = [&](float acc4[4], int u, int i) {
+      // h of 16 rows from their gate and up sums (lanes 0..15 of the calling
+      // wave): SwiGLU (c/qwen.c:3419), then two int8 digits per 16-value chunk
+      // (A = amax/127, B = A/254) and the record.  The hidden vector is
+      // quantised next, so the hardware exponential is within the tolerance.
+      auto finish_h = [&](float gsum, float usum, int u) {
         const int j = u / a.nrt_i, r16 = u % a.nrt_i;
         const int e = rt.idx[j];
+        const int r = lane;
+        float h = gsum / (1.0f + __expf(-gsum)) * usum;
+        if ((unsigned)e >= (unsigned)a.E || r16 * kTileRows + r >= a.I) h = 0.0f;
+        const float mm = row16_max(fabsf(h));
+        const float A = mm / 127.0f, B = A / 254.0f;
+        int q1 = 0, q2 = 0;
+        if (mm > 0.0f) {
+          const float invA = 127.0f / mm, invB = 254.0f / A;
+          q1 = (int)fminf(fmaxf(__builtin_rintf(h * invA), -127.0f), 127.0f);
+          const float rr2 = __builtin_fmaf(-(float)q1, A, h);
+          q2 = (int)fminf(fmaxf(__builtin_rintf(rr2 * invB), -127.0f), 127.0f);
+        }
+        const int s1 = row16_sum_i(q1), s2 = row16_sum_i(q2);
+        signed char *stg = (signed char *)(stage + 8 * wave);
+        stg[r] = (signed char)q1;
+        stg[16 + r] = (signed char)q2;
+        __builtin_amdgcn_wave_barrier();
+        unsigned v = 0;
+        if (r < 8) v = ((const unsigned *)stg)[r];
+        else if (r == 8) v = __float_as_uint(A);
+        else if (r == 9) v = __float_as_uint(B);
+        else if (r == 10) v = (unsigned)s1;
+        else if (r == 11) v = (unsigned)s2;
+        // a device-scope store: complete (and visible to every device-scope
+        // load) once vmcnt drains, which every wave waits for before the
+        // workgroup arrives at the barrier
+        if (r < kRecWords)
+          __hip_atomic_store(&a.hd[((size_t)j * a.ngi * 8 + r16) * kRecWords + r], v, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      };
+      // Partials of entry i go to red[i & 1]; after one barrier, wave i % 8
+      // finishes the entry while the others go on to the next one (the next
+      // entry's barrier keeps red[i & 1] until the finisher is done).
+      float gh = 0.0f, uh = 0.0f;  // the half's sums (wave 0, lanes 0..15)
+      auto finish_entry = [&](float acc4[4], int i) {
         float(*rb)[16] = red + (i & 1) * kW;
         digit_fold(acc4);
         if ((lane & 15) == 1) {
@@ -1413,65 +1464,94 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           const int r = lane;
           const float gsum = rb[0][r] + rb[1][r] + rb[2][r] + rb[3][r];
           const float usum = rb[4][r] + rb[5][r] + rb[6][r] + rb[7][r];
-          // SwiGLU (c/qwen.c:3419); the routed hidden vector is quantised next,
-          // so the hardware exponential is within the tolerance
-          float h = gsum / (1.0f + __expf(-gsum)) * usum;
-          if ((unsigned)e >= (unsigned)a.E || r16 * kTileRows + r >= a.I) h = 0.0f;
-          // two int8 digits of this 16-value chunk: A = amax/127, B = A/254
-          const float mm = row16_max(fabsf(h));
-          const float A = mm / 127.0f, B = A / 254.0f;
-          int q1 = 0, q2 = 0;
-          if (mm > 0.0f) {
-            const float invA = 127.0f / mm, invB = 254.0f / A;
-            q1 = (int)fminf(fmaxf(__builtin_rintf(h * invA), -127.0f), 127.0f);
-            const float rr2 = __builtin_fmaf(-(float)q1, A, h);
-            q2 = (int)fminf(fmaxf(__builtin_rintf(rr2 * invB), -127.0f), 127.0f);
+          if (has_half && i == 0) {
+            gh = gsum;
+            uh = usum;
+            if (half) {
+              unsigned long long *w = a.spl + ((size_t)(b >> 1) * 16 + r) * 2;
+              const unsigned long long tg = (unsigned long long)layer_tag(cs, l) << 32;
+              __hip_atomic_store(w, tg | __float_as_uint(gsum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(w + 1, tg | __float_as_uint(usum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          } else {
+            finish_h(gsum, usum, ent_unit(i));
           }
-          const int s1 = row16_sum_i(q1), s2 = row16_sum_i(q2);
-          signed char *stg = (signed char *)(stage + 8 * wave);
-          stg[r] = (signed char)q1;
-          stg[16 + r] = (signed char)q2;
-          __builtin_amdgcn_wave_barrier();
-          unsigned v = 0;
-          if (r < 8) v = ((const unsigned *)stg)[r];
-          else if (r == 8) v = __float_as_uint(A);
-          else if (r == 9) v = __float_as_uint(B);
-          else if (r == 10) v = (unsigned)s1;
-          else if (r == 11) v = (unsigned)s2;
-          // a device-scope store: complete (and visible to every device-scope
-          // load) once vmcnt drains, which published() waits for before the
-          // workgroup arrives at the barrier
-          if (r < kRecWords)
-            __hip_atomic_store(&a.hd[((size_t)j * a.ngi * 8 + r16) * kRecWords + r], v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
         }
       };
+      // The shared expert's down rows of this workgroup's output tile go first
+      // in every wave's queue; they are multiplied with the shared hidden
+      // vector (built in stage S) once the routed work is done.
+      signed char *gdsh = (signed char *)(ring - (size_t)wave * kGRing * kSlotG + (size_t)kW * kGRing * kSlotG);
+      const int tile = b, ntiles = a.H / kTileRows;
+      if (tile < ntiles)
+        for (int r = wave; r < kTileRows; r += kW)
+          for (int c0 = 0; c0 < a.Ish; c0 += 1024)
+            if (c0 + 16 * lane < a.Ish)
+              dma_b128(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane,
+                       lds_addr(gdsh + (size_t)r * (a.Ish + 16) + c0));
       if (nitems > 0) {
         unit_base(0);
 #pragma unroll
         for (int k = 0; k < kGRing - 1; k++) issue_next();
       }
-      int cs = 0;  // consume slot
-      for (int i = 0; i < nunits; i++) {
-        const int u = b + i * a.NB;
+      int csl = 0;  // consume slot
+      for (int i = 0; i < nent; i++) {
+        const int glo = (has_half && i == 0) ? hlo : 0, ghi = glo + ent_len(i);
         float acc4[4] = {0, 0, 0, 0};
         if (n > 0) {
 #pragma unroll
           for (int gi = 0; gi < kGMax; gi++)
-            if (gi < n) {
+            if (gi >= glo && gi < ghi) {
               issue_next();
               // this item's two copies are done once at most the 2(kGRing-1)
               // issued after them are outstanding (a wave's loads complete in
               // order; a store of finish_unit only makes the wait longer)
               asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (kGRing - 1)) : "memory");
-              g_item<FMT>(ring + cs * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
-              if (++cs == kGRing) cs = 0;
+              g_item<FMT>(ring + csl * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
+              if (++csl == kGRing) csl = 0;
             }
         }
-        finish_unit(acc4, u, i);
+        finish_entry(acc4, i);
+      }
+      if (has_half && !half && wave == 0 && lane < 16) {
+        // the partner's half of the split unit (published long ago: it was its
+        // first entry), added to this workgroup's in a fixed order
+        const unsigned long long *w = a.spl + ((size_t)(b >> 1) * 16 + lane) * 2;
+        const unsigned tag = layer_tag(cs, l);
+        unsigned long long vg = ld_agent(w), vu = ld_agent(w + 1);
+        const long long t0 = (long long)wall_clock64();
+        for (unsigned it = 0; (unsigned)(vg >> 32) != tag || (unsigned)(vu >> 32) != tag; it++) {
+          if ((it & 15) == 15 && wait_expired(t0, a)) {
+            s_abort = 1;
+            break;
+          }
+          vg = ld_agent(w);
+          vu = ld_agent(w + 1);
+        }
+        finish_h(gh + __uint_as_float((unsigned)vg), uh + __uint_as_float((unsigned)vu), hu);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the last item
-      lds_barrier();  // the last finisher is done with its partials
+      lds_barrier();  // the last finisher is done with its partials; every copy has landed
+      if (s_abort) return;
+      // shared down: exact int32 dots of the tile's 16 rows with hq, into
+      // stage D's shp (the ring is no longer read)
+      if (tile < ntiles) {
+        const DLayout dl = d_layout(a.K, a.ngi, a.Ish, FMT);
+        int *shp = (int *)(S.u + dl.shp);
+        const int nkd = a.Ish / 64, kb = lane >> 4;
+        const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
+        v4i cd = {0, 0, 0, 0};
+        const signed char *arow = gdsh + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
+        for (int kc = dk0; kc < dk1; kc++) {
+          const v4i av = *(const v4i *)(arow + kc * 64);
+          const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.hq + kc * 64 + kb * 16) : v4i{0, 0, 0, 0};
+          cd = mfma_i8(av, bv, cd);
+        }
+        if ((lane & 15) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) shp[wave * 16 + 4 * kb + i] = cd[i];
+        }
+      }
       // zero records of chunks past I inside the last group (only when I % 128 != 0)
       if (b == 0 && wave == 0) {
         const int pad = a.ngi * 8 - a.nrt_i;
@@ -1490,14 +1570,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       constexpr int BPL = FMT == 4 ? 16 : 12;
       constexpr int kSlot = 64 * BPL + 64;  // one tile-group: codes, then 16 row scales
       const int nq = a.K * a.ngi;
-      const int qa = wave * nq / kW, qb = (wave + 1) * nq / kW;
-      const int nkd = a.Ish / 64;
-      const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
-      const int tile0 = b, ntiles = a.H / kTileRows;
+      const int tile = b, ntiles = a.H / kTileRows;
       unsigned char *dtile = S.u + dl.dtile;
-      signed char *dsh = (signed char *)(S.u + dl.dsh);
-      // the tile's routed down tile-groups and shared down rows, straight into
-      // LDS, copied by waves 1..7 (wave 0 polls the barrier meanwhile)
+      // the tile's routed down tile-groups, straight into LDS, copied by waves
+      // 1..7 (wave 0 polls the barrier meanwhile)
       auto issue_down = [&](int tile) {
         if (wave == 0) return;
         for (int q = wave - 1; q < nq; q += kW - 1) {
@@ -1517,16 +1593,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           if (lane < kTileRows)
             dma_b32(L.scales + (size_t)e * a.expert_scales + 2 * a.gate_scales + tg * kTileRows + lane, slot + 64 * BPL);
         }
-        for (int r = wave - 1; r < kTileRows; r += kW - 1)
-          for (int c0 = 0; c0 < a.Ish; c0 += 1024)
-            if (c0 + 16 * lane < a.Ish)
-              dma_b128(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane,
-                       lds_addr(dsh + (size_t)r * (a.Ish + 16) + c0));
       };
       lds_barrier();
       stamp(a, l, 4);
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarH), a.NB);
-      if (tile0 < ntiles) issue_down(tile0);  // in flight across the barrier
+      if (tile < ntiles) issue_down(tile);  // in flight across the barrier
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
@@ -1542,6 +1613,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r + 1, 0ull, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
+      if (l == a.n - 1 && wave == 0 && lane < 32 && (b & 1) == 0 && (b >> 1) < kSplitUnits) {
+        // the split units' half sums (read by this workgroup only): cleared too
+        __hip_atomic_store(a.spl + (size_t)(b >> 1) * 32 + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (l == a.n - 1 && b == 0 && t == 0) {
         // every workgroup has read the call state: advance it for the next call
@@ -1560,7 +1635,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       unsigned *hrec = (unsigned *)(S.u + dl.hrec);  // [K][ngi*8][12]
       float *part = (float *)(S.u + dl.part);        // [K][kW][16]
       int *shp = (int *)(S.u + dl.shp);              // [kW][16]
-      const signed char *hq = S.hq;
       const float shx = s_misc[1];
       const int n64 = a.K * a.ngi * 8 * kRecWords / 2;
       {
@@ -1578,10 +1652,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int j = t + kHrecPT * kT; j < n64; j += kT)
           ((unsigned long long *)hrec)[j] = ld_agent((const unsigned long long *)a.hd + j);
       }
-      for (int i = t; i < kMaxK * kW * 16; i += kT) part[i] = 0.0f;
 
-      for (int tile = tile0; tile < ntiles; tile += a.NB) {
-        if (tile != tile0) issue_down(tile);
+      if (tile < ntiles) {
         wait_dma();     // this wave's LDS copies have landed
         lds_barrier();  // ... and every other wave's
         constexpr int OFF = FMT == 4 ? 8 : 4;
@@ -1590,17 +1662,18 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         const bool hi = c >= 8 && ((c - 8) >> 1) == kb;
         const int chb = lo ? kb : 4 + kb;
         // routed: per tile-group two MFMAs; B column c = (chunk c>>1, digit c&1).
-        // The next tile-group's LDS operands are read while this one computes.
+        // Wave w takes the tile-groups q = j*ngi + g with q % kW == w, and
+        // folds each one's route weight into its row scales (the combine's
+        // sum over routes, per wave).  Items go in pairs, both pairs' LDS
+        // operands read before either is computed.
         struct DOps {
           TileWord<FMT> cw;
           v4f s4;
           v4i dv;
-          float dscl, zq;
-          bool valid;
+          float dscl, zq, wk;
         };
-        auto load_ops = [&](DOps &o, int q, int jq, int gq) {
-          o.valid = (unsigned)rt.idx[jq] < (unsigned)a.E;
-          const unsigned char *tq = dtile + (size_t)q * kSlot;
+        auto load_ops = [&](DOps &o, int jq, int gq) {
+          const unsigned char *tq = dtile + (size_t)(jq * a.ngi + gq) * kSlot;
           if constexpr (FMT == 4) {
             const v4u v = *(const v4u *)(tq + 16 * lane);
             o.cw.w[0] = v.x;
@@ -1619,80 +1692,50 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           const unsigned *prm = rbase + (c >> 1) * kRecWords + 8;
           o.dscl = __uint_as_float(prm[c & 1]);
           o.zq = (float)(OFF * (int)prm[2 + (c & 1)]) * o.dscl;
+          // an invalid route (no expert) adds nothing
+          o.wk = (unsigned)rt.idx[jq] < (unsigned)a.E ? rt.w[jq] : 0.0f;
         };
-        float accr[4] = {0, 0, 0, 0};
-        int jn = qa / a.ngi, gn = qa % a.ngi;
-        int jcur = jn;
-        DOps cur, nxt;
-        if (qa < qb) load_ops(nxt, qa, jn, gn);
-        for (int q = qa; q < qb; q++) {
-          cur = nxt;
-          const int jq = jn;
-          if (++gn == a.ngi) {
-            gn = 0;
-            ++jn;
-          }
-          if (q + 1 < qb) load_ops(nxt, q + 1, jn, gn);
-          if (jq != jcur) {
+        float tot[4] = {0, 0, 0, 0};
+        auto compute = [&](const DOps &o) {
+          v4i a0, a1;
+          unpack_tile<FMT>(o.cw, a0, a1);
+          const v4i z = {0, 0, 0, 0};
+          v4i cc = {0, 0, 0, 0};
+          cc = mfma_i8(a0, lo ? o.dv : z, cc);
+          cc = mfma_i8(a1, hi ? o.dv : z, cc);
+          const float sv[4] = {o.s4.x * o.wk, o.s4.y * o.wk, o.s4.z * o.wk, o.s4.w * o.wk};
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-              const float v = row16_sum(accr[r]);
-              if (c == 0) part[(jcur * kW + wave) * 16 + 4 * kb + r] = v;
-              accr[r] = 0.0f;
-            }
-            jcur = jq;
-          }
-          if (cur.valid) {
-            v4i a0, a1;
-            unpack_tile<FMT>(cur.cw, a0, a1);
-            const v4i z = {0, 0, 0, 0};
-            v4i cc = {0, 0, 0, 0};
-            cc = mfma_i8(a0, lo ? cur.dv : z, cc);
-            cc = mfma_i8(a1, hi ? cur.dv : z, cc);
-            const float sv[4] = {cur.s4.x, cur.s4.y, cur.s4.z, cur.s4.w};
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-              accr[r] = __builtin_fmaf(__builtin_fmaf((float)cc[r], cur.dscl, -cur.zq), sv[r], accr[r]);
-          }
-        }
-        if (qa < qb) {
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float v = row16_sum(accr[r]);
-            if (c == 0) part[(jcur * kW + wave) * 16 + 4 * kb + r] = v;
-          }
-        }
-        // shared down: exact int32 dots of 16 rows (LDS) with hq
+          for (int r = 0; r < 4; r++) tot[r] = __builtin_fmaf(__builtin_fmaf((float)cc[r], o.dscl, -o.zq), sv[r], tot[r]);
+        };
+        // this wave's items, one per lane: item i is tile-group q = wave + kW*i
+        // (route q / ngi, group q % ngi)
+        const int nitw = nq > wave ? (nq - 1 - wave) / kW + 1 : 0;  // <= 64 (K*ngi <= 512)
+        int jl = 0, gl = 0;
         {
-          v4i cd = {0, 0, 0, 0};
-          const signed char *arow = dsh + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
-          for (int kc = dk0; kc < dk1; kc++) {
-            const v4i av = *(const v4i *)(arow + kc * 64);
-            const v4i bv = c == 0 ? *(const v4i *)(hq + kc * 64 + kb * 16) : v4i{0, 0, 0, 0};
-            cd = mfma_i8(av, bv, cd);
-          }
-          if (c == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) shp[wave * 16 + 4 * kb + i] = cd[i];
-          }
+          const int q = wave + kW * lane;
+          jl = q / a.ngi;
+          gl = q - jl * a.ngi;
         }
-        lds_barrier();
-        // each route's total over the waves, one (route, row) per thread, into
-        // the route's first partial row
-        for (int i = t; i < a.K * 16; i += kT) {
-          const int k = i >> 4, r = i & 15;
-          float v = 0.0f;
+        for (int i = 0; i < nitw; i += 2) {
+          DOps o0, o1;
+          const bool two = i + 1 < nitw;
+          load_ops(o0, __builtin_amdgcn_readlane(jl, i), __builtin_amdgcn_readlane(gl, i));
+          if (two) load_ops(o1, __builtin_amdgcn_readlane(jl, i + 1), __builtin_amdgcn_readlane(gl, i + 1));
+          compute(o0);
+          if (two) compute(o1);
+        }
 #pragma unroll
-          for (int w = 0; w < kW; w++) v += part[(k * kW + w) * 16 + r];
-          part[k * kW * 16 + r] = v;
+        for (int r = 0; r < 4; r++) {
+          const float v = row16_sum(tot[r]);
+          if (c == 0) part[wave * 16 + 4 * kb + r] = v;
         }
         lds_barrier();
         if (t < kTileRows) {
-          // moe_forward's combine: fma over k in route order, then shared * gate
+          // moe_forward's combine (routed sum, then fma(shared, gate)); the
+          // routed sum is taken per wave, then over the waves in order
           float out = 0.0f;
 #pragma unroll
-          for (int k = 0; k < kMaxK; k++)
-            if (k < a.K) out = __builtin_fmaf(part[k * kW * 16 + t], rt.w[k], out);
+          for (int w = 0; w < kW; w++) out += part[w * 16 + t];
           int dot = 0;
 #pragma unroll
           for (int w = 0; w < kW; w++) dot += shp[w * 16 + t];
@@ -1700,8 +1743,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
-        lds_barrier();
-        for (int i = t; i < kMaxK * kW * 16; i += kT) part[i] = 0.0f;
       }
       lds_barrier();
     }
@@ -1755,7 +1796,7 @@ static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, 
                      (size_t)kRSlots * H * 4 + (size_t)Ish * 4;
   const size_t dst = d_layout(K, ngi, Ish, fmt).end;
   const int bpl = fmt == 4 ? 16 : 12;
-  const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64);
+  const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64) + (size_t)kTileRows * (Ish + 16);
   size_t u = rlay;
   if (sel > u) u = sel;
   if (dst > u) u = dst;
@@ -1784,7 +1825,9 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
   if (ngh > 32) return false;                                         // G: 8 groups per wave
-  if ((K * (I / kTileRows) + NB - 1) / NB > 64) return false;         // G: one unit per lane
+  if (K * ngi > 64 * kW) return false;                                // D: one item per lane of a wave
+  if (H / kTileRows > NB) return false;                               // D: one output tile per workgroup
+  if ((K * (I / kTileRows) + NB - 1) / NB > 63) return false;         // G: one entry per lane (+1 split half)
   const int Hp = ngh * kGroup;
   const int rslots = (E + 1 + NB - 1) / NB;
   const int KQ = stack_kq(NB, H, E, Ish);
@@ -1800,6 +1843,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
 constexpr size_t kRecRegion = ((size_t)(kStackMaxE + 1) * 16 + 255) & ~(size_t)255;  // router records
 constexpr size_t kExRegion = ((size_t)kStackMaxE * 4 + 255) & ~(size_t)255;          // exact logits
 constexpr size_t kStateRegion = 256;                                                  // call state
+constexpr size_t kSplitRegion = (size_t)kSplitUnits * 16 * 2 * 8;                     // split units' half sums
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
@@ -1818,7 +1862,8 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
     ctx->stack_cap_layers = cap;
   }
   const int ngi = (s.intermediate + kGroup - 1) / kGroup;
-  const size_t scratch = kRecRegion + kExRegion + kStateRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
+  const size_t scratch =
+      kRecRegion + kExRegion + kStateRegion + kSplitRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
   const void *before = ctx->scratch[kScrStack];
   if (ensure_scratch(ctx, kScrStack, scratch, "MoE stack scratch allocation")) return -1;
   if (ctx->scratch[kScrStack] != before) {
@@ -1940,7 +1985,8 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   char *scr = (char *)ctx->scratch[kScrStack];
   a.rec = (double *)scr;
   a.ex = (float *)(scr + kRecRegion);
-  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion);
+  a.spl = (unsigned long long *)(scr + kRecRegion + kExRegion + kStateRegion);
+  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kSplitRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
   a.acc = (int *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
