@@ -62,6 +62,9 @@ constexpr int kLine = 32;        // words between counters (one 128-byte line)
 constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h, y
 constexpr int kBarWords = 9 * kLine;
 constexpr int kRecWords = 12;    // h chunk record: d1[16] d2[16] (8 words) | A B Q1 Q2
+constexpr int kGMax = 8;         // stage G: groups per wave and unit
+constexpr int kGRing = 6;        // stage G: ring slots per wave
+constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
 // Layer pointers as the kernel receives them: typed as device-global memory,
@@ -541,8 +544,6 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
 // stage (the wave always takes the same groups): the MFMA B operands of both
 // steps (column c = lane%16: digit c of token 0 for c < 2, zero otherwise)
 // and the group's digit scale and offset correction.
-constexpr int kGMax = 8;   // groups per wave and unit
-constexpr int kGRing = 6;  // stage G ring slots per wave
 struct XOps {
   v4i b0[kGMax], b1[kGMax];
   float dsc[kGMax], zq[kGMax];
@@ -638,8 +639,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 // ---------------------------------------------------------------------------
 constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
 static_assert(kStackMaxE + 1 <= kSelRec * kT, "every record has a thread in stage S");
-constexpr int kHrecPT = 8;
-constexpr int kSplitUnits = 128;  // units of the last round that may be split in halves  // h-record words (64-bit) per thread loaded in one batch
+constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
 constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
@@ -1572,32 +1572,27 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int nq = a.K * a.ngi;
       const int tile = b, ntiles = a.H / kTileRows;
       unsigned char *dtile = S.u + dl.dtile;
-      // the tile's routed down tile-groups, straight into LDS, copied by waves
-      // 1..7 (wave 0 polls the barrier meanwhile)
-      auto issue_down = [&](int tile) {
-        if (wave == 0) return;
-        for (int q = wave - 1; q < nq; q += kW - 1) {
-          const int j = q / a.ngi, g = q % a.ngi;
-          const int e = rt.idx[j];
-          if ((unsigned)e >= (unsigned)a.E) continue;
-          const size_t tg = (size_t)tile * a.ngi + g;
-          const unsigned char *src = L.codes + (size_t)e * a.expert_codes + 2 * a.gate_codes + (tg * 64 + lane) * BPL;
-          const unsigned slot = lds_addr(dtile + (size_t)q * kSlot);
-          if constexpr (FMT == 4) {
-            dma_b128(src, slot);
-          } else {
-            // three dword planes [3][64]: plane i holds word i of every lane's 12 bytes
-#pragma unroll
-            for (int i = 0; i < 3; i++) dma_b32(src + 4 * i, slot + 256 * i);
-          }
-          if (lane < kTileRows)
-            dma_b32(L.scales + (size_t)e * a.expert_scales + 2 * a.gate_scales + tg * kTileRows + lane, slot + 64 * BPL);
-        }
-      };
       lds_barrier();
       stamp(a, l, 4);
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarH), a.NB);
-      if (tile < ntiles) issue_down(tile);  // in flight across the barrier
+      // the tile's routed down tile-groups, straight into LDS, copied by waves
+      // 1..7 while the barrier completes (wave 0 polls it: a wave's loads
+      // return in order, so its poll waits behind no copy); 16 bytes per lane
+      // (12-byte copies are not reliable)
+      if (tile < ntiles && wave != 0) {
+        for (int q = wave - 1; q < nq; q += kW - 1) {
+          const int j = q / a.ngi, gq = q - j * a.ngi;
+          const int e = rt.idx[j];
+          if ((unsigned)e >= (unsigned)a.E) continue;
+          const size_t tg = (size_t)tile * a.ngi + gq;
+          const unsigned char *src = L.codes + (size_t)e * a.expert_codes + 2 * a.gate_codes + tg * 64 * BPL;
+          const unsigned char *ssrc = (const unsigned char *)(L.scales + (size_t)e * a.expert_scales +
+                                                              2 * a.gate_scales + tg * kTileRows);
+          const unsigned slot = lds_addr(dtile + (size_t)q * kSlot);
+          if (16 * lane < 64 * BPL) dma_b128(src + 16 * lane, slot);
+          if (16 * lane < 64) dma_b128(ssrc + 16 * lane, slot + 64 * BPL);
+        }
+      }
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
@@ -1681,10 +1676,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             o.cw.w[2] = v.z;
             o.cw.w[3] = v.w;
           } else {
-            const unsigned *wp = (const unsigned *)tq + lane;
+            const unsigned *wp = (const unsigned *)(tq + 12 * lane);
             o.cw.w[0] = wp[0];
-            o.cw.w[1] = wp[64];
-            o.cw.w[2] = wp[128];
+            o.cw.w[1] = wp[1];
+            o.cw.w[2] = wp[2];
           }
           o.s4 = *(const v4f *)(tq + 64 * BPL + 16 * kb);
           const unsigned *rbase = hrec + (size_t)(jq * a.ngi * 8 + gq * 8) * kRecWords;
