@@ -198,6 +198,10 @@ __device__ __forceinline__ void dma_b32(const void *gptr, unsigned base) {
 // the same copy from a wave-uniform base plus a per-lane 32-bit byte offset
 __device__ __forceinline__ void dma_b128_s(const void *sbase, unsigned voff, unsigned base) {
   base = __builtin_amdgcn_readfirstlane(base);
+  // the base is wave-uniform by construction; say so to the compiler
+  const unsigned long long sb = (unsigned long long)sbase;
+  sbase = (const void *)(((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(sb >> 32)) << 32) |
+                         (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)sb));
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(base)
                : "memory", "m0");
 }
@@ -373,6 +377,14 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   return d;
 }
 
+// Stage G's LDS (partials, staging, rings, shared down rows), from the
+// union's start.  The shared hidden vector, built in stage S and quantised
+// once stage G has started, lies past it.
+__host__ __device__ inline size_t g_region_end(int Ish, int fmt) {
+  const size_t bpl = fmt == 4 ? 16 : 12;
+  return 2048 + (size_t)kW * kGRing * (64 * bpl + 64) + (size_t)kTileRows * (Ish + 16);
+}
+
 // ---------------------------------------------------------------------------
 // Stage R
 // ---------------------------------------------------------------------------
@@ -524,16 +536,35 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
     }
   lds_barrier();
   if (lane == 0 && wave < kRSlots && (want & (1u << wave))) {
-    const float *p = prod + (size_t)wave * a.H;
+    // The chain is serial; what limits it is LDS latency, so products come
+    // in blocks of 32 read a block ahead of the adds (H % 64 == 0).
+    const v4f *p = (const v4f *)(prod + (size_t)wave * a.H);
+    constexpr int kB = 8;  // v4f per block
     float acc = 0.0f;
-    v4f nx = *(const v4f *)p;
-    for (int i = 0; i < a.H; i += 4) {
-      const v4f cur = nx;
-      if (i + 4 < a.H) nx = *(const v4f *)(p + i + 4);
-      acc = acc + cur.x;
-      acc = acc + cur.y;
-      acc = acc + cur.z;
-      acc = acc + cur.w;
+    v4f A[kB], B[kB];
+#pragma unroll
+    for (int k = 0; k < kB; k++) A[k] = p[k];
+    for (int i = 0; i < a.H / 4; i += 2 * kB) {
+#pragma unroll
+      for (int k = 0; k < kB; k++) B[k] = p[i + kB + k];
+#pragma unroll
+      for (int k = 0; k < kB; k++) {
+        acc = acc + A[k].x;
+        acc = acc + A[k].y;
+        acc = acc + A[k].z;
+        acc = acc + A[k].w;
+      }
+      if (i + 2 * kB < a.H / 4) {
+#pragma unroll
+        for (int k = 0; k < kB; k++) A[k] = p[i + 2 * kB + k];
+      }
+#pragma unroll
+      for (int k = 0; k < kB; k++) {
+        acc = acc + B[k].x;
+        acc = acc + B[k].y;
+        acc = acc + B[k].z;
+        acc = acc + B[k].w;
+      }
     }
     out[wave] = acc;
   }
@@ -645,11 +676,9 @@ struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
   unsigned long long mc[64];    // keys at or above the sample threshold
   unsigned long long wup[kW];   // each wave's largest upper bound below it
-  float shm[kW];                // each wave's largest |shared hidden value|
   int nmc;
   double theta, mxd;
   int cand[kMaxK + 1];
-  int state;      // 0 certified, 1 targeted exact, 2 full exact
   int nm;
   int m[kMaxAmbig];
   float exv[kMaxAmbig];
@@ -660,11 +689,23 @@ struct SelLds {
   float wsel[kMaxK];
 };
 
+// stage S's union layout: selection state, records, keys, exact-chain
+// products, then the shared hidden vector (past stage G's regions: it is
+// quantised after stage G has started copying)
+__host__ __device__ inline size_t s_hsh_offset(int E, int H, int Ish, int fmt) {
+  const size_t o = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (((size_t)E * 8 + 15) & ~(size_t)15) +
+                   (size_t)kRSlots * H * 4;
+  const size_t g = g_region_end(Ish, fmt);
+  return ((o > g ? o : g) + 15) & ~(size_t)15;
+}
+
 struct Routes {  // result of stage S, in static LDS
   int idx[kMaxK];
   float w[kMaxK];
-  float sg;      // sigmoid of the shared gate logit
-  int flag;      // barrier result broadcast
+  float sg;        // sigmoid of the shared gate logit
+  int flag;        // barrier result broadcast
+  int state;       // selection path: 0 certified, 1 targeted exact, 2 full exact
+  float shm[kW];   // each wave's largest |shared hidden value| (waves 1..7)
 };
 
 __device__ bool sync_barrier(const StackArgs &a, const CallState &cs, int l, int which, Routes &rt) {
@@ -1042,7 +1083,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // Every record of this layer is in, so every workgroup's shared gate/up
       // sums are too (each adds them before tagging its records): waves 1..7
       // load them now and build the shared hidden vector while wave 0 selects.
-      float *hsh = prod + (size_t)kRSlots * a.H;  // [Ish]
+      float *hsh = (float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));  // [Ish]
       int ag[kShPT], au[kShPT];
       float gsv[kShPT], usv[kShPT];
       auto sh_load = [&](int i0) {
@@ -1117,11 +1158,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
         }
         hm = wave_max_dpp(hm);
-        if (lane == 0) sel.shm[wave] = hm;
+        if (lane == 0) rt.shm[wave] = hm;
       } else {
         const int M = sel.nmc;
         if (M > 64) {
-          if (lane == 0) sel.state = 2;
+          if (lane == 0) rt.state = 2;
         } else {
           // rank of each candidate among the candidates
           const unsigned long long ck = lane < M ? sel.mc[lane] : 0ull;
@@ -1153,7 +1194,12 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           const double nx = dpp_row_shl1_d(v.x), ny = dpp_row_shl1_d(v.y);
           bool pair_ok = true;
           if (lane + 1 < K) pair_ok = vlo - (nx + ny) > order_margin(v.x, nx, mx);
-          bool ok = L.mode == 0 && __all(pair_ok);
+          // The set of K is certified by the K-th lower bound against every
+          // other expert's upper bound; their order by the pairs.  Without a
+          // route output (a stack call) the order only changes the rounding
+          // of the combine, so an uncertain order among a certified set is
+          // taken as is (the set and the weights are exact either way).
+          bool ok = L.mode == 0 && (__all(pair_ok) || (a.route_idx == nullptr && a.route_w == nullptr));
           if (ok && K < E) {
             const double up = key_double(upk);
             ok = klo - up > order_margin(kx, up, mx);
@@ -1179,22 +1225,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               sel.mxd = mx;
             }
           }
-          if (lane == 0) sel.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
+          if (lane == 0) rt.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
         }
       }
       lds_barrier();
-      {
-        // qrow_i8 of the shared hidden vector (stage D's shared down operand)
-        float shx = 0.0f;
-#pragma unroll
-        for (int w = 1; w < kW; w++) shx = fmaxf(shx, sel.shm[w]);
-        shx = shx / 127.0f;
-        if (shx < 1e-12f) shx = 1e-12f;
-        const float hinv = 1.0f / shx;
-        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
-        if (t == 0) s_misc[1] = shx;
-      }
-      if (sel.state == 1) {
+      if (rt.state == 1) {
         // Every expert whose upper bound reaches the lowest lower bound among
         // the K candidates (less a margin): the exact top K lies in this set,
         // since anything outside it is strictly below all K candidates.
@@ -1208,14 +1243,14 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
         }
         lds_barrier();
-        if (t == 0 && !(sel.nm <= kMaxAmbig && sel.nm >= K)) sel.state = 2;
+        if (t == 0 && !(sel.nm <= kMaxAmbig && sel.nm >= K)) rt.state = 2;
         lds_barrier();
       }
       if (b == 0 && t == 0) {
         atomicAdd(&L.stats[0], 1ull);
-        if (sel.state != 0) atomicAdd(&L.stats[1], 1ull);
+        if (rt.state != 0) atomicAdd(&L.stats[1], 1ull);
       }
-      if (sel.state == 1) {
+      if (rt.state == 1) {
         // exact chains of the ambiguous experts this workgroup owns
         unsigned want = 0;
         for (int i = 0; i < sel.nm; i++) {
@@ -1264,11 +1299,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               rt.w[lane] = ev / den;
             }
           }
-          if (lane == 0 && !ok) sel.state = 2;
+          if (lane == 0 && !ok) rt.state = 2;
         }
         lds_barrier();
       }
-      if (sel.state == 2) {
+      if (rt.state == 2) {
         // every expert's exact chain (owners compute theirs), then router_topk
         // (c/qwen.c:3421-3426) bit for bit: max, expf(l - max), the serial
         // denominator in expert order, division, K argmax rounds (lowest index
@@ -1340,7 +1375,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (a.route_idx) a.route_idx[t] = rt.idx[t];
         if (a.route_w) a.route_w[t] = rt.w[t];
       }
-      lds_barrier();  // the selection's LDS is reused below
+      // No barrier: the routes are in static LDS, the exact paths end with
+      // one, and after the last one nothing reads this stage's LDS but the
+      // shared hidden vector, which lies past stage G's regions.
     }
     stamp(a, l, 3);
 
@@ -1493,6 +1530,19 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         unit_base(0);
 #pragma unroll
         for (int k = 0; k < kGRing - 1; k++) issue_next();
+      }
+      {
+        // qrow_i8 of the shared hidden vector (operand of the shared down
+        // projection below), while the first copies are in flight
+        const float *hsh = (const float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));
+        float shx = 0.0f;
+#pragma unroll
+        for (int w = 1; w < kW; w++) shx = fmaxf(shx, rt.shm[w]);
+        shx = shx / 127.0f;
+        if (shx < 1e-12f) shx = 1e-12f;
+        const float hinv = 1.0f / shx;
+        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
+        if (t == 0) s_misc[1] = shx;
       }
       int csl = 0;  // consume slot
       for (int i = 0; i < nent; i++) {
@@ -1787,8 +1837,7 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
 // the selection's arrays, stage G's ring and stage D's layout.
 static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, int fmt, int rslots, int shkc) {
   const size_t rlay = r_layout(rslots, H, shkc).end;
-  const size_t sel = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (size_t)E * 8 + 16 +
-                     (size_t)kRSlots * H * 4 + (size_t)Ish * 4;
+  const size_t sel = s_hsh_offset(E, H, Ish, fmt) + (size_t)Ish * 4;
   const size_t dst = d_layout(K, ngi, Ish, fmt).end;
   const int bpl = fmt == 4 ? 16 : 12;
   const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64) + (size_t)kTileRows * (Ish + 16);
