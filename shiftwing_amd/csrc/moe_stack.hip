@@ -512,7 +512,7 @@ __device__ __forceinline__ void static_store(const StackArgs &a, const StaticReg
 }
 
 // The exact fp32 chain of the reference's dot() for the listed slots (rows
-// b + s*NB): products rn(x*w) written to LDS by every thread, then one lane per
+// b + s*NB): products rn(x*w) written to LDS by every thread, then one wave per
 // slot adds them in index order (H % 8 == 0: no fused tail).  Rows and x are
 // read again from memory: this path is rare, and keeping them in registers
 // through the selection would cost every stage after it.
@@ -535,38 +535,36 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
       }
     }
   lds_barrier();
-  if (lane == 0 && wave < kRSlots && (want & (1u << wave))) {
-    // The chain is serial; what limits it is LDS latency, so products come
-    // in blocks of 32 read a block ahead of the adds (H % 64 == 0).
+  if (wave < kRSlots && (want & (1u << wave))) {
+    // The chain is serial and its products wait in LDS: a whole wave reads
+    // 256 of them at a time (one v4f per lane, the next 256 in flight) and
+    // readlane feeds them to the adds in index order.  Few registers are
+    // held, so the long-lived state of the stages around this rare path is
+    // not pushed out of registers.
     const v4f *p = (const v4f *)(prod + (size_t)wave * a.H);
-    constexpr int kB = 8;  // v4f per block
+    const int nv = a.H / 4, nfull = nv & ~63;
     float acc = 0.0f;
-    v4f A[kB], B[kB];
+    v4f cur = nfull ? p[lane] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < nfull; i += 64) {
+      v4f nxt = cur;
+      if (i + 64 < nfull) nxt = p[i + 64 + lane];
 #pragma unroll
-    for (int k = 0; k < kB; k++) A[k] = p[k];
-    for (int i = 0; i < a.H / 4; i += 2 * kB) {
-#pragma unroll
-      for (int k = 0; k < kB; k++) B[k] = p[i + kB + k];
-#pragma unroll
-      for (int k = 0; k < kB; k++) {
-        acc = acc + A[k].x;
-        acc = acc + A[k].y;
-        acc = acc + A[k].z;
-        acc = acc + A[k].w;
+      for (int k = 0; k < 64; k++) {
+        acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.x), k));
+        acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.y), k));
+        acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.z), k));
+        acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.w), k));
       }
-      if (i + 2 * kB < a.H / 4) {
-#pragma unroll
-        for (int k = 0; k < kB; k++) A[k] = p[i + 2 * kB + k];
-      }
-#pragma unroll
-      for (int k = 0; k < kB; k++) {
-        acc = acc + B[k].x;
-        acc = acc + B[k].y;
-        acc = acc + B[k].z;
-        acc = acc + B[k].w;
-      }
+      cur = nxt;
     }
-    out[wave] = acc;
+    for (int i = nfull; i < nv; i++) {  // H % 256 != 0: the rest one by one
+      const v4f v = p[i];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+    }
+    if (lane == 0) out[wave] = acc;
   }
   lds_barrier();
 }
