@@ -415,6 +415,8 @@ __device__ __forceinline__ void sh_wave_range(const ShTask &t, int wave, int &k0
 
 struct RStageLds {
   double segT[kRSlots][kNch * 8];
+  double Lg[kRSlots];
+  double inc[kRSlots][kNch][kT];  // each thread's within-wave inclusive scan
   double Ap[kRSlots][kW], Pp[kRSlots][kW];
   float red[kW];
   int acc_i[kW][16];
@@ -853,7 +855,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       }
       if (t == 0) s_misc[0] = sx;
     }
-    // router pass 1: segment totals and |products|
+    // router pass 1: each wave's inclusive scan of its per-thread sums (kept
+    // for pass 2), segment totals, |products|
     double Aacc[kRSlots];
 #pragma unroll
     for (int s = 0; s < kRSlots; s++) {
@@ -873,8 +876,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               p3 = (double)xv[c].w * (double)w.w;
             }
             Aacc[s] += fabs(p0) + fabs(p1) + fabs(p2) + fabs(p3);
-            const double q = wave_sum_dpp(((p0 + p1) + p2) + p3);
-            if (lane == 0) R.segT[s][c * 8 + wave] = q;
+            const double inc = wave_inclusive_scan_d(((p0 + p1) + p2) + p3);
+            R.inc[s][c][t] = inc;
+            if (lane == 63) R.segT[s][c * 8 + wave] = inc;
           }
         }
       }
@@ -931,6 +935,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               const int hi_ = __builtin_amdgcn_readlane((int)__double2hiint(segi), sg - 1);
               carry = __hiloint2double(hi_, lo_);
             }
+            // the row's fp64 logit: the total over every segment
+            if (c == 0 && wave == 0 && lane == a.nch * 8 - 1) R.Lg[s] = segi;
             double p0 = 0, p1 = 0, p2 = 0, p3 = 0;
             if (e0 < a.H) {
               const v4f w = *(const v4f *)(rbuf + (size_t)s * a.H + e0);
@@ -940,8 +946,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               p3 = (double)xv[c].w * (double)w.w;
             }
             const double q0 = p0, q1 = q0 + p1, q2 = q1 + p2, q3 = q2 + p3;
-            const double inc = wave_inclusive_scan_d(q3);
-            const double pre = carry + (inc - q3);
+            const double pre = carry + (R.inc[s][c][t] - q3);
             if (e0 < a.H) P += fabs(pre + q0) + fabs(pre + q1) + fabs(pre + q2) + fabs(pre + q3);
           }
         }
@@ -963,8 +968,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         const int s = lane >> 1;
         const int r = b + s * a.NB;
         if (s < a.rslots && r <= a.E) {
-          double Lg = 0.0, A = 0.0, P = 0.0;
-          for (int k = 0; k < a.nch * 8; k++) Lg += R.segT[s][k];
+          const double Lg = R.Lg[s];
+          double A = 0.0, P = 0.0;
 #pragma unroll
           for (int w = 0; w < kW; w++) {
             A += R.Ap[s][w];
