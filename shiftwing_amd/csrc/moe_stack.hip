@@ -63,7 +63,7 @@ constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h,
 constexpr int kBarWords = 9 * kLine;
 constexpr int kRecWords = 12;    // h chunk record: d1[16] d2[16] (8 words) | A B Q1 Q2
 constexpr int kGMax = 8;         // stage G: groups per wave and unit
-constexpr int kGRing = 6;        // stage G: ring slots per wave
+constexpr int kGRing = 4;        // stage G: ring slots per wave
 constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
@@ -353,12 +353,11 @@ __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, i
   return s;
 }
 
-// Stage D's part of the stage-local union: h records, the shared hidden
-// vector, partial sums, then the LDS-loaded down tiles and shared down rows
-// (placed past everything stage G uses, since they are loaded before the "h"
-// barrier while stage G's buffers may still be read).
+// Stage D's part of the stage-local union: h records, partial sums, then the
+// LDS-loaded down tiles.  All of it is written only after a barrier that
+// every wave reaches once it is done with stage G's buffers.
 struct DLayout {
-  size_t hrec, part, shp, dtile, end;
+  size_t hrec, part, dtile, end;
 };
 __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   DLayout d;
@@ -371,7 +370,6 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   const size_t bpl = fmt == 4 ? 16 : 12;
   d.hrec = take((size_t)K * ngi * 8 * kRecWords * 4);
   d.part = take((size_t)kW * 16 * 4);
-  d.shp = take((size_t)kW * 16 * 4);
   d.dtile = take((size_t)K * ngi * (64 * bpl + 64));
   d.end = o;
   return d;
@@ -729,6 +727,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   __shared__ __align__(16) signed char zero16[16];
   __shared__ float s_misc[4];  // [0] sx of x, [1] sx of the shared hidden vector
   __shared__ int s_abort;      // a wait of this workgroup timed out or saw the abort word
+  // the shared down projection's per-wave int32 sums of this workgroup's
+  // output rows: written at the end of stage G while other waves may still
+  // read the shared down rows, so kept out of the stage-local union
+  __shared__ int s_shp[kW * 16];
   const int b = blockIdx.x;
   const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
@@ -1587,10 +1589,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       lds_barrier();  // the last finisher is done with its partials; every copy has landed
       if (s_abort) return;
       // shared down: exact int32 dots of the tile's 16 rows with hq, into
-      // stage D's shp (the ring is no longer read)
+      // s_shp (the ring is no longer read)
       if (tile < ntiles) {
-        const DLayout dl = d_layout(a.K, a.ngi, a.Ish, FMT);
-        int *shp = (int *)(S.u + dl.shp);
+        int *shp = s_shp;
         const int nkd = a.Ish / 64, kb = lane >> 4;
         const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
         v4i cd = {0, 0, 0, 0};
@@ -1682,7 +1683,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // h records of every route -> LDS (every load issued before the first is used)
       unsigned *hrec = (unsigned *)(S.u + dl.hrec);  // [K][ngi*8][12]
       float *part = (float *)(S.u + dl.part);        // [K][kW][16]
-      int *shp = (int *)(S.u + dl.shp);              // [kW][16]
+      const int *shp = s_shp;                        // [kW][16]
       const float shx = s_misc[1];
       const int n64 = a.K * a.ngi * 8 * kRecWords / 2;
       {
