@@ -39,6 +39,7 @@
 // leaves, and the host reports the error at the next sync.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -228,6 +229,33 @@ __device__ __forceinline__ LayerPtrs layer_ref(const StackArgs &a, int l) {
 #undef SW_FIELD
   p.mode = one ? a.one.mode : a.table[l].mode;
   return p;
+}
+// A layer's pointers as words in LDS (kept for this layer and the next one,
+// so that no stage waits on a load of the layer table): every lane reads the
+// same words, made scalar again.
+constexpr int kRefWords = (int)(sizeof(LayerRef) / 4);
+static_assert(sizeof(LayerRef) % 4 == 0 && kRefWords <= 64, "layer pointers: one word per lane of a wave");
+__device__ __forceinline__ LayerPtrs layer_ref_lds(const unsigned *w) {
+  auto u32 = [&](size_t off) { return (unsigned)__builtin_amdgcn_readfirstlane((int)w[off / 4]); };
+  auto p64 = [&](size_t off) { return ((unsigned long long)u32(off + 4) << 32) | u32(off); };
+  LayerPtrs p;
+  p.router = (const float *)p64(offsetof(LayerRef, router));
+  p.sgate = (const float *)p64(offsetof(LayerRef, sgate));
+  p.gq = (const signed char *)p64(offsetof(LayerRef, gq));
+  p.uq = (const signed char *)p64(offsetof(LayerRef, uq));
+  p.dq = (const signed char *)p64(offsetof(LayerRef, dq));
+  p.gs = (const float *)p64(offsetof(LayerRef, gs));
+  p.us = (const float *)p64(offsetof(LayerRef, us));
+  p.ds = (const float *)p64(offsetof(LayerRef, ds));
+  p.codes = (const unsigned char *)p64(offsetof(LayerRef, codes));
+  p.scales = (const float *)p64(offsetof(LayerRef, scales));
+  p.stats = (unsigned long long *)p64(offsetof(LayerRef, stats));
+  p.mode = (int)u32(offsetof(LayerRef, mode));
+  return p;
+}
+// word i of layer l's pointers from the kernel arguments or the layer table
+__device__ __forceinline__ unsigned layer_ref_word(const StackArgs &a, int l, int i) {
+  return a.n == 1 ? ((const unsigned *)&a.one)[i] : ((const SW_G unsigned *)(a.table + l))[i];
 }
 __device__ __forceinline__ unsigned *bar_of(const StackArgs &a, const CallState &cs, int l, int which) {
   return a.bars + ((size_t)(l * 2 + cs.parity) * kBars + which) * kBarWords;
@@ -731,6 +759,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   // output rows: written at the end of stage G while other waves may still
   // read the shared down rows, so kept out of the stage-local union
   __shared__ int s_shp[kW * 16];
+  __shared__ unsigned s_lref[2][kRefWords];  // layer l's pointers in s_lref[l & 1]
   const int b = blockIdx.x;
   const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
@@ -767,6 +796,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
   StaticRegs sreg;
   static_load(a0, layer_ref(a0, 0), sreg, threadIdx.x);
+  if (threadIdx.x < kRefWords) s_lref[0][threadIdx.x] = layer_ref_word(a0, 0, threadIdx.x);
+  lds_barrier();
 
   for (int l = 0; l < a0.n; l++) {
     // Lane indices are re-derived every layer: values hoisted out of the loop
@@ -775,7 +806,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     int t = (int)threadIdx.x;
     asm volatile("" : "+v"(t));
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const LayerPtrs L = layer_ref(a, l);
+    const LayerPtrs L = layer_ref_lds(s_lref[l & 1]);
+    // the next layer's pointers: loaded now by wave 7 (which waits on no
+    // memory before stage S), written to LDS once stage S is done
+    unsigned nref = 0;
+    if (l + 1 < a.n && t >= kT - 64 && t - (kT - 64) < kRefWords) nref = layer_ref_word(a, l + 1, t - (kT - 64));
     const float *x = a.x + (size_t)l * a.xs;
     int *acc = a.acc + (size_t)(l * 2 + cs.parity) * a.acc_stride;
 
@@ -1385,6 +1420,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // shared hidden vector, which lies past stage G's regions.
     }
     stamp(a, l, 3);
+    if (l + 1 < a.n && t >= kT - 64 && t - (kT - 64) < kRefWords) s_lref[(l + 1) & 1][t - (kT - 64)] = nref;
 
     // ======================= stage G =======================
     {
@@ -1701,6 +1737,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int j = t + kHrecPT * kT; j < n64; j += kT)
           ((unsigned long long *)hrec)[j] = ld_agent((const unsigned long long *)a.hd + j);
       }
+      // the shared down row scales of this workgroup's tile, for the combine
+      // (loaded after the records, so that waiting for those excludes them)
+      float dsr = 0.0f;
+      if (t < kTileRows && tile < ntiles) dsr = L.ds[tile * kTileRows + t];
 
       if (tile < ntiles) {
         wait_dma();     // this wave's LDS copies have landed
@@ -1788,7 +1828,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           int dot = 0;
 #pragma unroll
           for (int w = 0; w < kW; w++) dot += shp[w * 16 + t];
-          const float shv = (float)dot * L.ds[tile * kTileRows + t] * shx;
+          const float shv = (float)dot * dsr * shx;
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
@@ -1803,7 +1843,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
       // waves 1..7: the next layer's stage R inputs, loaded while the grid
       // finishes this layer (the memory system is otherwise idle then)
-      static_load(a, layer_ref(a, l + 1), sreg, t);
+      static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sreg, t);
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarY), a) ? 1 : 0;
       lds_barrier();
       if (!rt.flag) return;
