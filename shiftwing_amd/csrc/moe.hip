@@ -45,8 +45,6 @@ constexpr int kMaxTokensPerItem = 8;   // routed MFMA B columns: 8 tokens x 2 di
 constexpr int kSharedTokens = 16;      // shared IDOT B columns: 16 tokens
 constexpr int kMaxTokens = 2048;       // per call (bucketing LDS bitmap)
 
-inline int tile_bytes_per_lane(int fmt) { return fmt == 4 ? 16 : 12; }
-
 }  // namespace
 
 
@@ -71,8 +69,9 @@ __device__ inline int container_code(const unsigned char *row, int k, int cols, 
   return (int)((w >> shift) & 7u);
 }
 
-// one thread per (row tile, group, lane): container codes -> tile bytes
-__global__ void k_repack_codes(unsigned char *dst, const unsigned char *src, int rows, int cols, int rb,
+// one thread per (row tile, group, lane): container codes -> tile bytes of
+// the tile-group's record (record stride rs)
+__global__ void k_repack_codes(unsigned char *dst, unsigned rs, const unsigned char *src, int rows, int cols, int rb,
                                int ng, int fmt) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   long long total = (long long)(rows / kTileRows) * ng * 64;
@@ -95,7 +94,7 @@ __global__ void k_repack_codes(unsigned char *dst, const unsigned char *src, int
       for (int m = 0; m < 4; m++) v |= (uint32_t)(code[8 * i + m] | (code[8 * i + 4 + m] << 4)) << (8 * m);
       w[i] = v;
     }
-    uint32_t *d = (uint32_t *)(dst + tid * 16);
+    uint32_t *d = (uint32_t *)(dst + (size_t)tg * rs + lane * 16);
     d[0] = w[0];
     d[1] = w[1];
     d[2] = w[2];
@@ -110,15 +109,15 @@ __global__ void k_repack_codes(unsigned char *dst, const unsigned char *src, int
         L[j >> 2] |= (uint32_t)(c & 3) << (8 * m + 2 * (j & 3));
         H |= (uint32_t)((c >> 2) & 1) << (8 * m + j);
       }
-    uint32_t *d = (uint32_t *)(dst + tid * 12);
+    uint32_t *d = (uint32_t *)(dst + (size_t)tg * rs + lane * 12);
     d[0] = L[0];
     d[1] = L[1];
     d[2] = H;
   }
 }
 
-// scales [rows][ng] -> [rt][g][16]
-__global__ void k_repack_scales(float *dst, const float *src, int rows, int ng) {
+// scales [rows][ng] -> 16 per tile-group record, at byte so of the record
+__global__ void k_repack_scales(unsigned char *dst, unsigned rs, unsigned so, const float *src, int rows, int ng) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   long long total = (long long)rows * ng;
   if (tid >= total) return;
@@ -126,7 +125,7 @@ __global__ void k_repack_scales(float *dst, const float *src, int rows, int ng) 
   long long tg = tid >> 4;
   int g = (int)(tg % ng);
   int rt = (int)(tg / ng);
-  dst[tid] = src[(size_t)(rt * kTileRows + r) * ng + g];
+  ((float *)(dst + (size_t)tg * rs + so))[r] = src[(size_t)(rt * kTileRows + r) * ng + g];
 }
 
 // ---------------------------------------------------------------------------
@@ -152,15 +151,15 @@ __global__ void k_synth_normal(float *dst, size_t n, uint64_t key, float sigma, 
   if (i >= n) return;
   dst[i] = absolute ? sw_abs_normal_sigma(key, i, sigma) : sw_normal_sigma(key, i, sigma);
 }
-// tiled scales straight from the hash at their container index
-__global__ void k_synth_scales_tiled(float *dst, int rows, int ng, uint64_t key) {
+// tile-group scales straight from the hash at their container index
+__global__ void k_synth_scales_tiled(unsigned char *dst, unsigned rs, unsigned so, int rows, int ng, uint64_t key) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (tid >= (long long)rows * ng) return;
   int r = (int)(tid & 15);
   long long tg = tid >> 4;
   int g = (int)(tg % ng);
   int rt = (int)(tg / ng);
-  dst[tid] = sw_abs_normal_sigma(key, (uint64_t)(rt * kTileRows + r) * ng + g, 0.01f);
+  ((float *)(dst + (size_t)tg * rs + so))[r] = sw_abs_normal_sigma(key, (uint64_t)(rt * kTileRows + r) * ng + g, 0.01f);
 }
 
 inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -646,15 +645,14 @@ struct TokDigits {
 };
 
 template <int FMT>
-__device__ __forceinline__ void tile_gemv(const unsigned char *codes, const float *scales, int rt, int ng, int g0,
-                                          int g1, const signed char *dsrc, const float4 *gpsrc, float acc[4],
-                                          int lane) {
+__device__ __forceinline__ void tile_gemv(const TileMat &mat, int rt, int ng, int g0, int g1,
+                                          const signed char *dsrc, const float4 *gpsrc, float acc[4], int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
   constexpr int OFF = FMT == 4 ? 8 : 4;
   const int kb = lane >> 4;
   for (int g = g0; g < g1; g++) {
     v4i a0, a1;
-    unpack_tile<FMT>(codes + ((size_t)(rt * ng + g) * 64 + lane) * BPL, a0, a1);
+    unpack_tile<FMT>(tm_codes(mat, (size_t)rt * ng + g) + lane * BPL, a0, a1);
     v4i b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
     float dsc = 0.0f;
     int Q = 0;
@@ -671,7 +669,7 @@ __device__ __forceinline__ void tile_gemv(const unsigned char *codes, const floa
     v4i c = {0, 0, 0, 0};
     c = mfma_i8(a0, b0, c);
     c = mfma_i8(a1, b1, c);
-    float4 sc = *(const float4 *)(scales + (size_t)(rt * ng + g) * kTileRows + 4 * kb);
+    float4 sc = *(const float4 *)(tm_scales(mat, (size_t)rt * ng + g) + 4 * kb);
     float scv[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -771,8 +769,7 @@ __global__ void k_prep_hidden(Work w) {
 // then h = silu(g)*u per token.  grid (I/16, min(items bound, 1024)), 256 thr.
 // ---------------------------------------------------------------------------
 template <int FMT>
-__global__ void k_expert_gateup(Work w, const unsigned char *codes, const float *scales, size_t expert_codes,
-                                size_t expert_scales, size_t gate_codes, size_t gate_scales) {
+__global__ void k_expert_gateup(Work w, ExpertLayout xl) {
   __shared__ float part[4][2][64][4];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int rt = blockIdx.x;
@@ -791,13 +788,11 @@ __global__ void k_expert_gateup(Work w, const unsigned char *codes, const float 
     const signed char *dsrc;
     const float4 *gp;
     lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
-    const unsigned char *ce = codes + (size_t)e * expert_codes;
-    const float *se = scales + (size_t)e * expert_scales;
     int per = (w.ngh + 3) / 4, g0 = wave * per, g1 = min(w.ngh, g0 + per);
     float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
     if (g0 < g1) {
-      tile_gemv<FMT>(ce, se, rt, w.ngh, g0, g1, dsrc, gp, ag, lane);
-      tile_gemv<FMT>(ce + gate_codes, se + gate_scales, rt, w.ngh, g0, g1, dsrc, gp, au, lane);
+      tile_gemv<FMT>(xl.mat(e, 0), rt, w.ngh, g0, g1, dsrc, gp, ag, lane);
+      tile_gemv<FMT>(xl.mat(e, 1), rt, w.ngh, g0, g1, dsrc, gp, au, lane);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -827,9 +822,7 @@ __global__ void k_expert_gateup(Work w, const unsigned char *codes, const float 
 // shout[t][row].  grid (H/16, n_item_slots + ceil(T/16)), 64 threads.
 // ---------------------------------------------------------------------------
 template <int FMT>
-__global__ void k_down(Work w, const unsigned char *codes, const float *scales, size_t expert_codes,
-                       size_t expert_scales, size_t down_codes_off, size_t down_scales_off, int item_slots,
-                       const signed char *dq, const float *ds) {
+__global__ void k_down(Work w, ExpertLayout xl, int item_slots, const signed char *dq, const float *ds) {
   int lane = threadIdx.x;
   int rt = blockIdx.x;
   int kb = lane >> 4;
@@ -863,8 +856,7 @@ __global__ void k_down(Work w, const unsigned char *codes, const float *scales, 
     const float4 *gp;
     lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
     float acc[4] = {0, 0, 0, 0};
-    tile_gemv<FMT>(codes + (size_t)e * expert_codes + down_codes_off,
-                   scales + (size_t)e * expert_scales + down_scales_off, rt, w.ngi, 0, w.ngi, dsrc, gp, acc, lane);
+    tile_gemv<FMT>(xl.mat(e, 2), rt, w.ngi, 0, w.ngi, dsrc, gp, acc, lane);
     if ((lane & 1) && ((lane & 15) >> 1) < cnt) {
       int tt = (lane & 15) >> 1;
 #pragma unroll
@@ -937,15 +929,9 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   if (!L) return fail_arg("out of memory creating MoE layer");
   L->sh = *s;
   int H = s->hidden, I = s->intermediate, E = s->experts, Ish = s->shared_intermediate;
-  int bpl = tile_bytes_per_lane(s->expert_format);
   L->ngh = (H + kGroup - 1) / kGroup;
   L->ngi = (I + kGroup - 1) / kGroup;
-  L->gate_codes = (size_t)(I / kTileRows) * L->ngh * 64 * bpl;
-  L->down_codes = (size_t)(H / kTileRows) * L->ngi * 64 * bpl;
-  L->gate_scales = (size_t)I * L->ngh;
-  L->down_scales = (size_t)H * L->ngi;
-  L->expert_codes = 2 * L->gate_codes + L->down_codes;
-  L->expert_scales = 2 * L->gate_scales + L->down_scales;
+  L->xl = expert_layout(nullptr, H, I, s->expert_format);
   int rc = layer_alloc(L, (void **)&L->router, (size_t)E * H * 4, "router allocation") ||
            layer_alloc(L, (void **)&L->sgate_row, (size_t)H * 4, "shared gate allocation") ||
            layer_alloc(L, (void **)&L->sh_gq, (size_t)Ish * H, "shared gate allocation") ||
@@ -954,8 +940,7 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
            layer_alloc(L, (void **)&L->sh_gs, (size_t)Ish * 4, "shared scale allocation") ||
            layer_alloc(L, (void **)&L->sh_us, (size_t)Ish * 4, "shared scale allocation") ||
            layer_alloc(L, (void **)&L->sh_ds, (size_t)H * 4, "shared scale allocation") ||
-           layer_alloc(L, (void **)&L->codes, (size_t)E * L->expert_codes, "expert code allocation") ||
-           layer_alloc(L, (void **)&L->scales, (size_t)E * L->expert_scales * 4, "expert scale allocation") ||
+           layer_alloc(L, (void **)&L->experts, (size_t)E * L->xl.expert_bytes, "expert allocation") ||
            layer_alloc(L, (void **)&L->stats, 64, "router stats allocation");
   L->sync_words = decode_sync_words(*s);
   rc = rc || layer_alloc(L, (void **)&L->sync, L->sync_words * 4, "decode counter allocation");
@@ -963,6 +948,7 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
     coli_cuda_moe_layer_destroy(ctx, L);
     return -1;
   }
+  L->xl.base = L->experts;
   k_zero_u32<<<blocks_for(16, 256), 256, 0, ctx->stream>>>((unsigned *)L->stats, 16);
   k_zero_u32<<<blocks_for(L->sync_words, 256), 256, 0, ctx->stream>>>(L->sync, L->sync_words);
   *out = L;
@@ -1011,14 +997,15 @@ extern "C" int coli_cuda_moe_layer_set_shared_q8(ColiCuda *ctx, ColiMoeLayer *L,
   return launch_status("coli_cuda_moe_layer_set_shared_q8");
 }
 
-static int repack_matrix(ColiCuda *ctx, unsigned char *dst_codes, float *dst_scales, const unsigned char *q,
-                         const float *s, int rows, int cols, int fmt) {
+static int repack_matrix(ColiCuda *ctx, const TileMat &dst, const unsigned char *q, const float *s, int rows,
+                         int cols, int fmt) {
   int ng = (cols + kGroup - 1) / kGroup;
   int rb = fmt == 4 ? ng * kGroup / 2 : ng * kGroup * 3 / 8;
+  unsigned char *base = const_cast<unsigned char *>(dst.base);
   size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
-  k_repack_codes<<<blocks_for(lanes, 256), 256, 0, ctx->stream>>>(dst_codes, q, rows, cols, rb, ng, fmt);
+  k_repack_codes<<<blocks_for(lanes, 256), 256, 0, ctx->stream>>>(base, dst.rs, q, rows, cols, rb, ng, fmt);
   size_t ns = (size_t)rows * ng;
-  k_repack_scales<<<blocks_for(ns, 256), 256, 0, ctx->stream>>>(dst_scales, s, rows, ng);
+  k_repack_scales<<<blocks_for(ns, 256), 256, 0, ctx->stream>>>(base, dst.rs, dst.so, s, rows, ng);
   return launch_status("expert repack");
 }
 
@@ -1030,11 +1017,9 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
   if (expert < 0 || expert >= L->sh.experts)
     return fail_arg("coli_cuda_moe_layer_set_expert: expert %d outside [0,%d)", expert, L->sh.experts);
   int H = L->sh.hidden, I = L->sh.intermediate, fmt = L->sh.expert_format;
-  unsigned char *c = L->codes + (size_t)expert * L->expert_codes;
-  float *sc = L->scales + (size_t)expert * L->expert_scales;
-  if (repack_matrix(ctx, c, sc, gq, gs, I, H, fmt) ||
-      repack_matrix(ctx, c + L->gate_codes, sc + L->gate_scales, uq, us, I, H, fmt) ||
-      repack_matrix(ctx, c + 2 * L->gate_codes, sc + 2 * L->gate_scales, dq, ds, H, I, fmt))
+  if (repack_matrix(ctx, L->xl.mat(expert, 0), gq, gs, I, H, fmt) ||
+      repack_matrix(ctx, L->xl.mat(expert, 1), uq, us, I, H, fmt) ||
+      repack_matrix(ctx, L->xl.mat(expert, 2), dq, ds, H, I, fmt))
     return -1;
   return 0;
 }
@@ -1065,17 +1050,17 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
   if (ensure_scratch(ctx, kScrSetup, need, "synthesis scratch")) return -1;
   unsigned char *tmp = (unsigned char *)ctx->scratch[kScrSetup];
   for (int e = 0; e < E; e++) {
-    unsigned char *c = L->codes + (size_t)e * L->expert_codes;
-    float *sc = L->scales + (size_t)e * L->expert_scales;
     const int tq[3] = {SW_T_GATE_Q, SW_T_UP_Q, SW_T_DOWN_Q}, ts[3] = {SW_T_GATE_S, SW_T_UP_S, SW_T_DOWN_S};
     for (int m = 0; m < 3; m++) {
       int rows = m < 2 ? I : H, cols = m < 2 ? H : I, rb = m < 2 ? rbh : rbi, ng = m < 2 ? L->ngh : L->ngi;
       size_t nb = (size_t)rows * rb;
       k_synth_bytes<<<blocks_for((nb + 7) / 8, 256), 256, 0, st>>>(tmp, nb, sw_key(seed, li, (uint32_t)e, tq[m]));
+      const TileMat dst = L->xl.mat(e, m);
+      unsigned char *base = const_cast<unsigned char *>(dst.base);
       size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
-      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(c + m * L->gate_codes, tmp, rows, cols, rb, ng, fmt);
+      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(base, dst.rs, tmp, rows, cols, rb, ng, fmt);
       k_synth_scales_tiled<<<blocks_for((size_t)rows * ng, 256), 256, 0, st>>>(
-          sc + m * L->gate_scales, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
+          base, dst.rs, dst.so, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
     }
   }
   return launch_status("coli_cuda_moe_layer_synthesize");
@@ -1180,25 +1165,17 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
   if (L->sh.expert_format == 4)
-    k_expert_gateup<4><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->codes, L->scales, L->expert_codes,
-                                                                    L->expert_scales, L->gate_codes,
-                                                                    L->gate_scales);
+    k_expert_gateup<4><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->xl);
   else
-    k_expert_gateup<3><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->codes, L->scales, L->expert_codes,
-                                                                    L->expert_scales, L->gate_codes,
-                                                                    L->gate_scales);
+    k_expert_gateup<3><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->xl);
   mark(ctx, 4);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
   if (L->sh.expert_format == 4)
-    k_down<4><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
-        w, L->codes, L->scales, L->expert_codes, L->expert_scales, 2 * L->gate_codes, 2 * L->gate_scales, slots,
-        L->sh_dq, L->sh_ds);
+    k_down<4><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   else
-    k_down<3><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(
-        w, L->codes, L->scales, L->expert_codes, L->expert_scales, 2 * L->gate_codes, 2 * L->gate_scales, slots,
-        L->sh_dq, L->sh_ds);
+    k_down<3><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   mark(ctx, 6);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
   mark(ctx, 7);

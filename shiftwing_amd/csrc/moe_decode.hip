@@ -585,10 +585,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_route(Dec d, const float *__re
 // LDS: digits [2][Hp] | group parameters [ngh] | scales [2][ngh][16].
 // ---------------------------------------------------------------------------
 template <int FMT>
-__global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned char *__restrict__ codes,
-                                                          const float *__restrict__ scales, size_t expert_codes,
-                                                          size_t expert_scales, size_t gate_codes,
-                                                          size_t gate_scales) {
+__global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, ExpertLayout xl) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float part[2][4][64][4];
   __shared__ __align__(16) signed char zero16[16];
@@ -607,12 +604,16 @@ __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned 
   const float4 gr = d.xgp[tid < d.ngh ? tid : d.ngh - 1];
   const int e = d.idx[j];
   if ((unsigned)e >= (unsigned)d.E) return;  // router_topk's -1: the route contributes nothing
-  const unsigned char *cg = codes + (size_t)e * expert_codes;
-  const float *sg = scales + (size_t)e * expert_scales + (size_t)rt * d.ngh * kTileRows;
-  // this row tile's scales (2 x ngh x 16 floats, contiguous per matrix)
+  const TileMat mg = xl.mat(e, 0), mu = xl.mat(e, 1);
+  // this row tile's scales (2 x ngh x 16 floats): quad i is matrix i / ns4,
+  // group (i % ns4) / 4, rows 4 (i % 4) ..
   const int ns4 = d.ngh * 4;  // float4 per matrix
+  auto scale_quad = [&](int i) {
+    const int q = i % ns4;
+    return *(const v4f *)(tm_scales(i < ns4 ? mg : mu, (size_t)rt * d.ngh + (q >> 2)) + 4 * (q & 3));
+  };
   const int sq = tid < 2 * ns4 ? tid : 2 * ns4 - 1;
-  const v4f sr = *(const v4f *)((sq < ns4 ? sg : sg + gate_scales) + 4 * (sq % ns4));
+  const v4f sr = scale_quad(sq);
   const int per = (d.ngh + 3) / 4, g0 = wave * per;
   const int n = (d.ngh < g0 + per ? d.ngh : g0 + per) - g0;
   const DigitSrc src = lane_digits(lane, 1, dig, d.Hp, gp, d.ngh, zero16);
@@ -621,8 +622,8 @@ __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned 
   for (int c0 = 0; c0 == 0 || c0 < n; c0 += 8) {
     const int nn = n - c0 < 8 ? n - c0 : 8;
     TileCodes<FMT, 8> tg, tu;
-    tile_codes_prefetch<FMT, 8>(tg, cg, rt, d.ngh, g0 + c0, nn, lane);
-    tile_codes_prefetch<FMT, 8>(tu, cg + gate_codes, rt, d.ngh, g0 + c0, nn, lane);
+    tile_codes_prefetch<FMT, 8>(tg, mg, rt, d.ngh, g0 + c0, nn, lane);
+    tile_codes_prefetch<FMT, 8>(tu, mu, rt, d.ngh, g0 + c0, nn, lane);
     if (c0 == 0) {
       if (tid < n16) ((v4i *)dig)[tid] = dr0;
       if (tid + kThreads < n16) ((v4i *)dig)[tid + kThreads] = dr1;
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void k_dec_experts(Dec d, const unsigned 
       for (int i = kThreads + tid; i < d.ngh; i += kThreads) gp[i] = d.xgp[i];
       if (tid < 2 * ns4) ((v4f *)scl)[tid] = sr;
       for (int i = kThreads + tid; i < 2 * ns4; i += kThreads)
-        ((v4f *)scl)[i] = *(const v4f *)((i < ns4 ? sg : sg + gate_scales) + 4 * (i % ns4));
+        ((v4f *)scl)[i] = scale_quad(i);
       if (tid < 4) ((int *)zero16)[tid] = 0;
       __syncthreads();
     }
@@ -694,8 +695,7 @@ __device__ __forceinline__ void route_h_load(const float *hj, int I, v4f hv[4], 
 
 template <int FMT>
 __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
-    Dec d, const unsigned char *__restrict__ codes, const float *__restrict__ scales, size_t expert_codes,
-    size_t expert_scales, size_t down_codes_off, size_t down_scales_off, const signed char *__restrict__ dq,
+    Dec d, ExpertLayout xl, const signed char *__restrict__ dq,
     const float *__restrict__ ds, const float *__restrict__ gs, const float *__restrict__ us,
     float *__restrict__ y, int *route_idx, float *route_weight) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -733,8 +733,7 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
       route_h_load(hj, d.I, hv, lane);
       e = d.idx[wave];
       if ((unsigned)e < (unsigned)d.E) {
-        tile_prefetch<FMT, 8>(t, codes + (size_t)e * expert_codes + down_codes_off,
-                              scales + (size_t)e * expert_scales + down_scales_off, rt, d.ngi, 0,
+        tile_prefetch<FMT, 8>(t, xl.mat(e, 2), rt, d.ngi, 0,
                               d.ngi < 8 ? d.ngi : 8, lane);
         route_digits(hj, d.I, d.Ip, hv, dig, gp, lane);
       }
@@ -793,13 +792,12 @@ __global__ __launch_bounds__(64 * (kMaxDownWaves + 2)) void k_dec_down(
     for (int j = wave; j < d.K; j += nwr) {
       if (j != wave) e = d.idx[j];
       if ((unsigned)e >= (unsigned)d.E) continue;
-      const unsigned char *ce = codes + (size_t)e * expert_codes + down_codes_off;
-      const float *se = scales + (size_t)e * expert_scales + down_scales_off;
+      const TileMat md = xl.mat(e, 2);
       float acc[4] = {0, 0, 0, 0};
       for (int c0 = 0; c0 < d.ngi; c0 += 8) {
         const int nn = d.ngi - c0 < 8 ? d.ngi - c0 : 8;
         if (j != wave || c0 != 0) {
-          tile_prefetch<FMT, 8>(t, ce, se, rt, d.ngi, c0, nn, lane);
+          tile_prefetch<FMT, 8>(t, md, rt, d.ngi, c0, nn, lane);
           if (c0 == 0) {
             // a later route: its digits -> this wave's LDS (wave-local)
             const float *hj = d.h + (size_t)j * d.I;
@@ -918,20 +916,16 @@ int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *r
                                               L->stats);
   if (timing) (void)hipEventRecord(ctx->moe_event[1], st);
   if (L->sh.expert_format == 4)
-    k_dec_experts<4><<<p.g2, kThreads, p.lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                      L->gate_codes, L->gate_scales);
+    k_dec_experts<4><<<p.g2, kThreads, p.lds2, st>>>(d, L->xl);
   else
-    k_dec_experts<3><<<p.g2, kThreads, p.lds2, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                                      L->gate_codes, L->gate_scales);
+    k_dec_experts<3><<<p.g2, kThreads, p.lds2, st>>>(d, L->xl);
   if (timing) (void)hipEventRecord(ctx->moe_event[2], st);
   if (L->sh.expert_format == 4)
-    k_dec_down<4><<<p.g3, p.t3, p.lds3, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                              2 * L->gate_codes, 2 * L->gate_scales, L->sh_dq, L->sh_ds, L->sh_gs,
-                                              L->sh_us, y, route_idx, route_weight);
+    k_dec_down<4><<<p.g3, p.t3, p.lds3, st>>>(d, L->xl, L->sh_dq, L->sh_ds, L->sh_gs, L->sh_us, y, route_idx,
+                                              route_weight);
   else
-    k_dec_down<3><<<p.g3, p.t3, p.lds3, st>>>(d, L->codes, L->scales, L->expert_codes, L->expert_scales,
-                                              2 * L->gate_codes, 2 * L->gate_scales, L->sh_dq, L->sh_ds, L->sh_gs,
-                                              L->sh_us, y, route_idx, route_weight);
+    k_dec_down<3><<<p.g3, p.t3, p.lds3, st>>>(d, L->xl, L->sh_dq, L->sh_ds, L->sh_gs, L->sh_us, y, route_idx,
+                                              route_weight);
   if (timing) (void)hipEventRecord(ctx->moe_event[3], st);
   int rc = launch_status("MoE decode step");
   if (timing && rc == 0) {

@@ -63,9 +63,10 @@ constexpr int kLine = 32;        // words between counters (one 128-byte line)
 constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h, y
 constexpr int kBarWords = 9 * kLine;
 constexpr int kRecWords = 12;    // h chunk record: d1[16] d2[16] (8 words) | A B Q1 Q2
-constexpr int kGMax = 8;         // stage G: groups per wave and unit
+constexpr int kGMax = 4;         // stage G: groups per wave and unit
 constexpr int kGRing = 4;        // stage G: ring slots per wave
 constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
+constexpr int kGHead = 2560;     // stage G: partial sums and digit staging before the rings
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
 // Layer pointers as the kernel receives them: typed as device-global memory,
@@ -76,8 +77,7 @@ struct LayerRef {
   const SW_G float *router, *sgate;
   const SW_G signed char *gq, *uq, *dq;
   const SW_G float *gs, *us, *ds;
-  const SW_G unsigned char *codes;
-  const SW_G float *scales;
+  const SW_G unsigned char *experts;  // routed experts' records (sw_expert_layout.h)
   SW_G unsigned long long *stats;
   int mode, pad;
 };
@@ -85,8 +85,7 @@ struct LayerPtrs {
   const float *router, *sgate;
   const signed char *gq, *uq, *dq;
   const float *gs, *us, *ds;
-  const unsigned char *codes;
-  const float *scales;
+  const unsigned char *experts;
   unsigned long long *stats;
   int mode;
 };
@@ -105,7 +104,7 @@ struct StackArgs {
   const SW_G LayerRef *table;   // n > 1
   int n;
   int H, E, K, I, Ish, fmt, ngh, ngi, Hp, nrt_i, nch;
-  size_t expert_codes, expert_scales, gate_codes, gate_scales;
+  size_t expert_bytes, gu_bytes;  // one expert's records, its gate/up records (sw_expert_layout.h)
   int NB, rslots, KQ, n_sh_tasks, shkc;
   const float *x;
   size_t xs;
@@ -223,8 +222,7 @@ __device__ __forceinline__ LayerPtrs layer_ref(const StackArgs &a, int l) {
   SW_FIELD(gs, const float *);
   SW_FIELD(us, const float *);
   SW_FIELD(ds, const float *);
-  SW_FIELD(codes, const unsigned char *);
-  SW_FIELD(scales, const float *);
+  SW_FIELD(experts, const unsigned char *);
   SW_FIELD(stats, unsigned long long *);
 #undef SW_FIELD
   p.mode = one ? a.one.mode : a.table[l].mode;
@@ -247,8 +245,7 @@ __device__ __forceinline__ LayerPtrs layer_ref_lds(const unsigned *w) {
   p.gs = (const float *)p64(offsetof(LayerRef, gs));
   p.us = (const float *)p64(offsetof(LayerRef, us));
   p.ds = (const float *)p64(offsetof(LayerRef, ds));
-  p.codes = (const unsigned char *)p64(offsetof(LayerRef, codes));
-  p.scales = (const float *)p64(offsetof(LayerRef, scales));
+  p.experts = (const unsigned char *)p64(offsetof(LayerRef, experts));
   p.stats = (unsigned long long *)p64(offsetof(LayerRef, stats));
   p.mode = (int)u32(offsetof(LayerRef, mode));
   return p;
@@ -403,12 +400,12 @@ __host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
   return d;
 }
 
-// Stage G's LDS (partials, staging, rings, shared down rows), from the
-// union's start.  The shared hidden vector, built in stage S and quantised
-// once stage G has started, lies past it.
+// Stage G's LDS (partials, staging, rings of gate/up records, shared down
+// rows), from the union's start.  The shared hidden vector, built in stage S
+// and quantised once stage G has started, lies past it.
 __host__ __device__ inline size_t g_region_end(int Ish, int fmt) {
-  const size_t bpl = fmt == 4 ? 16 : 12;
-  return 2048 + (size_t)kW * kGRing * (64 * bpl + 64) + (size_t)kTileRows * (Ish + 16);
+  const size_t rec = 2 * (size_t)tile_codes_bytes(fmt) + 128;
+  return kGHead + (size_t)kW * kGRing * rec + (size_t)kTileRows * (Ish + 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -629,13 +626,13 @@ __device__ __forceinline__ void xops_load(XOps &xo, const DigitSrc &ds, int g0, 
   }
 }
 
-// One tile-group from a ring slot (codes, then the 16 row scales).
+// One tile-group from LDS: its codes at cbase, its 16 row scales at sbase.
 template <int FMT>
-__device__ __forceinline__ void g_item(const unsigned char *slot, const v4i &b0, const v4i &b1, float dsc, float zq,
-                                       float acc[4], int lane) {
+__device__ __forceinline__ void g_item(const unsigned char *cbase, const unsigned char *sbase, const v4i &b0,
+                                       const v4i &b1, float dsc, float zq, float acc[4], int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
   TileWord<FMT> tw;
-  const unsigned char *cp = slot + lane * BPL;
+  const unsigned char *cp = cbase + lane * BPL;
   if constexpr (FMT == 4) {
     const v4u v = *(const v4u *)cp;
     tw.w[0] = v.x;
@@ -647,7 +644,7 @@ __device__ __forceinline__ void g_item(const unsigned char *slot, const v4i &b0,
     tw.w[1] = ((const unsigned *)cp)[1];
     tw.w[2] = ((const unsigned *)cp)[2];
   }
-  const v4f s4 = *(const v4f *)(slot + 64 * BPL + 16 * (lane >> 4));
+  const v4f s4 = *(const v4f *)(sbase + 16 * (lane >> 4));
   v4i a0, a1;
   unpack_tile<FMT>(tw, a0, a1);
   v4i c = {0, 0, 0, 0};
@@ -1025,9 +1022,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     lds_barrier();  // stage R's LDS is reused below
     stamp(a, l, 2);
 
-    // stage G's waves: matrix m, groups [g0, g0+n) of x (n may be <= 0)
-    const int m = wave >> 2, qd = wave & 3;
-    const int per = (a.ngh + 3) / 4, g0 = qd * per;
+    // stage G's waves: groups [g0, g0+n) of every unit, gate and up (n may be <= 0)
+    const int per = (a.ngh + kW - 1) / kW, g0 = wave * per;
     const int n = (a.ngh < g0 + per ? a.ngh : g0 + per) - g0;
     XOps xo;
 
@@ -1424,24 +1420,26 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
     // ======================= stage G =======================
     {
-      float(*red)[16] = (float(*)[16])S.u;                  // [2][kW][16] partials
-      unsigned *stage = (unsigned *)(S.u + 2 * kW * 16 * 4);  // [kW][8] packed digits
+      float(*red)[2][16] = (float(*)[2][16])S.u;                 // [2][kW][gate, up][16] partials
+      unsigned *stage = (unsigned *)(S.u + 2 * kW * 2 * 16 * 4);  // [kW][8] packed digits
       const int nU = a.K * a.nrt_i;
       constexpr int BPL = FMT == 4 ? 16 : 12;
-      // Each wave streams its own tile-groups (its matrix, its groups, unit
-      // after unit) through a ring of kGRing slots in LDS: one tile-group's
-      // codes and row scales per slot, kGRing-1 of them in flight while one is
-      // computed.  Small in-flight amounts keep the copies from stalling the
-      // wave that issues them.
-      constexpr int kSlotG = 64 * BPL + 64;
-      unsigned char *ring = S.u + 2048 + (size_t)wave * kGRing * kSlotG;
+      constexpr int TGC = 64 * BPL;  // codes of one tile-group
+      // Each wave streams its own gate/up records (its groups, unit after
+      // unit) through a ring of kGRing slots in LDS: one record (both
+      // matrices' codes and row scales of one group) per slot, copied in
+      // 1 KB pieces, kGRing-1 records in flight while one is computed.
+      constexpr int kSlotG = 2 * TGC + 128;
+      constexpr int kGChunks = (kSlotG + 1023) / 1024;
+      static_assert(kGHead >= 2 * kW * 2 * 16 * 4 + kW * 8 * 4, "stage G head");
+      unsigned char *ring = S.u + kGHead + (size_t)wave * kGRing * kSlotG;
       // Units go round-robin over the workgroups.  When the last round would
       // leave half of them idle (nU % NB <= NB/2), its units are split in two
       // halves of every wave's groups, on workgroups 2k and 2k+1: each does
       // its half first; 2k+1 publishes its partial sums (tagged words) and 2k
       // adds them to its own at the end and builds the unit's record.
       const int F = nU / a.NB, remu = nU - F * a.NB;
-      const bool split = remu > 0 && 2 * remu <= a.NB && remu <= kSplitUnits && a.ngh % 8 == 0;
+      const bool split = remu > 0 && 2 * remu <= a.NB && remu <= kSplitUnits && a.ngh % (2 * kW) == 0;
       const bool has_half = split && b < 2 * remu;
       const int half = b & 1, hu = F * a.NB + (b >> 1);
       const int nfull = split ? F : (b < nU ? (nU - 1 - b) / a.NB + 1 : 0);
@@ -1450,39 +1448,36 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       auto ent_unit = [&](int e_) { return has_half ? (e_ == 0 ? hu : b + (e_ - 1) * a.NB) : b + e_ * a.NB; };
       auto ent_len = [&](int e_) { return (has_half && e_ == 0) ? nh : n; };
       const int nitems = n > 0 ? nfull * n + (has_half ? nh : 0) : 0;
-      // This wave's unit table, one entry per lane: byte offsets of the
-      // entry's first tile-group of this wave's matrix and groups (an invalid
-      // route reads the layer's first bytes instead; its results are discarded).
-      unsigned long long tc = 0ull, ts = 0ull;
+      // This wave's unit table, one entry per lane: byte offset of the
+      // entry's first record of this wave's groups (an invalid route reads the
+      // layer's first bytes instead; its results are discarded).
+      unsigned long long tc = 0ull;
       if (lane < nent) {
         const int u = ent_unit(lane), j = u / a.nrt_i, r16 = u - j * a.nrt_i;
         const int e = rt.idx[j];
         if ((unsigned)e < (unsigned)a.E) {
           const size_t tg = (size_t)r16 * a.ngh + g0 + ((has_half && lane == 0) ? hlo : 0);
-          tc = (size_t)e * a.expert_codes + (size_t)m * a.gate_codes + tg * 64 * BPL;
-          ts = ((size_t)e * a.expert_scales + (size_t)m * a.gate_scales + tg * kTileRows) * 4;
+          tc = (size_t)e * a.expert_bytes + tg * kSlotG;
         }
       }
       // Issue cursor (entry iu, group gu, ring slot su).  Every step issues the
-      // two copies of one tile-group; past the last item it keeps re-reading
-      // the last entry's groups (in bounds, never consumed), so that exactly
+      // kGChunks copies of one record; past the last item it keeps re-reading
+      // the last entry's records (in bounds, never consumed), so that exactly
       // kGRing-1 items are always in flight and one wait count serves all.
       int iu = 0, gu = 0, su = 0, glen = ent_len(0);
-      const unsigned char *cb = (const unsigned char *)L.codes, *sbp = (const unsigned char *)L.scales;
+      const unsigned char *cb = (const unsigned char *)L.experts;
       auto unit_base = [&](int i) {
         const int ii = i < nent ? i : nent - 1;
         const unsigned lo_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)tc, ii);
         const unsigned hi_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(tc >> 32), ii);
-        const unsigned lo_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)ts, ii);
-        const unsigned hi_s = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(ts >> 32), ii);
-        cb = (const unsigned char *)L.codes + (((unsigned long long)hi_c << 32) | lo_c);
-        sbp = (const unsigned char *)L.scales + (((unsigned long long)hi_s << 32) | lo_s);
+        cb = (const unsigned char *)L.experts + (((unsigned long long)hi_c << 32) | lo_c);
         glen = ent_len(ii);
       };
       auto issue_next = [&]() {
         const unsigned slot = lds_addr(ring + su * kSlotG);
-        if (16 * lane < 64 * BPL) dma_b128_s(cb + gu * 64 * BPL, 16 * lane, slot);
-        if (16 * lane < 64) dma_b128_s(sbp + gu * 64, 16 * lane, slot + 64 * BPL);
+#pragma unroll
+        for (int k = 0; k < kGChunks; k++)
+          if (16 * lane < kSlotG - 1024 * k) dma_b128_s(cb + gu * kSlotG + 1024 * k, 16 * lane, slot + 1024 * k);
         if (++su == kGRing) su = 0;
         if (++gu == glen) {
           gu = 0;
@@ -1530,18 +1525,26 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // finishes the entry while the others go on to the next one (the next
       // entry's barrier keeps red[i & 1] until the finisher is done).
       float gh = 0.0f, uh = 0.0f;  // the half's sums (wave 0, lanes 0..15)
-      auto finish_entry = [&](float acc4[4], int i) {
-        float(*rb)[16] = red + (i & 1) * kW;
-        digit_fold(acc4);
+      auto finish_entry = [&](float accg[4], float accu[4], int i) {
+        float(*rb)[2][16] = red + (i & 1) * kW;
+        digit_fold(accg);
+        digit_fold(accu);
         if ((lane & 15) == 1) {
 #pragma unroll
-          for (int q = 0; q < 4; q++) rb[wave][4 * (lane >> 4) + q] = acc4[q];
+          for (int q = 0; q < 4; q++) {
+            rb[wave][0][4 * (lane >> 4) + q] = accg[q];
+            rb[wave][1][4 * (lane >> 4) + q] = accu[q];
+          }
         }
         lds_barrier();
         if (wave == (i & (kW - 1)) && lane < 16) {
           const int r = lane;
-          const float gsum = rb[0][r] + rb[1][r] + rb[2][r] + rb[3][r];
-          const float usum = rb[4][r] + rb[5][r] + rb[6][r] + rb[7][r];
+          float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+          for (int w = 0; w < kW; w++) {
+            gsum += rb[w][0][r];
+            usum += rb[w][1][r];
+          }
           if (has_half && i == 0) {
             gh = gsum;
             uh = usum;
@@ -1588,21 +1591,23 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       int csl = 0;  // consume slot
       for (int i = 0; i < nent; i++) {
         const int glo = (has_half && i == 0) ? hlo : 0, ghi = glo + ent_len(i);
-        float acc4[4] = {0, 0, 0, 0};
+        float accg[4] = {0, 0, 0, 0}, accu[4] = {0, 0, 0, 0};
         if (n > 0) {
 #pragma unroll
           for (int gi = 0; gi < kGMax; gi++)
             if (gi >= glo && gi < ghi) {
               issue_next();
-              // this item's two copies are done once at most the 2(kGRing-1)
+              // this item's copies are done once at most the kGChunks(kGRing-1)
               // issued after them are outstanding (a wave's loads complete in
               // order; a store of finish_unit only makes the wait longer)
-              asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (kGRing - 1)) : "memory");
-              g_item<FMT>(ring + csl * kSlotG, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], acc4, lane);
+              asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kGChunks * (kGRing - 1)) : "memory");
+              const unsigned char *rec = ring + csl * kSlotG;
+              g_item<FMT>(rec, rec + 2 * TGC, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], accg, lane);
+              g_item<FMT>(rec + TGC, rec + 2 * TGC + 64, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], accu, lane);
               if (++csl == kGRing) csl = 0;
             }
         }
-        finish_entry(acc4, i);
+        finish_entry(accg, accu, i);
       }
       if (has_half && !half && wave == 0 && lane < 16) {
         // the partner's half of the split unit (published long ago: it was its
@@ -1665,22 +1670,19 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       lds_barrier();
       stamp(a, l, 4);
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarH), a.NB);
-      // the tile's routed down tile-groups, straight into LDS, copied by waves
-      // 1..7 while the barrier completes (wave 0 polls it: a wave's loads
-      // return in order, so its poll waits behind no copy); 16 bytes per lane
-      // (12-byte copies are not reliable)
+      // the tile's routed down records, straight into LDS in 1 KB copies by
+      // waves 1..7 while the barrier completes (wave 0 polls it: a wave's
+      // loads return in order, so its poll waits behind no copy).  A route's
+      // ngi records of this tile are contiguous in HBM and in LDS.
       if (tile < ntiles && wave != 0) {
-        for (int q = wave - 1; q < nq; q += kW - 1) {
-          const int j = q / a.ngi, gq = q - j * a.ngi;
-          const int e = rt.idx[j];
-          if ((unsigned)e >= (unsigned)a.E) continue;
-          const size_t tg = (size_t)tile * a.ngi + gq;
-          const unsigned char *src = L.codes + (size_t)e * a.expert_codes + 2 * a.gate_codes + tg * 64 * BPL;
-          const unsigned char *ssrc = (const unsigned char *)(L.scales + (size_t)e * a.expert_scales +
-                                                              2 * a.gate_scales + tg * kTileRows);
-          const unsigned slot = lds_addr(dtile + (size_t)q * kSlot);
-          if (16 * lane < 64 * BPL) dma_b128(src + 16 * lane, slot);
-          if (16 * lane < 64) dma_b128(ssrc + 16 * lane, slot + 64 * BPL);
+        const int rbytes = a.ngi * kSlot, nck = (rbytes + 1023) >> 10;
+        for (int c = wave - 1; c < a.K * nck; c += kW - 1) {
+          const int j = c / nck, k = c - j * nck;
+          int e = rt.idx[j];
+          if ((unsigned)e >= (unsigned)a.E) e = 0;  // in bounds; such a route's weight is zero
+          const unsigned char *src =
+              L.experts + (size_t)e * a.expert_bytes + a.gu_bytes + (size_t)tile * rbytes + 1024 * k;
+          if (16 * lane < rbytes - 1024 * k) dma_b128(src + 16 * lane, lds_addr(dtile + (size_t)j * rbytes + 1024 * k));
         }
       }
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
@@ -1870,8 +1872,7 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
   r.gs = (const SW_G float *)L->sh_gs;
   r.us = (const SW_G float *)L->sh_us;
   r.ds = (const SW_G float *)L->sh_ds;
-  r.codes = (const SW_G unsigned char *)L->codes;
-  r.scales = (const SW_G float *)L->scales;
+  r.experts = (const SW_G unsigned char *)L->experts;
   r.stats = (SW_G unsigned long long *)L->stats;
   r.mode = L->router_mode;
   return r;
@@ -1883,8 +1884,7 @@ static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, 
   const size_t rlay = r_layout(rslots, H, shkc).end;
   const size_t sel = s_hsh_offset(E, H, Ish, fmt) + (size_t)Ish * 4;
   const size_t dst = d_layout(K, ngi, Ish, fmt).end;
-  const int bpl = fmt == 4 ? 16 : 12;
-  const size_t ring = 2048 + (size_t)kW * kGRing * (64 * bpl + 64) + (size_t)kTileRows * (Ish + 16);
+  const size_t ring = g_region_end(Ish, fmt);
   size_t u = rlay;
   if (sel > u) u = sel;
   if (dst > u) u = dst;
@@ -1912,7 +1912,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   if (E > kStackMaxE) return false;                                   // selection keys in registers
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
-  if (ngh > 32) return false;                                         // G: 8 groups per wave
+  if ((ngh + kW - 1) / kW > kGMax) return false;                     // G: groups per wave
   if (K * ngi > 64 * kW) return false;                                // D: one item per lane of a wave
   if (H / kTileRows > NB) return false;                               // D: one output tile per workgroup
   if ((K * (I / kTileRows) + NB - 1) / NB > 63) return false;         // G: one entry per lane (+1 split half)
@@ -2053,10 +2053,8 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.Hp = a.ngh * kGroup;
   a.nrt_i = a.I / kTileRows;
   a.nch = (a.H + 2047) / 2048;
-  a.expert_codes = L0->expert_codes;
-  a.expert_scales = L0->expert_scales;
-  a.gate_codes = L0->gate_codes;
-  a.gate_scales = L0->gate_scales;
+  a.expert_bytes = L0->xl.expert_bytes;
+  a.gu_bytes = L0->xl.gu_bytes;
   a.NB = ctx->sm_count;
   a.rslots = (a.E + 1 + a.NB - 1) / a.NB;
   const int nsh_rt = 2 * (a.Ish / kTileRows);

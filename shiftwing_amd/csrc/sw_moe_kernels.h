@@ -10,10 +10,12 @@
 //         bits of code 4(4a+j')+m) and a high-bit plane H (byte m bit j =
 //         bit 2 of code 4j+m).
 // Unpacking yields 8 dwords D_j whose byte m is the code of lane slot 4j+m.
-// Per-(row, group) scales are stored [row tile][group][16 rows].
+// A tile-group's codes and its 16 per-row scales lie in one record
+// (sw_expert_layout.h).
 #pragma once
 
 #include "sw_device.h"
+#include "sw_expert_layout.h"
 
 namespace sw {
 
@@ -108,16 +110,16 @@ struct TilePrefetch {
 };
 
 template <int FMT, int NMAX>
-__device__ __forceinline__ void tile_prefetch(TilePrefetch<FMT, NMAX> &t, const unsigned char *codes,
-                                              const float *scales, int rt, int ng, int g0, int n, int lane) {
+__device__ __forceinline__ void tile_prefetch(TilePrefetch<FMT, NMAX> &t, const TileMat &mat, int rt, int ng, int g0,
+                                              int n, int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
   const int kb = lane >> 4;
 #pragma unroll
   for (int i = 0; i < NMAX; i++)
     if (i < n) {
       size_t tg = (size_t)rt * ng + g0 + i;
-      t.q[i] = load_tile<FMT>(codes + (tg * 64 + lane) * BPL);
-      t.sc[i] = __builtin_nontemporal_load((const v4f *)(scales + tg * kTileRows + 4 * kb));
+      t.q[i] = load_tile<FMT>(tm_codes(mat, tg) + lane * BPL);
+      t.sc[i] = __builtin_nontemporal_load((const v4f *)(tm_scales(mat, tg) + 4 * kb));
     }
 }
 
@@ -164,12 +166,12 @@ struct TileCodes {
 };
 
 template <int FMT, int NMAX>
-__device__ __forceinline__ void tile_codes_prefetch(TileCodes<FMT, NMAX> &t, const unsigned char *codes, int rt,
-                                                    int ng, int g0, int n, int lane) {
+__device__ __forceinline__ void tile_codes_prefetch(TileCodes<FMT, NMAX> &t, const TileMat &mat, int rt, int ng,
+                                                    int g0, int n, int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
 #pragma unroll
   for (int i = 0; i < NMAX; i++)
-    if (i < n) t.q[i] = load_tile<FMT>(codes + (((size_t)rt * ng + g0 + i) * 64 + lane) * BPL);
+    if (i < n) t.q[i] = load_tile<FMT>(tm_codes(mat, (size_t)rt * ng + g0 + i) + lane * BPL);
 }
 
 // tile_compute with the row tile's scales in LDS: sc[g][16 rows].
@@ -272,10 +274,10 @@ __device__ __forceinline__ void digit_fold(float acc[4]) {
 }
 
 template <int FMT, int NMAX>
-__device__ __forceinline__ void tile_gemv(const unsigned char *codes, const float *scales, int rt, int ng, int g0,
-                                          int n, const DigitSrc &ds, float acc[4], int lane) {
+__device__ __forceinline__ void tile_gemv(const TileMat &mat, int rt, int ng, int g0, int n, const DigitSrc &ds,
+                                          float acc[4], int lane) {
   TilePrefetch<FMT, NMAX> t;
-  tile_prefetch<FMT, NMAX>(t, codes, scales, rt, ng, g0, n, lane);
+  tile_prefetch<FMT, NMAX>(t, mat, rt, ng, g0, n, lane);
   tile_compute<FMT, NMAX>(t, g0, n, ds, acc, lane);
 }
 

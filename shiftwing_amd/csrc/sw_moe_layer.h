@@ -6,19 +6,17 @@
 #include <stddef.h>
 
 #include "shiftwing_moe.h"
+#include "sw_expert_layout.h"
 
 struct ColiMoeLayer {
   ColiMoeShape sh;
   int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
-  size_t gate_codes, down_codes; // bytes of one gate (= up) / down tiled matrix
-  size_t gate_scales, down_scales;
-  size_t expert_codes, expert_scales;  // per expert
   float *router;                 // [E][H]
   float *sgate_row;              // [H]
   signed char *sh_gq, *sh_uq, *sh_dq;  // row-major int8
   float *sh_gs, *sh_us, *sh_ds;
-  unsigned char *codes;          // [E][gate|up|down] tiled
-  float *scales;                 // [E][gate|up|down] tiled
+  unsigned char *experts;        // routed experts' records (sw_expert_layout.h)
+  sw::ExpertLayout xl;           // ... and where they lie
   unsigned long long *stats;     // device [2]: tokens, exact fallbacks
   // decode-step fan-in counters and int32 accumulators, owned by the layer
   // (zeroed at creation and returned to zero by every step), so a context
