@@ -1504,16 +1504,22 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           q2 = (int)fminf(fmaxf(__builtin_rintf(rr2 * invB), -127.0f), 127.0f);
         }
         const int s1 = row16_sum_i(q1), s2 = row16_sum_i(q2);
+        // stage D's digit scales with the route weight folded in, and the code
+        // offset's correction (OFF x digit sum x scale) ready to subtract
+        constexpr int OFFD = FMT == 4 ? 8 : 4;
+        const float wj = (unsigned)e < (unsigned)a.E ? rt.w[j] : 0.0f;
+        const float Aw = A * wj, Bw = B * wj;
+        const float z1 = (float)(OFFD * s1) * Aw, z2 = (float)(OFFD * s2) * Bw;
         signed char *stg = (signed char *)(stage + 8 * wave);
         stg[r] = (signed char)q1;
         stg[16 + r] = (signed char)q2;
         __builtin_amdgcn_wave_barrier();
         unsigned v = 0;
         if (r < 8) v = ((const unsigned *)stg)[r];
-        else if (r == 8) v = __float_as_uint(A);
-        else if (r == 9) v = __float_as_uint(B);
-        else if (r == 10) v = (unsigned)s1;
-        else if (r == 11) v = (unsigned)s2;
+        else if (r == 8) v = __float_as_uint(Aw);
+        else if (r == 9) v = __float_as_uint(Bw);
+        else if (r == 10) v = __float_as_uint(z1);
+        else if (r == 11) v = __float_as_uint(z2);
         // a device-scope store: complete (and visible to every device-scope
         // load) once vmcnt drains, which every wave waits for before the
         // workgroup arrives at the barrier
@@ -1747,21 +1753,20 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       if (tile < ntiles) {
         wait_dma();     // this wave's LDS copies have landed
         lds_barrier();  // ... and every other wave's
-        constexpr int OFF = FMT == 4 ? 8 : 4;
         const int c = lane & 15, kb = lane >> 4;
         const bool lo = c < 8 && (c >> 1) == kb;
         const bool hi = c >= 8 && ((c - 8) >> 1) == kb;
         const int chb = lo ? kb : 4 + kb;
         // routed: per tile-group two MFMAs; B column c = (chunk c>>1, digit c&1).
-        // Wave w takes the tile-groups q = j*ngi + g with q % kW == w, and
-        // folds each one's route weight into its row scales (the combine's
-        // sum over routes, per wave).  Items go in pairs, both pairs' LDS
-        // operands read before either is computed.
+        // Wave w takes the tile-groups q = j*ngi + g with q % kW == w; the
+        // route weight is folded into the h records' digit scales (the
+        // combine's sum over routes, per wave).  Items go in pairs, both
+        // pairs' LDS operands read before either is computed.
         struct DOps {
           TileWord<FMT> cw;
           v4f s4;
-          v4i dv;
-          float dscl, zq, wk;
+          v4i d0, d1;  // MFMA B operands of both steps (zero where the lane's column is the other step's)
+          float dscl, zq;
         };
         auto load_ops = [&](DOps &o, int jq, int gq) {
           const unsigned char *tq = dtile + (size_t)(jq * a.ngi + gq) * kSlot;
@@ -1779,22 +1784,23 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
           o.s4 = *(const v4f *)(tq + 64 * BPL + 16 * kb);
           const unsigned *rbase = hrec + (size_t)(jq * a.ngi * 8 + gq * 8) * kRecWords;
-          o.dv = *(const v4i *)(rbase + chb * kRecWords + (c & 1) * 4);
+          const v4i *dp = (const v4i *)(rbase + chb * kRecWords + (c & 1) * 4);
+          o.d0 = *(lo ? dp : (const v4i *)zero16);
+          o.d1 = *(hi ? dp : (const v4i *)zero16);
+          // digit scale and offset correction (route weight folded in; an
+          // invalid route's are zero)
           const unsigned *prm = rbase + (c >> 1) * kRecWords + 8;
           o.dscl = __uint_as_float(prm[c & 1]);
-          o.zq = (float)(OFF * (int)prm[2 + (c & 1)]) * o.dscl;
-          // an invalid route (no expert) adds nothing
-          o.wk = (unsigned)rt.idx[jq] < (unsigned)a.E ? rt.w[jq] : 0.0f;
+          o.zq = __uint_as_float(prm[2 + (c & 1)]);
         };
         float tot[4] = {0, 0, 0, 0};
         auto compute = [&](const DOps &o) {
           v4i a0, a1;
           unpack_tile<FMT>(o.cw, a0, a1);
-          const v4i z = {0, 0, 0, 0};
           v4i cc = {0, 0, 0, 0};
-          cc = mfma_i8(a0, lo ? o.dv : z, cc);
-          cc = mfma_i8(a1, hi ? o.dv : z, cc);
-          const float sv[4] = {o.s4.x * o.wk, o.s4.y * o.wk, o.s4.z * o.wk, o.s4.w * o.wk};
+          cc = mfma_i8(a0, o.d0, cc);
+          cc = mfma_i8(a1, o.d1, cc);
+          const float sv[4] = {o.s4.x, o.s4.y, o.s4.z, o.s4.w};
 #pragma unroll
           for (int r = 0; r < 4; r++) tot[r] = __builtin_fmaf(__builtin_fmaf((float)cc[r], o.dscl, -o.zq), sv[r], tot[r]);
         };
