@@ -71,7 +71,9 @@ enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
 // Layer pointers as the kernel receives them: typed as device-global memory,
 // so that every access through them compiles to global (not flat) memory
-// instructions.  LayerPtrs is the same set as plain pointers.
+// instructions (a flat access also counts as an LDS access, so every later
+// wait for LDS would wait for it too).  LayerPtrs is the same set as the
+// kernel uses it.
 #define SW_G __attribute__((address_space(1)))
 struct LayerRef {
   const SW_G float *router, *sgate;
@@ -82,11 +84,11 @@ struct LayerRef {
   int mode, pad;
 };
 struct LayerPtrs {
-  const float *router, *sgate;
-  const signed char *gq, *uq, *dq;
-  const float *gs, *us, *ds;
-  const unsigned char *experts;
-  unsigned long long *stats;
+  const SW_G float *router, *sgate;
+  const SW_G signed char *gq, *uq, *dq;
+  const SW_G float *gs, *us, *ds;
+  const SW_G unsigned char *experts;
+  SW_G unsigned long long *stats;
   int mode;
 };
 
@@ -213,17 +215,17 @@ __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" :
 __device__ __forceinline__ LayerPtrs layer_ref(const StackArgs &a, int l) {
   LayerPtrs p;
   const bool one = a.n == 1;
-#define SW_FIELD(f, T) p.f = (T)(one ? a.one.f : a.table[l].f)
-  SW_FIELD(router, const float *);
-  SW_FIELD(sgate, const float *);
-  SW_FIELD(gq, const signed char *);
-  SW_FIELD(uq, const signed char *);
-  SW_FIELD(dq, const signed char *);
-  SW_FIELD(gs, const float *);
-  SW_FIELD(us, const float *);
-  SW_FIELD(ds, const float *);
-  SW_FIELD(experts, const unsigned char *);
-  SW_FIELD(stats, unsigned long long *);
+#define SW_FIELD(f) p.f = one ? a.one.f : a.table[l].f
+  SW_FIELD(router);
+  SW_FIELD(sgate);
+  SW_FIELD(gq);
+  SW_FIELD(uq);
+  SW_FIELD(dq);
+  SW_FIELD(gs);
+  SW_FIELD(us);
+  SW_FIELD(ds);
+  SW_FIELD(experts);
+  SW_FIELD(stats);
 #undef SW_FIELD
   p.mode = one ? a.one.mode : a.table[l].mode;
   return p;
@@ -237,16 +239,16 @@ __device__ __forceinline__ LayerPtrs layer_ref_lds(const unsigned *w) {
   auto u32 = [&](size_t off) { return (unsigned)__builtin_amdgcn_readfirstlane((int)w[off / 4]); };
   auto p64 = [&](size_t off) { return ((unsigned long long)u32(off + 4) << 32) | u32(off); };
   LayerPtrs p;
-  p.router = (const float *)p64(offsetof(LayerRef, router));
-  p.sgate = (const float *)p64(offsetof(LayerRef, sgate));
-  p.gq = (const signed char *)p64(offsetof(LayerRef, gq));
-  p.uq = (const signed char *)p64(offsetof(LayerRef, uq));
-  p.dq = (const signed char *)p64(offsetof(LayerRef, dq));
-  p.gs = (const float *)p64(offsetof(LayerRef, gs));
-  p.us = (const float *)p64(offsetof(LayerRef, us));
-  p.ds = (const float *)p64(offsetof(LayerRef, ds));
-  p.experts = (const unsigned char *)p64(offsetof(LayerRef, experts));
-  p.stats = (unsigned long long *)p64(offsetof(LayerRef, stats));
+  p.router = (const SW_G float *)p64(offsetof(LayerRef, router));
+  p.sgate = (const SW_G float *)p64(offsetof(LayerRef, sgate));
+  p.gq = (const SW_G signed char *)p64(offsetof(LayerRef, gq));
+  p.uq = (const SW_G signed char *)p64(offsetof(LayerRef, uq));
+  p.dq = (const SW_G signed char *)p64(offsetof(LayerRef, dq));
+  p.gs = (const SW_G float *)p64(offsetof(LayerRef, gs));
+  p.us = (const SW_G float *)p64(offsetof(LayerRef, us));
+  p.ds = (const SW_G float *)p64(offsetof(LayerRef, ds));
+  p.experts = (const SW_G unsigned char *)p64(offsetof(LayerRef, experts));
+  p.stats = (SW_G unsigned long long *)p64(offsetof(LayerRef, stats));
   p.mode = (int)u32(offsetof(LayerRef, mode));
   return p;
 }
@@ -496,13 +498,13 @@ __device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs 
   if (t < 64) return;
   const StaticMap m = static_map(a);
   const ShTask st = sh_task(a);
-  const unsigned char *sbase =
-      (const unsigned char *)((st.m == 0 ? L.gq : L.uq) + (size_t)st.rt * kTileRows * a.H + st.kc0 * 64);
-  const unsigned char *rows[kRSlots];
+  const SW_G unsigned char *sbase =
+      (const SW_G unsigned char *)((st.m == 0 ? L.gq : L.uq) + (size_t)st.rt * kTileRows * a.H + st.kc0 * 64);
+  const SW_G unsigned char *rows[kRSlots];
 #pragma unroll
   for (int s2 = 0; s2 < kRSlots; s2++) {
     const int r = blockIdx.x + s2 * a.NB;
-    rows[s2] = (const unsigned char *)(r < a.E ? L.router + (size_t)r * a.H : L.sgate);
+    rows[s2] = (const SW_G unsigned char *)(r < a.E ? L.router + (size_t)r * a.H : L.sgate);
   }
 #pragma unroll
   for (int i = 0; i < kStRegs; i++) {
@@ -510,12 +512,12 @@ __device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs 
     v4u v = {0u, 0u, 0u, 0u};
     if (o < m.rbytes) {
       const int s2 = (o >= m.rowb) + (o >= 2 * m.rowb);
-      const unsigned char *row = s2 == 0 ? rows[0] : (s2 == 1 ? rows[1] : rows[2]);
-      v = __builtin_nontemporal_load((const v4u *)(row + (o - (unsigned)s2 * m.rowb)));
+      const SW_G unsigned char *row = s2 == 0 ? rows[0] : (s2 == 1 ? rows[1] : rows[2]);
+      v = __builtin_nontemporal_load((const SW_G v4u *)(row + (o - (unsigned)s2 * m.rowb)));
     } else if (o < m.total) {
       const unsigned o2 = o - m.rbytes;
       v = __builtin_nontemporal_load(
-          (const v4u *)(sbase + (size_t)((o2 >> 6) & 15) * a.H + (o2 >> 10) * 64 + (o2 & 63)));
+          (const SW_G v4u *)(sbase + (size_t)((o2 >> 6) & 15) * a.H + (o2 >> 10) * 64 + (o2 & 63)));
     }
     sr.v[i] = v;
   }
@@ -547,7 +549,7 @@ __device__ __forceinline__ void exact_chains(const StackArgs &a, const LayerPtrs
   for (int s = 0; s < kRSlots; s++)
     if (want & (1u << s)) {
       const int r = blockIdx.x + s * a.NB;
-      const float *row = L.router + (size_t)r * a.H;
+      const SW_G float *row = L.router + (size_t)r * a.H;
       for (int e0 = 4 * t; e0 < a.H; e0 += 4 * kT) {
         const v4f w = *(const v4f *)(row + e0);
         const v4f xv = *(const v4f *)(x + e0);
@@ -1283,8 +1285,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         lds_barrier();
       }
       if (b == 0 && t == 0) {
-        atomicAdd(&L.stats[0], 1ull);
-        if (rt.state != 0) atomicAdd(&L.stats[1], 1ull);
+        __hip_atomic_fetch_add(&L.stats[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (rt.state != 0) __hip_atomic_fetch_add(&L.stats[1], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (rt.state == 1) {
         // exact chains of the ambiguous experts this workgroup owns
@@ -1402,7 +1404,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               rt.idx[j] = sel.chosen[j];
               rt.w[j] = sel.wsel[j] / topden;
             }
-            if (b == 0) atomicAdd(&L.stats[2], 1ull);
+            if (b == 0) __hip_atomic_fetch_add(&L.stats[2], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
         lds_barrier();
@@ -1574,7 +1576,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int r = wave; r < kTileRows; r += kW)
           for (int c0 = 0; c0 < a.Ish; c0 += 1024)
             if (c0 + 16 * lane < a.Ish)
-              dma_b128(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane,
+              dma_b128((const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
                        lds_addr(gdsh + (size_t)r * (a.Ish + 16) + c0));
       if (nitems > 0) {
         unit_base(0);
@@ -1686,9 +1688,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           const int j = c / nck, k = c - j * nck;
           int e = rt.idx[j];
           if ((unsigned)e >= (unsigned)a.E) e = 0;  // in bounds; such a route's weight is zero
-          const unsigned char *src =
-              L.experts + (size_t)e * a.expert_bytes + a.gu_bytes + (size_t)tile * rbytes + 1024 * k;
-          if (16 * lane < rbytes - 1024 * k) dma_b128(src + 16 * lane, lds_addr(dtile + (size_t)j * rbytes + 1024 * k));
+          const void *src =
+              (const void *)(L.experts + (size_t)e * a.expert_bytes + a.gu_bytes + (size_t)tile * rbytes + 1024 * k);
+          if (16 * lane < rbytes - 1024 * k)
+            dma_b128((const unsigned char *)src + 16 * lane, lds_addr(dtile + (size_t)j * rbytes + 1024 * k));
         }
       }
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
