@@ -134,7 +134,7 @@ struct StackArgs {
 // D done, y passed.
 constexpr int kStamps = 8;
 __device__ __forceinline__ void stamp(const StackArgs &a, int l, int k) {
-  if (a.trace && threadIdx.x == 0) {
+  if (__builtin_expect(a.trace != nullptr, 0) && threadIdx.x == 0) {
     const size_t i = ((size_t)l * a.NB + blockIdx.x) * kStamps + k;
     if (i < a.trace_words) a.trace[i] = wall_clock64();
   }
@@ -269,8 +269,8 @@ __device__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) 
   for (unsigned it = 0;; it++) {
     if (ld_agent(p) >= target) return true;
     if ((it & 31) == 31) {
-      if (ld_agent(a.abort_word)) return false;
-      if ((long long)wall_clock64() - t0 > a.spin_ticks) {
+      if (__builtin_expect(ld_agent(a.abort_word) != 0, 0)) return false;
+      if (__builtin_expect((long long)wall_clock64() - t0 > a.spin_ticks, 0)) {
         atomicMax(a.abort_word, 1u);
         __hip_atomic_store(a.abort_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         return false;
@@ -299,8 +299,8 @@ __device__ __forceinline__ bool has_tag(unsigned long long v, unsigned tag) { re
 // the wait started at t0 must end (the abort word is set, or the time is up;
 // then every workgroup leaves through the abort word).
 __device__ bool wait_expired(long long t0, const StackArgs &a) {
-  if (ld_agent(a.abort_word)) return true;
-  if ((long long)wall_clock64() - t0 > a.spin_ticks) {
+  if (__builtin_expect(ld_agent(a.abort_word) != 0, 0)) return true;
+  if (__builtin_expect((long long)wall_clock64() - t0 > a.spin_ticks, 0)) {
     atomicMax(a.abort_word, 1u);
     __hip_atomic_store(a.abort_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     return true;
@@ -1061,7 +1061,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           for (int i = 0; i < kSelRec; i++)
             if (t + i * kT <= E) all = all && has_tag(rx[i], tag) && has_tag(ry[i], tag);
           if (all) break;
-          if ((it & 15) == 15 && wait_expired(t0, a)) {
+          if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
             s_abort = 1;
             break;
           }
@@ -1117,7 +1117,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (t == E - iE * kT) rt.sg = sigmoid_ref((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])));
       }
       lds_barrier();
-      if (s_abort) return;
+      if (__builtin_expect(s_abort != 0, 0)) return;
       // Every record of this layer is in, so every workgroup's shared gate/up
       // sums are too (each adds them before tagging its records): waves 1..7
       // load them now and build the shared hidden vector while wave 0 selects.
@@ -1199,7 +1199,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (lane == 0) rt.shm[wave] = hm;
       } else {
         const int M = sel.nmc;
-        if (M > 64) {
+        if (__builtin_expect(M > 64, 0)) {
           if (lane == 0) rt.state = 2;
         } else {
           // rank of each candidate among the candidates
@@ -1267,7 +1267,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
       lds_barrier();
-      if (rt.state == 1) {
+      if (__builtin_expect(rt.state == 1, 0)) {
         // Every expert whose upper bound reaches the lowest lower bound among
         // the K candidates (less a margin): the exact top K lies in this set,
         // since anything outside it is strictly below all K candidates.
@@ -1288,7 +1288,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         __hip_atomic_fetch_add(&L.stats[0], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (rt.state != 0) __hip_atomic_fetch_add(&L.stats[1], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      if (rt.state == 1) {
+      if (__builtin_expect(rt.state == 1, 0)) {
         // exact chains of the ambiguous experts this workgroup owns
         unsigned want = 0;
         for (int i = 0; i < sel.nm; i++) {
@@ -1341,7 +1341,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
         lds_barrier();
       }
-      if (rt.state == 2) {
+      if (__builtin_expect(rt.state == 2, 0)) {
         // every expert's exact chain (owners compute theirs), then router_topk
         // (c/qwen.c:3421-3426) bit for bit: max, expf(l - max), the serial
         // denominator in expert order, division, K argmax rounds (lowest index
@@ -1625,7 +1625,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         unsigned long long vg = ld_agent(w), vu = ld_agent(w + 1);
         const long long t0 = (long long)wall_clock64();
         for (unsigned it = 0; (unsigned)(vg >> 32) != tag || (unsigned)(vu >> 32) != tag; it++) {
-          if ((it & 15) == 15 && wait_expired(t0, a)) {
+          if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
             s_abort = 1;
             break;
           }
@@ -1636,7 +1636,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the last item
       lds_barrier();  // the last finisher is done with its partials; every copy has landed
-      if (s_abort) return;
+      if (__builtin_expect(s_abort != 0, 0)) return;
       // shared down: exact int32 dots of the tile's 16 rows with hq, into
       // s_shp (the ring is no longer read)
       if (tile < ntiles) {
@@ -1696,9 +1696,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       }
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarH), a) ? 1 : 0;
       lds_barrier();
-      if (!rt.flag) return;
+      if (__builtin_expect(!rt.flag, 0)) return;
       stamp(a, l, 5);
-      if (l == a.n - 1 && wave == 0 && lane < kRSlots) {
+      if (__builtin_expect(l == a.n - 1, 0) && wave == 0 && lane < kRSlots) {
         // Every workgroup has passed this call's last selection, so no one
         // reads the records any more: clear this workgroup's, so that a later
         // call never meets a word left by an older one (records are read
@@ -1710,11 +1710,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
                              __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      if (l == a.n - 1 && wave == 0 && lane < 32 && (b & 1) == 0 && (b >> 1) < kSplitUnits) {
+      if (__builtin_expect(l == a.n - 1, 0) && wave == 0 && lane < 32 && (b & 1) == 0 && (b >> 1) < kSplitUnits) {
         // the split units' half sums (read by this workgroup only): cleared too
         __hip_atomic_store(a.spl + (size_t)(b >> 1) * 32 + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      if (l == a.n - 1 && b == 0 && t == 0) {
+      if (__builtin_expect(l == a.n - 1, 0) && b == 0 && t == 0) {
         // every workgroup has read the call state: advance it for the next call
         const unsigned long long nl = layers_run + (unsigned long long)a.n;
         const int p = cs.parity;
@@ -1857,7 +1857,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sreg, t);
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarY), a) ? 1 : 0;
       lds_barrier();
-      if (!rt.flag) return;
+      if (__builtin_expect(!rt.flag, 0)) return;
       stamp(a, l, 7);
     }
   }
