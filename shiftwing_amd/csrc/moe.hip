@@ -327,6 +327,78 @@ __global__ void k_router_bounds(Work w, const float *x, const float *router, con
   }
 }
 
+// The same per-(token, row) arithmetic as k_router_bounds (lane j owns the
+// contiguous chunk j of CH = H/64 elements, same fma order, same wave
+// reductions, so L and B are bit-identical), arranged for many tokens: wave w
+// of a block holds router row e = 8*blockIdx.x + w in registers, read once,
+// and walks the block's tokens.  The tokens' activations are staged in LDS
+// kRbRound at a time, lane-major with one pad word per lane (pitch CH+1), so
+// lane j's reads of its chunk fall in distinct banks and the staging writes of
+// consecutive elements stay consecutive.  Row E is the shared-expert gate row.
+// grid (ceil((E+1)/8), ceil(T/tokens_per_block)), 512 threads, dynamic LDS
+// kRbRound*64*(CH+1) floats.  Requires x 16-byte aligned.
+constexpr int kRbRound = 4;
+template <int CH>
+__global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float *x, const float *router,
+                                                             const float *sgate_row, int tokens_per_block) {
+  extern __shared__ float rb_xs[];  // [kRbRound][64 * (CH + 1)]
+  constexpr int P = CH + 1, H = 64 * CH;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 8 + wave;
+  const bool live = e <= w.E;
+  float wr[CH];
+  if (live) {
+    const float *row = e < w.E ? router + (size_t)e * H : sgate_row;
+    const float4 *r4 = (const float4 *)(row + lane * CH);
+#pragma unroll
+    for (int c = 0; c < CH / 4; c++) {
+      float4 v = r4[c];
+      wr[4 * c] = v.x;
+      wr[4 * c + 1] = v.y;
+      wr[4 * c + 2] = v.z;
+      wr[4 * c + 3] = v.w;
+    }
+  }
+  const int t0 = blockIdx.y * tokens_per_block, t1 = min(t0 + tokens_per_block, w.T);
+  for (int tb = t0; tb < t1; tb += kRbRound) {
+    const int ng = min(kRbRound, t1 - tb);
+    __syncthreads();  // the previous round's reads are done
+    for (int k = threadIdx.x * 4; k < ng * H; k += 512 * 4) {
+      const int g = k / H, kk = k - g * H;
+      const float4 v = *(const float4 *)(x + (size_t)(tb + g) * H + kk);
+      float *d = rb_xs + g * 64 * P + (kk / CH) * P + (kk % CH);  // CH % 4 == 0: one chunk
+      d[0] = v.x;
+      d[1] = v.y;
+      d[2] = v.z;
+      d[3] = v.w;
+    }
+    __syncthreads();
+    if (!live) continue;
+    for (int g = 0; g < ng; g++) {
+      const float *xl = rb_xs + g * 64 * P + lane * P;
+      double lp = 0.0, pa = 0.0, aa = 0.0;
+#pragma unroll
+      for (int c = 0; c < CH; c++) {
+        double xd = (double)xl[c], wd = (double)wr[c];
+        lp = __builtin_fma(xd, wd, lp);
+        aa = __builtin_fma(fabs(xd), fabs(wd), aa);
+        pa += fabs(lp);
+      }
+      double off = wave_exclusive_scan(lp, lane);
+      double L = wave_sum(lp);
+      double Pb = wave_sum((double)CH * fabs(off) + pa);
+      double A = wave_sum(aa);
+      if (lane == 0) {
+        const int t = tb + g;
+        const double u = 0x1p-24;
+        double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+        w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, B);
+        if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
+      }
+    }
+  }
+}
+
 // block argmax over (value, index): largest value, lowest index on ties
 struct VI {
   double v;
@@ -604,28 +676,21 @@ __global__ void k_bucket_only(const int *idx, int T, int K, int E, int *offsets,
 }
 
 // ---------------------------------------------------------------------------
-// routed tile GEMV on int8 MFMA.  For row tile rt and groups [g0, g1) of a
-// tiled matrix, accumulates into acc[i] (rows 4*kb+i) the group-scaled dots
-// with up to 8 token activations given as digit arrays.  Valid results sit in
-// lanes with odd column c = lane%16: token c/2.
+// Tile unpacking: a lane's codes of one tile-group (16 bytes int4, 12 bytes
+// int3) become the two int8 MFMA A operands (group positions kb*16+[0,16) and
+// 64+kb*16+[0,16) of row lane%16), codes unsigned.
 // ---------------------------------------------------------------------------
 template <int FMT>
-__device__ __forceinline__ void unpack_tile(const unsigned char *tp, v4i &a0, v4i &a1) {
+__device__ __forceinline__ void unpack_words(const uint32_t *q, v4i &a0, v4i &a1) {
+  uint32_t d[8];
   if (FMT == 4) {
-    uint4 q = *(const uint4 *)tp;
-    uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    uint32_t d[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      d[2 * i] = w[i] & 0x0F0F0F0Fu;
-      d[2 * i + 1] = (w[i] >> 4) & 0x0F0F0F0Fu;
+      d[2 * i] = q[i] & 0x0F0F0F0Fu;
+      d[2 * i + 1] = (q[i] >> 4) & 0x0F0F0F0Fu;
     }
-    a0 = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
-    a1 = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
   } else {
-    const uint32_t *p = (const uint32_t *)tp;
-    uint32_t L0 = p[0], L1 = p[1], H = p[2];
-    uint32_t d[8];
+    uint32_t L0 = q[0], L1 = q[1], H = q[2];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       uint32_t L = j < 4 ? L0 : L1;
@@ -633,63 +698,109 @@ __device__ __forceinline__ void unpack_tile(const unsigned char *tp, v4i &a0, v4
       uint32_t hi = j <= 2 ? (H << (2 - j)) : (H >> (j - 2));
       d[j] = lo | (hi & 0x04040404u);
     }
-    a0 = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
-    a1 = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+  }
+  a0 = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+  a1 = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_words(const unsigned char *tp, uint32_t *q) {
+  if (FMT == 4) {
+    uint4 v = *(const uint4 *)tp;
+    q[0] = v.x;
+    q[1] = v.y;
+    q[2] = v.z;
+    q[3] = v.w;
+  } else {
+    const uint32_t *p = (const uint32_t *)tp;
+    q[0] = p[0];
+    q[1] = p[1];
+    q[2] = p[2];
   }
 }
 
-struct TokDigits {
-  const signed char *d1[kMaxTokensPerItem];  // per token digit arrays (group-major)
-  const signed char *d2[kMaxTokensPerItem];
-  const float4 *gp[kMaxTokensPerItem];
+template <int FMT>
+__device__ __forceinline__ void unpack_tile(const unsigned char *tp, v4i &a0, v4i &a1) {
+  uint32_t q[4];
+  load_words<FMT>(tp, q);
+  unpack_words<FMT>(q, a0, a1);
+}
+
+// Routed tile GEMV on int8 MFMA for up to 8 tokens: the loads of kMtBatch
+// consecutive groups (codes, row scales, token digits and digit parameters)
+// are issued together ahead of their MFMAs, so a wave has a batch of HBM
+// reads in flight.  Per group: two MFMAs give the exact int32 dots of the
+// codes with both digits of each token (B column c = lane%16: token c/2,
+// digit c%2); f = (dot - OFF*digit sum) * digit scale, the two digit columns
+// are added across lanes, and acc += f * row scale.  Results sit in the odd
+// lanes of each 16-lane row group.
+constexpr int kMtBatch = 4;
+template <int FMT>
+struct MtTiles {
+  uint32_t q[kMtBatch][FMT == 4 ? 4 : 3];
+  float4 sc[kMtBatch];
+};
+struct MtDigits {
+  v4i b0[kMtBatch], b1[kMtBatch];
+  float dsc[kMtBatch];
+  int Q[kMtBatch];
 };
 
 template <int FMT>
-__device__ __forceinline__ void tile_gemv(const TileMat &mat, int rt, int ng, int g0, int g1,
-                                          const signed char *dsrc, const float4 *gpsrc, float acc[4], int lane) {
+__device__ __forceinline__ void mt_load(MtTiles<FMT> &t, const TileMat &mat, size_t tg0, int n, int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
-  constexpr int OFF = FMT == 4 ? 8 : 4;
   const int kb = lane >> 4;
-  for (int g = g0; g < g1; g++) {
-    v4i a0, a1;
-    unpack_tile<FMT>(tm_codes(mat, (size_t)rt * ng + g) + lane * BPL, a0, a1);
-    v4i b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
-    float dsc = 0.0f;
-    int Q = 0;
-    if (dsrc) {
-      b0 = *(const v4i *)(dsrc + g * kGroup + kb * 16);
-      b1 = *(const v4i *)(dsrc + g * kGroup + 64 + kb * 16);
-    }
-    if (gpsrc) {
-      float4 p = gpsrc[g];
-      bool second = lane & 1;
-      dsc = second ? p.y : p.x;
-      Q = __float_as_int(second ? p.w : p.z);
-    }
-    v4i c = {0, 0, 0, 0};
-    c = mfma_i8(a0, b0, c);
-    c = mfma_i8(a1, b1, c);
-    float4 sc = *(const float4 *)(tm_scales(mat, (size_t)rt * ng + g) + 4 * kb);
-    float scv[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float f = (float)(c[i] - OFF * Q) * dsc;
-      float tsum = f + dpp_row_shr1(f);
-      acc[i] = __builtin_fmaf(tsum, scv[i], acc[i]);
+  for (int i = 0; i < kMtBatch; i++)
+    if (i < n) {
+      load_words<FMT>(tm_codes(mat, tg0 + i) + lane * BPL, t.q[i]);
+      t.sc[i] = *(const float4 *)(tm_scales(mat, tg0 + i) + 4 * kb);
     }
-  }
 }
 
-// B-operand source for lane column c: token c/2's digit array (c%2), or null
-__device__ inline void lane_digit_src(int lane, int cnt, const signed char *const *d1s, const signed char *const *d2s,
-                                      const float4 *const *gps, const signed char *&dsrc, const float4 *&gp) {
-  int c = lane & 15, tt = c >> 1;
-  dsrc = nullptr;
-  gp = nullptr;
-  if (tt < cnt) {
-    dsrc = (c & 1) ? d2s[tt] : d1s[tt];
-    gp = gps[tt];
-  }
+__device__ __forceinline__ void mt_digits(MtDigits &d, const signed char *dsrc, const float4 *gpsrc, int g0, int n,
+                                          int lane) {
+  const int kb = lane >> 4;
+  const bool second = lane & 1;
+#pragma unroll
+  for (int i = 0; i < kMtBatch; i++)
+    if (i < n) {
+      const int g = g0 + i;
+      d.b0[i] = v4i{0, 0, 0, 0};
+      d.b1[i] = v4i{0, 0, 0, 0};
+      d.dsc[i] = 0.0f;
+      d.Q[i] = 0;
+      if (dsrc) {
+        d.b0[i] = *(const v4i *)(dsrc + g * kGroup + kb * 16);
+        d.b1[i] = *(const v4i *)(dsrc + g * kGroup + 64 + kb * 16);
+      }
+      if (gpsrc) {
+        float4 p = gpsrc[g];
+        d.dsc[i] = second ? p.y : p.x;
+        d.Q[i] = __float_as_int(second ? p.w : p.z);
+      }
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void mt_compute(const MtTiles<FMT> &t, const MtDigits &d, int n, float acc[4]) {
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+#pragma unroll
+  for (int i = 0; i < kMtBatch; i++)
+    if (i < n) {
+      v4i a0, a1;
+      unpack_words<FMT>(t.q[i], a0, a1);
+      v4i c = {0, 0, 0, 0};
+      c = mfma_i8(a0, d.b0[i], c);
+      c = mfma_i8(a1, d.b1[i], c);
+      const float scv[4] = {t.sc[i].x, t.sc[i].y, t.sc[i].z, t.sc[i].w};
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float f = (float)(c[r] - OFF * d.Q[i]) * d.dsc[i];
+        float tsum = f + dpp_row_shr1(f);
+        acc[r] = __builtin_fmaf(tsum, scv[r], acc[r]);
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -764,103 +875,179 @@ __global__ void k_prep_hidden(Work w) {
                   w.hgp + (size_t)p * w.ngi);
 }
 
+// Workgroup barrier for LDS traffic only: __syncthreads() would also wait for
+// the next row tile's loads, which are meant to stay in flight across it.
+__device__ __forceinline__ void lds_only_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// h = silu(g)*u for one row tile of an item from the 8 waves' partial sums.
+__device__ __forceinline__ void gu_store(float (*part)[2][64][4], const float ag[4], const float au[4], int rt,
+                                         int p0, int cnt, const Work &w, int lane, int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    part[wave][0][lane][i] = ag[i];
+    part[wave][1][lane][i] = au[i];
+  }
+  lds_only_barrier();
+  if (wave == 0 && (lane & 1) && ((lane & 15) >> 1) < cnt) {
+    int tt = (lane & 15) >> 1, kb = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float g = part[0][0][lane][i], u = part[0][1][lane][i];
+      for (int v = 1; v < 8; v++) {
+        g += part[v][0][lane][i];
+        u += part[v][1][lane][i];
+      }
+      int row = rt * kTileRows + 4 * kb + i;
+      w.hroute[(size_t)(p0 + tt) * w.I + row] = silu_ref(g) * u;
+    }
+  }
+  lds_only_barrier();
+}
+
 // ---------------------------------------------------------------------------
-// 7. routed gate/up: item = (expert, <=8 tokens); 4 waves split the H groups,
-// then h = silu(g)*u per token.  grid (I/16, min(items bound, 1024)), 256 thr.
+// 7. routed gate/up: item = (expert, <=8 tokens) x kGuRowTiles row tiles; 8
+// waves split the H groups.  A wave loads its groups' token digits once per
+// item and keeps the next row tile's gate and up tiles in flight while it
+// computes the current one; then h = silu(g)*u per token.
+// grid (ceil(I/16/kGuRowTiles), min(items bound, 1024)), 512 threads.
 // ---------------------------------------------------------------------------
-template <int FMT>
-__global__ void k_expert_gateup(Work w, ExpertLayout xl) {
-  __shared__ float part[4][2][64][4];
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int rt = blockIdx.x;
+constexpr int kGuRowTiles = 8;
+template <int FMT, bool WIDE>
+__global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl) {
+  __shared__ float part[8][2][64][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nrt = w.I / kTileRows;
+  const int rt0 = blockIdx.x * kGuRowTiles, rt1 = min(nrt, rt0 + kGuRowTiles);
+  const int per = (w.ngh + 7) / 8, g0 = min(w.ngh, wave * per), g1 = min(w.ngh, g0 + per);
+  const int n = g1 - g0;
   int n_items = *w.nitems;
   for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
     int4 item = w.items[it];
     int e = item.x, p0 = item.y, cnt = item.z;
-    const signed char *d1s[kMaxTokensPerItem], *d2s[kMaxTokensPerItem];
-    const float4 *gps[kMaxTokensPerItem];
-    for (int j = 0; j < kMaxTokensPerItem; j++) {
-      int tok = j < cnt ? w.btok[p0 + j] : 0;
-      d1s[j] = w.xd1 + (size_t)tok * w.Hp;
-      d2s[j] = w.xd2 + (size_t)tok * w.Hp;
-      gps[j] = w.xgp + (size_t)tok * w.ngh;
+    // B column c = lane%16: token c/2 of the item, digit c%2
+    const int tt = (lane & 15) >> 1;
+    const signed char *dsrc = nullptr;
+    const float4 *gp = nullptr;
+    if (tt < cnt) {
+      const int tok = w.btok[p0 + tt];
+      dsrc = ((lane & 1) ? w.xd2 : w.xd1) + (size_t)tok * w.Hp;
+      gp = w.xgp + (size_t)tok * w.ngh;
     }
-    const signed char *dsrc;
-    const float4 *gp;
-    lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
-    int per = (w.ngh + 3) / 4, g0 = wave * per, g1 = min(w.ngh, g0 + per);
-    float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
-    if (g0 < g1) {
-      tile_gemv<FMT>(xl.mat(e, 0), rt, w.ngh, g0, g1, dsrc, gp, ag, lane);
-      tile_gemv<FMT>(xl.mat(e, 1), rt, w.ngh, g0, g1, dsrc, gp, au, lane);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      part[wave][0][lane][i] = ag[i];
-      part[wave][1][lane][i] = au[i];
-    }
-    __syncthreads();
-    if (wave == 0 && (lane & 1) && ((lane & 15) >> 1) < cnt) {
-      int tt = (lane & 15) >> 1, kb = lane >> 4;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float g = part[0][0][lane][i], u = part[0][1][lane][i];
-        for (int v = 1; v < 4; v++) {
-          g += part[v][0][lane][i];
-          u += part[v][1][lane][i];
+    const TileMat mg = xl.mat(e, 0), mu = xl.mat(e, 1);
+    if constexpr (!WIDE) {  // n <= kMtBatch
+      // pipeline over (row tile, matrix): the up tiles of rt load while its
+      // gate tiles are multiplied, the gate tiles of rt+1 while its up tiles are
+      MtDigits dg;
+      MtTiles<FMT> tg, tu;
+      if (n > 0) {
+        mt_digits(dg, dsrc, gp, g0, n, lane);
+        mt_load<FMT>(tg, mg, (size_t)rt0 * w.ngh + g0, n, lane);
+      }
+      for (int rt = rt0; rt < rt1; rt++) {
+        float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
+        if (n > 0) {
+          mt_load<FMT>(tu, mu, (size_t)rt * w.ngh + g0, n, lane);
+          mt_compute<FMT>(tg, dg, n, ag);
+          if (rt + 1 < rt1) mt_load<FMT>(tg, mg, (size_t)(rt + 1) * w.ngh + g0, n, lane);
+          mt_compute<FMT>(tu, dg, n, au);
         }
-        int row = rt * kTileRows + 4 * kb + i;
-        w.hroute[(size_t)(p0 + tt) * w.I + row] = silu_ref(g) * u;
+        gu_store(part, ag, au, rt, p0, cnt, w, lane, wave);
+      }
+    } else {  // more than kMtBatch groups per wave (H > 4096): batches in turn, no prefetch
+      for (int rt = rt0; rt < rt1; rt++) {
+        float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
+        for (int g = g0; g < g1; g += kMtBatch) {
+          const int m = min(kMtBatch, g1 - g);
+          MtTiles<FMT> tg, tu;
+          MtDigits dg;
+          mt_load<FMT>(tg, mg, (size_t)rt * w.ngh + g, m, lane);
+          mt_load<FMT>(tu, mu, (size_t)rt * w.ngh + g, m, lane);
+          mt_digits(dg, dsrc, gp, g, m, lane);
+          mt_compute<FMT>(tg, dg, m, ag);
+          mt_compute<FMT>(tu, dg, m, au);
+        }
+        gu_store(part, ag, au, rt, p0, cnt, w, lane, wave);
       }
     }
-    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------
 // 8. down: routed items -> rout[p][row]; shared token chunks (IDOT) ->
-// shout[t][row].  grid (H/16, n_item_slots + ceil(T/16)), 64 threads.
+// shout[t][row].  Each wave takes kDnRowTiles consecutive row tiles.
+// grid (ceil(H/16/(4*kDnRowTiles)), n_item_slots + ceil(T/16)), 256 threads.
 // ---------------------------------------------------------------------------
+#ifndef SW_DN_ROW_TILES
+#define SW_DN_ROW_TILES 2
+#endif
+constexpr int kDnRowTiles = SW_DN_ROW_TILES;  // row tiles per wave
 template <int FMT>
-__global__ void k_down(Work w, ExpertLayout xl, int item_slots, const signed char *dq, const float *ds) {
-  int lane = threadIdx.x;
-  int rt = blockIdx.x;
-  int kb = lane >> 4;
+__global__ __launch_bounds__(256) void k_down(Work w, ExpertLayout xl, int item_slots, const signed char *dq,
+                                              const float *ds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kb = lane >> 4;
+  const int nrt = w.H / kTileRows;
+  const int rt0 = min(nrt, (blockIdx.x * 4 + wave) * kDnRowTiles), rt1 = min(nrt, rt0 + kDnRowTiles);
   if ((int)blockIdx.y >= item_slots) {
     int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens;
-    v4i c = {0, 0, 0, 0};
-    idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
     int tok = t0 + (lane & 15);
-    if (tok < w.T) {
+    for (int rt = rt0; rt < rt1; rt++) {
+      v4i c = {0, 0, 0, 0};
+      idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
+      if (tok < w.T) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int row = rt * kTileRows + 4 * kb + i;
-        w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+        for (int i = 0; i < 4; i++) {
+          int row = rt * kTileRows + 4 * kb + i;
+          w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+        }
       }
     }
     return;
   }
+  // the wave's units (row tile, batch of groups) in order; unit u+1's tiles
+  // and digits load while unit u is multiplied
+  const int nb = (w.ngi + kMtBatch - 1) / kMtBatch;
+  const int units = (rt1 - rt0) * nb;
   int n_items = *w.nitems;
   for (int it = blockIdx.y; it < n_items; it += item_slots) {
     int4 item = w.items[it];
     int e = item.x, p0 = item.y, cnt = item.z;
-    const signed char *d1s[kMaxTokensPerItem], *d2s[kMaxTokensPerItem];
-    const float4 *gps[kMaxTokensPerItem];
-    for (int j = 0; j < kMaxTokensPerItem; j++) {
-      int p = p0 + (j < cnt ? j : 0);
-      d1s[j] = w.hd1 + (size_t)p * w.Ip;
-      d2s[j] = w.hd2 + (size_t)p * w.Ip;
-      gps[j] = w.hgp + (size_t)p * w.ngi;
+    const int tt = (lane & 15) >> 1;
+    const signed char *dsrc = nullptr;
+    const float4 *gp = nullptr;
+    if (tt < cnt) {
+      dsrc = ((lane & 1) ? w.hd2 : w.hd1) + (size_t)(p0 + tt) * w.Ip;
+      gp = w.hgp + (size_t)(p0 + tt) * w.ngi;
     }
-    const signed char *dsrc;
-    const float4 *gp;
-    lane_digit_src(lane, cnt, d1s, d2s, gps, dsrc, gp);
+    const TileMat md = xl.mat(e, 2);
+    auto unit_load = [&](MtTiles<FMT> &t, MtDigits &d, int u) {
+      const int rt = rt0 + u / nb, g = (u % nb) * kMtBatch, n = min(kMtBatch, w.ngi - g);
+      mt_load<FMT>(t, md, (size_t)rt * w.ngi + g, n, lane);
+      mt_digits(d, dsrc, gp, g, n, lane);
+    };
     float acc[4] = {0, 0, 0, 0};
-    tile_gemv<FMT>(xl.mat(e, 2), rt, w.ngi, 0, w.ngi, dsrc, gp, acc, lane);
-    if ((lane & 1) && ((lane & 15) >> 1) < cnt) {
-      int tt = (lane & 15) >> 1;
+    auto unit_compute = [&](const MtTiles<FMT> &t, const MtDigits &d, int u) {
+      const int rt = rt0 + u / nb, b = u % nb, g = b * kMtBatch, n = min(kMtBatch, w.ngi - g);
+      if (b == 0) acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+      mt_compute<FMT>(t, d, n, acc);
+      if (b == nb - 1 && (lane & 1) && tt < cnt) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + i] = acc[i];
+        for (int i = 0; i < 4; i++) w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + i] = acc[i];
+      }
+    };
+    MtTiles<FMT> ta, tb;
+    MtDigits da, db;
+    if (units > 0) unit_load(ta, da, 0);
+    for (int u = 0; u < units; u += 2) {
+      if (u + 1 < units) unit_load(tb, db, u + 1);
+      unit_compute(ta, da, u);
+      if (u + 1 >= units) break;
+      if (u + 2 < units) unit_load(ta, da, u + 2);
+      unit_compute(tb, db, u + 1);
     }
   }
 }
@@ -1084,16 +1271,40 @@ static Work make_work(const ColiMoeLayer *L, int T) {
 
 // dynamic LDS above 64 KiB must be enabled per kernel (gfx950: 160 KiB/CU)
 static int set_lds(const void *fn, size_t bytes) {
-  if (bytes > 160 * 1024) return fail_arg("MoE bucketing needs %zu bytes of LDS (> 160 KiB)", bytes);
+  if (bytes > 160 * 1024) return fail_arg("MoE step kernel needs %zu bytes of LDS (> 160 KiB)", bytes);
   if (bytes <= 64 * 1024) return 0;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   return e == hipSuccess ? 0 : fail_hip("hipFuncSetAttribute", e);
 }
 
+template <int CH>
+static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
+  const size_t lds = (size_t)kRbRound * 64 * (CH + 1) * 4;
+  if (set_lds((const void *)k_router_bounds_tiled<CH>, lds)) return -1;
+  // about 1024 blocks; a block's rows are read once per block
+  const int bx = (w.E + 1 + 7) / 8;
+  int tpb = (int)(((long long)w.T * bx + 1023) / 1024);
+  tpb = (tpb + kRbRound - 1) / kRbRound * kRbRound;
+  if (tpb < kRbRound) tpb = kRbRound;
+  const int by = (w.T + tpb - 1) / tpb;
+  k_router_bounds_tiled<CH><<<dim3(bx, by), 512, lds, ctx->stream>>>(w, x, L->router, L->sgate_row, tpb);
+  return 0;
+}
+
 static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
   hipStream_t st = ctx->stream;
   k_prep_x<<<w.T, 256, 0, st>>>(w, x);
-  k_router_bounds<<<dim3((w.E + 1 + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router, L->sgate_row);
+  int rc = 1;  // 1: shape or alignment outside the tiled router kernel
+  if (((uintptr_t)x & 15) == 0) switch (w.H) {
+      case 256: rc = router_bounds_tiled<4>(ctx, L, w, x); break;
+      case 512: rc = router_bounds_tiled<8>(ctx, L, w, x); break;
+      case 1024: rc = router_bounds_tiled<16>(ctx, L, w, x); break;
+      case 2048: rc = router_bounds_tiled<32>(ctx, L, w, x); break;
+      case 4096: rc = router_bounds_tiled<64>(ctx, L, w, x); break;
+      default: break;
+    }
+  if (rc < 0) return -1;
+  if (rc > 0) k_router_bounds<<<dim3((w.E + 1 + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router, L->sgate_row);
   k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
   k_exact_logits<<<dim3((w.E + 63) / 64, w.T), 64, 0, st>>>(w, x, L->router);
   k_topk_exact<<<w.T, 512, 0, st>>>(w);
@@ -1164,18 +1375,23 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
+  const int gu_blocks_x = (w.I / kTileRows + kGuRowTiles - 1) / kGuRowTiles;
+  const bool wide = (w.ngh + 7) / 8 > kMtBatch;  // a wave's groups exceed one batch
   if (L->sh.expert_format == 4)
-    k_expert_gateup<4><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->xl);
+    wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl)
+         : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl);
   else
-    k_expert_gateup<3><<<dim3(w.I / kTileRows, slots), 256, 0, st>>>(w, L->xl);
+    wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl)
+         : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl);
   mark(ctx, 4);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
+  const int dn_blocks_x = (w.H / kTileRows + 4 * kDnRowTiles - 1) / (4 * kDnRowTiles);
   if (L->sh.expert_format == 4)
-    k_down<4><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+    k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   else
-    k_down<3><<<dim3(w.H / kTileRows, slots + sh_chunks), 64, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+    k_down<3><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   mark(ctx, 6);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
   mark(ctx, 7);
