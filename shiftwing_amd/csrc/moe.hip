@@ -230,6 +230,7 @@ struct Work {
   signed char *xd1, *xd2; float4 *xgp;
   // router
   double2 *lb; float *sgate; int *certified; float *logits;
+  int *mset, *mcount;  // per token: experts of the targeted exact path (<= 64)
   int *idx; float *w;
   // bucket
   int *offsets, *btok, *bslot, *pos; int4 *items; int *nitems;
@@ -257,6 +258,8 @@ size_t carve(Work &w, char *base) {
   w.lb = (double2 *)take((size_t)T * (w.E + 1) * 16);
   w.sgate = (float *)take((size_t)T * 4);
   w.certified = (int *)take((size_t)T * 4);
+  w.mset = (int *)take((size_t)T * 64 * 4);
+  w.mcount = (int *)take((size_t)T * 4);
   w.logits = (float *)take((size_t)T * w.E * 4);
   w.idx = (int *)take((size_t)R * 4);
   w.w = (float *)take((size_t)R * 4);
@@ -496,19 +499,140 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// 4. exact fallback: the reference's fp32 serial dot for every expert of an
-// uncertified token (one lane per expert; blocks of 64 experts).
-// grid (ceil(E/64), T), 64 threads.
-// ---------------------------------------------------------------------------
-__global__ void k_exact_logits(Work w, const float *x, const float *router) {
-  int t = blockIdx.y;
-  if (w.certified[t]) return;
-  int e = blockIdx.x * 64 + threadIdx.x;
-  if (e >= w.E) return;
-  const float *xt = x + (size_t)t * w.H;
-  const float *row = router + (size_t)e * w.H;
-  int m = (w.H / 8) * 8;
+__device__ __forceinline__ double wave_max_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Certification with one wave per token (E <= 64*NV): the same tests as
+// k_certify.  A token the bounds do not certify gets the targeted exact set
+// M = {e : L_e + B_e >= lo - m}, lo the lowest lower bound among the K
+// candidates and m = 2^-20 (1 + 4 max_e(|L_e| + B_e)), which is at least the
+// separation margin of any pair: every expert outside M has an exact logit
+// below each candidate's by more than the margin, so the exact top-k lies in
+// M.  certified[t]: 1 certified, 2 targeted (M in mset, |M| <= 64), 0 every
+// chain.  grid ceil(T/4), 256 threads.
+template <int NV>
+__global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned long long *stats) {
+  __shared__ int cand_s[4][kMaxTopK + 1];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= w.T) return;
+  int *cand = cand_s[wv];
+  const double2 *lb = w.lb + (size_t)t * (w.E + 1);
+  double2 v[NV];
+  double amax = 0.0;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    int e = lane + 64 * j;
+    v[j] = e < w.E ? lb[e] : make_double2(0.0, 0.0);
+    if (e < w.E) amax = fmax(amax, fabs(v[j].x) + v[j].y);
+  }
+  amax = wave_max_d(amax);
+  const int nc = min(w.K + 1, w.E);
+  unsigned chosen = 0;
+  for (int r = 0; r < nc; r++) {
+    VI best = {0.0, -1};
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      int e = lane + 64 * j;
+      if (e < w.E && !((chosen >> j) & 1)) best = vi_better(best, VI{v[j].x, e});
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      VI y;
+      y.v = __shfl_xor(best.v, o, 64);
+      y.i = __shfl_xor(best.i, o, 64);
+      best = vi_better(best, y);
+    }
+    if (best.i >= 0 && (best.i & 63) == lane) chosen |= 1u << (best.i >> 6);
+    if (lane == 0) cand[r] = best.i;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // largest upper bound outside the top K
+  const int candK = nc > w.K ? cand[w.K] : -1;
+  double up = -__builtin_huge_val();
+  int upi = -1;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    int e = lane + 64 * j;
+    bool in_top = ((chosen >> j) & 1) && e != candK;
+    if (e < w.E && !in_top && v[j].x + v[j].y > up) {
+      up = v[j].x + v[j].y;
+      upi = e;
+    }
+  }
+  up = wave_max_d(up);
+  upi = wave_max_i(upi);
+  // lane 0 certifies; every lane needs the verdict for the targeted set
+  int verdict = 0;
+  double lo = 0.0;
+  if (lane == 0) {
+    double mx = lb[cand[0]].x;
+    bool ok = mode == 0 && w.K <= w.E;
+    for (int r = 0; ok && r + 1 < w.K; r++) {
+      double2 a = lb[cand[r]], b = lb[cand[r + 1]];
+      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
+      ok = (a.x - a.y) - (b.x + b.y) > margin;
+    }
+    if (ok && upi >= 0) {
+      double2 a = lb[cand[w.K - 1]];
+      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(up) + 2.0 * fabs(mx));
+      ok = (a.x - a.y) - up > margin;
+    }
+    if (ok) ok = (lb[cand[w.K - 1]].x - lb[cand[w.K - 1]].y) - (mx + lb[cand[0]].y) > -80.0;
+    verdict = ok ? 1 : 0;
+    if (ok) {
+      double p[kMaxTopK], den = 0.0;
+      for (int r = 0; r < w.K; r++) {
+        p[r] = exp(lb[cand[r]].x - mx);
+        den += p[r];
+      }
+      for (int r = 0; r < w.K; r++) {
+        w.idx[(size_t)t * w.K + r] = cand[r];
+        w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
+      }
+    } else if (mode == 0 && w.K <= w.E) {
+      lo = __builtin_huge_val();
+      for (int r = 0; r < w.K; r++) lo = fmin(lo, lb[cand[r]].x - lb[cand[r]].y);
+      verdict = 2;
+    }
+  }
+  verdict = __shfl(verdict, 0, 64);
+  if (verdict == 2) {
+    lo = __shfl(lo, 0, 64) - 0x1p-20 * (1.0 + 4.0 * amax);
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      int e = lane + 64 * j;
+      bool in_m = e < w.E && v[j].x + v[j].y >= lo;
+      unsigned long long bal = __ballot(in_m);
+      int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+      if (in_m && pos < 64) w.mset[(size_t)t * 64 + pos] = e;
+      base += __popcll(bal);
+    }
+    if (base > 64) verdict = 0;
+    if (lane == 0) w.mcount[t] = base;
+  }
+  if (lane == 0) {
+    w.certified[t] = verdict;
+    atomicAdd(&stats[0], 1ull);
+    if (verdict != 1) atomicAdd(&stats[1], 1ull);
+    if (verdict == 0) atomicAdd(&stats[2], 1ull);
+  }
+}
+
+// The reference's fp32 serial dot (c/qwen.c:1674 at -O3): s = rn(s + rn(x*w))
+// over the first H - H%8 terms in order, then fused multiply-adds.
+__device__ float exact_chain(const float *xt, const float *row, int H) {
+  int m = (H / 8) * 8;
   float s = 0.0f;
   int i = 0;
   for (; i + 4 <= m; i += 4) {
@@ -520,8 +644,50 @@ __global__ void k_exact_logits(Work w, const float *x, const float *router) {
     s = __fadd_rn(s, __fmul_rn(xv.w, wv.w));
   }
   for (; i < m; i++) s = __fadd_rn(s, __fmul_rn(xt[i], row[i]));
-  for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
-  w.logits[(size_t)t * w.E + e] = s;
+  for (; i < H; i++) s = __fmaf_rn(xt[i], row[i], s);
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// 4. exact logits for the tokens the bounds did not certify: the experts of
+// the targeted set (certified 2) or every expert (certified 0).  The products
+// rn(x*w) are independent of the chain order: the block's lanes form them
+// with coalesced loads into LDS, then one lane runs the serial sum over LDS,
+// s = rn(s + p_i), and the fused tail.  Same result as exact_chain.
+// grid (64, T), 64 threads, dynamic LDS 4*H bytes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, const float *router) {
+  extern __shared__ float prod[];
+  const int t = blockIdx.y;
+  const int c = w.certified[t];
+  if (c == 1) return;
+  const int n = c == 2 ? w.mcount[t] : w.E;
+  const float *xt = x + (size_t)t * w.H;
+  const int m = (w.H / 8) * 8;
+  for (int k = blockIdx.x; k < n; k += gridDim.x) {
+    const int e = c == 2 ? w.mset[(size_t)t * 64 + k] : k;
+    const float *row = router + (size_t)e * w.H;
+    for (int i = threadIdx.x * 4; i < m; i += 256) {
+      float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
+      *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
+                                          __fmul_rn(a.w, b.w));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.0f;
+      int i = 0;
+      for (; i < m; i += 4) {
+        float4 p = *(const float4 *)(prod + i);
+        s = __fadd_rn(s, p.x);
+        s = __fadd_rn(s, p.y);
+        s = __fadd_rn(s, p.z);
+        s = __fadd_rn(s, p.w);
+      }
+      for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+      w.logits[(size_t)t * w.E + e] = s;
+    }
+    __syncthreads();
+  }
 }
 
 // router_topk (c/qwen.c:3421-3426) on fp32 logits, bit-exact: serial max and
@@ -576,11 +742,65 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
   __syncthreads();
 }
 
-__global__ void k_topk_exact(Work w) {
+// Tokens on the targeted path: M ordered by (exact logit desc, index asc);
+// the order and the k|k+1 boundary hold if consecutive exact logits are
+// separated by the margin and the K-th lies within 80 of the max (experts
+// outside M are below every candidate by more than the margin).  Weights then
+// come from the fp64 logits as for certified tokens.  Otherwise, and for
+// tokens on the full path, every chain and the router_topk replica.
+// grid T, 512 threads.
+__global__ void k_topk_exact(Work w, const float *x, const float *router, unsigned long long *stats) {
   __shared__ VI red[16];
   __shared__ float prob[4096];
+  __shared__ int s_ok;
   int t = blockIdx.x;
-  if (w.certified[t]) return;
+  const int c = w.certified[t];
+  if (c == 1) return;
+  if (c == 2) {
+    if (threadIdx.x == 0) {
+      int n = w.mcount[t];
+      int ms[64];
+      float ls[64];
+      for (int i = 0; i < n; i++) {
+        int e = w.mset[(size_t)t * 64 + i];
+        float l = w.logits[(size_t)t * w.E + e];
+        int j = i;
+        for (; j > 0 && (ls[j - 1] < l || (ls[j - 1] == l && ms[j - 1] > e)); j--) {
+          ls[j] = ls[j - 1];
+          ms[j] = ms[j - 1];
+        }
+        ls[j] = l;
+        ms[j] = e;
+      }
+      const double mx = ls[0];
+      bool ok = n >= w.K;
+      for (int r = 0; ok && r < w.K && r + 1 < n; r++) {
+        double a = ls[r], b = ls[r + 1];
+        ok = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
+      }
+      if (ok) ok = (double)ls[w.K - 1] - mx > -80.0;
+      if (ok) {
+        const double2 *lb = w.lb + (size_t)t * (w.E + 1);
+        double lmx = lb[ms[0]].x, p[kMaxTopK], den = 0.0;
+        for (int r = 0; r < w.K; r++) {
+          p[r] = exp(lb[ms[r]].x - lmx);
+          den += p[r];
+        }
+        for (int r = 0; r < w.K; r++) {
+          w.idx[(size_t)t * w.K + r] = ms[r];
+          w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
+        }
+      } else {
+        atomicAdd(&stats[2], 1ull);
+      }
+      s_ok = ok;
+    }
+    __syncthreads();
+    if (s_ok) return;
+    for (int e = threadIdx.x; e < w.E; e += blockDim.x)
+      w.logits[(size_t)t * w.E + e] = exact_chain(x + (size_t)t * w.H, router + (size_t)e * w.H, w.H);
+    __syncthreads();
+  }
   topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
                    prob, red);
 }
@@ -982,7 +1202,7 @@ __global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl) 
 // grid (ceil(H/16/(4*kDnRowTiles)), n_item_slots + ceil(T/16)), 256 threads.
 // ---------------------------------------------------------------------------
 #ifndef SW_DN_ROW_TILES
-#define SW_DN_ROW_TILES 2
+#define SW_DN_ROW_TILES 1
 #endif
 constexpr int kDnRowTiles = SW_DN_ROW_TILES;  // row tiles per wave
 template <int FMT>
@@ -1305,9 +1525,15 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
     }
   if (rc < 0) return -1;
   if (rc > 0) k_router_bounds<<<dim3((w.E + 1 + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router, L->sgate_row);
-  k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
-  k_exact_logits<<<dim3((w.E + 63) / 64, w.T), 64, 0, st>>>(w, x, L->router);
-  k_topk_exact<<<w.T, 512, 0, st>>>(w);
+  if (w.E <= 512)
+    k_certify_wave<8><<<(w.T + 3) / 4, 256, 0, st>>>(w, L->router_mode, L->stats);
+  else if (w.E <= 1024)
+    k_certify_wave<16><<<(w.T + 3) / 4, 256, 0, st>>>(w, L->router_mode, L->stats);
+  else
+    k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
+  if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
+  k_exact_logits<<<dim3(64, w.T), 64, (size_t)w.H * 4, st>>>(w, x, L->router);
+  k_topk_exact<<<w.T, 512, 0, st>>>(w, x, L->router, L->stats);
   return launch_status("MoE routing kernels");
 }
 

@@ -139,3 +139,16 @@ def test_stack_forward_equals_per_layer_calls(be):
             assert np.array_equal(got[l].view(np.uint32), want.view(np.uint32)), (step, l)
     for L in layers:
         L.close()
+
+
+def test_router_paths_many_token_kernels(be, oracle):
+    """The same steered cases through the many-token kernels (one wave per
+    token certifies; targeted exact chains of the ambiguous experts; every
+    chain and the router_topk replica when those do not settle the order)."""
+    be.set_decode_kernels(0)
+    try:
+        seen = _run_cases(be, oracle, (512, 32, 4, 128, 128, 4), seeds=[11, 12, 13])
+    finally:
+        be.set_decode_kernels(1)
+    print("paths taken:", seen, flush=True)
+    assert seen["certified"] > 0 and seen["targeted"] > 0 and seen["full"] > 0, seen
