@@ -521,10 +521,12 @@ __device__ __forceinline__ int wave_max_i(int v) {
 template <int NV>
 __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned long long *stats) {
   __shared__ int cand_s[4][kMaxTopK + 1];
+  __shared__ double2 cv_s[4][kMaxTopK + 1];  // the candidates' (L, B)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wv;
   if (t >= w.T) return;
   int *cand = cand_s[wv];
+  double2 *cv = cv_s[wv];
   const double2 *lb = w.lb + (size_t)t * (w.E + 1);
   double2 v[NV];
   double amax = 0.0;
@@ -551,7 +553,13 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
       y.i = __shfl_xor(best.i, o, 64);
       best = vi_better(best, y);
     }
-    if (best.i >= 0 && (best.i & 63) == lane) chosen |= 1u << (best.i >> 6);
+    if (best.i >= 0 && (best.i & 63) == lane) {
+      const int jb = best.i >> 6;
+      chosen |= 1u << jb;
+#pragma unroll
+      for (int j = 0; j < NV; j++)
+        if (j == jb) cv[r] = v[j];
+    }
     if (lane == 0) cand[r] = best.i;
   }
   __builtin_amdgcn_wave_barrier();
@@ -575,33 +583,30 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
   int verdict = 0;
   double lo = 0.0;
   if (lane == 0) {
-    double mx = lb[cand[0]].x;
+    double mx = cv[0].x;
     bool ok = mode == 0 && w.K <= w.E;
-    for (int r = 0; ok && r + 1 < w.K; r++) {
-      double2 a = lb[cand[r]], b = lb[cand[r + 1]];
+    for (int r = 0; r + 1 < w.K; r++) {
+      double2 a = cv[r], b = cv[r + 1];
       double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
-      ok = (a.x - a.y) - (b.x + b.y) > margin;
+      ok = ok && (a.x - a.y) - (b.x + b.y) > margin;
     }
     if (ok && upi >= 0) {
-      double2 a = lb[cand[w.K - 1]];
+      double2 a = cv[w.K - 1];
       double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(up) + 2.0 * fabs(mx));
       ok = (a.x - a.y) - up > margin;
     }
-    if (ok) ok = (lb[cand[w.K - 1]].x - lb[cand[w.K - 1]].y) - (mx + lb[cand[0]].y) > -80.0;
+    if (ok) ok = (cv[w.K - 1].x - cv[w.K - 1].y) - (mx + cv[0].y) > -80.0;
     verdict = ok ? 1 : 0;
     if (ok) {
-      double p[kMaxTopK], den = 0.0;
-      for (int r = 0; r < w.K; r++) {
-        p[r] = exp(lb[cand[r]].x - mx);
-        den += p[r];
-      }
+      double den = 0.0;
+      for (int r = 0; r < w.K; r++) den += exp(cv[r].x - mx);
       for (int r = 0; r < w.K; r++) {
         w.idx[(size_t)t * w.K + r] = cand[r];
-        w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
+        w.w[(size_t)t * w.K + r] = (float)(exp(cv[r].x - mx) / den);
       }
     } else if (mode == 0 && w.K <= w.E) {
       lo = __builtin_huge_val();
-      for (int r = 0; r < w.K; r++) lo = fmin(lo, lb[cand[r]].x - lb[cand[r]].y);
+      for (int r = 0; r < w.K; r++) lo = fmin(lo, cv[r].x - cv[r].y);
       verdict = 2;
     }
   }
@@ -757,38 +762,39 @@ __global__ void k_topk_exact(Work w, const float *x, const float *router, unsign
   const int c = w.certified[t];
   if (c == 1) return;
   if (c == 2) {
+    __shared__ int um[64], sm[64];
+    __shared__ float ul[64], sl[64];
+    const int n = w.mcount[t], i = threadIdx.x;
+    if (i < n) {
+      um[i] = w.mset[(size_t)t * 64 + i];
+      ul[i] = w.logits[(size_t)t * w.E + um[i]];
+    }
+    __syncthreads();
+    if (i < n) {  // rank by (exact logit desc, index asc)
+      const int e = um[i];
+      const float l = ul[i];
+      int rank = 0;
+      for (int j = 0; j < n; j++) rank += ul[j] > l || (ul[j] == l && um[j] < e);
+      sm[rank] = e;
+      sl[rank] = l;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-      int n = w.mcount[t];
-      int ms[64];
-      float ls[64];
-      for (int i = 0; i < n; i++) {
-        int e = w.mset[(size_t)t * 64 + i];
-        float l = w.logits[(size_t)t * w.E + e];
-        int j = i;
-        for (; j > 0 && (ls[j - 1] < l || (ls[j - 1] == l && ms[j - 1] > e)); j--) {
-          ls[j] = ls[j - 1];
-          ms[j] = ms[j - 1];
-        }
-        ls[j] = l;
-        ms[j] = e;
-      }
-      const double mx = ls[0];
+      const double mx = sl[0];
       bool ok = n >= w.K;
       for (int r = 0; ok && r < w.K && r + 1 < n; r++) {
-        double a = ls[r], b = ls[r + 1];
+        double a = sl[r], b = sl[r + 1];
         ok = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
       }
-      if (ok) ok = (double)ls[w.K - 1] - mx > -80.0;
+      if (ok) ok = (double)sl[w.K - 1] - mx > -80.0;
       if (ok) {
         const double2 *lb = w.lb + (size_t)t * (w.E + 1);
-        double lmx = lb[ms[0]].x, p[kMaxTopK], den = 0.0;
+        const double lmx = lb[sm[0]].x;
+        double den = 0.0;
+        for (int r = 0; r < w.K; r++) den += exp(lb[sm[r]].x - lmx);
         for (int r = 0; r < w.K; r++) {
-          p[r] = exp(lb[ms[r]].x - lmx);
-          den += p[r];
-        }
-        for (int r = 0; r < w.K; r++) {
-          w.idx[(size_t)t * w.K + r] = ms[r];
-          w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
+          w.idx[(size_t)t * w.K + r] = sm[r];
+          w.w[(size_t)t * w.K + r] = (float)(exp(lb[sm[r]].x - lmx) / den);
         }
       } else {
         atomicAdd(&stats[2], 1ull);
@@ -834,17 +840,46 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
     cnt[e] = c;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0, ia = 0;
-    for (int e = 0; e < E; e++) {
+  {  // exclusive scans of the counts and item counts: thread i owns experts [per*i, per*i+per)
+    __shared__ int wsum[2][16];
+    const int nthr = blockDim.x, per = (E + nthr - 1) / nthr;
+    const int e0 = threadIdx.x * per, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int c = 0, ni = 0;
+    for (int e = e0; e < e0 + per && e < E; e++) {
+      c += cnt[e];
+      ni += (cnt[e] + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+    }
+    int ic = c, ii = ni;  // inclusive wave scans
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      int a = __shfl_up(ic, o, 64), b = __shfl_up(ii, o, 64);
+      if (lane >= o) {
+        ic += a;
+        ii += b;
+      }
+    }
+    if (lane == 63) {
+      wsum[0][wave] = ic;
+      wsum[1][wave] = ii;
+    }
+    __syncthreads();
+    int bc = 0, bi = 0;
+    for (int v = 0; v < wave; v++) {
+      bc += wsum[0][v];
+      bi += wsum[1][v];
+    }
+    int acc = bc + ic - c, ia = bi + ii - ni;
+    for (int e = e0; e < e0 + per && e < E; e++) {
       offsets[e] = acc;
       iofs[e] = ia;
       acc += cnt[e];
       ia += (cnt[e] + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
     }
-    offsets[E] = acc;
-    iofs[E] = ia;
-    *nitems = ia;
+    if (e0 < E && e0 + per >= E) {  // the thread owning the last expert
+      offsets[E] = acc;
+      iofs[E] = ia;
+      *nitems = ia;
+    }
   }
   __syncthreads();
   for (int r = threadIdx.x; r < T * K; r += blockDim.x) {
@@ -1513,7 +1548,7 @@ static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const fl
 
 static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
   hipStream_t st = ctx->stream;
-  k_prep_x<<<w.T, 256, 0, st>>>(w, x);
+  k_prep_x<<<w.T, 1024, 0, st>>>(w, x);
   int rc = 1;  // 1: shape or alignment outside the tiled router kernel
   if (((uintptr_t)x & 15) == 0) switch (w.H) {
       case 256: rc = router_bounds_tiled<4>(ctx, L, w, x); break;
