@@ -1037,6 +1037,45 @@ __device__ __forceinline__ void mt_digits(MtDigits &d, const signed char *dsrc, 
     }
 }
 
+// kMtBatch tile-groups of one group column g in consecutive row tiles
+// (tile-group stride ng), for the down projection, whose waves split groups.
+template <int FMT>
+__device__ __forceinline__ void mt_load_rows(MtTiles<FMT> &t, const TileMat &mat, size_t tg0, int ng, int n,
+                                             int lane) {
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+  const int kb = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < kMtBatch; i++)
+    if (i < n) {
+      load_words<FMT>(tm_codes(mat, tg0 + (size_t)i * ng) + lane * BPL, t.q[i]);
+      t.sc[i] = *(const float4 *)(tm_scales(mat, tg0 + (size_t)i * ng) + 4 * kb);
+    }
+}
+
+// mt_compute for tiles of one group (digits d slot 0) in kMtBatch row tiles:
+// acc[i] of row tile i.
+template <int FMT>
+__device__ __forceinline__ void mt_compute_rows(const MtTiles<FMT> &t, const MtDigits &d, int n,
+                                                float acc[kMtBatch][4]) {
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+#pragma unroll
+  for (int i = 0; i < kMtBatch; i++)
+    if (i < n) {
+      v4i a0, a1;
+      unpack_words<FMT>(t.q[i], a0, a1);
+      v4i c = {0, 0, 0, 0};
+      c = mfma_i8(a0, d.b0[0], c);
+      c = mfma_i8(a1, d.b1[0], c);
+      const float scv[4] = {t.sc[i].x, t.sc[i].y, t.sc[i].z, t.sc[i].w};
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float f = (float)(c[r] - OFF * d.Q[0]) * d.dsc[0];
+        float tsum = f + dpp_row_shr1(f);
+        acc[i][r] = __builtin_fmaf(tsum, scv[r], acc[i][r]);
+      }
+    }
+}
+
 template <int FMT>
 __device__ __forceinline__ void mt_compute(const MtTiles<FMT> &t, const MtDigits &d, int n, float acc[4]) {
   constexpr int OFF = FMT == 4 ? 8 : 4;
@@ -1303,6 +1342,92 @@ __global__ __launch_bounds__(256) void k_down(Work w, ExpertLayout xl, int item_
       if (u + 1 >= units) break;
       if (u + 2 < units) unit_load(ta, da, u + 2);
       unit_compute(tb, db, u + 1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 8b. down for I <= 1024 (at most 8 groups): 8 waves split the groups (wave w
+// takes group w) over kDnBlockRows row tiles of an item, kMtBatch row tiles
+// per batch, the next batch's tiles in flight while the current one
+// multiplies; the waves' partial sums meet in LDS.  Shared token chunks
+// (IDOT) in extra blocks, waves taking row tiles.
+// grid (ceil(H/16/kDnBlockRows), n_item_slots + ceil(T/16)), 512 threads.
+// ---------------------------------------------------------------------------
+constexpr int kDnBlockRows = 16;
+template <int FMT>
+__global__ __launch_bounds__(512) void k_down_split(Work w, ExpertLayout xl, int item_slots, const signed char *dq,
+                                                    const float *ds) {
+  __shared__ float part[8][kMtBatch][64][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kb = lane >> 4;
+  const int nrt = w.H / kTileRows;
+  const int rt0 = blockIdx.x * kDnBlockRows, rt1 = min(nrt, rt0 + kDnBlockRows);
+  if ((int)blockIdx.y >= item_slots) {
+    int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens;
+    int tok = t0 + (lane & 15);
+    for (int rt = rt0 + wave; rt < rt1; rt += 8) {
+      v4i c = {0, 0, 0, 0};
+      idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
+      if (tok < w.T) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          int row = rt * kTileRows + 4 * kb + i;
+          w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+        }
+      }
+    }
+    return;
+  }
+  const bool has = wave < w.ngi;
+  const int g = wave;
+  const int nw = min(8, w.ngi);
+  int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += item_slots) {
+    int4 item = w.items[it];
+    int e = item.x, p0 = item.y, cnt = item.z;
+    const int tt = (lane & 15) >> 1;
+    const signed char *dsrc = nullptr;
+    const float4 *gp = nullptr;
+    if (tt < cnt) {
+      dsrc = ((lane & 1) ? w.hd2 : w.hd1) + (size_t)(p0 + tt) * w.Ip;
+      gp = w.hgp + (size_t)(p0 + tt) * w.ngi;
+    }
+    const TileMat md = xl.mat(e, 2);
+    MtDigits dd;
+    MtTiles<FMT> ta, tb;
+    if (has) {
+      mt_digits(dd, dsrc, gp, g, 1, lane);
+      mt_load_rows<FMT>(ta, md, (size_t)rt0 * w.ngi + g, w.ngi, min(kMtBatch, rt1 - rt0), lane);
+    }
+    for (int rb = rt0; rb < rt1; rb += 2 * kMtBatch) {
+      for (int h = 0; h < 2; h++) {
+        const int r0 = rb + h * kMtBatch;
+        if (r0 >= rt1) break;
+        const int n = min(kMtBatch, rt1 - r0), r1 = r0 + kMtBatch;
+        float acc[kMtBatch][4] = {};
+        if (has) {
+          MtTiles<FMT> &cur = h == 0 ? ta : tb;
+          MtTiles<FMT> &nxt = h == 0 ? tb : ta;
+          if (r1 < rt1) mt_load_rows<FMT>(nxt, md, (size_t)r1 * w.ngi + g, w.ngi, min(kMtBatch, rt1 - r1), lane);
+          mt_compute_rows<FMT>(cur, dd, n, acc);
+        }
+#pragma unroll
+        for (int i = 0; i < kMtBatch; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) part[wave][i][lane][r] = acc[i][r];
+        lds_only_barrier();
+        for (int q = threadIdx.x; q < kMtBatch * 64 * 4; q += 512) {
+          const int i = q >> 8, l = (q >> 2) & 63, r = q & 3;
+          const int tq = (l & 15) >> 1;
+          if (i < n && (l & 1) && tq < cnt) {
+            float v = part[0][i][l][r];
+            for (int u = 1; u < nw; u++) v += part[u][i][l][r];
+            w.rout[(size_t)(p0 + tq) * w.H + (r0 + i) * kTileRows + 4 * (l >> 4) + r] = v;
+          }
+        }
+        lds_only_barrier();
+      }
     }
   }
 }
@@ -1649,10 +1774,14 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
   const int dn_blocks_x = (w.H / kTileRows + 4 * kDnRowTiles - 1) / (4 * kDnRowTiles);
+  const bool dn_split = w.ngi <= 8;
+  const int ds_blocks_x = (w.H / kTileRows + kDnBlockRows - 1) / kDnBlockRows;
   if (L->sh.expert_format == 4)
-    k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+    dn_split ? k_down_split<4><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
+             : k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   else
-    k_down<3><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+    dn_split ? k_down_split<3><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
+             : k_down<3><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   mark(ctx, 6);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
   mark(ctx, 7);
