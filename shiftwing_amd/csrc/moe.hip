@@ -681,6 +681,8 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
     if (threadIdx.x == 0) {
       float s = 0.0f;
       int i = 0;
+      // unrolled so that the LDS reads of 8 steps are issued ahead of their adds
+#pragma unroll 8
       for (; i < m; i += 4) {
         float4 p = *(const float4 *)(prod + i);
         s = __fadd_rn(s, p.x);
@@ -1209,7 +1211,10 @@ __device__ __forceinline__ void gu_store(float (*part)[2][64][4], const float ag
 // computes the current one; then h = silu(g)*u per token.
 // grid (ceil(I/16/kGuRowTiles), min(items bound, 1024)), 512 threads.
 // ---------------------------------------------------------------------------
-constexpr int kGuRowTiles = 8;
+#ifndef SW_GU_ROW_TILES
+#define SW_GU_ROW_TILES 8
+#endif
+constexpr int kGuRowTiles = SW_GU_ROW_TILES;
 template <int FMT, bool WIDE>
 __global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl) {
   __shared__ float part[8][2][64][4];
