@@ -382,7 +382,11 @@ __global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float
       double lp = 0.0, pa = 0.0, aa = 0.0;
 #pragma unroll
       for (int c = 0; c < CH; c++) {
-        double xd = (double)xl[c], wd = (double)wr[c];
+        // converted per token: a hoisted f64 copy of the row would double its
+        // registers and halve the occupancy
+        float wf = wr[c];
+        asm volatile("" : "+v"(wf));
+        double xd = (double)xl[c], wd = (double)wf;
         lp = __builtin_fma(xd, wd, lp);
         aa = __builtin_fma(fabs(xd), fabs(wd), aa);
         pa += fabs(lp);
