@@ -1215,16 +1215,16 @@ __device__ __forceinline__ void gu_store(float (*part)[2][64][4], const float ag
 // computes the current one; then h = silu(g)*u per token.
 // grid (ceil(I/16/kGuRowTiles), min(items bound, 1024)), 512 threads.
 // ---------------------------------------------------------------------------
-#ifndef SW_GU_ROW_TILES
-#define SW_GU_ROW_TILES 8
-#endif
-constexpr int kGuRowTiles = SW_GU_ROW_TILES;
+// Row tiles per block: 8, or 4 for small steps (T*K <= 64), where few items
+// leave the device short of blocks (measured at S397: 4 is faster at B = 4,
+// 8 at B = 32 and T = 512).
+constexpr int kGuRowTiles = 8, kGuRowTilesSmall = 4;
 template <int FMT, bool WIDE>
-__global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl) {
+__global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl, int row_tiles) {
   __shared__ float part[8][2][64][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nrt = w.I / kTileRows;
-  const int rt0 = blockIdx.x * kGuRowTiles, rt1 = min(nrt, rt0 + kGuRowTiles);
+  const int rt0 = blockIdx.x * row_tiles, rt1 = min(nrt, rt0 + row_tiles);
   const int per = (w.ngh + 7) / 8, g0 = min(w.ngh, wave * per), g1 = min(w.ngh, g0 + per);
   const int n = g1 - g0;
   int n_items = *w.nitems;
@@ -1770,14 +1770,15 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
-  const int gu_blocks_x = (w.I / kTileRows + kGuRowTiles - 1) / kGuRowTiles;
+  const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
+  const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
   const bool wide = (w.ngh + 7) / 8 > kMtBatch;  // a wave's groups exceed one batch
   if (L->sh.expert_format == 4)
-    wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl)
-         : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl);
+    wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
+         : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
   else
-    wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl)
-         : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl);
+    wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
+         : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
   mark(ctx, 4);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
   mark(ctx, 5);
