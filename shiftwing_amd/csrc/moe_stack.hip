@@ -1224,25 +1224,34 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
                                              __builtin_amdgcn_readlane(__double2loint(v.x), 0));
           const double mxy = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.y), 0),
                                               __builtin_amdgcn_readlane(__double2loint(v.y), 0));
-          const double kx = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), K - 1),
-                                             __builtin_amdgcn_readlane(__double2loint(v.x), K - 1));
-          const double klo = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), K - 1),
-                                              __builtin_amdgcn_readlane(__double2loint(vlo), K - 1));
+          // The lowest lower bound among the K candidates and their largest
+          // magnitude.  When every consecutive pair is certified the lower
+          // bounds fall with the rank and theta is the K-th one; otherwise a
+          // candidate ranked above K-1 may have the lowest lower bound, and
+          // the set test must use that one.
+          double theta = 1e300, kax = 0.0;
+          for (int r = 0; r < K; r++) {
+            theta = fmin(theta, __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), r),
+                                                 __builtin_amdgcn_readlane(__double2loint(vlo), r)));
+            kax = fmax(kax, fabs(__hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), r),
+                                                  __builtin_amdgcn_readlane(__double2loint(v.x), r))));
+          }
           // the next candidate's bounds (row shift left within lanes 0..15)
           const double nx = dpp_row_shl1_d(v.x), ny = dpp_row_shl1_d(v.y);
           bool pair_ok = true;
           if (lane + 1 < K) pair_ok = vlo - (nx + ny) > order_margin(v.x, nx, mx);
-          // The set of K is certified by the K-th lower bound against every
-          // other expert's upper bound; their order by the pairs.  Without a
-          // route output (a stack call) the order only changes the rounding
-          // of the combine, so an uncertain order among a certified set is
-          // taken as is (the set and the weights are exact either way).
+          // The set of K is certified by the lowest lower bound among the K
+          // against every other expert's upper bound; their order by the
+          // pairs.  Without a route output (a stack call) the order only
+          // changes the rounding of the combine, so an uncertain order among
+          // a certified set is taken as is (the set and the weights are exact
+          // either way).
           bool ok = L.mode == 0 && (__all(pair_ok) || (a.route_idx == nullptr && a.route_w == nullptr));
           if (ok && K < E) {
             const double up = key_double(upk);
-            ok = klo - up > order_margin(kx, up, mx);
+            ok = theta - up > order_margin(kax, up, mx);
           }
-          if (ok) ok = klo - (mx + mxy) > -75.0;
+          if (ok) ok = theta - (mx + mxy) > -75.0;
           if (ok) {
             // softmax over the K (lanes 0..15 hold them): fp32 suffices for
             // the weights' 1e-5 tolerance
@@ -1253,11 +1262,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               rt.w[lane] = ev / den;
             }
           } else {
-            // the lowest lower bound among the K candidates
-            double theta = 1e300;
-            for (int r = 0; r < K; r++)
-              theta = fmin(theta, __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), r),
-                                                   __builtin_amdgcn_readlane(__double2loint(vlo), r)));
             if (lane == 0) {
               sel.theta = theta;
               sel.mxd = mx;

@@ -54,7 +54,7 @@ def _check_bucket(be, oracle, idx, E):
     assert np.array_equal(be.download(slot, (T * K,), np.int32)[:n], o_slot)
 
 
-@pytest.mark.parametrize("B", [4, 32])
+@pytest.mark.parametrize("B", [4, 8, 16, 32])
 def test_batched_decode_zipf_s397(be, oracle, B):
     from shiftwing_amd import zipf
     H, E, K = S397[:3]
