@@ -164,6 +164,97 @@ int coli_cuda_shared_q4_mlp_f16(
     int hidden_groups, int down_row_bytes, int down_groups,
     int scale_row_bytes, int scale_groups);                          /* :140-148 */
 
+/* ---- Part 1b: entry points outside the MoE path ------------------------- */
+/* c/qwen.c links against these unconditionally (c/qwen.c:884, 900, 940, 966)
+ * and calls them only with its CUDA_GDN / CUDA_ATTN switches on (c/qwen.c:868,
+ * 925-926).  They are exported with the reference prototypes so the reference
+ * host links against this library unchanged; every call returns -1 with a
+ * message saying the path is not built here.  Run the reference host with
+ * CUDA_GDN=0 CUDA_ATTN=0 so those layers stay on its CPU path. */
+int coli_cuda_gdn_decode_q4_f16(
+    ColiCuda *ctx, float *out, const float *x, const float *a, const float *b,
+    const unsigned char *qkv_q, const float *qkv_s, int qkv_row_bytes,
+    int qkv_groups, const unsigned char *z_q, const float *z_s,
+    int z_row_bytes, int z_groups, const unsigned char *out_q,
+    const float *out_s, int out_row_bytes, int out_groups,
+    const float *conv_weight, const float *a_log, const float *dt_bias,
+    const float *norm_weight, float *conv_state, float *recurrent_state,
+    int position, int hidden, int key_heads, int value_heads, int key_dim,
+    int value_dim, int conv_kernel, int group_size, float eps); /* :149-158 */
+int coli_cuda_gdn_block_q4_f16(
+    ColiCuda *ctx, float *out, const float *x, const float *a, const float *b,
+    int batch, const unsigned char *qkv_q, const float *qkv_s,
+    int qkv_row_bytes, int qkv_groups, const unsigned char *z_q,
+    const float *z_s, int z_row_bytes, int z_groups,
+    const unsigned char *out_q, const float *out_s, int out_row_bytes,
+    int out_groups, const float *conv_weight, const float *a_log,
+    const float *dt_bias, const float *norm_weight, float *conv_state,
+    float *recurrent_state, int position, int hidden, int key_heads,
+    int value_heads, int key_dim, int value_dim, int conv_kernel,
+    int group_size, float eps);                                  /* :159-169 */
+int coli_cuda_gdn_slots_q4_f16(
+    ColiCuda *ctx, float *out, const float *x, const float *a, const float *b,
+    int batch, const int *slot, const int *position,
+    const unsigned char *qkv_q, const float *qkv_s, int qkv_row_bytes,
+    int qkv_groups, const unsigned char *z_q, const float *z_s,
+    int z_row_bytes, int z_groups, const unsigned char *out_q,
+    const float *out_s, int out_row_bytes, int out_groups,
+    const float *conv_weight, const float *a_log, const float *dt_bias,
+    const float *norm_weight, float *conv_state, float *recurrent_state,
+    int slots, int hidden, int key_heads, int value_heads, int key_dim,
+    int value_dim, int conv_kernel, int group_size, float eps);  /* :170-180 */
+int coli_cuda_gdn_slots_q4_f16_device(
+    ColiCuda *ctx, float *out, const float *x, const float *a, const float *b,
+    int batch, const int *slot, const int *position,
+    const unsigned char *qkv_q, const float *qkv_s, int qkv_row_bytes,
+    int qkv_groups, const unsigned char *z_q, const float *z_s,
+    int z_row_bytes, int z_groups, const unsigned char *out_q,
+    const float *out_s, int out_row_bytes, int out_groups,
+    const float *conv_weight, const float *a_log, const float *dt_bias,
+    const float *norm_weight, float *conv_state, float *recurrent_state,
+    int slots, int hidden, int key_heads, int value_heads, int key_dim,
+    int value_dim, int conv_kernel, int group_size, float eps);  /* :183-193 */
+int coli_cuda_gqa_decode_q4_f16(
+    ColiCuda *ctx, float *out, const float *x,
+    const unsigned char *q_q, const float *q_s, int q_rb, int q_ng,
+    const unsigned char *k_q, const float *k_s, int k_rb, int k_ng,
+    const unsigned char *v_q, const float *v_s, int v_rb, int v_ng,
+    const void *o_q, const float *o_s, int o_fmt, int o_rb, int o_ng,
+    const float *q_norm, const float *k_norm, float *k_cache,
+    float *v_cache, int position, int hidden, int query_heads,
+    int kv_heads, int head_dim, int rotary_dim, int group_size,
+    float theta, float eps);                                     /* :194-203 */
+int coli_cuda_gqa_prefill_q4_f16(
+    ColiCuda *ctx, float *out, const float *x, int rows, int base,
+    const unsigned char *q_q, const float *q_s, int q_rb, int q_ng,
+    const unsigned char *k_q, const float *k_s, int k_rb, int k_ng,
+    const unsigned char *v_q, const float *v_s, int v_rb, int v_ng,
+    const void *o_q, const float *o_s, int o_fmt, int o_rb, int o_ng,
+    const float *q_norm, const float *k_norm, float *k_cache,
+    float *v_cache, int max_seq, int hidden, int query_heads,
+    int kv_heads, int head_dim, int rotary_dim, int group_size,
+    float theta, float eps);                                     /* :206-215 */
+int coli_cuda_gqa_slots_q4_f16(
+    ColiCuda *ctx, float *out, const float *x, int batch, const int *slot,
+    const int *position, const unsigned char *q_q, const float *q_s,
+    int q_rb, int q_ng, const unsigned char *k_q, const float *k_s,
+    int k_rb, int k_ng, const unsigned char *v_q, const float *v_s,
+    int v_rb, int v_ng, const void *o_q, const float *o_s, int o_fmt,
+    int o_rb, int o_ng, const float *q_norm, const float *k_norm,
+    float *k_cache, float *v_cache, int slots, int max_seq, int hidden,
+    int query_heads, int kv_heads, int head_dim, int rotary_dim,
+    int group_size, float theta, float eps);                     /* :216-225 */
+int coli_cuda_gqa_slots_q4_f16_device(
+    ColiCuda *ctx, float *out, const float *x, int batch, const int *slot,
+    const int *position, const unsigned char *q_q, const float *q_s,
+    int q_rb, int q_ng, const unsigned char *k_q, const float *k_s,
+    int k_rb, int k_ng, const unsigned char *v_q, const float *v_s,
+    int v_rb, int v_ng, const void *o_q, const float *o_s, int o_fmt,
+    int o_rb, int o_ng, const float *q_norm, const float *k_norm,
+    float *k_cache, float *v_cache, int slots, int max_seq, int hidden,
+    int query_heads, int kv_heads, int head_dim, int rotary_dim,
+    int group_size, float theta, float eps);                     /* :227-236 */
+
 /* ---- Part 2: device-resident MoE step (no reference counterpart) -------- */
 
 /* fp32-activation variants of the grouped calls above (same arguments with

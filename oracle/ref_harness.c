@@ -16,9 +16,18 @@
 
 #include "moe_oracle.h"
 
-static QMat ref_qmat(const or_qmat *w) {
+static QMat ref_qmat_named(const or_qmat *w, const char *name) {
     QMat q;
     memset(&q, 0, sizeof(q));
+#ifdef COLI_CUDA
+    /* the reference's device weight cache keys tensors by name (c/qwen.c:576) */
+    if (name) {
+        snprintf(q.cuda_key, sizeof(q.cuda_key), "%s", name);
+        q.cuda_eligible = w->fmt == 1 || w->fmt == 3 || w->fmt == 4;
+    }
+#else
+    (void)name;
+#endif
     q.fmt = w->fmt;
     q.O = w->O;
     q.I = w->I;
@@ -34,6 +43,8 @@ static QMat ref_qmat(const or_qmat *w) {
         q.q4 = (uint8_t *)w->q;
     return q;
 }
+
+static QMat ref_qmat(const or_qmat *w) { return ref_qmat_named(w, NULL); }
 
 float ref_dot(const float *a, const float *b, int n) { return dot(a, b, n); }
 float ref_dot_q8f(const int8_t *w, const float *x, int n) { return dot_q8f(w, x, n); }
@@ -84,11 +95,23 @@ void *ref_layer_create(const or_layer *L) {
     r->m.layer = &r->l;
     r->m.expert_cap = L->E;
     MoeW *w = &r->l.moe;
-    w->router = ref_qmat(&L->router);
-    w->shared_gate = ref_qmat(&L->shared_gate);
-    w->shared_up = ref_qmat(&L->shared_up);
-    w->shared_down = ref_qmat(&L->shared_down);
-    w->shared_scale = ref_qmat(&L->shared_scale);
+    /* Tensor names as the reference container spells them (c/qwen.c:2198-2206).
+     * The reference's device weight cache is keyed by these names
+     * (c/qwen.c:576-578), so every harness layer gets a layer number of its
+     * own: layers of different shapes must never share a cached buffer. */
+    static int serial;
+    const int ln = __atomic_fetch_add(&serial, 1, __ATOMIC_RELAXED);
+    char nm[160];
+    snprintf(nm, sizeof(nm), "layers.%d.mlp.gate.weight", ln);
+    w->router = ref_qmat_named(&L->router, nm);
+    snprintf(nm, sizeof(nm), "layers.%d.mlp.shared_expert.gate_proj.weight", ln);
+    w->shared_gate = ref_qmat_named(&L->shared_gate, nm);
+    snprintf(nm, sizeof(nm), "layers.%d.mlp.shared_expert.up_proj.weight", ln);
+    w->shared_up = ref_qmat_named(&L->shared_up, nm);
+    snprintf(nm, sizeof(nm), "layers.%d.mlp.shared_expert.down_proj.weight", ln);
+    w->shared_down = ref_qmat_named(&L->shared_down, nm);
+    snprintf(nm, sizeof(nm), "layers.%d.mlp.shared_expert_gate.weight", ln);
+    w->shared_scale = ref_qmat_named(&L->shared_scale, nm);
     w->cap = L->E;
     w->layer = 0;
     w->expert = (Expert *)calloc((size_t)L->E, sizeof(Expert));
@@ -99,9 +122,12 @@ void *ref_layer_create(const or_layer *L) {
     pthread_cond_init(&w->pf_done, NULL);
     for (int e = 0; e < L->E; e++) {
         w->expert[e].eid = e;
-        w->expert[e].gate = ref_qmat(&L->gate[e]);
-        w->expert[e].up = ref_qmat(&L->up[e]);
-        w->expert[e].down = ref_qmat(&L->down[e]);
+        snprintf(nm, sizeof(nm), "layers.%d.mlp.experts.%d.gate_proj.weight", ln, e);
+        w->expert[e].gate = ref_qmat_named(&L->gate[e], nm);
+        snprintf(nm, sizeof(nm), "layers.%d.mlp.experts.%d.up_proj.weight", ln, e);
+        w->expert[e].up = ref_qmat_named(&L->up[e], nm);
+        snprintf(nm, sizeof(nm), "layers.%d.mlp.experts.%d.down_proj.weight", ln, e);
+        w->expert[e].down = ref_qmat_named(&L->down[e], nm);
     }
     return r;
 }
@@ -109,6 +135,19 @@ void *ref_layer_create(const or_layer *L) {
 void ref_layer_destroy(void *h) {
     RefLayer *r = (RefLayer *)h;
     if (!r) return;
+#ifdef COLI_CUDA
+    /* device cache entries must not point back at the freed matrices */
+    MoeW *w = &r->l.moe;
+    cuda_qmat_detach(&w->shared_gate);
+    cuda_qmat_detach(&w->shared_up);
+    cuda_qmat_detach(&w->shared_down);
+    cuda_qmat_detach(&w->shared_scale);
+    for (int e = 0; e < r->m.c.n_experts; e++) {
+        cuda_qmat_detach(&w->expert[e].gate);
+        cuda_qmat_detach(&w->expert[e].up);
+        cuda_qmat_detach(&w->expert[e].down);
+    }
+#endif
     free(r->l.moe.expert);
     free(r->l.moe.heat);
     free(r->l.moe.last);
@@ -142,3 +181,35 @@ void ref_set_threads(int n) {
     (void)n;
 #endif
 }
+
+#ifdef COLI_CUDA
+/* The reference's own GPU glue (c/qwen.c:462-1474, 3741-3809) driving
+ * whatever library provides the coli_cuda_* symbols it was linked against.
+ * The caller sets the reference's switches (COLI_CUDA=1, CUDA_DENSE=1,
+ * optionally CUDA_F16=1) before ref_cuda_start. */
+int ref_cuda_start(void) { return cuda_backend_start() && cuda_rt.active; }
+
+void ref_cuda_set_f16(int on) { cuda_rt.use_f16 = on != 0; }
+
+/* out: active, failed, grouped expert calls, grouped kernel calls, batched
+ * transactions, fused MLP calls, q3 native grouped calls */
+void ref_cuda_counters(unsigned long long out[7]) {
+    out[0] = (unsigned long long)cuda_rt.active;
+    out[1] = (unsigned long long)cuda_rt.failed;
+    out[2] = cuda_rt.grouped_calls;
+    out[3] = cuda_rt.grouped_kernel_calls;
+    out[4] = cuda_rt.batch_transactions;
+    out[5] = cuda_rt.mlp_calls;
+    out[6] = cuda_rt.q3_grouped_calls;
+}
+
+/* A speculative block of T = 2..8 tokens (moe_cuda_block, c/qwen.c:3741):
+ * returns 1 when the device path produced out. */
+int ref_moe_cuda_block(void *h, const float *x, int T, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    memset(out, 0, (size_t)T * r->m.c.hidden * sizeof(float));
+    return moe_cuda_block(&r->m, &r->l, x, T, out);
+}
+
+void ref_cuda_stop(void) { cuda_backend_stop(); }
+#endif

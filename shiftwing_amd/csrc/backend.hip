@@ -1,13 +1,15 @@
-// Context, memory and the reference backend's MoE-path entry points on
-// gfx950.  The ABI (names, arguments, 0/-1 returns, thread-local errors,
-// validation messages, y-overwrite vs y-accumulate semantics) follows
-// /root/reference/c/backend_cuda.h and c/backend_cuda.cu; the kernels are
-// written for wave64 and read the container layouts directly (no repack):
+// The reference backend's MoE-path compute entry points on gfx950
+// (c/backend_cuda.h:42-148): elementwise ops, row GEMVs over the container
+// layouts, the grouped routed-expert calls over caller pointer tables and the
+// shared-expert calls.  Arguments, limits and y-overwrite vs y-accumulate
+// semantics are the reference's; the kernels are written for wave64 and read
+// the container layouts directly (no repack):
 //   int4: row stride row_bytes, value i in byte i>>1 (low nibble first),
 //         w = (nibble-8)*scale[row*groups + i/group_size];
 //   int3: 8 codes per 24-bit little-endian triplet, w = (code-4)*scale;
 //   int8: one scale per row.
-// The HBM-resident fused MoE step lives in moe.hip.
+// The context (memory, streams, profiling) is context.hip; the HBM-resident
+// fused MoE step is moe.hip / moe_decode.hip / moe_stack.hip.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdio.h>
@@ -18,295 +20,7 @@
 #include "sw_stack.h"
 #include "sw_device.h"
 
-static thread_local char g_error[512];
-
-namespace sw {
-
-int fail_hip(const char *where, hipError_t e) {
-  snprintf(g_error, sizeof(g_error), "%s: %s", where, hipGetErrorString(e));
-  return -1;
-}
-
-int fail_arg(const char *fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_error, sizeof(g_error), fmt, ap);
-  va_end(ap);
-  return -1;
-}
-
-int launch_status(const char *where) {
-  hipError_t e = hipGetLastError();
-  return e == hipSuccess ? 0 : fail_hip(where, e);
-}
-
-int ensure_scratch(ColiCuda *ctx, Scratch which, size_t bytes, const char *where) {
-  if (ctx->scratch_cap[which] >= bytes) return 0;
-  if (ctx->scratch[which]) {
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return fail_hip(where, e);
-    hipFree(ctx->scratch[which]);
-  }
-  ctx->scratch[which] = nullptr;
-  ctx->scratch_cap[which] = 0;
-  size_t cap = bytes < 256 ? 256 : bytes;
-  hipError_t e = hipMalloc(&ctx->scratch[which], cap);
-  if (e != hipSuccess) return fail_hip(where, e);
-  ctx->scratch_cap[which] = cap;
-  return 0;
-}
-
-}  // namespace sw
-
 using namespace sw;
-
-// ---------------------------------------------------------------------------
-// context and memory (backend_cuda.h:13-40)
-// ---------------------------------------------------------------------------
-extern "C" const char *coli_cuda_last_error(void) {
-  return g_error[0] ? g_error : "no HIP error";
-}
-
-extern "C" int coli_cuda_create(ColiCuda **out, int device) {
-  if (!out) return fail_arg("coli_cuda_create: null output pointer");
-  *out = nullptr;
-  int count = 0;
-  hipError_t e = hipGetDeviceCount(&count);
-  if (e != hipSuccess) return fail_hip("hipGetDeviceCount", e);
-  if (device < 0 || device >= count)
-    return fail_arg("HIP device %d is outside [0,%d)", device, count);
-  e = hipSetDevice(device);
-  if (e != hipSuccess) return fail_hip("hipSetDevice", e);
-  hipDeviceProp_t prop;
-  e = hipGetDeviceProperties(&prop, device);
-  if (e != hipSuccess) return fail_hip("hipGetDeviceProperties", e);
-  ColiCuda *ctx = (ColiCuda *)calloc(1, sizeof(ColiCuda));
-  if (!ctx) return fail_arg("out of memory creating HIP context");
-  ctx->device = device;
-  ctx->major = prop.major;
-  ctx->minor = prop.minor;
-  ctx->sm_count = prop.multiProcessorCount;
-  ctx->shared_per_block = (int)prop.sharedMemPerBlock;
-  snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", prop.name, prop.gcnArchName);
-  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-  if (e != hipSuccess) {
-    free(ctx);
-    return fail_hip("hipStreamCreateWithFlags", e);
-  }
-  const char *async_env = getenv("CUDA_ASYNC_ALLOC");
-  if (!async_env || atoi(async_env) != 0) {
-    int supported = 0;
-    e = hipDeviceGetAttribute(&supported, hipDeviceAttributeMemoryPoolsSupported, device);
-    if (e == hipSuccess && supported) {
-      hipMemPool_t pool;
-      e = hipDeviceGetDefaultMemPool(&pool, device);
-      if (e == hipSuccess) {
-        uint64_t threshold = UINT64_MAX;
-        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
-      }
-      if (e == hipSuccess) ctx->async_alloc = 1;
-    }
-    (void)hipGetLastError();
-  }
-  const char *profile_env = getenv("CUDA_PROFILE_STAGES");
-  if (profile_env && atoi(profile_env) != 0) {
-    ctx->profile_stages = 1;
-    for (int i = 0; i < 9; i++) {
-      if (hipEventCreate(&ctx->profile_event[i]) != hipSuccess) {
-        for (int j = 0; j < i; j++) hipEventDestroy(ctx->profile_event[j]);
-        memset(ctx->profile_event, 0, sizeof(ctx->profile_event));
-        ctx->profile_stages = 0;
-        break;
-      }
-    }
-  }
-  g_error[0] = 0;
-  *out = ctx;
-  return 0;
-}
-
-extern "C" void coli_cuda_destroy(ColiCuda *ctx) {
-  if (!ctx) return;
-  hipSetDevice(ctx->device);
-  hipStreamSynchronize(ctx->stream);
-  for (int i = 0; i < kScrCount; i++)
-    if (ctx->scratch[i]) hipFree(ctx->scratch[i]);
-  stack_release(ctx);
-  if (ctx->profile_transactions)
-    fprintf(stderr,
-            "[HIP_MOE_STAGE] transactions=%llu setup_ms=%.3f routed_hidden_ms=%.3f "
-            "routed_down_ms=%.3f route_reduce_ms=%.3f shared_hidden_ms=%.3f "
-            "shared_scale_ms=%.3f shared_down_ms=%.3f download_ms=%.3f\n",
-            ctx->profile_transactions, ctx->profile_ms[0], ctx->profile_ms[1],
-            ctx->profile_ms[2], ctx->profile_ms[3], ctx->profile_ms[4], ctx->profile_ms[5],
-            ctx->profile_ms[6], ctx->profile_ms[7]);
-  for (int i = 0; i < 9; i++)
-    if (ctx->profile_event[i]) hipEventDestroy(ctx->profile_event[i]);
-  for (int i = 0; i < 2; i++)
-    if (ctx->timer_event[i]) hipEventDestroy(ctx->timer_event[i]);
-  for (int i = 0; i < 8; i++)
-    if (ctx->moe_event[i]) hipEventDestroy(ctx->moe_event[i]);
-  hipStreamDestroy(ctx->stream);
-  free(ctx);
-}
-
-extern "C" const char *coli_cuda_device_name(const ColiCuda *ctx) { return ctx ? ctx->name : ""; }
-
-extern "C" int coli_cuda_compute_capability(const ColiCuda *ctx, int *major, int *minor) {
-  if (!ctx || !major || !minor) return fail_arg("coli_cuda_compute_capability: null argument");
-  *major = ctx->major;
-  *minor = ctx->minor;
-  return 0;
-}
-
-extern "C" int coli_cuda_device_limits(const ColiCuda *ctx, int *sm_count, int *shared_per_block) {
-  if (!ctx) return fail_arg("coli_cuda_device_limits: null context");
-  if (sm_count) *sm_count = ctx->sm_count;
-  if (shared_per_block) *shared_per_block = ctx->shared_per_block;
-  return 0;
-}
-
-extern "C" int coli_cuda_async_alloc_enabled(const ColiCuda *ctx) { return ctx ? ctx->async_alloc : 0; }
-
-extern "C" int coli_cuda_memory_info(ColiCuda *ctx, size_t *free_bytes, size_t *total_bytes) {
-  if (!ctx || !free_bytes || !total_bytes) return fail_arg("coli_cuda_memory_info: null argument");
-  hipError_t e = hipMemGetInfo(free_bytes, total_bytes);
-  return e == hipSuccess ? 0 : fail_hip("hipMemGetInfo", e);
-}
-
-extern "C" int coli_cuda_malloc(ColiCuda *ctx, void **ptr, size_t bytes) {
-  if (!ctx || !ptr) return fail_arg("coli_cuda_malloc: null argument");
-  hipError_t e = ctx->async_alloc ? hipMallocAsync(ptr, bytes, ctx->stream) : hipMalloc(ptr, bytes);
-  return e == hipSuccess ? 0 : fail_hip(ctx->async_alloc ? "hipMallocAsync" : "hipMalloc", e);
-}
-
-extern "C" void coli_cuda_free(ColiCuda *ctx, void *ptr) {
-  if (!ctx || !ptr) return;
-  hipSetDevice(ctx->device);
-  if (ctx->async_alloc)
-    hipFreeAsync(ptr, ctx->stream);
-  else
-    hipFree(ptr);
-}
-
-extern "C" int coli_cuda_malloc_host(ColiCuda *ctx, void **ptr, size_t bytes) {
-  if (!ctx || !ptr) return fail_arg("coli_cuda_malloc_host: null argument");
-  hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
-  return e == hipSuccess ? 0 : fail_hip("hipHostMalloc", e);
-}
-
-extern "C" void coli_cuda_free_host(ColiCuda *ctx, void *ptr) {
-  if (!ctx || !ptr) return;
-  hipHostFree(ptr);
-}
-
-// Page-locking existing memory is not offered on this platform's GPU hosts;
-// the call reports an error so the caller keeps its pageable path
-// (c/qwen.c treats a failure as "not registered").
-extern "C" int coli_cuda_host_register(ColiCuda *ctx, void *ptr, size_t bytes) {
-  if (!ctx || !ptr || !bytes) return fail_arg("coli_cuda_host_register: null argument");
-  return fail_arg("coli_cuda_host_register: registering existing host memory is not "
-                  "supported; allocate with coli_cuda_malloc_host");
-}
-
-extern "C" void coli_cuda_host_unregister(ColiCuda *ctx, void *ptr) {
-  (void)ctx;
-  (void)ptr;
-}
-
-extern "C" int coli_cuda_upload(ColiCuda *ctx, void *dst, const void *src, size_t bytes) {
-  if (!ctx || !dst || !src) return fail_arg("coli_cuda_upload: null argument");
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
-  return e == hipSuccess ? 0 : fail_hip("hipMemcpyAsync H2D", e);
-}
-
-extern "C" int coli_cuda_download(ColiCuda *ctx, void *dst, const void *src, size_t bytes) {
-  if (!ctx || !dst || !src) return fail_arg("coli_cuda_download: null argument");
-  if (ctx->profile_pending && !ctx->profile_shared_marked) {
-    hipEventRecord(ctx->profile_event[5], ctx->stream);
-    hipEventRecord(ctx->profile_event[6], ctx->stream);
-    hipEventRecord(ctx->profile_event[7], ctx->stream);
-  }
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
-  if (e == hipSuccess && ctx->profile_pending) {
-    hipEventRecord(ctx->profile_event[8], ctx->stream);
-    ctx->profile_download_marked = 1;
-  }
-  return e == hipSuccess ? 0 : fail_hip("hipMemcpyAsync D2H", e);
-}
-
-extern "C" int coli_cuda_copy(ColiCuda *ctx, void *dst, const void *src, size_t bytes) {
-  if (!ctx || !dst || !src) return fail_arg("coli_cuda_copy: null argument");
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
-  return e == hipSuccess ? 0 : fail_hip("hipMemcpyAsync D2D", e);
-}
-
-extern "C" int coli_cuda_memset(ColiCuda *ctx, void *dst, int value, size_t bytes) {
-  if (!ctx || !dst) return fail_arg("coli_cuda_memset: null argument");
-  hipError_t e = hipMemsetAsync(dst, value, bytes, ctx->stream);
-  return e == hipSuccess ? 0 : fail_hip("hipMemsetAsync", e);
-}
-
-extern "C" int coli_cuda_sync(ColiCuda *ctx) {
-  if (!ctx) return fail_arg("coli_cuda_sync: null context");
-  hipError_t e = hipStreamSynchronize(ctx->stream);
-  if (e == hipSuccess && stack_check_abort(ctx)) return -1;
-  if (e == hipSuccess && ctx->profile_pending && ctx->profile_download_marked) {
-    for (int i = 0; i < 8; i++) {
-      float ms = 0.0f;
-      if (hipEventElapsedTime(&ms, ctx->profile_event[i], ctx->profile_event[i + 1]) == hipSuccess)
-        ctx->profile_ms[i] += ms;
-    }
-    ctx->profile_transactions++;
-    ctx->profile_pending = 0;
-    ctx->profile_shared_marked = 0;
-    ctx->profile_download_marked = 0;
-  }
-  return e == hipSuccess ? 0 : fail_hip("hipStreamSynchronize", e);
-}
-
-extern "C" void coli_cuda_profile_reset(ColiCuda *ctx) {
-  if (!ctx || !ctx->profile_stages) return;
-  hipStreamSynchronize(ctx->stream);
-  memset(ctx->profile_ms, 0, sizeof(ctx->profile_ms));
-  ctx->profile_transactions = 0;
-  ctx->profile_pending = 0;
-  ctx->profile_shared_marked = 0;
-  ctx->profile_download_marked = 0;
-}
-
-extern "C" int coli_cuda_profile_snapshot(ColiCuda *ctx, unsigned long long *transactions,
-                                          double stage_ms[8]) {
-  if (!ctx || !transactions || !stage_ms) return fail_arg("coli_cuda_profile_snapshot: null argument");
-  if (!ctx->profile_stages) {
-    *transactions = 0;
-    memset(stage_ms, 0, 8 * sizeof(double));
-    return 1;
-  }
-  if (coli_cuda_sync(ctx)) return -1;
-  *transactions = ctx->profile_transactions;
-  memcpy(stage_ms, ctx->profile_ms, 8 * sizeof(double));
-  return 0;
-}
-
-extern "C" int coli_cuda_timer_start(ColiCuda *ctx) {
-  if (!ctx) return fail_arg("coli_cuda_timer_start: null context");
-  for (int i = 0; i < 2; i++)
-    if (!ctx->timer_event[i]) {
-      hipError_t e = hipEventCreate(&ctx->timer_event[i]);
-      if (e != hipSuccess) return fail_hip("hipEventCreate", e);
-    }
-  hipError_t e = hipEventRecord(ctx->timer_event[0], ctx->stream);
-  return e == hipSuccess ? 0 : fail_hip("hipEventRecord", e);
-}
-
-extern "C" int coli_cuda_timer_stop(ColiCuda *ctx, float *ms) {
-  if (!ctx || !ms || !ctx->timer_event[0]) return fail_arg("coli_cuda_timer_stop: timer not started");
-  hipError_t e = hipEventRecord(ctx->timer_event[1], ctx->stream);
-  if (e == hipSuccess) e = hipEventSynchronize(ctx->timer_event[1]);
-  if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->timer_event[0], ctx->timer_event[1]);
-  return e == hipSuccess ? 0 : fail_hip("coli_cuda_timer_stop", e);
-}
 
 // ---------------------------------------------------------------------------
 // elementwise and small kernels (backend_cuda.h:46-59)
@@ -639,16 +353,11 @@ static int grouped_mlp(ColiCuda *ctx, const char *name, float *y, const XT *x,
   float *h = (float *)ctx->scratch[kScrHidden];
   float *out = (float *)ctx->scratch[kScrRouteOut];
   float *dw = (float *)ctx->scratch[kScrWeight];
+  prof_open(ctx);
   hipError_t e = hipMemcpyAsync(dw, route_weight, (size_t)routes * sizeof(float), hipMemcpyHostToDevice,
                                 ctx->stream);
   if (e != hipSuccess) return fail_hip("grouped route weight upload", e);
-  if (ctx->profile_stages) {
-    hipEventRecord(ctx->profile_event[0], ctx->stream);
-    hipEventRecord(ctx->profile_event[1], ctx->stream);
-    ctx->profile_pending = 0;
-    ctx->profile_shared_marked = 0;
-    ctx->profile_download_marked = 0;
-  }
+  prof_mark(ctx, kStageSetup);
   for (int r0 = 0; r0 < routes; r0 += kRoutesPerLaunch) {
     int n = routes - r0 < kRoutesPerLaunch ? routes - r0 : kRoutesPerLaunch;
     RouteTable t;
@@ -667,7 +376,7 @@ static int grouped_mlp(ColiCuda *ctx, const char *name, float *y, const XT *x,
     k_grouped_hidden<BITS, XT><<<dim3((I + 3) / 4, n), 256, 0, ctx->stream>>>(h, r0, x, t, I, H, gs, hrb,
                                                                              hgroups);
   }
-  if (ctx->profile_stages) hipEventRecord(ctx->profile_event[2], ctx->stream);
+  prof_mark(ctx, kStageRoutedHidden);
   for (int r0 = 0; r0 < routes; r0 += kRoutesPerLaunch) {
     int n = routes - r0 < kRoutesPerLaunch ? routes - r0 : kRoutesPerLaunch;
     RouteTable t;
@@ -679,13 +388,10 @@ static int grouped_mlp(ColiCuda *ctx, const char *name, float *y, const XT *x,
     k_grouped_down<BITS><<<dim3((H + 3) / 4, n), 256, 0, ctx->stream>>>(out, r0, h, t, H, I, gs, drb,
                                                                        dgroups);
   }
-  if (ctx->profile_stages) hipEventRecord(ctx->profile_event[3], ctx->stream);
+  prof_mark(ctx, kStageRoutedDown);
   k_route_reduce<<<dim3((H + 255) / 256, batch), 256, 0, ctx->stream>>>(y, out, dw, batch, K, H);
   int st = launch_status(name);
-  if (!st && ctx->profile_stages) {
-    hipEventRecord(ctx->profile_event[4], ctx->stream);
-    ctx->profile_pending = 1;
-  }
+  if (!st) prof_mark(ctx, kStageReduce);
   return st;
 }
 
@@ -780,17 +486,14 @@ static int shared_q4(ColiCuda *ctx, const char *name, float *y, const unsigned s
   const __half *xh = (const __half *)x;
   k_shared_q4_hidden<<<dim3((I + 3) / 4, batch), 256, 0, ctx->stream>>>(h, xh, gate_q, gate_s, up_q, up_s,
                                                                        I, H, gs, hrb, hgroups);
-  if (ctx->profile_pending) hipEventRecord(ctx->profile_event[5], ctx->stream);
+  prof_mark(ctx, kStageSharedHidden);
   k_q_gemm<4, __half><<<dim3(1, batch), 256, 0, ctx->stream>>>(logit, xh, scale_q, scale_s, 1, H, gs, srb,
                                                                sgroups);
-  if (ctx->profile_pending) hipEventRecord(ctx->profile_event[6], ctx->stream);
+  prof_mark(ctx, kStageSharedScale);
   k_shared_q4_down<<<dim3((H + 3) / 4, batch), 256, 0, ctx->stream>>>(y, h, down_q, down_s, logit, H, I, gs,
                                                                      drb, dgroups);
   int st = launch_status(name);
-  if (!st && ctx->profile_pending) {
-    hipEventRecord(ctx->profile_event[7], ctx->stream);
-    ctx->profile_shared_marked = 1;
-  }
+  if (!st) prof_mark(ctx, kStageSharedDown);
   return st;
 }
 
@@ -877,34 +580,6 @@ __global__ static void k_idot_gemm(float *y, const signed char *xq, const float 
   if (lane == 0) y[(size_t)b * rows + row] = (float)d * scales[row] * sx[b];
 }
 
-__global__ static void k_idot_swiglu(float *h, const signed char *xq, const float *sx,
-                                     const signed char *gq, const float *gs, int grb, const signed char *uq,
-                                     const float *us, int urb, int I, int H) {
-  int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y;
-  if (row >= I) return;
-  const signed char *xs = xq + (size_t)b * H;
-  int dg = wave_sum_i(lane_idot(gq + (size_t)row * grb, xs, H, lane));
-  int du = wave_sum_i(lane_idot(uq + (size_t)row * urb, xs, H, lane));
-  if (lane == 0) {
-    float g = (float)dg * gs[row] * sx[b];
-    float u = (float)du * us[row] * sx[b];
-    h[(size_t)b * I + row] = silu_ref(g) * u;
-  }
-}
-
-// y[b,row] += scale[b] * ((float)dot * ds[row]) * shx[b]
-__global__ static void k_idot_down_add(float *y, const signed char *hq, const float *shx,
-                                       const signed char *dq, const float *ds, int drb,
-                                       const float *sample_scale, int H, int I) {
-  int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y;
-  if (row >= H) return;
-  int d = wave_sum_i(lane_idot(dq + (size_t)row * drb, hq + (size_t)b * I, I, lane));
-  if (lane == 0) {
-    float shared = (float)d * ds[row] * shx[b];
-    y[(size_t)b * H + row] += shared * sample_scale[b];
-  }
-}
-
 extern "C" int coli_cuda_idot_q8_gemm(ColiCuda *ctx, float *y, const float *x, int batch,
                                       const signed char *q, const float *scales, int rows, int cols,
                                       int row_bytes) {
@@ -921,8 +596,22 @@ extern "C" int coli_cuda_idot_q8_gemm(ColiCuda *ctx, float *y, const float *x, i
   return launch_status("coli_cuda_idot_q8_gemm");
 }
 
-// shared int8 expert: IDOT arithmetic end to end (the CPU path's shared expert,
-// c/qwen.c:3737 -> 1765-1768), so the int32 dots match the CPU bit for bit.
+// shared int8 expert for the reference's batched call (backend_cuda.h:128-139):
+// fp32 activations x int8 rows, the same row dot as coli_cuda_q8_gemv, so a
+// batch equals per-token q8_gemv + silu_mul + q8_gemv calls bit for bit (the
+// reference's batch-vs-single contract, c/tests/test_backend_cuda.c:487-531).
+// The CPU path's IDOT arithmetic is coli_cuda_idot_q8_gemm and the fused MoE
+// step, which match c/qwen.c:1765-1768 bit for bit.
+//
+// y[b,row] += ((down[row] . h_b) * ds[row]) * sample_scale[b]
+__global__ static void k_q8_down_scaled_add(float *y, const float *h, const signed char *dq, const float *ds,
+                                            int drb, const float *sample_scale, int H, int I) {
+  int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y;
+  if (row >= H) return;
+  float v = wave_sum(lane_dot_q8(dq + (size_t)row * drb, h + (size_t)b * I, I, lane));
+  if (lane == 0) y[(size_t)b * H + row] += v * ds[row] * sample_scale[b];
+}
+
 static int shared_q8(ColiCuda *ctx, float *y, const float *x, const float *scale, int device_scale,
                      const signed char *gate_q, const float *gate_s, int grb, const signed char *up_q,
                      const float *up_s, int urb, const signed char *down_q, const float *down_s, int drb,
@@ -930,22 +619,17 @@ static int shared_q8(ColiCuda *ctx, float *y, const float *x, const float *scale
   if (!ctx || !y || !x || !scale || !gate_q || !gate_s || !up_q || !up_s || !down_q || !down_s ||
       batch <= 0 || batch > 8 || H <= 0 || I <= 0 || grb < H || urb < H || drb < I)
     return fail_arg("coli_cuda_shared_q8_mlp_batch: invalid argument");
-  size_t xqb = ((size_t)batch * H + 255) & ~(size_t)255, hqb = ((size_t)batch * I + 255) & ~(size_t)255;
-  size_t hb = (size_t)batch * I * sizeof(float);
-  size_t total = xqb + hqb + hb + 3 * (size_t)batch * sizeof(float) + 256;
+  const size_t gb = (size_t)batch * I * sizeof(float);
+  const size_t total = 2 * gb + (size_t)batch * sizeof(float);
   if (ensure_scratch(ctx, kScrGate, total, "shared q8 allocation")) return -1;
-  char *base = (char *)ctx->scratch[kScrGate];
-  signed char *xq = (signed char *)base;
-  signed char *hq = (signed char *)(base + xqb);
-  float *h = (float *)(base + xqb + hqb);
-  float *sx = (float *)(base + xqb + hqb + hb);
-  float *shx = sx + batch;
-  float *dscale = shx + batch;
-  k_qrow_i8<<<batch, 256, 0, ctx->stream>>>(xq, sx, x, H);
-  k_idot_swiglu<<<dim3((I + 3) / 4, batch), 256, 0, ctx->stream>>>(h, xq, sx, gate_q, gate_s, grb, up_q,
-                                                                   up_s, urb, I, H);
-  k_qrow_i8<<<batch, 256, 0, ctx->stream>>>(hq, shx, h, I);
-  if (ctx->profile_pending) hipEventRecord(ctx->profile_event[5], ctx->stream);
+  float *g = (float *)ctx->scratch[kScrGate];
+  float *u = g + (size_t)batch * I;
+  float *dscale = u + (size_t)batch * I;
+  const dim3 hid((I + 3) / 4, batch);
+  k_q_gemm<8, float><<<hid, 256, 0, ctx->stream>>>(g, x, (const unsigned char *)gate_q, gate_s, I, H, 0, grb, 0);
+  k_q_gemm<8, float><<<hid, 256, 0, ctx->stream>>>(u, x, (const unsigned char *)up_q, up_s, I, H, 0, urb, 0);
+  k_silu_mul<<<(batch * I + 255) / 256, 256, 0, ctx->stream>>>(g, g, u, batch * I);
+  prof_mark(ctx, kStageSharedHidden);
   const float *sc = scale;
   if (!device_scale) {
     hipError_t e = hipMemcpyAsync(dscale, scale, (size_t)batch * sizeof(float), hipMemcpyHostToDevice,
@@ -953,14 +637,10 @@ static int shared_q8(ColiCuda *ctx, float *y, const float *x, const float *scale
     if (e != hipSuccess) return fail_hip("shared q8 scale upload", e);
     sc = dscale;
   }
-  if (ctx->profile_pending) hipEventRecord(ctx->profile_event[6], ctx->stream);
-  k_idot_down_add<<<dim3((H + 3) / 4, batch), 256, 0, ctx->stream>>>(y, hq, shx, down_q, down_s, drb, sc,
-                                                                     H, I);
+  prof_mark(ctx, kStageSharedScale);
+  k_q8_down_scaled_add<<<dim3((H + 3) / 4, batch), 256, 0, ctx->stream>>>(y, g, down_q, down_s, drb, sc, H, I);
   int st = launch_status("shared batch q8 MLP kernels");
-  if (!st && ctx->profile_pending) {
-    hipEventRecord(ctx->profile_event[7], ctx->stream);
-    ctx->profile_shared_marked = 1;
-  }
+  if (!st) prof_mark(ctx, kStageSharedDown);
   return st;
 }
 
@@ -981,4 +661,77 @@ extern "C" int coli_cuda_shared_q8_mlp_batch_device_scale(
     int intermediate) {
   return shared_q8(ctx, y, x, device_scale, 1, gate_q, gate_s, gate_row_bytes, up_q, up_s, up_row_bytes,
                    down_q, down_s, down_row_bytes, batch, hidden, intermediate);
+}
+
+// ---------------------------------------------------------------------------
+// Entry points outside the MoE path (backend_cuda.h:149-236).  c/qwen.c links
+// against them unconditionally (c/qwen.c:884, 900, 940, 966) but only calls
+// them when its CUDA_GDN / CUDA_ATTN switches are on (c/qwen.c:868, 925-926).
+// They are exported so the reference host links unchanged; each reports that
+// the path is not built here, and the reference host then runs those layers
+// on the CPU.
+// ---------------------------------------------------------------------------
+static int not_built(const char *entry, const char *path, const char *env) {
+  return fail_arg("%s: the %s path is not part of this MoE library; run the reference host with %s=0", entry,
+                  path, env);
+}
+
+extern "C" int coli_cuda_gdn_decode_q4_f16(ColiCuda *, float *, const float *, const float *, const float *,
+                                           const unsigned char *, const float *, int, int, const unsigned char *,
+                                           const float *, int, int, const unsigned char *, const float *, int, int,
+                                           const float *, const float *, const float *, const float *, float *,
+                                           float *, int, int, int, int, int, int, int, int, float) {
+  return not_built("coli_cuda_gdn_decode_q4_f16", "Gated DeltaNet", "CUDA_GDN");
+}
+extern "C" int coli_cuda_gdn_block_q4_f16(ColiCuda *, float *, const float *, const float *, const float *, int,
+                                          const unsigned char *, const float *, int, int, const unsigned char *,
+                                          const float *, int, int, const unsigned char *, const float *, int, int,
+                                          const float *, const float *, const float *, const float *, float *,
+                                          float *, int, int, int, int, int, int, int, int, float) {
+  return not_built("coli_cuda_gdn_block_q4_f16", "Gated DeltaNet", "CUDA_GDN");
+}
+extern "C" int coli_cuda_gdn_slots_q4_f16(ColiCuda *, float *, const float *, const float *, const float *, int,
+                                          const int *, const int *, const unsigned char *, const float *, int, int,
+                                          const unsigned char *, const float *, int, int, const unsigned char *,
+                                          const float *, int, int, const float *, const float *, const float *,
+                                          const float *, float *, float *, int, int, int, int, int, int, int, int,
+                                          float) {
+  return not_built("coli_cuda_gdn_slots_q4_f16", "Gated DeltaNet", "CUDA_GDN");
+}
+extern "C" int coli_cuda_gdn_slots_q4_f16_device(ColiCuda *, float *, const float *, const float *, const float *,
+                                                 int, const int *, const int *, const unsigned char *,
+                                                 const float *, int, int, const unsigned char *, const float *, int,
+                                                 int, const unsigned char *, const float *, int, int, const float *,
+                                                 const float *, const float *, const float *, float *, float *, int,
+                                                 int, int, int, int, int, int, int, float) {
+  return not_built("coli_cuda_gdn_slots_q4_f16_device", "Gated DeltaNet", "CUDA_GDN");
+}
+extern "C" int coli_cuda_gqa_decode_q4_f16(ColiCuda *, float *, const float *, const unsigned char *,
+                                           const float *, int, int, const unsigned char *, const float *, int, int,
+                                           const unsigned char *, const float *, int, int, const void *,
+                                           const float *, int, int, int, const float *, const float *, float *,
+                                           float *, int, int, int, int, int, int, int, float, float) {
+  return not_built("coli_cuda_gqa_decode_q4_f16", "GQA attention", "CUDA_ATTN");
+}
+extern "C" int coli_cuda_gqa_prefill_q4_f16(ColiCuda *, float *, const float *, int, int, const unsigned char *,
+                                            const float *, int, int, const unsigned char *, const float *, int, int,
+                                            const unsigned char *, const float *, int, int, const void *,
+                                            const float *, int, int, int, const float *, const float *, float *,
+                                            float *, int, int, int, int, int, int, int, float, float) {
+  return not_built("coli_cuda_gqa_prefill_q4_f16", "GQA attention", "CUDA_ATTN");
+}
+extern "C" int coli_cuda_gqa_slots_q4_f16(ColiCuda *, float *, const float *, int, const int *, const int *,
+                                          const unsigned char *, const float *, int, int, const unsigned char *,
+                                          const float *, int, int, const unsigned char *, const float *, int, int,
+                                          const void *, const float *, int, int, int, const float *, const float *,
+                                          float *, float *, int, int, int, int, int, int, int, int, float, float) {
+  return not_built("coli_cuda_gqa_slots_q4_f16", "GQA attention", "CUDA_ATTN");
+}
+extern "C" int coli_cuda_gqa_slots_q4_f16_device(ColiCuda *, float *, const float *, int, const int *,
+                                                 const int *, const unsigned char *, const float *, int, int,
+                                                 const unsigned char *, const float *, int, int,
+                                                 const unsigned char *, const float *, int, int, const void *,
+                                                 const float *, int, int, int, const float *, const float *, float *,
+                                                 float *, int, int, int, int, int, int, int, int, float, float) {
+  return not_built("coli_cuda_gqa_slots_q4_f16_device", "GQA attention", "CUDA_ATTN");
 }

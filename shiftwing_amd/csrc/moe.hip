@@ -1744,6 +1744,7 @@ static void stage_accumulate(ColiCuda *ctx) {
 extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int tokens,
                                      int *route_idx, float *route_weight) {
   if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
+  if (!prof_active(ctx)) prof_open(ctx);
   if (tokens == 1 && !ctx->moe_generic_only) {
     if (ctx->moe_decode_mode == 0) {
       ColiMoeLayer *one[1] = {L};
@@ -1764,9 +1765,11 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
   k_bucket<<<1, 1024, bucket_lds, st>>>(w);
   mark(ctx, 2);
+  prof_mark(ctx, kStageSetup);
   k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedTokens - 1) / kSharedTokens), 512, 0, st>>>(
       w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
   mark(ctx, 3);
+  prof_mark(ctx, kStageSharedHidden);
   int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
@@ -1780,6 +1783,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
          : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
   mark(ctx, 4);
+  prof_mark(ctx, kStageRoutedHidden);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
@@ -1793,8 +1797,10 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     dn_split ? k_down_split<3><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<3><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
   mark(ctx, 6);
+  prof_mark(ctx, kStageRoutedDown);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
   mark(ctx, 7);
+  prof_mark(ctx, kStageReduce);
   int rc = launch_status("coli_cuda_moe_forward");
   stage_accumulate(ctx);
   return rc;
@@ -1806,6 +1812,7 @@ extern "C" int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *
     return fail_arg("coli_cuda_moe_forward_layers: invalid argument");
   for (int l = 0; l < n_layers; l++)
     if (!layers[l]) return fail_arg("coli_cuda_moe_forward_layers: null layer %d", l);
+  if (!prof_active(ctx)) prof_open(ctx);
   if (tokens == 1 && !ctx->moe_generic_only && ctx->moe_decode_mode == 0) {
     int rc = stack_step(ctx, layers, n_layers, y, ys, x, xs, nullptr, nullptr);
     if (rc <= 0) return rc;

@@ -915,11 +915,13 @@ int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *r
   k_dec_route<<<p.g1, kThreads, p.lds1, st>>>(d, x, L->router, L->sgate_row, L->sh_gq, L->sh_uq, L->router_mode,
                                               L->stats);
   if (timing) (void)hipEventRecord(ctx->moe_event[1], st);
+  prof_mark(ctx, kStageSetup);  // router, top-k and the shared gate/up
   if (L->sh.expert_format == 4)
     k_dec_experts<4><<<p.g2, kThreads, p.lds2, st>>>(d, L->xl);
   else
     k_dec_experts<3><<<p.g2, kThreads, p.lds2, st>>>(d, L->xl);
   if (timing) (void)hipEventRecord(ctx->moe_event[2], st);
+  prof_mark(ctx, kStageRoutedHidden);
   if (L->sh.expert_format == 4)
     k_dec_down<4><<<p.g3, p.t3, p.lds3, st>>>(d, L->xl, L->sh_dq, L->sh_ds, L->sh_gs, L->sh_us, y, route_idx,
                                               route_weight);
@@ -927,6 +929,7 @@ int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *r
     k_dec_down<3><<<p.g3, p.t3, p.lds3, st>>>(d, L->xl, L->sh_dq, L->sh_ds, L->sh_gs, L->sh_us, y, route_idx,
                                               route_weight);
   if (timing) (void)hipEventRecord(ctx->moe_event[3], st);
+  prof_mark(ctx, kStageRoutedDown);  // routed and shared down, combine
   int rc = launch_status("MoE decode step");
   if (timing && rc == 0) {
     (void)hipEventSynchronize(ctx->moe_event[3]);

@@ -2096,6 +2096,15 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.spin_ticks = 200000000LL;  // 2 s of the 100 MHz wall clock
   a.trace = (unsigned long long *)ctx->stack_trace;
   a.trace_words = ctx->stack_trace_words;
+  if (!a.trace) {
+    // stage profiling: the launch's stages come from its own clock stamps
+    if (ctx->prof.stamp_layers > 0) {
+      // an earlier launch of this transaction still holds the buffer
+      (void)hipStreamSynchronize(ctx->stream);
+      prof_flush_stamps(ctx);
+    }
+    a.trace = prof_stamp_buffer(ctx, n, &a.trace_words);
+  }
   const size_t Hp = (size_t)a.Hp;
   const size_t u = stack_union_bytes(a.E, a.H, a.K, a.ngh, a.ngi, a.Ish, a.fmt, a.rslots, a.shkc);
   size_t lds = lds_fixed((int)Hp, a.ngh, a.Ish) + u;
@@ -2114,6 +2123,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   if (e != hipSuccess) return fail_hip("MoE stack kernel attributes", e);
   int rc = launch_status("MoE stack step");
   if (rc) return rc;
+  prof_mark(ctx, kStageStamped);  // the launch's span; its stamps split it
   return 0;
 }
 

@@ -1,0 +1,177 @@
+"""The reference's own host code driving this library on the GPU.
+
+oracle/_ref holds reference sources compiled in place against
+libshiftwing_moe.so in place of backend_cuda.o (`make -C oracle ref-hip`;
+c/Makefile:124-125, 148-149 with CUDA=1):
+
+- _ref/test_backend_cuda: the reference's GPU test, c/tests/test_backend_cuda.c,
+  unmodified.  It checks every Part 1 compute entry point against a scalar
+  host reference on non-power-of-two shapes (N=2053, ROWS=37, COLS=1027,
+  padded int8 rows), batch against single calls, q3 native against expanded q4
+  at the 397B expert shape, and the stage profiler's transaction count, with
+  the reference's tolerances (c/tests/test_backend_cuda.c:546-555).
+- _ref/libref_hip.so: the reference's GPU glue (c/qwen.c:462-1474, 3741-3809)
+  behind moe_forward and moe_cuda_block, run on synthetic layers and checked
+  against the same layer on the reference's CPU path, with the shared expert
+  in the fp32 arithmetic the reference's GPU path uses for it.
+
+The binaries are built here (the reference tree is not on the GPU box) and
+travel with the tree; a test skips when they were not built."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, assert_close_rms
+
+pytestmark = pytest.mark.gpu
+
+REF = os.path.join(ROOT, "oracle", "_ref")
+TEST_BIN = os.path.join(REF, "test_backend_cuda")
+GLUE_LIB = os.path.join(REF, "libref_hip.so")
+
+
+def test_reference_backend_test_passes():
+    if not os.path.exists(TEST_BIN):
+        pytest.skip("oracle/_ref/test_backend_cuda not built (make -C oracle ref-hip)")
+    print("[reference GPU test] c/tests/test_backend_cuda.c against libshiftwing_moe.so", flush=True)
+    r = subprocess.run([TEST_BIN], capture_output=True, text=True, timeout=240)
+    print(r.stdout[-3000:], r.stderr[-3000:], flush=True)
+    assert r.returncode == 0, f"reference GPU test failed (rc {r.returncode})"
+    line = [l for l in r.stdout.splitlines() if "maxdiff" in l]
+    assert line, r.stdout
+    diffs = {k: float(v) for k, v in re.findall(r"([\w-]+)(?: maxdiff)?=([0-9.eE+-]+)", line[0])}
+    print("reference test diffs:", diffs, flush=True)
+
+
+class Glue:
+    """ctypes view of oracle/_ref/libref_hip.so."""
+
+    def __init__(self):
+        from oracle.pyoracle import OrLayer, f32p
+        lib = C.CDLL(GLUE_LIB)
+        lib.ref_cuda_start.restype = C.c_int
+        lib.ref_cuda_set_f16.argtypes = [C.c_int]
+        lib.ref_cuda_counters.argtypes = [C.POINTER(C.c_ulonglong)]
+        lib.ref_layer_create.restype = C.c_void_p
+        lib.ref_layer_create.argtypes = [C.POINTER(OrLayer)]
+        lib.ref_layer_destroy.argtypes = [C.c_void_p]
+        lib.ref_moe_forward.argtypes = [C.c_void_p, f32p, f32p]
+        lib.ref_moe_cuda_block.restype = C.c_int
+        lib.ref_moe_cuda_block.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        self.lib = lib
+        self.f32p = f32p
+
+    def counters(self):
+        out = (C.c_ulonglong * 7)()
+        self.lib.ref_cuda_counters(out)
+        keys = ["active", "failed", "grouped", "grouped_kernel", "batch", "mlp", "q3_native"]
+        return dict(zip(keys, [int(v) for v in out]))
+
+    def forward(self, h, x, H):
+        from oracle.pyoracle import ptr
+        out = np.zeros(H, np.float32)
+        self.lib.ref_moe_forward(h, ptr(x, self.f32p), ptr(out, self.f32p))
+        return out
+
+    def block(self, h, x):
+        from oracle.pyoracle import ptr
+        T, H = x.shape
+        out = np.zeros((T, H), np.float32)
+        used = self.lib.ref_moe_cuda_block(h, ptr(np.ascontiguousarray(x), self.f32p), T, ptr(out, self.f32p))
+        return used, out
+
+
+def _with_fp32_shared(oracle, hl, x, want, trace):
+    """The reference CPU output with its shared expert recomputed in the fp32
+    arithmetic its CUDA glue uses (q8 rows x fp32 activations, qmat_mul_ex
+    with IDOT off, c/qwen.c:1757, 1765): the reference's GPU path runs the
+    int8 shared expert through coli_cuda_q8_gemv / shared_q8_mlp_batch, not
+    through IDOT, so its output differs from the CPU path's by the int8
+    activation quantisation (about 1% of the shared term here)."""
+    x = np.atleast_2d(x)
+    want = np.atleast_2d(want).astype(np.float64)
+    sh_idot = np.atleast_2d(trace["shared"]).astype(np.float64)
+    sg = np.atleast_1d(trace["sgate"]).astype(np.float64)
+    out = np.empty_like(want)
+    for t in range(x.shape[0]):
+        g = oracle.qmat_mul(x[t], hl.shared_gate, 0)
+        u = oracle.qmat_mul(x[t], hl.shared_up, 0)
+        h = np.array([oracle.lib.or_siluf(float(v)) for v in g], np.float32) * u
+        sh = oracle.qmat_mul(h.astype(np.float32), hl.shared_down, 0).astype(np.float64)
+        out[t] = want[t] - sg[t] * sh_idot[t] + sg[t] * sh
+    return out
+
+
+@pytest.fixture(scope="module")
+def glue():
+    if not os.path.exists(GLUE_LIB):
+        pytest.skip("oracle/_ref/libref_hip.so not built (make -C oracle ref-hip)")
+    # the reference's switches (c/qwen.c:533-536, 1168-1169): device backend on,
+    # fp16 activations, q3 experts uploaded natively (not expanded to q4)
+    os.environ.update({"COLI_CUDA": "1", "CUDA_DENSE": "1", "CUDA_F16": "1", "Q3_NATIVE": "1"})
+    g = Glue()
+    assert g.lib.ref_cuda_start() == 1, "the reference glue could not start the device backend"
+    yield g
+    g.lib.ref_cuda_stop()
+
+
+@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397)],
+                         ids=["s35_q4", "s397_q3"])
+def test_reference_glue_moe_forward(glue, oracle, shape, seed):
+    """moe_forward with the device backend active: the reference routes on the
+    host and runs cuda_experts_try (c/qwen.c:1270) -> coli_cuda_grouped_q{4,3}_mlp_f16
+    and the q8 shared expert via cuda_mlp_try (q8_gemv, silu_mul) on this
+    library.  fp16 activations (CUDA_F16=1), then fp32 (per-expert q4/q3 gemv
+    + silu_mul + axpy)."""
+    H, E, K, I, Ish, fmt = shape
+    hl = oracle.host_layer(seed, 2, H, E, K, I, Ish, fmt)
+    h = glue.lib.ref_layer_create(C.byref(hl.st))
+    try:
+        for f16, tol in ((1, 5e-3), (0, 1e-4)):
+            glue.lib.ref_cuda_set_f16(f16)
+            for t in range(3):
+                print(f"[reference glue] {shape[0]} f16={f16} token {t}", flush=True)
+                x = oracle.synth_x(seed, 2, t, H)
+                before = glue.counters()
+                got = glue.forward(h, x, H)
+                after = glue.counters()
+                assert after["active"] == 1 and after["failed"] == 0, after
+                assert after["grouped"] == before["grouped"] + 1, (before, after)
+                if f16:
+                    assert after["grouped_kernel"] == before["grouped_kernel"] + 1
+                    if fmt == 3:
+                        assert after["q3_native"] == before["q3_native"] + 1
+                want, tr = oracle.moe_forward(hl, x, trace=True)
+                want = _with_fp32_shared(oracle, hl, x, want, tr)[0]
+                assert_close_rms(got, want, tol, f"reference glue f16={f16} t={t}")
+    finally:
+        glue.lib.ref_layer_destroy(h)
+
+
+def test_reference_glue_speculative_block(glue, oracle):
+    """moe_cuda_block (c/qwen.c:3741) for T = 2, 4 and 8 tokens: host routing,
+    route dedup, coli_cuda_grouped_q4_mlp_batch_f16 and the batched int8 shared
+    expert (coli_cuda_shared_q8_mlp_batch with host gate scales) on this
+    library, against moe_prefill_grouped on the CPU."""
+    H, E, K, I, Ish, fmt = 2048, 64, 8, 512, 512, 4
+    hl = oracle.host_layer(41, 1, H, E, K, I, Ish, fmt)
+    h = glue.lib.ref_layer_create(C.byref(hl.st))
+    glue.lib.ref_cuda_set_f16(1)
+    try:
+        for T in (2, 4, 8):
+            print(f"[reference glue] speculative block T={T}", flush=True)
+            x = np.stack([oracle.synth_x(41, 1, 100 + t, H) for t in range(T)])
+            before = glue.counters()
+            used, got = glue.block(h, x)
+            after = glue.counters()
+            assert used == 1 and after["failed"] == 0, (used, after)
+            assert after["batch"] == before["batch"] + 1
+            want, tr = oracle.moe_prefill(hl, x, trace=True)
+            want = _with_fp32_shared(oracle, hl, x, want, tr)
+            assert_close_rms(got, want, 5e-3, f"speculative block T={T}")
+    finally:
+        glue.lib.ref_layer_destroy(h)

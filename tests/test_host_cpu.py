@@ -131,3 +131,45 @@ def test_graft_entry_points_exist():
     sys.path.insert(0, ROOT)
     import __graft_entry__ as ge
     assert callable(ge.build) and callable(ge.smoke)
+
+
+REF_C = "/root/reference/c"
+LIB_SO = os.path.join(ROOT, "shiftwing_amd", "libshiftwing_moe.so")
+
+
+def _defined_symbols(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if l.strip()}
+
+
+def _undefined_symbols(path):
+    out = subprocess.run(["nm", "-D", "--undefined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if l.strip()}
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_C), reason="the reference tree is not present")
+def test_reference_engine_links_against_this_library():
+    """The drop-in link: the reference engine c/qwen.c built with -DCOLI_CUDA
+    (its CUDA=1 configuration, c/Makefile:62-69, 124-125) links against
+    libshiftwing_moe.so in place of backend_cuda.o, and so do the reference's
+    GPU test and the glue harness.  Every coli_cuda_* symbol they import is
+    defined by this library and declared in include/shiftwing_moe.h."""
+    if not os.path.exists(LIB_SO):
+        pytest.skip("libshiftwing_moe.so is not built")
+    r = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref-hip"], capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    ours = _defined_symbols(LIB_SO)
+    declared = set(_declared_names())
+    for exe in ("qwen_hip", "test_backend_cuda", "libref_hip.so"):
+        path = os.path.join(ROOT, "oracle", "_ref", exe)
+        assert os.path.exists(path), path
+        wanted = {s for s in _undefined_symbols(path) if s.startswith("coli_cuda_")}
+        assert wanted, exe
+        assert wanted <= ours, (exe, sorted(wanted - ours))
+        assert wanted <= declared, (exe, sorted(wanted - declared))
+    # every coli_cuda_ name the reference engine source calls
+    src = open(os.path.join(REF_C, "qwen.c")).read()
+    called = set(re.findall(r"\b(coli_cuda_\w+)\s*\(", src))
+    assert called <= ours, sorted(called - ours)
