@@ -284,6 +284,19 @@ int coli_cuda_idot_q8_gemm(ColiCuda *ctx, float *y, const float *x, int batch,
                            const signed char *q, const float *scales,
                            int rows, int cols, int row_bytes);
 
+/* coli_cuda_idot_q8_gemm without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc).  The
+ * quantised activations live in a fixed 1 MiB device array per device instead
+ * of context scratch, so round_up(batch * cols, 256) + 4 * batch must not
+ * exceed 1 MiB (else -1 with a message).  Same results as
+ * coli_cuda_idot_q8_gemm bit for bit.  Calls that overlap on one device
+ * (several contexts or streams) race on that array. */
+int coli_cuda_idot_q8_gemm_noalloc(ColiCuda *ctx, float *y, const float *x,
+                                   int batch, const signed char *q,
+                                   const float *scales, int rows, int cols,
+                                   int row_bytes);
+
 /* router_topk (c/qwen.c:3421-3426) on device logits, bit-exact:
  * logits [tokens x experts] -> idx / weight [tokens x topk]. */
 int coli_cuda_router_topk(ColiCuda *ctx, const float *logits, int tokens,

@@ -16,6 +16,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "sw_backend.h"
 #include "sw_stack.h"
 #include "sw_device.h"
@@ -594,6 +596,63 @@ extern "C" int coli_cuda_idot_q8_gemm(ColiCuda *ctx, float *y, const float *x, i
   k_idot_gemm<<<dim3((rows + 3) / 4, batch), 256, 0, ctx->stream>>>(y, xq, sx, q, scales, rows, cols,
                                                                     row_bytes);
   return launch_status("coli_cuda_idot_q8_gemm");
+}
+
+// ---------------------------------------------------------------------------
+// IDOT GEMM without allocation (coli_cuda_idot_q8_gemm_noalloc).  The
+// quantised activations and their scales live in a fixed device array instead
+// of context scratch.  In host code `g_noalloc_scratch` names a host-side
+// stand-in, not the device array: its device address is fetched once per
+// device with hipGetSymbolAddress (at coli_cuda_create, with the device
+// current) and only that address is ever handed to kernels.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)1 << 20;  // 1 MiB per device
+static __device__ __align__(256) unsigned char g_noalloc_scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kNoAllocMaxDevices];  // device address per device ordinal
+}  // namespace
+
+namespace sw {
+// Called by coli_cuda_create with ctx->device current.
+int noalloc_bind(ColiCuda *ctx) {
+  if (ctx->device < 0 || ctx->device >= kNoAllocMaxDevices) return 0;  // entry point reports it
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[ctx->device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_noalloc_scratch));
+    if (e != hipSuccess || !p) return fail_hip("hipGetSymbolAddress(no-alloc scratch)", e);
+    g_noalloc_ptr[ctx->device] = p;
+  }
+  ctx->noalloc_scratch = g_noalloc_ptr[ctx->device];
+  return 0;
+}
+}  // namespace sw
+
+extern "C" int coli_cuda_idot_q8_gemm_noalloc(ColiCuda *ctx, float *y, const float *x, int batch,
+                                              const signed char *q, const float *scales, int rows, int cols,
+                                              int row_bytes) {
+  if (!ctx || !y || !x || !q || !scales || batch <= 0 || rows <= 0 || cols <= 0 || row_bytes < cols ||
+      batch > 65535)
+    return fail_arg("coli_cuda_idot_q8_gemm_noalloc: invalid argument");
+  const size_t qbytes = ((size_t)batch * (size_t)cols + 255) & ~(size_t)255;
+  const size_t need = qbytes + (size_t)batch * sizeof(float);
+  if (need > kNoAllocScratchBytes)
+    return fail_arg("coli_cuda_idot_q8_gemm_noalloc: batch x cols = %d x %d needs %zu scratch bytes, "
+                    "the fixed scratch holds %zu",
+                    batch, cols, need, kNoAllocScratchBytes);
+  if (!ctx->noalloc_scratch)
+    return fail_arg("coli_cuda_idot_q8_gemm_noalloc: no scratch address for device %d", ctx->device);
+  // Every byte read below is written first by k_qrow_i8 of this call, so
+  // nothing is cleared; calls overlapping on one device share the array.
+  signed char *xq = (signed char *)ctx->noalloc_scratch;
+  float *sx = (float *)((unsigned char *)ctx->noalloc_scratch + qbytes);
+  k_qrow_i8<<<batch, 256, 0, ctx->stream>>>(xq, sx, x, cols);
+  k_idot_gemm<<<dim3((rows + 3) / 4, batch), 256, 0, ctx->stream>>>(y, xq, sx, q, scales, rows, cols,
+                                                                    row_bytes);
+  return launch_status("coli_cuda_idot_q8_gemm_noalloc");
 }
 
 // shared int8 expert for the reference's batched call (backend_cuda.h:128-139):

@@ -295,6 +295,11 @@ extern "C" int coli_cuda_create(ColiCuda **out, int device) {
     delete ctx;
     return fail_hip("hipStreamCreateWithFlags", e);
   }
+  if (noalloc_bind(ctx)) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return -1;
+  }
   ctx->cache.enabled = env_flag("CUDA_ASYNC_ALLOC", 1) != 0;
   ctx->prof.on = env_flag("CUDA_PROFILE_STAGES", 0) != 0;
   t_error[0] = 0;

@@ -115,6 +115,8 @@ struct ColiCuda {
   unsigned *stack_abort_host = nullptr, *stack_abort_host_dev = nullptr;
   unsigned long long *stack_trace = nullptr;  // optional stage stamps (coli_cuda_moe_stack_trace)
   size_t stack_trace_words = 0;
+  // device address of the fixed scratch of coli_cuda_idot_q8_gemm_noalloc
+  void *noalloc_scratch = nullptr;
 };
 
 namespace sw {
@@ -136,5 +138,9 @@ bool prof_active(const ColiCuda *ctx);         // a transaction is open
 unsigned long long *prof_stamp_buffer(ColiCuda *ctx, int layers, size_t *words);
 // Charge a finished persistent launch's stamps to the stages (stream drained).
 void prof_flush_stamps(ColiCuda *ctx);
+
+// Fetch (once per device) the device address of the no-alloc entry point's
+// fixed scratch; called by coli_cuda_create with the device current.
+int noalloc_bind(ColiCuda *ctx);
 
 }  // namespace sw
