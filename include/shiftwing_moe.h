@@ -306,7 +306,10 @@ int coli_cuda_router_topk(ColiCuda *ctx, const float *logits, int tokens,
  * (c/qwen.c:4168, 3956-3968): experts ascending, tokens ascending.
  * idx [tokens x topk] -> offsets [experts+1], token [tokens*topk],
  * slot [tokens*topk] (the route index k).  Entries past offsets[experts]
- * are left untouched. */
+ * are left untouched.  One call takes experts <= 4096 and as many tokens as
+ * one workgroup's 160 KiB map holds: experts * ceil(tokens/32) * 4 +
+ * (2 * experts + 1) * 4 bytes (2048 tokens up to 512 experts, 1184 at 1024,
+ * 224 at 4096); else -1 with a message. */
 int coli_cuda_moe_bucket(ColiCuda *ctx, const int *idx, int tokens, int topk,
                          int experts, int *offsets, int *token, int *slot);
 
@@ -360,7 +363,9 @@ int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *layer,
 /* Device pointer to the layer's router [E x H] (for in-place edits). */
 float *coli_cuda_moe_layer_router(ColiMoeLayer *layer);
 
-/* The MoE step for `tokens` activation rows: y[t] = sum_k w[t,k] *
+/* The MoE step for `tokens` activation rows (any number: a long block runs
+ * as balanced steps of at most 2048 tokens, fewer for more than 512
+ * experts; tokens are independent): y[t] = sum_k w[t,k] *
  * expert_{idx[t,k]}(x[t]) + sigmoid(gate . x[t]) * shared(x[t]).
  * x, y: device [tokens x H] f32.  route_idx / route_weight: optional device
  * outputs [tokens x K].  Routing is bit-exact with router_topk over the

@@ -13,6 +13,10 @@
  * Every expert is resident (cap = E), so the expert cache never loads. */
 #define QWEN_NO_MAIN
 #include "qwen.c"
+#ifdef COLI_CUDA
+/* the device-resident MoE step as the reference engine would include it */
+#include "sw_qwen_bridge.inc"
+#endif
 
 #include "moe_oracle.h"
 
@@ -136,6 +140,7 @@ void ref_layer_destroy(void *h) {
     RefLayer *r = (RefLayer *)h;
     if (!r) return;
 #ifdef COLI_CUDA
+    sw_moe_unregister(&r->l);
     /* device cache entries must not point back at the freed matrices */
     MoeW *w = &r->l.moe;
     cuda_qmat_detach(&w->shared_gate);
@@ -183,6 +188,18 @@ void ref_set_threads(int n) {
 }
 
 #ifdef COLI_CUDA
+/* The device-resident MoE step of the bridge included above, on a harness
+ * layer. */
+int ref_sw_register(void *h) {
+    RefLayer *r = (RefLayer *)h;
+    return sw_moe_register(&r->m, &r->l);
+}
+
+int ref_sw_forward(void *h, const float *x, int T, float *out, int *idx) {
+    RefLayer *r = (RefLayer *)h;
+    return sw_moe_try(&r->m, &r->l, x, T, out, idx);
+}
+
 /* The reference's own GPU glue (c/qwen.c:462-1474, 3741-3809) driving
  * whatever library provides the coli_cuda_* symbols it was linked against.
  * The caller sets the reference's switches (COLI_CUDA=1, CUDA_DENSE=1,

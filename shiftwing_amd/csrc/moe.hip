@@ -828,7 +828,7 @@ __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx
 // 5. bucketing (c/qwen.c:4168 expert order, 3956-3968 token order): a stable
 // counting sort through per-expert token bitmaps.  Also emits the routed work
 // items {expert, first CSR entry, count <= 8} and pos[t*K+k] (CSR entry of
-// route (t,k)).  One block of 1024 threads; T <= 2048, E <= 512.
+// route (t,k)).  One block of 1024 threads; tokens_per_step(E) tokens at most (the E x T bit map fits 160 KiB).
 // ---------------------------------------------------------------------------
 __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
                              int *pos, int4 *items, int *nitems, unsigned *bits, int *cnt, int *iofs) {
@@ -1659,6 +1659,22 @@ static Work make_work(const ColiMoeLayer *L, int T) {
 }
 
 // dynamic LDS above 64 KiB must be enabled per kernel (gfx950: 160 KiB/CU)
+// Bytes of LDS the bucketing kernels need: an E x T bit map (one 32-token
+// word per expert and 32 tokens) plus 2E+1 counters.
+static size_t bucket_lds_bytes(int E, int T) {
+  return (size_t)E * ((T + 31) / 32) * 4 + (size_t)(2 * E + 1) * 4;
+}
+
+// Tokens one many-token step takes for E experts: the bucketing map must fit
+// a workgroup's 160 KiB of LDS, and at most kMaxTokens.  Longer blocks run as
+// several steps of balanced size (tokens are independent of each other).
+static int tokens_per_step(int E) {
+  const size_t cap = 160 * 1024, fixed = (size_t)(2 * E + 1) * 4;
+  if (E <= 0 || fixed >= cap) return 0;
+  const size_t t = (cap - fixed) / ((size_t)E * 4) * 32;
+  return t < (size_t)kMaxTokens ? (int)t : kMaxTokens;
+}
+
 static int set_lds(const void *fn, size_t bytes) {
   if (bytes > 160 * 1024) return fail_arg("MoE step kernel needs %zu bytes of LDS (> 160 KiB)", bytes);
   if (bytes <= 64 * 1024) return 0;
@@ -1718,6 +1734,18 @@ static int prepare(ColiCuda *ctx, ColiMoeLayer *L, int T, Work &w) {
 extern "C" int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *L, const float *x, int tokens, int *idx,
                                    float *weight) {
   if (!ctx || !L || !x || !idx || !weight) return fail_arg("coli_cuda_moe_route: null argument");
+  const int tmax = tokens_per_step(L->sh.experts);
+  if (tokens > tmax && tmax > 0) {
+    const int nc = (tokens + tmax - 1) / tmax;
+    const size_t H = (size_t)L->sh.hidden, K = (size_t)L->sh.topk;
+    for (int c = 0, t0 = 0; c < nc; c++) {
+      const int n = tokens / nc + (c < tokens % nc ? 1 : 0);
+      if (coli_cuda_moe_route(ctx, L, x + (size_t)t0 * H, n, idx + (size_t)t0 * K, weight + (size_t)t0 * K))
+        return -1;
+      t0 += n;
+    }
+    return 0;
+  }
   Work w;
   if (prepare(ctx, L, tokens, w)) return -1;
   if (route_launch(ctx, L, w, x)) return -1;
@@ -1745,6 +1773,22 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
                                      int *route_idx, float *route_weight) {
   if (!ctx || !L || !y || !x) return fail_arg("coli_cuda_moe_forward: null argument");
   if (!prof_active(ctx)) prof_open(ctx);
+  const int tmax = tokens_per_step(L->sh.experts);
+  if (tokens > tmax && tmax > 0) {
+    // a long block (a whole prompt): balanced steps of at most tmax tokens,
+    // never a lone token (which would take the decode kernels)
+    const int nc = (tokens + tmax - 1) / tmax;
+    const size_t H = (size_t)L->sh.hidden, K = (size_t)L->sh.topk;
+    for (int c = 0, t0 = 0; c < nc; c++) {
+      const int n = tokens / nc + (c < tokens % nc ? 1 : 0);
+      if (coli_cuda_moe_forward(ctx, L, y + (size_t)t0 * H, x + (size_t)t0 * H, n,
+                                route_idx ? route_idx + (size_t)t0 * K : nullptr,
+                                route_weight ? route_weight + (size_t)t0 * K : nullptr))
+        return -1;
+      t0 += n;
+    }
+    return 0;
+  }
   if (tokens == 1 && !ctx->moe_generic_only) {
     if (ctx->moe_decode_mode == 0) {
       ColiMoeLayer *one[1] = {L};
@@ -1761,7 +1805,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   mark(ctx, 0);
   if (route_launch(ctx, L, w, x)) return -1;
   mark(ctx, 1);
-  size_t bucket_lds = (size_t)w.E * ((T + 31) / 32) * 4 + (size_t)(2 * w.E + 1) * 4;
+  const size_t bucket_lds = bucket_lds_bytes(w.E, T);
   if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
   k_bucket<<<1, 1024, bucket_lds, st>>>(w);
   mark(ctx, 2);
@@ -1905,9 +1949,12 @@ extern "C" int coli_cuda_router_topk(ColiCuda *ctx, const float *logits, int tok
 
 extern "C" int coli_cuda_moe_bucket(ColiCuda *ctx, const int *idx, int tokens, int topk, int experts, int *offsets,
                                     int *token, int *slot) {
-  if (!ctx || !idx || !offsets || !token || !slot || tokens <= 0 || tokens > kMaxTokens || topk <= 0 ||
-      experts <= 0 || experts > 512)
-    return fail_arg("coli_cuda_moe_bucket: invalid argument (tokens<=%d, experts<=512)", kMaxTokens);
+  if (!ctx || !idx || !offsets || !token || !slot || tokens <= 0 || topk <= 0 || experts <= 0 || experts > 4096)
+    return fail_arg("coli_cuda_moe_bucket: invalid argument");
+  if (tokens > tokens_per_step(experts))
+    return fail_arg("coli_cuda_moe_bucket: %d tokens x %d experts exceed one workgroup's bucketing map "
+                    "(at most %d tokens for %d experts)",
+                    tokens, experts, tokens_per_step(experts), experts);
   size_t R = (size_t)tokens * topk;
   size_t need = R * 4 + (R + experts) * 16 + 256;
   if (ensure_scratch(ctx, kScrRoutes, need, "bucket scratch")) return -1;
@@ -1915,7 +1962,7 @@ extern "C" int coli_cuda_moe_bucket(ColiCuda *ctx, const int *idx, int tokens, i
   int *pos = (int *)b;
   int4 *items = (int4 *)(b + ((R * 4 + 15) & ~(size_t)15));
   int *nitems = (int *)(b + need - 64);
-  size_t lds = (size_t)experts * ((tokens + 31) / 32) * 4 + (size_t)(2 * experts + 1) * 4;
+  const size_t lds = bucket_lds_bytes(experts, tokens);
   if (set_lds((const void *)k_bucket_only, lds)) return -1;
   k_bucket_only<<<1, 1024, lds, ctx->stream>>>(idx, tokens, topk, experts, offsets, token, slot, pos, items,
                                                 nitems);

@@ -113,3 +113,39 @@ def test_batched_stack_equals_layer_calls(be):
     for l in range(nl):
         y1, _, _ = layers[l].forward_host(x[l])
         assert np.array_equal(ys[l].view(np.uint32), y1.view(np.uint32)), l
+
+
+@pytest.mark.parametrize("shape,T", [((512, 32, 4, 128, 128, 3), 4100), ((512, 1024, 8, 128, 128, 4), 1300)],
+                         ids=["E32_T4100", "E1024_T1300"])
+def test_long_block_runs_in_steps(be, oracle, shape, T):
+    """A block longer than one step (2048 tokens, or fewer when the bucketing
+    map of many experts fills the LDS: 1184 at E = 1024) runs as balanced
+    steps; every token's routes and output still match moe_prefill_grouped
+    (c/qwen.c:4141-4206) on the whole block."""
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish, fmt = shape
+    oracle.set_threads(16)
+    hl = oracle.host_layer(63, 1, H, E, K, I, Ish, fmt)
+    L = MoeLayer(be, H, E, K, I, Ish, fmt)
+    L.synthesize(63, 1)
+    x = np.stack([oracle.synth_x(63, 1, t, H) for t in range(T)])
+    print(f"[long block] E={E} T={T}", flush=True)
+    want, tr = oracle.moe_prefill(hl, x, trace=True)
+    y, idx, w = L.forward_host(x)
+    assert np.array_equal(idx, tr["idx"])
+    assert np.max(np.abs(w - tr["weight"])) <= 1e-5
+    assert_close_rms(y, want, 1e-3, f"long block E={E} T={T}")
+    L.close()
+
+
+def test_bucket_limit_follows_the_lds_map(be, oracle):
+    """coli_cuda_moe_bucket takes as many tokens as the E x T map fits in
+    160 KiB (1184 tokens at 1024 experts) and rejects one more with a message,
+    before any launch."""
+    rng = np.random.default_rng(12)
+    E, K = 1024, 8
+    idx = np.stack([rng.choice(E, K, replace=False) for _ in range(1184)]).astype(np.int32)
+    _check_bucket(be, oracle, idx, E)
+    d = be.alloc(1185 * K * 4)
+    rc = be.lib.coli_cuda_moe_bucket(be.ctx, d.p, 1185, K, E, d.p, d.p, d.p)
+    assert rc == -1 and "1184 tokens" in be.last_error(), be.last_error()

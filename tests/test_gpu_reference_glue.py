@@ -62,6 +62,10 @@ class Glue:
         lib.ref_moe_forward.argtypes = [C.c_void_p, f32p, f32p]
         lib.ref_moe_cuda_block.restype = C.c_int
         lib.ref_moe_cuda_block.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        lib.ref_sw_register.restype = C.c_int
+        lib.ref_sw_register.argtypes = [C.c_void_p]
+        lib.ref_sw_forward.restype = C.c_int
+        lib.ref_sw_forward.argtypes = [C.c_void_p, f32p, C.c_int, f32p, C.POINTER(C.c_int)]
         self.lib = lib
         self.f32p = f32p
 
@@ -76,6 +80,15 @@ class Glue:
         out = np.zeros(H, np.float32)
         self.lib.ref_moe_forward(h, ptr(x, self.f32p), ptr(out, self.f32p))
         return out
+
+    def sw_forward(self, h, x, K):
+        from oracle.pyoracle import ptr
+        T, H = x.shape
+        out = np.zeros((T, H), np.float32)
+        idx = np.zeros((T, K), np.int32)
+        used = self.lib.ref_sw_forward(h, ptr(np.ascontiguousarray(x), self.f32p), T, ptr(out, self.f32p),
+                                       ptr(idx, C.POINTER(C.c_int)))
+        return used, out, idx
 
     def block(self, h, x):
         from oracle.pyoracle import ptr
@@ -173,5 +186,37 @@ def test_reference_glue_speculative_block(glue, oracle):
             want, tr = oracle.moe_prefill(hl, x, trace=True)
             want = _with_fp32_shared(oracle, hl, x, want, tr)
             assert_close_rms(got, want, 5e-3, f"speculative block T={T}")
+    finally:
+        glue.lib.ref_layer_destroy(h)
+
+
+@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397)],
+                         ids=["s35_q4", "s397_q3"])
+def test_bridge_device_moe_step(glue, oracle, shape, seed):
+    """shiftwing_amd/integration/sw_qwen_bridge.inc compiled into the reference
+    engine: sw_moe_register copies a loaded MoeW (router, shared expert, every
+    routed expert) into an HBM-resident layer, and sw_moe_try runs the MoE step
+    on the device for T tokens.  Checked against moe_forward (T = 1) and
+    moe_prefill_grouped (T > 1) on the CPU: router indices exact (rank order
+    included), outputs within max-abs 1e-3 x RMS."""
+    H, E, K, I, Ish, fmt = shape
+    hl = oracle.host_layer(seed, 4, H, E, K, I, Ish, fmt)
+    h = glue.lib.ref_layer_create(C.byref(hl.st))
+    try:
+        print(f"[bridge] register {shape}", flush=True)
+        assert glue.lib.ref_sw_register(h) == 1
+        for T in (1, 4, 37):
+            print(f"[bridge] {shape[0]} T={T}", flush=True)
+            x = np.stack([oracle.synth_x(seed, 4, 200 + t, H) for t in range(T)])
+            used, got, idx = glue.sw_forward(h, x, K)
+            assert used == 1 and glue.counters()["failed"] == 0
+            if T == 1:
+                want, tr = oracle.moe_forward(hl, x[0], trace=True)
+                want, want_idx = want[None], tr["idx"][None]
+            else:
+                want, tr = oracle.moe_prefill(hl, x, trace=True)
+                want_idx = tr["idx"]
+            assert np.array_equal(idx, want_idx), (T, idx, want_idx)
+            assert_close_rms(got, want, 1e-3, f"bridge T={T}")
     finally:
         glue.lib.ref_layer_destroy(h)
