@@ -363,6 +363,31 @@ int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *layer,
 /* Device pointer to the layer's router [E x H] (for in-place edits). */
 float *coli_cuda_moe_layer_router(ColiMoeLayer *layer);
 
+/* A converted snapshot (the reference's container: every *.safetensors
+ * file of a directory, c/st.h; tensor names and formats of c/qwen.c:2165-2295,
+ * 2443-2457; the .q3 sidecar of c/tools/requantize_expert_q2.py).  Names are
+ * looked up with the reference's prefixes "", "model.", "model.language_model."
+ * and quantised matrices are classified as load_qmat_mode does (the .qtype
+ * tag, else the payload and scale sizes).  Errors return -1 with a message
+ * (the reference exits instead). */
+typedef struct ColiContainer ColiContainer;
+int coli_cuda_container_open(ColiContainer **out, const char *snapshot_dir);
+void coli_cuda_container_close(ColiContainer *c);
+/* tensors indexed over all files */
+int coli_cuda_container_tensors(const ColiContainer *c);
+/* MoE layer `layer` as stored: hidden, experts, intermediate,
+ * shared_intermediate, expert_format (3 or 4; 2 for int2, which the device
+ * layer does not take) and group_size.  topk is not stored: shape->topk is
+ * left as the caller set it.  use_q3 selects every routed expert's .q3
+ * sidecar (the reference's EXPERT_Q3=1). */
+int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int use_q3,
+                                  ColiMoeShape *shape);
+/* Create an HBM-resident layer and fill it from the container: router and
+ * gate row (F32, BF16 or F16), the int8 shared expert, every routed expert
+ * (int4, or int3 from the sidecar), repacked on the device. */
+int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer,
+                             int topk, int use_q3, ColiMoeLayer **out);
+
 /* The MoE step for `tokens` activation rows (any number: a long block runs
  * as balanced steps of at most 2048 tokens, fewer for more than 512
  * experts; tokens are independent): y[t] = sum_k w[t,k] *

@@ -15,7 +15,7 @@ import numpy as np
 
 from .abi import ColiMoeShape, load
 
-__all__ = ["Backend", "DeviceBuffer", "MoeLayer", "ColiMoeShape", "HipError", "load"]
+__all__ = ["Backend", "Container", "DeviceBuffer", "MoeLayer", "ColiMoeShape", "HipError", "load"]
 
 
 class HipError(RuntimeError):
@@ -114,8 +114,52 @@ class Backend:
             pass
 
 
+class Container:
+    """A converted snapshot directory (coli_cuda_container_*): the reference's
+    safetensors files, indexed once; layers are loaded from it with
+    MoeLayer.load."""
+
+    def __init__(self, snapshot_dir: str):
+        self.lib = load()
+        h = C.c_void_p()
+        if self.lib.coli_cuda_container_open(C.byref(h), snapshot_dir.encode()) != 0:
+            raise HipError(f"coli_cuda_container_open: {self.lib.coli_cuda_last_error().decode()}")
+        self.h = h
+
+    def tensors(self) -> int:
+        return self.lib.coli_cuda_container_tensors(self.h)
+
+    def moe_shape(self, layer: int, topk: int = 0, use_q3: bool = False) -> ColiMoeShape:
+        s = ColiMoeShape(0, 0, topk, 0, 0, 0, 0)
+        if self.lib.coli_cuda_container_moe_shape(self.h, layer, int(use_q3), C.byref(s)) != 0:
+            raise HipError(f"coli_cuda_container_moe_shape: {self.lib.coli_cuda_last_error().decode()}")
+        return s
+
+    def close(self):
+        if self.h:
+            self.lib.coli_cuda_container_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class MoeLayer:
     """An HBM-resident MoE layer (coli_cuda_moe_layer_*)."""
+
+    @classmethod
+    def load(cls, be: Backend, container: Container, layer: int, topk: int, use_q3: bool = False) -> "MoeLayer":
+        """The layer `layer` of a converted snapshot (coli_cuda_moe_layer_load)."""
+        shape = container.moe_shape(layer, topk, use_q3)
+        h = C.c_void_p()
+        be.check(be.lib.coli_cuda_moe_layer_load(be.ctx, container.h, layer, topk, int(use_q3), C.byref(h)),
+                 "coli_cuda_moe_layer_load")
+        self = cls.__new__(cls)
+        self.be, self.shape, self.h = be, shape, h
+        return self
 
     def __init__(self, be: Backend, hidden: int, experts: int, topk: int, intermediate: int,
                  shared_intermediate: int, expert_format: int, group_size: int = 128):

@@ -1,0 +1,122 @@
+"""The converted-snapshot loader's host side, without a GPU: indexing the
+safetensors files of a directory (c/st.h), the reference's name prefixes and
+format detection (load_qmat_mode, c/qwen.c:2224-2257: the .qtype tag, else the
+payload and scale sizes; the .q3 sidecar of c/tools/requantize_expert_q2.py),
+and its errors, which return -1 with a message where the reference exits."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import st_writer
+from conftest import ROOT
+
+SHAPE = (512, 16, 4, 256, 128)  # H, E, K, I, Ish
+
+
+def _lib():
+    from shiftwing_amd import abi
+    return abi.load()
+
+
+def _open(lib, d):
+    c = C.c_void_p()
+    rc = lib.coli_cuda_container_open(C.byref(c), d.encode())
+    return rc, c
+
+
+def _shape(lib, c, layer, use_q3):
+    from shiftwing_amd import ColiMoeShape
+    s = ColiMoeShape(0, 0, 7, 0, 0, 0, 0)
+    rc = lib.coli_cuda_container_moe_shape(c, layer, use_q3, C.byref(s))
+    return rc, s
+
+
+@pytest.fixture(scope="module")
+def layers(oracle):
+    H, E, K, I, Ish = SHAPE
+    return (oracle.host_layer(5, 3, H, E, K, I, Ish, 4), oracle.host_layer(5, 3, H, E, K, I, Ish, 3))
+
+
+@pytest.mark.parametrize("prefix", ["", "model.", "model.language_model."])
+def test_container_shapes_and_formats(tmp_path, layers, prefix):
+    hl4, hl3 = layers
+    lib = _lib()
+    t = st_writer.moe_layer_tensors(hl4, 3, prefix, q3=hl3)
+    st_writer.write_split(str(tmp_path), t, parts=3)
+    rc, c = _open(lib, str(tmp_path))
+    assert rc == 0, lib.coli_cuda_last_error()
+    try:
+        assert lib.coli_cuda_container_tensors(c) == len(t)
+        H, E, K, I, Ish = SHAPE
+        for use_q3, fmt in ((0, 4), (1, 3)):
+            rc, s = _shape(lib, c, 3, use_q3)
+            assert rc == 0, lib.coli_cuda_last_error()
+            assert (s.hidden, s.experts, s.topk, s.intermediate, s.shared_intermediate, s.expert_format,
+                    s.group_size) == (H, E, 7, I, Ish, fmt, 128)
+        rc, s = _shape(lib, c, 2, 0)  # no such layer
+        assert rc == -1 and "layer 2" in lib.coli_cuda_last_error().decode()
+    finally:
+        lib.coli_cuda_container_close(c)
+
+
+def test_container_formats_without_tags(tmp_path, layers):
+    """Without .qtype tags the sizes decide (c/qwen.c:2237-2254): the shared
+    rows are int8 (payload rows x cols, one scale per row), the experts int4."""
+    hl4, _ = layers
+    lib = _lib()
+    st_writer.write_split(str(tmp_path), st_writer.moe_layer_tensors(hl4, 0, qtype_tags=False), parts=1)
+    rc, c = _open(lib, str(tmp_path))
+    assert rc == 0, lib.coli_cuda_last_error()
+    rc, s = _shape(lib, c, 0, 0)
+    assert rc == 0 and s.expert_format == 4 and s.group_size == 128
+    lib.coli_cuda_container_close(c)
+
+
+def test_container_errors(tmp_path, layers):
+    hl4, _ = layers
+    lib = _lib()
+    # no safetensors file
+    rc, _ = _open(lib, str(tmp_path))
+    assert rc == -1 and "no .safetensors" in lib.coli_cuda_last_error().decode()
+    # a header that is not JSON
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    with open(bad / "x.safetensors", "wb") as f:
+        f.write((7).to_bytes(8, "little") + b"{nope!!")
+    rc, _ = _open(lib, str(bad))
+    assert rc == -1 and "x.safetensors" in lib.coli_cuda_last_error().decode()
+    # data offsets past the end of the file
+    bad2 = tmp_path / "bad2"
+    bad2.mkdir()
+    st_writer.write(str(bad2 / "y.safetensors"), {"a": np.zeros(4, np.float32)})
+    raw = open(bad2 / "y.safetensors", "rb").read()
+    open(bad2 / "y.safetensors", "wb").write(raw[:-4])
+    rc, _ = _open(lib, str(bad2))
+    assert rc == -1 and "does not fit" in lib.coli_cuda_last_error().decode()
+    # a quantized expert without .qs
+    t = st_writer.moe_layer_tensors(hl4, 0)
+    del t["layers.0.mlp.experts.0.gate_proj.weight.qs"]
+    d3 = tmp_path / "noqs"
+    st_writer.write_split(str(d3), t, parts=1)
+    rc, c = _open(lib, str(d3))
+    assert rc == 0
+    rc, _ = _shape(lib, c, 0, 0)
+    assert rc == -1 and ".qs" in lib.coli_cuda_last_error().decode()
+    # an unknown qtype tag
+    t = st_writer.moe_layer_tensors(hl4, 0)
+    t["layers.0.mlp.experts.0.gate_proj.weight.qtype"] = np.array([5], np.uint8)
+    d4 = tmp_path / "tag"
+    st_writer.write_split(str(d4), t, parts=1)
+    rc, c2 = _open(lib, str(d4))
+    rc, _ = _shape(lib, c2, 0, 0)
+    assert rc == -1 and "qtype" in lib.coli_cuda_last_error().decode()
+    lib.coli_cuda_container_close(c)
+    lib.coli_cuda_container_close(c2)
+    # the .q3 sidecar asked for but absent
+    st_writer.write_split(str(tmp_path / "noq3"), st_writer.moe_layer_tensors(hl4, 0), parts=1)
+    rc, c3 = _open(lib, str(tmp_path / "noq3"))
+    rc, _ = _shape(lib, c3, 0, 1)
+    assert rc == -1 and ".q3" in lib.coli_cuda_last_error().decode()
+    lib.coli_cuda_container_close(c3)
