@@ -399,6 +399,14 @@ int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *layer, float *y,
                           const float *x, int tokens, int *route_idx,
                           float *route_weight);
 
+/* The MoE half of a decoder layer on the residual stream, in place:
+ * n = rmsnorm_zero(x, norm_weight) (c/qwen.c:1780-1784, 4593), then
+ * x += MoE(n) (c/qwen.c:4594-4596).  x: device [tokens x H] f32, norm_weight:
+ * device [H] (the layer's post_norm).  The normalisation is a parallel sum of
+ * squares, within the output tolerance of the reference's serial one. */
+int coli_cuda_moe_block(ColiCuda *ctx, ColiMoeLayer *layer, float *x,
+                        const float *norm_weight, float eps, int tokens);
+
 /* Router only: idx / weight [tokens x K] (device). */
 int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *layer, const float *x,
                         int tokens, int *idx, float *weight);

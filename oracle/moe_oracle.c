@@ -281,6 +281,19 @@ void or_qmat_mul_batch(float *y, const float *x, int B, int ldx,
 }
 
 /* sigmoidf_stable / siluf, qwen.c:307-308 (glibc expf). */
+/* rmsnorm_zero (c/qwen.c:1780-1784), the step before the MoE
+ * (c/qwen.c:4593): the sum of squares is a serial chain, multiply then add,
+ * as the reference's flags compile it (the same finding as for dot()). */
+void or_rmsnorm_zero(float *out, const float *x, const float *w, int n, float eps) {
+    float ms = 0.f;
+    for (int i = 0; i < n; i++) {
+        const float p = x[i] * x[i];
+        ms = ms + p;
+    }
+    const float r = 1.f / sqrtf(ms / (float)n + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * r * (1.f + w[i]);
+}
+
 float or_expf(float x) { return expf(x); }
 float or_sigmoidf(float x) {
     if (x >= 0) {

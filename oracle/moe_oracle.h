@@ -64,6 +64,7 @@ void or_qmat_mul(float *y, const float *x, const or_qmat *w, int allow_idot);
 void or_qmat_mul_batch(float *y, const float *x, int B, int ldx,
                        const or_qmat *w, int allow_idot);
 float or_expf(float x);
+void or_rmsnorm_zero(float *out, const float *x, const float *w, int n, float eps);
 float or_sigmoidf(float x);
 float or_siluf(float x);
 void or_sigmoid_batch(const float *x, float *y, int64_t n);

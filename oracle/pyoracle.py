@@ -120,6 +120,8 @@ class Oracle:
         for nm in ("or_sigmoid_batch", "or_expf_batch"):
             getattr(L, nm).restype = None
             getattr(L, nm).argtypes = [f32p, f32p, C.c_int64]
+        L.or_rmsnorm_zero.restype = None
+        L.or_rmsnorm_zero.argtypes = [f32p, f32p, f32p, C.c_int, C.c_float]
         L.or_siluf.restype = C.c_float
         L.or_siluf.argtypes = [C.c_float]
         L.or_set_threads.restype = None
@@ -200,6 +202,15 @@ class Oracle:
     def set_threads(self, n: int):
         self.lib.or_set_threads(n)
 
+    def rmsnorm_zero(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        for r in range(x.shape[0] if x.ndim == 2 else 1):
+            xr = x[r] if x.ndim == 2 else x
+            orow = out[r] if x.ndim == 2 else out
+            self.lib.or_rmsnorm_zero(ptr(orow, f32p), ptr(xr, f32p), ptr(w, f32p), xr.size, eps)
+        return out
+
     def sigmoid_batch(self, x: np.ndarray) -> np.ndarray:
         y = np.empty_like(x)
         self.lib.or_sigmoid_batch(ptr(x, f32p), ptr(y, f32p), x.size)
@@ -249,6 +260,8 @@ class Reference:
         L.ref_moe_forward.argtypes = [C.c_void_p, f32p, f32p]
         L.ref_moe_prefill_grouped.restype = None
         L.ref_moe_prefill_grouped.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        L.ref_rmsnorm_zero.restype = None
+        L.ref_rmsnorm_zero.argtypes = [f32p, f32p, f32p, C.c_int, C.c_float]
         L.ref_set_threads.restype = None
         L.ref_set_threads.argtypes = [C.c_int]
         L.ref_omp_threads.restype = C.c_int
@@ -278,6 +291,12 @@ class Reference:
         q = np.zeros(x.size, np.int8)
         s = self.lib.ref_qrow_i8(ptr(x, f32p), ptr(q), x.size)
         return q, np.float32(s)
+
+    def rmsnorm_zero(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.ref_rmsnorm_zero(ptr(out, f32p), ptr(x, f32p), ptr(w, f32p), x.size, eps)
+        return out
 
     def layer(self, host_layer: "HostLayer"):
         return RefLayer(self, host_layer)

@@ -8,7 +8,7 @@
  * (c/qwen.c:68-94, 225-243) and calls its static functions:
  *   dot 1674, qrow_i8 1696, dot_i8i8 1697, dot_q4_group 1706,
  *   dot_q3_group 1730, qmat_mul_ex 1761, qmat_mul_batch 3305,
- *   router_topk 3421, mlp_one 3415, moe_forward 3717,
+ *   router_topk 3421, mlp_one 3415, moe_forward 3717, rmsnorm_zero 1780,
  *   moe_prefill_grouped 4141.
  * Every expert is resident (cap = E), so the expert cache never loads. */
 #define QWEN_NO_MAIN
@@ -57,6 +57,9 @@ int32_t ref_dot_i8i8(const int8_t *w, const int8_t *x, int n) { return dot_i8i8(
 float ref_dot_q4_group(const uint8_t *w, const float *x, int n) { return dot_q4_group(w, x, n); }
 float ref_dot_q3_group(const uint8_t *w, const float *x, int n) { return dot_q3_group(w, x, n); }
 float ref_expf(float x) { return expf(x); }
+void ref_rmsnorm_zero(float *out, const float *x, const float *w, int n, float eps) {
+    rmsnorm_zero(out, x, w, n, eps);
+}
 float ref_siluf(float x) { return siluf(x); }
 
 void ref_qmat_mul(float *y, const float *x, const or_qmat *w, int allow_idot) {

@@ -1867,6 +1867,25 @@ extern "C" int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *
   return 0;
 }
 
+// x[i] += y[i] (the residual add after the MoE, c/qwen.c:4596)
+__global__ static void k_residual_add(float *x, const float *y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] += y[i];
+}
+
+extern "C" int coli_cuda_moe_block(ColiCuda *ctx, ColiMoeLayer *L, float *x, const float *norm_weight, float eps,
+                                   int tokens) {
+  if (!ctx || !L || !x || !norm_weight || tokens <= 0) return fail_arg("coli_cuda_moe_block: invalid argument");
+  const size_t H = (size_t)L->sh.hidden, n = (size_t)tokens * H;
+  if (ensure_scratch(ctx, kScrBlock, 2 * n * sizeof(float), "MoE block scratch")) return -1;
+  float *xn = (float *)ctx->scratch[kScrBlock], *y = xn + n;
+  if (coli_cuda_rmsnorm_zero_batch(ctx, xn, x, norm_weight, tokens, (int)H, eps) ||
+      coli_cuda_moe_forward(ctx, L, y, xn, tokens, nullptr, nullptr))
+    return -1;
+  k_residual_add<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(x, y, n);
+  return launch_status("coli_cuda_moe_block");
+}
+
 __global__ static void k_synth_x(float *x, int rows, int cols, uint64_t seed, uint32_t layer, int step0) {
   int r = blockIdx.y;
   int i = blockIdx.x * blockDim.x + threadIdx.x;

@@ -39,6 +39,7 @@ enum Scratch {
   kScrRoutes,      // many-token step: idx / weights / buckets
   kScrShared,      // three-kernel decode: shared expert int32 sums + h
   kScrStack,       // persistent decode: router records, exact logits, h records
+  kScrBlock,       // MoE block: normalised activations and the MoE output
   kScrCount
 };
 

@@ -237,3 +237,38 @@ def test_oracle_matches_compiled_reference(oracle):
         for t in range(4):
             assert np.array_equal(_bits(oracle.moe_forward(hl, X[t])), _bits(rl.forward(X[t]))), (seed, t)
         assert np.array_equal(_bits(oracle.moe_prefill(hl, X)), _bits(rl.prefill(X))), seed
+
+
+def test_rmsnorm_zero_matches_compiled_reference_and_closed_form(oracle):
+    """or_rmsnorm_zero (c/qwen.c:1780-1784): bit-exact with the compiled
+    reference where oracle/_ref is built; a constant row c gives
+    c / sqrt(c^2 + eps) * (1 + w) exactly as the reference's float steps
+    compute it; a fused multiply-add chain (a plausible mistake) does not
+    match the reference on random rows."""
+    import numpy as np
+    rng = np.random.default_rng(8)
+    x = np.full(64, 0.75, np.float32)
+    w = (rng.standard_normal(64) * 0.1).astype(np.float32)
+    got = oracle.rmsnorm_zero(x, w, 1e-6)
+    ms = np.float32(0)
+    for v in x:
+        ms = np.float32(ms + np.float32(v * v))
+    r = np.float32(1) / np.sqrt(np.float32(ms / np.float32(64) + np.float32(1e-6)))
+    assert np.array_equal(got, (x * r).astype(np.float32) * (np.float32(1) + w))
+    try:
+        from oracle.pyoracle import Reference
+        ref = Reference()
+    except FileNotFoundError:
+        pytest.skip("oracle/_ref not built")
+    fma_differs = 0
+    for n in (4096, 2048, 1027):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        w = (rng.standard_normal(n) * 0.1).astype(np.float32)
+        a, b = oracle.rmsnorm_zero(x, w, 1e-6), ref.rmsnorm_zero(x, w, 1e-6)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), n
+        ms = np.float32(0)
+        for v in x:  # fused chain: one rounding per term
+            ms = np.float32(np.float64(v) * np.float64(v) + np.float64(ms))
+        r = np.float32(1) / np.sqrt(np.float32(ms / np.float32(n) + np.float32(1e-6)))
+        fma_differs += not np.array_equal(((x * r) * (np.float32(1) + w)).astype(np.float32), b)
+    assert fma_differs > 0
