@@ -1,20 +1,26 @@
 """MoE decode benchmark on one MI355X.
 
-Workload (the north-star config): a
+Headline (the north-star config): a
 Qwen3.5-397B-A17B-shaped MoE stack, 60 layers, hidden 4096, 512 routed experts
 in grouped int3 (g128, uniform random codes, |N(0,0.01)| scales), top-10
 softmax router (fp32 ~N(0,0.02)), one int8 shared expert (intermediate 1024);
 all 157 GB of expert weights resident in HBM; batch-1 decode with seeded
-N(0,1) activations per (step, layer).  `--workload s35` runs configs[1]
-(35B-A3B shape, 40 layers, int4) instead.
+N(0,1) activations per (step, layer).  A step is one decoded token through
+every layer of the stack, layer l+1 starting after layer l's output is written
+(strict decode order).  `value` is tokens/s with all inputs already in HBM.
 
-A step is one decoded token through every layer of the stack, layer l+1
-starting after layer l's output is written (strict decode order).  `value` is
-tokens/s with all inputs already in HBM.  The roofline object reports the
-dominant kernel of the step: algorithmic bytes per launch over its average
-duration, measured with HIP events on the context stream.  cpu_baseline times
-the reference's own CPU MoE code (c/qwen.c moe_forward, compiled in place into
-oracle/_ref) on the host cores over a bounded sample of the same workload.
+The default run also times, in the same process, and reports under
+"configs": configs[3] (continuous-batch decode on the same stack with Zipf(1.1)
+routing, B = 1, 4, 8, 16, 32), configs[4] (a 512-token prefill chunk through
+one S397 and one S35 layer) and configs[1] (the 40-layer S35 int4 stack,
+batch-1 decode, Zipf routing).  `--workload` runs one of them alone.
+
+Every result carries a roofline object for its dominant kernel (algorithmic
+bytes per launch over the launch's duration, HIP events on the context
+stream) and a cpu_baseline: the reference's own CPU MoE code (c/qwen.c
+moe_forward / moe_prefill_grouped, compiled in place into oracle/_ref) on a
+bounded sample of the same workload, with every usable host CPU and with 8
+threads, next to the host CPU's model and physical core count.
 """
 from __future__ import annotations
 
@@ -22,6 +28,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -84,47 +91,106 @@ def kernel_bytes(H, E, K, I, Ish, fmt):
             K * down + H * Ish + 2 * Ish * 4 + H * 4]
 
 
-def cpu_baseline(cfg, budget_s: float):
-    """The reference CPU path on a bounded sample: two layers of the stack
-    materialised on the host (identical bytes), decode tokens until the time
-    budget is spent; tok/s scaled to the full stack."""
+def cpu_info():
+    """The host CPU as lscpu describes it, and the CPUs this process may use
+    (the GPU box gives a job a share of the host's CPUs)."""
+    info = {"model": None, "physical_cores": None, "logical_cpus": os.cpu_count(),
+            "usable_cpus": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                kv[k.strip()] = v.strip()
+        info["model"] = kv.get("Model name")
+        cps, sockets = kv.get("Core(s) per socket"), kv.get("Socket(s)")
+        if cps and sockets and cps.isdigit() and sockets.isdigit():
+            info["physical_cores"] = int(cps) * int(sockets)
+    except Exception:
+        pass
+    return info
+
+
+_HOST_LAYERS = {}
+
+
+def host_layer(o, seed, l, H, E, K, I, Ish, fmt):
+    key = (seed, l, H, E, K, I, Ish, fmt)
+    if key not in _HOST_LAYERS:
+        _HOST_LAYERS[key] = o.host_layer(seed, l, H, E, K, I, Ish, fmt)
+    return _HOST_LAYERS[key]
+
+
+def _timed(run_one, budget_s, max_n):
+    run_one(0)  # warm the caches
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < max_n:
+        n += run_one(n + 1)
+    return n, time.perf_counter() - t0
+
+
+def cpu_baseline(cfg, budget_s: float, zipf_rec=None):
+    """The reference CPU path (c/qwen.c moe_forward, compiled in place into
+    oracle/_ref) on a bounded sample: two layers of the same synthetic stack
+    materialised on the host (identical bytes), tokens decoded until the time
+    budget is spent, tok/s scaled to the full stack.  Timed with every usable
+    host CPU, then again with 8 threads (the reference's 8-core desktop
+    figures)."""
     H, E, K, I, Ish, fmt, layers, seed, _ = cfg
     from oracle import pyoracle as po
     o = po.Oracle()
-    kind = "port"
-    runner = None
+    kind, ref = "port", None
     try:
         ref = po.Reference()
         kind = "reference"
     except Exception:
-        ref = None
-    threads = os.cpu_count() or 1
+        pass
     sample_layers = 2
-    hls = [o.host_layer(seed, l, H, E, K, I, Ish, fmt) for l in range(sample_layers)]
-    if ref is not None:
-        ref.set_threads(threads)
-        rls = [ref.layer(hl) for hl in hls]
-        runner = lambda l, x: rls[l].forward(x)  # noqa: E731
-    else:
-        o.set_threads(threads)
-        runner = lambda l, x: o.moe_forward(hls[l], x)  # noqa: E731
-    # warm the caches once per layer
-    for l in range(sample_layers):
-        runner(l, o.synth_x(seed, l, 0, H))
-    n, t0 = 0, time.perf_counter()
-    step = 1
-    while time.perf_counter() - t0 < budget_s and n < 4096:
+    hls = [host_layer(o, seed, l, H, E, K, I, Ish, fmt) for l in range(sample_layers)]
+    if zipf_rec is not None:
+        from shiftwing_amd import zipf
+        for l, hl in enumerate(hls):
+            hl.set_router_column(H - 1, zipf.zipf_column(E, zipf_rec["beta"], seed, l))
+    rls = [ref.layer(hl) for hl in hls] if ref is not None else None
+
+    def x_of(l, step):
+        x = o.synth_x(seed, l, step, H)
+        if zipf_rec is not None:
+            x[H - 1] = 1.0
+        return x
+
+    def one(i):
         for l in range(sample_layers):
-            runner(l, o.synth_x(seed, l, step, H))
-            n += 1
-        step += 1
-    dt = time.perf_counter() - t0
-    per_token_layer = dt / n
-    value = 1.0 / (per_token_layer * layers)
-    return {"value": round(value, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n} token-layers over layers 0..{sample_layers - 1} of the same synthetic stack "
-                      f"({dt:.1f} s, {per_token_layer * 1e3:.3f} ms per token-layer), scaled to {layers} layers",
-            "lib": os.path.basename(ref.path) if ref is not None else "liboracle.so"}
+            x = x_of(l, i)
+            rls[l].forward(x) if rls is not None else o.moe_forward(hls[l], x)
+        return sample_layers
+
+    info = cpu_info()
+    out = {"unit": "tok/s", "kind": kind, "lib": os.path.basename(ref.path) if ref is not None else "liboracle.so",
+           "cpu_model": info["model"], "physical_cores": info["physical_cores"],
+           "logical_cpus": info["logical_cpus"]}
+    for threads, key in ((info["usable_cpus"], "value"), (8, "value_8_threads")):
+        (ref.set_threads if ref is not None else o.set_threads)(threads)
+        n, dt = _timed(one, budget_s if key == "value" else budget_s / 2, 4096)
+        out[key] = round(1.0 / (dt / n * layers), 3)
+        if key == "value":
+            out["cores"] = threads
+            out["sample"] = (f"{n} token-layers over layers 0..{sample_layers - 1} of the same synthetic stack "
+                             f"({dt:.1f} s, {dt / n * 1e3:.3f} ms per token-layer, {threads} threads), "
+                             f"scaled to {layers} layers")
+    if zipf_rec is not None:
+        for l, hl in enumerate(hls):  # the cached layers go back to uniform routing
+            hl.set_router_column(H - 1, _uniform_column(o, seed, l, H, E))
+    return out
+
+
+def _uniform_column(o, seed, l, H, E):
+    from oracle import pyoracle as po
+    r = np.zeros((E, H), np.float32)
+    g = np.zeros(H, np.float32)
+    o.lib.or_synth_router(seed, l, E, H, po.ptr(r, po.f32p), po.ptr(g, po.f32p))
+    return r[:, H - 1].copy()
 
 
 def copy_probe(mib: int):
@@ -206,98 +272,186 @@ def stage_model(H, E, K, I, Ish, fmt, T, U):
     return names, nbytes, flops
 
 
-def cpu_baseline_many(cfg, T, zipf_cfg, budget_s: float):
+def cpu_baseline_many(cfg, T, zipf_rec, budget_s: float, layers_per_step: int):
     """The reference CPU path for T-token blocks (c/qwen.c moe_prefill_grouped,
-    compiled in place) on one layer of the same synthetic stack, Zipf column
-    and constant feature included when the workload routes by Zipf; repeated
-    blocks until the budget is spent, tok/s per layer scaled to the layer
-    count of the GPU step."""
-    H, E, K, I, Ish, fmt, layers, seed, _ = cfg
+    compiled in place) on layer 0 of the same synthetic stack, with the Zipf
+    column and constant feature when the workload routes by Zipf; blocks
+    repeated until the budget is spent, tok/s per layer scaled to the layer
+    count of the GPU step.  Every usable host CPU, then 8 threads."""
+    H, E, K, I, Ish, fmt, _, seed, _ = cfg
     from oracle import pyoracle as po
     o = po.Oracle()
-    hl = o.host_layer(seed, 0, H, E, K, I, Ish, fmt)
-    if zipf_cfg is not None:
+    hl = host_layer(o, seed, 0, H, E, K, I, Ish, fmt)
+    if zipf_rec is not None:
         from shiftwing_amd import zipf
-        hl.set_router_column(H - 1, zipf.zipf_column(E, zipf_cfg["beta"], seed, 0))
-    threads = os.cpu_count() or 1
+        hl.set_router_column(H - 1, zipf.zipf_column(E, zipf_rec["beta"], seed, 0))
+    ref = None
     try:
         ref = po.Reference()
-        ref.set_threads(threads)
         rl = ref.layer(hl)
         run, kind, lib = rl.prefill, "reference", os.path.basename(ref.path)
     except Exception:
-        o.set_threads(threads)
         run, kind, lib = (lambda x: o.moe_prefill(hl, x)), "port", "liboracle.so"
 
     def block(i):
         x = np.stack([o.synth_x(seed, 0, i * T + t, H) for t in range(T)])
-        if zipf_cfg is not None:
+        if zipf_rec is not None:
             x[:, H - 1] = 1.0
         return x
 
-    run(block(0))
-    n, t0, i = 0, time.perf_counter(), 1
-    while time.perf_counter() - t0 < budget_s and i < 64:
-        run(block(i))
-        n += 1
-        i += 1
-    dt = time.perf_counter() - t0
-    per_block = dt / max(n, 1)
-    return {"value": round(T / (per_block * layers), 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n} blocks of {T} tokens through layer 0 of the same synthetic stack ({dt:.1f} s, "
-                      f"{per_block * 1e3:.1f} ms per block-layer), scaled to {layers} layer(s) per step",
-            "lib": lib}
+    blocks = [block(i) for i in range(3)]
+
+    def one(i):
+        run(blocks[i % 3])
+        return 1
+
+    info = cpu_info()
+    out = {"unit": "tok/s", "kind": kind, "lib": lib, "cpu_model": info["model"],
+           "physical_cores": info["physical_cores"], "logical_cpus": info["logical_cpus"]}
+    for threads, key in ((info["usable_cpus"], "value"), (8, "value_8_threads")):
+        (ref.set_threads if ref is not None else o.set_threads)(threads)
+        n, dt = _timed(one, budget_s if key == "value" else budget_s / 2, 64)
+        out[key] = round(T / (dt / n * layers_per_step), 3)
+        if key == "value":
+            out["cores"] = threads
+            out["sample"] = (f"{n} blocks of {T} tokens through layer 0 of the same synthetic stack ({dt:.1f} s, "
+                             f"{dt / n * 1e3:.1f} ms per block-layer, {threads} threads), scaled to "
+                             f"{layers_per_step} layer(s) per step")
+    if zipf_rec is not None:
+        hl.set_router_column(H - 1, _uniform_column(o, seed, 0, H, E))
+    return out
 
 
-def bench_many(args):
-    """Configs 3 and 4: many tokens per MoE step through the many-token
-    kernels (bucketing, grouped gate/up and down, combine)."""
-    from shiftwing_amd import Backend, MoeLayer
-    base, nl, T, use_zipf, desc = MANY[args.workload]
-    H, E, K, I, Ish, fmt, layers_full, seed, _ = WORKLOADS[base]
-    cfg = (H, E, K, I, Ish, fmt, nl, seed, desc)
-    if T is None:
-        T = args.batch
-    if args.layers:
-        nl = args.layers
-    prefill = args.workload.startswith("prefill")
-    be = Backend(0)
-    lib = be.lib
-    t0 = time.perf_counter()
+ARITH = ("int3/int4 codes x two int8 activation digits on MFMA, fp32 group scaling; int8 IDOT shared expert; "
+         "fp64-certified exact fp32 router")
+
+
+def build_stack(be, name, n):
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish, fmt, _, seed, _ = WORKLOADS[name]
     stack = []
-    for l in range(nl):
+    for l in range(n):
         L = MoeLayer(be, H, E, K, I, Ish, fmt)
         L.synthesize(seed, l)
         stack.append(L)
     be.sync()
-    zipf_rec = apply_zipf(be, stack, cfg) if use_zipf else None
-    gen_s = time.perf_counter() - t0
-    resident = sum(L.nbytes() for L in stack)
-    total = args.warmup + args.steps
-    # activations: [layer][step][T][H] for the stack, [step][T][H] for prefill
+    return stack
+
+
+def measure_decode(be, stack, cfg, steps, warmup, zipf_rec, workload_key, decode_kernels=1):
+    """Batch-1 decode through the whole stack, one coli_cuda_moe_forward_layers
+    call per token (strict decode order)."""
+    H, E, K, I, Ish, fmt, layers, seed, desc = cfg
+    lib = be.lib
+    total = warmup + steps
+    xs = be.alloc(layers * total * H * 4)
+    for l in range(layers):
+        be.check(lib.coli_cuda_synth_activations(
+            be.ctx, C.c_void_p(xs.ptr + l * total * H * 4), total, H, C.c_ulonglong(seed), l, 0))
+    if zipf_rec is not None:
+        set_constant_feature(be, xs, layers * total, H)
+    ys = be.alloc(layers * H * 4)
+    arr = (C.c_void_p * layers)(*[L.h.value for L in stack])
+    stats0 = [L.route_stats_full() for L in stack]
+
+    def run(step):
+        be.check(lib.coli_cuda_moe_forward_layers(be.ctx, arr, layers, ys.p, C.c_void_p(xs.ptr + step * H * 4),
+                                                  1, total * H, H), "forward_layers")
+
+    for s in range(warmup):
+        run(s)
+    be.sync()
+    be.check(lib.coli_cuda_timer_start(be.ctx))
+    for s in range(warmup, total):
+        run(s)
+    ms = C.c_float()
+    be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(ms)))
+    ms_per_step = ms.value / steps
+    kb = kernel_bytes(H, E, K, I, Ish, fmt)
+    step_bytes = sum(kb)
+    if decode_kernels == 1:
+        # one persistent kernel per step: HIP events on the context stream
+        # right before and after single launches give its duration
+        durs = []
+        for s in range(warmup, warmup + min(steps, 16)):
+            be.check(lib.coli_cuda_timer_start(be.ctx))
+            run(s)
+            m1 = C.c_float()
+            be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(m1)))
+            durs.append(m1.value)
+        launch_ms = sum(durs) / len(durs)
+        kname, launch_bytes, per_launch_layers = "k_stack", layers * step_bytes, layers
+        kernel_us = {"k_stack": round(launch_ms * 1e3, 3), "per_layer": round(launch_ms * 1e3 / layers, 3)}
+    else:
+        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
+        nst = min(steps, 8)
+        for s in range(warmup, warmup + nst):
+            run(s)
+        be.sync()
+        kms = (C.c_double * 3)()
+        calls = C.c_ulonglong()
+        be.check(lib.coli_cuda_moe_decode_times(be.ctx, kms, C.byref(calls)))
+        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 0))
+        per_call = [kms[i] / max(calls.value, 1) for i in range(3)]
+        dom = max(range(3), key=lambda i: per_call[i])
+        kname, launch_bytes, per_launch_layers = KERNELS[dom], kb[dom], 1
+        launch_ms = per_call[dom]
+        kernel_us = {KERNELS[i]: round(per_call[i] * 1e3, 3) for i in range(3)}
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    stats = [L.route_stats_full() for L in stack]
+    routed = sum(b[0] - a[0] for a, b in zip(stats0, stats))
+    unc = sum(b[1] - a[1] for a, b in zip(stats0, stats))
+    full = sum(b[2] - a[2] for a, b in zip(stats0, stats))
+    return {
+        "metric": METRIC, "value": round(steps / (ms.value / 1e3), 3), "unit": "tok/s",
+        "ms_per_step": round(ms_per_step, 4), "steps": steps, "warmup": warmup,
+        "config": {"workload": desc, "hidden": H, "experts": E, "topk": K, "intermediate": I,
+                   "shared_intermediate": Ish, "expert_format": f"int{fmt}-g128", "layers": layers, "batch": 1,
+                   "seed": seed, "resident_gb": round(sum(L.nbytes() for L in stack) / 1e9, 2), "zipf": zipf_rec,
+                   "arithmetic": ARITH},
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(workload_key, kname, per_launch_layers),
+                     "bytes_per_launch": launch_bytes, "avg_launch_us": round(launch_ms * 1e3, 3)},
+        "step": {"algorithmic_bytes_per_layer": step_bytes,
+                 "effective_gbs": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9, 1),
+                 "frac_of_peak": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "kernel_us": kernel_us,
+                 "router_not_certified": f"{unc}/{routed} token-layers ({full} needed every chain)"},
+    }
+
+
+def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_key):
+    """Configs 3 and 4: T tokens per MoE step through the many-token kernels
+    (bucketing, grouped gate/up and down, combine); a prefill step is one
+    layer (the resident copies used in turn), a batched-decode step every
+    layer of the stack."""
+    H, E, K, I, Ish, fmt, _, seed, desc = cfg
+    lib = be.lib
+    nl = len(stack)
+    total = warmup + steps
     rows_per_layer = total * T
-    xs = be.alloc((nl if not prefill else 1) * rows_per_layer * H * 4)
-    for l in range(nl if not prefill else 1):
-        off = l * rows_per_layer * H * 4
-        done = 0
+    nx = 1 if prefill else nl
+    xs = be.alloc(nx * rows_per_layer * H * 4)
+    for l in range(nx):
+        off, done = l * rows_per_layer * H * 4, 0
         while done < rows_per_layer:
             n = min(65535, rows_per_layer - done)
             be.check(lib.coli_cuda_synth_activations(be.ctx, C.c_void_p(xs.ptr + off + done * H * 4), n, H,
                                                      C.c_ulonglong(seed), l, done))
             done += n
-    nrows = (nl if not prefill else 1) * rows_per_layer
-    xh = np.empty((nrows, H), np.float32)
+    xh = np.empty((nx * rows_per_layer, H), np.float32)
     be.check(lib.coli_cuda_download(be.ctx, xh.ctypes.data_as(C.c_void_p), xs.p, xh.nbytes), "download")
     be.sync()
     if prefill:  # bf16-valued activations (round to nearest even), passed as f32
         u = xh.view(np.uint32)
         u += 0x7FFF + ((u >> 16) & 1)
         u &= 0xFFFF0000
-    if use_zipf:
+    if zipf_rec is not None:
         xh[:, H - 1] = 1.0
     be.check(lib.coli_cuda_upload(be.ctx, xs.p, xh.ctypes.data_as(C.c_void_p), xh.nbytes), "upload")
     be.sync()
-    ys = be.alloc((nl if not prefill else 1) * T * H * 4)
+    ys = be.alloc(nx * T * H * 4)
     arr = (C.c_void_p * nl)(*[L.h.value for L in stack])
 
     def x_at(l, step):
@@ -305,40 +459,35 @@ def bench_many(args):
 
     def run(step):
         if prefill:
-            L = stack[step % nl]
-            be.check(lib.coli_cuda_moe_forward(be.ctx, L.h, ys.p, x_at(0, step), T, None, None), "forward")
+            be.check(lib.coli_cuda_moe_forward(be.ctx, stack[step % nl].h, ys.p, x_at(0, step), T, None, None),
+                     "forward")
         else:
-            be.check(lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, ys.p, x_at(0, step), T,
-                                                      rows_per_layer * H, T * H), "forward_layers")
+            be.check(lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, ys.p, x_at(0, step), T, rows_per_layer * H,
+                                                      T * H), "forward_layers")
 
-    for s in range(args.warmup):
+    for s in range(warmup):
         run(s)
     be.sync()
     be.check(lib.coli_cuda_timer_start(be.ctx))
-    for s in range(args.warmup, total):
+    for s in range(warmup, total):
         run(s)
     ms = C.c_float()
     be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(ms)))
-    ms_per_step = ms.value / args.steps
+    ms_per_step = ms.value / steps
     layers_per_step = 1 if prefill else nl
-    tok_s = T / (ms_per_step * 1e-3)
-
     # routing of the timed steps (untimed): distinct experts per layer-step
     di, dw = be.alloc(T * K * 4), be.alloc(T * K * 4)
     uniq = []
-    for s in range(args.warmup, total):
+    for s in range(warmup, total):
         for l in ([s % nl] if prefill else range(nl)):
             be.check(lib.coli_cuda_moe_route(be.ctx, stack[l].h, x_at(l, s), T, di.p, dw.p), "route")
-            idx = be.download(di, (T, K), np.int32)
-            uniq.append(len(np.unique(idx)))
+            uniq.append(len(np.unique(be.download(di, (T, K), np.int32))))
     U = float(np.mean(uniq))
     names, nbytes, flops = stage_model(H, E, K, I, Ish, fmt, T, U)
-    layer_bytes = sum(nbytes)
-    layer_flops = sum(flops)
-
+    layer_bytes, layer_flops = sum(nbytes), sum(flops)
     # per-stage device times (HIP events between the step's kernels)
     be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
-    for s in range(args.warmup, args.warmup + min(args.steps, 4)):
+    for s in range(warmup, warmup + min(steps, 4)):
         run(s)
     be.sync()
     sms = (C.c_double * 8)()
@@ -354,75 +503,64 @@ def bench_many(args):
         per = None
         kname, dom_bytes, dom_ms = "k_stack", layer_bytes * layers_per_step, ms_per_step
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 3),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {
-            "workload": desc,
-            "hidden": H, "experts": E, "topk": K, "intermediate": I, "shared_intermediate": Ish,
-            "expert_format": f"int{fmt}-g128", "layers_per_step": layers_per_step, "tokens_per_step": T,
-            "resident_layers": nl, "seed": seed, "resident_gb": round(resident / 1e9, 2),
-            "zipf": zipf_rec,
-            "arithmetic": "int3/int4 codes x two int8 activation digits on MFMA, fp32 group scaling; "
-                          "int8 IDOT shared expert; fp64-certified exact fp32 router",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": kname,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "bytes_per_launch": int(dom_bytes),
-            "avg_launch_us": round(dom_ms * 1e3, 3),
-        },
-        "mfma": {
-            "flops_per_layer": int(layer_flops),
-            "achieved_tflops": round(layer_flops * layers_per_step / step_s / 1e12, 3),
-            "frac_bf16_peak": round(layer_flops * layers_per_step / step_s / 1e12 / BF16_PEAK_TFLOPS, 5),
-            "int8_ops_issued_per_layer": int(2 * (flops[2] + flops[3] + flops[5])),
-            "frac_int8_peak": round(2 * (flops[2] + flops[3] + flops[5]) * layers_per_step / step_s / 1e12
-                                    / INT8_PEAK_TOPS, 5),
-        },
-        "step": {
-            "distinct_experts_per_layer": round(U, 2),
-            "algorithmic_bytes_per_layer": int(layer_bytes),
-            "effective_gbs": round(layer_bytes * layers_per_step / step_s / 1e9, 1),
-            "frac_of_peak": round(layer_bytes * layers_per_step / step_s / 1e9 / HBM_PEAK_GBS, 4),
-            "stage_us": {names[i]: round(per[i] * 1e3, 2) for i in range(7)} if per else None,
-            "stage_gbs": ({names[i]: round(nbytes[i] / (per[i] * 1e-3) / 1e9, 1) for i in range(7)
-                           if nbytes[i] and per[i] > 0} if per else None),
-            "weight_generation_s": round(gen_s, 1),
-        },
+    return {
+        "value": round(T / step_s, 3), "unit": "tok/s", "ms_per_step": round(ms_per_step, 4), "steps": steps,
+        "config": {"workload": desc, "tokens_per_step": T, "layers_per_step": layers_per_step,
+                   "resident_layers": nl, "zipf": zipf_rec},
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(workload_key, kname.replace("stage ", ""), 1),
+                     "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_ms * 1e3, 3)},
+        "mfma": {"flops_per_layer": int(layer_flops),
+                 "achieved_tflops": round(layer_flops * layers_per_step / step_s / 1e12, 3),
+                 "frac_bf16_peak": round(layer_flops * layers_per_step / step_s / 1e12 / BF16_PEAK_TFLOPS, 5),
+                 "int8_ops_issued_per_layer": int(2 * (flops[2] + flops[3] + flops[5])),
+                 "frac_int8_peak": round(2 * (flops[2] + flops[3] + flops[5]) * layers_per_step / step_s / 1e12
+                                         / INT8_PEAK_TOPS, 5)},
+        "step": {"distinct_experts_per_layer": round(U, 2), "algorithmic_bytes_per_layer": int(layer_bytes),
+                 "effective_gbs": round(layer_bytes * layers_per_step / step_s / 1e9, 1),
+                 "frac_of_peak": round(layer_bytes * layers_per_step / step_s / 1e9 / HBM_PEAK_GBS, 4),
+                 "stage_us": {names[i]: round(per[i] * 1e3, 2) for i in range(7)} if per else None,
+                 "stage_gbs": ({names[i]: round(nbytes[i] / (per[i] * 1e-3) / 1e9, 1) for i in range(7)
+                                if nbytes[i] and per[i] > 0} if per else None)},
     }
+
+
+def progress(msg):
+    """A progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def with_cpu(result, args, fn):
     if not args.no_cpu:
         try:
-            result["cpu_baseline"] = cpu_baseline_many(cfg if prefill else (H, E, K, I, Ish, fmt, nl, seed, desc),
-                                                       T, zipf_rec, args.cpu_seconds)
+            result["cpu_baseline"] = fn()
         except Exception as e:  # the CPU leg never hides the GPU number
             result["cpu_baseline"] = {"value": None, "error": str(e)}
-    print(json.dumps(result), flush=True)
+    return result
+
+
+def headline(result, args, n_gpus=1):
+    """The driver's fields around a config-2 decode result."""
+    out = {"metric": METRIC, "value": result["value"], "unit": "tok/s", "n_gpus": n_gpus, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": result["ms_per_step"], "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic"}
+    for k in ("config", "roofline", "step", "cpu_baseline"):
+        if k in result:
+            out[k] = result[k]
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
-    ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--workload", default="s397", choices=sorted(WORKLOADS) + sorted(MANY))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS) + sorted(MANY),
+                    help="all (default): config 2 is the headline; configs 1, 3 (B = 1..32) and 4 are timed in "
+                         "the same run and reported under 'configs'")
     ap.add_argument("--batch", type=int, default=8, help="tokens per step of --workload s397-batch")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (testing)")
     ap.add_argument("--decode-kernels", type=int, default=1, choices=[1, 2],
@@ -438,141 +576,93 @@ def main():
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return
-    if args.workload in MANY:
-        bench_many(args)
-        return
-
-    from shiftwing_amd import Backend, MoeLayer
-    H, E, K, I, Ish, fmt, layers, seed, desc = WORKLOADS[args.workload]
-    if args.layers:
-        layers = args.layers
+    from shiftwing_amd import Backend
     be = Backend(0)
     be.set_decode_kernels(args.decode_kernels)
-    lib = be.lib
     t0 = time.perf_counter()
-    stack = []
-    for l in range(layers):
-        L = MoeLayer(be, H, E, K, I, Ish, fmt)
-        L.synthesize(seed, l)
-        stack.append(L)
-    be.sync()
-    zipf_rec = apply_zipf(be, stack, WORKLOADS[args.workload]) if args.workload in ZIPF_DECODE else None
+
+    def cfg_of(name, layers=None):
+        H, E, K, I, Ish, fmt, nl, seed, desc = WORKLOADS[name]
+        return (H, E, K, I, Ish, fmt, layers or args.layers or nl, seed, desc)
+
+    if args.workload in MANY:
+        base, nl, T, use_zipf, desc = MANY[args.workload]
+        nl = args.layers or nl
+        T = T or args.batch
+        prefill = args.workload.startswith("prefill")
+        stack = build_stack(be, base, nl)
+        cfg = cfg_of(base, nl)[:8] + (desc,)
+        zipf_rec = apply_zipf(be, stack, cfg) if use_zipf else None
+        r = measure_many(be, stack, cfg, T, prefill, args.steps, args.warmup, zipf_rec, args.workload)
+        r = with_cpu(r, args, lambda: cpu_baseline_many(cfg, T, zipf_rec, args.cpu_seconds, 1 if prefill else nl))
+        print(json.dumps({"metric": METRIC, "n_gpus": 1, "warmup": args.warmup, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic", **r}),
+              flush=True)
+        return
+    if args.workload == "s35":
+        cfg = cfg_of("s35")
+        stack = build_stack(be, "s35", cfg[6])
+        zipf_rec = apply_zipf(be, stack, cfg)
+        r = measure_decode(be, stack, cfg, args.steps, args.warmup, zipf_rec, "s35", args.decode_kernels)
+        r = with_cpu(r, args, lambda: cpu_baseline(cfg, args.cpu_seconds, zipf_rec))
+        print(json.dumps(headline(r, args)), flush=True)
+        return
+
+    # config 2, the headline: the S397 int3 stack, batch-1 decode, uniform routing
+    cfg2 = cfg_of("s397")
+    s397 = build_stack(be, "s397", cfg2[6])
     gen_s = time.perf_counter() - t0
-    resident = sum(L.nbytes() for L in stack)
-    total_steps = args.warmup + args.steps
-    xs = be.alloc(layers * total_steps * H * 4)
-    for l in range(layers):
-        be.check(lib.coli_cuda_synth_activations(
-            be.ctx, C.c_void_p(xs.ptr + l * total_steps * H * 4), total_steps, H, C.c_ulonglong(seed), l, 0))
-    if zipf_rec is not None:
-        set_constant_feature(be, xs, layers * total_steps, H)
-    ys = be.alloc(layers * H * 4)
-    arr = (C.c_void_p * layers)(*[L.h.value for L in stack])
-
-    def run(step):
-        be.check(lib.coli_cuda_moe_forward_layers(be.ctx, arr, layers, ys.p, C.c_void_p(xs.ptr + step * H * 4),
-                                                  1, total_steps * H, H), "forward_layers")
-
-    for s in range(args.warmup):
-        run(s)
-    be.sync()
-    be.check(lib.coli_cuda_timer_start(be.ctx))
-    for s in range(args.warmup, total_steps):
-        run(s)
-    ms = C.c_float()
-    be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(ms)))
-    total_ms = ms.value
-    ms_per_step = total_ms / args.steps
-    tok_s = args.steps / (total_ms / 1e3)
-
-    kb = kernel_bytes(H, E, K, I, Ish, fmt)
-    step_bytes = sum(kb)
-    if args.decode_kernels == 1:
-        # one persistent kernel per step: HIP events on the context stream
-        # right before and after single launches give its duration
-        durs = []
-        for s in range(args.warmup, args.warmup + min(args.steps, 16)):
-            be.check(lib.coli_cuda_timer_start(be.ctx))
-            run(s)
-            m1 = C.c_float()
-            be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(m1)))
-            durs.append(m1.value)
-        launch_ms = sum(durs) / len(durs)
-        kname, launch_bytes, layers_per_launch = "k_stack", layers * step_bytes, layers
-        kernel_us = {"k_stack": round(launch_ms * 1e3, 3), "per_layer": round(launch_ms * 1e3 / layers, 3)}
-        kernel_gbs = {"k_stack": round(launch_bytes / (launch_ms * 1e-3) / 1e9, 1)}
-    else:
-        # per-kernel timing pass: HIP events on the context stream around each
-        # of the three decode kernels (the kernels' own stream)
-        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 1))
-        nst = min(args.steps, 8)
-        for s in range(args.warmup, args.warmup + nst):
-            run(s)
-        be.sync()
-        kms = (C.c_double * 3)()
-        calls = C.c_ulonglong()
-        be.check(lib.coli_cuda_moe_decode_times(be.ctx, kms, C.byref(calls)))
-        be.check(lib.coli_cuda_moe_stage_timing(be.ctx, 0))
-        per_call = [kms[i] / max(calls.value, 1) for i in range(3)]
-        dom = max(range(3), key=lambda i: per_call[i])
-        kname, launch_bytes, layers_per_launch = KERNELS[dom], kb[dom], 1
-        launch_ms = per_call[dom]
-        kernel_us = {KERNELS[i]: round(per_call[i] * 1e3, 3) for i in range(3)}
-        kernel_gbs = {KERNELS[i]: round(kb[i] / (per_call[i] * 1e-3) / 1e9, 1) for i in range(3)}
-    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    stats = [L.route_stats_full() for L in stack]
-    tokens_routed = sum(t for t, _, _ in stats)
-    fallbacks = sum(f for _, f, _ in stats)
-    full = sum(u for _, _, u in stats)
-
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 3),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {
-            "workload": desc,
-            "hidden": H, "experts": E, "topk": K, "intermediate": I, "shared_intermediate": Ish,
-            "expert_format": f"int{fmt}-g128", "layers": layers, "batch": 1, "seed": seed,
-            "resident_gb": round(resident / 1e9, 2), "zipf": zipf_rec,
-            "arithmetic": "int3/int4 codes x two int8 activation digits on MFMA, fp32 group scaling; "
-                          "int8 IDOT shared expert; fp64-certified exact fp32 router",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": kname,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.workload, kname, layers_per_launch),
-            "bytes_per_launch": launch_bytes,
-            "avg_launch_us": round(launch_ms * 1e3, 3),
-        },
-        "step": {
-            "algorithmic_bytes_per_layer": step_bytes,
-            "effective_gbs": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9, 1),
-            "frac_of_peak": round(step_bytes * layers / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel_us": kernel_us,
-            "kernel_gbs": kernel_gbs,
-            "router_not_certified": f"{fallbacks}/{tokens_routed} token-layers ({full} needed every chain)",
-            "weight_generation_s": round(gen_s, 1),
-        },
-    }
-    if not args.no_cpu:
-        try:
-            result["cpu_baseline"] = cpu_baseline(WORKLOADS[args.workload], args.cpu_seconds)
-        except Exception as e:  # the CPU leg never hides the GPU number
-            result["cpu_baseline"] = {"value": None, "error": str(e)}
-    print(json.dumps(result), flush=True)
+    progress(f"S397 stack resident in {gen_s:.1f} s")
+    r2 = measure_decode(be, s397, cfg2, args.steps, args.warmup, None, "s397", args.decode_kernels)
+    progress(f"config 2 decode: {r2['value']} tok/s")
+    r2["step"]["weight_generation_s"] = round(gen_s, 1)
+    r2 = with_cpu(r2, args, lambda: cpu_baseline(cfg2, args.cpu_seconds))
+    progress("config 2 CPU baseline done")
+    line = headline(r2, args)
+    if args.workload == "s397":
+        print(json.dumps(line), flush=True)
+        return
+    configs = {}
+    # config 4, S397: one 512-token prefill chunk through one layer (4 resident
+    # copies used in turn), uniform routing
+    d4 = MANY["prefill-s397"][4]
+    c4 = cfg2[:8] + (d4,)
+    p397 = measure_many(be, s397[:4], c4, 512, True, 8, 2, None, "prefill-s397")
+    progress(f"config 4 S397 prefill: {p397['value']} tok/s")
+    p397 = with_cpu(p397, args, lambda: cpu_baseline_many(c4, 512, None, args.cpu_seconds / 2, 1))
+    # config 3: continuous-batch decode on the same stack with Zipf routing
+    zipf397 = apply_zipf(be, s397, cfg2)
+    d3 = MANY["s397-batch"][4]
+    c3 = cfg2[:8] + (d3,)
+    batch = {}
+    for B in (1, 4, 8, 16, 32):
+        rb = measure_many(be, s397, c3, B, False, 6, 2, zipf397, "s397-batch")
+        if B in (4, 32):
+            rb = with_cpu(rb, args, lambda: cpu_baseline_many(c3, B, zipf397, args.cpu_seconds / 2, len(s397)))
+        batch[f"B{B}"] = rb
+        progress(f"config 3 B={B}: {rb['value']} tok/s")
+    configs["config3"] = batch
+    for L in s397:
+        L.close()
+    del s397
+    # the S35 stack: config 4 (S35 prefill, uniform routing), then config 1
+    # (40-layer batch-1 decode with Zipf routing)
+    cfg1 = cfg_of("s35")
+    s35 = build_stack(be, "s35", cfg1[6])
+    d4s = MANY["prefill-s35"][4]
+    c4s = cfg1[:8] + (d4s,)
+    p35 = measure_many(be, s35[:4], c4s, 512, True, 8, 2, None, "prefill-s35")
+    progress(f"config 4 S35 prefill: {p35['value']} tok/s")
+    p35 = with_cpu(p35, args, lambda: cpu_baseline_many(c4s, 512, None, args.cpu_seconds / 2, 1))
+    configs["config4"] = {"s35": p35, "s397": p397}
+    zipf35 = apply_zipf(be, s35, cfg1)
+    r1 = measure_decode(be, s35, cfg1, args.steps, args.warmup, zipf35, "s35", args.decode_kernels)
+    progress(f"config 1 decode: {r1['value']} tok/s")
+    r1 = with_cpu(r1, args, lambda: cpu_baseline(cfg1, args.cpu_seconds, zipf35))
+    configs["config1"] = r1
+    line["configs"] = configs
+    line["wall_s"] = round(time.perf_counter() - t0, 1)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":
