@@ -473,6 +473,15 @@ int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode);
  * trace = NULL, words = 0 switches it off. */
 int coli_cuda_moe_stack_trace(ColiCuda *ctx, unsigned long long *trace,
                               size_t words);
+/* Fault drill of the persistent decode kernel (no counterpart in the
+ * reference; for tests of its timeout path).  The next launch keeps its last
+ * `absent_workgroups` workgroups out, as if they never became resident, and
+ * gives each wait `wait_limit_us` (1..2,000,000) instead of 2 s: every other
+ * workgroup times out, raises the abort word and leaves, and the next
+ * coli_cuda_sync returns -1 with the abort message after clearing the
+ * kernel's device state.  0 absent workgroups disarms; a launch disarms. */
+int coli_cuda_moe_stack_drill(ColiCuda *ctx, int absent_workgroups,
+                              int wait_limit_us);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "liboracle.so")
+# SHIFTWING_ORACLE_LIB names another build of the checker (the sanitizer build)
+ORACLE_SO = os.environ.get("SHIFTWING_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
 f32p = C.POINTER(C.c_float)

@@ -13,7 +13,9 @@ import re
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HEADER = os.path.join(ROOT, "include", "shiftwing_moe.h")
-LIB_PATH = os.path.join(HERE, "libshiftwing_moe.so")
+# SHIFTWING_MOE_LIB names another build of the same library (the host-only
+# sanitizer build that the CPU tests load)
+LIB_PATH = os.environ.get("SHIFTWING_MOE_LIB") or os.path.join(HERE, "libshiftwing_moe.so")
 
 
 class ColiMoeShape(C.Structure):

@@ -125,6 +125,7 @@ struct StackArgs {
   unsigned *abort_word; // device
   unsigned *abort_host; // host-mapped status
   long long spin_ticks; // wall-clock budget of one wait (100 MHz ticks)
+  int absent;           // fault drill: the last `absent` workgroups stay out (0 otherwise)
   unsigned long long *trace;  // optional stage stamps [layer][NB][kStamps]
   size_t trace_words;
 };
@@ -763,6 +764,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
+  // Fault drill: these workgroups leave before taking any part, as if they
+  // never became resident.  Every other one then meets a wait that cannot be
+  // met (their router records, at the latest) and leaves through the abort word.
+  if (b >= a0.NB - a0.absent) return;
 
   // The call state, read by every workgroup before any of them can pass the
   // first grid barrier (workgroup 0 advances it after the last one).
@@ -2094,6 +2099,11 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.abort_word = (unsigned *)ctx->stack_abort;
   a.abort_host = ctx->stack_abort_host_dev;
   a.spin_ticks = 200000000LL;  // 2 s of the 100 MHz wall clock
+  a.absent = 0;
+  if (ctx->stack_drill_absent) {  // coli_cuda_moe_stack_drill: disarmed at the launch
+    a.absent = ctx->stack_drill_absent;
+    a.spin_ticks = ctx->stack_drill_ticks;
+  }
   a.trace = (unsigned long long *)ctx->stack_trace;
   a.trace_words = ctx->stack_trace_words;
   if (!a.trace) {
@@ -2113,6 +2123,22 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   if (lds < one_per_cu) lds = one_per_cu;
   if (lds + 1024 > (size_t)ctx->shared_per_block) return 1;
   hipError_t e;
+  {
+    // every workgroup must be resident at once, one per compute unit: a
+    // compute unit must hold one with this LDS (registers and waves
+    // included), else the shape takes the three-kernel path
+    size_t &fit = ctx->stack_fit_lds[a.fmt == 4];
+    if (fit != lds) {
+      int per_cu = 0;
+      const void *fn = a.fmt == 4 ? (const void *)k_stack<4> : (const void *)k_stack<3>;
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kT, lds);
+      if (e != hipSuccess) return fail_hip("MoE stack occupancy query", e);
+      if (per_cu < 1) return 1;
+      fit = lds;
+    }
+  }
+  ctx->stack_drill_absent = 0;
   if (a.fmt == 4) {
     e = hipFuncSetAttribute((const void *)k_stack<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e == hipSuccess) k_stack<4><<<a.NB, kT, lds, ctx->stream>>>(a);
@@ -2146,5 +2172,17 @@ extern "C" int coli_cuda_moe_stack_trace(ColiCuda *ctx, unsigned long long *trac
   if (!ctx || (words && !trace)) return sw::fail_arg("coli_cuda_moe_stack_trace: invalid argument");
   ctx->stack_trace = trace;
   ctx->stack_trace_words = trace ? words : 0;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_stack_drill(ColiCuda *ctx, int absent_workgroups, int wait_limit_us) {
+  if (!ctx) return sw::fail_arg("coli_cuda_moe_stack_drill: null context");
+  if (absent_workgroups < 0 || absent_workgroups >= ctx->sm_count)
+    return sw::fail_arg("coli_cuda_moe_stack_drill: %d absent workgroups (0 disarms, at most %d)", absent_workgroups,
+                        ctx->sm_count - 1);
+  if (absent_workgroups && (wait_limit_us < 1 || wait_limit_us > 2000000))
+    return sw::fail_arg("coli_cuda_moe_stack_drill: wait limit %d us outside [1, 2000000]", wait_limit_us);
+  ctx->stack_drill_absent = absent_workgroups;
+  ctx->stack_drill_ticks = 100LL * wait_limit_us;  // 100 MHz wall clock
   return 0;
 }

@@ -116,6 +116,13 @@ struct ColiCuda {
   unsigned *stack_abort_host = nullptr, *stack_abort_host_dev = nullptr;
   unsigned long long *stack_trace = nullptr;  // optional stage stamps (coli_cuda_moe_stack_trace)
   size_t stack_trace_words = 0;
+  // dynamic LDS bytes per format (index 0: int3, 1: int4) at which a compute
+  // unit was last found to hold one workgroup of the kernel (0: not checked)
+  size_t stack_fit_lds[2] = {0, 0};
+  // fault drill (coli_cuda_moe_stack_drill), armed until the next launch:
+  // workgroups kept out, wait limit in 100 MHz ticks
+  int stack_drill_absent = 0;
+  long long stack_drill_ticks = 0;
   // device address of the fixed scratch of coli_cuda_idot_q8_gemm_noalloc
   void *noalloc_scratch = nullptr;
 };

@@ -120,3 +120,68 @@ def test_container_errors(tmp_path, layers):
     rc, _ = _shape(lib, c3, 0, 1)
     assert rc == -1 and ".q3" in lib.coli_cuda_last_error().decode()
     lib.coli_cuda_container_close(c3)
+
+
+def _pick(rng, values):
+    return values[int(rng.integers(0, len(values)))]
+
+
+def _corrupt(raw: bytes, rng) -> bytes:
+    """One damaged copy of a container file: truncated, a header byte
+    changed, the header length changed, or a number in the header changed."""
+    hlen = int.from_bytes(raw[:8], "little")
+    kind = int(rng.integers(0, 4))
+    if kind == 0:
+        return raw[:int(rng.integers(0, len(raw)))]
+    if kind == 1:
+        b = bytearray(raw)
+        for _ in range(int(rng.integers(1, 4))):
+            b[8 + int(rng.integers(0, hlen))] = int(rng.choice(list(b'{}[]":,0123456789-e. \x00\xff')))
+        return bytes(b)
+    if kind == 2:
+        n = _pick(rng, [0, 1, hlen - 1, hlen + 1, len(raw) - 8, len(raw), 2**31, 2**63 - 1, 2**64 - 1])
+        return n.to_bytes(8, "little") + raw[8:]
+    head = raw[8:8 + hlen].decode()
+    digits = [i for i, ch in enumerate(head) if ch.isdigit()]
+    i = int(rng.choice(digits))
+    j = i
+    while j < len(head) and head[j].isdigit():
+        j += 1
+    new = str(_pick(rng, [0, 1, 7, 2**31 - 1, 2**31, 2**32 + 3, 2**62, 10**30, -1]))
+    head = head[:i] + new + head[j:]
+    h = head.encode()
+    return len(h).to_bytes(8, "little") + h + raw[8 + hlen:]
+
+
+def test_container_survives_corrupt_files(tmp_path, layers):
+    """Damaged files open with an error or, where the damage is harmless, load
+    their shapes; nothing reads outside what the file holds (the sanitizer
+    run of this test makes an out-of-bounds read fail it)."""
+    hl4, hl3 = layers
+    lib = _lib()
+    src = tmp_path / "src"
+    src.mkdir()
+    st_writer.write(str(src / "m.safetensors"), st_writer.moe_layer_tensors(hl4, 0, q3=hl3))
+    raw = open(src / "m.safetensors", "rb").read()
+    rng = np.random.default_rng(23)
+    opened = failed = 0
+    for k in range(240):
+        d = tmp_path / f"c{k}"
+        d.mkdir()
+        with open(d / "m.safetensors", "wb") as f:
+            f.write(_corrupt(raw, rng))
+        rc, c = _open(lib, str(d))
+        if rc != 0:
+            assert rc == -1 and lib.coli_cuda_last_error(), k
+            failed += 1
+            continue
+        opened += 1
+        assert lib.coli_cuda_container_tensors(c) >= 0
+        for use_q3 in (0, 1):
+            rc, s = _shape(lib, c, 0, use_q3)
+            assert rc in (0, -1), k
+            if rc == 0:
+                assert s.hidden > 0 and s.experts > 0 and s.expert_format in (2, 3, 4), k
+        lib.coli_cuda_container_close(c)
+        os.remove(d / "m.safetensors")
+    assert failed > 0 and opened > 0, (failed, opened)
