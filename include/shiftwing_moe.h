@@ -326,8 +326,12 @@ typedef struct {
 } ColiMoeShape;
 
 /* Allocate an HBM-resident layer (all experts).  Requires hidden % 64 == 0,
- * intermediate % 16 == 0, shared_intermediate % 64 == 0, group_size 128,
- * expert_format 3 or 4, topk <= 32 and experts <= 4096. */
+ * group_size 128, expert_format 3 or 4, topk <= 32 and experts <= 4096.
+ * Any intermediate and shared_intermediate: a ragged one is held rounded up
+ * to the row tiles (16 and 64 rows) with zero rows, which add exact zeros
+ * (the reference's tail groups, c/qwen.c:1706-1754, as in
+ * c/tests/test_quant_matmul.c:12-93); the set_* calls take the caller's
+ * shape. */
 int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out,
                                const ColiMoeShape *shape);
 void coli_cuda_moe_layer_destroy(ColiCuda *ctx, ColiMoeLayer *layer);

@@ -71,8 +71,9 @@ __device__ inline int container_code(const unsigned char *row, int k, int cols, 
 
 // one thread per (row tile, group, lane): container codes -> tile bytes of
 // the tile-group's record (record stride rs)
-__global__ void k_repack_codes(unsigned char *dst, unsigned rs, const unsigned char *src, int rows, int cols, int rb,
-                               int ng, int fmt) {
+// (rows past rows_src, the tile padding of a ragged I, get zero values)
+__global__ void k_repack_codes(unsigned char *dst, unsigned rs, const unsigned char *src, int rows, int rows_src,
+                               int cols, int rb, int ng, int fmt) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   long long total = (long long)(rows / kTileRows) * ng * 64;
   if (tid >= total) return;
@@ -81,10 +82,11 @@ __global__ void k_repack_codes(unsigned char *dst, unsigned rs, const unsigned c
   int g = (int)(tg % ng);
   int rt = (int)(tg / ng);
   int r = rt * kTileRows + (lane & 15), kb = lane >> 4;
-  const unsigned char *row = src + (size_t)r * rb;
+  const bool live = r < rows_src;
+  const unsigned char *row = src + (size_t)(live ? r : 0) * rb;
   int code[32];
 #pragma unroll
-  for (int s = 0; s < 32; s++) code[s] = container_code(row, g * kGroup + slot_k(s, kb), cols, fmt);
+  for (int s = 0; s < 32; s++) code[s] = container_code(row, g * kGroup + slot_k(s, kb), live ? cols : 0, fmt);
   if (fmt == 4) {
     uint32_t w[4];
 #pragma unroll
@@ -117,7 +119,8 @@ __global__ void k_repack_codes(unsigned char *dst, unsigned rs, const unsigned c
 }
 
 // scales [rows][ng] -> 16 per tile-group record, at byte so of the record
-__global__ void k_repack_scales(unsigned char *dst, unsigned rs, unsigned so, const float *src, int rows, int ng) {
+__global__ void k_repack_scales(unsigned char *dst, unsigned rs, unsigned so, const float *src, int rows,
+                                int rows_src, int ng) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   long long total = (long long)rows * ng;
   if (tid >= total) return;
@@ -125,7 +128,8 @@ __global__ void k_repack_scales(unsigned char *dst, unsigned rs, unsigned so, co
   long long tg = tid >> 4;
   int g = (int)(tg % ng);
   int rt = (int)(tg / ng);
-  ((float *)(dst + (size_t)tg * rs + so))[r] = src[(size_t)(rt * kTileRows + r) * ng + g];
+  const int row = rt * kTileRows + r;
+  ((float *)(dst + (size_t)tg * rs + so))[r] = row < rows_src ? src[(size_t)row * ng + g] : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -146,20 +150,30 @@ __global__ void k_synth_i8(signed char *dst, size_t n, uint64_t key) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = sw_i8(key, i);
 }
+// a [rows x cols] matrix generated as if contiguous, stored with row pitch `pitch`
+__global__ void k_synth_i8_rows(signed char *dst, int rows, int cols, int pitch, uint64_t key) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * cols) return;
+  const size_t r = i / (size_t)cols, c = i - r * (size_t)cols;
+  dst[r * (size_t)pitch + c] = sw_i8(key, i);
+}
 __global__ void k_synth_normal(float *dst, size_t n, uint64_t key, float sigma, int absolute) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   dst[i] = absolute ? sw_abs_normal_sigma(key, i, sigma) : sw_normal_sigma(key, i, sigma);
 }
 // tile-group scales straight from the hash at their container index
-__global__ void k_synth_scales_tiled(unsigned char *dst, unsigned rs, unsigned so, int rows, int ng, uint64_t key) {
+__global__ void k_synth_scales_tiled(unsigned char *dst, unsigned rs, unsigned so, int rows, int rows_src, int ng,
+                                     uint64_t key) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (tid >= (long long)rows * ng) return;
   int r = (int)(tid & 15);
   long long tg = tid >> 4;
   int g = (int)(tg % ng);
   int rt = (int)(tg / ng);
-  ((float *)(dst + (size_t)tg * rs + so))[r] = sw_abs_normal_sigma(key, (uint64_t)(rt * kTileRows + r) * ng + g, 0.01f);
+  const int row = rt * kTileRows + r;
+  ((float *)(dst + (size_t)tg * rs + so))[r] =
+      row < rows_src ? sw_abs_normal_sigma(key, (uint64_t)row * ng + g, 0.01f) : 0.0f;
 }
 
 inline unsigned blocks_for(size_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -1496,15 +1510,23 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   if (!ctx || !out || !s) return fail_arg("coli_cuda_moe_layer_create: null argument");
   *out = nullptr;
   if (s->hidden <= 0 || s->experts <= 0 || s->topk <= 0 || s->intermediate <= 0 ||
-      s->shared_intermediate <= 0 || s->hidden % 64 || s->intermediate % 16 || s->shared_intermediate % 64 ||
-      s->topk > kMaxTopK || s->topk > s->experts || s->experts > 4096 || s->group_size != kGroup ||
-      (s->expert_format != 3 && s->expert_format != 4))
-    return fail_arg("coli_cuda_moe_layer_create: unsupported shape (H%%64, I%%16, I_sh%%64, "
-                    "group_size 128, format 3|4, topk<=32, experts<=4096)");
+      s->shared_intermediate <= 0 || s->hidden % 64 || s->topk > kMaxTopK || s->topk > s->experts ||
+      s->experts > 4096 || s->group_size != kGroup || (s->expert_format != 3 && s->expert_format != 4))
+    return fail_arg("coli_cuda_moe_layer_create: unsupported shape (H%%64, group_size 128, format 3|4, "
+                    "topk<=32, experts<=4096)");
   ColiMoeLayer *L = (ColiMoeLayer *)calloc(1, sizeof(ColiMoeLayer));
   if (!L) return fail_arg("out of memory creating MoE layer");
+  // A ragged I or shared I is held as the next multiple of the row tiles:
+  // the extra rows have zero codes and scales, so they add exact zeros (the
+  // hidden values there are silu(0)*0 = 0, and the down columns they meet
+  // hold zero values).
   L->sh = *s;
-  int H = s->hidden, I = s->intermediate, E = s->experts, Ish = s->shared_intermediate;
+  L->I_src = s->intermediate;
+  L->Ish_src = s->shared_intermediate;
+  L->sh.intermediate = (s->intermediate + kTileRows - 1) / kTileRows * kTileRows;
+  L->sh.shared_intermediate = (s->shared_intermediate + 63) / 64 * 64;
+  const bool ragged = L->sh.intermediate != L->I_src || L->sh.shared_intermediate != L->Ish_src;
+  int H = s->hidden, I = L->sh.intermediate, E = s->experts, Ish = L->sh.shared_intermediate;
   L->ngh = (H + kGroup - 1) / kGroup;
   L->ngi = (I + kGroup - 1) / kGroup;
   L->xl = expert_layout(nullptr, H, I, s->expert_format);
@@ -1518,7 +1540,7 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
            layer_alloc(L, (void **)&L->sh_ds, (size_t)H * 4, "shared scale allocation") ||
            layer_alloc(L, (void **)&L->experts, (size_t)E * L->xl.expert_bytes, "expert allocation") ||
            layer_alloc(L, (void **)&L->stats, 64, "router stats allocation");
-  L->sync_words = decode_sync_words(*s);
+  L->sync_words = decode_sync_words(L->sh);
   rc = rc || layer_alloc(L, (void **)&L->sync, L->sync_words * 4, "decode counter allocation");
   if (rc) {
     coli_cuda_moe_layer_destroy(ctx, L);
@@ -1527,6 +1549,13 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   L->xl.base = L->experts;
   k_zero_u32<<<blocks_for(16, 256), 256, 0, ctx->stream>>>((unsigned *)L->stats, 16);
   k_zero_u32<<<blocks_for(L->sync_words, 256), 256, 0, ctx->stream>>>(L->sync, L->sync_words);
+  if (ragged) {  // the padding rows and columns start (and stay) zero
+    const struct { void *p; size_t n; } z[] = {
+        {L->sh_gq, (size_t)Ish * H}, {L->sh_uq, (size_t)Ish * H}, {L->sh_dq, (size_t)H * Ish},
+        {L->sh_gs, (size_t)Ish * 4}, {L->sh_us, (size_t)Ish * 4}, {L->experts, (size_t)E * L->xl.expert_bytes}};
+    for (const auto &r : z)
+      k_zero_u32<<<blocks_for(r.n / 4, 256), 256, 0, ctx->stream>>>((unsigned *)r.p, r.n / 4);
+  }
   *out = L;
   return launch_status("coli_cuda_moe_layer_create");
 }
@@ -1562,26 +1591,31 @@ extern "C" int coli_cuda_moe_layer_set_shared_q8(ColiCuda *ctx, ColiMoeLayer *L,
                                                  const signed char *dq, const float *ds) {
   if (!ctx || !L || !gq || !gs || !uq || !us || !dq || !ds)
     return fail_arg("coli_cuda_moe_layer_set_shared_q8: null argument");
-  size_t H = L->sh.hidden, I = L->sh.shared_intermediate;
+  // the caller's I rows; the down rows land at the device pitch (I rounded up)
+  size_t H = L->sh.hidden, I = L->Ish_src, Ip = L->sh.shared_intermediate;
   hipStream_t st = ctx->stream;
-  hipMemcpyAsync(L->sh_gq, gq, I * H, hipMemcpyDeviceToDevice, st);
-  hipMemcpyAsync(L->sh_uq, uq, I * H, hipMemcpyDeviceToDevice, st);
-  hipMemcpyAsync(L->sh_dq, dq, H * I, hipMemcpyDeviceToDevice, st);
-  hipMemcpyAsync(L->sh_gs, gs, I * 4, hipMemcpyDeviceToDevice, st);
-  hipMemcpyAsync(L->sh_us, us, I * 4, hipMemcpyDeviceToDevice, st);
-  hipMemcpyAsync(L->sh_ds, ds, H * 4, hipMemcpyDeviceToDevice, st);
+  hipError_t e = hipMemcpyAsync(L->sh_gq, gq, I * H, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(L->sh_uq, uq, I * H, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpy2DAsync(L->sh_dq, Ip, dq, I, I, H, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(L->sh_gs, gs, I * 4, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(L->sh_us, us, I * 4, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(L->sh_ds, ds, H * 4, hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return fail_hip("coli_cuda_moe_layer_set_shared_q8", e);
   return launch_status("coli_cuda_moe_layer_set_shared_q8");
 }
 
+// container rows [rows_src x cols] into tile records of `rows` (a multiple of
+// the tile rows) rows
 static int repack_matrix(ColiCuda *ctx, const TileMat &dst, const unsigned char *q, const float *s, int rows,
-                         int cols, int fmt) {
+                         int rows_src, int cols, int fmt) {
   int ng = (cols + kGroup - 1) / kGroup;
   int rb = fmt == 4 ? ng * kGroup / 2 : ng * kGroup * 3 / 8;
   unsigned char *base = const_cast<unsigned char *>(dst.base);
   size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
-  k_repack_codes<<<blocks_for(lanes, 256), 256, 0, ctx->stream>>>(base, dst.rs, q, rows, cols, rb, ng, fmt);
+  k_repack_codes<<<blocks_for(lanes, 256), 256, 0, ctx->stream>>>(base, dst.rs, q, rows, rows_src, cols, rb, ng,
+                                                                   fmt);
   size_t ns = (size_t)rows * ng;
-  k_repack_scales<<<blocks_for(ns, 256), 256, 0, ctx->stream>>>(base, dst.rs, dst.so, s, rows, ng);
+  k_repack_scales<<<blocks_for(ns, 256), 256, 0, ctx->stream>>>(base, dst.rs, dst.so, s, rows, rows_src, ng);
   return launch_status("expert repack");
 }
 
@@ -1592,10 +1626,10 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
     return fail_arg("coli_cuda_moe_layer_set_expert: null argument");
   if (expert < 0 || expert >= L->sh.experts)
     return fail_arg("coli_cuda_moe_layer_set_expert: expert %d outside [0,%d)", expert, L->sh.experts);
-  int H = L->sh.hidden, I = L->sh.intermediate, fmt = L->sh.expert_format;
-  if (repack_matrix(ctx, L->xl.mat(expert, 0), gq, gs, I, H, fmt) ||
-      repack_matrix(ctx, L->xl.mat(expert, 1), uq, us, I, H, fmt) ||
-      repack_matrix(ctx, L->xl.mat(expert, 2), dq, ds, H, I, fmt))
+  int H = L->sh.hidden, I = L->sh.intermediate, Is = L->I_src, fmt = L->sh.expert_format;
+  if (repack_matrix(ctx, L->xl.mat(expert, 0), gq, gs, I, Is, H, fmt) ||
+      repack_matrix(ctx, L->xl.mat(expert, 1), uq, us, I, Is, H, fmt) ||
+      repack_matrix(ctx, L->xl.mat(expert, 2), dq, ds, H, H, Is, fmt))
     return -1;
   return 0;
 }
@@ -1603,7 +1637,9 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
 extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long seed,
                                               int layer_index) {
   if (!ctx || !L) return fail_arg("coli_cuda_moe_layer_synthesize: null argument");
-  int H = L->sh.hidden, I = L->sh.intermediate, E = L->sh.experts, Ish = L->sh.shared_intermediate;
+  // generated at the caller's shape (I_src, Ish_src), stored at the device's
+  int H = L->sh.hidden, I = L->I_src, E = L->sh.experts, Ish = L->Ish_src;
+  const int Ip = L->sh.intermediate, Ishp = L->sh.shared_intermediate;
   int fmt = L->sh.expert_format;
   uint32_t li = (uint32_t)layer_index;
   hipStream_t st = ctx->stream;
@@ -1615,7 +1651,7 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
   n = (size_t)Ish * H;
   k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_gq, n, sw_key(seed, li, 0, SW_T_SH_GATE_Q));
   k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_uq, n, sw_key(seed, li, 0, SW_T_SH_UP_Q));
-  k_synth_i8<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_dq, n, sw_key(seed, li, 0, SW_T_SH_DOWN_Q));
+  k_synth_i8_rows<<<blocks_for(n, 256), 256, 0, st>>>(L->sh_dq, H, Ish, Ishp, sw_key(seed, li, 0, SW_T_SH_DOWN_Q));
   k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_gs, Ish, sw_key(seed, li, 0, SW_T_SH_GATE_S), 0.01f, 1);
   k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_us, Ish, sw_key(seed, li, 0, SW_T_SH_UP_S), 0.01f, 1);
   k_synth_normal<<<blocks_for(H, 256), 256, 0, st>>>(L->sh_ds, H, sw_key(seed, li, 0, SW_T_SH_DOWN_S), 0.01f, 1);
@@ -1629,14 +1665,15 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
     const int tq[3] = {SW_T_GATE_Q, SW_T_UP_Q, SW_T_DOWN_Q}, ts[3] = {SW_T_GATE_S, SW_T_UP_S, SW_T_DOWN_S};
     for (int m = 0; m < 3; m++) {
       int rows = m < 2 ? I : H, cols = m < 2 ? H : I, rb = m < 2 ? rbh : rbi, ng = m < 2 ? L->ngh : L->ngi;
+      const int rows_dev = m < 2 ? Ip : H;
       size_t nb = (size_t)rows * rb;
       k_synth_bytes<<<blocks_for((nb + 7) / 8, 256), 256, 0, st>>>(tmp, nb, sw_key(seed, li, (uint32_t)e, tq[m]));
       const TileMat dst = L->xl.mat(e, m);
       unsigned char *base = const_cast<unsigned char *>(dst.base);
-      size_t lanes = (size_t)(rows / kTileRows) * ng * 64;
-      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(base, dst.rs, tmp, rows, cols, rb, ng, fmt);
-      k_synth_scales_tiled<<<blocks_for((size_t)rows * ng, 256), 256, 0, st>>>(
-          base, dst.rs, dst.so, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
+      size_t lanes = (size_t)(rows_dev / kTileRows) * ng * 64;
+      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(base, dst.rs, tmp, rows_dev, rows, cols, rb, ng, fmt);
+      k_synth_scales_tiled<<<blocks_for((size_t)rows_dev * ng, 256), 256, 0, st>>>(
+          base, dst.rs, dst.so, rows_dev, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
     }
   }
   return launch_status("coli_cuda_moe_layer_synthesize");

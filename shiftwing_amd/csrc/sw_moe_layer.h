@@ -9,7 +9,8 @@
 #include "sw_expert_layout.h"
 
 struct ColiMoeLayer {
-  ColiMoeShape sh;
+  ColiMoeShape sh;               // the device shape: I and shared I rounded up to the tiles (16, 64)
+  int I_src, Ish_src;            // the caller's I and shared I (rows past them hold zeros)
   int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
   float *router;                 // [E][H]
   float *sgate_row;              // [H]
