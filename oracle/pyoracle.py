@@ -267,6 +267,23 @@ class Reference:
         L.ref_set_threads.argtypes = [C.c_int]
         L.ref_omp_threads.restype = C.c_int
 
+    def route_gather_all(self, idx: np.ndarray, weight: np.ndarray, E: int):
+        """moe_prefill_route_gather for experts 0..E-1: (offsets, tokens,
+        weights, gathered rows) in the reference's order."""
+        T, K = idx.shape
+        idx = np.ascontiguousarray(idx, np.int32)
+        weight = np.ascontiguousarray(weight, np.float32)
+        off = np.zeros(E + 1, np.int32)
+        tok = np.zeros(T * K, np.int32)
+        wt = np.zeros(T * K, np.float32)
+        xb = np.zeros(T * K, np.float32)
+        L = self.lib
+        L.ref_route_gather_all.restype = C.c_int
+        L.ref_route_gather_all.argtypes = [i32p, f32p, C.c_int, C.c_int, C.c_int, i32p, i32p, f32p, f32p]
+        n = L.ref_route_gather_all(ptr(idx, i32p), ptr(weight, f32p), T, K, E, ptr(off, i32p), ptr(tok, i32p),
+                                   ptr(wt, f32p), ptr(xb, f32p))
+        return off, tok[:n], wt[:n], xb[:n]
+
     def dot(self, a, b):
         return self.lib.ref_dot(ptr(a, f32p), ptr(b, f32p), a.size)
 

@@ -174,6 +174,25 @@ void ref_moe_prefill_grouped(void *h, const float *x, int T, float *out) {
     moe_prefill_grouped(&r->m, &r->l, x, T, out, 0);
 }
 
+/* moe_prefill_route_gather (c/qwen.c:3956-3968) for every expert in
+ * ascending id, the order moe_prefill_grouped serves them in: per expert its
+ * tokens and weights in gather order.  The gathered rows come from x[t] = t
+ * (H = 1), so xb also shows which token each row copied.  Returns the total. */
+int ref_route_gather_all(const int *idx, const float *weight, int T, int K, int E, int *offsets, int *token,
+                         float *wt, float *xb) {
+    float *x = (float *)malloc((size_t)(T > 0 ? T : 1) * sizeof(float));
+    if (!x) return -1;
+    for (int t = 0; t < T; t++) x[t] = (float)t;
+    int n = 0;
+    for (int e = 0; e < E; e++) {
+        offsets[e] = n;
+        n += moe_prefill_route_gather(e, idx, weight, x, T, K, 1, token + n, wt + n, xb + n);
+    }
+    offsets[E] = n;
+    free(x);
+    return n;
+}
+
 int ref_omp_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

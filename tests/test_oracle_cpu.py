@@ -188,6 +188,38 @@ def test_bucket_is_stable_counting_sort(oracle):
         assert np.array_equal(tok, want_tok) and np.array_equal(slot, want_slot)
 
 
+def test_bucket_matches_compiled_route_gather(oracle):
+    """or_bucket against the reference's own moe_prefill_route_gather
+    (c/qwen.c:3956-3968, compiled in place), walked over the experts in
+    ascending id as moe_prefill_grouped does: the same offsets and tokens in
+    the same order, each gathered row the token's, each weight the token's
+    first route to that expert (also when a row repeats an expert, where the
+    reference's loop stops at the first match)."""
+    from oracle.pyoracle import Reference
+    try:
+        ref = Reference()
+    except Exception as e:  # not built (no reference sources here)
+        pytest.skip(f"compiled reference not available: {e}")
+    rng = np.random.default_rng(31)
+    cases = []
+    for T, K, E in [(1, 8, 256), (7, 4, 16), (33, 10, 512), (300, 8, 256)]:
+        cases.append(np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32))
+    dup = rng.integers(0, 6, (40, 5)).astype(np.int32)  # repeats within a row, unused experts
+    cases.append(dup)
+    for idx in cases:
+        T, K = idx.shape
+        E = 6 if idx is dup else int(idx.max()) + 1 + (idx is not dup) * 3
+        weight = rng.random((T, K)).astype(np.float32)
+        off, tok, slot = oracle.bucket(idx, E)
+        roff, rtok, rwt, rxb = ref.route_gather_all(idx, weight, E)
+        assert np.array_equal(off, roff) and np.array_equal(tok, rtok), (T, K, E)
+        assert np.array_equal(rxb, rtok.astype(np.float32))
+        assert np.array_equal(rwt, weight[tok, slot])
+        for e in range(E):
+            for n in range(off[e], off[e + 1]):
+                assert idx[tok[n], slot[n]] == e and e not in idx[tok[n], :slot[n]]
+
+
 # ---------------------------------------------------------------- layers
 def _layer(oracle, name):
     g = np.load(os.path.join(GOLDEN, f"layer_{name}.npz"))
