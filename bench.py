@@ -526,6 +526,96 @@ def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_k
     }
 
 
+HEAD_SHAPE = (248320, 4096)  # vocab x hidden of the S397 model (c/fixtures/qwen3_5_config/config.json:9,98)
+
+
+def measure_head(be, steps, warmup, batch=1):
+    """The output head (the final norm and the int8 lm_head through IDOT,
+    coli_cuda_output_head_q8) at the S397 model's vocab x hidden, for `batch`
+    final rows per step: HIP events on the context stream around each call.
+    The matrix bytes are a constant fill (timing does not depend on values;
+    the GPU tests check the arithmetic)."""
+    vocab, H = HEAD_SHAPE
+    lib = be.lib
+    q, sc = be.alloc(vocab * H), be.alloc(vocab * 4)
+    be.check(lib.coli_cuda_memset(be.ctx, q.p, 0x35, vocab * H))
+    be.check(lib.coli_cuda_synth_activations(be.ctx, sc.p, 1, vocab, C.c_ulonglong(7), 0, 0))
+    x, w = be.alloc(batch * H * 4), be.alloc(H * 4)
+    be.check(lib.coli_cuda_synth_activations(be.ctx, x.p, batch, H, C.c_ulonglong(8), 0, 0))
+    be.check(lib.coli_cuda_synth_activations(be.ctx, w.p, 1, H, C.c_ulonglong(9), 0, 0))
+    lg, hid = be.alloc(batch * vocab * 4), be.alloc(batch * H * 4)
+
+    def run():
+        be.check(lib.coli_cuda_output_head_q8(be.ctx, lg.p, hid.p, x.p, w.p, C.c_float(1e-6), batch, q.p, sc.p,
+                                              vocab, H, H), "output_head_q8")
+
+    for _ in range(warmup):
+        run()
+    be.sync()
+    durs = []
+    for _ in range(steps):
+        be.check(lib.coli_cuda_timer_start(be.ctx))
+        run()
+        m = C.c_float()
+        be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(m)))
+        durs.append(m.value)
+    ms = sum(durs) / len(durs)
+    nbytes = vocab * H + vocab * 4 + batch * vocab * 4 + batch * H * 8  # rows, scales, logits, x and n
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    for b in (q, sc, x, w, lg, hid):
+        b.free()
+    return {
+        "metric": "output head calls/s (final norm + int8 lm_head, IDOT, bit-exact)", "value": round(1e3 / ms, 2),
+        "unit": "calls/s", "ms_per_step": round(ms, 4), "steps": steps, "warmup": warmup,
+        "config": {"workload": "f4: output head of the S397 model, vocab 248,320 x hidden 4096 int8 lm_head "
+                               "(one f32 scale per row), final rmsnorm_zero", "vocab": vocab, "hidden": H,
+                   "rows_per_call": batch},
+        "roofline": {"bound": "hbm", "kernel": "k_head_norm + k_head_q8", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("output-head", "k_head_q8", 1), "bytes_per_launch": nbytes,
+                     "avg_launch_us": round(ms * 1e3, 3)},
+    }
+
+
+def cpu_baseline_head(budget_s: float, batch=1):
+    """The CPU path's output head (rmsnorm_zero + IDOT over the int8 lm_head)
+    at the full vocab x hidden: the 1 GB matrix streams from host memory as
+    it does in the reference (a row sample would sit in the CPU's cache)."""
+    from oracle import pyoracle as po
+    vocab, H = HEAD_SHAPE
+    o = po.Oracle()
+    kind, ref = "port", None
+    try:
+        ref = po.Reference()
+        kind = "reference"
+    except Exception:
+        pass
+    rows = vocab
+    rng = np.random.default_rng(5)
+    q = rng.integers(-127, 128, (rows, H), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(rows)) * 0.01).astype(np.float32)
+    x = rng.standard_normal((batch, H)).astype(np.float32)
+    w = (rng.standard_normal(H) * 0.1).astype(np.float32)
+    m = po.HostQMat(1, rows, H, 0, q=q, s=s)
+    impl = ref if ref is not None else o
+
+    def one(i):
+        n = np.stack([impl.rmsnorm_zero(x[b], w, 1e-6) for b in range(batch)])
+        impl.qmat_mul_batch(n, m, 1)
+        return 1
+
+    info = cpu_info()
+    out = {"unit": "calls/s", "kind": kind, "cpu_model": info["model"], "physical_cores": info["physical_cores"]}
+    for threads, key in ((info["usable_cpus"], "value"), (8, "value_8_threads")):
+        impl.set_threads(threads)
+        n, dt = _timed(one, budget_s if key == "value" else budget_s / 2, 200)
+        out[key] = round(n / dt, 3)
+        if key == "value":
+            out["cores"] = threads
+            out["sample"] = f"{n} calls over all {vocab} rows ({dt:.1f} s, {threads} threads)"
+    return out
+
+
 def progress(msg):
     """A progress line on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -556,7 +646,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["all"] + sorted(WORKLOADS) + sorted(MANY),
+    ap.add_argument("--workload", default="all", choices=["all", "output-head"] + sorted(WORKLOADS) + sorted(MANY),
                     help="all (default): config 2 is the headline; configs 1, 3 (B = 1..32) and 4 are timed in "
                          "the same run and reported under 'configs'")
     ap.add_argument("--batch", type=int, default=8, help="tokens per step of --workload s397-batch")
@@ -585,6 +675,12 @@ def main():
         H, E, K, I, Ish, fmt, nl, seed, desc = WORKLOADS[name]
         return (H, E, K, I, Ish, fmt, layers or args.layers or nl, seed, desc)
 
+    if args.workload == "output-head":
+        r = measure_head(be, args.steps, args.warmup, 1)
+        r = with_cpu(r, args, lambda: cpu_baseline_head(args.cpu_seconds))
+        print(json.dumps({"n_gpus": 1, "higher_is_better": True, "dtype": "int8", "data": "synthetic", **r}),
+              flush=True)
+        return
     if args.workload in MANY:
         base, nl, T, use_zipf, desc = MANY[args.workload]
         nl = args.layers or nl
@@ -660,6 +756,13 @@ def main():
     progress(f"config 1 decode: {r1['value']} tok/s")
     r1 = with_cpu(r1, args, lambda: cpu_baseline(cfg1, args.cpu_seconds, zipf35))
     configs["config1"] = r1
+    for L in s35:
+        L.close()
+    del s35
+    # f4: the output head after the last layer (one decode token)
+    hd = measure_head(be, 10, 3)
+    progress(f"output head: {hd['roofline']['avg_launch_us']} us per call")
+    configs["output_head"] = with_cpu(hd, args, lambda: cpu_baseline_head(args.cpu_seconds / 2))
     line["configs"] = configs
     line["wall_s"] = round(time.perf_counter() - t0, 1)
     print(json.dumps(line), flush=True)

@@ -477,6 +477,20 @@ int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode);
  * trace = NULL, words = 0 switches it off. */
 int coli_cuda_moe_stack_trace(ColiCuda *ctx, unsigned long long *trace,
                               size_t words);
+/* The output head (c/qwen.c:4505-4516 for B rows, 4613-4616 for decode; the
+ * device glue cuda_resident_output_try, 1097-1124): for each of `batch` rows
+ * of x [batch x cols], n = rmsnorm_zero(x, norm_w, eps) (c/qwen.c:1780-1784,
+ * the serial fp32 sum of squares) and logits [batch x vocab] = the int8
+ * lm_head [vocab x row_bytes] (one f32 scale per row) applied with the CPU
+ * path's IDOT (qrow_i8(n), exact int32 dots, ((float)dot * scale) * sx;
+ * c/qwen.c:1696-1705, 1765-1768).  Bit-exact with the CPU path.  `hidden`
+ * (optional, [batch x cols]) receives n, which the reference also returns.
+ * cols <= 16384; the matrix is streamed once per group of four rows. */
+int coli_cuda_output_head_q8(ColiCuda *ctx, float *logits, float *hidden,
+                             const float *x, const float *norm_w, float eps,
+                             int batch, const signed char *q,
+                             const float *scales, int vocab, int cols,
+                             int row_bytes);
 /* Fault drill of the persistent decode kernel (no counterpart in the
  * reference; for tests of its timeout path).  The next launch keeps its last
  * `absent_workgroups` workgroups out, as if they never became resident, and

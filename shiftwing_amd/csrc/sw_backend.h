@@ -40,6 +40,7 @@ enum Scratch {
   kScrShared,      // three-kernel decode: shared expert int32 sums + h
   kScrStack,       // persistent decode: router records, exact logits, h records
   kScrBlock,       // MoE block: normalised activations and the MoE output
+  kScrHead,        // output head: quantised normalised rows and their scales
   kScrCount
 };
 
