@@ -656,6 +656,8 @@ def main():
     ap.add_argument("--decode-kernels", type=int, default=1, choices=[1, 2],
                     help="1: the persistent decode kernel, one launch per stack step (default); "
                          "2: the three per-layer decode kernels")
+    ap.add_argument("--item-tokens", type=int, default=0, choices=[0, 8, 16],
+                    help="many-token steps: tokens per expert item (0 automatic; for measurement)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="time a plain device-to-device copy of MIB MiB (the counter calibration kernel) and exit")
     args = ap.parse_args()
@@ -669,6 +671,7 @@ def main():
     from shiftwing_amd import Backend
     be = Backend(0)
     be.set_decode_kernels(args.decode_kernels)
+    be.check(be.lib.coli_cuda_moe_set_item_tokens(be.ctx, args.item_tokens), "set_item_tokens")
     t0 = time.perf_counter()
 
     def cfg_of(name, layers=None):

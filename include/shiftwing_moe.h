@@ -469,6 +469,11 @@ int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3],
  * not take fall back to 2); 2 the three per-layer decode kernels; 0 the
  * many-token kernels.  Same results to the stated tolerance (for tests). */
 int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode);
+/* Many-token steps: tokens per expert work item.  0 (default) picks 16 when
+ * the step has at least two routes per expert on average (each expert's
+ * tiles are then read once per 16 tokens), else 8; 8 or 16 force one.  Same
+ * indices; outputs to the stated tolerance (for tests and measurement). */
+int coli_cuda_moe_set_item_tokens(ColiCuda *ctx, int tokens);
 /* Stage stamps of the persistent decode kernel (measurement): while set,
  * every call writes the device wall clock (100 MHz) into the caller's device
  * buffer at [layer][workgroup][8]: layer start, router/shared done, router

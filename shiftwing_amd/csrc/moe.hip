@@ -239,6 +239,7 @@ __device__ float qrow_i8_block(const float *x, int n, signed char *q, float *red
 // ---------------------------------------------------------------------------
 struct Work {
   int T, H, E, K, I, Ish, ngh, ngi, Hp, Ip;
+  int itok;  // tokens per bucketing item: 8 (one MFMA column set) or kWideTokens
   // prep
   signed char *xq; float *sx;
   signed char *xd1, *xd2; float4 *xgp;
@@ -420,6 +421,192 @@ __global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float
   }
 }
 
+// ---------------------------------------------------------------------------
+// 2g. Router for many tokens as an fp64 GEMM on MFMA, with an a-priori bound
+// tightened where it matters.
+//
+// L[t][e] = sum_i x_t[i] w_e[i] in fp64 (fp32 inputs: every product is exact
+// in fp64) on v_mfma_f64_16x16x4.  Any evaluation order of the reference's
+// fp32 dot (c/qwen.c:1674) is within gamma_H * sum|x_i w_i| of the exact sum
+// (gamma_n = n u / (1 - n u), u = 2^-24, products and sums rounded once
+// each), and so is L within the fp64 analogue; sum|x_i w_i| <= ||x_t|| ||w_e||
+// (Cauchy-Schwarz).  So B0 = (gamma_H + gamma'_H) ||x_t|| ||w_e|| (with
+// slack) bounds |fp32 logit - L| for every (t, e).  B0 is about a hundred
+// times looser than the prefix-sum bound of k_router_bounds, so
+// k_router_refine replaces it by that tight bound for the experts that could
+// be among a token's top K; the rest are far below the K-th logit and keep
+// B0.  Every (L, B) pair stays a valid enclosure, so the certification that
+// follows is rigorous whichever experts were refined.
+// ---------------------------------------------------------------------------
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ double wave_max_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// a-priori bound factor: (gamma_H(2^-24) + gamma_H(2^-53)) with slack for the
+// rounding of the norms and of the product that applies it
+__device__ __forceinline__ double gemm_bound_factor(int H) {
+  const double n = (double)H, u = 0x1p-24, v = 0x1p-53;
+  return (n * u / (1.0 - n * u) + n * v / (1.0 - n * v)) * (1.0 + 0x1p-20);
+}
+
+// One 16-token x 16-row tile of L per block; its 4 waves take a quarter of
+// the k range each and their sums meet in LDS in wave order.  MFMA step c of
+// k block kb pairs x_t[16 kb + 4 (l >> 4) + c] with w_e[16 kb + 4 (l >> 4) +
+// c] at lane l (A: token t0 + l % 16, B: row e0 + l % 16), so every lane
+// loads float4s; the result holds token t0 + (l >> 4) + 4 v, row e0 + l % 16
+// at lane l, item v (the f64 16x16x4 output layout: D[(l >> 4) + 4 v][l % 16]).
+// The same loads give ||x_t|| and ||w_e|| (fp64 sums of squares).
+// grid (ceil((E+1)/16), ceil(T/16)), 256 threads.  H % 64 == 0, x 16-byte aligned.
+__global__ __launch_bounds__(256) void k_router_gemm(Work w, const float *x, const float *router,
+                                                     const float *sgate_row) {
+  __shared__ double s_acc[4][4][64];
+  __shared__ double s_nx[4][64], s_nw[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  const int H = w.H, kq = H / 4;
+  const int ta = min(t0 + (lane & 15), w.T - 1), eb = min(e0 + (lane & 15), w.E);
+  const float *xa = x + (size_t)ta * H + wave * kq + 4 * (lane >> 4);
+  const float *wb = (eb < w.E ? router + (size_t)eb * H : sgate_row) + wave * kq + 4 * (lane >> 4);
+  v4d acc = {0.0, 0.0, 0.0, 0.0};
+  double qa = 0.0, qb = 0.0;
+#pragma unroll 4
+  for (int k = 0; k < kq; k += 16) {
+    const float4 a = *(const float4 *)(xa + k), b = *(const float4 *)(wb + k);
+    const double a0 = a.x, a1 = a.y, a2 = a.z, a3 = a.w, b0 = b.x, b1 = b.y, b2 = b.z, b3 = b.w;
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
+    qa = __builtin_fma(a0, a0, __builtin_fma(a1, a1, __builtin_fma(a2, a2, __builtin_fma(a3, a3, qa))));
+    qb = __builtin_fma(b0, b0, __builtin_fma(b1, b1, __builtin_fma(b2, b2, __builtin_fma(b3, b3, qb))));
+  }
+  // sums of squares: lanes l, l^16, l^32, l^48 share a token / a row
+  qa += __shfl_xor(qa, 16, 64);
+  qa += __shfl_xor(qa, 32, 64);
+  qb += __shfl_xor(qb, 16, 64);
+  qb += __shfl_xor(qb, 32, 64);
+#pragma unroll
+  for (int v = 0; v < 4; v++) s_acc[wave][v][lane] = acc[v];
+  s_nx[wave][lane] = qa;
+  s_nw[wave][lane] = qb;
+  __syncthreads();
+  if (wave != 0) return;
+  const int e = e0 + (lane & 15);
+  if (e > w.E) return;
+  const double nw = sqrt(((s_nw[0][lane] + s_nw[1][lane]) + s_nw[2][lane]) + s_nw[3][lane]);
+  const double f = gemm_bound_factor(H) * nw;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int i = (lane >> 4) + 4 * v, t = t0 + i;
+    if (t >= w.T) continue;
+    const double L = ((s_acc[0][v][lane] + s_acc[1][v][lane]) + s_acc[2][v][lane]) + s_acc[3][v][lane];
+    const double nx = sqrt(((s_nx[0][i] + s_nx[1][i]) + s_nx[2][i]) + s_nx[3][i]);
+    w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, f * nx + 1e-36);
+    if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
+  }
+}
+
+// Per token: the experts whose interval reaches below-threshold get the tight
+// bound of k_router_bounds (lane j's contiguous chunk, exact local prefixes,
+// chunk offsets by a wave scan).  The threshold is the K-th largest of the
+// lanes' largest logits (at most the K-th largest logit) less the largest
+// a-priori bound; experts under it cannot reach any of the top K.  Wave 0
+// selects; the waves refine the candidates in turn, the token's x staged in
+// LDS lane-major with one pad word per lane.  More than kRefineMax candidates:
+// the token keeps the a-priori bounds (the certification then takes its exact
+// paths).  grid T, 256 threads, dynamic LDS 64 (H/64 + 1) floats.
+constexpr int kRefineMax = 64;
+__global__ __launch_bounds__(256) void k_router_refine(Work w, const float *x, const float *router) {
+  extern __shared__ float rf_x[];
+  __shared__ int cand[kRefineMax];
+  __shared__ int s_n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = blockIdx.x;
+  const int E = w.E, K = w.K, H = w.H, CH = H / 64, P = CH + 1;
+  const double2 *lb = w.lb + (size_t)t * (E + 1);
+  const float *xt = x + (size_t)t * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) rf_x[(i / CH) * P + i % CH] = xt[i];
+  if (wave == 0) {
+    double m = -1e300, bmax = 0.0;
+    for (int e = lane; e < E; e += 64) {
+      const double2 v = lb[e];
+      m = fmax(m, v.x);
+      bmax = fmax(bmax, v.y);
+    }
+    bmax = wave_max_d(bmax);
+    // K-th largest lane maximum: K rounds that retire the largest
+    double thr = m;
+    bool out = false;
+    for (int k = 0; k < K && k < 64; k++) {
+      const double v = out ? -1e300 : m;
+      const double g = wave_max_d(v);
+      const unsigned long long hit = __ballot(!out && m == g);
+      if (hit && lane == __ffsll((long long)hit) - 1) out = true;
+      thr = g;
+    }
+    thr -= bmax;
+    int n = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      bool c = false;
+      if (e < E) {
+        const double2 v = lb[e];
+        c = v.x + v.y >= thr;
+      }
+      const unsigned long long bal = __ballot(c);
+      const int before = __popcll(bal & ((1ull << lane) - 1ull));
+      if (c && n + before < kRefineMax) cand[n + before] = e;
+      n += __popcll(bal);
+    }
+    if (lane == 0) s_n = n <= kRefineMax ? n : 0;
+  }
+  __syncthreads();
+  const int n = s_n;
+  const float *xl = rf_x + lane * P;
+  for (int c = wave; c < n; c += 4) {
+    const int e = cand[c];
+    const float *row = router + (size_t)e * H + lane * CH;
+    double lp = 0.0, pa = 0.0, aa = 0.0;
+    if ((CH & 3) == 0) {
+      for (int i = 0; i < CH; i += 4) {
+        const float4 r = *(const float4 *)(row + i);
+        const float rv[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const double xd = (double)xl[i + q], wd = (double)rv[q];
+          lp = __builtin_fma(xd, wd, lp);
+          aa = __builtin_fma(fabs(xd), fabs(wd), aa);
+          pa += fabs(lp);
+        }
+      }
+    } else {
+      for (int i = 0; i < CH; i++) {
+        const double xd = (double)xl[i], wd = (double)row[i];
+        lp = __builtin_fma(xd, wd, lp);
+        aa = __builtin_fma(fabs(xd), fabs(wd), aa);
+        pa += fabs(lp);
+      }
+    }
+    const double off = wave_exclusive_scan(lp, lane);
+    const double L = wave_sum(lp);
+    const double Pb = wave_sum((double)CH * fabs(off) + pa);
+    const double A = wave_sum(aa);
+    if (lane == 0) {
+      const double u = 0x1p-24;
+      const double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+      w.lb[(size_t)t * (E + 1) + e] = make_double2(L, B);
+    }
+  }
+}
+
 // block argmax over (value, index): largest value, lowest index on ties
 struct VI {
   double v;
@@ -517,11 +704,6 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
   }
 }
 
-__device__ __forceinline__ double wave_max_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
-  return v;
-}
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
@@ -845,7 +1027,7 @@ __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx
 // route (t,k)).  One block of 1024 threads; tokens_per_step(E) tokens at most (the E x T bit map fits 160 KiB).
 // ---------------------------------------------------------------------------
 __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
-                             int *pos, int4 *items, int *nitems, unsigned *bits, int *cnt, int *iofs) {
+                             int *pos, int4 *items, int *nitems, unsigned *bits, int *cnt, int *iofs, int itok) {
   int words = (T + 31) / 32;
   for (int i = threadIdx.x; i < E * words; i += blockDim.x) bits[i] = 0;
   __syncthreads();
@@ -867,7 +1049,7 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
     int c = 0, ni = 0;
     for (int e = e0; e < e0 + per && e < E; e++) {
       c += cnt[e];
-      ni += (cnt[e] + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+      ni += (cnt[e] + itok - 1) / itok;
     }
     int ic = c, ii = ni;  // inclusive wave scans
 #pragma unroll
@@ -893,7 +1075,7 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
       offsets[e] = acc;
       iofs[e] = ia;
       acc += cnt[e];
-      ia += (cnt[e] + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+      ia += (cnt[e] + itok - 1) / itok;
     }
     if (e0 < E && e0 + per >= E) {  // the thread owning the last expert
       offsets[E] = acc;
@@ -926,8 +1108,7 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
   }
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int n = cnt[e];
-    for (int i = 0, it = iofs[e]; i < n; i += kMaxTokensPerItem, it++)
-      items[it] = make_int4(e, offsets[e] + i, min(kMaxTokensPerItem, n - i), 0);
+    for (int i = 0, it = iofs[e]; i < n; i += itok, it++) items[it] = make_int4(e, offsets[e] + i, min(itok, n - i), 0);
   }
 }
 
@@ -937,7 +1118,8 @@ __global__ void k_bucket(Work w) {
   unsigned *bits = smem;
   int *cnt = (int *)(smem + w.E * words);
   int *iofs = cnt + w.E;
-  bucket_block(w.idx, w.T, w.K, w.E, w.offsets, w.btok, w.bslot, w.pos, w.items, w.nitems, bits, cnt, iofs);
+  bucket_block(w.idx, w.T, w.K, w.E, w.offsets, w.btok, w.bslot, w.pos, w.items, w.nitems, bits, cnt, iofs,
+               w.itok);
 }
 
 __global__ void k_bucket_only(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
@@ -947,7 +1129,7 @@ __global__ void k_bucket_only(const int *idx, int T, int K, int E, int *offsets,
   unsigned *bits = smem;
   int *cnt = (int *)(smem + E * words);
   int *iofs = cnt + E;
-  bucket_block(idx, T, K, E, offsets, btok, bslot, pos, items, nitems, bits, cnt, iofs);
+  bucket_block(idx, T, K, E, offsets, btok, bslot, pos, items, nitems, bits, cnt, iofs, kMaxTokensPerItem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1456,6 +1638,253 @@ __global__ __launch_bounds__(512) void k_down_split(Work w, ExpertLayout xl, int
 }
 
 // ---------------------------------------------------------------------------
+// 7w / 8w.  Wide items, for many-token steps with several tokens per expert:
+// an item holds up to kWideTokens tokens of one expert, so every weight tile
+// of the expert is read once per kWideTokens tokens instead of once per 8.
+// The item's activation digits are staged in LDS in the MFMA B-operand order
+// of mt_digits (chunk j = tokens 8j..8j+7); waves own row tiles and walk
+// every group, a batch of groups' tiles in flight while the previous batch
+// multiplies, and each tile feeds 2 MFMAs per chunk.  A wave's dot over the
+// groups is one accumulation in group order (no cross-wave sums).
+// grid (row-tile blocks, item slots), 512 threads, dynamic LDS wide_lds_bytes.
+// ---------------------------------------------------------------------------
+constexpr int kWideChunks = 2;                // 8-token column chunks per item
+constexpr int kWideTokens = 8 * kWideChunks;  // tokens per item
+// row tiles per wave and groups per load batch (a wave holds two batches):
+// gate/up 1 row tile of both matrices x 2 groups, down 4 row tiles x 1 group
+constexpr int kWideRt = 1, kWideGuBatch = 2;
+constexpr int kWideDnRt = 4, kWideDnBatch = 1;
+
+// LDS of one item over ng groups: digits [chunk][group][half][lane] 16 B,
+// then the digit parameters [chunk][group][column] (scale, digit sum)
+__host__ __device__ inline size_t wide_lds_bytes(int ng) { return (size_t)kWideChunks * ng * (2 * 1024 + 16 * 8); }
+
+// Stage an item's digits.  Token tt of the item is row rows_of[p0+tt] of the
+// digit planes (rows_of null: row p0+tt); tokens past cnt stage zeros.
+__device__ void wide_stage(unsigned char *lds, int ng, int ld, const signed char *d1, const signed char *d2,
+                           const float4 *gp, const int *rows_of, int p0, int cnt) {
+  const int nunits = kWideChunks * ng * 128;
+  for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
+    const int l = u & 63, h = (u >> 6) & 1, jg = u >> 7;
+    const int j = jg / ng, g = jg - j * ng;
+    const int tt = 8 * j + ((l & 15) >> 1);
+    v4i v = {0, 0, 0, 0};
+    if (tt < cnt) {
+      const int row = rows_of ? rows_of[p0 + tt] : p0 + tt;
+      v = *(const v4i *)(((l & 1) ? d2 : d1) + (size_t)row * ld + g * kGroup + h * 64 + (l >> 4) * 16);
+    }
+    *(v4i *)(lds + (size_t)u * 16) = v;
+  }
+  float2 *P = (float2 *)(lds + (size_t)kWideChunks * ng * 2048);
+  for (int v = threadIdx.x; v < kWideChunks * ng * 16; v += blockDim.x) {
+    const int c = v & 15, jg = v >> 4, j = jg / ng, g = jg - j * ng;
+    const int tt = 8 * j + (c >> 1);
+    float2 pv = make_float2(0.0f, 0.0f);
+    if (tt < cnt) {
+      const int row = rows_of ? rows_of[p0 + tt] : p0 + tt;
+      const float4 q = gp[(size_t)row * ng + g];
+      pv = (c & 1) ? make_float2(q.y, q.w) : make_float2(q.x, q.z);
+    }
+    P[v] = pv;
+  }
+}
+
+struct WideDigits {
+  v4i b0[kWideChunks], b1[kWideChunks];
+  float dsc[kWideChunks];
+  int Q[kWideChunks];
+};
+__device__ __forceinline__ void wide_digits(WideDigits &d, const unsigned char *lds, int ng, int g, int lane) {
+  const v4i *D = (const v4i *)lds;
+  const float2 *P = (const float2 *)(lds + (size_t)kWideChunks * ng * 2048);
+#pragma unroll
+  for (int j = 0; j < kWideChunks; j++) {
+    d.b0[j] = D[((j * ng + g) * 2 + 0) * 64 + lane];
+    d.b1[j] = D[((j * ng + g) * 2 + 1) * 64 + lane];
+    const float2 p = P[(j * ng + g) * 16 + (lane & 15)];
+    d.dsc[j] = p.x;
+    d.Q[j] = __float_as_int(p.y);
+  }
+}
+
+// one tile (codes unpacked to a0/a1, row scales sc) times every chunk
+template <int FMT>
+__device__ __forceinline__ void wide_mac(const uint32_t *q, const float4 sc, const WideDigits &d,
+                                         float acc[kWideChunks][4]) {
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+  v4i a0, a1;
+  unpack_words<FMT>(q, a0, a1);
+  const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+  for (int j = 0; j < kWideChunks; j++) {
+    v4i c = {0, 0, 0, 0};
+    c = mfma_i8(a0, d.b0[j], c);
+    c = mfma_i8(a1, d.b1[j], c);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float f = (float)(c[r] - OFF * d.Q[j]) * d.dsc[j];
+      const float tsum = f + dpp_row_shr1(f);
+      acc[j][r] = __builtin_fmaf(tsum, scv[r], acc[j][r]);
+    }
+  }
+}
+
+template <int FMT, int NB, int NR, int NM>
+struct WideTiles {
+  uint32_t q[NB][NR][NM][FMT == 4 ? 4 : 3];
+  float4 sc[NB][NR][NM];
+};
+
+// tiles of groups [gb, gb + NB) for row tiles [rt0, rt0 + NR) of the NM
+// matrices (mats[m]); row tiles past nrt and groups past ng are skipped
+template <int FMT, int NB, int NR, int NM>
+__device__ __forceinline__ void wide_load(WideTiles<FMT, NB, NR, NM> &t, const TileMat *mats, int rt0, int nrt,
+                                          int ng, int gb, int lane) {
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+  const int kb = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < NB; i++)
+#pragma unroll
+    for (int rr = 0; rr < NR; rr++)
+#pragma unroll
+      for (int m = 0; m < NM; m++) {
+        const int g = gb + i, rt = rt0 + rr;
+        if (g < ng && rt < nrt) {
+          const size_t tg = (size_t)rt * ng + g;
+          load_words<FMT>(tm_codes(mats[m], tg) + lane * BPL, t.q[i][rr][m]);
+          t.sc[i][rr][m] = *(const float4 *)(tm_scales(mats[m], tg) + 4 * kb);
+        }
+      }
+}
+
+template <int FMT, int NB, int NR, int NM>
+__device__ __forceinline__ void wide_compute(const WideTiles<FMT, NB, NR, NM> &t, const unsigned char *lds, int rt0,
+                                             int nrt, int ng, int gb, int lane,
+                                             float acc[NR][NM][kWideChunks][4]) {
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    const int g = gb + i;
+    if (g >= ng) break;
+    WideDigits d;
+    wide_digits(d, lds, ng, g, lane);
+#pragma unroll
+    for (int rr = 0; rr < NR; rr++)
+      if (rt0 + rr < nrt)
+#pragma unroll
+        for (int m = 0; m < NM; m++) wide_mac<FMT>(t.q[i][rr][m], t.sc[i][rr][m], d, acc[rr][m]);
+  }
+}
+
+// the groups of row tiles [rt0, rt0 + NR): two tile buffers, the next batch
+// loading while the current one multiplies
+template <int FMT, int NB, int NR, int NM>
+__device__ __forceinline__ void wide_rows(const TileMat *mats, const unsigned char *lds, int rt0, int nrt, int ng,
+                                          int lane, float acc[NR][NM][kWideChunks][4]) {
+  WideTiles<FMT, NB, NR, NM> ta, tb;
+  wide_load<FMT, NB, NR, NM>(ta, mats, rt0, nrt, ng, 0, lane);
+  for (int gb = 0; gb < ng; gb += 2 * NB) {
+    if (gb + NB < ng) wide_load<FMT, NB, NR, NM>(tb, mats, rt0, nrt, ng, gb + NB, lane);
+    wide_compute<FMT, NB, NR, NM>(ta, lds, rt0, nrt, ng, gb, lane, acc);
+    if (gb + NB >= ng) break;
+    if (gb + 2 * NB < ng) wide_load<FMT, NB, NR, NM>(ta, mats, rt0, nrt, ng, gb + 2 * NB, lane);
+    wide_compute<FMT, NB, NR, NM>(tb, lds, rt0, nrt, ng, gb + NB, lane, acc);
+  }
+}
+
+// routed gate/up of wide items: h = silu(g)*u.  Block: 8 waves x kWideRt row
+// tiles of I; grid (ceil(I/16 / (8 kWideRt)), item slots).
+template <int FMT>
+__global__ __launch_bounds__(512) void k_gateup_wide(Work w, ExpertLayout xl) {
+  extern __shared__ __align__(16) unsigned char wlds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
+  const int nrt = w.I / kTileRows;
+  const int rt0 = (blockIdx.x * 8 + wave) * kWideRt;
+  const int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
+    const int4 item = w.items[it];
+    const int e = item.x, p0 = item.y, cnt = item.z;
+    __syncthreads();  // the previous item's digits are read no more
+    wide_stage(wlds, w.ngh, w.Hp, w.xd1, w.xd2, w.xgp, w.btok, p0, cnt);
+    __syncthreads();
+    if (rt0 >= nrt) continue;
+    const TileMat mats[2] = {xl.mat(e, 0), xl.mat(e, 1)};
+    float acc[kWideRt][2][kWideChunks][4] = {};
+    wide_rows<FMT, kWideGuBatch, kWideRt, 2>(mats, wlds, rt0, nrt, w.ngh, lane, acc);
+    if (lane & 1) {
+#pragma unroll
+      for (int j = 0; j < kWideChunks; j++) {
+        const int tt = 8 * j + ((lane & 15) >> 1);
+        if (tt >= cnt) continue;
+#pragma unroll
+        for (int rr = 0; rr < kWideRt; rr++) {
+          const int rt = rt0 + rr;
+          if (rt >= nrt) continue;
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            w.hroute[(size_t)(p0 + tt) * w.I + rt * kTileRows + 4 * kb + r] =
+                silu_ref(acc[rr][0][j][r]) * acc[rr][1][j][r];
+        }
+      }
+    }
+  }
+}
+
+// routed down of wide items, plus the shared expert's token chunks (IDOT) in
+// the extra blocks y >= item_slots.  Block: 8 waves x kWideDnRt row tiles of H.
+template <int FMT>
+__global__ __launch_bounds__(512) void k_down_wide(Work w, ExpertLayout xl, int item_slots, const signed char *dq,
+                                                   const float *ds) {
+  extern __shared__ __align__(16) unsigned char wlds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
+  const int nrt = w.H / kTileRows;
+  const int rtb = blockIdx.x * 8 * kWideDnRt;
+  if ((int)blockIdx.y >= item_slots) {
+    const int rt1 = min(nrt, rtb + 8 * kWideDnRt);
+    const int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens, tok = t0 + (lane & 15);
+    for (int rt = rtb + wave; rt < rt1; rt += 8) {
+      v4i c = {0, 0, 0, 0};
+      idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
+      if (tok < w.T) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int row = rt * kTileRows + 4 * kb + i;
+          w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+        }
+      }
+    }
+    return;
+  }
+  const int rt0 = rtb + wave * kWideDnRt;
+  const int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += item_slots) {
+    const int4 item = w.items[it];
+    const int e = item.x, p0 = item.y, cnt = item.z;
+    __syncthreads();
+    wide_stage(wlds, w.ngi, w.Ip, w.hd1, w.hd2, w.hgp, nullptr, p0, cnt);
+    __syncthreads();
+    if (rt0 >= nrt) continue;
+    const TileMat mats[1] = {xl.mat(e, 2)};
+    float acc[kWideDnRt][1][kWideChunks][4] = {};
+    wide_rows<FMT, kWideDnBatch, kWideDnRt, 1>(mats, wlds, rt0, nrt, w.ngi, lane, acc);
+    if (lane & 1) {
+#pragma unroll
+      for (int j = 0; j < kWideChunks; j++) {
+        const int tt = 8 * j + ((lane & 15) >> 1);
+        if (tt >= cnt) continue;
+#pragma unroll
+        for (int rr = 0; rr < kWideDnRt; rr++) {
+          const int rt = rt0 + rr;
+          if (rt >= nrt) continue;
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + r] = acc[rr][0][j][r];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 9. combine.  One token (moe_forward 3734-3737): out = fma chain over k of
 // tmp_k * w_k, then fma(shared, sg).  Many tokens (moe_prefill_grouped
 // 4151-4152, 3977, 4203): shared *= sg, routed = tmp*w, out = sum_k routed +
@@ -1682,6 +2111,7 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
 static Work make_work(const ColiMoeLayer *L, int T) {
   Work w;
   memset(&w, 0, sizeof(w));
+  w.itok = kMaxTokensPerItem;
   w.T = T;
   w.H = L->sh.hidden;
   w.E = L->sh.experts;
@@ -1733,11 +2163,18 @@ static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const fl
   return 0;
 }
 
+// Steps of at least this many tokens route through the fp64 MFMA GEMM
+constexpr int kRouterGemmTokens = 32;
+
 static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
   hipStream_t st = ctx->stream;
   k_prep_x<<<w.T, 1024, 0, st>>>(w, x);
   int rc = 1;  // 1: shape or alignment outside the tiled router kernel
-  if (((uintptr_t)x & 15) == 0) switch (w.H) {
+  if (w.T >= kRouterGemmTokens && w.H % 64 == 0 && ((uintptr_t)x & 15) == 0) {
+    k_router_gemm<<<dim3((w.E + 1 + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router, L->sgate_row);
+    k_router_refine<<<w.T, 256, (size_t)64 * (w.H / 64 + 1) * 4, st>>>(w, x, L->router);
+    rc = 0;
+  } else if (((uintptr_t)x & 15) == 0) switch (w.H) {
       case 256: rc = router_bounds_tiled<4>(ctx, L, w, x); break;
       case 512: rc = router_bounds_tiled<8>(ctx, L, w, x); break;
       case 1024: rc = router_bounds_tiled<16>(ctx, L, w, x); break;
@@ -1759,9 +2196,21 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   return launch_status("MoE routing kernels");
 }
 
+// Tokens per bucketing item.  Steps with at least two routes per expert on
+// average take the wide items (each expert's tiles read once per
+// kWideTokens tokens) when an item's digits fit the LDS; the context's
+// setting (coli_cuda_moe_set_item_tokens) can force either.
+static int item_tokens(const ColiCuda *ctx, const ColiMoeLayer *L, int T) {
+  const int mode = ctx->moe_item_tokens;
+  const bool fits = wide_lds_bytes(L->ngh) <= 160 * 1024 && wide_lds_bytes(L->ngi) <= 160 * 1024;
+  const bool want = mode == kWideTokens || (mode == 0 && T * L->sh.topk >= 2 * L->sh.experts);
+  return want && fits && mode != kMaxTokensPerItem ? kWideTokens : kMaxTokensPerItem;
+}
+
 static int prepare(ColiCuda *ctx, ColiMoeLayer *L, int T, Work &w) {
   if (T <= 0 || T > kMaxTokens) return fail_arg("MoE step: tokens %d outside [1,%d]", T, kMaxTokens);
   w = make_work(L, T);
+  w.itok = item_tokens(ctx, L, T);
   size_t bytes = carve(w, nullptr);
   if (ensure_scratch(ctx, kScrXPrep, bytes, "MoE workspace allocation")) return -1;
   carve(w, (char *)ctx->scratch[kScrXPrep]);
@@ -1851,18 +2300,31 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
       w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
   mark(ctx, 3);
   prof_mark(ctx, kStageSharedHidden);
-  int item_bound = w.E + (T * w.K + kMaxTokensPerItem - 1) / kMaxTokensPerItem;
+  int item_bound = w.E + (T * w.K + w.itok - 1) / w.itok;
   int slots = item_bound < T * w.K ? item_bound : T * w.K;
   if (slots > 1024) slots = 1024;
-  const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
-  const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
-  const bool wide = (w.ngh + 7) / 8 > kMtBatch;  // a wave's groups exceed one batch
-  if (L->sh.expert_format == 4)
-    wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
-         : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
-  else
-    wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
-         : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
+  const bool fmt4 = L->sh.expert_format == 4;
+  const bool wide_items = w.itok > kMaxTokensPerItem;
+  if (wide_items) {
+    const size_t lg = wide_lds_bytes(w.ngh);
+    const void *fn = fmt4 ? (const void *)k_gateup_wide<4> : (const void *)k_gateup_wide<3>;
+    if (set_lds(fn, lg)) return -1;
+    const dim3 grid((w.I / kTileRows + 8 * kWideRt - 1) / (8 * kWideRt), slots);
+    if (fmt4)
+      k_gateup_wide<4><<<grid, 512, lg, st>>>(w, L->xl);
+    else
+      k_gateup_wide<3><<<grid, 512, lg, st>>>(w, L->xl);
+  } else {
+    const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
+    const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
+    const bool wide = (w.ngh + 7) / 8 > kMtBatch;  // a wave's groups exceed one batch
+    if (fmt4)
+      wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
+           : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
+    else
+      wide ? k_expert_gateup<3, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
+           : k_expert_gateup<3, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
+  }
   mark(ctx, 4);
   prof_mark(ctx, kStageRoutedHidden);
   k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
@@ -1871,12 +2333,22 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   const int dn_blocks_x = (w.H / kTileRows + 4 * kDnRowTiles - 1) / (4 * kDnRowTiles);
   const bool dn_split = w.ngi <= 8;
   const int ds_blocks_x = (w.H / kTileRows + kDnBlockRows - 1) / kDnBlockRows;
-  if (L->sh.expert_format == 4)
+  if (wide_items) {
+    const size_t ld = wide_lds_bytes(w.ngi);
+    const void *fn = fmt4 ? (const void *)k_down_wide<4> : (const void *)k_down_wide<3>;
+    if (set_lds(fn, ld)) return -1;
+    const dim3 grid((w.H / kTileRows + 8 * kWideDnRt - 1) / (8 * kWideDnRt), slots + sh_chunks);
+    if (fmt4)
+      k_down_wide<4><<<grid, 512, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+    else
+      k_down_wide<3><<<grid, 512, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+  } else if (fmt4) {
     dn_split ? k_down_split<4><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
-  else
+  } else {
     dn_split ? k_down_split<3><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<3><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+  }
   mark(ctx, 6);
   prof_mark(ctx, kStageRoutedDown);
   k_combine<<<dim3((w.H + 255) / 256, T), 256, 0, st>>>(w, y, route_idx, route_weight);
@@ -1966,6 +2438,14 @@ extern "C" int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3], unsigned 
   if (!ctx || !ms || !calls) return fail_arg("coli_cuda_moe_decode_times: null argument");
   memcpy(ms, ctx->moe_dec_ms, sizeof(ctx->moe_dec_ms));
   *calls = ctx->moe_dec_calls;
+  return 0;
+}
+
+extern "C" int coli_cuda_moe_set_item_tokens(ColiCuda *ctx, int tokens) {
+  if (!ctx || (tokens != 0 && tokens != kMaxTokensPerItem && tokens != kWideTokens))
+    return fail_arg("coli_cuda_moe_set_item_tokens: %d (0 automatic, %d or %d)", tokens, kMaxTokensPerItem,
+                    kWideTokens);
+  ctx->moe_item_tokens = tokens;
   return 0;
 }
 

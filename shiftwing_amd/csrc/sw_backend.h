@@ -104,6 +104,7 @@ struct ColiCuda {
   unsigned long long moe_dec_calls = 0;
   int moe_generic_only = 0;  // single-token steps take the many-token kernels
   int moe_decode_mode = 0;   // 0 persistent stack kernel (default), 1 three-kernel decode
+  int moe_item_tokens = 0;   // many-token steps: tokens per expert item (0 automatic, 8, 16)
   // persistent stack kernel (moe_stack.hip): counters / integer sums in two
   // parity sets (the call state that selects them is device-side), the
   // device layer table, the abort status

@@ -149,3 +149,46 @@ def test_bucket_limit_follows_the_lds_map(be, oracle):
     d = be.alloc(1185 * K * 4)
     rc = be.lib.coli_cuda_moe_bucket(be.ctx, d.p, 1185, K, E, d.p, d.p, d.p)
     assert rc == -1 and "1184 tokens" in be.last_error(), be.last_error()
+
+
+ITEM_CASES = [
+    ("s35_T200", S35, 35, 200, None),
+    ("s397_zipf_B32", S397, 397, 32, "zipf"),
+    ("s397_T64", S397, 397, 64, None),
+    ("ragged_T64", (384, 32, 8, 257, 129, 4), 13, 64, None),
+    ("I1152_T50", (512, 16, 4, 1152, 128, 3), 11, 50, None),
+    ("H4224_T40", (4224, 16, 4, 256, 128, 4), 11, 40, None),
+]
+
+
+@pytest.mark.parametrize("items", [8, 16])
+@pytest.mark.parametrize("name,shape,seed,T,routing", ITEM_CASES, ids=[c[0] for c in ITEM_CASES])
+def test_item_kernels_vs_oracle(be, oracle, items, name, shape, seed, T, routing):
+    """Both routed-expert kernel families of the many-token step against
+    moe_prefill_grouped (c/qwen.c:4141-4206): items of 8 tokens (k split over
+    the waves) and of 16 tokens (one read of each tile per 16 tokens, digits
+    staged in LDS), forced through coli_cuda_moe_set_item_tokens.  Hot Zipf
+    experts span several 16-token items; ragged I, I > 1024 and H > 4096
+    cover the padding, more than 8 down groups and more than 32 hidden groups."""
+    from shiftwing_amd import zipf
+    H, E, K = shape[:3]
+    beta = zipf.calibrate_beta(H, E, K)[0] if routing == "zipf" else None
+    hl, L = _pair(be, oracle, shape, seed, 2, beta)
+    x = np.stack([oracle.synth_x(seed, 2, 500 + t, H) for t in range(T)])
+    if beta is not None:
+        x[:, H - 1] = 1.0
+    print(f"[item kernels] {name} items of {items}", flush=True)
+    be.check(be.lib.coli_cuda_moe_set_item_tokens(be.ctx, items), "set_item_tokens")
+    try:
+        want, tr = oracle.moe_prefill(hl, x, trace=True)
+        y, idx, w = L.forward_host(x)
+    finally:
+        be.check(be.lib.coli_cuda_moe_set_item_tokens(be.ctx, 0), "set_item_tokens")
+        L.close()
+    assert np.array_equal(idx, tr["idx"])
+    assert_close_rms(y, want, 1e-3, f"{name} items of {items}")
+
+
+def test_item_tokens_rejects_other_sizes(be):
+    assert be.lib.coli_cuda_moe_set_item_tokens(be.ctx, 12) == -1
+    assert "automatic" in be.last_error()
