@@ -475,14 +475,20 @@ def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_k
     be.check(lib.coli_cuda_timer_stop(be.ctx, C.byref(ms)))
     ms_per_step = ms.value / steps
     layers_per_step = 1 if prefill else nl
-    # routing of the timed steps (untimed): distinct experts per layer-step
+    # routing of the timed steps (untimed): distinct experts per layer-step,
+    # and how often the fp64 bounds left a token's top K to the exact chains
     di, dw = be.alloc(T * K * 4), be.alloc(T * K * 4)
     uniq = []
+    stats0 = [L.route_stats_full() for L in stack]
     for s in range(warmup, total):
         for l in ([s % nl] if prefill else range(nl)):
             be.check(lib.coli_cuda_moe_route(be.ctx, stack[l].h, x_at(l, s), T, di.p, dw.p), "route")
             uniq.append(len(np.unique(be.download(di, (T, K), np.int32))))
     U = float(np.mean(uniq))
+    stats1 = [L.route_stats_full() for L in stack]
+    routed = sum(b[0] - a[0] for a, b in zip(stats0, stats1))
+    unc = sum(b[1] - a[1] for a, b in zip(stats0, stats1))
+    full = sum(b[2] - a[2] for a, b in zip(stats0, stats1))
     names, nbytes, flops = stage_model(H, E, K, I, Ish, fmt, T, U)
     layer_bytes, layer_flops = sum(nbytes), sum(flops)
     # per-stage device times (HIP events between the step's kernels)
@@ -497,7 +503,8 @@ def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_k
     step_s = ms_per_step * 1e-3
     if calls.value:
         per = [sms[i] / calls.value for i in range(7)]
-        dom = max(range(7), key=lambda i: per[i])
+        # the roofline's kernel: the longer of the two HBM-bound expert stages
+        dom = max((names.index("routed_gateup"), names.index("down")), key=lambda i: per[i])
         kname, dom_bytes, dom_ms = f"stage {names[dom]}", nbytes[dom], per[dom]
     else:  # one token: the persistent decode kernel, one launch per step
         per = None
@@ -518,6 +525,7 @@ def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_k
                  "frac_int8_peak": round(2 * (flops[2] + flops[3] + flops[5]) * layers_per_step / step_s / 1e12
                                          / INT8_PEAK_TOPS, 5)},
         "step": {"distinct_experts_per_layer": round(U, 2), "algorithmic_bytes_per_layer": int(layer_bytes),
+                 "router_not_certified": f"{unc}/{routed} token-layers ({full} needed every chain)",
                  "effective_gbs": round(layer_bytes * layers_per_step / step_s / 1e9, 1),
                  "frac_of_peak": round(layer_bytes * layers_per_step / step_s / 1e9 / HBM_PEAK_GBS, 4),
                  "stage_us": {names[i]: round(per[i] * 1e3, 2) for i in range(7)} if per else None,

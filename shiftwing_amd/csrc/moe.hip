@@ -245,6 +245,7 @@ struct Work {
   signed char *xd1, *xd2; float4 *xgp;
   // router
   double2 *lb; float *sgate; int *certified; float *logits;
+  int *ulist, *ucount;  // tokens the bounds did not certify, and their count
   int *mset, *mcount;  // per token: experts of the targeted exact path (<= 64)
   int *idx; float *w;
   // bucket
@@ -273,6 +274,8 @@ size_t carve(Work &w, char *base) {
   w.lb = (double2 *)take((size_t)T * (w.E + 1) * 16);
   w.sgate = (float *)take((size_t)T * 4);
   w.certified = (int *)take((size_t)T * 4);
+  w.ulist = (int *)take((size_t)T * 4);
+  w.ucount = (int *)take(16);
   w.mset = (int *)take((size_t)T * 64 * 4);
   w.mcount = (int *)take((size_t)T * 4);
   w.logits = (float *)take((size_t)T * w.E * 4);
@@ -304,6 +307,7 @@ __global__ void k_prep_x(Work w, const float *x) {
   __shared__ float red[16];
   int t = blockIdx.x;
   const float *xt = x + (size_t)t * w.H;
+  if (t == 0 && threadIdx.x == 0) *w.ucount = 0;  // the certification appends to it
   float s = qrow_i8_block(xt, w.H, w.xq + (size_t)t * w.H, red);
   if (threadIdx.x == 0) w.sx[t] = s;
   quantize_digits(xt, w.H, w.ngh, w.xd1 + (size_t)t * w.Hp, w.xd2 + (size_t)t * w.Hp, w.xgp + (size_t)t * w.ngh);
@@ -685,6 +689,7 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
     }
     if (ok) ok = (lb[cand[w.K - 1]].x - lb[cand[w.K - 1]].y) - (mx + lb[cand[0]].y) > -80.0;
     w.certified[t] = ok ? 1 : 0;
+    if (!ok) w.ulist[atomicAdd(w.ucount, 1)] = t;
     if (ok) {
       double p[kMaxTopK], den = 0.0;
       for (int r = 0; r < w.K; r++) {
@@ -828,6 +833,7 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
   }
   if (lane == 0) {
     w.certified[t] = verdict;
+    if (verdict != 1) w.ulist[atomicAdd(w.ucount, 1)] = t;
     atomicAdd(&stats[0], 1ull);
     if (verdict != 1) atomicAdd(&stats[1], 1ull);
     if (verdict == 0) atomicAdd(&stats[2], 1ull);
@@ -859,41 +865,45 @@ __device__ float exact_chain(const float *xt, const float *row, int H) {
 // rn(x*w) are independent of the chain order: the block's lanes form them
 // with coalesced loads into LDS, then one lane runs the serial sum over LDS,
 // s = rn(s + p_i), and the fused tail.  Same result as exact_chain.
-// grid (64, T), 64 threads, dynamic LDS 4*H bytes.
+// Blocks walk the list of uncertain tokens (few: most launches find none).
+// grid (64, kUncertainSlots), 64 threads, dynamic LDS 4*H bytes.
 // ---------------------------------------------------------------------------
+constexpr int kUncertainSlots = 128;
 __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, const float *router) {
   extern __shared__ float prod[];
-  const int t = blockIdx.y;
-  const int c = w.certified[t];
-  if (c == 1) return;
-  const int n = c == 2 ? w.mcount[t] : w.E;
-  const float *xt = x + (size_t)t * w.H;
+  const int nu = *w.ucount;
   const int m = (w.H / 8) * 8;
-  for (int k = blockIdx.x; k < n; k += gridDim.x) {
-    const int e = c == 2 ? w.mset[(size_t)t * 64 + k] : k;
-    const float *row = router + (size_t)e * w.H;
-    for (int i = threadIdx.x * 4; i < m; i += 256) {
-      float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
-      *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
-                                          __fmul_rn(a.w, b.w));
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float s = 0.0f;
-      int i = 0;
-      // unrolled so that the LDS reads of 8 steps are issued ahead of their adds
-#pragma unroll 8
-      for (; i < m; i += 4) {
-        float4 p = *(const float4 *)(prod + i);
-        s = __fadd_rn(s, p.x);
-        s = __fadd_rn(s, p.y);
-        s = __fadd_rn(s, p.z);
-        s = __fadd_rn(s, p.w);
+  for (int ui = blockIdx.y; ui < nu; ui += gridDim.y) {
+    const int t = w.ulist[ui];
+    const int c = w.certified[t];
+    const int n = c == 2 ? w.mcount[t] : w.E;
+    const float *xt = x + (size_t)t * w.H;
+    for (int k = blockIdx.x; k < n; k += gridDim.x) {
+      const int e = c == 2 ? w.mset[(size_t)t * 64 + k] : k;
+      const float *row = router + (size_t)e * w.H;
+      for (int i = threadIdx.x * 4; i < m; i += 256) {
+        float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
+        *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
+                                            __fmul_rn(a.w, b.w));
       }
-      for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
-      w.logits[(size_t)t * w.E + e] = s;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float s = 0.0f;
+        int i = 0;
+        // unrolled so that the LDS reads of 8 steps are issued ahead of their adds
+#pragma unroll 8
+        for (; i < m; i += 4) {
+          float4 p = *(const float4 *)(prod + i);
+          s = __fadd_rn(s, p.x);
+          s = __fadd_rn(s, p.y);
+          s = __fadd_rn(s, p.z);
+          s = __fadd_rn(s, p.w);
+        }
+        for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+        w.logits[(size_t)t * w.E + e] = s;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -956,13 +966,10 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
 // come from the fp64 logits as for certified tokens.  Otherwise, and for
 // tokens on the full path, every chain and the router_topk replica.
 // grid T, 512 threads.
-__global__ void k_topk_exact(Work w, const float *x, const float *router, unsigned long long *stats) {
-  __shared__ VI red[16];
-  __shared__ float prob[4096];
+__device__ void topk_exact_token(Work &w, int t, const float *x, const float *router, unsigned long long *stats,
+                                 VI *red, float *prob) {
   __shared__ int s_ok;
-  int t = blockIdx.x;
   const int c = w.certified[t];
-  if (c == 1) return;
   if (c == 2) {
     __shared__ int um[64], sm[64];
     __shared__ float ul[64], sl[64];
@@ -1011,6 +1018,18 @@ __global__ void k_topk_exact(Work w, const float *x, const float *router, unsign
   }
   topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
                    prob, red);
+}
+
+// Blocks walk the list of uncertain tokens.  grid kTopkSlots, 512 threads.
+constexpr int kTopkSlots = 128;
+__global__ void k_topk_exact(Work w, const float *x, const float *router, unsigned long long *stats) {
+  __shared__ VI red[16];
+  __shared__ float prob[4096];
+  const int nu = *w.ucount;
+  for (int ui = blockIdx.x; ui < nu; ui += gridDim.x) {
+    topk_exact_token(w, w.ulist[ui], x, router, stats, red, prob);
+    __syncthreads();  // the token's LDS is read no more
+  }
 }
 
 __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx, float *weight) {
@@ -1639,93 +1658,112 @@ __global__ __launch_bounds__(512) void k_down_split(Work w, ExpertLayout xl, int
 
 // ---------------------------------------------------------------------------
 // 7w / 8w.  Wide items, for many-token steps with several tokens per expert:
-// an item holds up to kWideTokens tokens of one expert, so every weight tile
-// of the expert is read once per kWideTokens tokens instead of once per 8.
-// The item's activation digits are staged in LDS in the MFMA B-operand order
-// of mt_digits (chunk j = tokens 8j..8j+7); waves own row tiles and walk
-// every group, a batch of groups' tiles in flight while the previous batch
-// multiplies, and each tile feeds 2 MFMAs per chunk.  A wave's dot over the
-// groups is one accumulation in group order (no cross-wave sums).
+// an item holds up to kWideTokens = 16 tokens of one expert, so every weight
+// tile of the expert is read once per 16 tokens instead of once per 8.  The
+// MFMA's 16 B columns are the item's 16 tokens, one digit plane per MFMA
+// pair: c_d = sum code * digit_d (codes unsigned, exact int32), and a row's
+// group value is A c_1 + B c_2 - K with K = OFF (A Q_1 + B Q_2) staged per
+// (group, token) (Q_d: the token's digit sums, A and B its digit scales), so
+// no lane is spent on the digit combination.  The item's digits and (A, B,
+// K) are staged in LDS in the B-operand order; waves own row tiles and walk
+// every group, a ring of groups' tiles in flight while one multiplies.  A
+// wave's dot over the groups is one accumulation in group order.
 // grid (row-tile blocks, item slots), 512 threads, dynamic LDS wide_lds_bytes.
 // ---------------------------------------------------------------------------
-constexpr int kWideChunks = 2;                // 8-token column chunks per item
-constexpr int kWideTokens = 8 * kWideChunks;  // tokens per item
-// row tiles per wave and groups per load batch (a wave holds two batches):
-// gate/up 1 row tile of both matrices x 2 groups, down 4 row tiles x 1 group
-constexpr int kWideRt = 1, kWideGuBatch = 2;
-constexpr int kWideDnRt = 4, kWideDnBatch = 1;
+constexpr int kWideTokens = 16;  // tokens per item (the MFMA's B columns)
+// Row tiles per wave and groups in flight (the tile ring's slots): gate/up
+// 1 row tile of both matrices x 2 groups, down 2 row tiles x 1 group; with
+// the digits staged at most SW_WIDE_LDS_KB at a time, two 8-wave blocks share
+// a compute unit.  Measured at S397 and S35 (512-token prefill): more waves a
+// compute unit beat deeper rings.
+#ifndef SW_WIDE_GU_RING
+#define SW_WIDE_GU_RING 2
+#endif
+#ifndef SW_WIDE_DN_RING
+#define SW_WIDE_DN_RING 1
+#endif
+#ifndef SW_WIDE_WAVES
+#define SW_WIDE_WAVES 8
+#endif
+constexpr int kWideWaves = SW_WIDE_WAVES;  // waves per block
+constexpr int kWideRt = 1, kWideGuBatch = SW_WIDE_GU_RING;
+constexpr int kWideDnRt = 2, kWideDnBatch = SW_WIDE_DN_RING;
 
-// LDS of one item over ng groups: digits [chunk][group][half][lane] 16 B,
-// then the digit parameters [chunk][group][column] (scale, digit sum)
-__host__ __device__ inline size_t wide_lds_bytes(int ng) { return (size_t)kWideChunks * ng * (2 * 1024 + 16 * 8); }
+// LDS of one item over ng groups: digits [group][plane][half][lane] 16 B,
+// then (A, B, K, 0) per [group][token]
+__host__ __device__ inline size_t wide_lds_bytes(int ng) { return (size_t)ng * (4 * 1024 + 16 * 16); }
 
 // Stage an item's digits.  Token tt of the item is row rows_of[p0+tt] of the
-// digit planes (rows_of null: row p0+tt); tokens past cnt stage zeros.
-__device__ void wide_stage(unsigned char *lds, int ng, int ld, const signed char *d1, const signed char *d2,
-                           const float4 *gp, const int *rows_of, int p0, int cnt) {
-  const int nunits = kWideChunks * ng * 128;
-  for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
-    const int l = u & 63, h = (u >> 6) & 1, jg = u >> 7;
-    const int j = jg / ng, g = jg - j * ng;
-    const int tt = 8 * j + ((l & 15) >> 1);
-    v4i v = {0, 0, 0, 0};
-    if (tt < cnt) {
-      const int row = rows_of ? rows_of[p0 + tt] : p0 + tt;
-      v = *(const v4i *)(((l & 1) ? d2 : d1) + (size_t)row * ld + g * kGroup + h * 64 + (l >> 4) * 16);
+// digit planes (rows_of null: row p0+tt); tokens past cnt stage zeros.  Lane
+// l of unit (g, plane d, half h) holds token l % 16's digits d at k = 128 g
+// + 64 h + 16 (l >> 4): a thread's token is the same for every unit it
+// stages (blockDim.x % 64 == 0), so its row is looked up once, and four
+// units' loads are issued before their stores.
+__device__ void wide_stage(unsigned char *lds, int hg, int g0, int gn, int ng, int ld, const signed char *d1,
+                           const signed char *d2, const float4 *gp, const int *rows_of, int p0, int cnt, float off) {
+  const int l = threadIdx.x & 63, tok = l & 15;
+  const bool live = tok < cnt;
+  const int row = live ? (rows_of ? rows_of[p0 + tok] : p0 + tok) : 0;
+  const int nunits = gn * 256;
+  for (int u0 = threadIdx.x; u0 < nunits; u0 += 4 * blockDim.x) {
+    v4i v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int u = u0 + q * blockDim.x;
+      const int h = (u >> 6) & 1, d = (u >> 7) & 1, g = g0 + (u >> 8);
+      v[q] = v4i{0, 0, 0, 0};
+      if (u < nunits && live)
+        v[q] = *(const v4i *)((d ? d2 : d1) + (size_t)row * ld + g * kGroup + h * 64 + (l >> 4) * 16);
     }
-    *(v4i *)(lds + (size_t)u * 16) = v;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int u = u0 + q * blockDim.x;
+      if (u < nunits) *(v4i *)(lds + (size_t)u * 16) = v[q];
+    }
   }
-  float2 *P = (float2 *)(lds + (size_t)kWideChunks * ng * 2048);
-  for (int v = threadIdx.x; v < kWideChunks * ng * 16; v += blockDim.x) {
-    const int c = v & 15, jg = v >> 4, j = jg / ng, g = jg - j * ng;
-    const int tt = 8 * j + (c >> 1);
-    float2 pv = make_float2(0.0f, 0.0f);
-    if (tt < cnt) {
-      const int row = rows_of ? rows_of[p0 + tt] : p0 + tt;
-      const float4 q = gp[(size_t)row * ng + g];
-      pv = (c & 1) ? make_float2(q.y, q.w) : make_float2(q.x, q.z);
+  float4 *P = (float4 *)(lds + (size_t)hg * 4096);
+  for (int v = threadIdx.x; v < gn * 16; v += blockDim.x) {
+    const int t = v & 15, g = g0 + (v >> 4);
+    float4 pv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < cnt) {
+      const int r = rows_of ? rows_of[p0 + t] : p0 + t;
+      const float4 q = gp[(size_t)r * ng + g];  // A, B, Q1, Q2
+      const float k = off * (q.x * (float)__float_as_int(q.z) + q.y * (float)__float_as_int(q.w));
+      pv = make_float4(q.x, q.y, k, 0.0f);
     }
     P[v] = pv;
   }
 }
 
 struct WideDigits {
-  v4i b0[kWideChunks], b1[kWideChunks];
-  float dsc[kWideChunks];
-  int Q[kWideChunks];
+  v4i b[2][2];  // [plane][half]
+  float A, B, K;
 };
-__device__ __forceinline__ void wide_digits(WideDigits &d, const unsigned char *lds, int ng, int g, int lane) {
+__device__ __forceinline__ void wide_digits(WideDigits &d, const unsigned char *lds, int hg, int g, int lane) {
   const v4i *D = (const v4i *)lds;
-  const float2 *P = (const float2 *)(lds + (size_t)kWideChunks * ng * 2048);
 #pragma unroll
-  for (int j = 0; j < kWideChunks; j++) {
-    d.b0[j] = D[((j * ng + g) * 2 + 0) * 64 + lane];
-    d.b1[j] = D[((j * ng + g) * 2 + 1) * 64 + lane];
-    const float2 p = P[(j * ng + g) * 16 + (lane & 15)];
-    d.dsc[j] = p.x;
-    d.Q[j] = __float_as_int(p.y);
-  }
+  for (int q = 0; q < 4; q++) d.b[q >> 1][q & 1] = D[(g * 4 + q) * 64 + lane];
+  const float4 p = ((const float4 *)(lds + (size_t)hg * 4096))[g * 16 + (lane & 15)];
+  d.A = p.x;
+  d.B = p.y;
+  d.K = p.z;
 }
 
-// one tile (codes unpacked to a0/a1, row scales sc) times every chunk
+// one tile (codes, row scales sc) into acc: rows 4 (lane >> 4) + r, token lane % 16
 template <int FMT>
-__device__ __forceinline__ void wide_mac(const uint32_t *q, const float4 sc, const WideDigits &d,
-                                         float acc[kWideChunks][4]) {
-  constexpr int OFF = FMT == 4 ? 8 : 4;
+__device__ __forceinline__ void wide_mac(const uint32_t *q, const float4 sc, const WideDigits &d, float acc[4]) {
   v4i a0, a1;
   unpack_words<FMT>(q, a0, a1);
+  v4i c1 = {0, 0, 0, 0}, c2 = {0, 0, 0, 0};
+  c1 = mfma_i8(a0, d.b[0][0], c1);
+  c2 = mfma_i8(a0, d.b[1][0], c2);
+  c1 = mfma_i8(a1, d.b[0][1], c1);
+  c2 = mfma_i8(a1, d.b[1][1], c2);
   const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-  for (int j = 0; j < kWideChunks; j++) {
-    v4i c = {0, 0, 0, 0};
-    c = mfma_i8(a0, d.b0[j], c);
-    c = mfma_i8(a1, d.b1[j], c);
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float f = (float)(c[r] - OFF * d.Q[j]) * d.dsc[j];
-      const float tsum = f + dpp_row_shr1(f);
-      acc[j][r] = __builtin_fmaf(tsum, scv[r], acc[j][r]);
-    }
+  for (int r = 0; r < 4; r++) {
+    const float f = __builtin_fmaf(d.A, (float)c1[r], __builtin_fmaf(d.B, (float)c2[r], -d.K));
+    acc[r] = __builtin_fmaf(f, scv[r], acc[r]);
   }
 }
 
@@ -1735,113 +1773,126 @@ struct WideTiles {
   float4 sc[NB][NR][NM];
 };
 
-// tiles of groups [gb, gb + NB) for row tiles [rt0, rt0 + NR) of the NM
-// matrices (mats[m]); row tiles past nrt and groups past ng are skipped
+// Slot i of the tile ring holds one group's tiles for row tiles [rt0, rt0 +
+// NR) of the NM matrices (mats[m]); row tiles past nrt are skipped.
 template <int FMT, int NB, int NR, int NM>
-__device__ __forceinline__ void wide_load(WideTiles<FMT, NB, NR, NM> &t, const TileMat *mats, int rt0, int nrt,
-                                          int ng, int gb, int lane) {
+__device__ __forceinline__ void wide_load_slot(WideTiles<FMT, NB, NR, NM> &t, int i, const TileMat *mats, int rt0,
+                                               int nrt, int ng, int g, int lane) {
   constexpr int BPL = FMT == 4 ? 16 : 12;
   const int kb = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < NB; i++)
+  for (int rr = 0; rr < NR; rr++)
 #pragma unroll
-    for (int rr = 0; rr < NR; rr++)
-#pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const int g = gb + i, rt = rt0 + rr;
-        if (g < ng && rt < nrt) {
-          const size_t tg = (size_t)rt * ng + g;
-          load_words<FMT>(tm_codes(mats[m], tg) + lane * BPL, t.q[i][rr][m]);
-          t.sc[i][rr][m] = *(const float4 *)(tm_scales(mats[m], tg) + 4 * kb);
-        }
+    for (int m = 0; m < NM; m++) {
+      const int rt = rt0 + rr;
+      if (rt < nrt) {
+        const size_t tg = (size_t)rt * ng + g;
+        load_words<FMT>(tm_codes(mats[m], tg) + lane * BPL, t.q[i][rr][m]);
+        t.sc[i][rr][m] = *(const float4 *)(tm_scales(mats[m], tg) + 4 * kb);
       }
+    }
 }
 
-template <int FMT, int NB, int NR, int NM>
-__device__ __forceinline__ void wide_compute(const WideTiles<FMT, NB, NR, NM> &t, const unsigned char *lds, int rt0,
-                                             int nrt, int ng, int gb, int lane,
-                                             float acc[NR][NM][kWideChunks][4]) {
+// Every group of row tiles [rt0, rt0 + NR) through a ring of NB slots: group
+// g's tiles are loaded NB groups ahead, into the slot group g - NB has just
+// left, so NB groups' tiles are in flight while one multiplies.  The item's
+// digits are staged hg groups at a time (hg % NB == 0) between block
+// barriers; the ring's loads run on across them.  Waves without row tiles
+// (active false) take part in the staging and the barriers only.
+template <int FMT, int NB, int NR, int NM, class Stage>
+__device__ __forceinline__ void wide_rows(const TileMat *mats, const unsigned char *lds, int hg, int rt0, int nrt,
+                                          int ng, bool active, int lane, float acc[NR][NM][4], Stage stage) {
+  WideTiles<FMT, NB, NR, NM> t;
+  if (active) {
 #pragma unroll
-  for (int i = 0; i < NB; i++) {
-    const int g = gb + i;
-    if (g >= ng) break;
-    WideDigits d;
-    wide_digits(d, lds, ng, g, lane);
+    for (int i = 0; i < NB; i++)
+      if (i < ng) wide_load_slot<FMT, NB, NR, NM>(t, i, mats, rt0, nrt, ng, i, lane);
+  }
+  for (int g0 = 0; g0 < ng; g0 += hg) {
+    const int g1 = min(ng, g0 + hg);
+    __syncthreads();  // every wave is done with the previous digits
+    stage(g0, g1 - g0);
+    __syncthreads();
+    if (!active) continue;
+    for (int gb = g0; gb < g1; gb += NB) {
 #pragma unroll
-    for (int rr = 0; rr < NR; rr++)
-      if (rt0 + rr < nrt)
+      for (int i = 0; i < NB; i++) {
+        const int g = gb + i;
+        if (g >= g1) break;
+        WideDigits d;
+        wide_digits(d, lds, hg, g - g0, lane);
 #pragma unroll
-        for (int m = 0; m < NM; m++) wide_mac<FMT>(t.q[i][rr][m], t.sc[i][rr][m], d, acc[rr][m]);
+        for (int rr = 0; rr < NR; rr++)
+          if (rt0 + rr < nrt)
+#pragma unroll
+            for (int m = 0; m < NM; m++) wide_mac<FMT>(t.q[i][rr][m], t.sc[i][rr][m], d, acc[rr][m]);
+        if (g + NB < ng) wide_load_slot<FMT, NB, NR, NM>(t, i, mats, rt0, nrt, ng, g + NB, lane);
+      }
+    }
   }
 }
 
-// the groups of row tiles [rt0, rt0 + NR): two tile buffers, the next batch
-// loading while the current one multiplies
-template <int FMT, int NB, int NR, int NM>
-__device__ __forceinline__ void wide_rows(const TileMat *mats, const unsigned char *lds, int rt0, int nrt, int ng,
-                                          int lane, float acc[NR][NM][kWideChunks][4]) {
-  WideTiles<FMT, NB, NR, NM> ta, tb;
-  wide_load<FMT, NB, NR, NM>(ta, mats, rt0, nrt, ng, 0, lane);
-  for (int gb = 0; gb < ng; gb += 2 * NB) {
-    if (gb + NB < ng) wide_load<FMT, NB, NR, NM>(tb, mats, rt0, nrt, ng, gb + NB, lane);
-    wide_compute<FMT, NB, NR, NM>(ta, lds, rt0, nrt, ng, gb, lane, acc);
-    if (gb + NB >= ng) break;
-    if (gb + 2 * NB < ng) wide_load<FMT, NB, NR, NM>(ta, mats, rt0, nrt, ng, gb + 2 * NB, lane);
-    wide_compute<FMT, NB, NR, NM>(tb, lds, rt0, nrt, ng, gb + NB, lane, acc);
-  }
+// Groups per staging round for ng groups: the fewest rounds whose LDS fits a
+// compute unit, rounded up to the ring's slot count.
+#ifndef SW_WIDE_LDS_KB
+#define SW_WIDE_LDS_KB 76
+#endif
+__host__ __device__ inline int wide_stage_groups(int ng, int nb) {
+  const size_t cap = SW_WIDE_LDS_KB * 1024;
+  int parts = (int)(((size_t)ng * 4352 + cap - 1) / cap);
+  if (parts < 1) parts = 1;
+  const int hg = (ng + parts - 1) / parts;
+  return (hg + nb - 1) / nb * nb;
 }
 
-// routed gate/up of wide items: h = silu(g)*u.  Block: 8 waves x kWideRt row
-// tiles of I; grid (ceil(I/16 / (8 kWideRt)), item slots).
+// routed gate/up of wide items: h = silu(g)*u.  Block: kWideWaves waves x
+// kWideRt row tiles of I; grid (ceil(I/16 / (kWideWaves kWideRt)), item
+// slots), dynamic LDS wide_lds_bytes(hg).
 template <int FMT>
-__global__ __launch_bounds__(512) void k_gateup_wide(Work w, ExpertLayout xl) {
+__global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertLayout xl, int hg) {
   extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.I / kTileRows;
-  const int rt0 = (blockIdx.x * 8 + wave) * kWideRt;
+  const int rt0 = (blockIdx.x * kWideWaves + wave) * kWideRt;
   const int n_items = *w.nitems;
   for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
     const int4 item = w.items[it];
     const int e = item.x, p0 = item.y, cnt = item.z;
-    __syncthreads();  // the previous item's digits are read no more
-    wide_stage(wlds, w.ngh, w.Hp, w.xd1, w.xd2, w.xgp, w.btok, p0, cnt);
-    __syncthreads();
-    if (rt0 >= nrt) continue;
     const TileMat mats[2] = {xl.mat(e, 0), xl.mat(e, 1)};
-    float acc[kWideRt][2][kWideChunks][4] = {};
-    wide_rows<FMT, kWideGuBatch, kWideRt, 2>(mats, wlds, rt0, nrt, w.ngh, lane, acc);
-    if (lane & 1) {
+    float acc[kWideRt][2][4] = {};
+    wide_rows<FMT, kWideGuBatch, kWideRt, 2>(
+        mats, wlds, hg, rt0, nrt, w.ngh, rt0 < nrt, lane, acc, [&](int g0, int gn) {
+          wide_stage(wlds, hg, g0, gn, w.ngh, w.Hp, w.xd1, w.xd2, w.xgp, w.btok, p0, cnt, FMT == 4 ? 8.0f : 4.0f);
+        });
+    const int tt = lane & 15;
+    if (tt < cnt && rt0 < nrt) {
 #pragma unroll
-      for (int j = 0; j < kWideChunks; j++) {
-        const int tt = 8 * j + ((lane & 15) >> 1);
-        if (tt >= cnt) continue;
+      for (int rr = 0; rr < kWideRt; rr++) {
+        const int rt = rt0 + rr;
+        if (rt >= nrt) continue;
 #pragma unroll
-        for (int rr = 0; rr < kWideRt; rr++) {
-          const int rt = rt0 + rr;
-          if (rt >= nrt) continue;
-#pragma unroll
-          for (int r = 0; r < 4; r++)
-            w.hroute[(size_t)(p0 + tt) * w.I + rt * kTileRows + 4 * kb + r] =
-                silu_ref(acc[rr][0][j][r]) * acc[rr][1][j][r];
-        }
+        for (int r = 0; r < 4; r++)
+          w.hroute[(size_t)(p0 + tt) * w.I + rt * kTileRows + 4 * kb + r] = silu_ref(acc[rr][0][r]) * acc[rr][1][r];
       }
     }
   }
 }
 
 // routed down of wide items, plus the shared expert's token chunks (IDOT) in
-// the extra blocks y >= item_slots.  Block: 8 waves x kWideDnRt row tiles of H.
+// the extra blocks y >= item_slots.  Block: kWideWaves waves x kWideDnRt row
+// tiles of H; grid (ceil(H/16 / (kWideWaves kWideDnRt)), item slots +
+// shared chunks).
 template <int FMT>
-__global__ __launch_bounds__(512) void k_down_wide(Work w, ExpertLayout xl, int item_slots, const signed char *dq,
-                                                   const float *ds) {
+__global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLayout xl, int item_slots,
+                                                               const signed char *dq, const float *ds, int hg) {
   extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.H / kTileRows;
-  const int rtb = blockIdx.x * 8 * kWideDnRt;
+  const int rtb = blockIdx.x * kWideWaves * kWideDnRt;
   if ((int)blockIdx.y >= item_slots) {
-    const int rt1 = min(nrt, rtb + 8 * kWideDnRt);
+    const int rt1 = min(nrt, rtb + kWideWaves * kWideDnRt);
     const int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens, tok = t0 + (lane & 15);
-    for (int rt = rtb + wave; rt < rt1; rt += 8) {
+    for (int rt = rtb + wave; rt < rt1; rt += kWideWaves) {
       v4i c = {0, 0, 0, 0};
       idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
       if (tok < w.T) {
@@ -1859,26 +1910,20 @@ __global__ __launch_bounds__(512) void k_down_wide(Work w, ExpertLayout xl, int 
   for (int it = blockIdx.y; it < n_items; it += item_slots) {
     const int4 item = w.items[it];
     const int e = item.x, p0 = item.y, cnt = item.z;
-    __syncthreads();
-    wide_stage(wlds, w.ngi, w.Ip, w.hd1, w.hd2, w.hgp, nullptr, p0, cnt);
-    __syncthreads();
-    if (rt0 >= nrt) continue;
     const TileMat mats[1] = {xl.mat(e, 2)};
-    float acc[kWideDnRt][1][kWideChunks][4] = {};
-    wide_rows<FMT, kWideDnBatch, kWideDnRt, 1>(mats, wlds, rt0, nrt, w.ngi, lane, acc);
-    if (lane & 1) {
+    float acc[kWideDnRt][1][4] = {};
+    wide_rows<FMT, kWideDnBatch, kWideDnRt, 1>(
+        mats, wlds, hg, rt0, nrt, w.ngi, rt0 < nrt, lane, acc, [&](int g0, int gn) {
+          wide_stage(wlds, hg, g0, gn, w.ngi, w.Ip, w.hd1, w.hd2, w.hgp, nullptr, p0, cnt, FMT == 4 ? 8.0f : 4.0f);
+        });
+    const int tt = lane & 15;
+    if (tt < cnt && rt0 < nrt) {
 #pragma unroll
-      for (int j = 0; j < kWideChunks; j++) {
-        const int tt = 8 * j + ((lane & 15) >> 1);
-        if (tt >= cnt) continue;
+      for (int rr = 0; rr < kWideDnRt; rr++) {
+        const int rt = rt0 + rr;
+        if (rt >= nrt) continue;
 #pragma unroll
-        for (int rr = 0; rr < kWideDnRt; rr++) {
-          const int rt = rt0 + rr;
-          if (rt >= nrt) continue;
-#pragma unroll
-          for (int r = 0; r < 4; r++)
-            w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + r] = acc[rr][0][j][r];
-        }
+        for (int r = 0; r < 4; r++) w.rout[(size_t)(p0 + tt) * w.H + rt * kTileRows + 4 * kb + r] = acc[rr][0][r];
       }
     }
   }
@@ -2191,8 +2236,9 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   else
     k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
   if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
-  k_exact_logits<<<dim3(64, w.T), 64, (size_t)w.H * 4, st>>>(w, x, L->router);
-  k_topk_exact<<<w.T, 512, 0, st>>>(w, x, L->router, L->stats);
+  k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(w, x,
+                                                                                                      L->router);
+  k_topk_exact<<<w.T < kTopkSlots ? w.T : kTopkSlots, 512, 0, st>>>(w, x, L->router, L->stats);
   return launch_status("MoE routing kernels");
 }
 
@@ -2202,7 +2248,8 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
 // setting (coli_cuda_moe_set_item_tokens) can force either.
 static int item_tokens(const ColiCuda *ctx, const ColiMoeLayer *L, int T) {
   const int mode = ctx->moe_item_tokens;
-  const bool fits = wide_lds_bytes(L->ngh) <= 160 * 1024 && wide_lds_bytes(L->ngi) <= 160 * 1024;
+  const bool fits = wide_lds_bytes(wide_stage_groups(L->ngh, kWideGuBatch)) <= 160 * 1024 &&
+                    wide_lds_bytes(wide_stage_groups(L->ngi, kWideDnBatch)) <= 160 * 1024;
   const bool want = mode == kWideTokens || (mode == 0 && T * L->sh.topk >= 2 * L->sh.experts);
   return want && fits && mode != kMaxTokensPerItem ? kWideTokens : kMaxTokensPerItem;
 }
@@ -2306,14 +2353,15 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   const bool fmt4 = L->sh.expert_format == 4;
   const bool wide_items = w.itok > kMaxTokensPerItem;
   if (wide_items) {
-    const size_t lg = wide_lds_bytes(w.ngh);
+    const int hg = wide_stage_groups(w.ngh, kWideGuBatch);
+    const size_t lg = wide_lds_bytes(hg);
     const void *fn = fmt4 ? (const void *)k_gateup_wide<4> : (const void *)k_gateup_wide<3>;
     if (set_lds(fn, lg)) return -1;
-    const dim3 grid((w.I / kTileRows + 8 * kWideRt - 1) / (8 * kWideRt), slots);
+    const dim3 grid((w.I / kTileRows + kWideWaves * kWideRt - 1) / (kWideWaves * kWideRt), slots);
     if (fmt4)
-      k_gateup_wide<4><<<grid, 512, lg, st>>>(w, L->xl);
+      k_gateup_wide<4><<<grid, 64 * kWideWaves, lg, st>>>(w, L->xl, hg);
     else
-      k_gateup_wide<3><<<grid, 512, lg, st>>>(w, L->xl);
+      k_gateup_wide<3><<<grid, 64 * kWideWaves, lg, st>>>(w, L->xl, hg);
   } else {
     const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
     const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
@@ -2334,14 +2382,15 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   const bool dn_split = w.ngi <= 8;
   const int ds_blocks_x = (w.H / kTileRows + kDnBlockRows - 1) / kDnBlockRows;
   if (wide_items) {
-    const size_t ld = wide_lds_bytes(w.ngi);
+    const int hg = wide_stage_groups(w.ngi, kWideDnBatch);
+    const size_t ld = wide_lds_bytes(hg);
     const void *fn = fmt4 ? (const void *)k_down_wide<4> : (const void *)k_down_wide<3>;
     if (set_lds(fn, ld)) return -1;
-    const dim3 grid((w.H / kTileRows + 8 * kWideDnRt - 1) / (8 * kWideDnRt), slots + sh_chunks);
+    const dim3 grid((w.H / kTileRows + kWideWaves * kWideDnRt - 1) / (kWideWaves * kWideDnRt), slots + sh_chunks);
     if (fmt4)
-      k_down_wide<4><<<grid, 512, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+      k_down_wide<4><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds, hg);
     else
-      k_down_wide<3><<<grid, 512, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
+      k_down_wide<3><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds, hg);
   } else if (fmt4) {
     dn_split ? k_down_split<4><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
