@@ -245,7 +245,8 @@ struct Work {
   signed char *xd1, *xd2; float4 *xgp;
   // router
   double2 *lb; float *sgate; int *certified; float *logits;
-  int *ulist, *ucount;  // tokens the bounds did not certify, and their count
+  int *ulist, *ucount;  // tokens on the targeted exact path, and their count
+  int *flist, *fcount;  // tokens needing every expert's chain and the router_topk replica
   int *mset, *mcount;  // per token: experts of the targeted exact path (<= 64)
   int *idx; float *w;
   // bucket
@@ -276,6 +277,8 @@ size_t carve(Work &w, char *base) {
   w.certified = (int *)take((size_t)T * 4);
   w.ulist = (int *)take((size_t)T * 4);
   w.ucount = (int *)take(16);
+  w.flist = (int *)take((size_t)T * 4);
+  w.fcount = (int *)take(16);
   w.mset = (int *)take((size_t)T * 64 * 4);
   w.mcount = (int *)take((size_t)T * 4);
   w.logits = (float *)take((size_t)T * w.E * 4);
@@ -307,7 +310,7 @@ __global__ void k_prep_x(Work w, const float *x) {
   __shared__ float red[16];
   int t = blockIdx.x;
   const float *xt = x + (size_t)t * w.H;
-  if (t == 0 && threadIdx.x == 0) *w.ucount = 0;  // the certification appends to it
+  if (t == 0 && threadIdx.x == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
   float s = qrow_i8_block(xt, w.H, w.xq + (size_t)t * w.H, red);
   if (threadIdx.x == 0) w.sx[t] = s;
   quantize_digits(xt, w.H, w.ngh, w.xd1 + (size_t)t * w.Hp, w.xd2 + (size_t)t * w.Hp, w.xgp + (size_t)t * w.ngh);
@@ -689,7 +692,7 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
     }
     if (ok) ok = (lb[cand[w.K - 1]].x - lb[cand[w.K - 1]].y) - (mx + lb[cand[0]].y) > -80.0;
     w.certified[t] = ok ? 1 : 0;
-    if (!ok) w.ulist[atomicAdd(w.ucount, 1)] = t;
+    if (!ok) w.flist[atomicAdd(w.fcount, 1)] = t;
     if (ok) {
       double p[kMaxTopK], den = 0.0;
       for (int r = 0; r < w.K; r++) {
@@ -833,7 +836,8 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
   }
   if (lane == 0) {
     w.certified[t] = verdict;
-    if (verdict != 1) w.ulist[atomicAdd(w.ucount, 1)] = t;
+    if (verdict == 2) w.ulist[atomicAdd(w.ucount, 1)] = t;
+    if (verdict == 0) w.flist[atomicAdd(w.fcount, 1)] = t;
     atomicAdd(&stats[0], 1ull);
     if (verdict != 1) atomicAdd(&stats[1], 1ull);
     if (verdict == 0) atomicAdd(&stats[2], 1ull);
@@ -875,11 +879,10 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
   const int m = (w.H / 8) * 8;
   for (int ui = blockIdx.y; ui < nu; ui += gridDim.y) {
     const int t = w.ulist[ui];
-    const int c = w.certified[t];
-    const int n = c == 2 ? w.mcount[t] : w.E;
+    const int n = w.mcount[t];
     const float *xt = x + (size_t)t * w.H;
     for (int k = blockIdx.x; k < n; k += gridDim.x) {
-      const int e = c == 2 ? w.mset[(size_t)t * 64 + k] : k;
+      const int e = w.mset[(size_t)t * 64 + k];
       const float *row = router + (size_t)e * w.H;
       for (int i = threadIdx.x * 4; i < m; i += 256) {
         float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
@@ -963,17 +966,17 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
 // the order and the k|k+1 boundary hold if consecutive exact logits are
 // separated by the margin and the K-th lies within 80 of the max (experts
 // outside M are below every candidate by more than the margin).  Weights then
-// come from the fp64 logits as for certified tokens.  Otherwise, and for
-// tokens on the full path, every chain and the router_topk replica.
-// grid T, 512 threads.
-__device__ void topk_exact_token(Work &w, int t, const float *x, const float *router, unsigned long long *stats,
-                                 VI *red, float *prob) {
-  __shared__ int s_ok;
-  const int c = w.certified[t];
-  if (c == 2) {
-    __shared__ int um[64], sm[64];
-    __shared__ float ul[64], sl[64];
-    const int n = w.mcount[t], i = threadIdx.x;
+// come from the fp64 logits as for certified tokens.  Otherwise the token
+// joins the full path (every chain and the router_topk replica).
+// grid kTopkSlots, 64 threads; blocks walk the targeted list.
+constexpr int kTopkSlots = 128;
+__global__ __launch_bounds__(64) void k_topk_check(Work w, unsigned long long *stats) {
+  __shared__ int um[64], sm[64];
+  __shared__ float ul[64], sl[64];
+  const int nu = *w.ucount, i = threadIdx.x;
+  for (int ui = blockIdx.x; ui < nu; ui += gridDim.x) {
+    const int t = w.ulist[ui];
+    const int n = w.mcount[t];
     if (i < n) {
       um[i] = w.mset[(size_t)t * 64 + i];
       ul[i] = w.logits[(size_t)t * w.E + um[i]];
@@ -988,7 +991,7 @@ __device__ void topk_exact_token(Work &w, int t, const float *x, const float *ro
       sl[rank] = l;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (i == 0) {
       const double mx = sl[0];
       bool ok = n >= w.K;
       for (int r = 0; ok && r < w.K && r + 1 < n; r++) {
@@ -1007,28 +1010,63 @@ __device__ void topk_exact_token(Work &w, int t, const float *x, const float *ro
         }
       } else {
         atomicAdd(&stats[2], 1ull);
+        w.certified[t] = 0;
+        w.flist[atomicAdd(w.fcount, 1)] = t;
       }
-      s_ok = ok;
     }
-    __syncthreads();
-    if (s_ok) return;
-    for (int e = threadIdx.x; e < w.E; e += blockDim.x)
-      w.logits[(size_t)t * w.E + e] = exact_chain(x + (size_t)t * w.H, router + (size_t)e * w.H, w.H);
-    __syncthreads();
+    __syncthreads();  // the token's LDS is read no more
   }
-  topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
-                   prob, red);
 }
 
-// Blocks walk the list of uncertain tokens.  grid kTopkSlots, 512 threads.
-constexpr int kTopkSlots = 128;
-__global__ void k_topk_exact(Work w, const float *x, const float *router, unsigned long long *stats) {
+// Every expert's exact logit for the tokens on the full path: one block an
+// (expert, token) pair, the products formed with coalesced loads into LDS and
+// summed serially by one lane as in k_exact_logits.
+// grid (min(E, 1024), kFullSlots), 64 threads, dynamic LDS 4*H bytes.
+constexpr int kFullSlots = 8;
+__global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const float *router) {
+  extern __shared__ float prod[];
+  const int nf = *w.fcount;
+  const int m = (w.H / 8) * 8;
+  for (int fi = blockIdx.y; fi < nf; fi += gridDim.y) {
+    const int t = w.flist[fi];
+    const float *xt = x + (size_t)t * w.H;
+    for (int e = blockIdx.x; e < w.E; e += gridDim.x) {
+      const float *row = router + (size_t)e * w.H;
+      for (int i = threadIdx.x * 4; i < m; i += 256) {
+        float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
+        *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
+                                            __fmul_rn(a.w, b.w));
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float s = 0.0f;
+        int i = 0;
+#pragma unroll 8
+        for (; i < m; i += 4) {
+          float4 p = *(const float4 *)(prod + i);
+          s = __fadd_rn(s, p.x);
+          s = __fadd_rn(s, p.y);
+          s = __fadd_rn(s, p.z);
+          s = __fadd_rn(s, p.w);
+        }
+        for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+        w.logits[(size_t)t * w.E + e] = s;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// router_topk replica for the tokens on the full path.  grid kFullSlots, 512 threads.
+__global__ void k_topk_full(Work w) {
   __shared__ VI red[16];
   __shared__ float prob[4096];
-  const int nu = *w.ucount;
-  for (int ui = blockIdx.x; ui < nu; ui += gridDim.x) {
-    topk_exact_token(w, w.ulist[ui], x, router, stats, red, prob);
-    __syncthreads();  // the token's LDS is read no more
+  const int nf = *w.fcount;
+  for (int fi = blockIdx.x; fi < nf; fi += gridDim.x) {
+    const int t = w.flist[fi];
+    topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
+                     prob, red);
+    __syncthreads();
   }
 }
 
@@ -1337,40 +1375,72 @@ __device__ __forceinline__ void idot_tile(const signed char *W, int ld, int row0
   }
 }
 
-__global__ void k_shared_swiglu(Work w, const signed char *gq, const float *gs, const signed char *uq,
-                                const float *us) {
-  __shared__ int part[8][2][256];
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  int rt = blockIdx.x, t0 = blockIdx.y * kSharedTokens;
-  int nk = w.H / 64;
-  int per = (nk + nw - 1) / nw, kc0 = wave * per, kc1 = min(nk, kc0 + per);
-  v4i cg = {0, 0, 0, 0}, cu = {0, 0, 0, 0};
+// idot_tile for NS consecutive 16-token chunks sharing each A load: c[s]
+// holds tokens t0 + 16 s + lane % 16 (exact int32 sums, like idot_tile)
+template <int NS>
+__device__ __forceinline__ void idot_tiles(const signed char *W, int ld, int row0, int kc0, int kc1,
+                                           const signed char *xq, int xld, int t0, int T, v4i c[NS], int lane) {
+  const int r = lane & 15, kb = lane >> 4;
+  const signed char *arow = W + (size_t)(row0 + r) * ld + kb * 16;
+  const signed char *brow[NS];
+#pragma unroll
+  for (int q = 0; q < NS; q++) {
+    const int tok = t0 + 16 * q + r;
+    brow[q] = tok < T ? xq + (size_t)tok * xld + kb * 16 : nullptr;
+  }
+  for (int kc = kc0; kc < kc1; kc++) {
+    const v4i a = *(const v4i *)(arow + kc * 64);
+#pragma unroll
+    for (int q = 0; q < NS; q++) {
+      v4i b = {0, 0, 0, 0};
+      if (brow[q]) b = *(const v4i *)(brow[q] + kc * 64);
+      c[q] = mfma_i8(a, b, c[q]);
+    }
+  }
+}
+
+// Shared expert steps of many tokens: blocks take kSharedSub 16-token chunks,
+// so each shared weight tile is read once per 64 tokens.
+constexpr int kSharedSub = 4;
+constexpr int kSharedBlockTokens = 16 * kSharedSub;
+
+__global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char *gq, const float *gs,
+                                                       const signed char *uq, const float *us) {
+  __shared__ int part[4][2][kSharedSub][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rt = blockIdx.x, t0 = blockIdx.y * kSharedBlockTokens;
+  const int nk = w.H / 64;
+  const int per = (nk + 3) / 4, kc0 = wave * per, kc1 = min(nk, kc0 + per);
+  v4i cg[kSharedSub] = {}, cu[kSharedSub] = {};
   if (kc0 < kc1) {
-    idot_tile(gq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cg, lane);
-    idot_tile(uq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cu, lane);
+    idot_tiles<kSharedSub>(gq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cg, lane);
+    idot_tiles<kSharedSub>(uq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cu, lane);
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    part[wave][0][lane * 4 + i] = cg[i];
-    part[wave][1][lane * 4 + i] = cu[i];
-  }
-  __syncthreads();
-  if (wave == 0) {
-    int kb = lane >> 4, tok = t0 + (lane & 15);
+  for (int q = 0; q < kSharedSub; q++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      int dg = 0, du = 0;
-      for (int v = 0; v < nw; v++) {
-        dg += part[v][0][lane * 4 + i];
-        du += part[v][1][lane * 4 + i];
-      }
-      int row = rt * kTileRows + 4 * kb + i;
-      if (tok < w.T) {
-        float sx = w.sx[tok];
-        float g = (float)dg * gs[row] * sx;
-        float u = (float)du * us[row] * sx;
-        w.hsh[(size_t)tok * w.Ish + row] = silu_ref(g) * u;
-      }
+      part[wave][0][q][lane * 4 + i] = cg[q][i];
+      part[wave][1][q][lane * 4 + i] = cu[q][i];
+    }
+  __syncthreads();
+  // wave q finishes chunk q: the waves' k-range sums (exact), then the
+  // reference's rounding of g, u and h
+  const int q = wave, kb = lane >> 4, tok = t0 + 16 * q + (lane & 15);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int dg = 0, du = 0;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      dg += part[v][0][q][lane * 4 + i];
+      du += part[v][1][q][lane * 4 + i];
+    }
+    const int row = rt * kTileRows + 4 * kb + i;
+    if (tok < w.T) {
+      const float sx = w.sx[tok];
+      const float g = (float)dg * gs[row] * sx;
+      const float u = (float)du * us[row] * sx;
+      w.hsh[(size_t)tok * w.Ish + row] = silu_ref(g) * u;
     }
   }
 }
@@ -1879,35 +1949,39 @@ __global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertL
 }
 
 // routed down of wide items, plus the shared expert's token chunks (IDOT) in
-// the extra blocks y >= item_slots.  Block: kWideWaves waves x kWideDnRt row
-// tiles of H; grid (ceil(H/16 / (kWideWaves kWideDnRt)), item slots +
-// shared chunks).
+// the first blocks y < shc (scheduled first, they overlap the routed work).
+// Block: kWideWaves waves x kWideDnRt row tiles of H; grid (ceil(H/16 /
+// (kWideWaves kWideDnRt)), shc + item slots).
 template <int FMT>
-__global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLayout xl, int item_slots,
+__global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLayout xl, int shc,
                                                                const signed char *dq, const float *ds, int hg) {
   extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.H / kTileRows;
   const int rtb = blockIdx.x * kWideWaves * kWideDnRt;
-  if ((int)blockIdx.y >= item_slots) {
+  if ((int)blockIdx.y < shc) {  // shared down, kSharedBlockTokens tokens a block
     const int rt1 = min(nrt, rtb + kWideWaves * kWideDnRt);
-    const int t0 = ((int)blockIdx.y - item_slots) * kSharedTokens, tok = t0 + (lane & 15);
+    const int t0 = (int)blockIdx.y * kSharedBlockTokens;
     for (int rt = rtb + wave; rt < rt1; rt += kWideWaves) {
-      v4i c = {0, 0, 0, 0};
-      idot_tile(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
-      if (tok < w.T) {
+      v4i c[kSharedSub] = {};
+      idot_tiles<kSharedSub>(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int row = rt * kTileRows + 4 * kb + i;
-          w.shout[(size_t)tok * w.H + row] = (float)c[i] * ds[row] * w.shx[tok];
+      for (int q = 0; q < kSharedSub; q++) {
+        const int tok = t0 + 16 * q + (lane & 15);
+        if (tok < w.T) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int row = rt * kTileRows + 4 * kb + i;
+            w.shout[(size_t)tok * w.H + row] = (float)c[q][i] * ds[row] * w.shx[tok];
+          }
         }
       }
     }
     return;
   }
   const int rt0 = rtb + wave * kWideDnRt;
-  const int n_items = *w.nitems;
-  for (int it = blockIdx.y; it < n_items; it += item_slots) {
+  const int n_items = *w.nitems, item_slots = (int)gridDim.y - shc;
+  for (int it = (int)blockIdx.y - shc; it < n_items; it += item_slots) {
     const int4 item = w.items[it];
     const int e = item.x, p0 = item.y, cnt = item.z;
     const TileMat mats[1] = {xl.mat(e, 2)};
@@ -2238,7 +2312,10 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
   k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(w, x,
                                                                                                       L->router);
-  k_topk_exact<<<w.T < kTopkSlots ? w.T : kTopkSlots, 512, 0, st>>>(w, x, L->router, L->stats);
+  k_topk_check<<<w.T < kTopkSlots ? w.T : kTopkSlots, 64, 0, st>>>(w, L->stats);
+  k_exact_full<<<dim3(w.E < 1024 ? w.E : 1024, w.T < kFullSlots ? w.T : kFullSlots), 64, (size_t)w.H * 4, st>>>(
+      w, x, L->router);
+  k_topk_full<<<w.T < kFullSlots ? w.T : kFullSlots, 512, 0, st>>>(w);
   return launch_status("MoE routing kernels");
 }
 
@@ -2343,7 +2420,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   k_bucket<<<1, 1024, bucket_lds, st>>>(w);
   mark(ctx, 2);
   prof_mark(ctx, kStageSetup);
-  k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedTokens - 1) / kSharedTokens), 512, 0, st>>>(
+  k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedBlockTokens - 1) / kSharedBlockTokens), 256, 0, st>>>(
       w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
   mark(ctx, 3);
   prof_mark(ctx, kStageSharedHidden);
@@ -2386,11 +2463,12 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     const size_t ld = wide_lds_bytes(hg);
     const void *fn = fmt4 ? (const void *)k_down_wide<4> : (const void *)k_down_wide<3>;
     if (set_lds(fn, ld)) return -1;
-    const dim3 grid((w.H / kTileRows + kWideWaves * kWideDnRt - 1) / (kWideWaves * kWideDnRt), slots + sh_chunks);
+    const int shc = (T + kSharedBlockTokens - 1) / kSharedBlockTokens;
+    const dim3 grid((w.H / kTileRows + kWideWaves * kWideDnRt - 1) / (kWideWaves * kWideDnRt), shc + slots);
     if (fmt4)
-      k_down_wide<4><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds, hg);
+      k_down_wide<4><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg);
     else
-      k_down_wide<3><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds, hg);
+      k_down_wide<3><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg);
   } else if (fmt4) {
     dn_split ? k_down_split<4><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
