@@ -25,12 +25,13 @@
 //   -- barrier "y" (strict decode order: layer l+1 starts after layer l).
 //
 // Weights that do not depend on the token (the next layer's router rows and
-// shared gate/up tile) are loaded into registers before the "y" barrier; the
-// down tiles of the selected experts are loaded before the "h" barrier.
+// shared gate/up tile) are loaded into registers while stage D computes; the
+// down tiles of the selected experts are loaded into LDS before the "h"
+// barrier.
 //
 // Cross-workgroup data is published with device-scope stores and atomics and
 // read with device-scope loads; barriers are two-level counters (8 groups,
-// then one top counter).  Counters and integer sums come in two parity sets:
+// then one top counter) and a release word.  Counters and integer sums come in two parity sets:
 // a call uses set p and clears set 1-p for the next call.  The call state
 // (parity, dirty extents, the running layer count behind the tags) lives in
 // device memory and is advanced by the kernel itself, so no call needs a
@@ -61,10 +62,16 @@ constexpr int kNch = 2;          // 2048-float chunks per router row (H <= 4096)
 constexpr int kMaxAmbig = 64;    // experts the targeted exact selection can take
 constexpr int kLine = 32;        // words between counters (one 128-byte line)
 constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h, y
-constexpr int kBarWords = 9 * kLine;
+constexpr int kBarWords = 10 * kLine;  // release word, 8 group counters, top counter
 constexpr int kRecWords = 12;    // h chunk record: d1[16] d2[16] (8 words) | A B Q1 Q2
 constexpr int kGMax = 4;         // stage G: groups per wave and unit
-constexpr int kGRing = 4;        // stage G: ring slots per wave
+#ifndef SW_SHDOWN_LATE
+#define SW_SHDOWN_LATE 1
+#endif
+#ifndef SW_STACK_GRING
+#define SW_STACK_GRING 4
+#endif
+constexpr int kGRing = SW_STACK_GRING;  // stage G: ring slots per wave
 constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
 constexpr int kGHead = 2560;     // stage G: partial sums and digit staging before the rings
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
@@ -118,7 +125,7 @@ struct StackArgs {
   float *ex;            // [E] exact logits
   unsigned *hd;         // [K][ngi*8][kRecWords]
   unsigned long long *spl;  // [kSplitUnits][16][2] tagged half sums of split units
-  int *acc;             // [layer][parity][2*Ish]
+  unsigned long long *acc;  // [layer][parity][2*Ish] counted shared gate/up sums
   unsigned *bars;       // [layer][parity][kBars][kBarWords]
   size_t acc_stride;    // words per (layer, parity) acc block
   unsigned *state;      // call state, advanced by every call (StackState)
@@ -129,6 +136,17 @@ struct StackArgs {
   unsigned long long *trace;  // optional stage stamps [layer][NB][kStamps]
   size_t trace_words;
 };
+
+
+// The kernel arguments, read again from the kernel-argument segment (scalar
+// loads through the constant cache): laundered so that no stage keeps every
+// field live in scalar registers across the whole layer loop.
+__device__ __forceinline__ StackArgs kargs() {
+  typedef const __attribute__((address_space(4))) StackArgs KA;
+  KA *p = (KA *)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *(const StackArgs *)(const void *)p;
+}
 
 // Optional per-stage wall-clock stamps (100 MHz device clock), thread 0 of
 // every workgroup: layer start, R done, lb passed, S done, G done, h passed,
@@ -158,6 +176,14 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 }
 __device__ __forceinline__ double ld_agent(const double *p) {
   return __longlong_as_double((long long)ld_agent((const unsigned long long *)p));
+}
+// A device-scope load that waits for itself inside the same statement: the
+// compiler sees no load in flight afterwards, so it places no wait for it
+// elsewhere (such a wait would also wait for every copy issued before it).
+__device__ __forceinline__ unsigned long long ld_agent_sync(const unsigned long long *p) {
+  unsigned long long v;
+  asm volatile("global_load_dwordx2 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+  return v;
 }
 // A returning exchange: once its value is back, the word is visible to every
 // device-scope load on the device.  The xor of the returns feeds published().
@@ -193,6 +219,11 @@ __device__ __forceinline__ unsigned lds_addr(const void *p) {
 __device__ __forceinline__ void dma_b128(const void *gptr, unsigned base) {
   base = __builtin_amdgcn_readfirstlane(base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(base) : "memory", "m0");
+}
+// device-scope (sc1): sees other workgroups' atomics once they are done
+__device__ __forceinline__ void dma_b128_dev(const void *gptr, unsigned base) {
+  base = __builtin_amdgcn_readfirstlane(base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(gptr), "s"(base) : "memory", "m0");
 }
 __device__ __forceinline__ void dma_b32(const void *gptr, unsigned base) {
   base = __builtin_amdgcn_readfirstlane(base);
@@ -255,7 +286,10 @@ __device__ __forceinline__ LayerPtrs layer_ref_lds(const unsigned *w) {
 }
 // word i of layer l's pointers from the kernel arguments or the layer table
 __device__ __forceinline__ unsigned layer_ref_word(const StackArgs &a, int l, int i) {
-  return a.n == 1 ? ((const unsigned *)&a.one)[i] : ((const SW_G unsigned *)(a.table + l))[i];
+  const __attribute__((address_space(4))) unsigned *one =
+      (const __attribute__((address_space(4))) unsigned *)__builtin_amdgcn_kernarg_segment_ptr() +
+      offsetof(StackArgs, one) / 4;
+  return a.n == 1 ? one[i] : ((const SW_G unsigned *)(a.table + l))[i];
 }
 __device__ __forceinline__ unsigned *bar_of(const StackArgs &a, const CallState &cs, int l, int which) {
   return a.bars + ((size_t)(l * 2 + cs.parity) * kBars + which) * kBarWords;
@@ -265,7 +299,7 @@ __device__ __forceinline__ unsigned *bar_of(const StackArgs &a, const CallState 
 // Bounded waits and the two-level grid barrier (thread 0 acts; the caller
 // brackets with __syncthreads and distributes the result through LDS).
 // ---------------------------------------------------------------------------
-__device__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) {
+__device__ __forceinline__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) {
   const long long t0 = (long long)wall_clock64();
   for (unsigned it = 0;; it++) {
     if (ld_agent(p) >= target) return true;
@@ -279,6 +313,18 @@ __device__ bool wait_ge(const unsigned *p, unsigned target, const StackArgs &a) 
     }
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// Counted integer sums.  A shared gate/up row's sum has KQ parts (one per
+// k-range task); each part is added as (v + 2^32) + 2^48, so the word holds
+// the number of parts in bits 48.. and the biased sum below: the sum is exact
+// (|sum| < 2^31, at most 255 parts) and a reader knows when it is complete.
+__device__ __forceinline__ unsigned long long acc_term(int v) {
+  return (unsigned long long)((long long)v + (1ll << 32)) + (1ull << 48);
+}
+__device__ __forceinline__ int acc_parts(unsigned long long w) { return (int)(w >> 48); }
+__device__ __forceinline__ int acc_sum(unsigned long long w) {
+  return (int)((long long)(w & ((1ull << 48) - 1)) - ((long long)(w >> 48) << 32));
 }
 
 // Tagged words.  A word exchanged between workgroups within a layer carries
@@ -299,7 +345,7 @@ __device__ __forceinline__ bool has_tag(unsigned long long v, unsigned tag) { re
 // round trip per round) until every one is.  Rounds are bounded: true when
 // the wait started at t0 must end (the abort word is set, or the time is up;
 // then every workgroup leaves through the abort word).
-__device__ bool wait_expired(long long t0, const StackArgs &a) {
+__device__ __forceinline__ bool wait_expired(long long t0, const StackArgs &a) {
   if (__builtin_expect(ld_agent(a.abort_word) != 0, 0)) return true;
   if (__builtin_expect((long long)wall_clock64() - t0 > a.spin_ticks, 0)) {
     atomicMax(a.abort_word, 1u);
@@ -309,35 +355,45 @@ __device__ bool wait_expired(long long t0, const StackArgs &a) {
   return false;
 }
 
-// arrive: the workgroup's published words must have returned already
+// arrive: the workgroup's published words must have returned already.  The
+// last arriver of each group of workgroups (b % 8) counts its group on the top
+// counter; the last group's arriver then stores the release word, which the
+// waiters poll (a word written once, not a counter taking 8 additions).
 __device__ __forceinline__ void bar_arrive(unsigned *bar, int NB) {
   const int g = blockIdx.x & 7;
   const unsigned cnt = (unsigned)((NB - 1 - g) / 8 + 1);
-  unsigned old = atomicAdd(&bar[kLine * (1 + g)], 1u);
-  if (old == cnt - 1) atomicAdd(&bar[0], 1u);
+  const unsigned ng = (unsigned)(NB < 8 ? NB : 8);
+  const unsigned old = atomicAdd(&bar[kLine * (1 + g)], 1u);
+  if (old == cnt - 1) {
+    const unsigned o2 = atomicAdd(&bar[kLine * 9], 1u);
+    if (o2 == ng - 1) __hip_atomic_store(&bar[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
-__device__ __forceinline__ bool bar_wait(unsigned *bar, const StackArgs &a) {
-  return wait_ge(&bar[0], (unsigned)(a.NB < 8 ? a.NB : 8), a);
-}
+__device__ __forceinline__ bool bar_wait(unsigned *bar, const StackArgs &a) { return wait_ge(&bar[0], 1u, a); }
 
 // ---------------------------------------------------------------------------
 // wave helpers
 // ---------------------------------------------------------------------------
-#define SW_DPP_D_ADD(v, ctrl, rm, bc)                             \
-  {                                                               \
-    int lo_ = SW_DPP_I(0, (int)__double2loint(v), ctrl, rm, bc); \
-    int hi_ = SW_DPP_I(0, (int)__double2hiint(v), ctrl, rm, bc); \
-    v += __hiloint2double(hi_, lo_);                              \
-  }
-__device__ __forceinline__ double wave_inclusive_scan_d(double v) {
-  SW_DPP_D_ADD(v, 0x111, 0xF, true);
-  SW_DPP_D_ADD(v, 0x112, 0xF, true);
-  SW_DPP_D_ADD(v, 0x114, 0xF, true);
-  SW_DPP_D_ADD(v, 0x118, 0xF, true);
-  SW_DPP_D_ADD(v, 0x142, 0xA, false);
-  SW_DPP_D_ADD(v, 0x143, 0xC, false);
+// Inclusive prefix sums in lane order: within each 16-lane row (row_shr 1,
+// 2, 4, 8), then over the rows (row_bcast15 into rows 1 and 3, row_bcast31
+// into rows 2 and 3).
+__device__ __forceinline__ float row16_inclusive_scan_f(float v) {
+  v += SW_DPP_F(0.0f, v, 0x111, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x112, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x114, 0xF, true);
+  v += SW_DPP_F(0.0f, v, 0x118, 0xF, true);
   return v;
 }
+__device__ __forceinline__ float wave_inclusive_scan_f(float v) {
+  v = row16_inclusive_scan_f(v);
+  v += SW_DPP_F(0.0f, v, 0x142, 0xA, false);
+  v += SW_DPP_F(0.0f, v, 0x143, 0xC, false);
+  return v;
+}
+// lane l receives lane l-1 (wave_shr 1; lane 0 receives 0)
+__device__ __forceinline__ float dpp_wave_shr1_f(float v) { return SW_DPP_F(0.0f, v, 0x138, 0xF, true); }
+// lane l receives lane l-1 within its 16-lane row (the row's lane 0 receives 0)
+__device__ __forceinline__ float dpp_row_shr1_f(float v) { return SW_DPP_F(0.0f, v, 0x111, 0xF, true); }
 // total of each 16-lane row, in every lane of the row
 __device__ __forceinline__ float row16_sum(float v) {
   v += SW_DPP_F(0.0f, v, 0xB1, 0xF, true);
@@ -353,6 +409,55 @@ __device__ __forceinline__ double dpp_row_shl1_d(double v) {
   const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), 0x101, 0xF, 0xF, false);
   return __hiloint2double(hi, lo);
 }
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long v, int q) {
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, q);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), q);
+  return ((unsigned long long)hi << 32) | lo;
+}
+// How many of lanes 0..n-1 hold a key above this lane's (n <= 64; lanes n..63
+// hold 0, below every key).  Four independent compares per step: a chain of
+// single broadcasts waits on each one's latency.
+__device__ __forceinline__ int count_greater(unsigned long long v, int n) {
+  int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+  for (int q = 0; q < n; q += 4) {
+    r0 += readlane_u64(v, q) > v;
+    r1 += readlane_u64(v, q + 1) > v;
+    r2 += readlane_u64(v, q + 2) > v;
+    r3 += readlane_u64(v, q + 3) > v;
+  }
+  return (r0 + r1) + (r2 + r3);
+}
+__device__ __forceinline__ double readlane_d(double v, int q) {
+  return __longlong_as_double((long long)readlane_u64((unsigned long long)__double_as_longlong(v), q));
+}
+// forward permute of a double: the lane whose byte address is pa receives v
+__device__ __forceinline__ double permute_d(int pa, double v) {
+  const int lo = __builtin_amdgcn_ds_permute(pa, __double2loint(v));
+  const int hi = __builtin_amdgcn_ds_permute(pa, __double2hiint(v));
+  return __hiloint2double(hi, lo);
+}
+// minimum / maximum over each 16-lane row, read from lane 0
+#define SW_DPP_D_OP(v, ctrl, op)                                                     \
+  {                                                                                  \
+    const int lo_ = __builtin_amdgcn_update_dpp(0, __double2loint(v), ctrl, 0xF, 0xF, false); \
+    const int hi_ = __builtin_amdgcn_update_dpp(0, __double2hiint(v), ctrl, 0xF, 0xF, false); \
+    v = op(v, __hiloint2double(hi_, lo_));                                           \
+  }
+__device__ __forceinline__ double row16_min_d(double v) {
+  SW_DPP_D_OP(v, 0xB1, fmin);
+  SW_DPP_D_OP(v, 0x4E, fmin);
+  SW_DPP_D_OP(v, 0x141, fmin);
+  SW_DPP_D_OP(v, 0x140, fmin);
+  return readlane_d(v, 0);
+}
+__device__ __forceinline__ double row16_max_d(double v) {
+  SW_DPP_D_OP(v, 0xB1, fmax);
+  SW_DPP_D_OP(v, 0x4E, fmax);
+  SW_DPP_D_OP(v, 0x141, fmax);
+  SW_DPP_D_OP(v, 0x140, fmax);
+  return readlane_d(v, 0);
+}
+#undef SW_DPP_D_OP
 __device__ __forceinline__ double order_margin(double a, double b, double mx) {
   return 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
 }
@@ -433,6 +538,17 @@ __device__ __forceinline__ ShTask sh_task(const StackArgs &a) {
   return t;
 }
 // this wave's k-chunks of the task
+// the task as five words in LDS (computed once per call: the divisions by
+// runtime values cost tens of scalar instructions each)
+__device__ __forceinline__ ShTask sh_task_lds(const int *w) {
+  ShTask t;
+  t.valid = __builtin_amdgcn_readfirstlane(w[0]);
+  t.m = __builtin_amdgcn_readfirstlane(w[1]);
+  t.rt = __builtin_amdgcn_readfirstlane(w[2]);
+  t.kc0 = __builtin_amdgcn_readfirstlane(w[3]);
+  t.kc1 = __builtin_amdgcn_readfirstlane(w[4]);
+  return t;
+}
 __device__ __forceinline__ void sh_wave_range(const ShTask &t, int wave, int &k0, int &k1) {
   const int n = t.kc1 - t.kc0;
   k0 = t.kc0 + wave * n / kW;
@@ -440,102 +556,49 @@ __device__ __forceinline__ void sh_wave_range(const ShTask &t, int wave, int &k0
 }
 
 struct RStageLds {
-  double segT[kRSlots][kNch * 8];
-  double Lg[kRSlots];
-  double inc[kRSlots][kNch][kT];  // each thread's within-wave inclusive scan
-  double Ap[kRSlots][kW], Pp[kRSlots][kW];
+  float segT[kRSlots][16];        // prefix-scan segment totals, segment c*8 + wave
+  double Lp[kRSlots][kW];         // per-wave partial logits
+  float Ap[kRSlots][kW], Pp[kRSlots][kW];
   float red[kW];
   int acc_i[kW][16];
 };
+__host__ __device__ inline size_t r_lds_bytes() { return (sizeof(RStageLds) + 255) & ~(size_t)255; }
 
-// Stage R's inputs in the stage-local LDS union: this workgroup's router rows
-// [rslots][H] f32 and its shared gate/up tile [16 rows][k-chunks * 64] int8
-// (rows padded by 16 bytes against bank conflicts).  They do not depend on
-// the token, so they are copied in while the previous layer finishes.
-struct RLayout {
-  size_t rbuf, sbuf, srow, end;
-};
-__host__ __device__ inline RLayout r_layout(int rslots, int H, int shkc) {
-  RLayout r;
-  size_t o = (sizeof(RStageLds) + 255) & ~(size_t)255;
-  r.rbuf = o;
-  o += (size_t)rslots * H * 4;
-  r.srow = (size_t)shkc * 64 + 16;
-  r.sbuf = o;
-  o += (size_t)kTileRows * r.srow;
-  r.end = o;
-  return r;
-}
-
-// Stage R's inputs of the next layer travel in registers of waves 1..7
-// (wave 0 keeps no loads outstanding: it polls the grid barriers).  They are
-// loaded while the current layer waits on its last grid barrier (HBM is
-// otherwise idle then) and written to LDS when the next layer starts.
-// Thread T = t - 64 carries the 16-byte chunks T + 448 i of the byte stream
-// [router rows of this workgroup | shared tile in 1 KB blocks: k-chunk kc,
-// then 16 rows of 64 bytes].  Every offset is found with compares, shifts and
-// masks: integer division by a runtime value costs tens of instructions.
-constexpr int kStRegs = 12;
-constexpr int kStThreads = kT - 64;
+// Stage R's inputs do not depend on the token: every thread loads its own
+// part of them into registers while the previous layer's stage D computes
+// (HBM is otherwise idle then), in the layout it uses them in.
+//   w[s][c]: router row b + s*NB (the shared expert's gate row for row E),
+//            elements 2048c + 4t .. +3, the thread's elements of x;
+//   sa[i]:   k-chunk k0 + i of the workgroup's shared gate/up task, in the
+//            int8 MFMA A layout (lane l: row l % 16, bytes (l / 16) * 16).
+constexpr int kShMaxKc = 4;  // shared task k-chunks per wave
 struct StaticRegs {
-  v4u v[kStRegs];
+  v4f w[kRSlots][kNch];
+  v4i sa[kShMaxKc];
 };
-struct StaticMap {
-  unsigned rowb, rbytes;  // bytes per router row, all router rows (at most kRSlots)
-  unsigned total;         // whole stream
-};
-__device__ __forceinline__ StaticMap static_map(const StackArgs &a) {
-  StaticMap m;
-  int nrows = 0;
-  for (int s2 = 0; s2 < a.rslots; s2++)
-    if ((int)blockIdx.x + s2 * a.NB <= a.E) nrows = s2 + 1;
-  m.rowb = (unsigned)a.H * 4u;
-  m.rbytes = (unsigned)nrows * m.rowb;
-  const ShTask st = sh_task(a);
-  m.total = m.rbytes + (st.valid ? (unsigned)(st.kc1 - st.kc0) * 1024u : 0u);
-  return m;
-}
-__device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs &L, StaticRegs &sr, int t) {
-  if (t < 64) return;
-  const StaticMap m = static_map(a);
-  const ShTask st = sh_task(a);
-  const SW_G unsigned char *sbase =
-      (const SW_G unsigned char *)((st.m == 0 ? L.gq : L.uq) + (size_t)st.rt * kTileRows * a.H + st.kc0 * 64);
-  const SW_G unsigned char *rows[kRSlots];
+__device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs &L, const ShTask &st, StaticRegs &sr,
+                                            int t) {
+  const int b = blockIdx.x, lane = t & 63, wave = t >> 6;
 #pragma unroll
   for (int s2 = 0; s2 < kRSlots; s2++) {
-    const int r = blockIdx.x + s2 * a.NB;
-    rows[s2] = (const SW_G unsigned char *)(r < a.E ? L.router + (size_t)r * a.H : L.sgate);
-  }
+    const int r = b + s2 * a.NB;
+    const bool valid = s2 < a.rslots && r <= a.E;  // uniform
+    const SW_G float *row = r < a.E ? L.router + (size_t)r * a.H : L.sgate;
 #pragma unroll
-  for (int i = 0; i < kStRegs; i++) {
-    const unsigned o = 16u * (unsigned)((t - 64) + kStThreads * i);
-    v4u v = {0u, 0u, 0u, 0u};
-    if (o < m.rbytes) {
-      const int s2 = (o >= m.rowb) + (o >= 2 * m.rowb);
-      const SW_G unsigned char *row = s2 == 0 ? rows[0] : (s2 == 1 ? rows[1] : rows[2]);
-      v = __builtin_nontemporal_load((const SW_G v4u *)(row + (o - (unsigned)s2 * m.rowb)));
-    } else if (o < m.total) {
-      const unsigned o2 = o - m.rbytes;
-      v = __builtin_nontemporal_load(
-          (const SW_G v4u *)(sbase + (size_t)((o2 >> 6) & 15) * a.H + (o2 >> 10) * 64 + (o2 & 63)));
+    for (int c = 0; c < kNch; c++) {
+      const int e0 = 2048 * c + 4 * t;
+      sr.w[s2][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (valid && c < a.nch && e0 < a.H) sr.w[s2][c] = __builtin_nontemporal_load((const SW_G v4f *)(row + e0));
     }
-    sr.v[i] = v;
   }
-}
-__device__ __forceinline__ void static_store(const StackArgs &a, const StaticRegs &sr, unsigned char *u, int t) {
-  if (t < 64) return;
-  const StaticMap m = static_map(a);
-  const RLayout rl = r_layout(a.rslots, a.H, a.shkc);
+  int k0, k1;
+  sh_wave_range(st, wave, k0, k1);
+  const SW_G signed char *sbase = (st.m == 0 ? L.gq : L.uq) + (size_t)(st.rt * kTileRows + (lane & 15)) * a.H +
+                                  (lane >> 4) * 16;
 #pragma unroll
-  for (int i = 0; i < kStRegs; i++) {
-    const unsigned o = 16u * (unsigned)((t - 64) + kStThreads * i);
-    if (o < m.rbytes) {
-      *(v4u *)(u + rl.rbuf + o) = sr.v[i];
-    } else if (o < m.total) {
-      const unsigned o2 = o - m.rbytes;
-      *(v4u *)(u + rl.sbuf + ((o2 >> 6) & 15) * (unsigned)rl.srow + (o2 >> 10) * 64 + (o2 & 63)) = sr.v[i];
-    }
+  for (int i = 0; i < kShMaxKc; i++) {
+    sr.sa[i] = v4i{0, 0, 0, 0};
+    if (st.valid && k0 + i < k1) sr.sa[i] = __builtin_nontemporal_load((const SW_G v4i *)(sbase + (k0 + i) * 64));
   }
 }
 
@@ -684,7 +747,8 @@ __device__ __forceinline__ void wait_vm(int n) {
     asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); \
     break;
     SW_VM(1) SW_VM(2) SW_VM(3) SW_VM(4) SW_VM(5) SW_VM(6) SW_VM(7) SW_VM(8) SW_VM(9) SW_VM(10) SW_VM(11)
-    SW_VM(12) SW_VM(13) SW_VM(14) SW_VM(15) SW_VM(16) SW_VM(17)
+    SW_VM(12) SW_VM(13) SW_VM(14) SW_VM(15) SW_VM(16) SW_VM(17) SW_VM(18) SW_VM(19) SW_VM(20) SW_VM(21)
+    SW_VM(22) SW_VM(23) SW_VM(24) SW_VM(25) SW_VM(26) SW_VM(27) SW_VM(28) SW_VM(29) SW_VM(30)
 #undef SW_VM
     default:
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -697,14 +761,12 @@ __device__ __forceinline__ void wait_vm(int n) {
 constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
 static_assert(kStackMaxE + 1 <= kSelRec * kT, "every record has a thread in stage S");
 constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
-constexpr int kShPT = 4;    // shared hidden values per thread in one batch
 struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
   unsigned long long mc[64];    // keys at or above the sample threshold
   unsigned long long wup[kW];   // each wave's largest upper bound below it
   int nmc;
   double theta, mxd;
-  int cand[kMaxK + 1];
   int nm;
   int m[kMaxAmbig];
   float exv[kMaxAmbig];
@@ -725,16 +787,24 @@ __host__ __device__ inline size_t s_hsh_offset(int E, int H, int Ish, int fmt) {
   return ((o > g ? o : g) + 15) & ~(size_t)15;
 }
 
+// The shared gate/up sums (u64 [2 * Ish]) and row scales (f32 [2 * Ish]),
+// copied in during stage S and read at the start of stage G: past the shared
+// hidden vector, clear of stage G's regions.
+__host__ __device__ inline size_t s_stage_offset(int E, int H, int Ish, int fmt) {
+  return s_hsh_offset(E, H, Ish, fmt) + (((size_t)Ish * 4 + 15) & ~(size_t)15);
+}
+__host__ __device__ inline size_t s_stage_bytes(int Ish) { return (size_t)Ish * 24; }
+
 struct Routes {  // result of stage S, in static LDS
   int idx[kMaxK];
   float w[kMaxK];
   float sg;        // sigmoid of the shared gate logit
   int flag;        // barrier result broadcast
   int state;       // selection path: 0 certified, 1 targeted exact, 2 full exact
-  float shm[kW];   // each wave's largest |shared hidden value| (waves 1..7)
+  float shm[kW];   // each wave's largest |shared hidden value|
 };
 
-__device__ bool sync_barrier(const StackArgs &a, const CallState &cs, int l, int which, Routes &rt) {
+__device__ __forceinline__ bool sync_barrier(const StackArgs &a, const CallState &cs, int l, int which, Routes &rt) {
   lds_barrier();
   if (threadIdx.x == 0) {
     unsigned *bar = bar_of(a, cs, l, which);
@@ -760,10 +830,15 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   // read the shared down rows, so kept out of the stage-local union
   __shared__ int s_shp[kW * 16];
   __shared__ unsigned s_lref[2][kRefWords];  // layer l's pointers in s_lref[l & 1]
+  __shared__ int s_sht[5];                   // this workgroup's shared gate/up task
+  __shared__ unsigned s_shcnt;               // waves 1..7 whose stage S copies have landed, this call
+  __shared__ uint64_t s_exp2[32];            // expf's table: LDS reads wait behind no global load
   const int b = blockIdx.x;
   const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
+  if (threadIdx.x == 0) s_shcnt = 0;
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = kExp2Tab[threadIdx.x];
   // Fault drill: these workgroups leave before taking any part, as if they
   // never became resident.  Every other one then meets a wait that cannot be
   // met (their router records, at the latest) and leaves through the abort word.
@@ -793,20 +868,29 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     for (int l = 0; l < zero_layers; l++) {
       unsigned *bz = a.bars + (size_t)(l * 2 + op) * bw;
       for (size_t i = (size_t)b * kT + t; i < bw; i += (size_t)a.NB * kT) bz[i] = 0u;
-      int *az = a.acc + (size_t)(l * 2 + op) * a.acc_stride;
-      for (size_t i = (size_t)b * kT + t; i < (size_t)zero_acc_words; i += (size_t)a.NB * kT) az[i] = 0;
+      unsigned long long *az = a.acc + (size_t)(l * 2 + op) * a.acc_stride;
+      for (size_t i = (size_t)b * kT + t; i < (size_t)zero_acc_words; i += (size_t)a.NB * kT) az[i] = 0ull;
     }
   }
 
+  if (threadIdx.x == 0) {
+    const ShTask st = sh_task(a0);
+    s_sht[0] = st.valid;
+    s_sht[1] = st.m;
+    s_sht[2] = st.rt;
+    s_sht[3] = st.kc0;
+    s_sht[4] = st.kc1;
+  }
+  __syncthreads();
   StaticRegs sreg;
-  static_load(a0, layer_ref(a0, 0), sreg, threadIdx.x);
+  static_load(a0, layer_ref(a0, 0), sh_task_lds(s_sht), sreg, threadIdx.x);
   if (threadIdx.x < kRefWords) s_lref[0][threadIdx.x] = layer_ref_word(a0, 0, threadIdx.x);
   lds_barrier();
 
   for (int l = 0; l < a0.n; l++) {
     // Lane indices are re-derived every layer: values hoisted out of the loop
     // would stay live through every stage and spill.
-    const StackArgs &a = a0;
+    const StackArgs a = kargs();
     int t = (int)threadIdx.x;
     asm volatile("" : "+v"(t));
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -816,7 +900,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     unsigned nref = 0;
     if (l + 1 < a.n && t >= kT - 64 && t - (kT - 64) < kRefWords) nref = layer_ref_word(a, l + 1, t - (kT - 64));
     const float *x = a.x + (size_t)l * a.xs;
-    int *acc = a.acc + (size_t)(l * 2 + cs.parity) * a.acc_stride;
+    unsigned long long *acc = a.acc + (size_t)(l * 2 + cs.parity) * a.acc_stride;
 
     // ======================= stage R =======================
     stamp(a, l, 0);
@@ -871,11 +955,44 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       m = wave_max_dpp(m);
       if (lane == 0) R.red[wave] = m;
     }
-    // this layer's router rows and shared tile: registers -> LDS
-    static_store(a, sreg, S.u, t);
-    lds_barrier();
-    const RLayout rl = r_layout(a.rslots, a.H, a.shkc);
-    const float *rbuf = (const float *)(S.u + rl.rbuf);
+    // Router pass 1, on the rows in registers.  The logit is the fp64 sum of
+    // the exact products.  The bound needs A = sum |p| and P = sum_k |S_k|
+    // over the prefix sums S_k of the serial order; both are taken in fp32
+    // with their own rounding accounted for at the end: the prefixes go
+    // thread (4 elements), wave (a 256-element segment, inclusive scan), then
+    // over the row's segments (c * 8 + wave), whose carries need every wave's
+    // segment total.
+    double Lt[kRSlots];
+    float At[kRSlots], sv[kRSlots][kNch][4];
+#pragma unroll
+    for (int s = 0; s < kRSlots; s++) {
+      Lt[s] = 0.0;
+      At[s] = 0.0f;
+      const int r = b + s * a.NB;
+      if (s < a.rslots && r <= a.E) {
+#pragma unroll
+        for (int c = 0; c < kNch; c++) {
+          if (c < a.nch) {
+            const v4f w = sreg.w[s][c];
+            const float p0 = xv[c].x * w.x, p1 = xv[c].y * w.y, p2 = xv[c].z * w.z, p3 = xv[c].w * w.w;
+            Lt[s] = __builtin_fma((double)xv[c].x, (double)w.x, Lt[s]);
+            Lt[s] = __builtin_fma((double)xv[c].y, (double)w.y, Lt[s]);
+            Lt[s] = __builtin_fma((double)xv[c].z, (double)w.z, Lt[s]);
+            Lt[s] = __builtin_fma((double)xv[c].w, (double)w.w, Lt[s]);
+            At[s] += (fabsf(p0) + fabsf(p1)) + (fabsf(p2) + fabsf(p3));
+            const float q1 = p0 + p1, q2 = q1 + p2, q3 = q2 + p3;
+            const float inc = wave_inclusive_scan_f(q3);
+            const float ex = dpp_wave_shr1_f(inc);
+            sv[s][c][0] = ex + p0;
+            sv[s][c][1] = ex + q1;
+            sv[s][c][2] = ex + q2;
+            sv[s][c][3] = ex + q3;
+            if (lane == 63) R.segT[s][c * 8 + wave] = inc;
+          }
+        }
+      }
+    }
+    lds_barrier();  // red, segT complete
     // qrow_i8 of x (c/qwen.c:1696): sx = amax/127 (floor 1e-12), q = rint(x/sx)
     float sx;
     {
@@ -896,129 +1013,89 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       }
       if (t == 0) s_misc[0] = sx;
     }
-    // router pass 1: each wave's inclusive scan of its per-thread sums (kept
-    // for pass 2), segment totals, |products|
-    double Aacc[kRSlots];
+    // Router pass 2: the carries of the segments (an exclusive scan of the
+    // segment totals, 16 lanes), sum |S_k| and the wave sums of L, A, P.
 #pragma unroll
     for (int s = 0; s < kRSlots; s++) {
-      Aacc[s] = 0.0;
       const int r = b + s * a.NB;
       if (s < a.rslots && r <= a.E) {
+        const float g = lane < a.nch * 8 ? R.segT[s][lane] : 0.0f;
+        const float ge = dpp_row_shr1_f(row16_inclusive_scan_f(g));
+        float P = 0.0f;
 #pragma unroll
         for (int c = 0; c < kNch; c++) {
+          const int e0 = 2048 * c + 4 * t;
           if (c < a.nch) {
-            const int e0 = 2048 * c + 4 * t;
-            double p0 = 0, p1 = 0, p2 = 0, p3 = 0;
-            if (e0 < a.H) {
-              const v4f w = *(const v4f *)(rbuf + (size_t)s * a.H + e0);
-              p0 = (double)xv[c].x * (double)w.x;
-              p1 = (double)xv[c].y * (double)w.y;
-              p2 = (double)xv[c].z * (double)w.z;
-              p3 = (double)xv[c].w * (double)w.w;
-            }
-            Aacc[s] += fabs(p0) + fabs(p1) + fabs(p2) + fabs(p3);
-            const double inc = wave_inclusive_scan_d(((p0 + p1) + p2) + p3);
-            R.inc[s][c][t] = inc;
-            if (lane == 63) R.segT[s][c * 8 + wave] = inc;
+            const float carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ge), c * 8 + wave));
+            if (e0 < a.H)
+              P += (fabsf(carry + sv[s][c][0]) + fabsf(carry + sv[s][c][1])) +
+                   (fabsf(carry + sv[s][c][2]) + fabsf(carry + sv[s][c][3]));
           }
+        }
+        const double Lw = wave_sum_dpp(Lt[s]);
+        const float Aw = wave_sum_dpp(At[s]), Pw = wave_sum_dpp(P);
+        if (lane == 63) {
+          R.Lp[s][wave] = Lw;
+          R.Ap[s][wave] = Aw;
+          R.Pp[s][wave] = Pw;
         }
       }
     }
-    lds_barrier();  // xq, segT complete
-    // shared gate/up task: exact int32 dots of 16 rows with xq; the sums go
-    // out first, so that they are in before this workgroup's records show the
-    // layer's tag (stage S reads them once it has seen every record)
-    const ShTask st = sh_task(a);
+    lds_barrier();  // xq complete
+    // shared gate/up task: exact int32 dots of 16 rows with xq (A operands in
+    // registers), added to the layer's counted sums (stage S reads each sum
+    // once all of its KQ parts are in)
+    const ShTask st = sh_task_lds(s_sht);
     {
       v4i cs = {0, 0, 0, 0};
       if (st.valid) {
         int k0, k1;
         sh_wave_range(st, wave, k0, k1);
-        const signed char *arow = (const signed char *)(S.u + rl.sbuf) + (lane & 15) * rl.srow + (lane >> 4) * 16;
-        for (int kc = k0; kc < k1; kc++) {
-          const v4i av = *(const v4i *)(arow + (kc - st.kc0) * 64);
-          const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
-          cs = mfma_i8(av, bv, cs);
-        }
+#pragma unroll
+        for (int i = 0; i < kShMaxKc; i++)
+          if (k0 + i < k1) {
+            const int kc = k0 + i;
+            const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
+            cs = mfma_i8(sreg.sa[i], bv, cs);
+          }
         if ((lane & 15) == 0) {
 #pragma unroll
           for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
         }
       }
     }
-    lds_barrier();
-    unsigned dep_acc = 0;
-    if (wave == 0 && st.valid && lane >= 16 && lane < 32) {
-      const int r = lane - 16;
-      int v = 0;
-#pragma unroll
-      for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
-      dep_acc = (unsigned)atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], v);
-    }
-    // router pass 2: exact prefix sums -> sum |S_k|
-#pragma unroll
-    for (int s = 0; s < kRSlots; s++) {
-      const int r = b + s * a.NB;
-      double P = 0.0;
-      if (s < a.rslots && r <= a.E) {
-#pragma unroll
-        for (int c = 0; c < kNch; c++) {
-          if (c < a.nch) {
-            const int e0 = 2048 * c + 4 * t;
-            // exact prefix of the segments before this wave's: a scan of the
-            // segment totals held one per lane
-            const double segv = lane < a.nch * 8 ? R.segT[s][lane] : 0.0;
-            const double segi = wave_inclusive_scan_d(segv);
-            const int sg = c * 8 + wave;
-            double carry = 0.0;
-            if (sg > 0) {
-              const int lo_ = __builtin_amdgcn_readlane((int)__double2loint(segi), sg - 1);
-              const int hi_ = __builtin_amdgcn_readlane((int)__double2hiint(segi), sg - 1);
-              carry = __hiloint2double(hi_, lo_);
-            }
-            // the row's fp64 logit: the total over every segment
-            if (c == 0 && wave == 0 && lane == a.nch * 8 - 1) R.Lg[s] = segi;
-            double p0 = 0, p1 = 0, p2 = 0, p3 = 0;
-            if (e0 < a.H) {
-              const v4f w = *(const v4f *)(rbuf + (size_t)s * a.H + e0);
-              p0 = (double)xv[c].x * (double)w.x;
-              p1 = (double)xv[c].y * (double)w.y;
-              p2 = (double)xv[c].z * (double)w.z;
-              p3 = (double)xv[c].w * (double)w.w;
-            }
-            const double q0 = p0, q1 = q0 + p1, q2 = q1 + p2, q3 = q2 + p3;
-            const double pre = carry + (R.inc[s][c][t] - q3);
-            if (e0 < a.H) P += fabs(pre + q0) + fabs(pre + q1) + fabs(pre + q2) + fabs(pre + q3);
-          }
-        }
-        const double As = wave_sum_dpp(Aacc[s]);
-        P = wave_sum_dpp(P);
-        if (lane == 0) {
-          R.Ap[s][wave] = As;
-          R.Pp[s][wave] = P;
-        }
-      }
-    }
-    lds_barrier();  // Ap/Pp complete
+    lds_barrier();  // acc_i, Lp/Ap/Pp complete
     if (wave == 0) {
-      published(dep_acc);
-      // router records of this workgroup's rows, lanes 2s (logit) and 2s+1
-      // (bound), tagged: the tag replaces the low 8 bits of each double, and
-      // the bound grows by more than the logit can move (2^-44 relative)
+      if (st.valid && lane >= 16 && lane < 32) {
+        const int r = lane - 16;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
+        atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], acc_term(v));
+      }
+      // Router records of this workgroup's rows, lanes 2s (logit) and 2s+1
+      // (bound).  The bound of the reference's serial fp32 dot:
+      //   |fl(x.w) - x.w| <= u (A + sum_k |s^_k|) (u = 2^-24, s^_k its own
+      //   partial sums), sum_k |s^_k| <= (P* + n u A)(1 + 2 n u) with P* the
+      //   exact prefixes' sum; and P* <= P (1 + 2^-19) + 2^-7 A for the fp32
+      //   P above (every prefix within 22 u A, n <= 4096), A* <= A (1 + 2^-18).
+      // The fp64 logit is within 1e-12 A; flushed denormals within 1e-30.
       if (lane < 2 * kRSlots) {
         const int s = lane >> 1;
         const int r = b + s * a.NB;
         if (s < a.rslots && r <= a.E) {
-          const double Lg = R.Lg[s];
-          double A = 0.0, P = 0.0;
+          double Lg = 0.0, A = 0.0, P = 0.0;
 #pragma unroll
           for (int w = 0; w < kW; w++) {
-            A += R.Ap[s][w];
-            P += R.Pp[s][w];
+            Lg += R.Lp[s][w];
+            A += (double)R.Ap[s][w];
+            P += (double)R.Pp[s][w];
           }
-          double B = 0x1p-24 * (A + P) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+          double B = 0x1p-24 * (A * (1.0 + 0x1p-6) + P) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-30;
           B = (B + fabs(Lg) * 0x1p-43) * (1.0 + 0x1p-40);
           const double v = (lane & 1) ? B : Lg;
+          // the tag replaces the low 8 bits of each double; the bound grows
+          // by more than the logit can move (2^-44 relative)
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r + (lane & 1),
                              with_tag((unsigned long long)__double_as_longlong(v), layer_tag(cs, l)), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
@@ -1036,6 +1113,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
     // ======================= stage S =======================
     {
+      const StackArgs a = kargs();
       SelLds &sel = *(SelLds *)S.u;
       double2 *lb = (double2 *)(S.u + ((sizeof(SelLds) + 15) & ~(size_t)15));
       unsigned long long *lk = (unsigned long long *)(lb + a.E + 1);
@@ -1119,38 +1197,22 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       {
         // the shared expert's gate, by the thread holding record E
         const int iE = E / kT;
-        if (t == E - iE * kT) rt.sg = sigmoid_ref((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])));
+        if (t == E - iE * kT) rt.sg = sigmoid_ref_t((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])), s_exp2);
       }
       lds_barrier();
       if (__builtin_expect(s_abort != 0, 0)) return;
-      // Every record of this layer is in, so every workgroup's shared gate/up
-      // sums are too (each adds them before tagging its records): waves 1..7
-      // load them now and build the shared hidden vector while wave 0 selects.
+      // The shared gate/up sums and row scales: waves 1..7 copy them into LDS
+      // (device-scope copies of the counted sums, no registers held) and build
+      // the shared hidden vector from there while wave 0 selects.
       float *hsh = (float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));  // [Ish]
-      int ag[kShPT], au[kShPT];
-      float gsv[kShPT], usv[kShPT];
-      auto sh_load = [&](int i0) {
-#pragma unroll
-        for (int q = 0; q < kShPT; q++) {
-          const int i = i0 + q * kStThreads;
-          ag[q] = au[q] = 0;
-          gsv[q] = usv[q] = 0.0f;
-          if (i < a.Ish) {
-            ag[q] = ld_agent(&acc[i]);
-            au[q] = ld_agent(&acc[a.Ish + i]);
-            gsv[q] = L.gs[i];
-            usv[q] = L.us[i];
-          }
-        }
-      };
-      if (wave != 0) sh_load(t - 64);
+      unsigned long long *acs = (unsigned long long *)(S.u + s_stage_offset(a.E, a.H, a.Ish, FMT));  // [2 * Ish]
+      float *scs = (float *)(acs + 2 * a.Ish);                                                       // [2 * Ish]
       // T0, found by every wave: the sample with exactly K-1 larger ones
       unsigned long long T0;
       {
         const int ns = nl * c;
         const unsigned long long sv = lane < ns ? sel.samp[lane] : 0ull;
-        int rk = 0;
-        for (int q = 0; q < ns; q++) rk += sel.samp[q] > sv;
+        const int rk = count_greater(sv, ns);
         const unsigned long long bal = __ballot(sv != 0ull && rk == K - 1);
         T0 = 1ull;  // (unreachable: the sample holds K keys) every key
         if (bal) {
@@ -1184,67 +1246,103 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         up = wave_max_u64(up);
         if (lane == 0) sel.wup[wave] = up;
       }
+      // (issued after this wave's last use of its records: the compiler's
+      // wait for those loads would otherwise wait for the copies too)
+      if (wave != 0) {
+        // 1 KB pieces: sums (Ish % 64 == 0: whole pieces), then each scale row
+        const int nck_a = (a.Ish * 16) >> 10, nck_s = (a.Ish * 4 + 1023) >> 10;
+        for (int c = wave - 1; c < nck_a + 2 * nck_s; c += kW - 1) {
+          if (c < nck_a) {
+            dma_b128_dev(acc + (size_t)c * 128 + 2 * lane, lds_addr(acs) + 1024 * c);
+          } else {
+            const int c2 = c - nck_a, m = c2 >= nck_s, j = c2 - m * nck_s;
+            const float *src = (m ? (const float *)L.us : (const float *)L.gs) + (size_t)j * 256 + 4 * lane;
+            if (16 * lane < a.Ish * 4 - 1024 * j) dma_b128(src, lds_addr(scs + m * a.Ish) + 1024 * j);
+          }
+        }
+      }
       lds_barrier();
       if (wave != 0) {
+        // the copies of waves 1..7 (each waits for its own, then counts in)
+        wait_dma();
+        if (lane == 0) atomicAdd(&s_shcnt, 1u);
         // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
+        const unsigned long long *acs = (const unsigned long long *)(S.u + s_stage_offset(a.E, a.H, a.Ish, FMT));
+        const float *scs = (const float *)(acs + 2 * a.Ish);
+        const unsigned target = (unsigned)(kW - 1) * (unsigned)(l + 1);
+        while (__hip_atomic_load(&s_shcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+          __builtin_amdgcn_s_sleep(1);
+        const float sx = s_misc[0];
+        auto swiglu = [&](int i, unsigned long long wg, unsigned long long wu) {
+          const float h = silu_ref_t((float)acc_sum(wg) * scs[i] * sx, s_exp2) * ((float)acc_sum(wu) * scs[a.Ish + i] * sx);
+          hsh[i] = h;
+          return fabsf(h);
+        };
+        // from LDS only: a global load in this loop would make the compiler
+        // wait for every outstanding load (the copies included) first
         float hm = 0.0f;
-        for (int i0 = t - 64; i0 < a.Ish; i0 += kShPT * kStThreads) {
-          if (i0 != t - 64) sh_load(i0);
-#pragma unroll
-          for (int q = 0; q < kShPT; q++) {
-            const int i = i0 + q * kStThreads;
-            if (i < a.Ish) {
-              const float h = silu_ref((float)ag[q] * gsv[q] * sx) * ((float)au[q] * usv[q] * sx);
-              hsh[i] = h;
-              hm = fmaxf(hm, fabsf(h));
+        bool missing = false;
+        for (int i = t - 64; i < a.Ish; i += kT - 64) {
+          const unsigned long long wg = acs[i], wu = acs[a.Ish + i];
+          missing = missing || acc_parts(wg) != a.KQ || acc_parts(wu) != a.KQ;
+          hm = fmaxf(hm, swiglu(i, wg, wu));
+        }
+        if (__builtin_expect(__any(missing), 0)) {
+          // a sum still missing parts: read again from memory until complete
+          hm = 0.0f;
+          for (int i = t - 64; i < a.Ish; i += kT - 64) {
+            unsigned long long wg = acs[i], wu = acs[a.Ish + i];
+            const long long t0 = (long long)wall_clock64();
+            for (unsigned it = 0; acc_parts(wg) != a.KQ || acc_parts(wu) != a.KQ; it++) {
+              if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
+                s_abort = 1;
+                break;
+              }
+              wg = ld_agent_sync(&acc[i]);
+              wu = ld_agent_sync(&acc[a.Ish + i]);
             }
+            hm = fmaxf(hm, swiglu(i, wg, wu));
           }
         }
         hm = wave_max_dpp(hm);
         if (lane == 0) rt.shm[wave] = hm;
       } else {
         const int M = sel.nmc;
-        if (__builtin_expect(M > 64, 0)) {
+        if (__builtin_expect(M > 64 || M < K, 0)) {
           if (lane == 0) rt.state = 2;
         } else {
-          // rank of each candidate among the candidates
+          // every candidate in a lane: key, record (logit, bound), rank among
+          // the candidates (ranks by register broadcasts, no LDS round trips)
           const unsigned long long ck = lane < M ? sel.mc[lane] : 0ull;
-          int rk = 0;
-          for (int q = 0; q < M; q++) rk += sel.mc[q] > ck;
-          if (lane < M && rk < K) sel.cand[rk] = (int)(~(unsigned)ck);
-          // the largest upper bound outside the top K
+          const int ce = lane < M ? (int)(~(unsigned)ck) : 0;
+          const double2 v = lb[ce];
+          const int rk = count_greater(ck, M);
+          // the largest upper bound outside the top K: candidates ranked K
+          // and below, and every wave's bound of the keys below T0
           unsigned long long upk = lane < kW ? sel.wup[lane] : 0ull;
           if (lane < M && rk >= K) {
-            const double2 v = lb[(int)(~(unsigned)ck)];
             const unsigned long long k2 = double_key(v.x + v.y);
             upk = k2 > upk ? k2 : upk;
           }
           upk = wave_max_u64(upk);
-          __builtin_amdgcn_wave_barrier();
-          // certification, one candidate per lane (K <= 16: lanes 0..15)
-          const int ce = sel.cand[lane < K ? lane : 0];
-          const double2 v = lb[ce];
-          const double vlo = v.x - v.y;
-          const double mx = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), 0),
-                                             __builtin_amdgcn_readlane(__double2loint(v.x), 0));
-          const double mxy = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.y), 0),
-                                              __builtin_amdgcn_readlane(__double2loint(v.y), 0));
+          // the candidates in rank order (a forward permute: lane r receives
+          // the candidate of rank r; lanes past M keep their own)
+          const int pa = 4 * (lane < M ? rk : lane);
+          const double sL = permute_d(pa, v.x), sB = permute_d(pa, v.y);
+          const int se = __builtin_amdgcn_ds_permute(pa, ce);
+          const double vlo = sL - sB;
+          const double mx = readlane_d(sL, 0), mxy = readlane_d(sB, 0);
           // The lowest lower bound among the K candidates and their largest
           // magnitude.  When every consecutive pair is certified the lower
           // bounds fall with the rank and theta is the K-th one; otherwise a
           // candidate ranked above K-1 may have the lowest lower bound, and
           // the set test must use that one.
-          double theta = 1e300, kax = 0.0;
-          for (int r = 0; r < K; r++) {
-            theta = fmin(theta, __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(vlo), r),
-                                                 __builtin_amdgcn_readlane(__double2loint(vlo), r)));
-            kax = fmax(kax, fabs(__hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v.x), r),
-                                                  __builtin_amdgcn_readlane(__double2loint(v.x), r))));
-          }
+          const double theta = row16_min_d(lane < K ? vlo : 1e300);
+          const double kax = row16_max_d(lane < K ? fabs(sL) : 0.0);
           // the next candidate's bounds (row shift left within lanes 0..15)
-          const double nx = dpp_row_shl1_d(v.x), ny = dpp_row_shl1_d(v.y);
+          const double nx = dpp_row_shl1_d(sL), ny = dpp_row_shl1_d(sB);
           bool pair_ok = true;
-          if (lane + 1 < K) pair_ok = vlo - (nx + ny) > order_margin(v.x, nx, mx);
+          if (lane + 1 < K) pair_ok = vlo - (nx + ny) > order_margin(sL, nx, mx);
           // The set of K is certified by the lowest lower bound among the K
           // against every other expert's upper bound; their order by the
           // pairs.  Without a route output (a stack call) the order only
@@ -1260,10 +1358,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           if (ok) {
             // softmax over the K (lanes 0..15 hold them): fp32 suffices for
             // the weights' 1e-5 tolerance
-            const float ev = lane < K ? __expf((float)(v.x - mx)) : 0.0f;
+            const float ev = lane < K ? __expf((float)(sL - mx)) : 0.0f;
             const float den = row16_sum(ev);
             if (lane < K) {
-              rt.idx[lane] = ce;
+              rt.idx[lane] = se;
               rt.w[lane] = ev / den;
             }
           } else {
@@ -1378,7 +1476,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           if (lane == 0) sel.mx = m;
         }
         lds_barrier();
-        for (int e = t; e < E; e += kT) lgs[e] = expf_glibc(lgs[e] - sel.mx);
+        for (int e = t; e < E; e += kT) lgs[e] = expf_glibc_t(lgs[e] - sel.mx, s_exp2);
         lds_barrier();
         if (t == 0) {
           float den = 0.0f;
@@ -1431,6 +1529,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
     // ======================= stage G =======================
     {
+      const StackArgs a = kargs();
       float(*red)[2][16] = (float(*)[2][16])S.u;                 // [2][kW][gate, up][16] partials
       unsigned *stage = (unsigned *)(S.u + 2 * kW * 2 * 16 * 4);  // [kW][8] packed digits
       const int nU = a.K * a.nrt_i;
@@ -1442,6 +1541,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // 1 KB pieces, kGRing-1 records in flight while one is computed.
       constexpr int kSlotG = 2 * TGC + 128;
       constexpr int kGChunks = (kSlotG + 1023) / 1024;
+      static_assert(kGChunks * (kGRing - 1) <= 30, "stage G: ring waits within wait_vm's range");
       static_assert(kGHead >= 2 * kW * 2 * 16 * 4 + kW * 8 * 4, "stage G head");
       unsigned char *ring = S.u + kGHead + (size_t)wave * kGRing * kSlotG;
       // Units go round-robin over the workgroups.  When the last round would
@@ -1472,10 +1572,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
       // Issue cursor (entry iu, group gu, ring slot su).  Every step issues the
-      // kGChunks copies of one record; past the last item it keeps re-reading
-      // the last entry's records (in bounds, never consumed), so that exactly
-      // kGRing-1 items are always in flight and one wait count serves all.
-      int iu = 0, gu = 0, su = 0, glen = ent_len(0);
+      // kGChunks copies of one record, up to kGRing-1 items ahead of the one
+      // consumed, and none past the last item.
+      int iu = 0, gu = 0, su = 0, glen = ent_len(0), issued = 0;
       const unsigned char *cb = (const unsigned char *)L.experts;
       auto unit_base = [&](int i) {
         const int ii = i < nent ? i : nent - 1;
@@ -1485,6 +1584,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         glen = ent_len(ii);
       };
       auto issue_next = [&]() {
+        if (issued == nitems) return;
+        issued++;
         const unsigned slot = lds_addr(ring + su * kSlotG);
 #pragma unroll
         for (int k = 0; k < kGChunks; k++)
@@ -1581,21 +1682,27 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // vector (built in stage S) once the routed work is done.
       signed char *gdsh = (signed char *)(ring - (size_t)wave * kGRing * kSlotG + (size_t)kW * kGRing * kSlotG);
       const int tile = b, ntiles = a.H / kTileRows;
-      if (tile < ntiles)
-        for (int r = wave; r < kTileRows; r += kW)
-          for (int c0 = 0; c0 < a.Ish; c0 += 1024)
-            if (c0 + 16 * lane < a.Ish)
-              dma_b128((const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
-                       lds_addr(gdsh + (size_t)r * (a.Ish + 16) + c0));
+      auto issue_shdown = [&]() {
+        if (tile < ntiles)
+          for (int r = wave; r < kTileRows; r += kW)
+            for (int c0 = 0; c0 < a.Ish; c0 += 1024)
+              if (c0 + 16 * lane < a.Ish)
+                dma_b128((const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
+                         lds_addr(gdsh + (size_t)r * (a.Ish + 16) + c0));
+      };
+      // behind the first entry's records when there is one: the routed
+      // records are the ones the first computations wait for
+      if (!SW_SHDOWN_LATE || nent == 0) issue_shdown();
       if (nitems > 0) {
         unit_base(0);
 #pragma unroll
         for (int k = 0; k < kGRing - 1; k++) issue_next();
       }
+      float *hsh = (float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));
       {
         // qrow_i8 of the shared hidden vector (operand of the shared down
-        // projection below), while the first copies are in flight
-        const float *hsh = (const float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));
+        // projection at the end of this stage), while the first copies are in
+        // flight
         float shx = 0.0f;
 #pragma unroll
         for (int w = 1; w < kW; w++) shx = fmaxf(shx, rt.shm[w]);
@@ -1605,7 +1712,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
         if (t == 0) s_misc[1] = shx;
       }
-      int csl = 0;  // consume slot
+      int csl = 0, consumed = 0;  // consume slot, items consumed
       for (int i = 0; i < nent; i++) {
         const int glo = (has_half && i == 0) ? hlo : 0, ghi = glo + ent_len(i);
         float accg[4] = {0, 0, 0, 0}, accu[4] = {0, 0, 0, 0};
@@ -1614,10 +1721,12 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           for (int gi = 0; gi < kGMax; gi++)
             if (gi >= glo && gi < ghi) {
               issue_next();
-              // this item's copies are done once at most the kGChunks(kGRing-1)
-              // issued after them are outstanding (a wave's loads complete in
-              // order; a store of finish_unit only makes the wait longer)
-              asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kGChunks * (kGRing - 1)) : "memory");
+              // this item's copies are done once at most the copies of the
+              // items issued after it are outstanding (a wave's memory
+              // operations complete in order; a store of finish_h only makes
+              // the wait longer)
+              wait_vm(kGChunks * (issued - consumed - 1));
+              consumed++;
               const unsigned char *rec = ring + csl * kSlotG;
               g_item<FMT>(rec, rec + 2 * TGC, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], accg, lane);
               g_item<FMT>(rec + TGC, rec + 2 * TGC + 64, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], accu, lane);
@@ -1625,6 +1734,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             }
         }
         finish_entry(accg, accu, i);
+        if (SW_SHDOWN_LATE && i == 0) issue_shdown();
       }
       if (has_half && !half && wave == 0 && lane < 16) {
         // the partner's half of the split unit (published long ago: it was its
@@ -1678,6 +1788,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 
     // ======================= stage D (loads, then barrier h) =======================
     {
+      const StackArgs a = kargs();
       const DLayout dl = d_layout(a.K, a.ngi, a.Ish, FMT);
       constexpr int BPL = FMT == 4 ? 16 : 12;
       constexpr int kSlot = 64 * BPL + 64;  // one tile-group: codes, then 16 row scales
@@ -1833,6 +1944,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           compute(o0);
           if (two) compute(o1);
         }
+        // the next layer's stage R inputs, loaded while this stage finishes
+        // (HBM is otherwise idle then)
+        if (l + 1 < a.n) static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sh_task_lds(s_sht), sreg, t);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float v = row16_sum(tot[r]);
@@ -1852,6 +1966,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
+      } else if (l + 1 < a.n) {
+        static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sh_task_lds(s_sht), sreg, t);
       }
       lds_barrier();
     }
@@ -1861,9 +1977,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     if (l + 1 < a.n) {
       lds_barrier();
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
-      // waves 1..7: the next layer's stage R inputs, loaded while the grid
-      // finishes this layer (the memory system is otherwise idle then)
-      static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sreg, t);
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarY), a) ? 1 : 0;
       lds_barrier();
       if (__builtin_expect(!rt.flag, 0)) return;
@@ -1899,8 +2012,8 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
 // Bytes of the stage-local LDS union: the largest of stage R's inputs,
 // the selection's arrays, stage G's ring and stage D's layout.
 static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, int fmt, int rslots, int shkc) {
-  const size_t rlay = r_layout(rslots, H, shkc).end;
-  const size_t sel = s_hsh_offset(E, H, Ish, fmt) + (size_t)Ish * 4;
+  const size_t rlay = r_lds_bytes();
+  const size_t sel = s_stage_offset(E, H, Ish, fmt) + s_stage_bytes(Ish);
   const size_t dst = d_layout(K, ngi, Ish, fmt).end;
   const size_t ring = g_region_end(Ish, fmt);
   size_t u = rlay;
@@ -1939,7 +2052,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   const int KQ = stack_kq(NB, H, E, Ish);
   if (2 * (Ish / kTileRows) * KQ > E + 1) return false;              // tasks' workgroups own records
   const int shkc = (H / 64 + KQ - 1) / KQ;
-  if ((size_t)rslots * H * 4 + (size_t)shkc * 1024 > (size_t)16 * kStRegs * kStThreads) return false;  // registers
+  if ((shkc + kW - 1) / kW > kShMaxKc) return false;                 // shared task A operands in registers
   const size_t u = stack_union_bytes(E, H, K, ngh, ngi, Ish, s.expert_format, rslots, shkc);
   return lds_fixed(Hp, ngh, Ish) + u + 1024 <= (size_t)ctx->shared_per_block;
 }
@@ -1955,7 +2068,7 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
   // counters and the shared expert's integer sums
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
-  const size_t per_layer = ((size_t)kBars * kBarWords + acc_words) * 2 * 4;
+  const size_t per_layer = ((size_t)kBars * kBarWords * 4 + acc_words * 8) * 2;
   if (n > ctx->stack_cap_layers) {
     hipError_t e = hipSuccess;
     if (ctx->stack_sync) e = hipStreamSynchronize(ctx->stream);
@@ -2033,7 +2146,7 @@ int stack_check_abort(ColiCuda *ctx) {
   if (!ctx->stack_abort_host || !*ctx->stack_abort_host) return 0;
   // clear the device state the aborted call left behind
   *ctx->stack_abort_host = 0;
-  const size_t per_layer = ((size_t)kBars * kBarWords + 2 * (size_t)kStackMaxIsh) * 2 * 4;
+  const size_t per_layer = ((size_t)kBars * kBarWords * 4 + 2 * (size_t)kStackMaxIsh * 8) * 2;
   (void)hipMemsetAsync(ctx->stack_sync, 0, per_layer * ctx->stack_cap_layers, ctx->stream);
   (void)hipMemsetAsync(ctx->stack_abort, 0, 256, ctx->stream);
   if (ctx->scratch[kScrStack])  // tagged words an aborted call left behind
@@ -2093,7 +2206,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kSplitRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
-  a.acc = (int *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
+  a.acc = (unsigned long long *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
   a.acc_stride = acc_words;
   a.state = (unsigned *)(scr + kRecRegion + kExRegion);
   a.abort_word = (unsigned *)ctx->stack_abort;

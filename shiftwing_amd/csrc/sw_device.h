@@ -37,7 +37,9 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3fef3720dcef9069ULL, 0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL,
     0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+// The table may be passed in: a kernel that keeps a copy in LDS reads it
+// without waiting behind its own outstanding global loads.
+__device__ __forceinline__ float expf_glibc_t(float x, const uint64_t *tab) {
   // Special cases first (glibc: NaN propagates, overflow -> inf,
   // x < -0x1.9fe368p6 underflows to +0).
   if (!(x == x)) return x + x;
@@ -54,7 +56,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
   uint64_t ki = __builtin_bit_cast(uint64_t, kd);
   kd -= kShift;
   double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki & 31];
+  uint64_t t = tab[ki & 31];
   t += ki << (52 - 5);
   double s = __builtin_bit_cast(double, t);
   double z = __builtin_fma(kC0, r, kC1);
@@ -65,15 +67,19 @@ __device__ __forceinline__ float expf_glibc(float x) {
   return (float)y;
 }
 
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
+
 // sigmoidf_stable / siluf, c/qwen.c:307-308, bit-exact with glibc expf.
-__device__ __forceinline__ float sigmoid_ref(float x) {
+__device__ __forceinline__ float sigmoid_ref_t(float x, const uint64_t *tab) {
   if (x >= 0.0f) {
-    float z = expf_glibc(-x);
+    float z = expf_glibc_t(-x, tab);
     return 1.0f / (1.0f + z);
   }
-  float z = expf_glibc(x);
+  float z = expf_glibc_t(x, tab);
   return z / (1.0f + z);
 }
+__device__ __forceinline__ float sigmoid_ref(float x) { return sigmoid_ref_t(x, kExp2Tab); }
+__device__ __forceinline__ float silu_ref_t(float x, const uint64_t *tab) { return x * sigmoid_ref_t(x, tab); }
 __device__ __forceinline__ float silu_ref(float x) { return x * sigmoid_ref(x); }
 
 // ---------------------------------------------------------------------------
