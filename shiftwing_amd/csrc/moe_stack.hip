@@ -1713,7 +1713,17 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (t == 0) s_misc[1] = shx;
       }
       int csl = 0, consumed = 0;  // consume slot, items consumed
+      // the split unit's partner half (workgroups 2k): its two words are
+      // read while the last entry computes (first used after every copy has
+      // landed, so the compiler's wait for them waits for nothing else)
+      const bool partner = has_half && !half && wave == 0 && lane < 16;
+      const unsigned long long *pw = a.spl + ((size_t)(b >> 1) * 16 + (lane & 15)) * 2;
+      unsigned long long pvg = 0ull, pvu = 0ull;
       for (int i = 0; i < nent; i++) {
+        if (i == nent - 1 && partner) {
+          pvg = ld_agent(pw);
+          pvu = ld_agent(pw + 1);
+        }
         const int glo = (has_half && i == 0) ? hlo : 0, ghi = glo + ent_len(i);
         float accg[4] = {0, 0, 0, 0}, accu[4] = {0, 0, 0, 0};
         if (n > 0) {
@@ -1736,24 +1746,22 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         finish_entry(accg, accu, i);
         if (SW_SHDOWN_LATE && i == 0) issue_shdown();
       }
-      if (has_half && !half && wave == 0 && lane < 16) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every copy (and the partner words) has landed
+      if (partner) {
         // the partner's half of the split unit (published long ago: it was its
         // first entry), added to this workgroup's in a fixed order
-        const unsigned long long *w = a.spl + ((size_t)(b >> 1) * 16 + lane) * 2;
         const unsigned tag = layer_tag(cs, l);
-        unsigned long long vg = ld_agent(w), vu = ld_agent(w + 1);
         const long long t0 = (long long)wall_clock64();
-        for (unsigned it = 0; (unsigned)(vg >> 32) != tag || (unsigned)(vu >> 32) != tag; it++) {
+        for (unsigned it = 0; (unsigned)(pvg >> 32) != tag || (unsigned)(pvu >> 32) != tag; it++) {
           if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
             s_abort = 1;
             break;
           }
-          vg = ld_agent(w);
-          vu = ld_agent(w + 1);
+          pvg = ld_agent_sync(pw);
+          pvu = ld_agent_sync(pw + 1);
         }
-        finish_h(gh + __uint_as_float((unsigned)vg), uh + __uint_as_float((unsigned)vu), hu);
+        finish_h(gh + __uint_as_float((unsigned)pvg), uh + __uint_as_float((unsigned)pvu), hu);
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the last item
       lds_barrier();  // the last finisher is done with its partials; every copy has landed
       if (__builtin_expect(s_abort != 0, 0)) return;
       // shared down: exact int32 dots of the tile's 16 rows with hq, into
