@@ -115,6 +115,43 @@ def test_batched_stack_equals_layer_calls(be):
         assert np.array_equal(ys[l].view(np.uint32), y1.view(np.uint32)), l
 
 
+@pytest.mark.parametrize("T", [2, 4, 6])
+def test_small_batch_stack_runs_token_by_token(be, oracle, T):
+    """coli_cuda_moe_forward_layers with 2..6 tokens runs the persistent decode
+    kernel once per token: bit for bit the one-token calls, and each layer
+    within the tolerance of the oracle's moe_forward (c/qwen.c:3717-3739)."""
+    import ctypes as C
+
+    from conftest import assert_close_rms
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish, fmt = S35
+    nl = 2
+    layers, hls = [], []
+    for l in range(nl):
+        L = MoeLayer(be, H, E, K, I, Ish, fmt)
+        L.synthesize(91, l)
+        layers.append(L)
+        hls.append(oracle.host_layer(91, l, H, E, K, I, Ish, fmt))
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((nl, T, H)).astype(np.float32)
+    dx = be.upload(x)
+    dy = be.alloc(x.nbytes)
+    arr = (C.c_void_p * nl)(*[L.h.value for L in layers])
+    print(f"[small batch stack] T={T}", flush=True)
+    be.check(be.lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, dy.p, dx.p, T, T * H, T * H), "forward_layers")
+    ys = be.download(dy, (nl, T, H), np.float32)
+    for t in range(T):
+        d1 = be.alloc(nl * H * 4)
+        dxt = be.upload(np.ascontiguousarray(x[:, t, :]))
+        be.check(be.lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, d1.p, dxt.p, 1, H, H), "forward_layers 1")
+        y1 = be.download(d1, (nl, H), np.float32)
+        assert np.array_equal(ys[:, t, :].view(np.uint32), y1.view(np.uint32)), t
+    for l in range(nl):
+        for t in range(T):
+            want = oracle.moe_forward(hls[l], x[l, t])
+            assert_close_rms(ys[l, t], want, 1e-3, f"layer {l} token {t}")
+
+
 @pytest.mark.parametrize("shape,T", [((512, 32, 4, 128, 128, 3), 4100), ((512, 1024, 8, 128, 128, 4), 1300)],
                          ids=["E32_T4100", "E1024_T1300"])
 def test_long_block_runs_in_steps(be, oracle, shape, T):
