@@ -421,6 +421,44 @@ def measure_decode(be, stack, cfg, steps, warmup, zipf_rec, workload_key, decode
     }
 
 
+STAMP_NAMES = ["router_done", "router_workgroup_barrier", "selection_done", "routed_gateup_done",
+               "hidden_barrier_passed", "down_done", "layer_barrier_passed"]
+
+
+def stack_stamps(be, stack, cfg, steps=8):
+    """Per-stage stamps of the persistent decode kernel (coli_cuda_moe_stack_trace):
+    median and slowest-workgroup microseconds from each layer's start, over the
+    inner layers of `steps` further decode steps (after the timed region)."""
+    H, E, K, I, Ish, fmt, layers, seed, desc = cfg
+    lib = be.lib
+    sm, lds = C.c_int(), C.c_int()
+    be.check(lib.coli_cuda_device_limits(be.ctx, C.byref(sm), C.byref(lds)), "device_limits")
+    NB, KS = sm.value, 8
+    xs = be.alloc(layers * steps * H * 4)
+    for l in range(layers):
+        be.check(lib.coli_cuda_synth_activations(be.ctx, C.c_void_p(xs.ptr + l * steps * H * 4), steps, H,
+                                                 C.c_ulonglong(seed + 1), l, 0))
+    ys = be.alloc(layers * H * 4)
+    arr = (C.c_void_p * layers)(*[L.h.value for L in stack])
+    words = layers * NB * KS
+    tr = be.alloc(words * 8)
+    be.check(lib.coli_cuda_moe_stack_trace(be.ctx, tr.p, words))
+    rel = []
+    for s_ in range(steps):
+        be.check(lib.coli_cuda_moe_forward_layers(be.ctx, arr, layers, ys.p, C.c_void_p(xs.ptr + s_ * H * 4), 1,
+                                                  steps * H, H), "forward_layers")
+        be.sync()
+        t = be.download(tr, (layers, NB, KS), np.uint64).astype(np.int64)
+        rel.append((t[1:layers - 1] - t[1:layers - 1, :, 0:1]) / 100.0)
+    be.check(lib.coli_cuda_moe_stack_trace(be.ctx, None, 0))
+    r = np.stack(rel)
+    out = {}
+    for k, name in enumerate(STAMP_NAMES, start=1):
+        v = r[..., k].ravel()
+        out[name] = {"median_us": round(float(np.median(v)), 2), "max_us": round(float(v.max()), 2)}
+    return out
+
+
 def measure_many(be, stack, cfg, T, prefill, steps, warmup, zipf_rec, workload_key):
     """Configs 3 and 4: T tokens per MoE step through the many-token kernels
     (bucketing, grouped gate/up and down, combine); a prefill step is one
@@ -666,6 +704,9 @@ def main():
                          "2: the three per-layer decode kernels")
     ap.add_argument("--item-tokens", type=int, default=0, choices=[0, 8, 16],
                     help="many-token steps: tokens per expert item (0 automatic; for measurement)")
+    ap.add_argument("--stamps", action="store_true",
+                    help="--workload s397/s35: add the persistent kernel's per-stage stamps (measured after the "
+                         "timed region) under step.stage_stamps")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="time a plain device-to-device copy of MIB MiB (the counter calibration kernel) and exit")
     args = ap.parse_args()
@@ -711,6 +752,8 @@ def main():
         stack = build_stack(be, "s35", cfg[6])
         zipf_rec = apply_zipf(be, stack, cfg)
         r = measure_decode(be, stack, cfg, args.steps, args.warmup, zipf_rec, "s35", args.decode_kernels)
+        if args.stamps:
+            r["step"]["stage_stamps"] = stack_stamps(be, stack, cfg)
         r = with_cpu(r, args, lambda: cpu_baseline(cfg, args.cpu_seconds, zipf_rec))
         print(json.dumps(headline(r, args)), flush=True)
         return
@@ -722,6 +765,8 @@ def main():
     progress(f"S397 stack resident in {gen_s:.1f} s")
     r2 = measure_decode(be, s397, cfg2, args.steps, args.warmup, None, "s397", args.decode_kernels)
     progress(f"config 2 decode: {r2['value']} tok/s")
+    if args.stamps:
+        r2["step"]["stage_stamps"] = stack_stamps(be, s397, cfg2)
     r2["step"]["weight_generation_s"] = round(gen_s, 1)
     r2 = with_cpu(r2, args, lambda: cpu_baseline(cfg2, args.cpu_seconds))
     progress("config 2 CPU baseline done")
