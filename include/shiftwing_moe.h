@@ -435,7 +435,9 @@ int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
  * decode order: layer l+1 starts after layer l's output is written.  With
  * tokens == 1 and layers of one shape this is one persistent kernel that
  * needs every compute unit of the device for the duration of the call; a
- * call that cannot get them reports an error at the next coli_cuda_sync. */
+ * call that cannot get them reports an error at the next coli_cuda_sync.
+ * With 2..6 tokens the persistent kernel runs once per token (the tokens
+ * are independent), which is faster than one many-token step per layer. */
 int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers,
                                  int n_layers, float *y, const float *x,
                                  int tokens, size_t x_layer_stride,
