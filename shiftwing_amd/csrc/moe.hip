@@ -304,9 +304,88 @@ size_t carve(Work &w, char *base) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. activation prep: IDOT quantisation + routed digits; grid T, 256 threads
+// 1. activation prep: IDOT quantisation + routed digits.  The row is read once
+// into registers: C float4 chunks per thread (1024 threads, padded row of up
+// to C*4096 values); a group of 128 values is one half-wave's 32 chunks.
+// grid T, 1024 threads.  Rows longer than 32768 take k_prep_x_any.
 // ---------------------------------------------------------------------------
-__global__ void k_prep_x(Work w, const float *x) {
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ int half_wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ unsigned pack_i8x4(int a, int b, int c, int d) {
+  return (unsigned)(a & 255) | ((unsigned)(b & 255) << 8) | ((unsigned)(c & 255) << 16) | ((unsigned)d << 24);
+}
+
+template <int C>
+__global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x) {
+  __shared__ float red[16];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const float *xt = x + (size_t)t * w.H;
+  if (t == 0 && tid == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
+  const int nq = w.H / 4, nqp = w.ngh * 32;  // float4 chunks of the row, of the padded row
+  const bool al = ((uintptr_t)xt & 15) == 0;
+  float4 v[C];
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int i = tid + 1024 * c;
+    v[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (i < nq) v[c] = al ? *(const float4 *)(xt + 4 * i) : make_float4(xt[4 * i], xt[4 * i + 1], xt[4 * i + 2], xt[4 * i + 3]);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+  }
+  // qrow_i8 (c/qwen.c:1696): s = max|x|/127 (at least 1e-12), q = rint(x/s)
+  m = wave_max(m);
+  if (lane == 0) red[tid >> 6] = m;
+  __syncthreads();
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) a = fmaxf(a, red[i]);
+  float sx = a / 127.0f;
+  if (sx < 1e-12f) sx = 1e-12f;
+  const float inv = 1.0f / sx;
+  if (tid == 0) w.sx[t] = sx;
+  unsigned *xq = (unsigned *)(w.xq + (size_t)t * w.H);
+  unsigned *d1 = (unsigned *)(w.xd1 + (size_t)t * w.Hp), *d2 = (unsigned *)(w.xd2 + (size_t)t * w.Hp);
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int i = tid + 1024 * c;
+    if (i < nq)
+      xq[i] = pack_i8x4((int)__builtin_rintf(v[c].x * inv), (int)__builtin_rintf(v[c].y * inv),
+                        (int)__builtin_rintf(v[c].z * inv), (int)__builtin_rintf(v[c].w * inv));
+    // two digits per value of the group (half-wave), as quantize_digits
+    if (i < nqp) {  // uniform over the half-wave: nqp and 1024 are multiples of 32
+      const float amax = half_wave_max(fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+      const float A = amax / 127.0f, B = A / 254.0f;
+      int q1[4] = {0, 0, 0, 0}, q2[4] = {0, 0, 0, 0};
+      if (amax > 0.0f) {
+        const float invA = 127.0f / amax, invB = 254.0f / A;
+        const float e[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          q1[k] = (int)fminf(fmaxf(__builtin_rintf(e[k] * invA), -127.0f), 127.0f);
+          const float r = __builtin_fmaf(-(float)q1[k], A, e[k]);
+          q2[k] = (int)fminf(fmaxf(__builtin_rintf(r * invB), -127.0f), 127.0f);
+        }
+      }
+      d1[i] = pack_i8x4(q1[0], q1[1], q1[2], q1[3]);
+      d2[i] = pack_i8x4(q2[0], q2[1], q2[2], q2[3]);
+      const int Q1 = half_wave_sum_i(q1[0] + q1[1] + q1[2] + q1[3]);
+      const int Q2 = half_wave_sum_i(q2[0] + q2[1] + q2[2] + q2[3]);
+      if ((lane & 31) == 0) w.xgp[(size_t)t * w.ngh + i / 32] = make_float4(A, B, __int_as_float(Q1), __int_as_float(Q2));
+    }
+  }
+}
+
+// Any row length: quantize_digits and qrow_i8_block read the row from memory.
+// grid T, 1024 threads.
+__global__ void k_prep_x_any(Work w, const float *x) {
   __shared__ float red[16];
   int t = blockIdx.x;
   const float *xt = x + (size_t)t * w.H;
@@ -787,40 +866,40 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
   }
   up = wave_max_d(up);
   upi = wave_max_i(upi);
-  // lane 0 certifies; every lane needs the verdict for the targeted set
-  int verdict = 0;
-  double lo = 0.0;
-  if (lane == 0) {
-    double mx = cv[0].x;
-    bool ok = mode == 0 && w.K <= w.E;
-    for (int r = 0; r + 1 < w.K; r++) {
-      double2 a = cv[r], b = cv[r + 1];
-      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
-      ok = ok && (a.x - a.y) - (b.x + b.y) > margin;
-    }
-    if (ok && upi >= 0) {
-      double2 a = cv[w.K - 1];
-      double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(up) + 2.0 * fabs(mx));
-      ok = (a.x - a.y) - up > margin;
-    }
-    if (ok) ok = (cv[w.K - 1].x - cv[w.K - 1].y) - (mx + cv[0].y) > -80.0;
-    verdict = ok ? 1 : 0;
-    if (ok) {
-      double den = 0.0;
-      for (int r = 0; r < w.K; r++) den += exp(cv[r].x - mx);
-      for (int r = 0; r < w.K; r++) {
-        w.idx[(size_t)t * w.K + r] = cand[r];
-        w.w[(size_t)t * w.K + r] = (float)(exp(cv[r].x - mx) / den);
-      }
-    } else if (mode == 0 && w.K <= w.E) {
-      lo = __builtin_huge_val();
-      for (int r = 0; r < w.K; r++) lo = fmin(lo, cv[r].x - cv[r].y);
-      verdict = 2;
-    }
+  // the consecutive pairs (lane r: ranks r and r+1), the set against the
+  // largest outside upper bound and the softmax range, all lane-parallel;
+  // then the weights from the fp64 logits, one exp per lane
+  const double mx = cv[0].x;
+  bool pair = true;
+  if (lane + 1 < w.K) {
+    const double2 a = cv[lane], b = cv[lane + 1];
+    const double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
+    pair = (a.x - a.y) - (b.x + b.y) > margin;
   }
-  verdict = __shfl(verdict, 0, 64);
+  bool ok = mode == 0 && w.K <= w.E && __all(pair);
+  const double2 aK = cv[w.K - 1];
+  if (ok && upi >= 0) {
+    const double margin = 0x1p-20 * (1.0 + fabs(aK.x) + fabs(up) + 2.0 * fabs(mx));
+    ok = (aK.x - aK.y) - up > margin;
+  }
+  if (ok) ok = (aK.x - aK.y) - (mx + cv[0].y) > -80.0;
+  int verdict = ok ? 1 : 0;
+  double lo = 0.0;
+  if (ok) {
+    const double ev = lane < w.K ? exp(cv[lane].x - mx) : 0.0;
+    const double den = wave_sum(ev);
+    if (lane < w.K) {
+      w.idx[(size_t)t * w.K + lane] = cand[lane];
+      w.w[(size_t)t * w.K + lane] = (float)(ev / den);
+    }
+  } else if (mode == 0 && w.K <= w.E) {
+    lo = lane < w.K ? cv[lane].x - cv[lane].y : __builtin_huge_val();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lo = fmin(lo, __shfl_xor(lo, o, 64));
+    verdict = 2;
+  }
   if (verdict == 2) {
-    lo = __shfl(lo, 0, 64) - 0x1p-20 * (1.0 + 4.0 * amax);
+    lo = lo - 0x1p-20 * (1.0 + 4.0 * amax);
     int base = 0;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
@@ -863,6 +942,30 @@ __device__ float exact_chain(const float *xt, const float *row, int H) {
   return s;
 }
 
+// prod[i] = rn(x[i]*row[i]) for i < m (m % 4 == 0) by the block's 64 lanes:
+// kProdBatch float4 pairs of loads in flight per lane before the first store
+constexpr int kProdBatch = 8;
+__device__ __forceinline__ void form_products(const float *xt, const float *row, int m, float *prod) {
+  for (int i0 = threadIdx.x * 4; i0 < m; i0 += 256 * kProdBatch) {
+    float4 a[kProdBatch], b[kProdBatch];
+#pragma unroll
+    for (int u = 0; u < kProdBatch; u++) {
+      const int i = i0 + 256 * u;
+      if (i < m) {
+        a[u] = *(const float4 *)(xt + i);
+        b[u] = *(const float4 *)(row + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kProdBatch; u++) {
+      const int i = i0 + 256 * u;
+      if (i < m)
+        *(float4 *)(prod + i) = make_float4(__fmul_rn(a[u].x, b[u].x), __fmul_rn(a[u].y, b[u].y),
+                                            __fmul_rn(a[u].z, b[u].z), __fmul_rn(a[u].w, b[u].w));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 4. exact logits for the tokens the bounds did not certify: the experts of
 // the targeted set (certified 2) or every expert (certified 0).  The products
@@ -884,11 +987,7 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
     for (int k = blockIdx.x; k < n; k += gridDim.x) {
       const int e = w.mset[(size_t)t * 64 + k];
       const float *row = router + (size_t)e * w.H;
-      for (int i = threadIdx.x * 4; i < m; i += 256) {
-        float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
-        *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
-                                            __fmul_rn(a.w, b.w));
-      }
+      form_products(xt, row, m, prod);
       __syncthreads();
       if (threadIdx.x == 0) {
         float s = 0.0f;
@@ -991,24 +1090,26 @@ __global__ __launch_bounds__(64) void k_topk_check(Work w, unsigned long long *s
       sl[rank] = l;
     }
     __syncthreads();
-    if (i == 0) {
+    {
+      // lane r checks ranks r and r+1; the weights one exp per lane
       const double mx = sl[0];
-      bool ok = n >= w.K;
-      for (int r = 0; ok && r < w.K && r + 1 < n; r++) {
-        double a = sl[r], b = sl[r + 1];
-        ok = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
+      bool pair = true;
+      if (i < w.K && i + 1 < n) {
+        const double a = sl[i], b = sl[i + 1];
+        pair = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
       }
+      bool ok = n >= w.K && __all(pair);
       if (ok) ok = (double)sl[w.K - 1] - mx > -80.0;
       if (ok) {
         const double2 *lb = w.lb + (size_t)t * (w.E + 1);
         const double lmx = lb[sm[0]].x;
-        double den = 0.0;
-        for (int r = 0; r < w.K; r++) den += exp(lb[sm[r]].x - lmx);
-        for (int r = 0; r < w.K; r++) {
-          w.idx[(size_t)t * w.K + r] = sm[r];
-          w.w[(size_t)t * w.K + r] = (float)(exp(lb[sm[r]].x - lmx) / den);
+        const double ev = i < w.K ? exp(lb[sm[i]].x - lmx) : 0.0;
+        const double den = wave_sum(ev);
+        if (i < w.K) {
+          w.idx[(size_t)t * w.K + i] = sm[i];
+          w.w[(size_t)t * w.K + i] = (float)(ev / den);
         }
-      } else {
+      } else if (i == 0) {
         atomicAdd(&stats[2], 1ull);
         w.certified[t] = 0;
         w.flist[atomicAdd(w.fcount, 1)] = t;
@@ -1032,11 +1133,7 @@ __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const
     const float *xt = x + (size_t)t * w.H;
     for (int e = blockIdx.x; e < w.E; e += gridDim.x) {
       const float *row = router + (size_t)e * w.H;
-      for (int i = threadIdx.x * 4; i < m; i += 256) {
-        float4 a = *(const float4 *)(xt + i), b = *(const float4 *)(row + i);
-        *(float4 *)(prod + i) = make_float4(__fmul_rn(a.x, b.x), __fmul_rn(a.y, b.y), __fmul_rn(a.z, b.z),
-                                            __fmul_rn(a.w, b.w));
-      }
+      form_products(xt, row, m, prod);
       __syncthreads();
       if (threadIdx.x == 0) {
         float s = 0.0f;
@@ -1399,25 +1496,66 @@ __device__ __forceinline__ void idot_tiles(const signed char *W, int ld, int row
   }
 }
 
-// Shared expert steps of many tokens: blocks take kSharedSub 16-token chunks,
-// so each shared weight tile is read once per 64 tokens.
+// Shared expert steps of many tokens: blocks take NS 16-token chunks (1, 2
+// or 4 by the step's size), so each shared weight tile is read once per
+// 16*NS tokens.  The shared-down part of the down kernels takes
+// kSharedBlockTokens tokens a block.
 constexpr int kSharedSub = 4;
 constexpr int kSharedBlockTokens = 16 * kSharedSub;
+// k chunks per batch: a wave issues the gate, up and activation loads of
+// kShBatch chunks before the first MFMA, so a wave's k range costs
+// per/kShBatch memory latencies instead of 2*per
+constexpr int kShBatch = 4;
 
+__device__ __forceinline__ v4i ld_v4i_if(const signed char *p, bool ok) {
+  v4i v = {0, 0, 0, 0};
+  if (ok) v = *(const v4i *)p;
+  return v;
+}
+
+template <int NS>
 __global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char *gq, const float *gs,
                                                        const signed char *uq, const float *us) {
-  __shared__ int part[4][2][kSharedSub][256];
+  __shared__ int part[4][2][NS][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rt = blockIdx.x, t0 = blockIdx.y * kSharedBlockTokens;
+  const int rt = blockIdx.x, t0 = blockIdx.y * 16 * NS;
   const int nk = w.H / 64;
   const int per = (nk + 3) / 4, kc0 = wave * per, kc1 = min(nk, kc0 + per);
-  v4i cg[kSharedSub] = {}, cu[kSharedSub] = {};
-  if (kc0 < kc1) {
-    idot_tiles<kSharedSub>(gq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cg, lane);
-    idot_tiles<kSharedSub>(uq, w.H, rt * kTileRows, kc0, kc1, w.xq, w.H, t0, w.T, cu, lane);
+  v4i cg[NS] = {}, cu[NS] = {};
+  {
+    const int r = lane & 15, kb = lane >> 4;
+    const signed char *ga = gq + (size_t)(rt * kTileRows + r) * w.H + kb * 16;
+    const signed char *ua = uq + (size_t)(rt * kTileRows + r) * w.H + kb * 16;
+    const signed char *brow[NS];
+    bool bok[NS];
+#pragma unroll
+    for (int q = 0; q < NS; q++) {
+      const int tok = t0 + 16 * q + r;
+      bok[q] = tok < w.T;
+      brow[q] = w.xq + (size_t)(bok[q] ? tok : 0) * w.H + kb * 16;
+    }
+    for (int kc = kc0; kc < kc1; kc += kShBatch) {
+      v4i ag[kShBatch], au[kShBatch], bb[kShBatch][NS];
+#pragma unroll
+      for (int u = 0; u < kShBatch; u++) {
+        const bool ok = kc + u < kc1;
+        const int k = ok ? kc + u : kc0;  // in bounds; the operand is zeroed
+        ag[u] = ld_v4i_if(ga + k * 64, ok);
+        au[u] = ld_v4i_if(ua + k * 64, ok);
+#pragma unroll
+        for (int q = 0; q < NS; q++) bb[u][q] = ld_v4i_if(brow[q] + k * 64, ok && bok[q]);
+      }
+#pragma unroll
+      for (int u = 0; u < kShBatch; u++)
+#pragma unroll
+        for (int q = 0; q < NS; q++) {
+          cg[q] = mfma_i8(ag[u], bb[u][q], cg[q]);
+          cu[q] = mfma_i8(au[u], bb[u][q], cu[q]);
+        }
+    }
   }
 #pragma unroll
-  for (int q = 0; q < kSharedSub; q++)
+  for (int q = 0; q < NS; q++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       part[wave][0][q][lane * 4 + i] = cg[q][i];
@@ -1426,7 +1564,9 @@ __global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char
   __syncthreads();
   // wave q finishes chunk q: the waves' k-range sums (exact), then the
   // reference's rounding of g, u and h
-  const int q = wave, kb = lane >> 4, tok = t0 + 16 * q + (lane & 15);
+  const int q = wave;
+  if (q >= NS) return;
+  const int kb = lane >> 4, tok = t0 + 16 * q + (lane & 15);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     int dg = 0, du = 0;
@@ -2282,12 +2422,26 @@ static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const fl
   return 0;
 }
 
-// Steps of at least this many tokens route through the fp64 MFMA GEMM
-constexpr int kRouterGemmTokens = 32;
+// Steps of at least this many tokens route through the fp64 MFMA GEMM (at
+// S397 the tiled bounds kernel is faster up to 32 tokens: 110 against 124 us)
+#ifndef SW_ROUTER_GEMM_TOKENS
+#define SW_ROUTER_GEMM_TOKENS 64
+#endif
+constexpr int kRouterGemmTokens = SW_ROUTER_GEMM_TOKENS;
 
 static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
   hipStream_t st = ctx->stream;
-  k_prep_x<<<w.T, 1024, 0, st>>>(w, x);
+  const int hp4 = w.ngh * 128 / 4;  // float4 chunks of the padded row
+  if (hp4 <= 1024)
+    k_prep_x<1><<<w.T, 1024, 0, st>>>(w, x);
+  else if (hp4 <= 2048)
+    k_prep_x<2><<<w.T, 1024, 0, st>>>(w, x);
+  else if (hp4 <= 4096)
+    k_prep_x<4><<<w.T, 1024, 0, st>>>(w, x);
+  else if (hp4 <= 8192)
+    k_prep_x<8><<<w.T, 1024, 0, st>>>(w, x);
+  else
+    k_prep_x_any<<<w.T, 1024, 0, st>>>(w, x);
   int rc = 1;  // 1: shape or alignment outside the tiled router kernel
   if (w.T >= kRouterGemmTokens && w.H % 64 == 0 && ((uintptr_t)x & 15) == 0) {
     k_router_gemm<<<dim3((w.E + 1 + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router, L->sgate_row);
@@ -2420,8 +2574,13 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   k_bucket<<<1, 1024, bucket_lds, st>>>(w);
   mark(ctx, 2);
   prof_mark(ctx, kStageSetup);
-  k_shared_swiglu<<<dim3(w.Ish / kTileRows, (T + kSharedBlockTokens - 1) / kSharedBlockTokens), 256, 0, st>>>(
-      w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+  if (T <= 16)
+    k_shared_swiglu<1><<<dim3(w.Ish / kTileRows, 1), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+  else if (T <= 32)
+    k_shared_swiglu<2><<<dim3(w.Ish / kTileRows, 1), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+  else
+    k_shared_swiglu<4><<<dim3(w.Ish / kTileRows, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq,
+                                                                              L->sh_us);
   mark(ctx, 3);
   prof_mark(ctx, kStageSharedHidden);
   int item_bound = w.E + (T * w.K + w.itok - 1) / w.itok;
