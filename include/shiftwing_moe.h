@@ -436,7 +436,7 @@ int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
  * tokens == 1 and layers of one shape this is one persistent kernel that
  * needs every compute unit of the device for the duration of the call; a
  * call that cannot get them reports an error at the next coli_cuda_sync.
- * With 2..6 tokens the persistent kernel runs once per token (the tokens
+ * With 2..4 tokens the persistent kernel runs once per token (the tokens
  * are independent), which is faster than one many-token step per layer. */
 int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers,
                                  int n_layers, float *y, const float *x,
@@ -471,10 +471,10 @@ int coli_cuda_moe_decode_times(ColiCuda *ctx, double ms[3],
  * not take fall back to 2); 2 the three per-layer decode kernels; 0 the
  * many-token kernels.  Same results to the stated tolerance (for tests). */
 int coli_cuda_moe_set_decode_kernels(ColiCuda *ctx, int mode);
-/* Many-token steps: tokens per expert work item.  0 (default) picks 16 when
- * the step has at least two routes per expert on average (each expert's
- * tiles are then read once per 16 tokens), else 8; 8 or 16 force one.  Same
- * indices; outputs to the stated tolerance (for tests and measurement). */
+/* Many-token steps: tokens per expert work item.  0 (default) picks 16 (each
+ * expert's tiles read once per 16 tokens) when an item's activation digits
+ * fit the LDS, else 8; 8 or 16 force one.  Same indices; outputs to the
+ * stated tolerance (for tests and measurement). */
 int coli_cuda_moe_set_item_tokens(ColiCuda *ctx, int tokens);
 /* Stage stamps of the persistent decode kernel (measurement): while set,
  * every call writes the device wall clock (100 MHz) into the caller's device

@@ -33,6 +33,7 @@
 #include "sw_synth.h"
 #include "sw_moe_layer.h"
 #include "sw_stack.h"
+#include "sw_lds_dma.h"
 
 using namespace sw;
 
@@ -1705,6 +1706,112 @@ __global__ __launch_bounds__(512) void k_expert_gateup(Work w, ExpertLayout xl, 
 }
 
 // ---------------------------------------------------------------------------
+// 7b. routed gate/up of items of <= 8 tokens with the weights streamed through
+// LDS: each wave copies its groups' records (gate and up codes and row scales
+// of one (row tile, group), contiguous in HBM) for the block's row tiles into
+// a ring of kGuRing slots with global_load_lds in 1 KB pieces, kGuRing-1
+// records in flight while one is multiplied.  Same arithmetic and order as
+// k_expert_gateup (H <= 4096: a wave's groups fit one batch).
+// grid (ceil(I/16/row_tiles), item slots), 512 threads, dynamic LDS
+// 8*kGuRing*record bytes.
+// ---------------------------------------------------------------------------
+#ifndef SW_GU_RING
+#define SW_GU_RING 4
+#endif
+#ifndef SW_GU_USE_RING
+#define SW_GU_USE_RING 1
+#endif
+constexpr int kGuRing = SW_GU_RING;
+static_assert(3 * (kGuRing - 1) <= 30, "gate/up ring: waits within wait_vm's range");
+
+template <int FMT>
+__global__ __launch_bounds__(512) void k_gateup_ring(Work w, ExpertLayout xl, int row_tiles) {
+  extern __shared__ __align__(16) unsigned char glds[];
+  __shared__ float part[8][2][64][4];
+  constexpr int BPL = FMT == 4 ? 16 : 12;
+  constexpr int OFF = FMT == 4 ? 8 : 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
+  const int nrt = w.I / kTileRows;
+  const int rt0 = blockIdx.x * row_tiles, rt1 = min(nrt, rt0 + row_tiles);
+  const int per = (w.ngh + 7) / 8, g0 = min(w.ngh, wave * per), g1 = min(w.ngh, g0 + per);
+  const int n = g1 - g0;  // <= kMtBatch
+  const unsigned tgc = xl.tgc, rec = xl.rec_gu();
+  const int nck = (int)((rec + 1023) >> 10);
+  unsigned char *ring = glds + (size_t)wave * kGuRing * rec;
+  const int nit = n > 0 ? (rt1 - rt0) * n : 0;
+  const int n_items = *w.nitems;
+  for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
+    const int4 item = w.items[it];
+    const int e = item.x, p0 = item.y, cnt = item.z;
+    // this wave's records in order: row tile rt0 + j / n, group g0 + j % n
+    const unsigned char *xb = xl.base + (size_t)e * xl.expert_bytes + ((size_t)rt0 * w.ngh + g0) * rec;
+    int issued = 0, consumed = 0, su = 0, csl = 0, ir = 0, ig = 0;
+    auto issue = [&]() {
+      if (issued == nit) return;
+      const unsigned char *src = xb + ((size_t)ir * w.ngh + ig) * rec;
+      const unsigned slot = lds_addr(ring + (size_t)su * rec);
+      for (int k = 0; k < nck; k++)
+        if (16 * lane < (int)rec - 1024 * k) dma_b128_s(src + 1024 * k, 16 * lane, slot + 1024 * k);
+      issued++;
+      if (++su == kGuRing) su = 0;
+      if (++ig == n) {
+        ig = 0;
+        ir++;
+      }
+    };
+    for (int k = 0; k < kGuRing - 1; k++) issue();
+    // B column c = lane%16: token c/2 of the item, digit c%2 (loaded behind
+    // the first copies; the first record's wait covers them)
+    const int tt = (lane & 15) >> 1;
+    const signed char *dsrc = nullptr;
+    const float4 *gp = nullptr;
+    if (tt < cnt) {
+      const int tok = w.btok[p0 + tt];
+      dsrc = ((lane & 1) ? w.xd2 : w.xd1) + (size_t)tok * w.Hp;
+      gp = w.xgp + (size_t)tok * w.ngh;
+    }
+    MtDigits dg;
+    if (n > 0) mt_digits(dg, dsrc, gp, g0, n, lane);
+    for (int rt = rt0; rt < rt1; rt++) {
+      float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int gi = 0; gi < kMtBatch; gi++)
+        if (gi < n) {
+          issue();
+          // this record's copies are done once at most the copies of the
+          // records issued after it are outstanding (in order)
+          wait_vm(nck * (issued - consumed - 1));
+          consumed++;
+          const unsigned char *r = ring + (size_t)csl * rec;
+          if (++csl == kGuRing) csl = 0;
+#pragma unroll
+          for (int m = 0; m < 2; m++) {
+            uint32_t q[BPL / 4];
+            const unsigned *cp = (const unsigned *)(r + m * tgc + lane * BPL);
+#pragma unroll
+            for (int k = 0; k < BPL / 4; k++) q[k] = cp[k];
+            const float4 sc = *(const float4 *)(r + 2 * tgc + 64 * m + 16 * kb);
+            v4i a0, a1;
+            unpack_words<FMT>(q, a0, a1);
+            v4i c = {0, 0, 0, 0};
+            c = mfma_i8(a0, dg.b0[gi], c);
+            c = mfma_i8(a1, dg.b1[gi], c);
+            const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+            float *acc = m == 0 ? ag : au;
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+              const float f = (float)(c[rr] - OFF * dg.Q[gi]) * dg.dsc[gi];
+              const float tsum = f + dpp_row_shr1(f);
+              acc[rr] = __builtin_fmaf(tsum, scv[rr], acc[rr]);
+            }
+          }
+        }
+      gu_store(part, ag, au, rt, p0, cnt, w, lane, wave);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 8. down: routed items -> rout[p][row]; shared token chunks (IDOT) ->
 // shout[t][row].  Each wave takes kDnRowTiles consecutive row tiles.
 // grid (ceil(H/16/(4*kDnRowTiles)), n_item_slots + ceil(T/16)), 256 threads.
@@ -2473,22 +2580,24 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   return launch_status("MoE routing kernels");
 }
 
-// Tokens per bucketing item.  Steps with at least two routes per expert on
-// average take the wide items (each expert's tiles read once per
-// kWideTokens tokens) when an item's digits fit the LDS; the context's
-// setting (coli_cuda_moe_set_item_tokens) can force either.
-static int item_tokens(const ColiCuda *ctx, const ColiMoeLayer *L, int T) {
+// Tokens per bucketing item: the wide items (each expert's tiles read once
+// per kWideTokens tokens) whenever an item's digits fit the LDS.  Their
+// kernels give each wave whole row tiles, streamed through every group with
+// no block barrier, and are faster at every step size measured, however few
+// tokens an expert holds (S397: 834 against 686 tok/s at 8 tokens a step,
+// 1763 against 1388 at 32).  The context's setting
+// (coli_cuda_moe_set_item_tokens) can force either.
+static int item_tokens(const ColiCuda *ctx, const ColiMoeLayer *L) {
   const int mode = ctx->moe_item_tokens;
   const bool fits = wide_lds_bytes(wide_stage_groups(L->ngh, kWideGuBatch)) <= 160 * 1024 &&
                     wide_lds_bytes(wide_stage_groups(L->ngi, kWideDnBatch)) <= 160 * 1024;
-  const bool want = mode == kWideTokens || (mode == 0 && T * L->sh.topk >= 2 * L->sh.experts);
-  return want && fits && mode != kMaxTokensPerItem ? kWideTokens : kMaxTokensPerItem;
+  return fits && mode != kMaxTokensPerItem ? kWideTokens : kMaxTokensPerItem;
 }
 
 static int prepare(ColiCuda *ctx, ColiMoeLayer *L, int T, Work &w) {
   if (T <= 0 || T > kMaxTokens) return fail_arg("MoE step: tokens %d outside [1,%d]", T, kMaxTokens);
   w = make_work(L, T);
-  w.itok = item_tokens(ctx, L, T);
+  w.itok = item_tokens(ctx, L);
   size_t bytes = carve(w, nullptr);
   if (ensure_scratch(ctx, kScrXPrep, bytes, "MoE workspace allocation")) return -1;
   carve(w, (char *)ctx->scratch[kScrXPrep]);
@@ -2602,7 +2711,15 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
     const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
     const bool wide = (w.ngh + 7) / 8 > kMtBatch;  // a wave's groups exceed one batch
-    if (fmt4)
+    if (!wide && SW_GU_USE_RING) {
+      const size_t lg = (size_t)8 * kGuRing * L->xl.rec_gu();
+      const void *fn = fmt4 ? (const void *)k_gateup_ring<4> : (const void *)k_gateup_ring<3>;
+      if (set_lds(fn, lg + sizeof(float) * 8 * 2 * 64 * 4)) return -1;
+      if (fmt4)
+        k_gateup_ring<4><<<dim3(gu_blocks_x, slots), 512, lg, st>>>(w, L->xl, gu_rt);
+      else
+        k_gateup_ring<3><<<dim3(gu_blocks_x, slots), 512, lg, st>>>(w, L->xl, gu_rt);
+    } else if (fmt4)
       wide ? k_expert_gateup<4, true><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt)
            : k_expert_gateup<4, false><<<dim3(gu_blocks_x, slots), 512, 0, st>>>(w, L->xl, gu_rt);
     else
@@ -2646,9 +2763,12 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
 }
 
 // Token counts a stack call runs through the persistent kernel token by token
-// (S397: 2.1 ms per token for 60 layers, against 11.4 ms for a 4-token and
-// 13.7 ms for an 8-token many-token step).
-constexpr int kStackSeqTokens = 6;
+// (S397, 60 layers: 2.08 ms per token, against 7.4 ms for a 3-token, 8.7 ms
+// for a 4-token and 9.2 ms for a 6-token many-token step).
+#ifndef SW_STACK_SEQ_TOKENS
+#define SW_STACK_SEQ_TOKENS 4
+#endif
+constexpr int kStackSeqTokens = SW_STACK_SEQ_TOKENS;
 
 extern "C" int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers, int n_layers, float *y,
                                             const float *x, int tokens, size_t xs, size_t ys) {

@@ -115,11 +115,12 @@ def test_batched_stack_equals_layer_calls(be):
         assert np.array_equal(ys[l].view(np.uint32), y1.view(np.uint32)), l
 
 
-@pytest.mark.parametrize("T", [2, 4, 6])
+@pytest.mark.parametrize("T", [2, 4, 5])
 def test_small_batch_stack_runs_token_by_token(be, oracle, T):
-    """coli_cuda_moe_forward_layers with 2..6 tokens runs the persistent decode
-    kernel once per token: bit for bit the one-token calls, and each layer
-    within the tolerance of the oracle's moe_forward (c/qwen.c:3717-3739)."""
+    """coli_cuda_moe_forward_layers with 2..4 tokens runs the persistent decode
+    kernel once per token: bit for bit the one-token calls.  From 5 tokens the
+    many-token step runs.  Either way each layer is within the tolerance of
+    the oracle's moe_forward (c/qwen.c:3717-3739)."""
     import ctypes as C
 
     from conftest import assert_close_rms
@@ -145,7 +146,8 @@ def test_small_batch_stack_runs_token_by_token(be, oracle, T):
         dxt = be.upload(np.ascontiguousarray(x[:, t, :]))
         be.check(be.lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, d1.p, dxt.p, 1, H, H), "forward_layers 1")
         y1 = be.download(d1, (nl, H), np.float32)
-        assert np.array_equal(ys[:, t, :].view(np.uint32), y1.view(np.uint32)), t
+        if T <= 4:
+            assert np.array_equal(ys[:, t, :].view(np.uint32), y1.view(np.uint32)), t
     for l in range(nl):
         for t in range(T):
             want = oracle.moe_forward(hls[l], x[l, t])
