@@ -943,6 +943,37 @@ __device__ float exact_chain(const float *xt, const float *row, int H) {
   return s;
 }
 
+// s = rn(s + p[i]) for i < m in order (the reference's serial chain over
+// precomputed products), by one lane, m % 64 == 0: the LDS reads of the next
+// 32 terms are issued before the adds of the current 32, so the chain runs at
+// the rate of its dependent adds.
+__device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    s = __fadd_rn(s, v[k].x);
+    s = __fadd_rn(s, v[k].y);
+    s = __fadd_rn(s, v[k].z);
+    s = __fadd_rn(s, v[k].w);
+  }
+}
+__device__ __forceinline__ float serial_sum_lds(const float *p, int m) {
+  float s = 0.0f;
+  float4 a[8], b[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) a[k] = ((const float4 *)p)[k];
+  for (int i = 0; i < m; i += 64) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) b[k] = ((const float4 *)(p + i + 32))[k];
+    add32(s, a);
+    if (i + 64 < m) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) a[k] = ((const float4 *)(p + i + 64))[k];
+    }
+    add32(s, b);
+  }
+  return s;
+}
+
 // prod[i] = rn(x[i]*row[i]) for i < m (m % 4 == 0) by the block's 64 lanes:
 // kProdBatch float4 pairs of loads in flight per lane before the first store
 constexpr int kProdBatch = 8;
@@ -991,18 +1022,10 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
       form_products(xt, row, m, prod);
       __syncthreads();
       if (threadIdx.x == 0) {
-        float s = 0.0f;
-        int i = 0;
-        // unrolled so that the LDS reads of 8 steps are issued ahead of their adds
-#pragma unroll 8
-        for (; i < m; i += 4) {
-          float4 p = *(const float4 *)(prod + i);
-          s = __fadd_rn(s, p.x);
-          s = __fadd_rn(s, p.y);
-          s = __fadd_rn(s, p.z);
-          s = __fadd_rn(s, p.w);
-        }
-        for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+        const int m64 = m / 64 * 64;
+        float s = serial_sum_lds(prod, m64);
+        for (int i = m64; i < m; i++) s = __fadd_rn(s, prod[i]);
+        for (int i = m; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
         w.logits[(size_t)t * w.E + e] = s;
       }
       __syncthreads();
@@ -1137,17 +1160,10 @@ __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const
       form_products(xt, row, m, prod);
       __syncthreads();
       if (threadIdx.x == 0) {
-        float s = 0.0f;
-        int i = 0;
-#pragma unroll 8
-        for (; i < m; i += 4) {
-          float4 p = *(const float4 *)(prod + i);
-          s = __fadd_rn(s, p.x);
-          s = __fadd_rn(s, p.y);
-          s = __fadd_rn(s, p.z);
-          s = __fadd_rn(s, p.w);
-        }
-        for (; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
+        const int m64 = m / 64 * 64;
+        float s = serial_sum_lds(prod, m64);
+        for (int i = m64; i < m; i++) s = __fadd_rn(s, prod[i]);
+        for (int i = m; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
         w.logits[(size_t)t * w.E + e] = s;
       }
       __syncthreads();
@@ -2162,17 +2178,39 @@ __host__ __device__ inline int wide_stage_groups(int ng, int nb) {
   return (hg + nb - 1) / nb * nb;
 }
 
+// (chunk, slot) of block `lin` of a 1-D grid of nx chunks x ny item slots,
+// placed so that the nx chunks of one slot run on one XCD.  Blocks go to the
+// device's 8 XCDs round-robin by linear id and each XCD has its own L2, so an
+// item's activation digits, which every chunk stages, come from HBM once per
+// item instead of once per chunk.  Within each group of 8 slots, block
+// g*8*nx + 8*c + j is chunk c of slot g*8 + j; the slots past the last full
+// group follow in plain order.
+__device__ __forceinline__ void xcd_block(int lin, int nx, int ny, int &chunk, int &slot) {
+  const int full = ny / 8 * 8;
+  if (lin < full * nx) {
+    const int g = lin / (8 * nx), r = lin - g * 8 * nx;
+    chunk = r >> 3;
+    slot = g * 8 + (r & 7);
+  } else {
+    const int r = lin - full * nx;
+    chunk = r % nx;
+    slot = full + r / nx;
+  }
+}
+
 // routed gate/up of wide items: h = silu(g)*u.  Block: kWideWaves waves x
-// kWideRt row tiles of I; grid (ceil(I/16 / (kWideWaves kWideRt)), item
-// slots), dynamic LDS wide_lds_bytes(hg).
+// kWideRt row tiles of I; a 1-D grid of nx = ceil(I/16 / (kWideWaves kWideRt))
+// chunks x ny item slots placed by xcd_block, dynamic LDS wide_lds_bytes(hg).
 template <int FMT>
-__global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertLayout xl, int hg) {
+__global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertLayout xl, int hg, int nx, int ny) {
   extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.I / kTileRows;
-  const int rt0 = (blockIdx.x * kWideWaves + wave) * kWideRt;
+  int chunk, slot;
+  xcd_block((int)blockIdx.x, nx, ny, chunk, slot);
+  const int rt0 = (chunk * kWideWaves + wave) * kWideRt;
   const int n_items = *w.nitems;
-  for (int it = blockIdx.y; it < n_items; it += gridDim.y) {
+  for (int it = slot; it < n_items; it += ny) {
     const int4 item = w.items[it];
     const int e = item.x, p0 = item.y, cnt = item.z;
     const TileMat mats[2] = {xl.mat(e, 0), xl.mat(e, 1)};
@@ -2197,18 +2235,21 @@ __global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertL
 
 // routed down of wide items, plus the shared expert's token chunks (IDOT) in
 // the first blocks y < shc (scheduled first, they overlap the routed work).
-// Block: kWideWaves waves x kWideDnRt row tiles of H; grid (ceil(H/16 /
-// (kWideWaves kWideDnRt)), shc + item slots).
+// Block: kWideWaves waves x kWideDnRt row tiles of H; a 1-D grid of shc*nx
+// shared blocks, then nx = ceil(H/16 / (kWideWaves kWideDnRt)) chunks x ny
+// item slots placed by xcd_block.
 template <int FMT>
 __global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLayout xl, int shc,
-                                                               const signed char *dq, const float *ds, int hg) {
+                                                               const signed char *dq, const float *ds, int hg,
+                                                               int nx, int ny) {
   extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.H / kTileRows;
-  const int rtb = blockIdx.x * kWideWaves * kWideDnRt;
-  if ((int)blockIdx.y < shc) {  // shared down, kSharedBlockTokens tokens a block
+  const int lin = (int)blockIdx.x;
+  if (lin < shc * nx) {  // shared down, kSharedBlockTokens tokens a block
+    const int rtb = lin % nx * kWideWaves * kWideDnRt;
     const int rt1 = min(nrt, rtb + kWideWaves * kWideDnRt);
-    const int t0 = (int)blockIdx.y * kSharedBlockTokens;
+    const int t0 = lin / nx * kSharedBlockTokens;
     for (int rt = rtb + wave; rt < rt1; rt += kWideWaves) {
       v4i c[kSharedSub] = {};
       idot_tiles<kSharedSub>(dq, w.Ish, rt * kTileRows, 0, w.Ish / 64, w.hq, w.Ish, t0, w.T, c, lane);
@@ -2226,9 +2267,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLay
     }
     return;
   }
-  const int rt0 = rtb + wave * kWideDnRt;
-  const int n_items = *w.nitems, item_slots = (int)gridDim.y - shc;
-  for (int it = (int)blockIdx.y - shc; it < n_items; it += item_slots) {
+  int chunk, slot;
+  xcd_block(lin - shc * nx, nx, ny, chunk, slot);
+  const int rt0 = chunk * kWideWaves * kWideDnRt + wave * kWideDnRt;
+  const int n_items = *w.nitems;
+  for (int it = slot; it < n_items; it += ny) {
     const int4 item = w.items[it];
     const int e = item.x, p0 = item.y, cnt = item.z;
     const TileMat mats[1] = {xl.mat(e, 2)};
@@ -2702,11 +2745,11 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     const size_t lg = wide_lds_bytes(hg);
     const void *fn = fmt4 ? (const void *)k_gateup_wide<4> : (const void *)k_gateup_wide<3>;
     if (set_lds(fn, lg)) return -1;
-    const dim3 grid((w.I / kTileRows + kWideWaves * kWideRt - 1) / (kWideWaves * kWideRt), slots);
+    const int nx = (w.I / kTileRows + kWideWaves * kWideRt - 1) / (kWideWaves * kWideRt);
     if (fmt4)
-      k_gateup_wide<4><<<grid, 64 * kWideWaves, lg, st>>>(w, L->xl, hg);
+      k_gateup_wide<4><<<nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots);
     else
-      k_gateup_wide<3><<<grid, 64 * kWideWaves, lg, st>>>(w, L->xl, hg);
+      k_gateup_wide<3><<<nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots);
   } else {
     const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
     const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
@@ -2740,11 +2783,11 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     const void *fn = fmt4 ? (const void *)k_down_wide<4> : (const void *)k_down_wide<3>;
     if (set_lds(fn, ld)) return -1;
     const int shc = (T + kSharedBlockTokens - 1) / kSharedBlockTokens;
-    const dim3 grid((w.H / kTileRows + kWideWaves * kWideDnRt - 1) / (kWideWaves * kWideDnRt), shc + slots);
+    const int nx = (w.H / kTileRows + kWideWaves * kWideDnRt - 1) / (kWideWaves * kWideDnRt);
     if (fmt4)
-      k_down_wide<4><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg);
+      k_down_wide<4><<<nx * (shc + slots), 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg, nx, slots);
     else
-      k_down_wide<3><<<grid, 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg);
+      k_down_wide<3><<<nx * (shc + slots), 64 * kWideWaves, ld, st>>>(w, L->xl, shc, L->sh_dq, L->sh_ds, hg, nx, slots);
   } else if (fmt4) {
     dn_split ? k_down_split<4><<<dim3(ds_blocks_x, slots + sh_chunks), 512, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds)
              : k_down<4><<<dim3(dn_blocks_x, slots + sh_chunks), 256, 0, st>>>(w, L->xl, slots, L->sh_dq, L->sh_ds);
