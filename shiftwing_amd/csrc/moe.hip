@@ -235,6 +235,13 @@ __device__ float qrow_i8_block(const float *x, int n, signed char *q, float *red
   return s;
 }
 
+// Shared expert of many tokens: token chunks per block (kSharedBlockTokens
+// a block for the shared down), and steps of at most kShSplitTokens tokens
+// split the shared gate/up's k range over kShSplit blocks per row tile.
+constexpr int kSharedSub = 4;
+constexpr int kSharedBlockTokens = 16 * kSharedSub;
+constexpr int kShSplit = 4, kShSplitTokens = 32;
+
 // ---------------------------------------------------------------------------
 // per-call workspace carved from one scratch buffer
 // ---------------------------------------------------------------------------
@@ -254,6 +261,7 @@ struct Work {
   int *offsets, *btok, *bslot, *pos; int4 *items; int *nitems;
   // shared
   float *hsh; signed char *hq; float *shx; float *shout;
+  int *shpart; int shks;  // k-split shared gate/up: int32 partial dots [kShSplit][T][2][Ish] (shks 0: none)
   // routed
   float *hroute; signed char *hd1, *hd2; float4 *hgp; float *rout;
   size_t bytes;
@@ -292,6 +300,7 @@ size_t carve(Work &w, char *base) {
   w.items = (int4 *)take((size_t)(R + w.E) * 16);
   w.nitems = (int *)take(16);
   w.hsh = (float *)take((size_t)T * w.Ish * 4);
+  w.shpart = (int *)take((size_t)(T <= kShSplitTokens ? kShSplit : 0) * T * 2 * w.Ish * 4);
   w.hq = (signed char *)take((size_t)T * w.Ish);
   w.shx = (float *)take((size_t)T * 4);
   w.shout = (float *)take((size_t)T * w.H * 4);
@@ -1471,9 +1480,10 @@ __device__ __forceinline__ void mt_compute(const MtTiles<FMT> &t, const MtDigits
 }
 
 // ---------------------------------------------------------------------------
-// 6. shared expert gate/up, IDOT on MFMA: exact int32 dots for 16 rows x up
-// to 16 tokens, k split over the block's waves, then h = silu(g)*u with the
-// reference's rounding.  grid (Ish/16, ceil(T/16)), 512 threads.
+// 6. shared expert gate/up, IDOT on MFMA: exact int32 dots for 16 rows x
+// 16*NS tokens, k split over the block's waves, then h = silu(g)*u with the
+// reference's rounding.  grid (Ish/16, ceil(T/(16 NS))), 256 threads; steps
+// of at most kShSplitTokens tokens take k_shared_gu_split instead.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void idot_tile(const signed char *W, int ld, int row0, int kc0, int kc1,
                                           const signed char *xq, int xld, int t0, int T, v4i &c, int lane) {
@@ -1517,8 +1527,6 @@ __device__ __forceinline__ void idot_tiles(const signed char *W, int ld, int row
 // or 4 by the step's size), so each shared weight tile is read once per
 // 16*NS tokens.  The shared-down part of the down kernels takes
 // kSharedBlockTokens tokens a block.
-constexpr int kSharedSub = 4;
-constexpr int kSharedBlockTokens = 16 * kSharedSub;
 // k chunks per batch: a wave issues the gate, up and activation loads of
 // kShBatch chunks before the first MFMA, so a wave's k range costs
 // per/kShBatch memory latencies instead of 2*per
@@ -1602,11 +1610,122 @@ __global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char
   }
 }
 
+// Shared gate/up of small steps (T <= kShSplitTokens): block (row tile,
+// k part ks) forms the exact int32 dots of its 16 rows over k chunks
+// [ks*nk/kShSplit, (ks+1)*nk/kShSplit) for NS 16-token chunks, 4 waves
+// splitting the part, and stores them to shpart[ks]; k_prep_hidden adds the
+// parts (exact) and applies the reference's rounding.  grid (Ish/16,
+// kShSplit), 256 threads.
+template <int NS>
+__global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed char *gq, const signed char *uq) {
+  __shared__ int part[4][2][NS][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rt = blockIdx.x, ks = blockIdx.y;
+  const int nk = w.H / 64;
+  const int p0 = ks * nk / kShSplit, p1 = (ks + 1) * nk / kShSplit;
+  const int kc0 = p0 + wave * (p1 - p0) / 4, kc1 = p0 + (wave + 1) * (p1 - p0) / 4;
+  v4i cg[NS] = {}, cu[NS] = {};
+  {
+    const int r = lane & 15, kb = lane >> 4;
+    const signed char *ga = gq + (size_t)(rt * kTileRows + r) * w.H + kb * 16;
+    const signed char *ua = uq + (size_t)(rt * kTileRows + r) * w.H + kb * 16;
+    const signed char *brow[NS];
+    bool bok[NS];
+#pragma unroll
+    for (int q = 0; q < NS; q++) {
+      const int tok = 16 * q + r;
+      bok[q] = tok < w.T;
+      brow[q] = w.xq + (size_t)(bok[q] ? tok : 0) * w.H + kb * 16;
+    }
+    for (int kc = kc0; kc < kc1; kc += kShBatch) {
+      v4i ag[kShBatch], au[kShBatch], bb[kShBatch][NS];
+#pragma unroll
+      for (int u = 0; u < kShBatch; u++) {
+        const bool ok = kc + u < kc1;
+        const int k = ok ? kc + u : kc0;  // in bounds; the operand is zeroed
+        ag[u] = ld_v4i_if(ga + k * 64, ok);
+        au[u] = ld_v4i_if(ua + k * 64, ok);
+#pragma unroll
+        for (int q = 0; q < NS; q++) bb[u][q] = ld_v4i_if(brow[q] + k * 64, ok && bok[q]);
+      }
+#pragma unroll
+      for (int u = 0; u < kShBatch; u++)
+#pragma unroll
+        for (int q = 0; q < NS; q++) {
+          cg[q] = mfma_i8(ag[u], bb[u][q], cg[q]);
+          cu[q] = mfma_i8(au[u], bb[u][q], cu[q]);
+        }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NS; q++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      part[wave][0][q][lane * 4 + i] = cg[q][i];
+      part[wave][1][q][lane * 4 + i] = cu[q][i];
+    }
+  __syncthreads();
+  const int q = wave;
+  if (q >= NS) return;
+  const int kb = lane >> 4, tok = 16 * q + (lane & 15);
+  if (tok >= w.T) return;
+  int *dst = w.shpart + ((size_t)ks * w.T + tok) * 2 * w.Ish;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int dg = 0, du = 0;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      dg += part[v][0][q][lane * 4 + i];
+      du += part[v][1][q][lane * 4 + i];
+    }
+    const int row = rt * kTileRows + 4 * kb + i;
+    dst[row] = dg;
+    dst[w.Ish + row] = du;
+  }
+}
+
 // qrow_i8 of the shared hidden rows + digits of the routed hidden rows
-__global__ void k_prep_hidden(Work w) {
+__global__ void k_prep_hidden(Work w, const float *gs, const float *us) {
   __shared__ float red[16];
   int b = blockIdx.x;
   if (b < w.T) {
+    if (w.shks > 0) {
+      // the k parts of the shared gate/up dots (exact int32 sums), then
+      // h = silu(g)*u with the reference's rounding (as k_shared_swiglu)
+      // (every part's loads issued before the first add)
+      constexpr int kRows = 4;  // rows per thread per batch
+      const float sx = w.sx[b];
+      for (int i0 = threadIdx.x; i0 < w.Ish; i0 += kRows * blockDim.x) {
+        int pg[kRows][kShSplit], pu[kRows][kShSplit];
+        float gsi[kRows], usi[kRows];
+#pragma unroll
+        for (int j = 0; j < kRows; j++) {
+          const int i = min(i0 + j * (int)blockDim.x, w.Ish - 1);  // in bounds; stored only below Ish
+#pragma unroll
+          for (int ks = 0; ks < kShSplit; ks++) {
+            const int *src = w.shpart + ((size_t)ks * w.T + b) * 2 * w.Ish;
+            pg[j][ks] = src[i];
+            pu[j][ks] = src[w.Ish + i];
+          }
+          gsi[j] = gs[i];
+          usi[j] = us[i];
+        }
+#pragma unroll
+        for (int j = 0; j < kRows; j++) {
+          const int i = i0 + j * (int)blockDim.x;
+          int dg = 0, du = 0;
+#pragma unroll
+          for (int ks = 0; ks < kShSplit; ks++) {
+            dg += pg[j][ks];
+            du += pu[j][ks];
+          }
+          const float g = (float)dg * gsi[j] * sx;
+          const float u = (float)du * usi[j] * sx;
+          if (i < w.Ish) w.hsh[(size_t)b * w.Ish + i] = silu_ref(g) * u;
+        }
+      }
+      __syncthreads();
+    }
     float s = qrow_i8_block(w.hsh + (size_t)b * w.Ish, w.Ish, w.hq + (size_t)b * w.Ish, red);
     if (threadIdx.x == 0) w.shx[b] = s;
     return;
@@ -2531,6 +2650,7 @@ static Work make_work(const ColiMoeLayer *L, int T) {
   w.ngi = L->ngi;
   w.Hp = w.ngh * kGroup;
   w.Ip = w.ngi * kGroup;
+  w.shks = T <= kShSplitTokens ? kShSplit : 0;
   return w;
 }
 
@@ -2727,9 +2847,9 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   mark(ctx, 2);
   prof_mark(ctx, kStageSetup);
   if (T <= 16)
-    k_shared_swiglu<1><<<dim3(w.Ish / kTileRows, 1), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
-  else if (T <= 32)
-    k_shared_swiglu<2><<<dim3(w.Ish / kTileRows, 1), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq, L->sh_us);
+    k_shared_gu_split<1><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
+  else if (T <= kShSplitTokens)
+    k_shared_gu_split<2><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
   else
     k_shared_swiglu<4><<<dim3(w.Ish / kTileRows, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq,
                                                                               L->sh_us);
@@ -2771,7 +2891,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   }
   mark(ctx, 4);
   prof_mark(ctx, kStageRoutedHidden);
-  k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w);
+  k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w, L->sh_gs, L->sh_us);
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
   const int dn_blocks_x = (w.H / kTileRows + 4 * kDnRowTiles - 1) / (4 * kDnRowTiles);
