@@ -815,6 +815,12 @@ __device__ __forceinline__ int wave_max_i(int v) {
 // below each candidate's by more than the margin, so the exact top-k lies in
 // M.  certified[t]: 1 certified, 2 targeted (M in mset, |M| <= 64), 0 every
 // chain.  grid ceil(T/4), 256 threads.
+// order-preserving unsigned key of a float (larger float, larger key)
+__device__ __forceinline__ unsigned order_key(float f) {
+  const unsigned u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 template <int NV>
 __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned long long *stats) {
   __shared__ int cand_s[4][kMaxTopK + 1];
@@ -834,30 +840,34 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
     if (e < w.E) amax = fmax(amax, fabs(v[j].x) + v[j].y);
   }
   amax = wave_max_d(amax);
+  // The K+1 candidates by rounds of a wave maximum over 64-bit keys (the
+  // logit rounded to fp32, order-preserving, then the complemented index:
+  // the lowest index first among equal keys).  Candidates that the fp32
+  // rounding ranks wrongly differ by less than the pair margin, so the
+  // checks below send their token to the exact path.
   const int nc = min(w.K + 1, w.E);
+  unsigned long long key[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int e = lane + 64 * j;
+    key[j] = e < w.E ? ((unsigned long long)order_key((float)v[j].x) << 32) | (unsigned)(~e) : 0ull;
+  }
   unsigned chosen = 0;
   for (int r = 0; r < nc; r++) {
-    VI best = {0.0, -1};
+    unsigned long long best = 0ull;
 #pragma unroll
-    for (int j = 0; j < NV; j++) {
-      int e = lane + 64 * j;
-      if (e < w.E && !((chosen >> j) & 1)) best = vi_better(best, VI{v[j].x, e});
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      VI y;
-      y.v = __shfl_xor(best.v, o, 64);
-      y.i = __shfl_xor(best.i, o, 64);
-      best = vi_better(best, y);
-    }
-    if (best.i >= 0 && (best.i & 63) == lane) {
-      const int jb = best.i >> 6;
+    for (int j = 0; j < NV; j++)
+      if (!((chosen >> j) & 1) && key[j] > best) best = key[j];
+    best = wave_max_u64(best);
+    const int eb = best ? (int)(~(unsigned)best) : -1;
+    if (eb >= 0 && (eb & 63) == lane) {
+      const int jb = eb >> 6;
       chosen |= 1u << jb;
 #pragma unroll
       for (int j = 0; j < NV; j++)
         if (j == jb) cv[r] = v[j];
     }
-    if (lane == 0) cand[r] = best.i;
+    if (lane == 0) cand[r] = eb;
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
