@@ -488,7 +488,11 @@ __global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float
     }
     __syncthreads();
     if (!live) continue;
-    for (int g = 0; g < ng; g++) {
+    // the round's tokens unrolled, so that their independent reductions
+    // interleave
+#pragma unroll
+    for (int g = 0; g < kRbRound; g++) {
+      if (g >= ng) break;
       const float *xl = rb_xs + g * 64 * P + lane * P;
       double lp = 0.0, pa = 0.0, aa = 0.0;
 #pragma unroll
@@ -502,10 +506,12 @@ __global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float
         aa = __builtin_fma(fabs(xd), fabs(wd), aa);
         pa += fabs(lp);
       }
-      double off = wave_exclusive_scan(lp, lane);
-      double L = wave_sum(lp);
-      double Pb = wave_sum((double)CH * fabs(off) + pa);
-      double A = wave_sum(aa);
+      // DPP reductions: the inclusive scan's last lane is the logit
+      const double inc = wave_incl_scan_dpp(lp);
+      const double off = inc - lp;
+      const double L = readlane_d63(inc);
+      const double Pb = wave_sum_dpp((double)CH * fabs(off) + pa);
+      const double A = wave_sum_dpp(aa);
       if (lane == 0) {
         const int t = tb + g;
         const double u = 0x1p-24;

@@ -193,6 +193,23 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
   return __hiloint2double(hi, lo);
 }
 
+// inclusive scan of a double over the wave in lane order: row_shr 1, 2, 4, 8
+// within each 16-lane row, then row_bcast 15 and 31 carry the row totals
+__device__ __forceinline__ double wave_incl_scan_dpp(double v) {
+  SW_DPP_D_STEP(v, 0x111, 0xF, true);
+  SW_DPP_D_STEP(v, 0x112, 0xF, true);
+  SW_DPP_D_STEP(v, 0x114, 0xF, true);
+  SW_DPP_D_STEP(v, 0x118, 0xF, true);
+  SW_DPP_D_STEP(v, 0x142, 0xA, false);
+  SW_DPP_D_STEP(v, 0x143, 0xC, false);
+  return v;
+}
+__device__ __forceinline__ double readlane_d63(double v) {
+  const int lo = __builtin_amdgcn_readlane((int)__double2loint(v), 63);
+  const int hi = __builtin_amdgcn_readlane((int)__double2hiint(v), 63);
+  return __hiloint2double(hi, lo);
+}
+
 // largest 64-bit key over the wave (keys encode value and index)
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
 #define SW_U64_STEP(ctrl, rm, bc)                                                           \
