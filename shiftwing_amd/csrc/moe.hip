@@ -643,13 +643,13 @@ __global__ __launch_bounds__(256) void k_router_refine(Work w, const float *x, c
       m = fmax(m, v.x);
       bmax = fmax(bmax, v.y);
     }
-    bmax = wave_max_d(bmax);
+    bmax = wave_max_dpp(bmax);
     // K-th largest lane maximum: K rounds that retire the largest
     double thr = m;
     bool out = false;
     for (int k = 0; k < K && k < 64; k++) {
       const double v = out ? -1e300 : m;
-      const double g = wave_max_d(v);
+      const double g = wave_max_dpp(v);
       const unsigned long long hit = __ballot(!out && m == g);
       if (hit && lane == __ffsll((long long)hit) - 1) out = true;
       thr = g;
@@ -697,10 +697,11 @@ __global__ __launch_bounds__(256) void k_router_refine(Work w, const float *x, c
         pa += fabs(lp);
       }
     }
-    const double off = wave_exclusive_scan(lp, lane);
-    const double L = wave_sum(lp);
-    const double Pb = wave_sum((double)CH * fabs(off) + pa);
-    const double A = wave_sum(aa);
+    const double inc = wave_incl_scan_dpp(lp);
+    const double off = inc - lp;
+    const double L = readlane_d63(inc);
+    const double Pb = wave_sum_dpp((double)CH * fabs(off) + pa);
+    const double A = wave_sum_dpp(aa);
     if (lane == 0) {
       const double u = 0x1p-24;
       const double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;

@@ -204,6 +204,25 @@ __device__ __forceinline__ double wave_incl_scan_dpp(double v) {
   SW_DPP_D_STEP(v, 0x143, 0xC, false);
   return v;
 }
+// largest double over the wave (every lane), by DPP
+__device__ __forceinline__ double wave_max_dpp(double v) {
+#define SW_DPP_D_MAX(ctrl, rm, bc)                                                      \
+  {                                                                                     \
+    const int lo_ = SW_DPP_I((int)__double2loint(v), (int)__double2loint(v), ctrl, rm, bc); \
+    const int hi_ = SW_DPP_I((int)__double2hiint(v), (int)__double2hiint(v), ctrl, rm, bc); \
+    v = fmax(v, __hiloint2double(hi_, lo_));                                            \
+  }
+  SW_DPP_D_MAX(0xB1, 0xF, false);
+  SW_DPP_D_MAX(0x4E, 0xF, false);
+  SW_DPP_D_MAX(0x141, 0xF, false);
+  SW_DPP_D_MAX(0x140, 0xF, false);
+  SW_DPP_D_MAX(0x142, 0xA, false);
+  SW_DPP_D_MAX(0x143, 0xC, false);
+#undef SW_DPP_D_MAX
+  const int lo = __builtin_amdgcn_readlane((int)__double2loint(v), 63);
+  const int hi = __builtin_amdgcn_readlane((int)__double2hiint(v), 63);
+  return __hiloint2double(hi, lo);
+}
 __device__ __forceinline__ double readlane_d63(double v) {
   const int lo = __builtin_amdgcn_readlane((int)__double2loint(v), 63);
   const int hi = __builtin_amdgcn_readlane((int)__double2hiint(v), 63);
