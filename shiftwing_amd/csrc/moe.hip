@@ -1066,11 +1066,14 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
 __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, float *weight, float *prob,
                                  VI *red) {
   __shared__ float s_mx, s_den;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64) {
+    // the largest logit (its value does not depend on the scan order: +0 and
+    // -0 give the same logit - max)
     float mx = -__builtin_huge_valf();
-    for (int e = 0; e < E; e++)
+    for (int e = threadIdx.x; e < E; e += 64)
       if (logit[e] > mx) mx = logit[e];
-    s_mx = mx;
+    mx = wave_max_dpp(mx);
+    if (threadIdx.x == 0) s_mx = mx;
   }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += blockDim.x) prob[e] = expf_glibc(logit[e] - s_mx);
@@ -1085,21 +1088,32 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
   __syncthreads();
   __shared__ int s_idx[kMaxTopK];
   __shared__ float s_w[kMaxTopK];
-  for (int j = 0; j < K; j++) {
-    VI best = {-1.0, -1};
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-      bool used = false;
-      for (int p = 0; p < j; p++) used |= s_idx[p] == e;
-      float pv = prob[e];
-      if (!used && pv > -1.0f) best = vi_better(best, VI{(double)pv, e});
+  if (threadIdx.x < 64) {
+    // K argmax rounds by wave 0 over 64-bit keys (probability, order-
+    // preserving, then the complemented index: the lowest index among
+    // equal values, as the reference's strict '>' in expert order); values
+    // not above -1 never qualify
+    const int lane = threadIdx.x;
+    for (int j = 0; j < K; j++) {
+      unsigned long long best = 0ull;
+      for (int e = lane; e < E; e += 64) {
+        bool used = false;
+        for (int p = 0; p < j; p++) used |= s_idx[p] == e;
+        const float pv = prob[e];
+        const unsigned long long k2 = ((unsigned long long)order_key(pv) << 32) | (unsigned)(~e);
+        if (!used && pv > -1.0f && k2 > best) best = k2;
+      }
+      best = wave_max_u64(best);
+      if (lane == 0) {
+        const int c = best ? (int)(~(unsigned)best) : -1;
+        s_idx[j] = c;
+        s_w[j] = c >= 0 ? prob[c] : -1.0f;
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
-    best = block_argmax(best, red);
-    if (threadIdx.x == 0) {
-      s_idx[j] = best.i;
-      s_w[j] = best.i >= 0 ? (float)best.v : -1.0f;
-    }
-    __syncthreads();
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
     float topden = 0.0f;
     for (int j = 0; j < K; j++) topden += s_w[j];
