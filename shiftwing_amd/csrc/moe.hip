@@ -800,8 +800,7 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
         w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
       }
     }
-    atomicAdd(&stats[0], 1ull);
-    if (!ok) {
+    if (!ok) {  // (tokens routed: counted once per step by k_topk_check)
       atomicAdd(&stats[1], 1ull);
       atomicAdd(&stats[2], 1ull);  // this path always re-runs every expert's chain
     }
@@ -944,7 +943,8 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
     w.certified[t] = verdict;
     if (verdict == 2) w.ulist[atomicAdd(w.ucount, 1)] = t;
     if (verdict == 0) w.flist[atomicAdd(w.fcount, 1)] = t;
-    atomicAdd(&stats[0], 1ull);
+    // (tokens routed are counted once per step by k_topk_check: one atomic
+    // per token on one word would serialise hundreds of them)
     if (verdict != 1) atomicAdd(&stats[1], 1ull);
     if (verdict == 0) atomicAdd(&stats[2], 1ull);
   }
@@ -1137,6 +1137,7 @@ __global__ __launch_bounds__(64) void k_topk_check(Work w, unsigned long long *s
   __shared__ int um[64], sm[64];
   __shared__ float ul[64], sl[64];
   const int nu = *w.ucount, i = threadIdx.x;
+  if (blockIdx.x == 0 && i == 0) atomicAdd(&stats[0], (unsigned long long)w.T);  // tokens routed
   for (int ui = blockIdx.x; ui < nu; ui += gridDim.x) {
     const int t = w.ulist[ui];
     const int n = w.mcount[t];
