@@ -157,9 +157,10 @@ def test_router_paths_many_token_kernels(be, oracle):
 @pytest.mark.parametrize("shape", [(2048, 256, 8, 512, 512, 4), (4096, 512, 10, 1024, 1024, 3)],
                          ids=["s35", "s397"])
 def test_router_gemm_path_steered_block(be, oracle, shape):
-    """Blocks of at least 32 tokens route through the fp64 MFMA GEMM with the
-    a-priori bound, tightened for the experts near each token's top K.  A
-    48-token block whose tokens carry steered gaps (every GAPS value at the
+    """Blocks of at least 64 tokens route through the fp64 MFMA GEMM with the
+    a-priori bound, tightened for the experts near each token's top K.  An
+    80-token block (two full 32-token tiles and a partial one) whose tokens
+    carry steered gaps (every GAPS value at the
     K|K+1 boundary and inside the top K, plus unsteered tokens) must give
     router_topk's indices for every token (c/qwen.c:3421) and outputs within
     max-abs 1e-3 x RMS of moe_prefill_grouped."""
@@ -170,7 +171,7 @@ def test_router_gemm_path_steered_block(be, oracle, shape):
     L = MoeLayer(be, H, E, K, I, Ish, fmt)
     L.synthesize(seed, 4)
     xs = []
-    for t in range(48):
+    for t in range(80):
         x0 = oracle.synth_x(seed, 4, t, H)
         case = t % (2 * len(GAPS) + 2)
         if case < 2 * len(GAPS):
@@ -179,7 +180,7 @@ def test_router_gemm_path_steered_block(be, oracle, shape):
             x0 = _steer(hl.router_w, x0, int(order[rank]), int(order[rank + 1]), GAPS[case % len(GAPS)])
         xs.append(x0)
     x = np.stack(xs)
-    print(f"[router gemm] H{H} E{E} block of 48", flush=True)
+    print(f"[router gemm] H{H} E{E} block of 80", flush=True)
     before = L.route_stats_full()
     try:
         want, tr = oracle.moe_prefill(hl, x, trace=True)
@@ -187,7 +188,7 @@ def test_router_gemm_path_steered_block(be, oracle, shape):
         after = L.route_stats_full()
     finally:
         L.close()
-    bad = [t for t in range(48) if not np.array_equal(idx[t], tr["idx"][t])]
+    bad = [t for t in range(80) if not np.array_equal(idx[t], tr["idx"][t])]
     assert not bad, f"tokens {bad[:8]}: {idx[bad[0]]} vs {tr['idx'][bad[0]]}"
     assert np.max(np.abs(w - tr["weight"])) <= 1e-5
     assert_close_rms(y, want, 1e-3, f"router gemm block H{H}")
