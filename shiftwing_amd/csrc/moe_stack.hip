@@ -70,7 +70,7 @@ constexpr int kGMax = 4;         // stage G: groups per wave and unit
 #define SW_SHDOWN_LATE 1
 #endif
 #ifndef SW_STACK_GRING
-#define SW_STACK_GRING 4
+#define SW_STACK_GRING 2
 #endif
 constexpr int kGRing = SW_STACK_GRING;  // stage G: ring slots per wave
 constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
