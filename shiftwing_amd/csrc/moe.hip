@@ -254,6 +254,7 @@ struct Work {
   // router
   double2 *lb; float *sgate; int *certified; float *logits;
   int *ulist, *ucount;  // tokens on the targeted exact path, and their count
+  int *udone, *fdone;   // per token: exact chains finished (targeted, full path)
   int *flist, *fcount;  // tokens needing every expert's chain and the router_topk replica
   int *mset, *mcount;  // per token: experts of the targeted exact path (<= 64)
   int *idx; float *w;
@@ -285,6 +286,8 @@ size_t carve(Work &w, char *base) {
   w.sgate = (float *)take((size_t)T * 4);
   w.certified = (int *)take((size_t)T * 4);
   w.ulist = (int *)take((size_t)T * 4);
+  w.udone = (int *)take((size_t)T * 4);
+  w.fdone = (int *)take((size_t)T * 4);
   w.ucount = (int *)take(16);
   w.flist = (int *)take((size_t)T * 4);
   w.fcount = (int *)take(16);
@@ -339,6 +342,7 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x) {
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const float *xt = x + (size_t)t * w.H;
   if (t == 0 && tid == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
+  if (tid == 0) w.udone[t] = w.fdone[t] = 0;
   const int nq = w.H / 4, nqp = w.ngh * 32;  // float4 chunks of the row, of the padded row
   const bool al = ((uintptr_t)xt & 15) == 0;
   float4 v[C];
@@ -400,6 +404,7 @@ __global__ void k_prep_x_any(Work w, const float *x) {
   int t = blockIdx.x;
   const float *xt = x + (size_t)t * w.H;
   if (t == 0 && threadIdx.x == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
+  if (threadIdx.x == 0) w.udone[t] = w.fdone[t] = 0;
   float s = qrow_i8_block(xt, w.H, w.xq + (size_t)t * w.H, red);
   if (threadIdx.x == 0) w.sx[t] = s;
   quantize_digits(xt, w.H, w.ngh, w.xd1 + (size_t)t * w.Hp, w.xd2 + (size_t)t * w.Hp, w.xgp + (size_t)t * w.ngh);
@@ -800,7 +805,7 @@ __global__ void k_certify(Work w, int mode, unsigned long long *stats) {
         w.w[(size_t)t * w.K + r] = (float)(p[r] / den);
       }
     }
-    if (!ok) {  // (tokens routed: counted once per step by k_topk_check)
+    if (!ok) {  // (tokens routed: counted once per step by k_exact_logits)
       atomicAdd(&stats[1], 1ull);
       atomicAdd(&stats[2], 1ull);  // this path always re-runs every expert's chain
     }
@@ -943,7 +948,7 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
     w.certified[t] = verdict;
     if (verdict == 2) w.ulist[atomicAdd(w.ucount, 1)] = t;
     if (verdict == 0) w.flist[atomicAdd(w.fcount, 1)] = t;
-    // (tokens routed are counted once per step by k_topk_check: one atomic
+    // (tokens routed are counted once per step by k_exact_logits: one atomic
     // per token on one word would serialise hundreds of them)
     if (verdict != 1) atomicAdd(&stats[1], 1ull);
     if (verdict == 0) atomicAdd(&stats[2], 1ull);
@@ -1024,6 +1029,60 @@ __device__ __forceinline__ void form_products(const float *xt, const float *row,
   }
 }
 
+// Token t on the targeted path: M ordered by (exact logit desc, index asc);
+// the order and the k|k+1 boundary hold if consecutive exact logits are
+// separated by the margin and the K-th lies within 80 of the max (experts
+// outside M are below every candidate by more than the margin).  Weights then
+// come from the fp64 logits as for certified tokens.  Otherwise the token
+// joins the full path (every chain and the router_topk replica).  Run by one
+// 64-thread block once every chain of the token's M is written.
+__device__ void topk_check_token(Work &w, int t, unsigned long long *stats) {
+  __shared__ int um[64], sm[64];
+  __shared__ float ul[64], sl[64];
+  const int i = threadIdx.x;
+  const int n = w.mcount[t];
+  if (i < n) {
+    um[i] = w.mset[(size_t)t * 64 + i];
+    ul[i] = __hip_atomic_load(&w.logits[(size_t)t * w.E + um[i]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (i < n) {  // rank by (exact logit desc, index asc)
+    const int e = um[i];
+    const float l = ul[i];
+    int rank = 0;
+    for (int j = 0; j < n; j++) rank += ul[j] > l || (ul[j] == l && um[j] < e);
+    sm[rank] = e;
+    sl[rank] = l;
+  }
+  __syncthreads();
+  {
+    // lane r checks ranks r and r+1; the weights one exp per lane
+    const double mx = sl[0];
+    bool pair = true;
+    if (i < w.K && i + 1 < n) {
+      const double a = sl[i], b = sl[i + 1];
+      pair = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
+    }
+    bool ok = n >= w.K && __all(pair);
+    if (ok) ok = (double)sl[w.K - 1] - mx > -80.0;
+    if (ok) {
+      const double2 *lb = w.lb + (size_t)t * (w.E + 1);
+      const double lmx = lb[sm[0]].x;
+      const double ev = i < w.K ? exp(lb[sm[i]].x - lmx) : 0.0;
+      const double den = wave_sum(ev);
+      if (i < w.K) {
+        w.idx[(size_t)t * w.K + i] = sm[i];
+        w.w[(size_t)t * w.K + i] = (float)(ev / den);
+      }
+    } else if (i == 0) {
+      atomicAdd(&stats[2], 1ull);
+      w.certified[t] = 0;
+      w.flist[atomicAdd(w.fcount, 1)] = t;
+    }
+  }
+  __syncthreads();  // the token's LDS is read no more
+}
+
 // ---------------------------------------------------------------------------
 // 4. exact logits for the tokens the bounds did not certify: the experts of
 // the targeted set (certified 2) or every expert (certified 0).  The products
@@ -1034,8 +1093,12 @@ __device__ __forceinline__ void form_products(const float *xt, const float *row,
 // grid (64, kUncertainSlots), 64 threads, dynamic LDS 4*H bytes.
 // ---------------------------------------------------------------------------
 constexpr int kUncertainSlots = 128;
-__global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, const float *router) {
+__global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, const float *router,
+                                                     unsigned long long *stats) {
   extern __shared__ float prod[];
+  __shared__ int s_last;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    atomicAdd(&stats[0], (unsigned long long)w.T);  // tokens routed, once per step
   const int nu = *w.ucount;
   const int m = (w.H / 8) * 8;
   for (int ui = blockIdx.y; ui < nu; ui += gridDim.y) {
@@ -1052,8 +1115,12 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
         float s = serial_sum_lds(prod, m64);
         for (int i = m64; i < m; i++) s = __fadd_rn(s, prod[i]);
         for (int i = m; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
-        w.logits[(size_t)t * w.E + e] = s;
+        __hip_atomic_store(&w.logits[(size_t)t * w.E + e], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the block that writes the token's last chain checks it
+        s_last = __hip_atomic_fetch_add(&w.udone[t], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
       }
+      __syncthreads();
+      if (s_last) topk_check_token(w, t, stats);
       __syncthreads();
     }
   }
@@ -1063,8 +1130,7 @@ __global__ __launch_bounds__(64) void k_exact_logits(Work w, const float *x, con
 // denominator in expert order, glibc expf, K argmax rounds with strict '>'
 // (lowest index on ties, -1 if nothing beats -1), serial renormalisation.
 // One block per token; `skip` (may be null) marks certified tokens.
-__device__ void topk_exact_block(const float *logit, int E, int K, int *idx, float *weight, float *prob,
-                                 VI *red) {
+__device__ void topk_exact_block(const float *logit, int E, int K, int *idx, float *weight, float *prob) {
   __shared__ float s_mx, s_den;
   if (threadIdx.x < 64) {
     // the largest logit (its value does not depend on the scan order: +0 and
@@ -1125,72 +1191,15 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
   __syncthreads();
 }
 
-// Tokens on the targeted path: M ordered by (exact logit desc, index asc);
-// the order and the k|k+1 boundary hold if consecutive exact logits are
-// separated by the margin and the K-th lies within 80 of the max (experts
-// outside M are below every candidate by more than the margin).  Weights then
-// come from the fp64 logits as for certified tokens.  Otherwise the token
-// joins the full path (every chain and the router_topk replica).
-// grid kTopkSlots, 64 threads; blocks walk the targeted list.
-constexpr int kTopkSlots = 128;
-__global__ __launch_bounds__(64) void k_topk_check(Work w, unsigned long long *stats) {
-  __shared__ int um[64], sm[64];
-  __shared__ float ul[64], sl[64];
-  const int nu = *w.ucount, i = threadIdx.x;
-  if (blockIdx.x == 0 && i == 0) atomicAdd(&stats[0], (unsigned long long)w.T);  // tokens routed
-  for (int ui = blockIdx.x; ui < nu; ui += gridDim.x) {
-    const int t = w.ulist[ui];
-    const int n = w.mcount[t];
-    if (i < n) {
-      um[i] = w.mset[(size_t)t * 64 + i];
-      ul[i] = w.logits[(size_t)t * w.E + um[i]];
-    }
-    __syncthreads();
-    if (i < n) {  // rank by (exact logit desc, index asc)
-      const int e = um[i];
-      const float l = ul[i];
-      int rank = 0;
-      for (int j = 0; j < n; j++) rank += ul[j] > l || (ul[j] == l && um[j] < e);
-      sm[rank] = e;
-      sl[rank] = l;
-    }
-    __syncthreads();
-    {
-      // lane r checks ranks r and r+1; the weights one exp per lane
-      const double mx = sl[0];
-      bool pair = true;
-      if (i < w.K && i + 1 < n) {
-        const double a = sl[i], b = sl[i + 1];
-        pair = a - b > 0x1p-20 * (1.0 + fabs(a) + fabs(b) + 2.0 * fabs(mx));
-      }
-      bool ok = n >= w.K && __all(pair);
-      if (ok) ok = (double)sl[w.K - 1] - mx > -80.0;
-      if (ok) {
-        const double2 *lb = w.lb + (size_t)t * (w.E + 1);
-        const double lmx = lb[sm[0]].x;
-        const double ev = i < w.K ? exp(lb[sm[i]].x - lmx) : 0.0;
-        const double den = wave_sum(ev);
-        if (i < w.K) {
-          w.idx[(size_t)t * w.K + i] = sm[i];
-          w.w[(size_t)t * w.K + i] = (float)(ev / den);
-        }
-      } else if (i == 0) {
-        atomicAdd(&stats[2], 1ull);
-        w.certified[t] = 0;
-        w.flist[atomicAdd(w.fcount, 1)] = t;
-      }
-    }
-    __syncthreads();  // the token's LDS is read no more
-  }
-}
-
 // Every expert's exact logit for the tokens on the full path: one block an
 // (expert, token) pair, the products formed with coalesced loads into LDS and
-// summed serially by one lane as in k_exact_logits.
-// grid (min(E, 1024), kFullSlots), 64 threads, dynamic LDS 4*H bytes.
+// summed serially by one lane as in k_exact_logits.  The block that writes a
+// token's last chain runs router_topk's replica for it.
+// grid (min(E, 1024), kFullSlots), 64 threads, dynamic LDS 4*max(H, 2E) bytes.
 constexpr int kFullSlots = 8;
 __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const float *router) {
-  extern __shared__ float prod[];
+  extern __shared__ float prod[];  // the products; for the replica, the token's logits and probabilities
+  __shared__ int s_last;
   const int nf = *w.fcount;
   const int m = (w.H / 8) * 8;
   for (int fi = blockIdx.y; fi < nf; fi += gridDim.y) {
@@ -1205,31 +1214,26 @@ __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const
         float s = serial_sum_lds(prod, m64);
         for (int i = m64; i < m; i++) s = __fadd_rn(s, prod[i]);
         for (int i = m; i < w.H; i++) s = __fmaf_rn(xt[i], row[i], s);
-        w.logits[(size_t)t * w.E + e] = s;
+        __hip_atomic_store(&w.logits[(size_t)t * w.E + e], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = __hip_atomic_fetch_add(&w.fdone[t], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == w.E - 1;
+      }
+      __syncthreads();
+      if (s_last) {
+        float *lg = prod, *pb = prod + w.E;
+        for (int e2 = threadIdx.x; e2 < w.E; e2 += blockDim.x)
+          lg[e2] = __hip_atomic_load(&w.logits[(size_t)t * w.E + e2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        topk_exact_block(lg, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K, pb);
       }
       __syncthreads();
     }
   }
 }
 
-// router_topk replica for the tokens on the full path.  grid kFullSlots, 512 threads.
-__global__ void k_topk_full(Work w) {
-  __shared__ VI red[16];
-  __shared__ float prob[4096];
-  const int nf = *w.fcount;
-  for (int fi = blockIdx.x; fi < nf; fi += gridDim.x) {
-    const int t = w.flist[fi];
-    topk_exact_block(w.logits + (size_t)t * w.E, w.E, w.K, w.idx + (size_t)t * w.K, w.w + (size_t)t * w.K,
-                     prob, red);
-    __syncthreads();
-  }
-}
-
 __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx, float *weight) {
-  __shared__ VI red[16];
   __shared__ float prob[4096];
   int t = blockIdx.x;
-  topk_exact_block(logits + (size_t)t * E, E, K, idx + (size_t)t * K, weight + (size_t)t * K, prob, red);
+  topk_exact_block(logits + (size_t)t * E, E, K, idx + (size_t)t * K, weight + (size_t)t * K, prob);
 }
 
 // ---------------------------------------------------------------------------
@@ -2766,12 +2770,12 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   else
     k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
   if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
-  k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(w, x,
-                                                                                                      L->router);
-  k_topk_check<<<w.T < kTopkSlots ? w.T : kTopkSlots, 64, 0, st>>>(w, L->stats);
-  k_exact_full<<<dim3(w.E < 1024 ? w.E : 1024, w.T < kFullSlots ? w.T : kFullSlots), 64, (size_t)w.H * 4, st>>>(
-      w, x, L->router);
-  k_topk_full<<<w.T < kFullSlots ? w.T : kFullSlots, 512, 0, st>>>(w);
+  k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(
+      w, x, L->router, L->stats);
+  const size_t full_lds = (size_t)4 * (w.H > 2 * w.E ? w.H : 2 * w.E);
+  if (set_lds((const void *)k_exact_full, full_lds)) return -1;
+  k_exact_full<<<dim3(w.E < 1024 ? w.E : 1024, w.T < kFullSlots ? w.T : kFullSlots), 64, full_lds, st>>>(w, x,
+                                                                                                       L->router);
   return launch_status("MoE routing kernels");
 }
 
