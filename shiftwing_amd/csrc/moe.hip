@@ -2174,8 +2174,14 @@ constexpr int kWideTokens = 16;  // tokens per item (the MFMA's B columns)
 #define SW_WIDE_WAVES 8
 #endif
 constexpr int kWideWaves = SW_WIDE_WAVES;  // waves per block
-constexpr int kWideRt = 1, kWideGuBatch = SW_WIDE_GU_RING;
-constexpr int kWideDnRt = 2, kWideDnBatch = SW_WIDE_DN_RING;
+#ifndef SW_WIDE_GU_RT
+#define SW_WIDE_GU_RT 1
+#endif
+#ifndef SW_WIDE_DN_RT
+#define SW_WIDE_DN_RT 2
+#endif
+constexpr int kWideRt = SW_WIDE_GU_RT, kWideGuBatch = SW_WIDE_GU_RING;
+constexpr int kWideDnRt = SW_WIDE_DN_RT, kWideDnBatch = SW_WIDE_DN_RING;
 
 // LDS of one item over ng groups: digits [group][plane][half][lane] 16 B,
 // then (A, B, K, 0) per [group][token]
