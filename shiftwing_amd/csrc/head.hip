@@ -12,9 +12,9 @@
 // The projection streams the vocab x hidden int8 matrix once per group of up
 // to four tokens (HBM-bound: 1.02 GB for 248,320 x 4096).  Each lane keeps
 // its 16-byte column chunks of the quantised activations in registers; a
-// wave takes kHeadRows rows, loads every chunk of them before the first
-// dot (16 KB in flight per wave at hidden 4096), and reduces the exact int32
-// sums across the wave.
+// wave takes kHeadRows rows (one: 1, 2, 4 and 8 measured 5,750, 5,680, 5,520
+// and 5,420 calls/s at S397), loads every chunk of them before the first
+// dot, and reduces the exact int32 sums across the wave by DPP.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,7 +72,13 @@ __global__ __launch_bounds__(256) void k_head_norm(signed char *xq, float *sx, f
   for (int i = threadIdx.x; i < pitch; i += blockDim.x) qs[i] = i < n ? (signed char)__builtin_rintf(hp[i] * inv) : 0;
 }
 
-constexpr int kHeadRows = 4;  // rows per wave
+#ifndef SW_HEAD_DPP
+#define SW_HEAD_DPP 1
+#endif
+#ifndef SW_HEAD_ROWS
+#define SW_HEAD_ROWS 1
+#endif
+constexpr int kHeadRows = SW_HEAD_ROWS;  // rows per wave
 
 __device__ __forceinline__ int dot16(const v4i w, const v4i x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
@@ -118,7 +124,11 @@ __global__ __launch_bounds__(256) void k_head_q8(float *logits, const signed cha
       int acc = 0;
 #pragma unroll
       for (int c = 0; c < NCH; c++) acc = dot16(wv[i][c], xr[b][c], acc);
+#if SW_HEAD_DPP
+      acc = wave_sum_dpp(acc);
+#else
       acc = wave_sum_i(acc);
+#endif
       if (lane == 0 && row < rows) logits[(size_t)b * rows + row] = ((float)acc * scales[row]) * sx[b];
     }
   }
