@@ -38,16 +38,10 @@ __global__ __launch_bounds__(256) void k_head_norm(signed char *xq, float *sx, f
   for (int i = threadIdx.x; i < n; i += blockDim.x) hp[i] = xs[i] * xs[i];
   __syncthreads();
   if (threadIdx.x == 0) {
-    float ms = 0.0f;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-      const float4 v = *(const float4 *)(hp + i);
-      ms = ms + v.x;
-      ms = ms + v.y;
-      ms = ms + v.z;
-      ms = ms + v.w;
-    }
-    for (; i < n; i++) ms = ms + hp[i];
+    // LDS reads of the next 32 squares issued before the current 32 adds
+    const int n64 = n / 64 * 64;
+    float ms = serial_sum_lds(hp, n64);
+    for (int i = n64; i < n; i++) ms = __fadd_rn(ms, hp[i]);
     s_r = 1.0f / sqrtf(ms / (float)n + eps);
   }
   __syncthreads();

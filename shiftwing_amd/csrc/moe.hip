@@ -974,37 +974,6 @@ __device__ float exact_chain(const float *xt, const float *row, int H) {
   return s;
 }
 
-// s = rn(s + p[i]) for i < m in order (the reference's serial chain over
-// precomputed products), by one lane, m % 64 == 0: the LDS reads of the next
-// 32 terms are issued before the adds of the current 32, so the chain runs at
-// the rate of its dependent adds.
-__device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; k++) {
-    s = __fadd_rn(s, v[k].x);
-    s = __fadd_rn(s, v[k].y);
-    s = __fadd_rn(s, v[k].z);
-    s = __fadd_rn(s, v[k].w);
-  }
-}
-__device__ __forceinline__ float serial_sum_lds(const float *p, int m) {
-  float s = 0.0f;
-  float4 a[8], b[8];
-#pragma unroll
-  for (int k = 0; k < 8; k++) a[k] = ((const float4 *)p)[k];
-  for (int i = 0; i < m; i += 64) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) b[k] = ((const float4 *)(p + i + 32))[k];
-    add32(s, a);
-    if (i + 64 < m) {
-#pragma unroll
-      for (int k = 0; k < 8; k++) a[k] = ((const float4 *)(p + i + 64))[k];
-    }
-    add32(s, b);
-  }
-  return s;
-}
-
 // prod[i] = rn(x[i]*row[i]) for i < m (m % 4 == 0) by the block's 64 lanes:
 // kProdBatch float4 pairs of loads in flight per lane before the first store
 constexpr int kProdBatch = 8;
