@@ -1213,14 +1213,20 @@ __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx
 // ---------------------------------------------------------------------------
 __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
                              int *pos, int4 *items, int *nitems, unsigned *bits, int *cnt, int *iofs, int itok) {
+  __shared__ int s_dup;  // some token lists an expert twice
   int words = (T + 31) / 32;
   for (int i = threadIdx.x; i < E * words; i += blockDim.x) bits[i] = 0;
+  if (threadIdx.x == 0) s_dup = 0;
   __syncthreads();
   for (int r = threadIdx.x; r < T * K; r += blockDim.x) {
     int e = idx[r];
-    if (e >= 0 && e < E) atomicOr(&bits[e * words + r / K / 32], 1u << ((r / K) & 31));
+    if (e >= 0 && e < E) {
+      const unsigned bit = 1u << ((r / K) & 31);
+      if (atomicOr(&bits[e * words + r / K / 32], bit) & bit) s_dup = 1;
+    }
   }
   __syncthreads();
+  const bool dup = s_dup != 0;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int c = 0;
     for (int q = 0; q < words; q++) c += __popc(bits[e * words + q]);
@@ -1275,9 +1281,11 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
       pos[r] = -1;
       continue;
     }
-    // the reference's gather takes the first matching k of a token
+    // the reference's gather takes the first matching k of a token (only a
+    // step with a repeated expert in some token's list needs the check)
     bool first = true;
-    for (int k2 = 0; k2 < k; k2++) first &= idx[t * K + k2] != e;
+    if (dup)
+      for (int k2 = 0; k2 < k; k2++) first &= idx[t * K + k2] != e;
     if (!first) {
       pos[r] = -1;
       continue;

@@ -95,3 +95,22 @@ def test_bucket_matches_reference_order(be, oracle):
         assert np.array_equal(be.download(do, (E + 1,), np.int32), off)
         assert np.array_equal(be.download(dt, (T * K,), np.int32)[:len(tok)], tok)
         assert np.array_equal(be.download(ds, (T * K,), np.int32)[:len(slot)], slot)
+
+
+def test_bucket_repeated_experts_match_reference(be, oracle):
+    """Lists that name an expert twice take the reference's first matching k
+    (moe_prefill_route_gather, c/qwen.c:3956-3968): a step of repeats on few
+    experts, and a step where one token of many repeats an expert (the device
+    checks first occurrences only when some list repeats)."""
+    rng = np.random.default_rng(21)
+    many = np.stack([rng.choice(512, 10, replace=False) for _ in range(300)]).astype(np.int32)
+    many[137, 6] = many[137, 2]
+    for idx, E in [(rng.integers(0, 6, (40, 5)).astype(np.int32), 6), (many, 512)]:
+        T, K = idx.shape
+        off, tok, slot = oracle.bucket(idx, E)
+        di = be.upload(idx)
+        do, dt, ds = be.alloc((E + 1) * 4), be.alloc(T * K * 4), be.alloc(T * K * 4)
+        be.check(be.lib.coli_cuda_moe_bucket(be.ctx, di.p, T, K, E, do.p, dt.p, ds.p))
+        assert np.array_equal(be.download(do, (E + 1,), np.int32), off)
+        assert np.array_equal(be.download(dt, (T * K,), np.int32)[:len(tok)], tok)
+        assert np.array_equal(be.download(ds, (T * K,), np.int32)[:len(slot)], slot)
