@@ -2438,26 +2438,40 @@ __global__ __launch_bounds__(64 * kWideWaves) void k_down_wide(Work w, ExpertLay
 // shared.  grid (ceil(H/256), T), 256 threads.
 // ---------------------------------------------------------------------------
 __global__ void k_combine(Work w, float *y, int *route_idx, float *route_weight) {
-  int h = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  // the token's positions and weights in LDS, then every route's value of
+  // this column loaded before the sums (which keep the reference's order)
+  __shared__ int s_pos[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
+  const int h = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (threadIdx.x < w.K) {
+    s_pos[threadIdx.x] = w.pos[(size_t)t * w.K + threadIdx.x];
+    s_w[threadIdx.x] = w.w[(size_t)t * w.K + threadIdx.x];
+  }
+  __syncthreads();
   if (h < w.H) {
-    float sg = w.sgate[t];
-    float sh = w.shout[(size_t)t * w.H + h];
+    const float sg = w.sgate[t];
+    const float sh = w.shout[(size_t)t * w.H + h];
+    float v[kMaxTopK];
+#pragma unroll
+    for (int k = 0; k < kMaxTopK; k++)
+      if (k < w.K) {
+        const int p = s_pos[k];
+        v[k] = p >= 0 ? w.rout[(size_t)p * w.H + h] : 0.0f;
+      }
     float out = 0.0f;
     if (w.T == 1) {
-      for (int k = 0; k < w.K; k++) {
-        int p = w.pos[(size_t)t * w.K + k];
-        float v = p >= 0 ? w.rout[(size_t)p * w.H + h] : 0.0f;
-        out = __builtin_fmaf(v, w.w[(size_t)t * w.K + k], out);
-      }
+#pragma unroll
+      for (int k = 0; k < kMaxTopK; k++)
+        if (k < w.K) out = __builtin_fmaf(v[k], s_w[k], out);
       out = __builtin_fmaf(sh, sg, out);
     } else {
-      float shs = sh * sg;
-      for (int k = 0; k < w.K; k++) {
-        int p = w.pos[(size_t)t * w.K + k];
-        float v = p >= 0 ? w.rout[(size_t)p * w.H + h] : 0.0f;
-        float r = v * w.w[(size_t)t * w.K + k];
-        out = out + r;
-      }
+      const float shs = sh * sg;
+#pragma unroll
+      for (int k = 0; k < kMaxTopK; k++)
+        if (k < w.K) {
+          const float r = v[k] * s_w[k];
+          out = out + r;
+        }
       out = out + shs;
     }
     y[(size_t)t * w.H + h] = out;
