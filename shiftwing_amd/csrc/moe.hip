@@ -552,11 +552,6 @@ __device__ __forceinline__ double wave_max_d(double v) {
   for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
   return v;
 }
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
-  return v;
-}
 
 // a-priori bound factor: (gamma_H(2^-24) + gamma_H(2^-53)) with slack for the
 // rounding of the norms and of the product that applies it
