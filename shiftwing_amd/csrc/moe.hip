@@ -1109,8 +1109,10 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
   for (int e = threadIdx.x; e < E; e += blockDim.x) prob[e] = expf_glibc(logit[e] - s_mx);
   __syncthreads();
   if (threadIdx.x == 0) {
-    float den = 0.0f;
-    for (int e = 0; e < E; e++) den += prob[e];
+    // the serial denominator in expert order, its LDS reads run ahead
+    const int e64 = E / 64 * 64;
+    float den = serial_sum_lds(prob, e64);
+    for (int e = e64; e < E; e++) den = __fadd_rn(den, prob[e]);
     s_den = den;
   }
   __syncthreads();
@@ -1159,7 +1161,7 @@ __device__ void topk_exact_block(const float *logit, int E, int K, int *idx, flo
 // (expert, token) pair, the products formed with coalesced loads into LDS and
 // summed serially by one lane as in k_exact_logits.  The block that writes a
 // token's last chain runs router_topk's replica for it.
-// grid (min(E, 1024), kFullSlots), 64 threads, dynamic LDS 4*max(H, 2E) bytes.
+// grid (min(E, 1024), kFullSlots), 64 threads, dynamic LDS 4*max(H, 2*round4(E)) bytes.
 constexpr int kFullSlots = 8;
 __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const float *router) {
   extern __shared__ float prod[];  // the products; for the replica, the token's logits and probabilities
@@ -1183,7 +1185,7 @@ __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const
       }
       __syncthreads();
       if (s_last) {
-        float *lg = prod, *pb = prod + w.E;
+        float *lg = prod, *pb = prod + ((w.E + 3) & ~3);  // 16-byte aligned: read as float4
         for (int e2 = threadIdx.x; e2 < w.E; e2 += blockDim.x)
           lg[e2] = __hip_atomic_load(&w.logits[(size_t)t * w.E + e2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
@@ -1195,7 +1197,7 @@ __global__ __launch_bounds__(64) void k_exact_full(Work w, const float *x, const
 }
 
 __global__ void k_router_topk_logits(const float *logits, int E, int K, int *idx, float *weight) {
-  __shared__ float prob[4096];
+  __shared__ __align__(16) float prob[4096];
   int t = blockIdx.x;
   topk_exact_block(logits + (size_t)t * E, E, K, idx + (size_t)t * K, weight + (size_t)t * K, prob);
 }
@@ -2764,7 +2766,8 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
   k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(
       w, x, L->router, L->stats);
-  const size_t full_lds = (size_t)4 * (w.H > 2 * w.E ? w.H : 2 * w.E);
+  const int e4 = (w.E + 3) & ~3;
+  const size_t full_lds = (size_t)4 * (w.H > 2 * e4 ? w.H : 2 * e4);
   if (set_lds((const void *)k_exact_full, full_lds)) return -1;
   k_exact_full<<<dim3(w.E < 1024 ? w.E : 1024, w.T < kFullSlots ? w.T : kFullSlots), 64, full_lds, st>>>(w, x,
                                                                                                        L->router);
