@@ -240,7 +240,10 @@ __device__ float qrow_i8_block(const float *x, int n, signed char *q, float *red
 // split the shared gate/up's k range over kShSplit blocks per row tile.
 constexpr int kSharedSub = 4;
 constexpr int kSharedBlockTokens = 16 * kSharedSub;
-constexpr int kShSplit = 4, kShSplitTokens = 32;
+#ifndef SW_SH_SPLIT_TOKENS
+#define SW_SH_SPLIT_TOKENS 64
+#endif
+constexpr int kShSplit = 4, kShSplitTokens = SW_SH_SPLIT_TOKENS;
 
 // ---------------------------------------------------------------------------
 // per-call workspace carved from one scratch buffer
@@ -1620,17 +1623,18 @@ __global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char
   }
 }
 
-// Shared gate/up of small steps (T <= kShSplitTokens): block (row tile,
-// k part ks) forms the exact int32 dots of its 16 rows over k chunks
-// [ks*nk/kShSplit, (ks+1)*nk/kShSplit) for NS 16-token chunks, 4 waves
-// splitting the part, and stores them to shpart[ks]; k_prep_hidden adds the
-// parts (exact) and applies the reference's rounding.  grid (Ish/16,
-// kShSplit), 256 threads.
+// Shared gate/up of small steps (T <= kShSplitTokens, 64: at S397 the split
+// halves the stage at 64 tokens and costs 4 us at 512): block (row tile, k
+// part ks, token block z) forms the exact int32 dots of its 16 rows over k
+// chunks [ks*nk/kShSplit, (ks+1)*nk/kShSplit) for NS 16-token chunks from
+// token 16*NS*z, 4 waves splitting the part, and stores them to shpart[ks];
+// k_prep_hidden adds the parts (exact) and applies the reference's rounding.
+// grid (Ish/16, kShSplit, ceil(T/(16 NS))), 256 threads.
 template <int NS>
 __global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed char *gq, const signed char *uq) {
   __shared__ int part[4][2][NS][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rt = blockIdx.x, ks = blockIdx.y;
+  const int rt = blockIdx.x, ks = blockIdx.y, t0 = blockIdx.z * 16 * NS;
   const int nk = w.H / 64;
   const int p0 = ks * nk / kShSplit, p1 = (ks + 1) * nk / kShSplit;
   const int kc0 = p0 + wave * (p1 - p0) / 4, kc1 = p0 + (wave + 1) * (p1 - p0) / 4;
@@ -1643,7 +1647,7 @@ __global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed ch
     bool bok[NS];
 #pragma unroll
     for (int q = 0; q < NS; q++) {
-      const int tok = 16 * q + r;
+      const int tok = t0 + 16 * q + r;
       bok[q] = tok < w.T;
       brow[q] = w.xq + (size_t)(bok[q] ? tok : 0) * w.H + kb * 16;
     }
@@ -1677,7 +1681,7 @@ __global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed ch
   __syncthreads();
   const int q = wave;
   if (q >= NS) return;
-  const int kb = lane >> 4, tok = 16 * q + (lane & 15);
+  const int kb = lane >> 4, tok = t0 + 16 * q + (lane & 15);
   if (tok >= w.T) return;
   int *dst = w.shpart + ((size_t)ks * w.T + tok) * 2 * w.Ish;
 #pragma unroll
@@ -2879,8 +2883,10 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   prof_mark(ctx, kStageSetup);
   if (T <= 16)
     k_shared_gu_split<1><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
-  else if (T <= kShSplitTokens)
+  else if (T <= 32)
     k_shared_gu_split<2><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
+  else if (T <= kShSplitTokens)
+    k_shared_gu_split<4><<<dim3(w.Ish / kTileRows, kShSplit, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
   else
     k_shared_swiglu<4><<<dim3(w.Ish / kTileRows, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq,
                                                                               L->sh_us);
