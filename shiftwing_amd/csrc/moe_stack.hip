@@ -73,7 +73,14 @@ constexpr int kGMax = 4;         // stage G: groups per wave and unit
 #define SW_STACK_GRING 2
 #endif
 constexpr int kGRing = SW_STACK_GRING;  // stage G: ring slots per wave
-constexpr int kSplitUnits = 128; // stage G: units of the last round that may be split in halves
+// Stage G: units of the last round that may be split in halves over pairs of
+// workgroups.  0 (no split) measured faster with the two-record ring: S397
+// 489 against 484 tok/s, S35 1,221 against 1,189 (the split's code and
+// exchange cost more than the uneven last round).
+#ifndef SW_SPLIT_UNITS
+#define SW_SPLIT_UNITS 0
+#endif
+constexpr int kSplitUnits = SW_SPLIT_UNITS;
 constexpr int kGHead = 2560;     // stage G: partial sums and digit staging before the rings
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
