@@ -380,17 +380,22 @@ void coli_cuda_container_close(ColiContainer *c);
 /* tensors indexed over all files */
 int coli_cuda_container_tensors(const ColiContainer *c);
 /* MoE layer `layer` as stored: hidden, experts, intermediate,
- * shared_intermediate, expert_format (3 or 4; 2 for int2, which the device
- * layer does not take) and group_size.  topk is not stored: shape->topk is
- * left as the caller set it.  use_q3 selects every routed expert's .q3
- * sidecar (the reference's EXPERT_Q3=1). */
-int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int use_q3,
+ * shared_intermediate, expert_format (3 or 4; 2 for int2) and group_size.
+ * topk is not stored: shape->topk is left as the caller set it.  sidecar
+ * selects the routed experts' payload as the reference's switches do
+ * (find_qmat_named, c/qwen.c:2198-2214): 0 the main payload, 1 the .q3
+ * sidecar of every expert (EXPERT_Q3=1; required), 2 the .q2 sidecar where an
+ * expert has one, else its main payload (EXPERT_Q2=1). */
+int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int sidecar,
                                   ColiMoeShape *shape);
 /* Create an HBM-resident layer and fill it from the container: router and
- * gate row (F32, BF16 or F16), the int8 shared expert, every routed expert
- * (int4, or int3 from the sidecar), repacked on the device. */
+ * gate row (F32, BF16 or F16), the int8 shared expert (one scale per row),
+ * every routed expert (int4, or int3 from the .q3 sidecar, in groups of 128),
+ * repacked on the device.  int2 experts (.q2 sidecars, .qtype 2) and other
+ * group sizes, which the reference's CPU path reads, return -1 with a message:
+ * the device layer does not take them. */
 int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer,
-                             int topk, int use_q3, ColiMoeLayer **out);
+                             int topk, int sidecar, ColiMoeLayer **out);
 
 /* The MoE step for `tokens` activation rows (any number: a long block runs
  * as balanced steps of at most 2048 tokens, fewer for more than 512
@@ -406,10 +411,16 @@ int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *layer, float *y,
 /* The MoE half of a decoder layer on the residual stream, in place:
  * n = rmsnorm_zero(x, norm_weight) (c/qwen.c:1780-1784, 4593), then
  * x += MoE(n) (c/qwen.c:4594-4596).  x: device [tokens x H] f32, norm_weight:
- * device [H] (the layer's post_norm).  The normalisation is a parallel sum of
- * squares, within the output tolerance of the reference's serial one. */
+ * device [H] (the layer's post_norm).  n is the CPU path's bit for bit (its
+ * serial fp32 sum of squares), so the router sees the reference's input. */
 int coli_cuda_moe_block(ColiCuda *ctx, ColiMoeLayer *layer, float *x,
                         const float *norm_weight, float eps, int tokens);
+/* coli_cuda_moe_block with its intermediates (each optional, device):
+ * hidden [tokens x H] receives n; route_idx / route_weight [tokens x K] the
+ * routes chosen on n, as coli_cuda_moe_forward returns them. */
+int coli_cuda_moe_block_ex(ColiCuda *ctx, ColiMoeLayer *layer, float *x,
+                           const float *norm_weight, float eps, int tokens,
+                           float *hidden, int *route_idx, float *route_weight);
 
 /* Router only: idx / weight [tokens x K] (device). */
 int coli_cuda_moe_route(ColiCuda *ctx, ColiMoeLayer *layer, const float *x,

@@ -316,6 +316,31 @@ class Reference:
         self.lib.ref_rmsnorm_zero(ptr(out, f32p), ptr(x, f32p), ptr(w, f32p), x.size, eps)
         return out
 
+    def load_qmat(self, snapshot_dir: str, base: str, rows: int, cols: int, use_q3: bool = False,
+                  use_q2: bool = False):
+        """The reference's load_qmat_mode (c/qwen.c:2224-2257) over a snapshot
+        directory indexed by st_init (c/st.h:211): ({fmt, gs, rb, ng, drb},
+        payload, scales).  payload: rows x rb bytes (uint8) for fmt 1-4, rows x
+        cols floats for fmt 0; scales: rows x ng floats (rows for fmt 1)."""
+        L = self.lib
+        L.ref_load_qmat.restype = C.c_int
+        L.ref_load_qmat.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, i32p,
+                                    C.c_void_p, C.c_size_t, f32p, C.c_size_t]
+        info = np.zeros(5, np.int32)
+        cap = rows * max(cols, 64) * 4
+        payload = np.zeros(cap, np.uint8)
+        scales = np.zeros(rows * (cols + 7), np.float32)
+        rc = L.ref_load_qmat(snapshot_dir.encode(), base.encode(), rows, cols, int(use_q3), int(use_q2),
+                             ptr(info, i32p), payload.ctypes.data, payload.size, ptr(scales, f32p), scales.size)
+        if rc != 0:
+            raise RuntimeError(f"ref_load_qmat {base}: capacity")
+        fmt, gs, rb, ng, drb = (int(v) for v in info)
+        d = dict(fmt=fmt, gs=gs, rb=rb, ng=ng, drb=drb)
+        if fmt == 0:
+            return d, payload[:rows * cols * 4].view(np.float32).reshape(rows, cols), None
+        nsc = rows if fmt == 1 else rows * ng
+        return d, payload[:rows * rb].reshape(rows, rb), scales[:nsc].copy()
+
     def layer(self, host_layer: "HostLayer"):
         return RefLayer(self, host_layer)
 

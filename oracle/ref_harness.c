@@ -193,6 +193,54 @@ int ref_route_gather_all(const int *idx, const float *weight, int T, int K, int 
     return n;
 }
 
+/* The reference's own reading of one matrix from a snapshot directory:
+ * st_init (c/st.h:211-297) indexes the shard files, load_qmat_mode
+ * (c/qwen.c:2224-2257) finds the tensor (find_qmat_named 2198-2214: the
+ * EXPERT_Q3 / EXPERT_Q2 sidecars of routed experts, set here from use_q3 /
+ * use_q2) and detects its format.  info = {fmt, gs, rb, ng, drb}.  payload
+ * receives rows*rb code bytes (fmt 1-4) or rows*cols floats (fmt 0), scales
+ * rows*ng floats, when the capacities (bytes, floats) allow; returns -1 when
+ * they do not.  The reference exits the process on a malformed file: this is
+ * for well-formed snapshots only. */
+int ref_load_qmat(const char *dir, const char *base, int rows, int cols, int use_q3, int use_q2, int info[5],
+                  void *payload, size_t payload_cap, float *scales, size_t scales_cap) {
+    Model *m = (Model *)calloc(1, sizeof(Model));
+    if (!m) return -1;
+    if (use_q3) setenv("EXPERT_Q3", "1", 1); else unsetenv("EXPERT_Q3");
+    if (use_q2) setenv("EXPERT_Q2", "1", 1); else unsetenv("EXPERT_Q2");
+    st_init(&m->S, dir);
+    QMat q = load_qmat_mode(m, base, rows, cols, 0);
+    info[0] = q.fmt;
+    info[1] = q.gs;
+    info[2] = q.rb;
+    info[3] = q.ng;
+    info[4] = q.drb;
+    int rc = 0;
+    if (q.fmt == 0) {
+        if ((size_t)rows * cols * 4 > payload_cap) rc = -1;
+        else memcpy(payload, q.f, (size_t)rows * cols * 4);
+    } else {
+        const size_t nb = (size_t)rows * q.rb, ns = (size_t)rows * (q.fmt == 1 ? 1 : q.ng);
+        if (nb > payload_cap || ns > scales_cap) rc = -1;
+        else {
+            memcpy(payload, q.fmt == 1 ? (const void *)q.q8 : (const void *)q.q4, nb);
+            memcpy(scales, q.s, ns * 4);
+        }
+    }
+    free(q.f);
+    free(q.q8);
+    free(q.q4);
+    free(q.s);
+    for (int i = 0; i < m->S.nfd; i++) close(m->S.fds[i]);
+    for (int i = 0; i < m->S.n; i++) free(m->S.t[i].name);
+    free(m->S.t);
+    free(m->S.hidx);
+    free(m);
+    unsetenv("EXPERT_Q3");
+    unsetenv("EXPERT_Q2");
+    return rc;
+}
+
 int ref_omp_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();
@@ -221,6 +269,56 @@ int ref_sw_forward(void *h, const float *x, int T, float *out, int *idx) {
     RefLayer *r = (RefLayer *)h;
     return sw_moe_try(&r->m, &r->l, x, T, out, idx);
 }
+
+/* sw_moe_try_device on activations the engine holds in device memory (the
+ * resident decode loop, c/qwen.c:4404-4522, in place of
+ * cuda_resident_moe_try 3825-3954): x goes to a device buffer of the
+ * reference's context, the step runs device to device, out comes back.
+ * Returns 1 when the device step ran, 0 when the caller would run its CPU
+ * path, -1 on a harness allocation or copy failure. */
+int ref_sw_forward_device(void *h, const float *x, int T, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    const size_t bytes = (size_t)T * r->m.c.hidden * sizeof(float);
+    void *dx = NULL, *dy = NULL;
+    int used = -1;
+    pthread_mutex_lock(&cuda_rt.lock);
+    int ok = !coli_cuda_malloc(cuda_rt.ctx, &dx, bytes) && !coli_cuda_malloc(cuda_rt.ctx, &dy, bytes) &&
+             !coli_cuda_upload(cuda_rt.ctx, dx, x, bytes) && !coli_cuda_sync(cuda_rt.ctx);
+    pthread_mutex_unlock(&cuda_rt.lock);
+    if (ok) {
+        used = sw_moe_try_device(&r->m, &r->l, (float *)dy, (const float *)dx, T);
+        pthread_mutex_lock(&cuda_rt.lock);
+        if (used == 1 && (coli_cuda_download(cuda_rt.ctx, out, dy, bytes) || coli_cuda_sync(cuda_rt.ctx))) used = -1;
+        pthread_mutex_unlock(&cuda_rt.lock);
+    }
+    pthread_mutex_lock(&cuda_rt.lock);
+    if (dx) coli_cuda_free(cuda_rt.ctx, dx);
+    if (dy) coli_cuda_free(cuda_rt.ctx, dy);
+    pthread_mutex_unlock(&cuda_rt.lock);
+    return used;
+}
+
+/* moe_forward (c/qwen.c:3717) and moe_prefill_grouped (4141) with the hook
+ * the integration patch puts first in each: the bridge's device step, and the
+ * reference's own body when the bridge declines (layer not registered, or the
+ * bridge switched off after a device error).  Returns whether the device step
+ * produced out. */
+int ref_hooked_moe_forward(void *h, const float *x, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    if (sw_moe_try(&r->m, &r->l, x, 1, out, NULL)) return 1;
+    moe_forward(&r->m, &r->l, x, out);
+    return 0;
+}
+
+int ref_hooked_moe_prefill(void *h, const float *x, int T, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    if (sw_moe_try(&r->m, &r->l, x, T, out, NULL)) return 1;
+    moe_prefill_grouped(&r->m, &r->l, x, T, out, 0);
+    return 0;
+}
+
+/* whether the bridge has switched itself off after a device error */
+int ref_sw_disabled(void) { return sw_moe.disabled; }
 
 /* The reference's own GPU glue (c/qwen.c:462-1474, 3741-3809) driving
  * whatever library provides the coli_cuda_* symbols it was linked against.

@@ -129,9 +129,10 @@ class Container:
     def tensors(self) -> int:
         return self.lib.coli_cuda_container_tensors(self.h)
 
-    def moe_shape(self, layer: int, topk: int = 0, use_q3: bool = False) -> ColiMoeShape:
+    def moe_shape(self, layer: int, topk: int = 0, sidecar: int = 0) -> ColiMoeShape:
+        """sidecar: 0 main payload, 1 (or True) the .q3 sidecar, 2 the .q2 sidecar."""
         s = ColiMoeShape(0, 0, topk, 0, 0, 0, 0)
-        if self.lib.coli_cuda_container_moe_shape(self.h, layer, int(use_q3), C.byref(s)) != 0:
+        if self.lib.coli_cuda_container_moe_shape(self.h, layer, int(sidecar), C.byref(s)) != 0:
             raise HipError(f"coli_cuda_container_moe_shape: {self.lib.coli_cuda_last_error().decode()}")
         return s
 
@@ -151,11 +152,12 @@ class MoeLayer:
     """An HBM-resident MoE layer (coli_cuda_moe_layer_*)."""
 
     @classmethod
-    def load(cls, be: Backend, container: Container, layer: int, topk: int, use_q3: bool = False) -> "MoeLayer":
-        """The layer `layer` of a converted snapshot (coli_cuda_moe_layer_load)."""
-        shape = container.moe_shape(layer, topk, use_q3)
+    def load(cls, be: Backend, container: Container, layer: int, topk: int, sidecar: int = 0) -> "MoeLayer":
+        """The layer `layer` of a converted snapshot (coli_cuda_moe_layer_load);
+        sidecar as in Container.moe_shape."""
+        shape = container.moe_shape(layer, topk, sidecar)
         h = C.c_void_p()
-        be.check(be.lib.coli_cuda_moe_layer_load(be.ctx, container.h, layer, topk, int(use_q3), C.byref(h)),
+        be.check(be.lib.coli_cuda_moe_layer_load(be.ctx, container.h, layer, topk, int(sidecar), C.byref(h)),
                  "coli_cuda_moe_layer_load")
         self = cls.__new__(cls)
         self.be, self.shape, self.h = be, shape, h

@@ -27,23 +27,35 @@ using namespace sw;
 // ---------------------------------------------------------------------------
 // elementwise and small kernels (backend_cuda.h:46-59)
 // ---------------------------------------------------------------------------
-__global__ static void k_rmsnorm_zero(float *y, const float *x, const float *w, int n, float eps) {
+// rmsnorm_zero (c/qwen.c:1780-1784) with the CPU path's arithmetic bit for
+// bit: ms = rn(ms + rn(x_i*x_i)) in element order (the serial chain the
+// reference's flags compile), r = 1/sqrtf(ms/n + eps) (correctly rounded
+// division and square root), y_i = rn(rn(x_i*r)*rn(1+w_i)).  One block per
+// row: the block writes a chunk of squares to LDS, one lane adds them in
+// order, the next chunk follows.
+constexpr int kNormChunk = 4096;
+__global__ __launch_bounds__(256) static void k_rmsnorm_zero(float *y, const float *x, const float *w, int n,
+                                                             float eps) {
+  __shared__ float sq[kNormChunk];
+  __shared__ float s_r;
   const float *xs = x + (size_t)blockIdx.x * n;
   float *ys = y + (size_t)blockIdx.x * n;
-  __shared__ float part[16];
-  float s = 0.0f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) s += xs[i] * xs[i];
-  s = wave_sum(s);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += part[i];
-    part[0] = 1.0f / sqrtf(t / (float)n + eps);
+  float ms = 0.0f;
+  for (int c0 = 0; c0 < n; c0 += kNormChunk) {
+    const int m = n - c0 < kNormChunk ? n - c0 : kNormChunk;
+    for (int i = threadIdx.x; i < m; i += blockDim.x) sq[i] = __fmul_rn(xs[c0 + i], xs[c0 + i]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int m64 = m / 64 * 64;
+      ms = serial_sum_lds(sq, m64, ms);
+      for (int i = m64; i < m; i++) ms = __fadd_rn(ms, sq[i]);
+    }
+    __syncthreads();
   }
+  if (threadIdx.x == 0) s_r = 1.0f / sqrtf(ms / (float)n + eps);
   __syncthreads();
-  float inv = part[0];
-  for (int i = threadIdx.x; i < n; i += blockDim.x) ys[i] = xs[i] * inv * (1.0f + w[i]);
+  const float r = s_r;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ys[i] = __fmul_rn(__fmul_rn(xs[i], r), 1.0f + w[i]);
 }
 
 extern "C" int coli_cuda_rmsnorm_zero(ColiCuda *ctx, float *y, const float *x, const float *w, int n,

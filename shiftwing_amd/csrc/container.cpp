@@ -8,13 +8,15 @@
 //   layers.L.mlp.gate.weight                         router, float [E, H]
 //   layers.L.mlp.shared_expert_gate.weight           gate row, float [1, H]
 //   layers.L.mlp.shared_expert.{gate,up,down}_proj.weight
-//   layers.L.mlp.experts.e.{gate,up,down}_proj.weight[.q3]
+//   layers.L.mlp.experts.e.{gate,up,down}_proj.weight[.q3|.q2]
 // A quantised matrix is a U8/I8 payload [rows, row bytes] with an f32 `.qs`
 // [rows, groups] ([rows] for int8) and an optional U8 `.qtype` tag (8, 4, 3,
 // 2); without a tag the sizes decide, as load_qmat_mode does.  The `.q3`
 // sidecar (c/tools/requantize_expert_q2.py) holds int3 experts with their own
 // `.qs` and `.qtype`; it is taken when the caller asks for it (the reference's
-// EXPERT_Q3=1).
+// EXPERT_Q3=1, which requires it).  The `.q2` sidecar (EXPERT_Q2=1) holds int2
+// experts; an expert without one is read from its main payload, as
+// find_qmat_named does (c/qwen.c:2198-2214).
 //
 // Loading reads tensors with pread into pinned host memory, copies them to a
 // device staging buffer and hands them to coli_cuda_moe_layer_set_*, which
@@ -299,13 +301,16 @@ struct QInfo {
   int rows = 0, cols = 0, rb = 0, ng = 0, gs = 0;
 };
 
-int qinfo(const ColiContainer *c, const std::string &base, int rows, int cols, bool q3, QInfo &qi) {
+// sidecar: 0 the main payload, 1 the `.q3` sidecar (required), 2 the `.q2`
+// sidecar where there is one, else the main payload
+int qinfo(const ColiContainer *c, const std::string &base, int rows, int cols, int sidecar, QInfo &qi) {
   std::string name;
   qi = QInfo();
   qi.rows = rows;
   qi.cols = cols;
-  qi.q = find(c, q3 ? base + ".q3" : base, &name);
-  if (!qi.q) return fail_arg("container: missing tensor %s%s", base.c_str(), q3 ? ".q3" : "");
+  qi.q = find(c, sidecar == 1 ? base + ".q3" : sidecar == 2 ? base + ".q2" : base, &name);
+  if (!qi.q && sidecar == 2) qi.q = find(c, base, &name);
+  if (!qi.q) return fail_arg("container: missing tensor %s%s", base.c_str(), sidecar == 1 ? ".q3" : "");
   const Tensor &t = *qi.q;
   if (t.dtype != kU8) {
     if (t.dtype == kI64 || t.numel != (int64_t)rows * cols)
@@ -330,6 +335,10 @@ int qinfo(const ColiContainer *c, const std::string &base, int rows, int cols, b
   if (qtype == 8 || (qtype == 0 && nb == (int64_t)rows * cols && ns == rows)) {
     qi.fmt = 1;
     if (qi.rb != cols) return fail_arg("container: %s: int8 rows of %d bytes, expected %d", name.c_str(), qi.rb, cols);
+    // one scale per row (the reference reads only s[row] of an int8 matrix,
+    // c/qwen.c:1765-1768); more would not fit the layer's per-row slots
+    if (qi.ng != 1)
+      return fail_arg("container: %s: int8 matrix with %d scales per row, expected 1", name.c_str(), qi.ng);
   } else if (qtype == 2) {
     qi.fmt = 2;
     qi.gs = qi.ng ? qi.rb * 4 / qi.ng : 0;
@@ -374,19 +383,20 @@ std::string expert_name(int layer, int e, const char *proj) {
 }
 
 // The layer's shape as stored (topk is not part of the container).
-int layer_shape(const ColiContainer *c, int layer, int use_q3, ColiMoeShape &s) {
+int layer_shape(const ColiContainer *c, int layer, int sidecar, ColiMoeShape &s) {
+  if (sidecar < 0 || sidecar > 2) return fail_arg("container: sidecar %d (0 main, 1 .q3, 2 .q2)", sidecar);
   const Tensor *r = find(c, layer_name(layer, "mlp.gate.weight"));
   if (!r) return fail_arg("container: layer %d has no router (mlp.gate.weight)", layer);
   if (r->shape.size() != 2 || r->dtype == kU8) return fail_arg("container: layer %d: router is not a float [E, H] matrix", layer);
   const int E = (int)r->shape[0], H = (int)r->shape[1];
   const std::string sgn = layer_name(layer, "mlp.shared_expert.gate_proj.weight");
-  const std::string egn = expert_name(layer, 0, "gate_proj") + (use_q3 ? ".q3" : "");
+  const std::string egn = expert_name(layer, 0, "gate_proj") + (sidecar == 1 ? ".q3" : "");
   const Tensor *sg = find(c, sgn), *eg = find(c, egn);
   if (!sg || sg->shape.empty()) return fail_arg("container: missing tensor %s", sgn.c_str());
   if (!eg || eg->shape.empty()) return fail_arg("container: missing tensor %s", egn.c_str());
   const int Ish = (int)sg->shape[0], I = (int)eg->shape[0];
   QInfo gq;
-  if (qinfo(c, expert_name(layer, 0, "gate_proj"), I, H, use_q3 != 0, gq)) return -1;
+  if (qinfo(c, expert_name(layer, 0, "gate_proj"), I, H, sidecar, gq)) return -1;
   s.hidden = H;
   s.experts = E;
   s.intermediate = I;
@@ -444,32 +454,35 @@ extern "C" void coli_cuda_container_close(ColiContainer *c) {
 
 extern "C" int coli_cuda_container_tensors(const ColiContainer *c) { return c ? (int)c->t.size() : 0; }
 
-extern "C" int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int use_q3, ColiMoeShape *shape) {
+extern "C" int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int sidecar, ColiMoeShape *shape) {
   if (!c || !shape || layer < 0) return fail_arg("coli_cuda_container_moe_shape: invalid argument");
   ColiMoeShape s = *shape;
-  if (layer_shape(c, layer, use_q3, s)) return -1;
+  if (layer_shape(c, layer, sidecar, s)) return -1;
   *shape = s;
   return 0;
 }
 
-extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer, int topk, int use_q3,
+extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer, int topk, int sidecar,
                                         ColiMoeLayer **out) {
   if (!ctx || !c || !out || layer < 0 || topk <= 0) return fail_arg("coli_cuda_moe_layer_load: invalid argument");
   *out = nullptr;
   ColiMoeShape s;
   memset(&s, 0, sizeof(s));
-  if (layer_shape(c, layer, use_q3, s)) return -1;
+  if (layer_shape(c, layer, sidecar, s)) return -1;
   s.topk = topk;
   const int H = s.hidden, E = s.experts, I = s.intermediate, Ish = s.shared_intermediate, fmt = s.expert_format;
   if (fmt != 3 && fmt != 4)
     return fail_arg("coli_cuda_moe_layer_load: layer %d: routed experts are format %d; the device layer takes "
-                    "int4 or int3 (use_q3 for the .q3 sidecar)", layer, fmt);
+                    "int4 or int3 (sidecar 1 for the .q3 sidecar)", layer, fmt);
+  if (s.group_size != 128)
+    return fail_arg("coli_cuda_moe_layer_load: layer %d: routed experts in groups of %d; the device layer takes "
+                    "groups of 128", layer, s.group_size);
   // the shared expert: int8 rows; router and gate row: float
   QInfo sgq, suq, sdq, gate_row;
-  if (qinfo(c, layer_name(layer, "mlp.shared_expert.gate_proj.weight"), Ish, H, false, sgq) ||
-      qinfo(c, layer_name(layer, "mlp.shared_expert.up_proj.weight"), Ish, H, false, suq) ||
-      qinfo(c, layer_name(layer, "mlp.shared_expert.down_proj.weight"), H, Ish, false, sdq) ||
-      qinfo(c, layer_name(layer, "mlp.shared_expert_gate.weight"), 1, H, false, gate_row))
+  if (qinfo(c, layer_name(layer, "mlp.shared_expert.gate_proj.weight"), Ish, H, 0, sgq) ||
+      qinfo(c, layer_name(layer, "mlp.shared_expert.up_proj.weight"), Ish, H, 0, suq) ||
+      qinfo(c, layer_name(layer, "mlp.shared_expert.down_proj.weight"), H, Ish, 0, sdq) ||
+      qinfo(c, layer_name(layer, "mlp.shared_expert_gate.weight"), 1, H, 0, gate_row))
     return -1;
   if (sgq.fmt != 1 || suq.fmt != 1 || sdq.fmt != 1 || gate_row.fmt != 0)
     return fail_arg("coli_cuda_moe_layer_load: layer %d: the shared expert must be int8 and its gate row float", layer);
@@ -479,7 +492,7 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
   for (int e = 0; e < E; e++)
     for (int k = 0; k < 3; k++) {
       QInfo &q = xq[(size_t)e * 3 + k];
-      if (qinfo(c, expert_name(layer, e, proj[k]), k == 2 ? H : I, k == 2 ? I : H, use_q3 != 0, q)) return -1;
+      if (qinfo(c, expert_name(layer, e, proj[k]), k == 2 ? H : I, k == 2 ? I : H, sidecar, q)) return -1;
       const QInfo &ref = xq[k];
       if (q.fmt != fmt || q.gs != s.group_size || q.rb != ref.rb || q.ng != ref.ng)
         return fail_arg("coli_cuda_moe_layer_load: layer %d expert %d %s: format %d / group %d differs from expert 0",

@@ -2998,17 +2998,23 @@ __global__ static void k_residual_add(float *x, const float *y, size_t n) {
   if (i < n) x[i] += y[i];
 }
 
-extern "C" int coli_cuda_moe_block(ColiCuda *ctx, ColiMoeLayer *L, float *x, const float *norm_weight, float eps,
-                                   int tokens) {
+extern "C" int coli_cuda_moe_block_ex(ColiCuda *ctx, ColiMoeLayer *L, float *x, const float *norm_weight,
+                                      float eps, int tokens, float *hidden, int *route_idx, float *route_weight) {
   if (!ctx || !L || !x || !norm_weight || tokens <= 0) return fail_arg("coli_cuda_moe_block: invalid argument");
   const size_t H = (size_t)L->sh.hidden, n = (size_t)tokens * H;
   if (ensure_scratch(ctx, kScrBlock, 2 * n * sizeof(float), "MoE block scratch")) return -1;
-  float *xn = (float *)ctx->scratch[kScrBlock], *y = xn + n;
+  float *xn = hidden ? hidden : (float *)ctx->scratch[kScrBlock], *y = (float *)ctx->scratch[kScrBlock] + n;
+  // the serial sum of squares of the CPU path, so the router sees its n bit for bit
   if (coli_cuda_rmsnorm_zero_batch(ctx, xn, x, norm_weight, tokens, (int)H, eps) ||
-      coli_cuda_moe_forward(ctx, L, y, xn, tokens, nullptr, nullptr))
+      coli_cuda_moe_forward(ctx, L, y, xn, tokens, route_idx, route_weight))
     return -1;
   k_residual_add<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(x, y, n);
   return launch_status("coli_cuda_moe_block");
+}
+
+extern "C" int coli_cuda_moe_block(ColiCuda *ctx, ColiMoeLayer *L, float *x, const float *norm_weight, float eps,
+                                   int tokens) {
+  return coli_cuda_moe_block_ex(ctx, L, x, norm_weight, eps, tokens, nullptr, nullptr, nullptr);
 }
 
 __global__ static void k_synth_x(float *x, int rows, int cols, uint64_t seed, uint32_t layer, int step0) {

@@ -229,8 +229,8 @@ __device__ __forceinline__ double readlane_d63(double v) {
   return __hiloint2double(hi, lo);
 }
 
-// s = rn(s + p[i]) for i < m in order (the reference's serial chain over
-// precomputed products), by one lane, m % 64 == 0: the LDS reads of the next
+// s = rn(s + p[i]) for i < m in order, from s (the reference's serial chain
+// over precomputed products), by one lane, m % 64 == 0: the LDS reads of the next
 // 32 terms are issued before the adds of the current 32, so the chain runs at
 // the rate of its dependent adds.
 __device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
@@ -242,8 +242,7 @@ __device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
     s = __fadd_rn(s, v[k].w);
   }
 }
-__device__ __forceinline__ float serial_sum_lds(const float *p, int m) {
-  float s = 0.0f;
+__device__ __forceinline__ float serial_sum_lds(const float *p, int m, float s = 0.0f) {
   if (m <= 0) return s;
   float4 a[8], b[8];
 #pragma unroll

@@ -185,3 +185,105 @@ def test_container_survives_corrupt_files(tmp_path, layers):
         lib.coli_cuda_container_close(c)
         os.remove(d / "m.safetensors")
     assert failed > 0 and opened > 0, (failed, opened)
+
+
+def _reference():
+    from oracle.pyoracle import Reference
+    try:
+        return Reference()
+    except FileNotFoundError:
+        pytest.skip("oracle/_ref not built (the reference tree is absent)")
+
+
+def _int2_tensors(rng, layer, E, H, I, prefix="", suffix="", gs=128):
+    """int2 routed experts (.qtype 2): rows of cols/4 bytes, 4 codes per byte,
+    value 2*code-3 (c/qwen.c:1717-1724, 2244-2246), one scale per group."""
+    t = {}
+    for e in range(E):
+        for nm, rows, cols in (("gate", I, H), ("up", I, H), ("down", H, I)):
+            base = f"{prefix}layers.{layer}.mlp.experts.{e}.{nm}_proj.weight{suffix}"
+            t[base] = rng.integers(0, 256, (rows, cols // 4), dtype=np.uint8)
+            t[base + ".qs"] = np.abs(rng.standard_normal((rows, cols // gs))).astype(np.float32) * 0.01
+            t[base + ".qtype"] = np.array([2], np.uint8)
+    return t
+
+
+def test_container_matches_the_reference_loader(tmp_path, layers, oracle):
+    """One snapshot directory read two ways: by the reference's own st.h index
+    and load_qmat_mode (c/st.h:211-297, c/qwen.c:2198-2257, compiled in place
+    in oracle/_ref) and by coli_cuda_container_moe_shape.  Formats, group sizes,
+    row bytes and group counts agree, and the reference reads back exactly the
+    payload bytes and scales of the host layer that coli_cuda_moe_layer_load
+    is checked against on the GPU (test_gpu_container.py), for the main int4
+    payload, the .q3 sidecar, the int8 shared expert and the float router."""
+    ref = _reference()
+    hl4, hl3 = layers
+    H, E, K, I, Ish = SHAPE
+    pre = "model.language_model."
+    st_writer.write_split(str(tmp_path), st_writer.moe_layer_tensors(hl4, 3, pre, q3=hl3), parts=3)
+    lib = _lib()
+    rc, c = _open(lib, str(tmp_path))
+    assert rc == 0, lib.coli_cuda_last_error()
+    try:
+        for side, hl in ((0, hl4), (1, hl3)):
+            rc, s = _shape(lib, c, 3, side)
+            assert rc == 0, lib.coli_cuda_last_error()
+            for e in (0, 5, E - 1):
+                for nm, rows, cols, q, sc in (("gate", I, H, hl.gq, hl.gsc), ("up", I, H, hl.uq, hl.usc),
+                                              ("down", H, I, hl.dq, hl.dsc)):
+                    info, pay, scl = ref.load_qmat(str(tmp_path), f"layers.3.mlp.experts.{e}.{nm}_proj.weight",
+                                                   rows, cols, use_q3=side == 1)
+                    assert info["fmt"] == s.expert_format and info["gs"] == s.group_size, (side, e, nm, info)
+                    assert info["rb"] == q.shape[2] and info["ng"] == sc.shape[2], (side, e, nm, info)
+                    assert np.array_equal(pay, q[e]), (side, e, nm)
+                    assert np.array_equal(scl.view(np.uint32), sc[e].reshape(-1).view(np.uint32)), (side, e, nm)
+        for nm, m, rows, cols in (("gate", hl4.shared_gate, Ish, H), ("up", hl4.shared_up, Ish, H),
+                                  ("down", hl4.shared_down, H, Ish)):
+            info, pay, scl = ref.load_qmat(str(tmp_path), f"layers.3.mlp.shared_expert.{nm}_proj.weight", rows, cols)
+            assert info["fmt"] == 1 and info["rb"] == cols, info
+            assert np.array_equal(pay.view(np.int8), np.asarray(m.q).reshape(rows, cols).view(np.int8))
+            assert np.array_equal(scl, np.asarray(m.s, np.float32))
+        info, pay, _ = ref.load_qmat(str(tmp_path), "layers.3.mlp.gate.weight", E, H)
+        assert info["fmt"] == 0 and np.array_equal(pay, hl4.router_w)
+        assert (s.hidden, s.experts, s.intermediate, s.shared_intermediate) == (H, E, I, Ish)
+    finally:
+        lib.coli_cuda_container_close(c)
+
+
+def test_container_int2_and_group_sizes_as_the_reference_reads_them(tmp_path, oracle):
+    """Formats the reference's CPU path reads and the device layer does not
+    take are still classified as the reference classifies them, so that
+    coli_cuda_moe_layer_load can refuse them by name (its GPU test checks the
+    refusal): int2 experts from .qtype 2 main payloads and from .q2 sidecars
+    (EXPERT_Q2=1, which falls back to the main payload for an expert without
+    one, c/qwen.c:2207-2214), and int4 experts in groups of 64."""
+    ref = _reference()
+    H, E, K, I, Ish = SHAPE
+    rng = np.random.default_rng(2)
+    lib = _lib()
+    hl = oracle.host_layer(6, 1, H, E, K, I, Ish, 4)
+    # int2 main payloads
+    t = st_writer.moe_layer_tensors(hl, 1)
+    t.update(_int2_tensors(rng, 1, E, H, I))
+    st_writer.write_split(str(tmp_path / "q2main"), t, parts=2)
+    # int4 main payloads with .q2 sidecars for every expert but the last
+    t = st_writer.moe_layer_tensors(hl, 1)
+    side = _int2_tensors(rng, 1, E, H, I, suffix=".q2")
+    t.update({k: v for k, v in side.items() if f".experts.{E - 1}." not in k})
+    st_writer.write_split(str(tmp_path / "q2side"), t, parts=2)
+    # int4 in groups of 64
+    hl64 = oracle.host_layer(6, 1, H, E, K, I, Ish, 4, gs=64)
+    st_writer.write_split(str(tmp_path / "g64"), st_writer.moe_layer_tensors(hl64, 1), parts=1)
+    cases = [("q2main", 0, 0, 2, 128), ("q2side", 2, 1, 2, 128), ("q2side", 0, 0, 4, 128), ("g64", 0, 0, 4, 64)]
+    for d, sidecar, use_q2, fmt, gs in cases:
+        rc, c = _open(lib, str(tmp_path / d))
+        assert rc == 0, lib.coli_cuda_last_error()
+        rc, s = _shape(lib, c, 1, sidecar)
+        assert rc == 0, lib.coli_cuda_last_error()
+        lib.coli_cuda_container_close(c)
+        assert (s.expert_format, s.group_size) == (fmt, gs), (d, sidecar)
+        for e in (0, E - 1):
+            info, _, _ = ref.load_qmat(str(tmp_path / d), f"layers.1.mlp.experts.{e}.gate_proj.weight", I, H,
+                                       use_q2=bool(use_q2))
+            want = 4 if (d == "q2side" and use_q2 and e == E - 1) else fmt
+            assert (info["fmt"], info["gs"]) == (want, gs), (d, sidecar, e, info)

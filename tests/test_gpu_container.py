@@ -66,3 +66,49 @@ def test_container_bf16_router(be, oracle, tmp_path):
     assert np.array_equal(idx, tr["idx"])
     assert_close_rms(y, want, 1e-3, "container bf16 router")
     Lc.close()
+
+
+def test_container_load_refusals(be, oracle, tmp_path):
+    """Layers the device layer does not take return -1 with a message from
+    coli_cuda_moe_layer_load, and nothing is created: int2 experts (.qtype 2
+    payloads, .q2 sidecars), int4 experts in groups of 64 (both read by the
+    reference's CPU path, c/qwen.c:2244-2254), and a shared expert tagged int8
+    with two scales per row (more than the one per row an int8 matrix uses,
+    c/qwen.c:1765-1768)."""
+    from test_container_cpu import _int2_tensors
+    H, E, K, I, Ish = SHAPE
+    rng = np.random.default_rng(3)
+    hl = oracle.host_layer(6, 1, H, E, K, I, Ish, 4)
+    t = st_writer.moe_layer_tensors(hl, 1)
+    t.update(_int2_tensors(rng, 1, E, H, I))
+    st_writer.write_split(str(tmp_path / "q2main"), t, parts=2)
+    t = st_writer.moe_layer_tensors(hl, 1)
+    t.update(_int2_tensors(rng, 1, E, H, I, suffix=".q2"))
+    st_writer.write_split(str(tmp_path / "q2side"), t, parts=2)
+    hl64 = oracle.host_layer(6, 1, H, E, K, I, Ish, 4, gs=64)
+    st_writer.write_split(str(tmp_path / "g64"), st_writer.moe_layer_tensors(hl64, 1), parts=1)
+    t = st_writer.moe_layer_tensors(hl, 1)
+    t["layers.1.mlp.shared_expert.down_proj.weight.qs"] = np.repeat(
+        np.asarray(hl.shared_down.s, np.float32)[:, None], 2, axis=1)
+    st_writer.write_split(str(tmp_path / "i8two"), t, parts=1)
+    from shiftwing_amd import Container
+    for d, sidecar, msg in (("q2main", 0, "format 2"), ("q2side", 2, "format 2"), ("g64", 0, "groups of 64"),
+                            ("i8two", 0, "2 scales per row")):
+        print(f"[container refusal] {d}", flush=True)
+        c = Container(str(tmp_path / d))
+        try:
+            h = C.c_void_p()
+            rc = be.lib.coli_cuda_moe_layer_load(be.ctx, c.h, 1, K, sidecar, C.byref(h))
+            err = be.lib.coli_cuda_last_error().decode()
+            assert rc == -1 and not h.value, (d, rc)
+            assert msg in err, (d, err)
+        finally:
+            c.close()
+    # the same directory's main int4 payloads still load (the .q2 sidecars unused)
+    Lc = _load(be, str(tmp_path / "q2side"), 1, K, 0, H)
+    x = oracle.synth_x(6, 1, 0, H)
+    want, tr = oracle.moe_forward(hl, x, trace=True)
+    y, idx, _ = Lc.forward_host(x)
+    assert np.array_equal(idx[0], tr["idx"])
+    assert_close_rms(y[0], want, 1e-3, "q2side main payload")
+    Lc.close()

@@ -66,6 +66,13 @@ class Glue:
         lib.ref_sw_register.argtypes = [C.c_void_p]
         lib.ref_sw_forward.restype = C.c_int
         lib.ref_sw_forward.argtypes = [C.c_void_p, f32p, C.c_int, f32p, C.POINTER(C.c_int)]
+        lib.ref_sw_forward_device.restype = C.c_int
+        lib.ref_sw_forward_device.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        lib.ref_hooked_moe_forward.restype = C.c_int
+        lib.ref_hooked_moe_forward.argtypes = [C.c_void_p, f32p, f32p]
+        lib.ref_hooked_moe_prefill.restype = C.c_int
+        lib.ref_hooked_moe_prefill.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        lib.ref_sw_disabled.restype = C.c_int
         self.lib = lib
         self.f32p = f32p
 
@@ -218,5 +225,73 @@ def test_bridge_device_moe_step(glue, oracle, shape, seed):
                 want_idx = tr["idx"]
             assert np.array_equal(idx, want_idx), (T, idx, want_idx)
             assert_close_rms(got, want, 1e-3, f"bridge T={T}")
+    finally:
+        glue.lib.ref_layer_destroy(h)
+
+
+@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397)],
+                         ids=["s35_q4", "s397_q3"])
+def test_bridge_device_activations_and_hooks(glue, oracle, shape, seed):
+    """The bridge's two other ways in, on a registered reference MoeW layer:
+    sw_moe_try_device on activations in device memory (the resident decode
+    loop's replacement of cuda_resident_moe_try, c/qwen.c:3825-3954, 4404-4522)
+    for T = 1 and 4; and moe_forward / moe_prefill_grouped (c/qwen.c:3717, 4141)
+    with the integration patch's hook as their first statement, which must take
+    the device step.  Outputs within max-abs 1e-3 x RMS of the CPU path; the
+    bridge stays on."""
+    from oracle.pyoracle import ptr
+    H, E, K, I, Ish, fmt = shape
+    hl = oracle.host_layer(seed, 5, H, E, K, I, Ish, fmt)
+    h = glue.lib.ref_layer_create(C.byref(hl.st))
+    f32p = glue.f32p
+    try:
+        assert glue.lib.ref_sw_register(h) == 1
+        for T in (1, 4):
+            print(f"[bridge device] {shape[0]} T={T}", flush=True)
+            x = np.ascontiguousarray(np.stack([oracle.synth_x(seed, 5, 300 + t, H) for t in range(T)]))
+            out = np.zeros((T, H), np.float32)
+            assert glue.lib.ref_sw_forward_device(h, ptr(x, f32p), T, ptr(out, f32p)) == 1
+            want = oracle.moe_forward(hl, x[0])[None] if T == 1 else oracle.moe_prefill(hl, x)
+            assert_close_rms(out, want, 1e-3, f"sw_moe_try_device T={T}")
+            hooked = np.zeros((T, H), np.float32)
+            if T == 1:
+                used = glue.lib.ref_hooked_moe_forward(h, ptr(x[0], f32p), ptr(hooked[0], f32p))
+            else:
+                used = glue.lib.ref_hooked_moe_prefill(h, ptr(x, f32p), T, ptr(hooked, f32p))
+            assert used == 1, T
+            assert_close_rms(hooked, want, 1e-3, f"hooked T={T}")
+        assert glue.lib.ref_sw_disabled() == 0 and glue.counters()["failed"] == 0
+    finally:
+        glue.lib.ref_layer_destroy(h)
+
+
+def test_bridge_declines_layers_it_does_not_take(glue, oracle):
+    """A reference layer whose routed experts use groups of 64 (which the
+    reference's CPU path computes, c/qwen.c:1706-1716 with gs = 64) is not
+    registered: sw_moe_register returns 0, the hooked moe_forward and
+    moe_prefill_grouped run the reference's own body (bit for bit with the
+    compiled reference's CPU path), sw_moe_try_device declines, and the bridge
+    stays on for other layers."""
+    from oracle.pyoracle import ptr
+    H, E, K, I, Ish = 512, 16, 4, 256, 128
+    hl = oracle.host_layer(8, 2, H, E, K, I, Ish, 4, gs=64)
+    h = glue.lib.ref_layer_create(C.byref(hl.st))
+    f32p = glue.f32p
+    try:
+        assert glue.lib.ref_sw_register(h) == 0
+        x = np.ascontiguousarray(np.stack([oracle.synth_x(8, 2, t, H) for t in range(3)]))
+        one = np.zeros(H, np.float32)
+        assert glue.lib.ref_hooked_moe_forward(h, ptr(x[0], f32p), ptr(one, f32p)) == 0
+        many = np.zeros((3, H), np.float32)
+        assert glue.lib.ref_hooked_moe_prefill(h, ptr(x, f32p), 3, ptr(many, f32p)) == 0
+        assert glue.lib.ref_sw_forward_device(h, ptr(x, f32p), 3, ptr(many.copy(), f32p)) == 0
+        # the same library's unhooked reference functions, bit for bit
+        assert np.array_equal(one.view(np.uint32), glue.forward(h, x[0], H).view(np.uint32))
+        plain = np.zeros((3, H), np.float32)
+        glue.lib.ref_moe_prefill_grouped.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        glue.lib.ref_moe_prefill_grouped(h, ptr(x, f32p), 3, ptr(plain, f32p))
+        assert np.array_equal(many.view(np.uint32), plain.view(np.uint32))
+        assert_close_rms(many, oracle.moe_prefill(hl, x), 5e-3, "declined prefill against the CPU checker")
+        assert glue.lib.ref_sw_disabled() == 0
     finally:
         glue.lib.ref_layer_destroy(h)

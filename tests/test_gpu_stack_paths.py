@@ -222,28 +222,3 @@ def test_shared_expert_bitexact_every_path(be, oracle, shape, seed):
         be.set_decode_kernels(1)
         L.close()
         L2.close()
-
-
-@pytest.mark.parametrize("shape,T", [(S35, 1), (S35, 7), ((512, 32, 4, 256, 128, 3), 300)],
-                         ids=["s35_T1", "s35_T7", "small_T300"])
-def test_moe_block_on_the_residual_stream(be, oracle, shape, T):
-    """coli_cuda_moe_block: x += MoE(rmsnorm_zero(x, post_norm)) on the device
-    (c/qwen.c:4593-4596) against the CPU checker's rmsnorm_zero (bit-exact
-    with the compiled reference) and moe_forward / moe_prefill_grouped."""
-    import ctypes as C
-    from shiftwing_amd import MoeLayer
-    H, E, K, I, Ish, fmt = shape
-    hl = oracle.host_layer(44, 1, H, E, K, I, Ish, fmt)
-    L = MoeLayer(be, H, E, K, I, Ish, fmt)
-    L.synthesize(44, 1)
-    rng = np.random.default_rng(44)
-    x = (rng.standard_normal((T, H)) * 2.5).astype(np.float32)
-    w = (rng.standard_normal(H) * 0.1).astype(np.float32)
-    n = oracle.rmsnorm_zero(x, w, 1e-6)
-    moe = oracle.moe_forward(hl, n[0])[None] if T == 1 else oracle.moe_prefill(hl, n)
-    dx, dw = be.upload(x), be.upload(w)
-    be.check(be.lib.coli_cuda_moe_block(be.ctx, L.h, dx.p, dw.p, C.c_float(1e-6), T), "moe_block")
-    got = be.download(dx, (T, H), np.float32)
-    assert_close_rms(got.astype(np.float64) - x, moe, 1e-3, f"moe block T={T}")
-    assert np.max(np.abs(got - (x + moe))) <= 1e-3 * float(np.sqrt(np.mean(moe.astype(np.float64) ** 2))) + 1e-6
-    L.close()
