@@ -2,26 +2,32 @@
 // kernel (moe_forward, c/qwen.c:3717-3739, applied layer after layer).
 //
 // One workgroup of 512 threads per CU, all resident for the whole call.  Per
-// layer l, every workgroup runs four stages separated by grid barriers:
+// layer l, every workgroup runs four stages separated by grid exchanges:
 //
 //   R  router rows (fp64 logit + rigorous bound of the reference's serial fp32
 //      dot, c/qwen.c:1674) for the rows this workgroup owns (row r belongs to
 //      workgroup r % NB), one shared-expert gate/up IDOT task (exact int32
 //      dots, c/qwen.c:1696-1705, summed over k-slices with integer atomics),
-//      and the activation digits of x for the routed GEMV.  Each workgroup's
-//      shared sums go out first; its router records follow, tagged with the
-//      layer (no barrier: readers read the records until all carry the tag).
+//      the activation digits of x for the routed GEMV, and the thread's part
+//      of the shared gate's logit.  Each workgroup's shared sums go out first;
+//      its router records follow, tagged with the layer (no barrier: readers
+//      read the records until all carry the tag).
 //   S  every workgroup selects the top-k itself from the published records
 //      (router_topk, c/qwen.c:3421-3426): certified by the bounds, else by
 //      the exact fp32 chains of the ambiguous experts (computed by the rows'
 //      owners and exchanged through one more barrier), else by the reference's
-//      full computation on every expert's exact chain.
+//      full computation on every expert's exact chain.  Meanwhile wave 1
+//      computes this workgroup's Ish/NB values of the shared hidden vector
+//      (SwiGLU of the counted sums) and publishes them tagged, and waves 2..7
+//      copy the shared down rows of the workgroup's output tile into LDS.
 //   G  routed gate/up: units (route, 16 rows) over the grid; each unit's
 //      h = silu(g) * u (c/qwen.c:3419) is quantised into two int8 digits per
-//      16-value chunk and published as a 48-byte record.
+//      16-value chunk and published as a 48-byte record.  At the end, the
+//      whole shared hidden vector (copied in a few items earlier), its qrow_i8
+//      and the shared down dots of the workgroup's output rows.
 //   -- barrier "h".
-//   D  routed down + shared down + combine for 16 output rows per task, in
-//      moe_forward's order (fma over k in route order, then shared * gate).
+//   D  routed down + combine for 16 output rows per task, in moe_forward's
+//      order (fma over k in route order, then shared * gate).
 //   -- barrier "y" (strict decode order: layer l+1 starts after layer l).
 //
 // Weights that do not depend on the token (the next layer's router rows and
@@ -66,21 +72,10 @@ constexpr int kBars = 5;         // barriers per layer: lb, exact-1, exact-2, h,
 constexpr int kBarWords = 10 * kLine;  // release word, 8 group counters, top counter
 constexpr int kRecWords = 12;    // h chunk record: d1[16] d2[16] (8 words) | A B Q1 Q2
 constexpr int kGMax = 4;         // stage G: groups per wave and unit
-#ifndef SW_SHDOWN_LATE
-#define SW_SHDOWN_LATE 1
-#endif
 #ifndef SW_STACK_GRING
 #define SW_STACK_GRING 2
 #endif
 constexpr int kGRing = SW_STACK_GRING;  // stage G: ring slots per wave
-// Stage G: units of the last round that may be split in halves over pairs of
-// workgroups.  0 (no split) measured faster with the two-record ring: S397
-// 489 against 484 tok/s, S35 1,221 against 1,189 (the split's code and
-// exchange cost more than the uneven last round).
-#ifndef SW_SPLIT_UNITS
-#define SW_SPLIT_UNITS 0
-#endif
-constexpr int kSplitUnits = SW_SPLIT_UNITS;
 constexpr int kGHead = 2560;     // stage G: partial sums and digit staging before the rings
 enum { kBarLb = 0, kBarEx1, kBarEx2, kBarH, kBarY };
 
@@ -132,7 +127,7 @@ struct StackArgs {
   double *rec;          // [E+1][2] logit, bound
   float *ex;            // [E] exact logits
   unsigned *hd;         // [K][ngi*8][kRecWords]
-  unsigned long long *spl;  // [kSplitUnits][16][2] tagged half sums of split units
+  unsigned long long *hs;  // [Ish] the shared hidden vector: (layer tag << 32) | f32 bits
   unsigned long long *acc;  // [layer][parity][2*Ish] counted shared gate/up sums
   unsigned *bars;       // [layer][parity][kBars][kBarWords]
   size_t acc_stride;    // words per (layer, parity) acc block
@@ -460,34 +455,40 @@ __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, i
   return s;
 }
 
-// Stage D's part of the stage-local union: h records, partial sums, then the
-// LDS-loaded down tiles.  All of it is written only after a barrier that
-// every wave reaches once it is done with stage G's buffers.
-struct DLayout {
-  size_t hrec, part, dtile, end;
+// The stage-local union (bytes from its start), by the stages that use it:
+//   R      RStageLds at 0.
+//   S      SelLds, the records (logit, bound) [E], the keys [E] and the exact
+//          chains' products [kRSlots][H] from 0 (sel_end).  The shared down
+//          rows of this workgroup's output tile (gdsh) are copied in during
+//          stage S, past sel_end.
+//   G      partials and digit staging (kGHead), the rings of gate/up records;
+//          the shared hidden vector as tagged words (hsw, copied in near the
+//          end) and as values (hsh).
+//   D      (after the hidden barrier) the routed down records of the output
+//          tile (dtile, copied while the barrier completes), h records and
+//          partial sums over gdsh and what follows it.
+struct ULayout {
+  size_t ring, dtile, gdsh, hsh, hsw, hrec, part, end;
 };
-__host__ __device__ inline DLayout d_layout(int K, int ngi, int Ish, int fmt) {
-  DLayout d;
-  size_t o = 0;
-  auto take = [&o](size_t n) {
-    const size_t p = o;
-    o = (o + n + 15) & ~(size_t)15;
-    return p;
-  };
-  const size_t bpl = fmt == 4 ? 16 : 12;
-  d.hrec = take((size_t)K * ngi * 8 * kRecWords * 4);
-  d.part = take((size_t)kW * 16 * 4);
-  d.dtile = take((size_t)K * ngi * (64 * bpl + 64));
-  d.end = o;
-  return d;
-}
-
-// Stage G's LDS (partials, staging, rings of gate/up records, shared down
-// rows), from the union's start.  The shared hidden vector, built in stage S
-// and quantised once stage G has started, lies past it.
-__host__ __device__ inline size_t g_region_end(int Ish, int fmt) {
+__host__ __device__ inline size_t sel_end(int E, int H);
+__host__ __device__ inline ULayout u_layout(int E, int H, int K, int ngi, int Ish, int fmt) {
+  auto al = [](size_t v) { return (v + 15) & ~(size_t)15; };
   const size_t rec = 2 * (size_t)tile_codes_bytes(fmt) + 128;
-  return kGHead + (size_t)kW * kGRing * rec + (size_t)kTileRows * (Ish + 16);
+  const size_t bpl = fmt == 4 ? 16 : 12;
+  ULayout u;
+  u.ring = kGHead;
+  u.dtile = al(u.ring + (size_t)kW * kGRing * rec);
+  const size_t dend = u.dtile + (size_t)K * ngi * (64 * bpl + 64);
+  const size_t s_end = sel_end(E, H);
+  u.gdsh = al(dend > s_end ? dend : s_end);
+  u.hsh = al(u.gdsh + (size_t)kTileRows * (Ish + 16));
+  u.hsw = al(u.hsh + (size_t)Ish * 4);
+  const size_t g_end = u.hsw + (size_t)((Ish + 127) / 128) * 1024;
+  u.hrec = u.gdsh;
+  u.part = al(u.hrec + (size_t)K * ngi * 8 * kRecWords * 4);
+  const size_t d_end = u.part + (size_t)kW * 16 * 4;
+  u.end = g_end > d_end ? g_end : d_end;
+  return u;
 }
 
 // ---------------------------------------------------------------------------
@@ -541,13 +542,17 @@ __host__ __device__ inline size_t r_lds_bytes() { return (sizeof(RStageLds) + 25
 // Stage R's inputs do not depend on the token: every thread loads its own
 // part of them into registers while the previous layer's stage D computes
 // (HBM is otherwise idle then), in the layout it uses them in.
-//   w[s][c]: router row b + s*NB (the shared expert's gate row for row E),
-//            elements 2048c + 4t .. +3, the thread's elements of x;
+//   w[s][c]: router row b + s*NB, elements 2048c + 4t .. +3, the thread's
+//            elements of x;
+//   g[c]:    the same elements of the shared expert's gate row (every
+//            workgroup computes the gate logit itself, off the path of the
+//            router records);
 //   sa[i]:   k-chunk k0 + i of the workgroup's shared gate/up task, in the
 //            int8 MFMA A layout (lane l: row l % 16, bytes (l / 16) * 16).
 constexpr int kShMaxKc = 4;  // shared task k-chunks per wave
 struct StaticRegs {
   v4f w[kRSlots][kNch];
+  v4f g[kNch];
   v4i sa[kShMaxKc];
 };
 __device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs &L, const ShTask &st, StaticRegs &sr,
@@ -556,14 +561,20 @@ __device__ __forceinline__ void static_load(const StackArgs &a, const LayerPtrs 
 #pragma unroll
   for (int s2 = 0; s2 < kRSlots; s2++) {
     const int r = b + s2 * a.NB;
-    const bool valid = s2 < a.rslots && r <= a.E;  // uniform
-    const SW_G float *row = r < a.E ? L.router + (size_t)r * a.H : L.sgate;
+    const bool valid = s2 < a.rslots && r < a.E;  // uniform
+    const SW_G float *row = L.router + (size_t)(valid ? r : 0) * a.H;
 #pragma unroll
     for (int c = 0; c < kNch; c++) {
       const int e0 = 2048 * c + 4 * t;
       sr.w[s2][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
       if (valid && c < a.nch && e0 < a.H) sr.w[s2][c] = __builtin_nontemporal_load((const SW_G v4f *)(row + e0));
     }
+  }
+#pragma unroll
+  for (int c = 0; c < kNch; c++) {
+    const int e0 = 2048 * c + 4 * t;
+    sr.g[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < a.nch && e0 < a.H) sr.g[c] = *(const SW_G v4f *)(L.sgate + e0);
   }
   int k0, k1;
   sh_wave_range(st, wave, k0, k1);
@@ -717,8 +728,8 @@ __device__ __forceinline__ int row16_sum_i(int v) {
 // ---------------------------------------------------------------------------
 // Stage S: selection from the published records (all workgroups identically).
 // ---------------------------------------------------------------------------
-constexpr int kSelRec = 3;  // records per thread (E + 1 <= 3 * 512)
-static_assert(kStackMaxE + 1 <= kSelRec * kT, "every record has a thread in stage S");
+constexpr int kSelRec = 3;  // records per thread (E <= 3 * 512)
+static_assert(kStackMaxE <= kSelRec * kT, "every record has a thread in stage S");
 constexpr int kHrecPT = 8;  // h-record words (64-bit) per thread loaded in one batch
 struct SelLds {
   unsigned long long samp[64];  // each 64-expert list's c largest keys
@@ -736,23 +747,12 @@ struct SelLds {
   float wsel[kMaxK];
 };
 
-// stage S's union layout: selection state, records, keys, exact-chain
-// products, then the shared hidden vector (past stage G's regions: it is
-// quantised after stage G has started copying)
-__host__ __device__ inline size_t s_hsh_offset(int E, int H, int Ish, int fmt) {
-  const size_t o = ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)(E + 1) * 16 + (((size_t)E * 8 + 15) & ~(size_t)15) +
-                   (size_t)kRSlots * H * 4;
-  const size_t g = g_region_end(Ish, fmt);
-  return ((o > g ? o : g) + 15) & ~(size_t)15;
+// stage S's own part of the union: selection state, records [E], keys [E],
+// exact-chain products [kRSlots][H]
+__host__ __device__ inline size_t sel_end(int E, int H) {
+  return ((sizeof(SelLds) + 15) & ~(size_t)15) + (size_t)E * 16 + (((size_t)E * 8 + 15) & ~(size_t)15) +
+         (size_t)kRSlots * H * 4;
 }
-
-// The shared gate/up sums (u64 [2 * Ish]) and row scales (f32 [2 * Ish]),
-// copied in during stage S and read at the start of stage G: past the shared
-// hidden vector, clear of stage G's regions.
-__host__ __device__ inline size_t s_stage_offset(int E, int H, int Ish, int fmt) {
-  return s_hsh_offset(E, H, Ish, fmt) + (((size_t)Ish * 4 + 15) & ~(size_t)15);
-}
-__host__ __device__ inline size_t s_stage_bytes(int Ish) { return (size_t)Ish * 24; }
 
 struct Routes {  // result of stage S, in static LDS
   int idx[kMaxK];
@@ -761,6 +761,7 @@ struct Routes {  // result of stage S, in static LDS
   int flag;        // barrier result broadcast
   int state;       // selection path: 0 certified, 1 targeted exact, 2 full exact
   float shm[kW];   // each wave's largest |shared hidden value|
+  double gp[kW];   // each wave's part of the shared gate logit (fp64)
 };
 
 __device__ __forceinline__ bool sync_barrier(const StackArgs &a, const CallState &cs, int l, int which, Routes &rt) {
@@ -790,13 +791,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   __shared__ int s_shp[kW * 16];
   __shared__ unsigned s_lref[2][kRefWords];  // layer l's pointers in s_lref[l & 1]
   __shared__ int s_sht[5];                   // this workgroup's shared gate/up task
-  __shared__ unsigned s_shcnt;               // waves 1..7 whose stage S copies have landed, this call
   __shared__ uint64_t s_exp2[32];            // expf's table: LDS reads wait behind no global load
   const int b = blockIdx.x;
   const Lds S = lds_carve(smem, a0.Hp, a0.ngh, a0.Ish);
   if (threadIdx.x < 4) ((int *)zero16)[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
-  if (threadIdx.x == 0) s_shcnt = 0;
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = kExp2Tab[threadIdx.x];
   // Fault drill: these workgroups leave before taking any part, as if they
   // never became resident.  Every other one then meets a wait that cannot be
@@ -923,12 +922,23 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     // segment total.
     double Lt[kRSlots];
     float At[kRSlots], sv[kRSlots][kNch][4];
+    // the shared gate logit's part of this thread: the fp64 sum of exact products
+    double Lgt = 0.0;
+#pragma unroll
+    for (int c = 0; c < kNch; c++) {
+      if (c >= a.nch) continue;
+      const v4f w = c * 2048 + 4 * t < a.H ? sreg.g[c] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      Lgt = __builtin_fma((double)xv[c].x, (double)w.x, Lgt);
+      Lgt = __builtin_fma((double)xv[c].y, (double)w.y, Lgt);
+      Lgt = __builtin_fma((double)xv[c].z, (double)w.z, Lgt);
+      Lgt = __builtin_fma((double)xv[c].w, (double)w.w, Lgt);
+    }
 #pragma unroll
     for (int s = 0; s < kRSlots; s++) {
       Lt[s] = 0.0;
       At[s] = 0.0f;
       const int r = b + s * a.NB;
-      if (s < a.rslots && r <= a.E) {
+      if (s < a.rslots && r < a.E) {
 #pragma unroll
         for (int c = 0; c < kNch; c++) {
           if (c < a.nch) {
@@ -977,7 +987,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 #pragma unroll
     for (int s = 0; s < kRSlots; s++) {
       const int r = b + s * a.NB;
-      if (s < a.rslots && r <= a.E) {
+      if (s < a.rslots && r < a.E) {
         const float g = lane < a.nch * 8 ? R.segT[s][lane] : 0.0f;
         const float ge = dpp_row_shr1_f(row16_inclusive_scan_f(g));
         float P = 0.0f;
@@ -1042,7 +1052,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       if (lane < 2 * kRSlots) {
         const int s = lane >> 1;
         const int r = b + s * a.NB;
-        if (s < a.rslots && r <= a.E) {
+        if (s < a.rslots && r < a.E) {
           double Lg = 0.0, A = 0.0, P = 0.0;
 #pragma unroll
           for (int w = 0; w < kW; w++) {
@@ -1075,7 +1085,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const StackArgs a = kargs();
       SelLds &sel = *(SelLds *)S.u;
       double2 *lb = (double2 *)(S.u + ((sizeof(SelLds) + 15) & ~(size_t)15));
-      unsigned long long *lk = (unsigned long long *)(lb + a.E + 1);
+      unsigned long long *lk = (unsigned long long *)(lb + a.E);
       float *prod = (float *)((unsigned char *)lk + (((size_t)a.E * 8 + 15) & ~(size_t)15));  // [kRSlots][H]
       const int E = a.E, K = a.K;
       // records -> LDS, and this thread's keys (experts t + i*kT) in registers;
@@ -1087,7 +1097,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       for (int i = 0; i < kSelRec; i++) {
         const int e = t + i * kT;
         rx[i] = ry[i] = 0ull;
-        if (e <= E) {
+        if (e < E) {
           rx[i] = ld_agent(rec + 2 * e);
           ry[i] = ld_agent(rec + 2 * e + 1);
         }
@@ -1101,7 +1111,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           bool all = true;
 #pragma unroll
           for (int i = 0; i < kSelRec; i++)
-            if (t + i * kT <= E) all = all && has_tag(rx[i], tag) && has_tag(ry[i], tag);
+            if (t + i * kT < E) all = all && has_tag(rx[i], tag) && has_tag(ry[i], tag);
           if (all) break;
           if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
             s_abort = 1;
@@ -1110,7 +1120,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 #pragma unroll
           for (int i = 0; i < kSelRec; i++) {
             const int e = t + i * kT;
-            if (e <= E) {
+            if (e < E) {
               if (!has_tag(rx[i], tag)) rx[i] = ld_agent(rec + 2 * e);
               if (!has_tag(ry[i], tag)) ry[i] = ld_agent(rec + 2 * e + 1);
             }
@@ -1127,8 +1137,14 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
 #pragma unroll
       for (int i = 0; i < kSelRec; i++) {
         const int e = t + i * kT;
-        if (e <= E) lb[e] = make_double2(lx[i], ly[i]);
+        if (e < E) lb[e] = make_double2(lx[i], ly[i]);
         key[i] = e < E ? ((unsigned long long)float_key((float)lx[i]) << 32) | (unsigned)(~e) : 0ull;
+      }
+      // the shared gate logit's part of this wave (waves 1..7 now, wave 0
+      // once it has selected)
+      if (wave != 0) {
+        const double g = wave_sum_dpp(Lgt);
+        if (lane == 63) rt.gp[wave] = g;
       }
       if (t == 0) {
         sel.nm = 0;
@@ -1153,19 +1169,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           if (kk == m) kk = 0ull;
         }
       }
-      {
-        // the shared expert's gate, by the thread holding record E
-        const int iE = E / kT;
-        if (t == E - iE * kT) rt.sg = sigmoid_ref_t((float)(iE == 0 ? lx[0] : (iE == 1 ? lx[1] : lx[2])), s_exp2);
-      }
       lds_barrier();
       if (__builtin_expect(s_abort != 0, 0)) return;
-      // The shared gate/up sums and row scales: waves 1..7 copy them into LDS
-      // (device-scope copies of the counted sums, no registers held) and build
-      // the shared hidden vector from there while wave 0 selects.
-      float *hsh = (float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));  // [Ish]
-      unsigned long long *acs = (unsigned long long *)(S.u + s_stage_offset(a.E, a.H, a.Ish, FMT));  // [2 * Ish]
-      float *scs = (float *)(acs + 2 * a.Ish);                                                       // [2 * Ish]
       // T0, found by every wave: the sample with exactly K-1 larger ones
       unsigned long long T0;
       {
@@ -1205,67 +1210,45 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         up = wave_max_u64(up);
         if (lane == 0) sel.wup[wave] = up;
       }
-      // (issued after this wave's last use of its records: the compiler's
-      // wait for those loads would otherwise wait for the copies too)
-      if (wave != 0) {
-        // 1 KB pieces: sums (Ish % 64 == 0: whole pieces), then each scale row
-        const int nck_a = (a.Ish * 16) >> 10, nck_s = (a.Ish * 4 + 1023) >> 10;
-        for (int c = wave - 1; c < nck_a + 2 * nck_s; c += kW - 1) {
-          if (c < nck_a) {
-            dma_b128_dev(acc + (size_t)c * 128 + 2 * lane, lds_addr(acs) + 1024 * c);
-          } else {
-            const int c2 = c - nck_a, m = c2 >= nck_s, j = c2 - m * nck_s;
-            const float *src = (m ? (const float *)L.us : (const float *)L.gs) + (size_t)j * 256 + 4 * lane;
-            if (16 * lane < a.Ish * 4 - 1024 * j) dma_b128(src, lds_addr(scs + m * a.Ish) + 1024 * j);
-          }
-        }
-      }
       lds_barrier();
-      if (wave != 0) {
-        // the copies of waves 1..7 (each waits for its own, then counts in)
-        wait_dma();
-        if (lane == 0) atomicAdd(&s_shcnt, 1u);
-        // IDOT epilogue ((float)dot * s_row) * sx (c/qwen.c:1766), then SwiGLU
-        const unsigned long long *acs = (const unsigned long long *)(S.u + s_stage_offset(a.E, a.H, a.Ish, FMT));
-        const float *scs = (const float *)(acs + 2 * a.Ish);
-        const unsigned target = (unsigned)(kW - 1) * (unsigned)(l + 1);
-        while (__hip_atomic_load(&s_shcnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
-          __builtin_amdgcn_s_sleep(1);
-        const float sx = s_misc[0];
-        auto swiglu = [&](int i, unsigned long long wg, unsigned long long wu) {
-          const float h = silu_ref_t((float)acc_sum(wg) * scs[i] * sx, s_exp2) * ((float)acc_sum(wu) * scs[a.Ish + i] * sx);
-          hsh[i] = h;
-          return fabsf(h);
-        };
-        // from LDS only: a global load in this loop would make the compiler
-        // wait for every outstanding load (the copies included) first
-        float hm = 0.0f;
-        bool missing = false;
-        for (int i = t - 64; i < a.Ish; i += kT - 64) {
-          const unsigned long long wg = acs[i], wu = acs[a.Ish + i];
-          missing = missing || acc_parts(wg) != a.KQ || acc_parts(wu) != a.KQ;
-          hm = fmaxf(hm, swiglu(i, wg, wu));
-        }
-        if (__builtin_expect(__any(missing), 0)) {
-          // a sum still missing parts: read again from memory until complete
-          hm = 0.0f;
-          for (int i = t - 64; i < a.Ish; i += kT - 64) {
-            unsigned long long wg = acs[i], wu = acs[a.Ish + i];
-            const long long t0 = (long long)wall_clock64();
-            for (unsigned it = 0; acc_parts(wg) != a.KQ || acc_parts(wu) != a.KQ; it++) {
-              if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
-                s_abort = 1;
-                break;
-              }
-              wg = ld_agent_sync(&acc[i]);
-              wu = ld_agent_sync(&acc[a.Ish + i]);
+      if (wave >= 2) {
+        // The shared expert's down rows of this workgroup's output tile, for
+        // stage D, copied while HBM is otherwise idle.  Issued after this
+        // wave's last use of its records: the compiler's wait for those loads
+        // would otherwise wait for the copies too.
+        const ULayout ul = u_layout(a.E, a.H, a.K, a.ngi, a.Ish, FMT);
+        if (b < a.H / kTileRows)
+          for (int r = wave - 2; r < kTileRows; r += kW - 2)
+            for (int c0 = 0; c0 < a.Ish; c0 += 1024)
+              if (c0 + 16 * lane < a.Ish)
+                dma_b128((const void *)(L.dq + (size_t)(b * kTileRows + r) * a.Ish + c0 + 16 * lane),
+                         lds_addr(S.u + ul.gdsh + (size_t)r * (a.Ish + 16) + c0));
+      } else if (wave == 1) {
+        // This workgroup's values of the shared hidden vector, i = b + j*NB
+        // (lane j), while wave 0 selects: the counted gate/up sums (complete
+        // once all KQ parts are in; the tagged records vouch that every
+        // workgroup has added its own), the IDOT epilogue
+        // ((float)dot * s_row) * sx (c/qwen.c:1766) and SwiGLU (c/qwen.c:3419),
+        // published (tagged with the layer) for every workgroup's stage G.
+        const int i = b + lane * a.NB;
+        if (i < a.Ish) {
+          unsigned long long wg = ld_agent(&acc[i]), wu = ld_agent(&acc[a.Ish + i]);
+          const float gsr = L.gs[i], usr = L.us[i];
+          const long long t0 = (long long)wall_clock64();
+          for (unsigned it = 0; acc_parts(wg) != a.KQ || acc_parts(wu) != a.KQ; it++) {
+            if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
+              s_abort = 1;
+              break;
             }
-            hm = fmaxf(hm, swiglu(i, wg, wu));
+            wg = ld_agent(&acc[i]);
+            wu = ld_agent(&acc[a.Ish + i]);
           }
+          const float sx = s_misc[0];
+          const float h = silu_ref_t((float)acc_sum(wg) * gsr * sx, s_exp2) * ((float)acc_sum(wu) * usr * sx);
+          __hip_atomic_store(a.hs + i, ((unsigned long long)layer_tag(cs, l) << 32) | __float_as_uint(h),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        hm = wave_max_dpp(hm);
-        if (lane == 0) rt.shm[wave] = hm;
-      } else {
+      } else if (wave == 0) {
         const int M = sel.nmc;
         if (__builtin_expect(M > 64 || M < K, 0)) {
           if (lane == 0) rt.state = 2;
@@ -1331,6 +1314,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           }
           if (lane == 0) rt.state = ok ? 0 : (L.mode != 0 ? 2 : 1);
         }
+        const double g = wave_sum_dpp(Lgt);
+        if (lane == 63) rt.gp[0] = g;
       }
       lds_barrier();
       if (__builtin_expect(rt.state == 1, 0)) {
@@ -1489,6 +1474,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     // ======================= stage G =======================
     {
       const StackArgs a = kargs();
+      const ULayout ul = u_layout(a.E, a.H, a.K, a.ngi, a.Ish, FMT);
       float(*red)[2][16] = (float(*)[2][16])S.u;                 // [2][kW][gate, up][16] partials
       unsigned *stage = (unsigned *)(S.u + 2 * kW * 2 * 16 * 4);  // [kW][8] packed digits
       const int nU = a.K * a.nrt_i;
@@ -1500,57 +1486,40 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // 1 KB pieces, kGRing-1 records in flight while one is computed.
       constexpr int kSlotG = 2 * TGC + 128;
       constexpr int kGChunks = (kSlotG + 1023) / 1024;
-      static_assert(kGChunks * (kGRing - 1) <= 30, "stage G: ring waits within wait_vm's range");
       static_assert(kGHead >= 2 * kW * 2 * 16 * 4 + kW * 8 * 4, "stage G head");
-      unsigned char *ring = S.u + kGHead + (size_t)wave * kGRing * kSlotG;
-      // Units go round-robin over the workgroups.  When the last round would
-      // leave half of them idle (nU % NB <= NB/2), its units are split in two
-      // halves of every wave's groups, on workgroups 2k and 2k+1: each does
-      // its half first; 2k+1 publishes its partial sums (tagged words) and 2k
-      // adds them to its own at the end and builds the unit's record.
-      const int F = nU / a.NB, remu = nU - F * a.NB;
-      const bool split = remu > 0 && 2 * remu <= a.NB && remu <= kSplitUnits && a.ngh % (2 * kW) == 0;
-      const bool has_half = split && b < 2 * remu;
-      const int half = b & 1, hu = F * a.NB + (b >> 1);
-      const int nfull = split ? F : (b < nU ? (nU - 1 - b) / a.NB + 1 : 0);
-      const int nent = nfull + (has_half ? 1 : 0);
-      const int nh = n / 2, hlo = half ? nh : 0;  // the half: groups [hlo, hlo + nh) of the wave's
-      auto ent_unit = [&](int e_) { return has_half ? (e_ == 0 ? hu : b + (e_ - 1) * a.NB) : b + e_ * a.NB; };
-      auto ent_len = [&](int e_) { return (has_half && e_ == 0) ? nh : n; };
-      const int nitems = n > 0 ? nfull * n + (has_half ? nh : 0) : 0;
+      unsigned char *ring = S.u + ul.ring + (size_t)wave * kGRing * kSlotG;
+      // Units (route, 16 rows) go round-robin over the workgroups.
+      const int nent = b < nU ? (nU - 1 - b) / a.NB + 1 : 0;
+      const int nitems = n > 0 ? nent * n : 0;
       // This wave's unit table, one entry per lane: byte offset of the
       // entry's first record of this wave's groups (an invalid route reads the
       // layer's first bytes instead; its results are discarded).
       unsigned long long tc = 0ull;
       if (lane < nent) {
-        const int u = ent_unit(lane), j = u / a.nrt_i, r16 = u - j * a.nrt_i;
+        const int u = b + lane * a.NB, j = u / a.nrt_i, r16 = u - j * a.nrt_i;
         const int e = rt.idx[j];
-        if ((unsigned)e < (unsigned)a.E) {
-          const size_t tg = (size_t)r16 * a.ngh + g0 + ((has_half && lane == 0) ? hlo : 0);
-          tc = (size_t)e * a.expert_bytes + tg * kSlotG;
-        }
+        if ((unsigned)e < (unsigned)a.E) tc = (size_t)e * a.expert_bytes + ((size_t)r16 * a.ngh + g0) * kSlotG;
       }
-      // Issue cursor (entry iu, group gu, ring slot su).  Every step issues the
-      // kGChunks copies of one record, up to kGRing-1 items ahead of the one
-      // consumed, and none past the last item.
-      int iu = 0, gu = 0, su = 0, glen = ent_len(0), issued = 0;
+      // Issue cursor (entry iu, group gu, ring slot su).  Every step issues
+      // the kGChunks copies of one record, up to kGRing-1 items ahead of the
+      // one consumed, and none past the last item.
+      int iu = 0, gu = 0, su = 0, issued = 0;
       const unsigned char *cb = (const unsigned char *)L.experts;
       auto unit_base = [&](int i) {
         const int ii = i < nent ? i : nent - 1;
         const unsigned lo_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)tc, ii);
         const unsigned hi_c = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(tc >> 32), ii);
         cb = (const unsigned char *)L.experts + (((unsigned long long)hi_c << 32) | lo_c);
-        glen = ent_len(ii);
       };
       auto issue_next = [&]() {
         if (issued == nitems) return;
-        issued++;
         const unsigned slot = lds_addr(ring + su * kSlotG);
 #pragma unroll
         for (int k = 0; k < kGChunks; k++)
           if (16 * lane < kSlotG - 1024 * k) dma_b128_s(cb + gu * kSlotG + 1024 * k, 16 * lane, slot + 1024 * k);
+        issued++;
         if (++su == kGRing) su = 0;
-        if (++gu == glen) {
+        if (++gu == n) {
           gu = 0;
           unit_base(++iu);
         }
@@ -1601,7 +1570,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // Partials of entry i go to red[i & 1]; after one barrier, wave i % 8
       // finishes the entry while the others go on to the next one (the next
       // entry's barrier keeps red[i & 1] until the finisher is done).
-      float gh = 0.0f, uh = 0.0f;  // the half's sums (wave 0, lanes 0..15)
       auto finish_entry = [&](float accg[4], float accu[4], int i) {
         float(*rb)[2][16] = red + (i & 1) * kW;
         digit_fold(accg);
@@ -1622,79 +1590,52 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             gsum += rb[w][0][r];
             usum += rb[w][1][r];
           }
-          if (has_half && i == 0) {
-            gh = gsum;
-            uh = usum;
-            if (half) {
-              unsigned long long *w = a.spl + ((size_t)(b >> 1) * 16 + r) * 2;
-              const unsigned long long tg = (unsigned long long)layer_tag(cs, l) << 32;
-              __hip_atomic_store(w, tg | __float_as_uint(gsum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              __hip_atomic_store(w + 1, tg | __float_as_uint(usum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-          } else {
-            finish_h(gsum, usum, ent_unit(i));
-          }
+          finish_h(gsum, usum, b + i * a.NB);
         }
       };
-      // The shared expert's down rows of this workgroup's output tile go first
-      // in every wave's queue; they are multiplied with the shared hidden
-      // vector (built in stage S) once the routed work is done.
-      signed char *gdsh = (signed char *)(ring - (size_t)wave * kGRing * kSlotG + (size_t)kW * kGRing * kSlotG);
-      const int tile = b, ntiles = a.H / kTileRows;
-      auto issue_shdown = [&]() {
-        if (tile < ntiles)
-          for (int r = wave; r < kTileRows; r += kW)
-            for (int c0 = 0; c0 < a.Ish; c0 += 1024)
-              if (c0 + 16 * lane < a.Ish)
-                dma_b128((const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
-                         lds_addr(gdsh + (size_t)r * (a.Ish + 16) + c0));
-      };
-      // behind the first entry's records when there is one: the routed
-      // records are the ones the first computations wait for
-      if (!SW_SHDOWN_LATE || nent == 0) issue_shdown();
       if (nitems > 0) {
         unit_base(0);
 #pragma unroll
         for (int k = 0; k < kGRing - 1; k++) issue_next();
       }
-      float *hsh = (float *)(S.u + s_hsh_offset(a.E, a.H, a.Ish, FMT));
-      {
-        // qrow_i8 of the shared hidden vector (operand of the shared down
-        // projection at the end of this stage), while the first copies are in
-        // flight
-        float shx = 0.0f;
+      // The shared hidden vector (every workgroup's values, published in stage
+      // S) as tagged words, copied into LDS in 1 KB pieces (piece p by wave
+      // p % kW) a few items before this wave's last, so that they have landed
+      // by the end of the stage: at consume step kh, after that step's
+      // record, so the waits for the records issued before them allow nhp
+      // more copies outstanding.
+      const int nhpc = (a.Ish + 127) / 128;
+      const int nhp = nhpc > wave ? (nhpc - 1 - wave) / kW + 1 : 0;
+      const int kh = nitems > 3 ? nitems - 3 : 0;
+      auto issue_hs = [&]() {
+        for (int q = 0; q < nhp; q++) {
+          const int pc = wave + kW * q, rem = a.Ish - 128 * pc;
+          if (2 * lane < rem) dma_b128_dev(a.hs + (size_t)pc * 128 + 2 * lane, lds_addr(S.u + ul.hsw) + 1024 * pc);
+        }
+      };
+      if (nitems == 0) issue_hs();
+      if (t == 64) {
+        // the shared expert's gate (c/qwen.c:3737) for stage D: its fp64
+        // logit, the waves' parts added in order, rounded, through
+        // sigmoidf_stable
+        double g = 0.0;
 #pragma unroll
-        for (int w = 1; w < kW; w++) shx = fmaxf(shx, rt.shm[w]);
-        shx = shx / 127.0f;
-        if (shx < 1e-12f) shx = 1e-12f;
-        const float hinv = 1.0f / shx;
-        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
-        if (t == 0) s_misc[1] = shx;
+        for (int w = 0; w < kW; w++) g += rt.gp[w];
+        rt.sg = sigmoid_ref_t((float)g, s_exp2);
       }
       int csl = 0, consumed = 0;  // consume slot, items consumed
-      // the split unit's partner half (workgroups 2k): its two words are
-      // read while the last entry computes (first used after every copy has
-      // landed, so the compiler's wait for them waits for nothing else)
-      const bool partner = has_half && !half && wave == 0 && lane < 16;
-      const unsigned long long *pw = a.spl + ((size_t)(b >> 1) * 16 + (lane & 15)) * 2;
-      unsigned long long pvg = 0ull, pvu = 0ull;
       for (int i = 0; i < nent; i++) {
-        if (i == nent - 1 && partner) {
-          pvg = ld_agent(pw);
-          pvu = ld_agent(pw + 1);
-        }
-        const int glo = (has_half && i == 0) ? hlo : 0, ghi = glo + ent_len(i);
         float accg[4] = {0, 0, 0, 0}, accu[4] = {0, 0, 0, 0};
         if (n > 0) {
 #pragma unroll
           for (int gi = 0; gi < kGMax; gi++)
-            if (gi >= glo && gi < ghi) {
+            if (gi < n) {
               issue_next();
-              // this item's copies are done once at most the copies of the
-              // items issued after it are outstanding (a wave's memory
-              // operations complete in order; a store of finish_h only makes
-              // the wait longer)
-              wait_vm(kGChunks * (issued - consumed - 1));
+              if (consumed == kh) issue_hs();
+              // this item's copies are done once at most the copies issued
+              // after it are outstanding (a wave's memory operations complete
+              // in order; a store of finish_h only makes the wait longer)
+              wait_vm(kGChunks * (issued - consumed - 1) + (consumed >= kh && consumed < kh + kGRing ? nhp : 0));
               consumed++;
               const unsigned char *rec = ring + csl * kSlotG;
               g_item<FMT>(rec, rec + 2 * TGC, xo.b0[gi], xo.b1[gi], xo.dsc[gi], xo.zq[gi], accg, lane);
@@ -1703,44 +1644,67 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
             }
         }
         finish_entry(accg, accu, i);
-        if (SW_SHDOWN_LATE && i == 0) issue_shdown();
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every copy (and the partner words) has landed
-      if (partner) {
-        // the partner's half of the split unit (published long ago: it was its
-        // first entry), added to this workgroup's in a fixed order
+      // every copy has landed and every h record store is complete
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();  // the last finisher is done with its partials; the tagged words are in
+      {
+        // The shared hidden vector's values (a word not yet carrying this
+        // layer's tag when copied is read again: rare), its qrow_i8
+        // (c/qwen.c:1696: s = amax/127, floor 1e-12, q = rint(h/s)), then the
+        // shared down: exact int32 dots of the tile's 16 rows with it, into
+        // s_shp (the ring is no longer read).
         const unsigned tag = layer_tag(cs, l);
-        const long long t0 = (long long)wall_clock64();
-        for (unsigned it = 0; (unsigned)(pvg >> 32) != tag || (unsigned)(pvu >> 32) != tag; it++) {
-          if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
-            s_abort = 1;
-            break;
+        const unsigned long long *hw = (const unsigned long long *)(S.u + ul.hsw);
+        float *hsh = (float *)(S.u + ul.hsh);
+        float hm = 0.0f;
+        for (int i = t; i < a.Ish; i += kT) {
+          unsigned long long w = hw[i];
+          if (__builtin_expect((unsigned)(w >> 32) != tag, 0)) {
+            const long long t0 = (long long)wall_clock64();
+            for (unsigned it = 0; (unsigned)(w >> 32) != tag; it++) {
+              if ((it & 15) == 15 && __builtin_expect(wait_expired(t0, a), 0)) {
+                s_abort = 1;
+                break;
+              }
+              w = ld_agent_sync(a.hs + i);
+            }
           }
-          pvg = ld_agent_sync(pw);
-          pvu = ld_agent_sync(pw + 1);
+          const float h = __uint_as_float((unsigned)w);
+          hsh[i] = h;
+          hm = fmaxf(hm, fabsf(h));
         }
-        finish_h(gh + __uint_as_float((unsigned)pvg), uh + __uint_as_float((unsigned)pvu), hu);
-      }
-      lds_barrier();  // the last finisher is done with its partials; every copy has landed
-      if (__builtin_expect(s_abort != 0, 0)) return;
-      // shared down: exact int32 dots of the tile's 16 rows with hq, into
-      // s_shp (the ring is no longer read)
-      if (tile < ntiles) {
-        int *shp = s_shp;
-        const int nkd = a.Ish / 64, kb = lane >> 4;
-        const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
-        v4i cd = {0, 0, 0, 0};
-        const signed char *arow = gdsh + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
-        for (int kc = dk0; kc < dk1; kc++) {
-          const v4i av = *(const v4i *)(arow + kc * 64);
-          const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.hq + kc * 64 + kb * 16) : v4i{0, 0, 0, 0};
-          cd = mfma_i8(av, bv, cd);
-        }
-        if ((lane & 15) == 0) {
+        hm = wave_max_dpp(hm);
+        if (lane == 0) rt.shm[wave] = hm;
+        lds_barrier();
+        float shx = 0.0f;
 #pragma unroll
-          for (int i = 0; i < 4; i++) shp[wave * 16 + 4 * kb + i] = cd[i];
+        for (int w = 0; w < kW; w++) shx = fmaxf(shx, rt.shm[w]);
+        shx = shx / 127.0f;
+        if (shx < 1e-12f) shx = 1e-12f;
+        const float hinv = 1.0f / shx;
+        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
+        if (t == 0) s_misc[1] = shx;
+        lds_barrier();
+        const int ntiles = a.H / kTileRows;
+        if (b < ntiles) {
+          const signed char *gdsh = (const signed char *)(S.u + ul.gdsh);
+          const int nkd = a.Ish / 64, kb = lane >> 4;
+          const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
+          v4i cd = {0, 0, 0, 0};
+          const signed char *arow = gdsh + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
+          for (int kc = dk0; kc < dk1; kc++) {
+            const v4i av = *(const v4i *)(arow + kc * 64);
+            const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.hq + kc * 64 + kb * 16) : v4i{0, 0, 0, 0};
+            cd = mfma_i8(av, bv, cd);
+          }
+          if ((lane & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_shp[wave * 16 + 4 * kb + i] = cd[i];
+          }
         }
       }
+      if (__builtin_expect(s_abort != 0, 0)) return;
       // zero records of chunks past I inside the last group (only when I % 128 != 0)
       if (b == 0 && wave == 0) {
         const int pad = a.ngi * 8 - a.nrt_i;
@@ -1756,7 +1720,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     // ======================= stage D (loads, then barrier h) =======================
     {
       const StackArgs a = kargs();
-      const DLayout dl = d_layout(a.K, a.ngi, a.Ish, FMT);
+      const ULayout dl = u_layout(a.E, a.H, a.K, a.ngi, a.Ish, FMT);
       constexpr int BPL = FMT == 4 ? 16 : 12;
       constexpr int kSlot = 64 * BPL + 64;  // one tile-group: codes, then 16 row scales
       const int nq = a.K * a.ngi;
@@ -1791,15 +1755,17 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         // call never meets a word left by an older one (records are read
         // only where a call writes them, and tags repeat)
         const int r = b + lane * a.NB;
-        if (lane < a.rslots && r <= a.E) {
+        if (lane < a.rslots && r < a.E) {
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store((unsigned long long *)a.rec + 2 * r + 1, 0ull, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      if (__builtin_expect(l == a.n - 1, 0) && wave == 0 && lane < 32 && (b & 1) == 0 && (b >> 1) < kSplitUnits) {
-        // the split units' half sums (read by this workgroup only): cleared too
-        __hip_atomic_store(a.spl + (size_t)(b >> 1) * 32 + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_expect(l == a.n - 1, 0) && wave == 1 && b + lane * a.NB < a.Ish) {
+        // the shared hidden words this workgroup published: every workgroup
+        // has read them (before the hidden barrier), so cleared as the
+        // records are
+        __hip_atomic_store(a.hs + b + lane * a.NB, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (__builtin_expect(l == a.n - 1, 0) && b == 0 && t == 0) {
         // every workgroup has read the call state: advance it for the next call
@@ -1820,12 +1786,18 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int *shp = s_shp;                        // [kW][16]
       const float shx = s_misc[1];
       const int n64 = a.K * a.ngi * 8 * kRecWords / 2;
+      // Every load unconditional, from a clamped index (values past the end
+      // are loaded twice and not used): a register first zeroed and then
+      // loaded under a lane mask makes the compiler wait for the earlier
+      // loads before zeroing the next one.
+      // the shared down row scales of this workgroup's tile, for the combine
+      const float dsr = L.ds[(tile < ntiles ? tile : 0) * kTileRows + (t & (kTileRows - 1))];
       {
         unsigned long long hv[kHrecPT];
 #pragma unroll
         for (int i = 0; i < kHrecPT; i++) {
           const int j = t + i * kT;
-          hv[i] = j < n64 ? ld_agent((const unsigned long long *)a.hd + j) : 0ull;
+          hv[i] = ld_agent((const unsigned long long *)a.hd + (j < n64 ? j : 0));
         }
 #pragma unroll
         for (int i = 0; i < kHrecPT; i++) {
@@ -1835,14 +1807,10 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         for (int j = t + kHrecPT * kT; j < n64; j += kT)
           ((unsigned long long *)hrec)[j] = ld_agent((const unsigned long long *)a.hd + j);
       }
-      // the shared down row scales of this workgroup's tile, for the combine
-      // (loaded after the records, so that waiting for those excludes them)
-      float dsr = 0.0f;
-      if (t < kTileRows && tile < ntiles) dsr = L.ds[tile * kTileRows + t];
 
+      wait_dma();     // this wave's LDS copies have landed
+      lds_barrier();  // ... and every other wave's; every h record is in
       if (tile < ntiles) {
-        wait_dma();     // this wave's LDS copies have landed
-        lds_barrier();  // ... and every other wave's
         const int c = lane & 15, kb = lane >> 4;
         const bool lo = c < 8 && (c >> 1) == kb;
         const bool hi = c >= 8 && ((c - 8) >> 1) == kb;
@@ -1936,6 +1904,12 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       } else if (l + 1 < a.n) {
         static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sh_task_lds(s_sht), sreg, t);
       }
+      // The next layer's stage R inputs, loaded while the layer barrier
+      // completes (HBM is otherwise idle then), by waves 1..7; wave 0, whose
+      // barrier arrival and polls would wait behind them (a wave's loads
+      // complete in order), loads its part once it has passed the barrier.
+      // Issued after the combine: the compiler's wait for the combine's own
+      // loads would otherwise wait for these too.
       lds_barrier();
     }
 
@@ -1980,14 +1954,8 @@ static LayerRef make_ref(const ColiMoeLayer *L) {
 // the selection's arrays, stage G's ring and stage D's layout.
 static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, int fmt, int rslots, int shkc) {
   const size_t rlay = r_lds_bytes();
-  const size_t sel = s_stage_offset(E, H, Ish, fmt) + s_stage_bytes(Ish);
-  const size_t dst = d_layout(K, ngi, Ish, fmt).end;
-  const size_t ring = g_region_end(Ish, fmt);
-  size_t u = rlay;
-  if (sel > u) u = sel;
-  if (dst > u) u = dst;
-  if (ring > u) u = ring;
-  return u;
+  const size_t u = u_layout(E, H, K, ngi, Ish, fmt).end;
+  return u > rlay ? u : rlay;
 }
 
 // shared gate/up tasks: 16-row tiles of both matrices, each split into KQ
@@ -1997,7 +1965,7 @@ static int stack_kq(int NB, int H, int E, int Ish) {
   const int nsh_rt = 2 * (Ish / kTileRows);
   if (nsh_rt == 0) return 1;
   int KQ = NB / nsh_rt;
-  if (KQ > (E + 1) / nsh_rt) KQ = (E + 1) / nsh_rt;
+  if (KQ > E / nsh_rt) KQ = E / nsh_rt;
   if (KQ > H / 64) KQ = H / 64;
   return KQ < 1 ? 1 : KQ;
 }
@@ -2006,18 +1974,19 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
   const int NB = ctx->sm_count;
   const int H = s.hidden, E = s.experts, K = s.topk, I = s.intermediate, Ish = s.shared_intermediate;
   if (H > 2048 * kNch || H % 64 || K > kMaxK || K > E || I % 16 || Ish % 64 || Ish > kStackMaxIsh) return false;
-  if ((E + 1 + NB - 1) / NB > kRSlots) return false;                 // router rows in registers
+  if ((E + NB - 1) / NB > kRSlots) return false;                     // router rows in registers
   if (E > kStackMaxE) return false;                                   // selection keys in registers
   if (2 * (Ish / kTileRows) > NB) return false;                       // one shared task per workgroup
+  if (Ish > 64 * NB) return false;                                    // shared hidden: a lane per value
   const int ngh = (H + kGroup - 1) / kGroup, ngi = (I + kGroup - 1) / kGroup;
   if ((ngh + kW - 1) / kW > kGMax) return false;                     // G: groups per wave
   if (K * ngi > 64 * kW) return false;                                // D: one item per lane of a wave
   if (H / kTileRows > NB) return false;                               // D: one output tile per workgroup
-  if ((K * (I / kTileRows) + NB - 1) / NB > 63) return false;         // G: one entry per lane (+1 split half)
+  if ((K * (I / kTileRows) + NB - 1) / NB > 64) return false;         // G: one entry per lane
   const int Hp = ngh * kGroup;
-  const int rslots = (E + 1 + NB - 1) / NB;
+  const int rslots = (E + NB - 1) / NB;
   const int KQ = stack_kq(NB, H, E, Ish);
-  if (2 * (Ish / kTileRows) * KQ > E + 1) return false;              // tasks' workgroups own records
+  if (2 * (Ish / kTileRows) * KQ > E) return false;                  // tasks' workgroups own records
   const int shkc = (H / 64 + KQ - 1) / KQ;
   if ((shkc + kW - 1) / kW > kShMaxKc) return false;                 // shared task A operands in registers
   const size_t u = stack_union_bytes(E, H, K, ngh, ngi, Ish, s.expert_format, rslots, shkc);
@@ -2029,7 +1998,7 @@ bool stack_shape_ok(const ColiCuda *ctx, const ColiMoeShape &s) {
 constexpr size_t kRecRegion = ((size_t)(kStackMaxE + 1) * 16 + 255) & ~(size_t)255;  // router records
 constexpr size_t kExRegion = ((size_t)kStackMaxE * 4 + 255) & ~(size_t)255;          // exact logits
 constexpr size_t kStateRegion = 256;                                                  // call state
-constexpr size_t kSplitRegion = (size_t)kSplitUnits * 16 * 2 * 8;                     // split units' half sums
+constexpr size_t kHsRegion = (size_t)kStackMaxIsh * 8;                                 // shared hidden vector
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
@@ -2049,7 +2018,7 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   }
   const int ngi = (s.intermediate + kGroup - 1) / kGroup;
   const size_t scratch =
-      kRecRegion + kExRegion + kStateRegion + kSplitRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
+      kRecRegion + kExRegion + kStateRegion + kHsRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
   const void *before = ctx->scratch[kScrStack];
   if (ensure_scratch(ctx, kScrStack, scratch, "MoE stack scratch allocation")) return -1;
   if (ctx->scratch[kScrStack] != before) {
@@ -2154,7 +2123,7 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.expert_bytes = L0->xl.expert_bytes;
   a.gu_bytes = L0->xl.gu_bytes;
   a.NB = ctx->sm_count;
-  a.rslots = (a.E + 1 + a.NB - 1) / a.NB;
+  a.rslots = (a.E + a.NB - 1) / a.NB;
   const int nsh_rt = 2 * (a.Ish / kTileRows);
   const int KQ = stack_kq(a.NB, a.H, a.E, a.Ish);
   a.KQ = KQ;
@@ -2169,8 +2138,8 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   char *scr = (char *)ctx->scratch[kScrStack];
   a.rec = (double *)scr;
   a.ex = (float *)(scr + kRecRegion);
-  a.spl = (unsigned long long *)(scr + kRecRegion + kExRegion + kStateRegion);
-  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kSplitRegion);
+  a.hs = (unsigned long long *)(scr + kRecRegion + kExRegion + kStateRegion);
+  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kHsRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
   a.acc = (unsigned long long *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);

@@ -39,7 +39,8 @@ __device__ __forceinline__ void dma_b128_s(const void *sbase, unsigned voff, uns
 #pragma clang diagnostic pop
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n (the immediate is encoded per case)
+// s_waitcnt vmcnt(n) for a wave-uniform n (the immediate is encoded per case;
+// gfx950's counter holds 6 bits, so n > 63 waits for everything)
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
 #define SW_VM(k) \
@@ -49,6 +50,10 @@ __device__ __forceinline__ void wait_vm(int n) {
     SW_VM(1) SW_VM(2) SW_VM(3) SW_VM(4) SW_VM(5) SW_VM(6) SW_VM(7) SW_VM(8) SW_VM(9) SW_VM(10) SW_VM(11)
     SW_VM(12) SW_VM(13) SW_VM(14) SW_VM(15) SW_VM(16) SW_VM(17) SW_VM(18) SW_VM(19) SW_VM(20) SW_VM(21)
     SW_VM(22) SW_VM(23) SW_VM(24) SW_VM(25) SW_VM(26) SW_VM(27) SW_VM(28) SW_VM(29) SW_VM(30)
+    SW_VM(31) SW_VM(32) SW_VM(33) SW_VM(34) SW_VM(35) SW_VM(36) SW_VM(37) SW_VM(38) SW_VM(39) SW_VM(40)
+    SW_VM(41) SW_VM(42) SW_VM(43) SW_VM(44) SW_VM(45) SW_VM(46) SW_VM(47) SW_VM(48) SW_VM(49) SW_VM(50)
+    SW_VM(51) SW_VM(52) SW_VM(53) SW_VM(54) SW_VM(55) SW_VM(56) SW_VM(57) SW_VM(58) SW_VM(59) SW_VM(60)
+    SW_VM(61) SW_VM(62) SW_VM(63)
 #undef SW_VM
     default:
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
