@@ -128,6 +128,7 @@ struct StackArgs {
   float *ex;            // [E] exact logits
   unsigned *hd;         // [K][ngi*8][kRecWords]
   unsigned long long *hs;  // [Ish] the shared hidden vector: (layer tag << 32) | f32 bits
+  float *shv;           // [H] shared down values computed by a paired workgroup (see g_pairing)
   unsigned long long *acc;  // [layer][parity][2*Ish] counted shared gate/up sums
   unsigned *bars;       // [layer][parity][kBars][kBarWords]
   size_t acc_stride;    // words per (layer, parity) acc block
@@ -438,19 +439,16 @@ struct Lds {
   signed char *xd;   // [2][Hp] routed activation digits
   float4 *xgp;       // [ngh]
   signed char *xq;   // [Hp] IDOT quantisation of x
-  signed char *hq;   // [Ish] IDOT quantisation of the shared hidden vector
   unsigned char *u;  // stage-local union
 };
 __host__ __device__ inline size_t lds_fixed(int Hp, int ngh, int Ish) {
-  return (((size_t)2 * Hp + 15) & ~(size_t)15) + (size_t)ngh * 16 + (((size_t)Hp + 15) & ~(size_t)15) +
-         (((size_t)Ish + 15) & ~(size_t)15) + 16;
+  return (((size_t)2 * Hp + 15) & ~(size_t)15) + (size_t)ngh * 16 + (((size_t)Hp + 15) & ~(size_t)15) + 16;
 }
 __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, int Ish) {
   Lds s;
   s.xd = (signed char *)smem;
   s.xgp = (float4 *)(smem + (((size_t)2 * Hp + 15) & ~(size_t)15));
   s.xq = (signed char *)(s.xgp + ngh);
-  s.hq = s.xq + (((size_t)Hp + 15) & ~(size_t)15);
   s.u = smem + lds_fixed(Hp, ngh, Ish);
   return s;
 }
@@ -463,12 +461,13 @@ __device__ __forceinline__ Lds lds_carve(unsigned char *smem, int Hp, int ngh, i
 //          stage S, past sel_end.
 //   G      partials and digit staging (kGHead), the rings of gate/up records;
 //          the shared hidden vector as tagged words (hsw, copied in near the
-//          end) and as values (hsh).
+//          end); a paired workgroup's shared down rows (gdsh2, copied in
+//          stage S).
 //   D      (after the hidden barrier) the routed down records of the output
 //          tile (dtile, copied while the barrier completes), h records and
 //          partial sums over gdsh and what follows it.
 struct ULayout {
-  size_t ring, dtile, gdsh, hsh, hsw, hrec, part, end;
+  size_t ring, dtile, gdsh, hsw, gdsh2, hrec, part, end;
 };
 __host__ __device__ inline size_t sel_end(int E, int H);
 __host__ __device__ inline ULayout u_layout(int E, int H, int K, int ngi, int Ish, int fmt) {
@@ -481,9 +480,9 @@ __host__ __device__ inline ULayout u_layout(int E, int H, int K, int ngi, int Is
   const size_t dend = u.dtile + (size_t)K * ngi * (64 * bpl + 64);
   const size_t s_end = sel_end(E, H);
   u.gdsh = al(dend > s_end ? dend : s_end);
-  u.hsh = al(u.gdsh + (size_t)kTileRows * (Ish + 16));
-  u.hsw = al(u.hsh + (size_t)Ish * 4);
-  const size_t g_end = u.hsw + (size_t)((Ish + 127) / 128) * 1024;
+  u.hsw = al(u.gdsh + (size_t)kTileRows * (Ish + 16));
+  u.gdsh2 = al(u.hsw + (size_t)((Ish + 127) / 128) * 1024);
+  const size_t g_end = u.gdsh2 + (size_t)kTileRows * (Ish + 16);
   u.hrec = u.gdsh;
   u.part = al(u.hrec + (size_t)K * ngi * 8 * kRecWords * 4);
   const size_t d_end = u.part + (size_t)kW * 16 * 4;
@@ -725,6 +724,24 @@ __device__ __forceinline__ int row16_sum_i(int v) {
 }
 
 
+// Stage G's pairing: the first rr = nU % NB workgroups take one unit more than
+// the others (nU units round-robin).  When rr <= NB/2, light workgroup b + rr
+// also computes heavy workgroup b's shared down values (it finishes its units
+// about one unit earlier) and publishes them for b's stage D, so the heavy
+// ones, which the hidden barrier waits for, skip that work.
+struct GPair {
+  bool heavy;    // this workgroup's shared down values come from b + rr
+  int partner;   // the heavy workgroup whose values this one also computes, or -1
+};
+__device__ __forceinline__ GPair g_pairing(const StackArgs &a, int b) {
+  const int nU = a.K * a.nrt_i, rr = nU % a.NB, ntiles = a.H / kTileRows;
+  const bool pairs = rr > 0 && 2 * rr <= a.NB;
+  GPair p;
+  p.heavy = pairs && b < rr && b < ntiles;
+  p.partner = (pairs && b >= rr && b < 2 * rr && b - rr < ntiles) ? b - rr : -1;
+  return p;
+}
+
 // ---------------------------------------------------------------------------
 // Stage S: selection from the published records (all workgroups identically).
 // ---------------------------------------------------------------------------
@@ -789,6 +806,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
   // output rows: written at the end of stage G while other waves may still
   // read the shared down rows, so kept out of the stage-local union
   __shared__ int s_shp[kW * 16];
+  __shared__ int s_shp2[kW * 16];  // the same for the paired heavy workgroup's rows
   __shared__ unsigned s_lref[2][kRefWords];  // layer l's pointers in s_lref[l & 1]
   __shared__ int s_sht[5];                   // this workgroup's shared gate/up task
   __shared__ uint64_t s_exp2[32];            // expf's table: LDS reads wait behind no global load
@@ -1217,12 +1235,16 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         // wave's last use of its records: the compiler's wait for those loads
         // would otherwise wait for the copies too.
         const ULayout ul = u_layout(a.E, a.H, a.K, a.ngi, a.Ish, FMT);
-        if (b < a.H / kTileRows)
+        const GPair gp = g_pairing(a, b);
+        auto copy_tile = [&](int tile, size_t dst) {
           for (int r = wave - 2; r < kTileRows; r += kW - 2)
             for (int c0 = 0; c0 < a.Ish; c0 += 1024)
               if (c0 + 16 * lane < a.Ish)
-                dma_b128((const void *)(L.dq + (size_t)(b * kTileRows + r) * a.Ish + c0 + 16 * lane),
-                         lds_addr(S.u + ul.gdsh + (size_t)r * (a.Ish + 16) + c0));
+                dma_b128((const void *)(L.dq + (size_t)(tile * kTileRows + r) * a.Ish + c0 + 16 * lane),
+                         lds_addr(S.u + dst + (size_t)r * (a.Ish + 16) + c0));
+        };
+        if (b < a.H / kTileRows && !gp.heavy) copy_tile(b, ul.gdsh);
+        if (gp.partner >= 0) copy_tile(gp.partner, ul.gdsh2);
       } else if (wave == 1) {
         // This workgroup's values of the shared hidden vector, i = b + j*NB
         // (lane j), while wave 0 selects: the counted gate/up sums (complete
@@ -1604,7 +1626,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       // by the end of the stage: at consume step kh, after that step's
       // record, so the waits for the records issued before them allow nhp
       // more copies outstanding.
-      const int nhpc = (a.Ish + 127) / 128;
+      const int nhpc = g_pairing(a, b).heavy ? 0 : (a.Ish + 127) / 128;  // a heavy workgroup needs none
       const int nhp = nhpc > wave ? (nhpc - 1 - wave) / kW + 1 : 0;
       const int kh = nitems > 3 ? nitems - 3 : 0;
       auto issue_hs = [&]() {
@@ -1645,18 +1667,27 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
         finish_entry(accg, accu, i);
       }
-      // every copy has landed and every h record store is complete
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // Every copy has landed.  The last entry's finisher may still have its
+      // h-record store in flight (its last memory operation): it is waited
+      // for before the workgroup arrives at the hidden barrier.
+      if (nent > 0 && wave == ((nent - 1) & (kW - 1)))
+        wait_vm(1);
+      else
+        wait_dma();
       lds_barrier();  // the last finisher is done with its partials; the tagged words are in
-      {
+      const GPair gp = g_pairing(a, b);
+      if (!gp.heavy) {
         // The shared hidden vector's values (a word not yet carrying this
         // layer's tag when copied is read again: rare), its qrow_i8
-        // (c/qwen.c:1696: s = amax/127, floor 1e-12, q = rint(h/s)), then the
-        // shared down: exact int32 dots of the tile's 16 rows with it, into
-        // s_shp (the ring is no longer read).
+        // (c/qwen.c:1696: s = amax/127, floor 1e-12, q = rint(h/s)) applied
+        // as the operands are read, and the shared down: exact int32 dots of
+        // the tile's 16 rows with it, into s_shp (the ring is no longer read);
+        // with a partner, its tile's too, published as the combine's shared
+        // values ((float)dot * s_row) * sx.
         const unsigned tag = layer_tag(cs, l);
-        const unsigned long long *hw = (const unsigned long long *)(S.u + ul.hsw);
-        float *hsh = (float *)(S.u + ul.hsh);
+        unsigned long long *hw = (unsigned long long *)(S.u + ul.hsw);
+        const int ntiles = a.H / kTileRows;
+        const float pds = gp.partner >= 0 && t < kTileRows ? L.ds[gp.partner * kTileRows + t] : 0.0f;
         float hm = 0.0f;
         for (int i = t; i < a.Ish; i += kT) {
           unsigned long long w = hw[i];
@@ -1669,10 +1700,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
               }
               w = ld_agent_sync(a.hs + i);
             }
+            hw[i] = w;
           }
-          const float h = __uint_as_float((unsigned)w);
-          hsh[i] = h;
-          hm = fmaxf(hm, fabsf(h));
+          hm = fmaxf(hm, fabsf(__uint_as_float((unsigned)w)));
         }
         hm = wave_max_dpp(hm);
         if (lane == 0) rt.shm[wave] = hm;
@@ -1683,24 +1713,45 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         shx = shx / 127.0f;
         if (shx < 1e-12f) shx = 1e-12f;
         const float hinv = 1.0f / shx;
-        for (int i = t; i < a.Ish; i += kT) S.hq[i] = (signed char)__builtin_rintf(hsh[i] * hinv);
         if (t == 0) s_misc[1] = shx;
-        lds_barrier();
-        const int ntiles = a.H / kTileRows;
-        if (b < ntiles) {
-          const signed char *gdsh = (const signed char *)(S.u + ul.gdsh);
-          const int nkd = a.Ish / 64, kb = lane >> 4;
-          const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
+        const int nkd = a.Ish / 64, kb = lane >> 4;
+        const int dk0 = wave * nkd / kW, dk1 = (wave + 1) * nkd / kW;
+        auto shared_down = [&](const signed char *rows, int *out) {
           v4i cd = {0, 0, 0, 0};
-          const signed char *arow = gdsh + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
+          const signed char *arow = rows + (size_t)(lane & 15) * (a.Ish + 16) + kb * 16;
           for (int kc = dk0; kc < dk1; kc++) {
             const v4i av = *(const v4i *)(arow + kc * 64);
-            const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.hq + kc * 64 + kb * 16) : v4i{0, 0, 0, 0};
+            v4i bv = {0, 0, 0, 0};
+            if ((lane & 15) == 0) {
+              const v4u *hp = (const v4u *)(hw + kc * 64 + kb * 16);  // 16 words: (tag, bits) pairs
+#pragma unroll
+              for (int q = 0; q < 4; q++) {
+                const v4u u0 = hp[2 * q], u1 = hp[2 * q + 1];
+                const int q0 = (int)__builtin_rintf(__uint_as_float(u0.x) * hinv);
+                const int q1 = (int)__builtin_rintf(__uint_as_float(u0.z) * hinv);
+                const int q2 = (int)__builtin_rintf(__uint_as_float(u1.x) * hinv);
+                const int q3 = (int)__builtin_rintf(__uint_as_float(u1.z) * hinv);
+                bv[q] = (q0 & 255) | (q1 & 255) << 8 | (q2 & 255) << 16 | (q3 & 255) << 24;
+              }
+            }
             cd = mfma_i8(av, bv, cd);
           }
           if ((lane & 15) == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) s_shp[wave * 16 + 4 * kb + i] = cd[i];
+            for (int i = 0; i < 4; i++) out[wave * 16 + 4 * kb + i] = cd[i];
+          }
+        };
+        if (b < ntiles) shared_down((const signed char *)(S.u + ul.gdsh), s_shp);
+        if (gp.partner >= 0) {
+          shared_down((const signed char *)(S.u + ul.gdsh2), s_shp2);
+          lds_barrier();
+          if (t < kTileRows) {
+            int dot = 0;
+#pragma unroll
+            for (int w = 0; w < kW; w++) dot += s_shp2[w * 16 + t];
+            // stored before this workgroup arrives at the hidden barrier
+            __hip_atomic_store(a.shv + gp.partner * kTileRows + t, (float)dot * pds * shx, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
           }
         }
       }
@@ -1726,6 +1777,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       const int nq = a.K * a.ngi;
       const int tile = b, ntiles = a.H / kTileRows;
       unsigned char *dtile = S.u + dl.dtile;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every h record store is complete
       lds_barrier();
       stamp(a, l, 4);
       if (t == 0) bar_arrive(bar_of(a, cs, l, kBarH), a.NB);
@@ -1780,6 +1832,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         __hip_atomic_store(a.state + kStParity, (unsigned)(p ^ 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
 
+      // a heavy workgroup's shared down values, computed by its partner
+      const bool heavy = g_pairing(a, b).heavy;
+      const float hshv = heavy ? ld_agent(a.shv + (tile < ntiles ? tile : 0) * kTileRows + (t & (kTileRows - 1))) : 0.0f;
       // h records of every route -> LDS (every load issued before the first is used)
       unsigned *hrec = (unsigned *)(S.u + dl.hrec);  // [K][ngi*8][12]
       float *part = (float *)(S.u + dl.part);        // [K][kW][16]
@@ -1897,7 +1952,7 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           int dot = 0;
 #pragma unroll
           for (int w = 0; w < kW; w++) dot += shp[w * 16 + t];
-          const float shv = (float)dot * dsr * shx;
+          const float shv = heavy ? hshv : (float)dot * dsr * shx;
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
@@ -1999,6 +2054,7 @@ constexpr size_t kRecRegion = ((size_t)(kStackMaxE + 1) * 16 + 255) & ~(size_t)2
 constexpr size_t kExRegion = ((size_t)kStackMaxE * 4 + 255) & ~(size_t)255;          // exact logits
 constexpr size_t kStateRegion = 256;                                                  // call state
 constexpr size_t kHsRegion = (size_t)kStackMaxIsh * 8;                                 // shared hidden vector
+constexpr size_t kShvRegion = (size_t)2048 * kNch * 4;                                 // paired shared down values
 
 static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   // device scratch: records, exact logits, h records; per layer and parity:
@@ -2018,7 +2074,7 @@ static int stack_prepare(ColiCuda *ctx, int n, const ColiMoeShape &s) {
   }
   const int ngi = (s.intermediate + kGroup - 1) / kGroup;
   const size_t scratch =
-      kRecRegion + kExRegion + kStateRegion + kHsRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
+      kRecRegion + kExRegion + kStateRegion + kHsRegion + kShvRegion + (size_t)s.topk * ngi * 8 * kRecWords * 4;
   const void *before = ctx->scratch[kScrStack];
   if (ensure_scratch(ctx, kScrStack, scratch, "MoE stack scratch allocation")) return -1;
   if (ctx->scratch[kScrStack] != before) {
@@ -2139,7 +2195,8 @@ int stack_step(ColiCuda *ctx, ColiMoeLayer *const *layers, int n, float *y, size
   a.rec = (double *)scr;
   a.ex = (float *)(scr + kRecRegion);
   a.hs = (unsigned long long *)(scr + kRecRegion + kExRegion + kStateRegion);
-  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kHsRegion);
+  a.shv = (float *)(scr + kRecRegion + kExRegion + kStateRegion + kHsRegion);
+  a.hd = (unsigned *)(scr + kRecRegion + kExRegion + kStateRegion + kHsRegion + kShvRegion);
   const size_t acc_words = 2 * (size_t)kStackMaxIsh;
   a.bars = (unsigned *)ctx->stack_sync;
   a.acc = (unsigned long long *)((unsigned *)ctx->stack_sync + (size_t)ctx->stack_cap_layers * 2 * kBars * kBarWords);
