@@ -251,6 +251,11 @@ constexpr int kShSplit = 4, kShSplitTokens = SW_SH_SPLIT_TOKENS;
 struct Work {
   int T, H, E, K, I, Ish, ngh, ngi, Hp, Ip;
   int itok;  // tokens per bucketing item: 8 (one MFMA column set) or kWideTokens
+  // 1 when the step returns no routes: a certified set of K experts is taken
+  // in the order of its bounds when they cannot settle it (the set and the
+  // weights are exact either way; only the combine's rounding order depends
+  // on the order)
+  int order_free;
   // prep
   signed char *xq; float *sx;
   signed char *xd1, *xd2; float4 *xgp;
@@ -905,13 +910,22 @@ __global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned
     const double margin = 0x1p-20 * (1.0 + fabs(a.x) + fabs(b.x) + 2.0 * fabs(mx));
     pair = (a.x - a.y) - (b.x + b.y) > margin;
   }
-  bool ok = mode == 0 && w.K <= w.E && __all(pair);
-  const double2 aK = cv[w.K - 1];
-  if (ok && upi >= 0) {
-    const double margin = 0x1p-20 * (1.0 + fabs(aK.x) + fabs(up) + 2.0 * fabs(mx));
-    ok = (aK.x - aK.y) - up > margin;
+  bool ok = mode == 0 && w.K <= w.E && (w.order_free || __all(pair));
+  // the lowest lower bound among the K and its candidate's logit (the K-th
+  // candidate's when every pair is certified; any of them when the order is
+  // taken as it is)
+  double klo = lane < w.K ? cv[lane].x - cv[lane].y : __builtin_huge_val();
+  double kax = lane < w.K ? fabs(cv[lane].x) : 0.0;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    klo = fmin(klo, __shfl_xor(klo, o, 64));
+    kax = fmax(kax, __shfl_xor(kax, o, 64));
   }
-  if (ok) ok = (aK.x - aK.y) - (mx + cv[0].y) > -80.0;
+  if (ok && upi >= 0) {
+    const double margin = 0x1p-20 * (1.0 + kax + fabs(up) + 2.0 * fabs(mx));
+    ok = klo - up > margin;
+  }
+  if (ok) ok = klo - (mx + cv[0].y) > -80.0;
   int verdict = ok ? 1 : 0;
   double lo = 0.0;
   if (ok) {
@@ -2871,6 +2885,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   }
   Work w;
   if (prepare(ctx, L, tokens, w)) return -1;
+  w.order_free = route_idx == nullptr && route_weight == nullptr;
   hipStream_t st = ctx->stream;
   int T = tokens;
   mark(ctx, 0);
