@@ -344,9 +344,25 @@ __device__ __forceinline__ unsigned pack_i8x4(int a, int b, int c, int d) {
   return (unsigned)(a & 255) | ((unsigned)(b & 255) << 8) | ((unsigned)(c & 255) << 16) | ((unsigned)d << 24);
 }
 
+// The shared-expert gate sigmoid(x . g) of token t from the block's fp64
+// partial dots (every product exact, one fp64 rounding per sum): wave sums,
+// then thread 0 adds the 16 waves' in wave order.  The gate scales the shared
+// expert's output, which is compared within the output tolerance.
+__device__ __forceinline__ void block_gate(Work &w, int t, double d, double *redd) {
+  d = wave_sum_dpp(d);
+  if ((threadIdx.x & 63) == 0) redd[threadIdx.x >> 6] = d;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double L = 0.0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) L += redd[i];
+    w.sgate[t] = sigmoid_ref((float)L);
+  }
+}
+
 template <int C>
-__global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x) {
+__global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const float *sgate_row) {
   __shared__ float red[16];
+  __shared__ double redd[16];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const float *xt = x + (size_t)t * w.H;
   if (t == 0 && tid == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
@@ -362,6 +378,19 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x) {
     if (i < nq) v[c] = al ? *(const float4 *)(xt + 4 * i) : make_float4(xt[4 * i], xt[4 * i + 1], xt[4 * i + 2], xt[4 * i + 3]);
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
   }
+  double gd = 0.0;
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int i = tid + 1024 * c;
+    if (i < nq) {
+      const float4 g = *(const float4 *)(sgate_row + 4 * i);
+      gd = __builtin_fma((double)v[c].x, (double)g.x, gd);
+      gd = __builtin_fma((double)v[c].y, (double)g.y, gd);
+      gd = __builtin_fma((double)v[c].z, (double)g.z, gd);
+      gd = __builtin_fma((double)v[c].w, (double)g.w, gd);
+    }
+  }
+  block_gate(w, t, gd, redd);
   // qrow_i8 (c/qwen.c:1696): s = max|x|/127 (at least 1e-12), q = rint(x/s)
   m = wave_max(m);
   if (lane == 0) red[tid >> 6] = m;
@@ -407,10 +436,14 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x) {
 
 // Any row length: quantize_digits and qrow_i8_block read the row from memory.
 // grid T, 1024 threads.
-__global__ void k_prep_x_any(Work w, const float *x) {
+__global__ void k_prep_x_any(Work w, const float *x, const float *sgate_row) {
   __shared__ float red[16];
+  __shared__ double redd[16];
   int t = blockIdx.x;
   const float *xt = x + (size_t)t * w.H;
+  double gd = 0.0;
+  for (int i = threadIdx.x; i < w.H; i += blockDim.x) gd = __builtin_fma((double)xt[i], (double)sgate_row[i], gd);
+  block_gate(w, t, gd, redd);
   if (t == 0 && threadIdx.x == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
   if (threadIdx.x == 0) w.udone[t] = w.fdone[t] = 0;
   float s = qrow_i8_block(xt, w.H, w.xq + (size_t)t * w.H, red);
@@ -424,59 +457,65 @@ __global__ void k_prep_x_any(Work w, const float *x) {
 // tail FMA).  Each step's rounding is at most u*|partial| (u = 2^-24), each
 // product's at most u*|x*w|, so |err| <= u*(sum|x w| + sum_k |S_k|)*(1+uH).
 // Lane j owns the contiguous chunk j of the row; the prefix sums S_k are the
-// chunk offset O_j plus the local prefix, bounded by |O_j| + |local|.
-// Row E is the shared-expert gate row.  grid (ceil((E+1)/4), T), 256 threads.
+// chunk offset O_j plus the local prefix, bounded by |O_j| + |local|.  L and
+// the prefix sums are fp64 (every product exact); sum|x w| is an fp32 sum of
+// non-negative terms per lane, at most gamma_n (n = chunk length) below the
+// exact one, so it is scaled by 1 + 2^-23 n.  grid (ceil(E/4), T), 256 threads.
 // ---------------------------------------------------------------------------
-__global__ void k_router_bounds(Work w, const float *x, const float *router, const float *sgate_row) {
+__device__ __forceinline__ double router_bound(double A, double Pb) {
+  const double u = 0x1p-24;
+  return u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
+}
+
+__global__ void k_router_bounds(Work w, const float *x, const float *router) {
   int lane = threadIdx.x & 63;
   int e = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
-  if (e > w.E) return;
-  const float *row = e < w.E ? router + (size_t)e * w.H : sgate_row;
+  if (e >= w.E) return;
+  const float *row = router + (size_t)e * w.H;
   const float *xt = x + (size_t)t * w.H;
   int chunk = (w.H + 63) / 64;
   int i0 = lane * chunk, i1 = min(i0 + chunk, w.H);
-  double lp = 0.0, pa = 0.0, aa = 0.0;
+  double lp = 0.0, pa = 0.0;
+  float aa = 0.0f;
   for (int i = i0; i < i1; i++) {
-    double xd = (double)xt[i], wd = (double)row[i];
-    lp = __builtin_fma(xd, wd, lp);
-    aa = __builtin_fma(fabs(xd), fabs(wd), aa);
+    const float xf = xt[i], wf = row[i];
+    lp = __builtin_fma((double)xf, (double)wf, lp);
+    aa = __builtin_fmaf(fabsf(xf), fabsf(wf), aa);
     pa += fabs(lp);
   }
   double off = wave_exclusive_scan(lp, lane);
   double L = wave_sum(lp);
   double Pb = wave_sum((double)(i1 > i0 ? i1 - i0 : 0) * fabs(off) + pa);
-  double A = wave_sum(aa);
-  if (lane == 0) {
-    const double u = 0x1p-24;
-    double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
-    w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, B);
-    if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
-  }
+  double A = wave_sum((double)aa) * (1.0 + 0x1p-23 * chunk);
+  if (lane == 0) w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, router_bound(A, Pb));
 }
 
-// The same per-(token, row) arithmetic as k_router_bounds (lane j owns the
-// contiguous chunk j of CH = H/64 elements, same fma order, same wave
-// reductions, so L and B are bit-identical), arranged for many tokens: wave w
-// of a block holds router row e = 8*blockIdx.x + w in registers, read once,
-// and walks the block's tokens.  The tokens' activations are staged in LDS
-// kRbRound at a time, lane-major with one pad word per lane (pitch CH+1), so
-// lane j's reads of its chunk fall in distinct banks and the staging writes of
-// consecutive elements stay consecutive.  Row E is the shared-expert gate row.
-// grid (ceil((E+1)/8), ceil(T/tokens_per_block)), 512 threads, dynamic LDS
-// kRbRound*64*(CH+1) floats.  Requires x 16-byte aligned.
+// The bound of k_router_bounds (lane j owns the contiguous chunk j of CH =
+// H/64 elements, same per-lane fma order), arranged for many tokens: wave w of
+// a block holds router row e = RB*blockIdx.x + w in registers, read once, and
+// walks the block's tokens kRbRound at a time.  A round's tokens share each
+// element's conversion of the row value and run as kRbRound independent fma
+// chains, element-major, so the chains hide each other's latency.
+//
+// A round's activations reach LDS by global->LDS copies, all in flight at
+// once.  Lane j reads its chunk as float4s; the chunk's 16-byte units are
+// stored XOR-swizzled (unit q of chunk j at position q ^ (j & m), m = min(7,
+// CH/4 - 1)), so the eight lanes of a 128-bit LDS pass hit distinct banks.
+// grid (ceil(E/RB), ceil(T/tokens_per_block)), 64*RB threads, dynamic LDS
+// kRbRound*H floats.  Requires x 16-byte aligned, CH % 4 == 0.
 constexpr int kRbRound = 4;
-template <int CH>
-__global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float *x, const float *router,
-                                                             const float *sgate_row, int tokens_per_block) {
-  extern __shared__ float rb_xs[];  // [kRbRound][64 * (CH + 1)]
-  constexpr int P = CH + 1, H = 64 * CH;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = blockIdx.x * 8 + wave;
-  const bool live = e <= w.E;
+template <int CH, int RB>
+__global__ __launch_bounds__(64 * RB) __attribute__((amdgpu_waves_per_eu(4))) void k_router_bounds_tiled(
+    Work w, const float *x, const float *router, int tokens_per_block) {
+  extern __shared__ float4 rb_xs4[];  // [kRbRound][H / 4], swizzled within chunks
+  static_assert(CH % 4 == 0 && (CH & (CH - 1)) == 0, "chunks of a power of two of float4s");
+  constexpr unsigned H = 64 * CH, U = CH / 4, M = U < 8 ? U - 1 : 7, HU = H / 4;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e = blockIdx.x * RB + wave;
+  const bool live = e < w.E;
   float wr[CH];
   if (live) {
-    const float *row = e < w.E ? router + (size_t)e * H : sgate_row;
-    const float4 *r4 = (const float4 *)(row + lane * CH);
+    const float4 *r4 = (const float4 *)(router + (size_t)e * H + lane * CH);
 #pragma unroll
     for (int c = 0; c < CH / 4; c++) {
       float4 v = r4[c];
@@ -486,52 +525,77 @@ __global__ __launch_bounds__(512) void k_router_bounds_tiled(Work w, const float
       wr[4 * c + 3] = v.w;
     }
   }
+  const unsigned sw16 = (unsigned)(lane & M) << 4;  // this lane's read swizzle, bytes
   const int t0 = blockIdx.y * tokens_per_block, t1 = min(t0 + tokens_per_block, w.T);
   for (int tb = t0; tb < t1; tb += kRbRound) {
-    const int ng = min(kRbRound, t1 - tb);
+    const unsigned ng = min(kRbRound, t1 - tb);
     __syncthreads();  // the previous round's reads are done
-    for (int k = threadIdx.x * 4; k < ng * H; k += 512 * 4) {
-      const int g = k / H, kk = k - g * H;
-      const float4 v = *(const float4 *)(x + (size_t)(tb + g) * H + kk);
-      float *d = rb_xs + g * 64 * P + (kk / CH) * P + (kk % CH);  // CH % 4 == 0: one chunk
-      d[0] = v.x;
-      d[1] = v.y;
-      d[2] = v.z;
-      d[3] = v.w;
+    // LDS unit u (a wave's 64 consecutive units per copy) of token g = u / HU
+    // holds element 4 q of chunk j: uu = u mod HU, j = uu / U, q = uu mod U ^ (j & M)
+    for (unsigned u0 = wave * 64; u0 < ng * HU; u0 += 64 * RB) {  // wave-uniform
+      const unsigned u = u0 + lane, g = u / HU, uu = u % HU, j = uu / U, q = (uu % U) ^ (j & M);
+      dma_b128(x + (size_t)(tb + g) * H + j * CH + 4 * q, lds_addr(rb_xs4 + u0));
     }
+    wait_dma();
     __syncthreads();
     if (!live) continue;
-    // the round's tokens unrolled, so that their independent reductions
-    // interleave
+    // the row is converted per round, not hoisted out of the round loop (a
+    // double copy would take 2*CH registers): opaque to the compiler from here
+#pragma unroll
+    for (int c = 0; c < CH; c++) asm volatile("" : "+v"(wr[c]));
+    // rounds of fewer tokens compute on stale activations and store nothing
+    double lp[kRbRound], pa[kRbRound];
+    float aa[kRbRound];
 #pragma unroll
     for (int g = 0; g < kRbRound; g++) {
-      if (g >= ng) break;
-      const float *xl = rb_xs + g * 64 * P + lane * P;
-      double lp = 0.0, pa = 0.0, aa = 0.0;
+      lp[g] = pa[g] = 0.0;
+      aa[g] = 0.0f;
+    }
+    const char *xs = (const char *)rb_xs4 + lane * CH * 4;  // the lane's chunk of token 0
+    float4 xv[kRbRound], xn[kRbRound];
 #pragma unroll
-      for (int c = 0; c < CH; c++) {
-        // converted per token: a hoisted f64 copy of the row would double its
-        // registers and halve the occupancy
-        float wf = wr[c];
-        asm volatile("" : "+v"(wf));
-        double xd = (double)xl[c], wd = (double)wf;
-        lp = __builtin_fma(xd, wd, lp);
-        aa = __builtin_fma(fabs(xd), fabs(wd), aa);
-        pa += fabs(lp);
+    for (int g = 0; g < kRbRound; g++) xn[g] = *(const float4 *)(xs + sw16 + g * H * 4);
+#pragma unroll
+    for (int c0 = 0; c0 < CH; c0 += 4) {
+      // one step of prefetch: the next reads' address depends (opaquely) on
+      // every chain's step before, so the compiler neither hoists every read
+      // of the unrolled loop to the top (which spills) nor sinks a chain's
+      // arithmetic to the end
+      static_assert(kRbRound == 4, "the dependency names four chains");
+      unsigned dep = 0;
+      if (c0 >= 4)
+        asm("v_mov_b32 %0, 0"
+            : "=v"(dep)
+            : "v"(lp[0]), "v"(lp[1]), "v"(lp[2]), "v"(lp[3]), "v"(pa[0]), "v"(pa[1]), "v"(pa[2]), "v"(pa[3]),
+              "v"(aa[0]), "v"(aa[1]), "v"(aa[2]), "v"(aa[3]));
+      const unsigned nx = ((unsigned)(c0 + 4) << 2 ^ sw16) + dep;  // next step's unit, bytes
+#pragma unroll
+      for (int g = 0; g < kRbRound; g++) {
+        xv[g] = xn[g];
+        if (c0 + 4 < CH) xn[g] = *(const float4 *)(xs + nx + g * H * 4);
       }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float wf = wr[c0 + q];
+        const double wd = (double)wf;
+#pragma unroll
+        for (int g = 0; g < kRbRound; g++) {
+          const float xf = q == 0 ? xv[g].x : q == 1 ? xv[g].y : q == 2 ? xv[g].z : xv[g].w;
+          lp[g] = __builtin_fma((double)xf, wd, lp[g]);
+          aa[g] = __builtin_fmaf(fabsf(xf), fabsf(wf), aa[g]);
+          pa[g] += fabs(lp[g]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < kRbRound; g++) {
       // DPP reductions: the inclusive scan's last lane is the logit
-      const double inc = wave_incl_scan_dpp(lp);
-      const double off = inc - lp;
+      const double inc = wave_incl_scan_dpp(lp[g]);
+      const double off = inc - lp[g];
       const double L = readlane_d63(inc);
-      const double Pb = wave_sum_dpp((double)CH * fabs(off) + pa);
-      const double A = wave_sum_dpp(aa);
-      if (lane == 0) {
-        const int t = tb + g;
-        const double u = 0x1p-24;
-        double B = u * (A + Pb) * (1.0 + 0x1p-10) + 1e-12 * A + 1e-36;
-        w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, B);
-        if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
-      }
+      const double Pb = wave_sum_dpp((double)CH * fabs(off) + pa[g]);
+      const double A = wave_sum_dpp((double)aa[g]) * (1.0 + 0x1p-23 * CH);
+      if (lane == 0 && g < (int)ng) w.lb[(size_t)(tb + g) * (w.E + 1) + e] = make_double2(L, router_bound(A, Pb));
     }
   }
 }
@@ -575,17 +639,16 @@ __device__ __forceinline__ double gemm_bound_factor(int H) {
 // loads float4s; the result holds token t0 + (l >> 4) + 4 v, row e0 + l % 16
 // at lane l, item v (the f64 16x16x4 output layout: D[(l >> 4) + 4 v][l % 16]).
 // The same loads give ||x_t|| and ||w_e|| (fp64 sums of squares).
-// grid (ceil((E+1)/16), ceil(T/16)), 256 threads.  H % 64 == 0, x 16-byte aligned.
-__global__ __launch_bounds__(256) void k_router_gemm(Work w, const float *x, const float *router,
-                                                     const float *sgate_row) {
+// grid (ceil(E/16), ceil(T/16)), 256 threads.  H % 64 == 0, x 16-byte aligned.
+__global__ __launch_bounds__(256) void k_router_gemm(Work w, const float *x, const float *router) {
   __shared__ double s_acc[4][4][64];
   __shared__ double s_nx[4][64], s_nw[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
   const int H = w.H, kq = H / 4;
-  const int ta = min(t0 + (lane & 15), w.T - 1), eb = min(e0 + (lane & 15), w.E);
+  const int ta = min(t0 + (lane & 15), w.T - 1), eb = min(e0 + (lane & 15), w.E - 1);
   const float *xa = x + (size_t)ta * H + wave * kq + 4 * (lane >> 4);
-  const float *wb = (eb < w.E ? router + (size_t)eb * H : sgate_row) + wave * kq + 4 * (lane >> 4);
+  const float *wb = router + (size_t)eb * H + wave * kq + 4 * (lane >> 4);
   v4d acc = {0.0, 0.0, 0.0, 0.0};
   double qa = 0.0, qb = 0.0;
 #pragma unroll 4
@@ -611,7 +674,7 @@ __global__ __launch_bounds__(256) void k_router_gemm(Work w, const float *x, con
   __syncthreads();
   if (wave != 0) return;
   const int e = e0 + (lane & 15);
-  if (e > w.E) return;
+  if (e >= w.E) return;
   const double nw = sqrt(((s_nw[0][lane] + s_nw[1][lane]) + s_nw[2][lane]) + s_nw[3][lane]);
   const double f = gemm_bound_factor(H) * nw;
 #pragma unroll
@@ -621,7 +684,6 @@ __global__ __launch_bounds__(256) void k_router_gemm(Work w, const float *x, con
     const double L = ((s_acc[0][v][lane] + s_acc[1][v][lane]) + s_acc[2][v][lane]) + s_acc[3][v][lane];
     const double nx = sqrt(((s_nx[0][i] + s_nx[1][i]) + s_nx[2][i]) + s_nx[3][i]);
     w.lb[(size_t)t * (w.E + 1) + e] = make_double2(L, f * nx + 1e-36);
-    if (e == w.E) w.sgate[t] = sigmoid_ref((float)L);
   }
 }
 
@@ -2726,17 +2788,48 @@ static int set_lds(const void *fn, size_t bytes) {
   return e == hipSuccess ? 0 : fail_hip("hipFuncSetAttribute", e);
 }
 
+// Block shape of the tiled bounds kernel: RB rows (waves) by tpb tokens.
+// Every wave-round (one row, kRbRound tokens) costs about the same, so the
+// shape that gives the busiest SIMD the fewest wave-rounds wins, then the one
+// whose blocks all stay resident (two per compute unit: LDS), then the one
+// with the most blocks (latency hiding).  S397 (512 rows): 8 tokens take 4-row
+// blocks, one per compute unit; 32 tokens 8-row blocks of 4 tokens, two per
+// compute unit.
+struct RbShape {
+  int rb, tpb, nb;
+};
+static RbShape rb_shape(int E, int T, int cus) {
+  RbShape best = {0, 0, 0};
+  long long best_w = 0;
+  bool best_over = true;
+  for (int rb = 8; rb >= 4; rb -= 4)
+    for (int tpb = kRbRound; tpb < T + kRbRound; tpb += kRbRound) {
+      const int nb = (E + rb - 1) / rb * ((T + tpb - 1) / tpb);
+      const long long wr = (long long)((nb + cus - 1) / cus) * (rb / 4) * (tpb / kRbRound);
+      const bool over = nb > 2 * cus;
+      const bool better = best.rb == 0 || wr < best_w || (wr == best_w && best_over && !over) ||
+                          (wr == best_w && over == best_over && !over && nb > best.nb);
+      if (better) {
+        best = {rb, tpb, nb};
+        best_w = wr;
+        best_over = over;
+      }
+    }
+  return best;
+}
+
 template <int CH>
 static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
-  const size_t lds = (size_t)kRbRound * 64 * (CH + 1) * 4;
-  if (set_lds((const void *)k_router_bounds_tiled<CH>, lds)) return -1;
-  // about 1024 blocks; a block's rows are read once per block
-  const int bx = (w.E + 1 + 7) / 8;
-  int tpb = (int)(((long long)w.T * bx + 1023) / 1024);
-  tpb = (tpb + kRbRound - 1) / kRbRound * kRbRound;
-  if (tpb < kRbRound) tpb = kRbRound;
-  const int by = (w.T + tpb - 1) / tpb;
-  k_router_bounds_tiled<CH><<<dim3(bx, by), 512, lds, ctx->stream>>>(w, x, L->router, L->sgate_row, tpb);
+  const size_t lds = (size_t)kRbRound * 64 * CH * 4;
+  const RbShape sh = rb_shape(w.E, w.T, ctx->sm_count > 0 ? ctx->sm_count : 256);
+  const dim3 grid((w.E + sh.rb - 1) / sh.rb, (w.T + sh.tpb - 1) / sh.tpb);
+  if (sh.rb == 8) {
+    if (set_lds((const void *)k_router_bounds_tiled<CH, 8>, lds)) return -1;
+    k_router_bounds_tiled<CH, 8><<<grid, 512, lds, ctx->stream>>>(w, x, L->router, sh.tpb);
+  } else {
+    if (set_lds((const void *)k_router_bounds_tiled<CH, 4>, lds)) return -1;
+    k_router_bounds_tiled<CH, 4><<<grid, 256, lds, ctx->stream>>>(w, x, L->router, sh.tpb);
+  }
   return 0;
 }
 
@@ -2751,18 +2844,18 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
   hipStream_t st = ctx->stream;
   const int hp4 = w.ngh * 128 / 4;  // float4 chunks of the padded row
   if (hp4 <= 1024)
-    k_prep_x<1><<<w.T, 1024, 0, st>>>(w, x);
+    k_prep_x<1><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
   else if (hp4 <= 2048)
-    k_prep_x<2><<<w.T, 1024, 0, st>>>(w, x);
+    k_prep_x<2><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
   else if (hp4 <= 4096)
-    k_prep_x<4><<<w.T, 1024, 0, st>>>(w, x);
+    k_prep_x<4><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
   else if (hp4 <= 8192)
-    k_prep_x<8><<<w.T, 1024, 0, st>>>(w, x);
+    k_prep_x<8><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
   else
-    k_prep_x_any<<<w.T, 1024, 0, st>>>(w, x);
+    k_prep_x_any<<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
   int rc = 1;  // 1: shape or alignment outside the tiled router kernel
   if (w.T >= kRouterGemmTokens && w.H % 64 == 0 && ((uintptr_t)x & 15) == 0) {
-    k_router_gemm<<<dim3((w.E + 1 + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router, L->sgate_row);
+    k_router_gemm<<<dim3((w.E + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router);
     k_router_refine<<<w.T, 256, (size_t)64 * (w.H / 64 + 1) * 4, st>>>(w, x, L->router);
     rc = 0;
   } else if (((uintptr_t)x & 15) == 0) switch (w.H) {
@@ -2774,7 +2867,7 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
       default: break;
     }
   if (rc < 0) return -1;
-  if (rc > 0) k_router_bounds<<<dim3((w.E + 1 + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router, L->sgate_row);
+  if (rc > 0) k_router_bounds<<<dim3((w.E + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router);
   if (w.E <= 512)
     k_certify_wave<8><<<(w.T + 3) / 4, 256, 0, st>>>(w, L->router_mode, L->stats);
   else if (w.E <= 1024)
