@@ -359,21 +359,32 @@ __device__ __forceinline__ void block_gate(Work &w, int t, double d, double *red
   }
 }
 
-template <int C>
-__global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const float *sgate_row) {
-  __shared__ float red[16];
-  __shared__ double redd[16];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+// The certification's lists and per-token chain counters start the step at
+// zero (the certification appends to the lists).
+__device__ __forceinline__ void reset_counters(Work &w, int t) {
+  if (threadIdx.x == 0) {
+    if (t == 0) *w.ucount = *w.fcount = 0;
+    w.udone[t] = w.fdone[t] = 0;
+  }
+}
+
+// Token t's activation forms, by a block of NT threads (C float4s each,
+// C * NT >= the padded row's float4s): the row quantisation, the two-digit
+// groups, the shared gate; RESET: the step's certification counters too.
+template <int C, int NT, bool RESET>
+__device__ __forceinline__ void prep_token(Work &w, const float *x, const float *sgate_row, int t, float *red,
+                                           double *redd) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
   const float *xt = x + (size_t)t * w.H;
-  if (t == 0 && tid == 0) *w.ucount = *w.fcount = 0;  // the certification appends to them
-  if (tid == 0) w.udone[t] = w.fdone[t] = 0;
+  if (RESET) reset_counters(w, t);
   const int nq = w.H / 4, nqp = w.ngh * 32;  // float4 chunks of the row, of the padded row
   const bool al = ((uintptr_t)xt & 15) == 0;
   float4 v[C];
   float m = 0.0f;
 #pragma unroll
   for (int c = 0; c < C; c++) {
-    const int i = tid + 1024 * c;
+    const int i = tid + NT * c;
     v[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (i < nq) v[c] = al ? *(const float4 *)(xt + 4 * i) : make_float4(xt[4 * i], xt[4 * i + 1], xt[4 * i + 2], xt[4 * i + 3]);
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
@@ -381,7 +392,7 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const f
   double gd = 0.0;
 #pragma unroll
   for (int c = 0; c < C; c++) {
-    const int i = tid + 1024 * c;
+    const int i = tid + NT * c;
     if (i < nq) {
       const float4 g = *(const float4 *)(sgate_row + 4 * i);
       gd = __builtin_fma((double)v[c].x, (double)g.x, gd);
@@ -397,7 +408,7 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const f
   __syncthreads();
   float a = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; i++) a = fmaxf(a, red[i]);
+  for (int i = 0; i < NW; i++) a = fmaxf(a, red[i]);
   float sx = a / 127.0f;
   if (sx < 1e-12f) sx = 1e-12f;
   const float inv = 1.0f / sx;
@@ -406,12 +417,12 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const f
   unsigned *d1 = (unsigned *)(w.xd1 + (size_t)t * w.Hp), *d2 = (unsigned *)(w.xd2 + (size_t)t * w.Hp);
 #pragma unroll
   for (int c = 0; c < C; c++) {
-    const int i = tid + 1024 * c;
+    const int i = tid + NT * c;
     if (i < nq)
       xq[i] = pack_i8x4((int)__builtin_rintf(v[c].x * inv), (int)__builtin_rintf(v[c].y * inv),
                         (int)__builtin_rintf(v[c].z * inv), (int)__builtin_rintf(v[c].w * inv));
     // two digits per value of the group (half-wave), as quantize_digits
-    if (i < nqp) {  // uniform over the half-wave: nqp and 1024 are multiples of 32
+    if (i < nqp) {  // uniform over the half-wave: nqp and NT are multiples of 32
       const float amax = half_wave_max(fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
       const float A = amax / 127.0f, B = A / 254.0f;
       int q1[4] = {0, 0, 0, 0}, q2[4] = {0, 0, 0, 0};
@@ -432,6 +443,13 @@ __global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const f
       if ((lane & 31) == 0) w.xgp[(size_t)t * w.ngh + i / 32] = make_float4(A, B, __int_as_float(Q1), __int_as_float(Q2));
     }
   }
+}
+
+template <int C>
+__global__ __launch_bounds__(1024) void k_prep_x(Work w, const float *x, const float *sgate_row) {
+  __shared__ float red[16];
+  __shared__ double redd[16];
+  prep_token<C, 1024, true>(w, x, sgate_row, blockIdx.x, red, redd);
 }
 
 // Any row length: quantize_digits and qrow_i8_block read the row from memory.
@@ -501,8 +519,9 @@ __global__ void k_router_bounds(Work w, const float *x, const float *router) {
 // once.  Lane j reads its chunk as float4s; the chunk's 16-byte units are
 // stored XOR-swizzled (unit q of chunk j at position q ^ (j & m), m = min(7,
 // CH/4 - 1)), so the eight lanes of a 128-bit LDS pass hit distinct banks.
-// grid (ceil(E/RB), ceil(T/tokens_per_block)), 64*RB threads, dynamic LDS
-// kRbRound*H floats.  Requires x 16-byte aligned, CH % 4 == 0.
+// The first column of blocks also resets the certification counters of its
+// tokens.  grid (ceil(E/RB), ceil(T/tokens_per_block)), 64*RB threads, dynamic
+// LDS kRbRound*H floats.  Requires x 16-byte aligned, CH % 4 == 0.
 constexpr int kRbRound = 4;
 template <int CH, int RB>
 __global__ __launch_bounds__(64 * RB) __attribute__((amdgpu_waves_per_eu(4))) void k_router_bounds_tiled(
@@ -510,6 +529,9 @@ __global__ __launch_bounds__(64 * RB) __attribute__((amdgpu_waves_per_eu(4))) vo
   extern __shared__ float4 rb_xs4[];  // [kRbRound][H / 4], swizzled within chunks
   static_assert(CH % 4 == 0 && (CH & (CH - 1)) == 0, "chunks of a power of two of float4s");
   constexpr unsigned H = 64 * CH, U = CH / 4, M = U < 8 ? U - 1 : 7, HU = H / 4;
+  if (blockIdx.x == 0)
+    for (int t = blockIdx.y * tokens_per_block; t < min((int)(blockIdx.y + 1) * tokens_per_block, w.T); t++)
+      reset_counters(w, t);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int e = blockIdx.x * RB + wave;
   const bool live = e < w.E;
@@ -897,10 +919,20 @@ __device__ __forceinline__ unsigned order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-template <int NV>
-__global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned long long *stats) {
+// PC > 0: the blocks after the certification's form the activations of one
+// token each (prep_token with C = PC), independent of the certification; the
+// counters were reset by the bounds kernel.  grid ceil(T/4) (+ T), 256 threads.
+template <int NV, int PC>
+__global__ __launch_bounds__(256) void k_certify_wave(Work w, int mode, unsigned long long *stats, const float *x,
+                                                      const float *sgate_row) {
   __shared__ int cand_s[4][kMaxTopK + 1];
   __shared__ double2 cv_s[4][kMaxTopK + 1];  // the candidates' (L, B)
+  if (PC > 0 && (int)blockIdx.x >= (w.T + 3) / 4) {
+    __shared__ float red[4];
+    __shared__ double redd[4];
+    prep_token<(PC > 0 ? PC : 1), 256, false>(w, x, sgate_row, blockIdx.x - (w.T + 3) / 4, red, redd);
+    return;
+  }
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wv;
   if (t >= w.T) return;
@@ -2840,25 +2872,19 @@ static int router_bounds_tiled(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const fl
 #endif
 constexpr int kRouterGemmTokens = SW_ROUTER_GEMM_TOKENS;
 
+template <int NV, int PC>
+static void certify_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
+  k_certify_wave<NV, PC><<<(w.T + 3) / 4 + (PC > 0 ? w.T : 0), 256, 0, ctx->stream>>>(w, L->router_mode, L->stats, x,
+                                                                                       L->sgate_row);
+}
+
 static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x) {
   hipStream_t st = ctx->stream;
-  const int hp4 = w.ngh * 128 / 4;  // float4 chunks of the padded row
-  if (hp4 <= 1024)
-    k_prep_x<1><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
-  else if (hp4 <= 2048)
-    k_prep_x<2><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
-  else if (hp4 <= 4096)
-    k_prep_x<4><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
-  else if (hp4 <= 8192)
-    k_prep_x<8><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
-  else
-    k_prep_x_any<<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+  // the tiled bounds kernel resets the certification counters and the
+  // certification kernel forms the activations in blocks of its own; the
+  // other router paths take k_prep_x first
   int rc = 1;  // 1: shape or alignment outside the tiled router kernel
-  if (w.T >= kRouterGemmTokens && w.H % 64 == 0 && ((uintptr_t)x & 15) == 0) {
-    k_router_gemm<<<dim3((w.E + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router);
-    k_router_refine<<<w.T, 256, (size_t)64 * (w.H / 64 + 1) * 4, st>>>(w, x, L->router);
-    rc = 0;
-  } else if (((uintptr_t)x & 15) == 0) switch (w.H) {
+  if (w.T < kRouterGemmTokens && ((uintptr_t)x & 15) == 0 && w.E <= 1024) switch (w.H) {
       case 256: rc = router_bounds_tiled<4>(ctx, L, w, x); break;
       case 512: rc = router_bounds_tiled<8>(ctx, L, w, x); break;
       case 1024: rc = router_bounds_tiled<16>(ctx, L, w, x); break;
@@ -2867,13 +2893,41 @@ static int route_launch(ColiCuda *ctx, ColiMoeLayer *L, Work &w, const float *x)
       default: break;
     }
   if (rc < 0) return -1;
-  if (rc > 0) k_router_bounds<<<dim3((w.E + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router);
-  if (w.E <= 512)
-    k_certify_wave<8><<<(w.T + 3) / 4, 256, 0, st>>>(w, L->router_mode, L->stats);
-  else if (w.E <= 1024)
-    k_certify_wave<16><<<(w.T + 3) / 4, 256, 0, st>>>(w, L->router_mode, L->stats);
-  else
-    k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
+  if (rc == 0) {
+    // prep_token with 256 threads: C = padded row float4s / 256 = H / 1024
+    const bool e8 = w.E <= 512;
+    switch (w.H) {
+      case 256:
+      case 512:
+      case 1024: e8 ? certify_launch<8, 1>(ctx, L, w, x) : certify_launch<16, 1>(ctx, L, w, x); break;
+      case 2048: e8 ? certify_launch<8, 2>(ctx, L, w, x) : certify_launch<16, 2>(ctx, L, w, x); break;
+      default: e8 ? certify_launch<8, 4>(ctx, L, w, x) : certify_launch<16, 4>(ctx, L, w, x); break;
+    }
+  } else {
+    const int hp4 = w.ngh * 128 / 4;  // float4 chunks of the padded row
+    if (hp4 <= 1024)
+      k_prep_x<1><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+    else if (hp4 <= 2048)
+      k_prep_x<2><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+    else if (hp4 <= 4096)
+      k_prep_x<4><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+    else if (hp4 <= 8192)
+      k_prep_x<8><<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+    else
+      k_prep_x_any<<<w.T, 1024, 0, st>>>(w, x, L->sgate_row);
+    if (w.T >= kRouterGemmTokens && w.H % 64 == 0 && ((uintptr_t)x & 15) == 0) {
+      k_router_gemm<<<dim3((w.E + 15) / 16, (w.T + 15) / 16), 256, 0, st>>>(w, x, L->router);
+      k_router_refine<<<w.T, 256, (size_t)64 * (w.H / 64 + 1) * 4, st>>>(w, x, L->router);
+    } else {
+      k_router_bounds<<<dim3((w.E + 3) / 4, w.T), 256, 0, st>>>(w, x, L->router);
+    }
+    if (w.E <= 512)
+      certify_launch<8, 0>(ctx, L, w, x);
+    else if (w.E <= 1024)
+      certify_launch<16, 0>(ctx, L, w, x);
+    else
+      k_certify<<<w.T, 512, 0, st>>>(w, L->router_mode, L->stats);
+  }
   if (set_lds((const void *)k_exact_logits, (size_t)w.H * 4)) return -1;
   k_exact_logits<<<dim3(64, w.T < kUncertainSlots ? w.T : kUncertainSlots), 64, (size_t)w.H * 4, st>>>(
       w, x, L->router, L->stats);
