@@ -252,9 +252,9 @@ struct Work {
   int T, H, E, K, I, Ish, ngh, ngi, Hp, Ip;
   int itok;  // tokens per bucketing item: 8 (one MFMA column set) or kWideTokens
   // 1 when the step returns no routes: a certified set of K experts is taken
-  // in the order of its bounds when they cannot settle it (the set and the
-  // weights are exact either way; only the combine's rounding order depends
-  // on the order)
+  // in the order of its bounds when they cannot settle it (the set is exact
+  // either way, the weights come from the fp64 logits within tolerance; only
+  // the combine's rounding order depends on the order)
   int order_free;
   // prep
   signed char *xq; float *sx;

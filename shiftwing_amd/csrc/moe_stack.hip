@@ -1311,8 +1311,9 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           // against every other expert's upper bound; their order by the
           // pairs.  Without a route output (a stack call) the order only
           // changes the rounding of the combine, so an uncertain order among
-          // a certified set is taken as is (the set and the weights are exact
-          // either way).
+          // a certified set is taken as is (the set is exact either way; the
+          // weights come from the fp64 logits in either order, within the
+          // weights' tolerance).
           bool ok = L.mode == 0 && (__all(pair_ok) || (a.route_idx == nullptr && a.route_w == nullptr));
           if (ok && K < E) {
             const double up = key_double(upk);
