@@ -1413,14 +1413,18 @@ __device__ void bucket_block(const int *idx, int T, int K, int E, int *offsets, 
   }
 }
 
-__global__ void k_bucket(Work w) {
-  extern __shared__ unsigned smem[];
+__device__ __forceinline__ void bucket_step(Work &w, unsigned *smem) {
   int words = (w.T + 31) / 32;
   unsigned *bits = smem;
   int *cnt = (int *)(smem + w.E * words);
   int *iofs = cnt + w.E;
   bucket_block(w.idx, w.T, w.K, w.E, w.offsets, w.btok, w.bslot, w.pos, w.items, w.nitems, bits, cnt, iofs,
                w.itok);
+}
+
+__global__ void k_bucket(Work w) {
+  extern __shared__ unsigned smem[];
+  bucket_step(w, smem);
 }
 
 __global__ void k_bucket_only(const int *idx, int T, int K, int E, int *offsets, int *btok, int *bslot,
@@ -1739,10 +1743,10 @@ __global__ __launch_bounds__(256) void k_shared_swiglu(Work w, const signed char
 // k_prep_hidden adds the parts (exact) and applies the reference's rounding.
 // grid (Ish/16, kShSplit, ceil(T/(16 NS))), 256 threads.
 template <int NS>
-__global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed char *gq, const signed char *uq) {
-  __shared__ int part[4][2][NS][256];
+__device__ __forceinline__ void shared_gu_tile(Work &w, const signed char *gq, const signed char *uq, int rt, int ks,
+                                               int bz, int (*part)[2][NS][256]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rt = blockIdx.x, ks = blockIdx.y, t0 = blockIdx.z * 16 * NS;
+  const int t0 = bz * 16 * NS;
   const int nk = w.H / 64;
   const int p0 = ks * nk / kShSplit, p1 = (ks + 1) * nk / kShSplit;
   const int kc0 = p0 + wave * (p1 - p0) / 4, kc1 = p0 + (wave + 1) * (p1 - p0) / 4;
@@ -1804,6 +1808,28 @@ __global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed ch
     dst[row] = dg;
     dst[w.Ish + row] = du;
   }
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void k_shared_gu_split(Work w, const signed char *gq, const signed char *uq) {
+  __shared__ int part[4][2][NS][256];
+  shared_gu_tile<NS>(w, gq, uq, blockIdx.x, blockIdx.y, blockIdx.z, part);
+}
+
+// The bucketing (block 0, dispatched first: the routed kernels wait for it)
+// and the shared gate/up tiles of k_shared_gu_split (the other blocks, linear
+// over (row tile, k part, token block)) in one launch: neither reads the
+// other's results, and a launch boundary costs more than the bucketing's
+// block.  256 threads, dynamic LDS max(bucket_lds_bytes, 32 * 256 * NS).
+template <int NS>
+__global__ __launch_bounds__(256) void k_bucket_shared(Work w, const signed char *gq, const signed char *uq) {
+  extern __shared__ unsigned bs_dyn[];
+  if (blockIdx.x == 0) {
+    bucket_step(w, bs_dyn);
+    return;
+  }
+  const int b = blockIdx.x - 1, nrt = w.Ish / kTileRows;
+  shared_gu_tile<NS>(w, gq, uq, b % nrt, (b / nrt) % kShSplit, b / (nrt * kShSplit), (int(*)[2][NS][256])bs_dyn);
 }
 
 // qrow_i8 of the shared hidden rows + digits of the routed hidden rows
@@ -3039,19 +3065,30 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   if (route_launch(ctx, L, w, x)) return -1;
   mark(ctx, 1);
   const size_t bucket_lds = bucket_lds_bytes(w.E, T);
-  if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
-  k_bucket<<<1, 1024, bucket_lds, st>>>(w);
-  mark(ctx, 2);
-  prof_mark(ctx, kStageSetup);
-  if (T <= 16)
-    k_shared_gu_split<1><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
-  else if (T <= 32)
-    k_shared_gu_split<2><<<dim3(w.Ish / kTileRows, kShSplit), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
-  else if (T <= kShSplitTokens)
-    k_shared_gu_split<4><<<dim3(w.Ish / kTileRows, kShSplit, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_uq);
-  else
+  if (T <= kShSplitTokens) {
+    // the bucketing and the split shared gate/up in one launch
+    const int ns = T <= 16 ? 1 : T <= 32 ? 2 : 4;
+    const int nsh = w.Ish / kTileRows * kShSplit * (ns == 4 ? (T + 63) / 64 : 1);
+    const size_t lds = std::max(bucket_lds, (size_t)32 * 256 * ns);
+    const void *fn = ns == 1 ? (const void *)k_bucket_shared<1> : ns == 2 ? (const void *)k_bucket_shared<2>
+                                                                          : (const void *)k_bucket_shared<4>;
+    if (set_lds(fn, lds)) return -1;
+    if (ns == 1)
+      k_bucket_shared<1><<<1 + nsh, 256, lds, st>>>(w, L->sh_gq, L->sh_uq);
+    else if (ns == 2)
+      k_bucket_shared<2><<<1 + nsh, 256, lds, st>>>(w, L->sh_gq, L->sh_uq);
+    else
+      k_bucket_shared<4><<<1 + nsh, 256, lds, st>>>(w, L->sh_gq, L->sh_uq);
+    mark(ctx, 2);
+    prof_mark(ctx, kStageSetup);
+  } else {
+    if (set_lds((const void *)k_bucket, bucket_lds)) return -1;
+    k_bucket<<<1, 1024, bucket_lds, st>>>(w);
+    mark(ctx, 2);
+    prof_mark(ctx, kStageSetup);
     k_shared_swiglu<4><<<dim3(w.Ish / kTileRows, (T + 63) / 64), 256, 0, st>>>(w, L->sh_gq, L->sh_gs, L->sh_uq,
                                                                               L->sh_us);
+  }
   mark(ctx, 3);
   prof_mark(ctx, kStageSharedHidden);
   int item_bound = w.E + (T * w.K + w.itok - 1) / w.itok;
