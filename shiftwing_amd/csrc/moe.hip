@@ -1833,10 +1833,11 @@ __global__ __launch_bounds__(256) void k_bucket_shared(Work w, const signed char
 }
 
 // qrow_i8 of the shared hidden rows + digits of the routed hidden rows
-__global__ void k_prep_hidden(Work w, const float *gs, const float *us) {
-  __shared__ float red[16];
-  int b = blockIdx.x;
-  if (b < w.T) {
+// Token b's shared hidden row: the k parts of the split shared gate/up dots
+// (exact int32 sums) and h = silu(g)*u with the reference's rounding (as
+// k_shared_swiglu) when the step split them, then qrow_i8 of the row (hq,
+// shx).  By one block of any size.
+__device__ void prep_shared_hidden(Work &w, const float *gs, const float *us, int b, float *red) {
     if (w.shks > 0) {
       // the k parts of the shared gate/up dots (exact int32 sums), then
       // h = silu(g)*u with the reference's rounding (as k_shared_swiglu)
@@ -1876,6 +1877,13 @@ __global__ void k_prep_hidden(Work w, const float *gs, const float *us) {
     }
     float s = qrow_i8_block(w.hsh + (size_t)b * w.Ish, w.Ish, w.hq + (size_t)b * w.Ish, red);
     if (threadIdx.x == 0) w.shx[b] = s;
+}
+
+__global__ void k_prep_hidden(Work w, const float *gs, const float *us) {
+  __shared__ float red[16];
+  int b = blockIdx.x;
+  if (b < w.T) {
+    prep_shared_hidden(w, gs, us, b, red);
     return;
   }
   int p = b - w.T;
@@ -2474,13 +2482,31 @@ __device__ __forceinline__ void xcd_block(int lin, int nx, int ny, int &chunk, i
 // routed gate/up of wide items: h = silu(g)*u.  Block: kWideWaves waves x
 // kWideRt row tiles of I; a 1-D grid of nx = ceil(I/16 / (kWideWaves kWideRt))
 // chunks x ny item slots placed by xcd_block, dynamic LDS wide_lds_bytes(hg).
+//
+// A block's kWideWaves row tiles are one 128-value group of I, so the block
+// also forms the down kernel's activation digits of its group (as
+// quantize_digits: the group's maximum, two int8 digits per value, the digit
+// sums), the waves meeting in LDS for the group's maximum and sums; rows past
+// I are zero values.  The first nsb blocks (a multiple of 8, so that the
+// item blocks keep their XCD placement) form the shared expert's hidden rows
+// (prep_shared_hidden) of tokens 0..T-1 instead: k_prep_hidden's work, with
+// no launch of its own.
+static_assert(kWideWaves * kWideRt * kTileRows == kGroup, "a wide gate/up block is one digit group of I");
 template <int FMT>
-__global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertLayout xl, int hg, int nx, int ny) {
+__global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertLayout xl, int hg, int nx, int ny,
+                                                                 int nsb, const float *sh_gs, const float *sh_us) {
   extern __shared__ __align__(16) unsigned char wlds[];
+  __shared__ float s_red[16];
+  __shared__ float s_amax[kWideWaves][16];
+  __shared__ int s_q[kWideWaves][2][16];
+  if ((int)blockIdx.x < nsb) {
+    if ((int)blockIdx.x < w.T) prep_shared_hidden(w, sh_gs, sh_us, blockIdx.x, s_red);
+    return;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kb = lane >> 4;
   const int nrt = w.I / kTileRows;
   int chunk, slot;
-  xcd_block((int)blockIdx.x, nx, ny, chunk, slot);
+  xcd_block((int)blockIdx.x - nsb, nx, ny, chunk, slot);
   const int rt0 = (chunk * kWideWaves + wave) * kWideRt;
   const int n_items = *w.nitems;
   for (int it = slot; it < n_items; it += ny) {
@@ -2492,16 +2518,59 @@ __global__ __launch_bounds__(64 * kWideWaves) void k_gateup_wide(Work w, ExpertL
         mats, wlds, hg, rt0, nrt, w.ngh, rt0 < nrt, lane, acc, [&](int g0, int gn) {
           wide_stage(wlds, hg, g0, gn, w.ngh, w.Hp, w.xd1, w.xd2, w.xgp, w.btok, p0, cnt, FMT == 4 ? 8.0f : 4.0f);
         });
+    // h = silu(g)*u of the wave's 16 rows (4 a lane) for token lane % 16
+    // (zero past I: a wave without rows holds zero sums), then the group's
+    // digits for the down kernel
     const int tt = lane & 15;
-    if (tt < cnt && rt0 < nrt) {
+    float h[4];
+    float m = 0.0f;
 #pragma unroll
-      for (int rr = 0; rr < kWideRt; rr++) {
-        const int rt = rt0 + rr;
-        if (rt >= nrt) continue;
+    for (int r = 0; r < 4; r++) {
+      h[r] = silu_ref(acc[0][0][r]) * acc[0][1][r];
+      m = fmaxf(m, fabsf(h[r]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (kb == 0) s_amax[wave][tt] = m;
+    __syncthreads();
+    float amax = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-          w.hroute[(size_t)(p0 + tt) * w.I + rt * kTileRows + 4 * kb + r] = silu_ref(acc[rr][0][r]) * acc[rr][1][r];
+    for (int v = 0; v < kWideWaves; v++) amax = fmaxf(amax, s_amax[v][tt]);
+    const float A = amax / 127.0f, B = A / 254.0f;
+    int q1[4] = {0, 0, 0, 0}, q2[4] = {0, 0, 0, 0};
+    if (amax > 0.0f) {
+      const float invA = 127.0f / amax, invB = 254.0f / A;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        q1[r] = (int)fminf(fmaxf(__builtin_rintf(h[r] * invA), -127.0f), 127.0f);
+        const float rr = __builtin_fmaf(-(float)q1[r], A, h[r]);
+        q2[r] = (int)fminf(fmaxf(__builtin_rintf(rr * invB), -127.0f), 127.0f);
       }
+    }
+    const int g = chunk;  // this block's group of I
+    const size_t at = (size_t)(p0 + tt) * w.Ip + (size_t)g * kGroup + (size_t)wave * kTileRows + 4 * kb;
+    if (tt < cnt) {
+      *(unsigned *)(w.hd1 + at) = pack_i8x4(q1[0], q1[1], q1[2], q1[3]);
+      *(unsigned *)(w.hd2 + at) = pack_i8x4(q2[0], q2[1], q2[2], q2[3]);
+    }
+    int Q1 = q1[0] + q1[1] + q1[2] + q1[3], Q2 = q2[0] + q2[1] + q2[2] + q2[3];
+    Q1 += __shfl_xor(Q1, 16, 64);
+    Q1 += __shfl_xor(Q1, 32, 64);
+    Q2 += __shfl_xor(Q2, 16, 64);
+    Q2 += __shfl_xor(Q2, 32, 64);
+    if (kb == 0) {
+      s_q[wave][0][tt] = Q1;
+      s_q[wave][1][tt] = Q2;
+    }
+    __syncthreads();
+    if (wave == 0 && kb == 0 && tt < cnt) {
+      int S1 = 0, S2 = 0;
+#pragma unroll
+      for (int v = 0; v < kWideWaves; v++) {
+        S1 += s_q[v][0][tt];
+        S2 += s_q[v][1][tt];
+      }
+      w.hgp[(size_t)(p0 + tt) * w.ngi + g] = make_float4(A, B, __int_as_float(S1), __int_as_float(S2));
     }
   }
 }
@@ -3102,10 +3171,13 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
     const void *fn = fmt4 ? (const void *)k_gateup_wide<4> : (const void *)k_gateup_wide<3>;
     if (set_lds(fn, lg)) return -1;
     const int nx = (w.I / kTileRows + kWideWaves * kWideRt - 1) / (kWideWaves * kWideRt);
+    const int nsb = (T + 7) / 8 * 8;  // the shared hidden rows' blocks (k_prep_hidden's work)
     if (fmt4)
-      k_gateup_wide<4><<<nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots);
+      k_gateup_wide<4><<<nsb + nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots, nsb, L->sh_gs,
+                                                                      L->sh_us);
     else
-      k_gateup_wide<3><<<nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots);
+      k_gateup_wide<3><<<nsb + nx * slots, 64 * kWideWaves, lg, st>>>(w, L->xl, hg, nx, slots, nsb, L->sh_gs,
+                                                                      L->sh_us);
   } else {
     const int gu_rt = T * w.K <= 64 ? kGuRowTilesSmall : kGuRowTiles;
     const int gu_blocks_x = (w.I / kTileRows + gu_rt - 1) / gu_rt;
@@ -3127,7 +3199,7 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
   }
   mark(ctx, 4);
   prof_mark(ctx, kStageRoutedHidden);
-  k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w, L->sh_gs, L->sh_us);
+  if (!wide_items) k_prep_hidden<<<T + T * w.K, 256, 0, st>>>(w, L->sh_gs, L->sh_us);  // else in k_gateup_wide
   mark(ctx, 5);
   int sh_chunks = (T + kSharedTokens - 1) / kSharedTokens;
   const int dn_blocks_x = (w.H / kTileRows + 4 * kDnRowTiles - 1) / (4 * kDnRowTiles);
