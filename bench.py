@@ -699,9 +699,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (testing)")
-    ap.add_argument("--decode-kernels", type=int, default=1, choices=[1, 2],
+    ap.add_argument("--decode-kernels", type=int, default=1, choices=[0, 1, 2],
                     help="1: the persistent decode kernel, one launch per stack step (default); "
-                         "2: the three per-layer decode kernels")
+                         "2: the three per-layer decode kernels; 0: the many-token kernels for every "
+                         "step size")
     ap.add_argument("--item-tokens", type=int, default=0, choices=[0, 8, 16],
                     help="many-token steps: tokens per expert item (0 automatic; for measurement)")
     ap.add_argument("--stamps", action="store_true",

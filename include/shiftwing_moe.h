@@ -447,8 +447,9 @@ int coli_cuda_moe_set_router_mode(ColiMoeLayer *layer, int mode);
  * tokens == 1 and layers of one shape this is one persistent kernel that
  * needs every compute unit of the device for the duration of the call; a
  * call that cannot get them reports an error at the next coli_cuda_sync.
- * With 2..4 tokens the persistent kernel runs once per token (the tokens
- * are independent), which is faster than one many-token step per layer. */
+ * With 2 tokens the persistent kernel runs once per token (the tokens are
+ * independent), which is faster than one many-token step per layer; from 3
+ * tokens the many-token step is the faster. */
 int coli_cuda_moe_forward_layers(ColiCuda *ctx, ColiMoeLayer *const *layers,
                                  int n_layers, float *y, const float *x,
                                  int tokens, size_t x_layer_stride,

@@ -3234,10 +3234,11 @@ extern "C" int coli_cuda_moe_forward(ColiCuda *ctx, ColiMoeLayer *L, float *y, c
 }
 
 // Token counts a stack call runs through the persistent kernel token by token
-// (S397, 60 layers: 2.08 ms per token, against 7.4 ms for a 3-token, 8.7 ms
-// for a 4-token and 9.2 ms for a 6-token many-token step).
+// (S397, 60 layers: 1.96 ms per token, against 5.18 ms for a 2-token, 5.41 ms
+// for a 3-token and 5.97 ms for a 4-token many-token step; S35, 40 layers:
+// 0.81 ms per token, against 2.20, 2.24 and 2.33 ms).
 #ifndef SW_STACK_SEQ_TOKENS
-#define SW_STACK_SEQ_TOKENS 4
+#define SW_STACK_SEQ_TOKENS 2
 #endif
 constexpr int kStackSeqTokens = SW_STACK_SEQ_TOKENS;
 

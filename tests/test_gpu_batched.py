@@ -122,10 +122,10 @@ def test_batched_stack_equals_layer_calls(be):
         assert_close_rms(ys[l], y1, 1e-3, f"stack layer {l} against a call with route outputs")
 
 
-@pytest.mark.parametrize("T", [2, 4, 5])
+@pytest.mark.parametrize("T", [2, 3, 5])
 def test_small_batch_stack_runs_token_by_token(be, oracle, T):
-    """coli_cuda_moe_forward_layers with 2..4 tokens runs the persistent decode
-    kernel once per token: bit for bit the one-token calls.  From 5 tokens the
+    """coli_cuda_moe_forward_layers with 2 tokens runs the persistent decode
+    kernel once per token: bit for bit the one-token calls.  From 3 tokens the
     many-token step runs.  Either way each layer is within the tolerance of
     the oracle's moe_forward (c/qwen.c:3717-3739)."""
     import ctypes as C
@@ -153,7 +153,7 @@ def test_small_batch_stack_runs_token_by_token(be, oracle, T):
         dxt = be.upload(np.ascontiguousarray(x[:, t, :]))
         be.check(be.lib.coli_cuda_moe_forward_layers(be.ctx, arr, nl, d1.p, dxt.p, 1, H, H), "forward_layers 1")
         y1 = be.download(d1, (nl, H), np.float32)
-        if T <= 4:
+        if T <= 2:
             assert np.array_equal(ys[:, t, :].view(np.uint32), y1.view(np.uint32)), t
     for l in range(nl):
         for t in range(T):
