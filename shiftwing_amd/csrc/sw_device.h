@@ -260,24 +260,29 @@ __device__ __forceinline__ float serial_sum_lds(const float *p, int m, float s =
   return s;
 }
 
-// largest 64-bit key over the wave (keys encode value and index)
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
-#define SW_U64_STEP(ctrl, rm, bc)                                                           \
-  {                                                                                         \
-    unsigned lo_ = (unsigned)SW_DPP_I(0, (int)(unsigned)k, ctrl, rm, bc);                  \
-    unsigned hi_ = (unsigned)SW_DPP_I(0, (int)(unsigned)(k >> 32), ctrl, rm, bc);          \
-    unsigned long long o_ = ((unsigned long long)hi_ << 32) | lo_;                          \
-    k = o_ > k ? o_ : k;                                                                    \
+// largest unsigned value over the wave; rows a step leaves out keep 0, the
+// identity of the maximum, and lane 63 ends with the whole wave's maximum
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+#define SW_U32_STEP(ctrl, rm, bc)                                         \
+  {                                                                       \
+    const unsigned o_ = (unsigned)SW_DPP_I(0, (int)v, ctrl, rm, bc);      \
+    v = o_ > v ? o_ : v;                                                  \
   }
-  SW_U64_STEP(0xB1, 0xF, true);
-  SW_U64_STEP(0x4E, 0xF, true);
-  SW_U64_STEP(0x141, 0xF, true);
-  SW_U64_STEP(0x140, 0xF, true);
-  SW_U64_STEP(0x142, 0xA, false);
-  SW_U64_STEP(0x143, 0xC, false);
-#undef SW_U64_STEP
-  unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)k, 63);
-  unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(k >> 32), 63);
+  SW_U32_STEP(0xB1, 0xF, true);
+  SW_U32_STEP(0x4E, 0xF, true);
+  SW_U32_STEP(0x141, 0xF, true);
+  SW_U32_STEP(0x140, 0xF, true);
+  SW_U32_STEP(0x142, 0xA, false);
+  SW_U32_STEP(0x143, 0xC, false);
+#undef SW_U32_STEP
+  return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// largest 64-bit key over the wave (keys encode value and index): the
+// largest high word, then the largest low word among the lanes holding it
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+  const unsigned hi = wave_max_u32((unsigned)(k >> 32));
+  const unsigned lo = wave_max_u32((unsigned)(k >> 32) == hi ? (unsigned)k : 0u);
   return ((unsigned long long)hi << 32) | lo;
 }
 
