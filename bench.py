@@ -662,6 +662,155 @@ def cpu_baseline_head(budget_s: float, batch=1):
     return out
 
 
+# f2: the S397 decoder's mixer layers (Qwen3.5-397B-A17B: hidden 4096; Gated
+# DeltaNet 16 key / 64 value heads of 128, conv kernel 4; GQA 32 query / 2 kv
+# heads of 256, rotary 64, theta 1e7), int4-g128 projections
+MIXER_GDN = dict(hidden=4096, key_heads=16, value_heads=64, key_dim=128, value_dim=128, conv_kernel=4)
+MIXER_GQA = dict(hidden=4096, query_heads=32, kv_heads=2, head_dim=256, rotary_dim=64)
+
+
+def _rand_q4(rng, O, I, gs=128):
+    rb = row_bytes(4, I, gs)
+    return (rng.integers(0, 256, (O, rb), dtype=np.uint8),
+            (np.abs(rng.standard_normal((O, (I + gs - 1) // gs))) * 0.005).astype(np.float32))
+
+
+def _call_ms(be, run, steps, warmup):
+    for _ in range(warmup):
+        run()
+    be.sync()
+    durs = []
+    for _ in range(steps):
+        be.check(be.lib.coli_cuda_timer_start(be.ctx))
+        run()
+        m = C.c_float()
+        be.check(be.lib.coli_cuda_timer_stop(be.ctx, C.byref(m)))
+        durs.append(m.value)
+    return sum(durs) / len(durs)
+
+
+def measure_mixers(be, steps, warmup, batch=1, ctx_len=4096):
+    """f2: one decode step of the S397 decoder's Gated DeltaNet layer
+    (coli_cuda_gdn_slots_q4_f16_device, `batch` sequences in their own slots)
+    and of its GQA attention layer at `ctx_len` cached positions
+    (coli_cuda_gqa_slots_q4_f16_device), device-resident inputs and outputs,
+    HIP events on the context stream.  Algorithmic bytes: every projection
+    byte once, the recurrent state read and written, the KV prefix read."""
+    from shiftwing_amd.mixers import DeviceAttn, DeviceGdn
+    rng = np.random.default_rng(2024)
+    lib = be.lib
+    g = MIXER_GDN
+    H, kh, vh, dk, dv, K = (g[k] for k in ("hidden", "key_heads", "value_heads", "key_dim", "value_dim",
+                                           "conv_kernel"))
+    cd, vd = 2 * kh * dk + vh * dv, vh * dv
+    gdn = DeviceGdn(be, **g, group_size=128, eps=1e-6, qkv=_rand_q4(rng, cd, H), z=_rand_q4(rng, vd, H),
+                    out=_rand_q4(rng, H, vd), conv=rng.standard_normal((cd, K)).astype(np.float32) * 0.5,
+                    A_log=rng.standard_normal(vh).astype(np.float32) * 0.5,
+                    dt_bias=rng.standard_normal(vh).astype(np.float32) * 0.5,
+                    norm=np.ones(dv, np.float32), slots=batch)
+    x = be.alloc(batch * H * 4)
+    ab = be.alloc(batch * vh * 4)
+    y = be.alloc(batch * H * 4)
+    be.check(lib.coli_cuda_synth_activations(be.ctx, x.p, batch, H, C.c_ulonglong(31), 0, 0))
+    be.check(lib.coli_cuda_synth_activations(be.ctx, ab.p, batch, vh, C.c_ulonglong(32), 0, 0))
+    slot = np.arange(batch, dtype=np.int32)
+    pos = np.full(batch, 7, np.int32)
+
+    def run_gdn():
+        be.check(lib.coli_cuda_gdn_slots_q4_f16_device(
+            be.ctx, y.p, x.p, ab.p, ab.p, batch, C.c_void_p(slot.ctypes.data), C.c_void_p(pos.ctypes.data),
+            *gdn._weights(), batch, H, kh, vh, dk, dv, K, 128, C.c_float(1e-6)), "gdn_slots_device")
+
+    ms_gdn = _call_ms(be, run_gdn, steps, warmup)
+    wbytes = sum(m.q.nbytes + m.s.nbytes for m in (gdn.qkv, gdn.z, gdn.out))
+    gdn_bytes = wbytes + batch * (2 * vh * dk * dv * 4 + (K + 1) * cd * 4 + 2 * H * 4 + 2 * vh * 4)
+    a = MIXER_GQA
+    nh, nkv, hd, rd = (a[k] for k in ("query_heads", "kv_heads", "head_dim", "rotary_dim"))
+    kvrows, ctxn = nkv * hd, nh * hd
+    max_seq = ctx_len + 1
+    att = DeviceAttn(be, **a, group_size=128, theta=1e7, eps=1e-6, q=_rand_q4(rng, 2 * ctxn, H),
+                     k=_rand_q4(rng, kvrows, H), v=_rand_q4(rng, kvrows, H), o=_rand_q4(rng, H, ctxn), o_fmt=4,
+                     q_norm=np.zeros(hd, np.float32), k_norm=np.zeros(hd, np.float32), max_seq=max_seq,
+                     slots=batch)
+    for sl in range(batch):
+        off = sl * max_seq * kvrows * 4
+        for buf, seed in ((att.k_cache, 33), (att.v_cache, 34)):
+            be.check(lib.coli_cuda_synth_activations(be.ctx, C.c_void_p(buf.ptr + off), max_seq, kvrows,
+                                                     C.c_ulonglong(seed), sl, 0))
+    apos = np.full(batch, ctx_len, np.int32)
+
+    def run_gqa():
+        be.check(lib.coli_cuda_gqa_slots_q4_f16_device(
+            be.ctx, y.p, x.p, batch, C.c_void_p(slot.ctypes.data), C.c_void_p(apos.ctypes.data), *att._weights(),
+            batch, max_seq, *att._tail()), "gqa_slots_device")
+
+    ms_gqa = _call_ms(be, run_gqa, steps, warmup)
+    wq = sum(m.q.nbytes + m.s.nbytes for m in (att.q, att.k, att.v, att.o))
+    gqa_bytes = wq + batch * (2 * (ctx_len + 1) * kvrows * 4 + 2 * H * 4)
+    for b in (x, ab, y):
+        b.free()
+
+    def rl(nbytes, ms, kern):
+        ach = nbytes / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "kernel": kern, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_call": int(nbytes),
+                "avg_call_us": round(ms * 1e3, 2)}
+
+    return {
+        "metric": "mixer-layer decode steps/s (S397 Gated DeltaNet and GQA layers, int4 projections)",
+        "unit": "steps/s", "steps": steps, "warmup": warmup,
+        "config": {"workload": "f2: one decode step through the S397 decoder's Gated DeltaNet layer and its GQA "
+                               f"attention layer at {ctx_len} cached positions, {batch} sequence(s), "
+                               "device-resident activations", "batch": batch, "context": ctx_len,
+                   **{f"gdn_{k}": v for k, v in MIXER_GDN.items()}, **{f"gqa_{k}": v for k, v in MIXER_GQA.items()}},
+        "gdn": {"value": round(1e3 / ms_gdn, 2), "ms_per_step": round(ms_gdn, 4),
+                "roofline": rl(gdn_bytes, ms_gdn, "k_mix_proj<4,CONV> + k_gdn_recur + k_mix_proj<4>")},
+        "gqa": {"value": round(1e3 / ms_gqa, 2), "ms_per_step": round(ms_gqa, 4),
+                "roofline": rl(gqa_bytes, ms_gqa, "k_mix_proj + k_gqa_prep + k_gqa_attn + k_gqa_combine "
+                                                  "+ k_mix_proj")},
+    }
+
+
+def cpu_baseline_mixers(budget_s: float, ctx_len=4096):
+    """The reference's own gdn_forward and attn_forward (c/qwen.c:3005, 3094,
+    compiled in place into oracle/_ref) at the same shapes: one decode token,
+    the attention layer at ctx_len cached positions."""
+    from oracle import pyoracle as po
+    try:
+        lib, kind = po.Reference().lib, "reference"
+    except Exception:
+        lib, kind = None, "port"
+    orc = po.Oracle()
+    g = MIXER_GDN
+    hg = po.HostGdn(5, g["hidden"], g["key_heads"], g["value_heads"], g["key_dim"], g["value_dim"], g["conv_kernel"])
+    a = MIXER_GQA
+    ha = po.HostAttn(6, a["hidden"], a["query_heads"], a["kv_heads"], a["head_dim"], a["rotary_dim"], o_fmt=4)
+    x = np.random.default_rng(7).standard_normal(g["hidden"]).astype(np.float32)
+    info = cpu_info()
+    out = {"unit": "steps/s", "kind": kind, "cpu_model": info["model"], "physical_cores": info["physical_cores"],
+           "cores": info["usable_cpus"]}
+    if lib is not None:
+        rg = po.RefMixer(lib, hg)
+        ra = po.RefMixer(lib, ha, max_seq=ctx_len + 1)
+        ra.k_cache[:] = np.random.default_rng(8).standard_normal(ra.k_cache.shape).astype(np.float32)
+        ra.v_cache[:] = np.random.default_rng(9).standard_normal(ra.v_cache.shape).astype(np.float32)
+        step_g = lambda i: rg.gdn(x, 7 + i)
+        step_a = lambda i: ra.attn(x, ctx_len)
+    else:
+        cs, st = [v[0] for v in hg.new_state()]
+        kc, vc = [v[0] for v in ha.new_cache(ctx_len + 1)]
+        ab = np.zeros(g["value_heads"], np.float32)
+        step_g = lambda i: po.oracle_gdn_step(orc, hg, x, ab, ab, 7 + i, cs, st)
+        step_a = lambda i: po.oracle_attn_step(orc, ha, x, ctx_len, kc, vc)
+    ng, dg = _timed(lambda i: (step_g(i), 1)[1], budget_s / 2, 200)
+    na, da = _timed(lambda i: (step_a(i), 1)[1], budget_s / 2, 200)
+    out["gdn_value"] = round(ng / dg, 3)
+    out["gqa_value"] = round(na / da, 3)
+    out["value"] = out["gdn_value"]
+    out["sample"] = f"{ng} Gated DeltaNet steps in {dg:.1f} s, {na} attention steps at {ctx_len} positions in {da:.1f} s"
+    return out
+
+
 def progress(msg):
     """A progress line on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -692,7 +841,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["all", "output-head"] + sorted(WORKLOADS) + sorted(MANY),
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "output-head", "mixers"] + sorted(WORKLOADS) + sorted(MANY),
                     help="all (default): config 2 is the headline; configs 1, 3 (B = 1..32) and 4 are timed in "
                          "the same run and reported under 'configs'")
     ap.add_argument("--batch", type=int, default=8, help="tokens per step of --workload s397-batch")
@@ -732,6 +882,12 @@ def main():
         r = measure_head(be, args.steps, args.warmup, 1)
         r = with_cpu(r, args, lambda: cpu_baseline_head(args.cpu_seconds))
         print(json.dumps({"n_gpus": 1, "higher_is_better": True, "dtype": "int8", "data": "synthetic", **r}),
+              flush=True)
+        return
+    if args.workload == "mixers":
+        r = measure_mixers(be, args.steps, args.warmup, args.batch if args.batch != 8 else 1)
+        r = with_cpu(r, args, lambda: cpu_baseline_mixers(args.cpu_seconds))
+        print(json.dumps({"n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic", **r}),
               flush=True)
         return
     if args.workload in MANY:
@@ -820,6 +976,10 @@ def main():
     hd = measure_head(be, 10, 3)
     progress(f"output head: {hd['roofline']['avg_launch_us']} us per call")
     configs["output_head"] = with_cpu(hd, args, lambda: cpu_baseline_head(args.cpu_seconds / 2))
+    # f2: the decoder's mixer layers around the MoE block (one decode token)
+    mx = measure_mixers(be, 10, 3)
+    progress(f"mixer layers: GDN {mx['gdn']['ms_per_step']} ms, GQA {mx['gqa']['ms_per_step']} ms per step")
+    configs["mixers"] = with_cpu(mx, args, lambda: cpu_baseline_mixers(args.cpu_seconds / 2))
     line["configs"] = configs
     line["wall_s"] = round(time.perf_counter() - t0, 1)
     print(json.dumps(line), flush=True)

@@ -164,13 +164,23 @@ int coli_cuda_shared_q4_mlp_f16(
     int hidden_groups, int down_row_bytes, int down_groups,
     int scale_row_bytes, int scale_groups);                          /* :140-148 */
 
-/* ---- Part 1b: entry points outside the MoE path ------------------------- */
-/* c/qwen.c links against these unconditionally (c/qwen.c:884, 900, 940, 966)
- * and calls them only with its CUDA_GDN / CUDA_ATTN switches on (c/qwen.c:868,
- * 925-926).  They are exported with the reference prototypes so the reference
- * host links against this library unchanged; every call returns -1 with a
- * message saying the path is not built here.  Run the reference host with
- * CUDA_GDN=0 CUDA_ATTN=0 so those layers stay on its CPU path. */
+/* ---- Part 1b: the mixer layers either side of the MoE block ------------- */
+/* The hybrid decoder's Gated DeltaNet and gated GQA attention layers
+ * (c/backend_cuda.h:149-236), called by the reference engine through
+ * cuda_gdn_try, cuda_gdn_block_try, cuda_gdn_slots_try (c/qwen.c:881-911),
+ * cuda_attn_try, cuda_attn_prefill_try, cuda_attn_slots_try (935-991) and
+ * cuda_resident_core_try (994-1075).  Same arguments, ownership and 0/-1
+ * convention as the reference: weights, norms, conv/recurrent state and KV
+ * caches are device pointers; x, a, b and out are host pointers except in the
+ * *_device forms (which do not synchronize); slot and position tables are
+ * host arrays.  Arithmetic is fp32 on fp32 activations (the reference rounds
+ * them to fp16 first) and matches the reference CPU path (gdn_forward
+ * c/qwen.c:3005, attn_forward 3094) within 1e-3 x RMS.  Layouts taken: int4
+ * projections with group sizes and widths that are multiples of 32 and row
+ * strides that are multiples of 16 bytes (the converter's g128 rows), int8 or
+ * int4 o projection, key_dim <= 128, value_dim <= 256, head_dim 64, 128 or
+ * 256 with at most 16 query heads per kv head; other layouts return -1 with a
+ * message. */
 int coli_cuda_gdn_decode_q4_f16(
     ColiCuda *ctx, float *out, const float *x, const float *a, const float *b,
     const unsigned char *qkv_q, const float *qkv_s, int qkv_row_bytes,

@@ -598,3 +598,177 @@ void or_synth_x(uint64_t seed, int layer, int step, int H, float *x) {
     or_synth_normals(sw_key(seed, (uint32_t)layer, (uint32_t)step, SW_T_X), x, H,
                      1.0f, 0);
 }
+
+/* ---- the mixer layers either side of the MoE block ----------------------
+ * Gated DeltaNet decode (gdn_forward, c/qwen.c:3005-3030, with
+ * gdn_rule_step 2907-2927) and gated GQA attention decode (attn_forward,
+ * c/qwen.c:3094-3137, with rope_head 3031-3033).  The projections are
+ * qmat_mul_ex (restated above); the transcendental functions are glibc's, as
+ * the reference calls them.  Which products gcc fuses into an FMA in these
+ * loops is pinned against the compiled reference (tests/test_oracle_cpu.py). */
+
+/* softplusf_stable, c/qwen.c:309 */
+static float or_softplusf(float x) {
+    return x > 20.f ? x : (x < -20.f ? expf(x) : log1pf(expf(x)));
+}
+
+void or_gdn_gates(const or_gdn *G, const float *x, float *a, float *b) {
+    or_qmat_mul(b, x, &G->b, 0);
+    or_qmat_mul(a, x, &G->a, 0);
+}
+
+/* gdn_rule_step, c/qwen.c:2907-2927, for one token */
+static void or_gdn_rule_step(float *core, float *state, const float *q, const float *k,
+                             const float *v, const float *z, const float *a, const float *b,
+                             const or_gdn *G) {
+    const int kh = G->kh, vh = G->vh, dk = G->dk, dv = G->dv, ratio = vh / kh;
+    const float invsqrt = 1.f / sqrtf((float)dk);
+    for (int h = 0; h < vh; h++) {
+        const int hk = h / ratio;
+        float *S = state + (int64_t)h * dk * dv;
+        const float *qh = q + (int64_t)hk * dk, *kv = k + (int64_t)hk * dk, *vv = v + (int64_t)h * dv;
+        float qn = 0.f, kn = 0.f;
+        for (int i = 0; i < dk; i++) {
+            const float pq = qh[i] * qh[i], pk = kv[i] * kv[i];
+            qn = qn + pq;
+            kn = kn + pk;
+        }
+        qn = 1.f / sqrtf(qn + 1e-6f);
+        kn = 1.f / sqrtf(kn + 1e-6f);
+        const float beta = or_sigmoidf(b[h]);
+        const float decay = expf(-expf(G->A_log[h]) * or_softplusf(a[h] + G->dt_bias[h]));
+        for (int64_t i = 0; i < (int64_t)dk * dv; i++) S[i] *= decay;
+        for (int j = 0; j < dv; j++) {
+            float mem = 0.f;
+            for (int i = 0; i < dk; i++) {
+                const float p = S[(int64_t)i * dv + j] * (kv[i] * kn);
+                mem = mem + p;
+            }
+            const float delta = (vv[j] - mem) * beta;
+            for (int i = 0; i < dk; i++)
+                S[(int64_t)i * dv + j] = fmaf(kv[i] * kn, delta, S[(int64_t)i * dv + j]);
+        }
+        for (int j = 0; j < dv; j++) {
+            float sum = 0.f;
+            for (int i = 0; i < dk; i++) {
+                const float p = S[(int64_t)i * dv + j] * (qh[i] * qn * invsqrt);
+                sum = sum + p;
+            }
+            core[(int64_t)h * dv + j] = sum;
+        }
+        float ms = 0.f;
+        for (int j = 0; j < dv; j++) {
+            const float c0 = core[(int64_t)h * dv + j];
+            const float p = c0 * c0;
+            ms = ms + p;
+        }
+        const float r = 1.f / sqrtf(ms / (float)dv + G->eps);
+        for (int j = 0; j < dv; j++)
+            core[(int64_t)h * dv + j] =
+                core[(int64_t)h * dv + j] * r * G->norm[j] * or_siluf(z[(int64_t)h * dv + j]);
+    }
+}
+
+/* gdn_forward, c/qwen.c:3005-3030, after the a/b projections */
+void or_gdn_forward(const or_gdn *G, const float *x, const float *a, const float *b, int pos,
+                    float *conv_state, float *state, float *out) {
+    const int kd = G->kh * G->dk, vd = G->vh * G->dv, cd = 2 * kd + vd, K = G->K;
+    float *raw = (float *)calloc((size_t)cd, sizeof(float));
+    float *mix = (float *)calloc((size_t)cd, sizeof(float));
+    float *z = (float *)calloc((size_t)vd, sizeof(float));
+    float *core = (float *)calloc((size_t)vd, sizeof(float));
+    or_qmat_mul(raw, x, &G->qkv, 0);
+    or_qmat_mul(z, x, &G->z, 0);
+    memcpy(conv_state + (int64_t)(pos % K) * cd, raw, (size_t)cd * sizeof(float));
+    for (int ch = 0; ch < cd; ch++) {
+        float acc = 0.f;
+        for (int tap = 0; tap < K; tap++) {
+            const int src = pos - (K - 1 - tap);
+            if (src >= 0)
+                acc = fmaf(G->conv[(int64_t)ch * K + tap], conv_state[(int64_t)(src % K) * cd + ch], acc);
+        }
+        mix[ch] = or_siluf(acc);
+    }
+    or_gdn_rule_step(core, state, mix, mix + kd, mix + 2 * kd, z, a, b, G);
+    or_qmat_mul(out, core, &G->out, 0);
+    free(raw);
+    free(mix);
+    free(z);
+    free(core);
+}
+
+/* rope_head, c/qwen.c:3031-3033 */
+static void or_rope_head(float *x, int rd, int pos, float theta) {
+    const int half = rd / 2;
+    for (int i = 0; i < half; i++) {
+        const float angle = (float)pos * powf(theta, -2.f * (float)i / (float)rd);
+        const float co = cosf(angle), si = sinf(angle);
+        const float a = x[i], b = x[i + half];
+        x[i] = fmaf(a, co, -(b * si));
+        x[i + half] = fmaf(b, co, a * si);
+    }
+}
+
+/* attn_forward, c/qwen.c:3094-3137: fp32 caches, no indexer mask */
+void or_attn_forward(const or_attn *A, const float *x, int pos, float *k_cache, float *v_cache,
+                     float *out) {
+    const int nh = A->nh, nkv = A->nkv, hd = A->hd;
+    const int qrows = nh * hd * 2, kvrows = nkv * hd;
+    float *qp = (float *)calloc((size_t)qrows, sizeof(float));
+    float *q = (float *)calloc((size_t)nh * hd, sizeof(float));
+    float *gate = (float *)calloc((size_t)nh * hd, sizeof(float));
+    float *k = (float *)calloc((size_t)kvrows, sizeof(float));
+    float *v = (float *)calloc((size_t)kvrows, sizeof(float));
+    float *ctx = (float *)calloc((size_t)nh * hd, sizeof(float));
+    float *scores = (float *)calloc((size_t)nh * (pos + 1), sizeof(float));
+    or_qmat_mul(qp, x, &A->q, 0);
+    or_qmat_mul(k, x, &A->k, 0);
+    or_qmat_mul(v, x, &A->v, 0);
+    for (int h = 0; h < nh; h++) {
+        memcpy(q + (int64_t)h * hd, qp + (int64_t)h * 2 * hd, (size_t)hd * sizeof(float));
+        memcpy(gate + (int64_t)h * hd, qp + (int64_t)h * 2 * hd + hd, (size_t)hd * sizeof(float));
+        or_rmsnorm_zero(q + (int64_t)h * hd, q + (int64_t)h * hd, A->q_norm, hd, A->eps);
+        or_rope_head(q + (int64_t)h * hd, A->rd, pos, A->theta);
+    }
+    for (int h = 0; h < nkv; h++) {
+        or_rmsnorm_zero(k + (int64_t)h * hd, k + (int64_t)h * hd, A->k_norm, hd, A->eps);
+        or_rope_head(k + (int64_t)h * hd, A->rd, pos, A->theta);
+    }
+    memcpy(k_cache + (int64_t)pos * kvrows, k, (size_t)kvrows * sizeof(float));
+    memcpy(v_cache + (int64_t)pos * kvrows, v, (size_t)kvrows * sizeof(float));
+    const int rep = nh / nkv;
+    const float scale = 1.f / sqrtf((float)hd);
+    for (int h = 0; h < nh; h++) {
+        const int hk = h / rep;
+        float *sh = scores + (int64_t)h * (pos + 1);
+        float mx = -INFINITY;
+        for (int t = 0; t <= pos; t++) {
+            float z0 = 0.f;
+            const int64_t off = (int64_t)t * kvrows + (int64_t)hk * hd;
+            for (int j = 0; j < hd; j++) z0 = fmaf(q[(int64_t)h * hd + j], k_cache[off + j], z0);
+            sh[t] = z0 * scale;
+            if (sh[t] > mx) mx = sh[t];
+        }
+        float den = 0.f;
+        for (int t = 0; t <= pos; t++) {
+            sh[t] = sh[t] == -INFINITY ? 0.f : expf(sh[t] - mx);
+            den += sh[t];
+        }
+        for (int j = 0; j < hd; j++) {
+            float sum = 0.f;
+            for (int t = 0; t <= pos; t++) {
+                const int64_t off = (int64_t)t * kvrows + (int64_t)hk * hd + j;
+                sum = fmaf(sh[t] / den, v_cache[off], sum);
+            }
+            ctx[(int64_t)h * hd + j] = sum * or_sigmoidf(gate[(int64_t)h * hd + j]);
+        }
+    }
+    or_qmat_mul(out, ctx, &A->o, 0);
+    free(qp);
+    free(q);
+    free(gate);
+    free(k);
+    free(v);
+    free(ctx);
+    free(scores);
+}

@@ -82,6 +82,39 @@ void or_moe_forward(const or_layer *L, const float *x, float *out,
 void or_moe_prefill_grouped(const or_layer *L, const float *x, int T,
                             float *out, or_trace *tr);
 
+/* The two mixer layers either side of the MoE block in the reference's
+ * hybrid decoder: the Gated DeltaNet layer (GdnW, c/qwen.c:95-104, with the
+ * Cfg fields lin_* and conv_kernel) and the gated GQA attention layer (AttnW,
+ * c/qwen.c:105-114, Cfg n_heads, n_kv_heads, head_dim, partial_rotary,
+ * theta).  Channels of qkv: [q: kh*dk | k: kh*dk | v: vh*dv]. */
+typedef struct {
+    int H, kh, vh, dk, dv, K;
+    float eps;
+    or_qmat qkv, z, a, b, out;   /* qkv, z, out int4; a, b any format (vh x H) */
+    const float *conv;           /* channels x K */
+    const float *A_log, *dt_bias; /* vh */
+    const float *norm;           /* dv */
+} or_gdn;
+
+typedef struct {
+    int H, nh, nkv, hd, rd;
+    float theta, eps;
+    or_qmat q, k, v, o;          /* q: 2*nh*hd rows (query | gate per head) */
+    const float *q_norm, *k_norm; /* hd */
+} or_attn;
+
+/* a = W_a x, b = W_b x as gdn_forward forms them (c/qwen.c:3008). */
+void or_gdn_gates(const or_gdn *G, const float *x, float *a, float *b);
+/* One decode step at position pos; conv_state [K][channels] and state
+ * [vh][dk][dv] are updated in place (c/qwen.c:3004-3025, 2907-2927). */
+void or_gdn_forward(const or_gdn *G, const float *x, const float *a,
+                    const float *b, int pos, float *conv_state, float *state,
+                    float *out);
+/* One decode step at position pos over fp32 caches [positions][nkv*hd]
+ * (attn_forward without the Qwen4-Exp indexer, c/qwen.c:3116-3153). */
+void or_attn_forward(const or_attn *A, const float *x, int pos,
+                     float *k_cache, float *v_cache, float *out);
+
 /* token->expert bucketing in the order of moe_prefill_grouped as a CSR:
  * offsets[E+1]; entry n of expert e holds token[n] (ascending) and slot[n]
  * (the route index k with idx[token*K+k]==e).  Returns the route count. */

@@ -442,3 +442,203 @@ class HostLayer:
     def set_router_column(self, col: int, values: np.ndarray):
         """Overwrite one router column in place (the Zipf bias feature)."""
         self.router_w[:, col] = values
+
+
+# -- the mixer layers either side of the MoE block ----------------------------
+
+class OrGdn(C.Structure):
+    _fields_ = [("H", C.c_int), ("kh", C.c_int), ("vh", C.c_int), ("dk", C.c_int),
+                ("dv", C.c_int), ("K", C.c_int), ("eps", C.c_float), ("qkv", OrQMat),
+                ("z", OrQMat), ("a", OrQMat), ("b", OrQMat), ("out", OrQMat),
+                ("conv", f32p), ("A_log", f32p), ("dt_bias", f32p), ("norm", f32p)]
+
+
+class OrAttn(C.Structure):
+    _fields_ = [("H", C.c_int), ("nh", C.c_int), ("nkv", C.c_int), ("hd", C.c_int),
+                ("rd", C.c_int), ("theta", C.c_float), ("eps", C.c_float), ("q", OrQMat),
+                ("k", OrQMat), ("v", OrQMat), ("o", OrQMat), ("q_norm", f32p),
+                ("k_norm", f32p)]
+
+
+def random_q4(rng: np.random.Generator, O: int, I: int, gs: int = 128, scale: float = 0.005):
+    """An int4 container matrix: uniform random nibbles, |N(0, scale)| group scales."""
+    rb = row_bytes(4, I, gs)
+    q = rng.integers(0, 256, size=(O, rb), dtype=np.uint8)
+    s = np.abs(rng.normal(0.0, scale, size=(O, (I + gs - 1) // gs))).astype(np.float32)
+    return HostQMat(4, O, I, gs, q=q, s=s)
+
+
+def random_q8(rng: np.random.Generator, O: int, I: int, scale: float = 0.0004):
+    q = rng.integers(-127, 128, size=(O, I), dtype=np.int8)
+    s = np.abs(rng.normal(0.0, scale, size=O)).astype(np.float32)
+    return HostQMat(1, O, I, q=q, s=s)
+
+
+class HostGdn:
+    """A Gated DeltaNet layer (GdnW, c/qwen.c:95-104) with random weights:
+    int4 qkv / z / out projections, fp32 a / b gate rows."""
+
+    def __init__(self, seed: int, H: int, kh: int, vh: int, dk: int, dv: int, K: int = 4,
+                 gs: int = 128, eps: float = 1e-6):
+        rng = np.random.default_rng(seed)
+        self.H, self.kh, self.vh, self.dk, self.dv, self.K, self.gs, self.eps = H, kh, vh, dk, dv, K, gs, eps
+        self.kd, self.vd = kh * dk, vh * dv
+        self.cd = 2 * self.kd + self.vd
+        self.qkv = random_q4(rng, self.cd, H, gs)
+        self.z = random_q4(rng, self.vd, H, gs)
+        self.out = random_q4(rng, H, self.vd, gs, scale=0.004)
+        self.wa = rng.normal(0.0, 0.02, size=(vh, H)).astype(np.float32)
+        self.wb = rng.normal(0.0, 0.02, size=(vh, H)).astype(np.float32)
+        self.a = HostQMat(0, vh, H, f=self.wa)
+        self.b = HostQMat(0, vh, H, f=self.wb)
+        self.conv = rng.normal(0.0, 0.5, size=(self.cd, K)).astype(np.float32)
+        self.A_log = rng.normal(0.0, 0.5, size=vh).astype(np.float32)
+        self.dt_bias = rng.normal(0.0, 0.5, size=vh).astype(np.float32)
+        self.norm = (1.0 + rng.normal(0.0, 0.1, size=dv)).astype(np.float32)
+        self.st = OrGdn(H, kh, vh, dk, dv, K, eps, self.qkv.st, self.z.st, self.a.st, self.b.st,
+                        self.out.st, ptr(self.conv, f32p), ptr(self.A_log, f32p),
+                        ptr(self.dt_bias, f32p), ptr(self.norm, f32p))
+
+    def new_state(self, slots: int = 1):
+        """(conv_state [slots][K][channels], recurrent state [slots][vh][dk][dv]), zero."""
+        return (np.zeros((slots, self.K, self.cd), np.float32),
+                np.zeros((slots, self.vh, self.dk, self.dv), np.float32))
+
+
+class HostAttn:
+    """A gated GQA attention layer (AttnW, c/qwen.c:105-114) with random
+    weights: int4 q (query | gate per head) / k / v, o in int8 (fmt 1) or int4."""
+
+    def __init__(self, seed: int, H: int, nh: int, nkv: int, hd: int, rd: int,
+                 o_fmt: int = 1, theta: float = 1e7, gs: int = 128, eps: float = 1e-6):
+        rng = np.random.default_rng(seed)
+        self.H, self.nh, self.nkv, self.hd, self.rd = H, nh, nkv, hd, rd
+        self.theta, self.gs, self.eps, self.o_fmt = theta, gs, eps, o_fmt
+        self.kvrows, self.ctxn = nkv * hd, nh * hd
+        self.q = random_q4(rng, 2 * nh * hd, H, gs)
+        self.k = random_q4(rng, self.kvrows, H, gs)
+        self.v = random_q4(rng, self.kvrows, H, gs)
+        self.o = (random_q8(rng, H, self.ctxn) if o_fmt == 1
+                  else random_q4(rng, H, self.ctxn, gs, scale=0.004))
+        self.q_norm = rng.normal(0.0, 0.1, size=hd).astype(np.float32)
+        self.k_norm = rng.normal(0.0, 0.1, size=hd).astype(np.float32)
+        self.st = OrAttn(H, nh, nkv, hd, rd, theta, eps, self.q.st, self.k.st, self.v.st,
+                         self.o.st, ptr(self.q_norm, f32p), ptr(self.k_norm, f32p))
+
+    def new_cache(self, max_seq: int, slots: int = 1):
+        return (np.zeros((slots, max_seq, self.kvrows), np.float32),
+                np.zeros((slots, max_seq, self.kvrows), np.float32))
+
+
+def _declare_mixers(L, prefix: str):
+    if prefix == "or_":
+        L.or_gdn_gates.restype = None
+        L.or_gdn_gates.argtypes = [C.POINTER(OrGdn), f32p, f32p, f32p]
+        L.or_gdn_forward.restype = None
+        L.or_gdn_forward.argtypes = [C.POINTER(OrGdn), f32p, f32p, f32p, C.c_int, f32p, f32p, f32p]
+        L.or_attn_forward.restype = None
+        L.or_attn_forward.argtypes = [C.POINTER(OrAttn), f32p, C.c_int, f32p, f32p, f32p]
+    else:
+        L.ref_gdn_create.restype = C.c_void_p
+        L.ref_gdn_create.argtypes = [C.POINTER(OrGdn), f32p, f32p]
+        L.ref_gdn_forward.restype = None
+        L.ref_gdn_forward.argtypes = [C.c_void_p, f32p, C.c_int, f32p, f32p, f32p]
+        L.ref_gdn_block.restype = None
+        L.ref_gdn_block.argtypes = [C.c_void_p, f32p, C.c_int, C.c_int, f32p]
+        L.ref_attn_create.restype = C.c_void_p
+        L.ref_attn_create.argtypes = [C.POINTER(OrAttn), f32p, f32p, C.c_int]
+        L.ref_attn_forward.restype = None
+        L.ref_attn_forward.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
+        L.ref_attn_prefill.restype = None
+        L.ref_attn_prefill.argtypes = [C.c_void_p, f32p, C.c_int, C.c_int, f32p]
+        L.ref_mixer_destroy.restype = None
+        L.ref_mixer_destroy.argtypes = [C.c_void_p]
+
+
+def oracle_gdn_gates(orc: "Oracle", g: HostGdn, x: np.ndarray):
+    _declare_mixers(orc.lib, "or_")
+    x = np.ascontiguousarray(x, np.float32)
+    a = np.zeros(g.vh, np.float32)
+    b = np.zeros(g.vh, np.float32)
+    orc.lib.or_gdn_gates(C.byref(g.st), ptr(x, f32p), ptr(a, f32p), ptr(b, f32p))
+    return a, b
+
+
+def oracle_gdn_step(orc: "Oracle", g: HostGdn, x, a, b, pos: int, conv_state, state):
+    """One token through the restatement; conv_state [K][channels] and state
+    [vh][dk][dv] (views of one slot) advance in place."""
+    _declare_mixers(orc.lib, "or_")
+    x = np.ascontiguousarray(x, np.float32)
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.zeros(g.H, np.float32)
+    orc.lib.or_gdn_forward(C.byref(g.st), ptr(x, f32p), ptr(a, f32p), ptr(b, f32p), pos,
+                           ptr(conv_state, f32p), ptr(state, f32p), ptr(out, f32p))
+    return out
+
+
+def oracle_attn_step(orc: "Oracle", at: HostAttn, x, pos: int, k_cache, v_cache):
+    """One token through the restatement; k_cache / v_cache [max_seq][nkv*hd]
+    (views of one slot) receive position pos."""
+    _declare_mixers(orc.lib, "or_")
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(at.H, np.float32)
+    orc.lib.or_attn_forward(C.byref(at.st), ptr(x, f32p), pos, ptr(k_cache, f32p),
+                            ptr(v_cache, f32p), ptr(out, f32p))
+    return out
+
+
+class RefMixer:
+    """A reference GdnW or AttnW layer (ref_harness.c) over caller buffers
+    that this object keeps alive."""
+
+    def __init__(self, lib, layer, *, max_seq: int = 0):
+        _declare_mixers(lib, "ref_")
+        self.lib, self.layer = lib, layer
+        if isinstance(layer, HostGdn):
+            self.conv_state, self.state = [a[0].copy() for a in layer.new_state()]
+            self.h = lib.ref_gdn_create(C.byref(layer.st), ptr(self.conv_state, f32p),
+                                        ptr(self.state, f32p))
+        else:
+            self.k_cache, self.v_cache = [a[0].copy() for a in layer.new_cache(max_seq)]
+            self.h = lib.ref_attn_create(C.byref(layer.st), ptr(self.k_cache, f32p),
+                                         ptr(self.v_cache, f32p), max_seq)
+
+    def gdn(self, x, pos: int):
+        """(out, a, b) of gdn_forward at position pos."""
+        g = self.layer
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(g.H, np.float32)
+        a = np.zeros(g.vh, np.float32)
+        b = np.zeros(g.vh, np.float32)
+        self.lib.ref_gdn_forward(self.h, ptr(x, f32p), pos, ptr(out, f32p), ptr(a, f32p), ptr(b, f32p))
+        return out, a, b
+
+    def gdn_block(self, x, base: int):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros((x.shape[0], self.layer.H), np.float32)
+        self.lib.ref_gdn_block(self.h, ptr(x, f32p), x.shape[0], base, ptr(out, f32p))
+        return out
+
+    def attn(self, x, pos: int):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(self.layer.H, np.float32)
+        self.lib.ref_attn_forward(self.h, ptr(x, f32p), pos, ptr(out, f32p))
+        return out
+
+    def attn_prefill(self, x, base: int):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros((x.shape[0], self.layer.H), np.float32)
+        self.lib.ref_attn_prefill(self.h, ptr(x, f32p), x.shape[0], base, ptr(out, f32p))
+        return out
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.ref_mixer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

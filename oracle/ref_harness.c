@@ -164,6 +164,137 @@ void ref_layer_destroy(void *h) {
     free(r);
 }
 
+/* The mixer layers of the hybrid decoder: a Gated DeltaNet layer (GdnW,
+ * c/qwen.c:95-104) and a gated GQA attention layer (AttnW, 105-114) in a
+ * one-layer Model, driven through gdn_forward 3005, gdn_decode_block 4642,
+ * attn_forward 3094 and attn_prefill_layer 3138.  The caller owns every
+ * buffer, including the CPU-side conv/recurrent state and KV caches; in the
+ * -DCOLI_CUDA build those functions take the reference's device paths
+ * (cuda_gdn_try 881, cuda_gdn_block_try 888, cuda_attn_try 935,
+ * cuda_attn_prefill_try 957) whenever its switches allow. */
+void *ref_gdn_create(const or_gdn *G, float *conv_state, float *state) {
+    RefLayer *r = (RefLayer *)calloc(1, sizeof(RefLayer));
+    if (!r) return NULL;
+    Cfg *c = &r->m.c;
+    c->n_layers = 1;
+    c->hidden = G->H;
+    c->lin_k_heads = G->kh;
+    c->lin_v_heads = G->vh;
+    c->lin_k_dim = G->dk;
+    c->lin_v_dim = G->dv;
+    c->conv_kernel = G->K;
+    c->eps = G->eps;
+    r->m.layer = &r->l;
+    r->l.type = LT_LINEAR;
+    static int serial;
+    const int ln = __atomic_fetch_add(&serial, 1, __ATOMIC_RELAXED);
+    char nm[160];
+    GdnW *w = &r->l.gdn;
+    snprintf(nm, sizeof(nm), "mixer.%d.linear_attn.in_proj_qkv.weight", ln);
+    w->qkv = ref_qmat_named(&G->qkv, nm);
+    snprintf(nm, sizeof(nm), "mixer.%d.linear_attn.in_proj_z.weight", ln);
+    w->z = ref_qmat_named(&G->z, nm);
+    snprintf(nm, sizeof(nm), "mixer.%d.linear_attn.out_proj.weight", ln);
+    w->out = ref_qmat_named(&G->out, nm);
+    w->a = ref_qmat(&G->a);
+    w->b = ref_qmat(&G->b);
+    w->conv = (float *)G->conv;
+    w->A_log = (float *)G->A_log;
+    w->dt_bias = (float *)G->dt_bias;
+    w->norm = (float *)G->norm;
+    w->conv_state = conv_state;
+    w->state = state;
+    return r;
+}
+
+/* one decode token at position pos (gdn_forward); a and b receive the gate
+ * projections gdn_forward forms from x */
+void ref_gdn_forward(void *h, const float *x, int pos, float *out, float *a, float *b) {
+    RefLayer *r = (RefLayer *)h;
+    if (a) qmat_mul_ex(a, x, &r->l.gdn.a, 0);
+    if (b) qmat_mul_ex(b, x, &r->l.gdn.b, 0);
+    r->m.pos = pos;
+    gdn_forward(&r->m, &r->l, x, out);
+}
+
+/* T consecutive tokens from position base (gdn_decode_block) */
+void ref_gdn_block(void *h, const float *x, int T, int base, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    gdn_decode_block(&r->m, &r->l, x, T, base, out);
+}
+
+void *ref_attn_create(const or_attn *A, float *k_cache, float *v_cache, int max_seq) {
+    RefLayer *r = (RefLayer *)calloc(1, sizeof(RefLayer));
+    if (!r) return NULL;
+    Cfg *c = &r->m.c;
+    c->n_layers = 1;
+    c->hidden = A->H;
+    c->n_heads = A->nh;
+    c->n_kv_heads = A->nkv;
+    c->head_dim = A->hd;
+    c->partial_rotary = (float)A->rd / (float)A->hd;
+    c->theta = A->theta;
+    c->eps = A->eps;
+    r->m.layer = &r->l;
+    r->m.max_seq = max_seq;
+    r->l.type = LT_FULL;
+    static int serial;
+    const int ln = __atomic_fetch_add(&serial, 1, __ATOMIC_RELAXED);
+    char nm[160];
+    AttnW *w = &r->l.attn;
+    snprintf(nm, sizeof(nm), "mixer.%d.self_attn.q_proj.weight", ln);
+    w->q = ref_qmat_named(&A->q, nm);
+    snprintf(nm, sizeof(nm), "mixer.%d.self_attn.k_proj.weight", ln);
+    w->k = ref_qmat_named(&A->k, nm);
+    snprintf(nm, sizeof(nm), "mixer.%d.self_attn.v_proj.weight", ln);
+    w->v = ref_qmat_named(&A->v, nm);
+    snprintf(nm, sizeof(nm), "mixer.%d.self_attn.o_proj.weight", ln);
+    w->o = ref_qmat_named(&A->o, nm);
+    w->q_norm = (float *)A->q_norm;
+    w->k_norm = (float *)A->k_norm;
+    w->k_cache = k_cache;
+    w->v_cache = v_cache;
+    return r;
+}
+
+void ref_attn_forward(void *h, const float *x, int pos, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    r->m.pos = pos;
+    attn_forward(&r->m, &r->l, x, out);
+}
+
+/* T consecutive rows from position base (attn_prefill_layer) */
+void ref_attn_prefill(void *h, const float *x, int T, int base, float *out) {
+    RefLayer *r = (RefLayer *)h;
+    attn_prefill_layer(&r->m, &r->l, x, T, base, out);
+}
+
+void ref_mixer_destroy(void *h) {
+    RefLayer *r = (RefLayer *)h;
+    if (!r) return;
+#ifdef COLI_CUDA
+    if (r->l.type == LT_LINEAR) {
+        GdnW *w = &r->l.gdn;
+        cuda_qmat_detach(&w->qkv);
+        cuda_qmat_detach(&w->z);
+        cuda_qmat_detach(&w->out);
+        float *d[] = {w->d_conv, w->d_A_log, w->d_dt_bias, w->d_norm, w->d_conv_state, w->d_state};
+        for (size_t i = 0; i < sizeof(d) / sizeof(d[0]); i++)
+            if (d[i]) coli_cuda_free(cuda_rt.ctx, d[i]);
+    } else {
+        AttnW *w = &r->l.attn;
+        cuda_qmat_detach(&w->q);
+        cuda_qmat_detach(&w->k);
+        cuda_qmat_detach(&w->v);
+        cuda_qmat_detach(&w->o);
+        float *d[] = {w->d_q_norm, w->d_k_norm, w->d_k_cache, w->d_v_cache};
+        for (size_t i = 0; i < sizeof(d) / sizeof(d[0]); i++)
+            if (d[i]) coli_cuda_free(cuda_rt.ctx, d[i]);
+    }
+#endif
+    free(r);
+}
+
 void ref_moe_forward(void *h, const float *x, float *out) {
     RefLayer *r = (RefLayer *)h;
     moe_forward(&r->m, &r->l, x, out);
@@ -338,6 +469,15 @@ void ref_cuda_counters(unsigned long long out[7]) {
     out[4] = cuda_rt.batch_transactions;
     out[5] = cuda_rt.mlp_calls;
     out[6] = cuda_rt.q3_grouped_calls;
+}
+
+/* out: GDN device calls, attention device calls, attention prefill calls
+ * (cuda_rt counters bumped by cuda_gdn_try 889, cuda_gdn_block_try 890,
+ * cuda_attn_try 940 and cuda_attn_prefill_try 968) */
+void ref_cuda_mixer_counters(unsigned long long out[3]) {
+    out[0] = (unsigned long long)cuda_rt.gdn_calls;
+    out[1] = (unsigned long long)cuda_rt.attn_calls;
+    out[2] = (unsigned long long)cuda_rt.attn_prefill_calls;
 }
 
 /* A speculative block of T = 2..8 tokens (moe_cuda_block, c/qwen.c:3741):

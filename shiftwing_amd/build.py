@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["context.hip", "backend.hip", "moe.hip", "moe_decode.hip", "moe_stack.hip", "head.hip", "container.cpp"]
+SOURCES = ["context.hip", "backend.hip", "moe.hip", "moe_decode.hip", "moe_stack.hip", "head.hip", "mixer.hip", "container.cpp"]
 LIB = os.path.join(HERE, "libshiftwing_moe.so")
 # the same sources with the host code under AddressSanitizer and
 # UndefinedBehaviorSanitizer (clang's runtime, linked shared: a process loads

@@ -733,76 +733,3 @@ extern "C" int coli_cuda_shared_q8_mlp_batch_device_scale(
   return shared_q8(ctx, y, x, device_scale, 1, gate_q, gate_s, gate_row_bytes, up_q, up_s, up_row_bytes,
                    down_q, down_s, down_row_bytes, batch, hidden, intermediate);
 }
-
-// ---------------------------------------------------------------------------
-// Entry points outside the MoE path (backend_cuda.h:149-236).  c/qwen.c links
-// against them unconditionally (c/qwen.c:884, 900, 940, 966) but only calls
-// them when its CUDA_GDN / CUDA_ATTN switches are on (c/qwen.c:868, 925-926).
-// They are exported so the reference host links unchanged; each reports that
-// the path is not built here, and the reference host then runs those layers
-// on the CPU.
-// ---------------------------------------------------------------------------
-static int not_built(const char *entry, const char *path, const char *env) {
-  return fail_arg("%s: the %s path is not part of this MoE library; run the reference host with %s=0", entry,
-                  path, env);
-}
-
-extern "C" int coli_cuda_gdn_decode_q4_f16(ColiCuda *, float *, const float *, const float *, const float *,
-                                           const unsigned char *, const float *, int, int, const unsigned char *,
-                                           const float *, int, int, const unsigned char *, const float *, int, int,
-                                           const float *, const float *, const float *, const float *, float *,
-                                           float *, int, int, int, int, int, int, int, int, float) {
-  return not_built("coli_cuda_gdn_decode_q4_f16", "Gated DeltaNet", "CUDA_GDN");
-}
-extern "C" int coli_cuda_gdn_block_q4_f16(ColiCuda *, float *, const float *, const float *, const float *, int,
-                                          const unsigned char *, const float *, int, int, const unsigned char *,
-                                          const float *, int, int, const unsigned char *, const float *, int, int,
-                                          const float *, const float *, const float *, const float *, float *,
-                                          float *, int, int, int, int, int, int, int, int, float) {
-  return not_built("coli_cuda_gdn_block_q4_f16", "Gated DeltaNet", "CUDA_GDN");
-}
-extern "C" int coli_cuda_gdn_slots_q4_f16(ColiCuda *, float *, const float *, const float *, const float *, int,
-                                          const int *, const int *, const unsigned char *, const float *, int, int,
-                                          const unsigned char *, const float *, int, int, const unsigned char *,
-                                          const float *, int, int, const float *, const float *, const float *,
-                                          const float *, float *, float *, int, int, int, int, int, int, int, int,
-                                          float) {
-  return not_built("coli_cuda_gdn_slots_q4_f16", "Gated DeltaNet", "CUDA_GDN");
-}
-extern "C" int coli_cuda_gdn_slots_q4_f16_device(ColiCuda *, float *, const float *, const float *, const float *,
-                                                 int, const int *, const int *, const unsigned char *,
-                                                 const float *, int, int, const unsigned char *, const float *, int,
-                                                 int, const unsigned char *, const float *, int, int, const float *,
-                                                 const float *, const float *, const float *, float *, float *, int,
-                                                 int, int, int, int, int, int, int, float) {
-  return not_built("coli_cuda_gdn_slots_q4_f16_device", "Gated DeltaNet", "CUDA_GDN");
-}
-extern "C" int coli_cuda_gqa_decode_q4_f16(ColiCuda *, float *, const float *, const unsigned char *,
-                                           const float *, int, int, const unsigned char *, const float *, int, int,
-                                           const unsigned char *, const float *, int, int, const void *,
-                                           const float *, int, int, int, const float *, const float *, float *,
-                                           float *, int, int, int, int, int, int, int, float, float) {
-  return not_built("coli_cuda_gqa_decode_q4_f16", "GQA attention", "CUDA_ATTN");
-}
-extern "C" int coli_cuda_gqa_prefill_q4_f16(ColiCuda *, float *, const float *, int, int, const unsigned char *,
-                                            const float *, int, int, const unsigned char *, const float *, int, int,
-                                            const unsigned char *, const float *, int, int, const void *,
-                                            const float *, int, int, int, const float *, const float *, float *,
-                                            float *, int, int, int, int, int, int, int, float, float) {
-  return not_built("coli_cuda_gqa_prefill_q4_f16", "GQA attention", "CUDA_ATTN");
-}
-extern "C" int coli_cuda_gqa_slots_q4_f16(ColiCuda *, float *, const float *, int, const int *, const int *,
-                                          const unsigned char *, const float *, int, int, const unsigned char *,
-                                          const float *, int, int, const unsigned char *, const float *, int, int,
-                                          const void *, const float *, int, int, int, const float *, const float *,
-                                          float *, float *, int, int, int, int, int, int, int, int, float, float) {
-  return not_built("coli_cuda_gqa_slots_q4_f16", "GQA attention", "CUDA_ATTN");
-}
-extern "C" int coli_cuda_gqa_slots_q4_f16_device(ColiCuda *, float *, const float *, int, const int *,
-                                                 const int *, const unsigned char *, const float *, int, int,
-                                                 const unsigned char *, const float *, int, int,
-                                                 const unsigned char *, const float *, int, int, const void *,
-                                                 const float *, int, int, int, const float *, const float *, float *,
-                                                 float *, int, int, int, int, int, int, int, int, float, float) {
-  return not_built("coli_cuda_gqa_slots_q4_f16_device", "GQA attention", "CUDA_ATTN");
-}

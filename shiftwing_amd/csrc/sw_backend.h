@@ -41,6 +41,7 @@ enum Scratch {
   kScrStack,       // persistent decode: router records, exact logits, h records
   kScrBlock,       // MoE block: normalised activations and the MoE output
   kScrHead,        // output head: quantised normalised rows and their scales
+  kScrMixer,       // Gated DeltaNet / GQA layers: staged inputs, projections, partials
   kScrCount
 };
 

@@ -295,3 +295,73 @@ def test_bridge_declines_layers_it_does_not_take(glue, oracle):
         assert glue.lib.ref_sw_disabled() == 0
     finally:
         glue.lib.ref_layer_destroy(h)
+
+
+def test_reference_glue_mixers(glue, oracle):
+    """The reference's own mixer layers with its device switches on (CUDA_GDN
+    and CUDA_ATTN default on, c/qwen.c:868, 919; CUDA_SPEC_GDN=1 for the
+    speculative block, 912): gdn_forward -> cuda_gdn_try ->
+    coli_cuda_gdn_decode_q4_f16, gdn_decode_block -> cuda_gdn_block_try ->
+    coli_cuda_gdn_block_q4_f16, attn_forward -> cuda_attn_try ->
+    coli_cuda_gqa_decode_q4_f16 and attn_prefill_layer ->
+    cuda_attn_prefill_try -> coli_cuda_gqa_prefill_q4_f16, each on this
+    library with the state kept on the device between calls, against the
+    oracle's CPU restatement of the same layers (bit-exact with c/qwen.c)."""
+    from oracle import pyoracle as po
+    lib = glue.lib
+    lib.ref_cuda_mixer_counters.argtypes = [C.POINTER(C.c_ulonglong)]
+
+    def counters():
+        out = (C.c_ulonglong * 3)()
+        lib.ref_cuda_mixer_counters(out)
+        return [int(v) for v in out]
+
+    glue.lib.ref_cuda_set_f16(1)
+    os.environ["CUDA_SPEC_GDN"] = "1"
+    rng = np.random.default_rng(93)
+    g = po.HostGdn(91, 2048, 16, 32, 128, 128)
+    rm = po.RefMixer(lib, g)
+    cs, st = [a[0] for a in g.new_state()]
+    try:
+        for pos in range(4):
+            print(f"[reference glue] gdn_forward pos {pos}", flush=True)
+            x = rng.standard_normal(2048).astype(np.float32)
+            before = counters()
+            got, a, b = rm.gdn(x, pos)
+            assert counters()[0] == before[0] + 1, "gdn_forward did not take the device path"
+            want = po.oracle_gdn_step(oracle, g, x, a, b, pos, cs, st)
+            assert_close_rms(got, want, 1e-3, f"reference gdn_forward pos {pos}")
+        X = rng.standard_normal((3, 2048)).astype(np.float32)
+        print("[reference glue] gdn_decode_block T=3 from 4", flush=True)
+        before = counters()
+        got = rm.gdn_block(X, 4)
+        assert counters()[0] == before[0] + 3, "gdn_decode_block did not take the device block path"
+        for t in range(3):
+            a, b = po.oracle_gdn_gates(oracle, g, X[t])
+            want = po.oracle_gdn_step(oracle, g, X[t], a, b, 4 + t, cs, st)
+            assert_close_rms(got[t], want, 1e-3, f"reference gdn_decode_block token {t}")
+    finally:
+        rm.close()
+        os.environ.pop("CUDA_SPEC_GDN", None)
+
+    at = po.HostAttn(92, 2048, 16, 2, 256, 64, o_fmt=1)
+    ra = po.RefMixer(lib, at, max_seq=64)
+    kc, vc = [a[0] for a in at.new_cache(64)]
+    try:
+        for pos in range(20):
+            x = rng.standard_normal(2048).astype(np.float32)
+            before = counters()
+            got = ra.attn(x, pos)
+            assert counters()[1] == before[1] + 1, "attn_forward did not take the device path"
+            want = po.oracle_attn_step(oracle, at, x, pos, kc, vc)
+            assert_close_rms(got, want, 1e-3, f"reference attn_forward pos {pos}")
+        print("[reference glue] attn_prefill_layer 20 rows from 20", flush=True)
+        X = rng.standard_normal((20, 2048)).astype(np.float32)
+        before = counters()
+        got = ra.attn_prefill(X, 20)
+        assert counters()[2] == before[2] + 1, "attn_prefill_layer did not take the device prefill path"
+        for r in range(20):
+            want = po.oracle_attn_step(oracle, at, X[r], 20 + r, kc, vc)
+            assert_close_rms(got[r], want, 1e-3, f"reference attn_prefill_layer row {20 + r}")
+    finally:
+        ra.close()

@@ -304,3 +304,128 @@ def test_rmsnorm_zero_matches_compiled_reference_and_closed_form(oracle):
         r = np.float32(1) / np.sqrt(np.float32(ms / np.float32(n) + np.float32(1e-6)))
         fma_differs += not np.array_equal(((x * r) * (np.float32(1) + w)).astype(np.float32), b)
     assert fma_differs > 0
+
+
+# ------------------------------------------- the mixer layers around the MoE
+def _avx512_reference():
+    """The compiled reference when it is an AVX-512 build (the lane structure
+    the oracle's grouped dots restate), else None."""
+    from oracle.pyoracle import Reference, ref_lib_candidates
+    c = [p for p in ref_lib_candidates() if p.endswith(("libref_native.so", "libref_v4.so"))]
+    return Reference(c[0]) if c else None
+
+
+def test_gdn_and_attention_match_compiled_reference():
+    """or_gdn_forward / or_attn_forward (c/qwen.c:3005, 2907, 3094, 3031)
+    against the reference's own gdn_forward and attn_forward compiled in place:
+    bit for bit over several decode steps with the state carried, including
+    the gate projections a and b and every conv and recurrent state word.
+    The restatement's unfused sums (q/k norms, memory read-out, output sum)
+    and fused updates are the ones gcc emits for c/qwen.c at its flags; a
+    plausible slip (a fused sum, a dropped 1/sqrt(dk), the rotation sign)
+    breaks the equality."""
+    from oracle import pyoracle as po
+    ref = _avx512_reference()
+    if ref is None:
+        pytest.skip("no AVX-512 build of the compiled reference (oracle/_ref)")
+    orc = po.Oracle()
+    rng = np.random.default_rng(101)
+    g = po.HostGdn(7, 512, 2, 8, 128, 128)
+    rm = po.RefMixer(ref.lib, g)
+    cs, st = [a[0] for a in g.new_state()]
+    for pos in range(6):
+        x = rng.standard_normal(512).astype(np.float32)
+        want, a, b = rm.gdn(x, pos)
+        a2, b2 = po.oracle_gdn_gates(orc, g, x)
+        assert np.array_equal(_bits(a), _bits(a2)) and np.array_equal(_bits(b), _bits(b2))
+        got = po.oracle_gdn_step(orc, g, x, a, b, pos, cs, st)
+        assert np.array_equal(_bits(got), _bits(want)), pos
+        assert np.array_equal(_bits(st), _bits(rm.state)) and np.array_equal(_bits(cs), _bits(rm.conv_state))
+    for o_fmt in (1, 4):
+        at = po.HostAttn(8 + o_fmt, 512, 4, 2, 256, 64, o_fmt=o_fmt)
+        ra = po.RefMixer(ref.lib, at, max_seq=24)
+        kc, vc = [a[0] for a in at.new_cache(24)]
+        for pos in range(20):
+            x = rng.standard_normal(512).astype(np.float32)
+            want = ra.attn(x, pos)
+            got = po.oracle_attn_step(orc, at, x, pos, kc, vc)
+            assert np.array_equal(_bits(got), _bits(want)), (o_fmt, pos)
+        assert np.array_equal(_bits(kc), _bits(ra.k_cache)) and np.array_equal(_bits(vc), _bits(ra.v_cache))
+
+
+def test_gdn_first_step_closed_form(oracle):
+    """From a zero state the delta rule gives S = beta k_hat v^T, so the
+    pre-norm output of value head h is beta (k_hat . q_hat) / sqrt(dk) v_h;
+    with the conv kernel K = 1 (tap weight w) the mixer value of a channel is
+    silu(w raw), raw = W x.  fp32 weights (format 0) and the identity out
+    projection expose the gated RMS-normed core directly.  Checked in fp64
+    against the oracle's fp32 path."""
+    from oracle import pyoracle as po
+    H, kh, vh, dk, dv = 64, 1, 2, 16, 16
+    rng = np.random.default_rng(5)
+    g = po.HostGdn(3, 512, 2, 4, 128, 128)  # a template; every field is replaced below
+    cd, vd = 2 * kh * dk + vh * dv, vh * dv
+    Wqkv = rng.standard_normal((cd, H)).astype(np.float32) * 0.2
+    Wz = rng.standard_normal((vd, H)).astype(np.float32) * 0.2
+    Wo = np.eye(H, vd, dtype=np.float32)
+    conv = np.full((cd, 1), 0.75, np.float32)
+    A_log = np.array([0.3, -0.2], np.float32)
+    dt_bias = np.array([0.1, 0.4], np.float32)
+    norm = (1 + rng.standard_normal(dv) * 0.1).astype(np.float32)
+    keep = [Wqkv, Wz, Wo, conv, A_log, dt_bias, norm]
+    g.H, g.kh, g.vh, g.dk, g.dv, g.K = H, kh, vh, dk, dv, 1
+    g.qkv, g.z, g.out = po.HostQMat(0, cd, H, f=Wqkv), po.HostQMat(0, vd, H, f=Wz), po.HostQMat(0, H, vd, f=Wo)
+    g.st = po.OrGdn(H, kh, vh, dk, dv, 1, 1e-6, g.qkv.st, g.z.st, g.a.st, g.b.st, g.out.st,
+                    po.ptr(conv, po.f32p), po.ptr(A_log, po.f32p), po.ptr(dt_bias, po.f32p), po.ptr(norm, po.f32p))
+    x = rng.standard_normal(H).astype(np.float32)
+    a = np.array([0.5, -1.0], np.float32)
+    b = np.array([0.2, 1.5], np.float32)
+    cs = np.zeros((1, cd), np.float32)
+    st = np.zeros((vh, dk, dv), np.float32)
+    out = po.oracle_gdn_step(oracle, g, x, a, b, 0, cs, st)
+    x64 = x.astype(np.float64)
+    raw = Wqkv.astype(np.float64) @ x64
+    mix = 0.75 * raw / (1 + np.exp(-0.75 * raw))
+    q, k, v = mix[:dk], mix[dk:2 * dk], mix[2 * dk:]
+    qh = q / np.sqrt(q @ q + 1e-6) / np.sqrt(dk)
+    kh_ = k / np.sqrt(k @ k + 1e-6)
+    z = Wz.astype(np.float64) @ x64
+    core = np.zeros(vd)
+    for h in range(vh):
+        beta = 1 / (1 + np.exp(-b[h]))
+        o = beta * (kh_ @ qh) * v[h * dv:(h + 1) * dv]
+        r = 1 / np.sqrt(np.mean(o * o) + 1e-6)
+        zz = z[h * dv:(h + 1) * dv]
+        core[h * dv:(h + 1) * dv] = o * r * norm * zz / (1 + np.exp(-zz))
+        # the state after one step is beta k_hat v^T (the decay multiplies zeros)
+        assert np.allclose(st[h], beta * np.outer(kh_, v[h * dv:(h + 1) * dv]), rtol=2e-4, atol=1e-6)
+    assert np.allclose(out, Wo.astype(np.float64) @ core, rtol=2e-4, atol=1e-5)
+    del keep
+
+
+def test_attention_first_position_closed_form(oracle):
+    """At position 0 the softmax has one key, so the context of query head h is
+    v_{kv(h)} * sigmoid(gate_h) and the output is W_o of that, whatever q, k
+    and the rotation are; the cache row 0 holds the RMS-normed, rotated k
+    (at position 0 the rotation is the identity) and the raw v."""
+    from oracle import pyoracle as po
+    rng = np.random.default_rng(6)
+    at = po.HostAttn(12, 256, 4, 2, 64, 16, o_fmt=4)
+    kc, vc = [a[0] for a in at.new_cache(4)]
+    x = rng.standard_normal(256).astype(np.float32)
+    out = po.oracle_attn_step(oracle, at, x, 0, kc, vc)
+    qp = oracle.qmat_mul(x, at.q, 0).astype(np.float64)
+    v = oracle.qmat_mul(x, at.v, 0).astype(np.float64)
+    k = oracle.qmat_mul(x, at.k, 0).astype(np.float64)
+    ctx = np.zeros(at.nh * at.hd)
+    for h in range(at.nh):
+        gate = qp[h * 2 * at.hd + at.hd:(h + 1) * 2 * at.hd]
+        kv = h // (at.nh // at.nkv)
+        ctx[h * at.hd:(h + 1) * at.hd] = v[kv * at.hd:(kv + 1) * at.hd] / (1 + np.exp(-gate))
+    want = oracle.qmat_mul(ctx.astype(np.float32), at.o, 0)
+    assert np.allclose(out, want, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(vc[0], v.astype(np.float32))
+    for h in range(at.nkv):
+        kh_ = k[h * at.hd:(h + 1) * at.hd]
+        kn = kh_ / np.sqrt(np.mean(kh_ * kh_) + 1e-6) * (1 + at.k_norm.astype(np.float64))
+        assert np.allclose(kc[0, h * at.hd:(h + 1) * at.hd], kn, rtol=1e-5, atol=1e-6)
