@@ -81,7 +81,22 @@ struct ProjArgs {
   int K;
   long long conv_slot_stride;
   MixTok tok;
+  // optional per-(token, head) activation scale r = 1/sqrt(sum(msp) / hw + eps),
+  // msp [B][cols / hw][nsp] partial sums of squares (the Gated DeltaNet
+  // output's RMS norm, applied as the out projection reads its input)
+  const float *msp;
+  int nsp, hw;
+  float eps;
 };
+
+__device__ __forceinline__ float proj_xscale(const ProjArgs &a, int t, int c) {
+  if (!a.msp) return 1.0f;
+  const int nh = a.cols / a.hw, h = c / a.hw;
+  const float *m = a.msp + ((size_t)t * nh + h) * a.nsp;
+  float ms = 0.0f;
+  for (int k = 0; k < a.nsp; k++) ms += m[k];
+  return 1.f / sqrtf(ms / (float)a.hw + a.eps);
+}
 
 // y[t][row] = sum_g s[row][g] * sum_{i in g} code(row, i) * x[t][i]
 // FMT 4: int4 low nibble first, code = nibble - 8, one scale per group;
@@ -127,7 +142,8 @@ __global__ __launch_bounds__(256) void k_mix_proj(ProjArgs a) {
       const int t = t0 + tt, c = c0 + ci * CH + l * CPL + 4 * k;
       const bool ok = u < total && t < a.B && c < a.cols;
       const float4 ld = *(const float4 *)(a.x + (ok ? (size_t)t * a.ldx + c : 0));
-      v[j] = ok ? ld : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float sc = ok ? proj_xscale(a, t, c) : 0.0f;
+      v[j] = ok ? make_float4(ld.x * sc, ld.y * sc, ld.z * sc, ld.w * sc) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   auto stage_put = [&](const float4(&v)[8], int b0, int total) {
@@ -338,10 +354,13 @@ __global__ __launch_bounds__(256) void k_mix_proj(ProjArgs a) {
 
 // ---------------------------------------------------------------------------
 // Gated DeltaNet recurrence (gdn_rule_step, c/qwen.c:2907-2927) for one value
-// head and one group of tokens that share a slot, in order.  Lane layout: wave
-// w holds value columns j = 32w + (lane & 31); lane half (lane >> 5) holds key
-// rows [64 half, 64 half + 64) of those columns in registers.
-// grid (value_heads, groups), 64 * max(2, ceil(dv / 32)) threads.
+// head, one run of 32 value columns and one group of tokens that share a
+// slot, in order: one wave, lanes j = lane & 31 hold the columns, lane half
+// (lane >> 5) holds key rows [64 half, 64 half + 64) of them in registers
+// (dk <= 128), read and written once per call.  The head's RMS norm couples
+// its columns, so the wave writes u = o * norm * silu(z) and its partial sum
+// of o^2; the out projection applies 1/sqrt(sum / dv + eps) as it reads u.
+// grid (value_heads * ceil(dv / 32), groups), 64 threads.
 struct GdnGroups {
   int n;
   int start[kMixMaxTok + 1];
@@ -352,9 +371,9 @@ struct GdnArgs {
   const float *A_log, *dt_bias, *norm;
   float *state;  // [slot][vh][dk][dv]
   long long state_slot_stride;
-  float *core;  // [B][vd]
+  float *core;  // [B][vd]: o * norm * silu(z)
+  float *msp;   // [B][vh][ceil(dv / 32)]: partial sums of o^2
   int kh, vh, dk, dv;
-  float eps;
   MixTok tok;
   GdnGroups grp;
 };
@@ -363,31 +382,40 @@ __device__ __forceinline__ float softplus_ref(float x) {
   return x > 20.f ? x : (x < -20.f ? expf(x) : log1pf(expf(x)));
 }
 
-__global__ __launch_bounds__(512) void k_gdn_recur(GdnArgs g) {
-  const int h = blockIdx.x, gi = blockIdx.y;
+__global__ __launch_bounds__(64) void k_gdn_recur(GdnArgs g) {
+  const int nsp = (g.dv + 31) / 32;
+  const int h = blockIdx.x / nsp, js = blockIdx.x % nsp, gi = blockIdx.y;
   if (gi >= g.grp.n) return;
-  __shared__ float sq[128], sk[128], sred[8];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int half = lane >> 5, j = wave * 32 + (lane & 31), i0 = half * 64;
+  __shared__ float sq[128], sk[128];
+  const int lane = threadIdx.x, half = lane >> 5, j = js * 32 + (lane & 31), i0 = half * 64;
   const int dk = g.dk, dv = g.dv, kd = g.kh * dk, vd = g.vh * dv, C = 2 * kd + vd;
   const int hk = h / (g.vh / g.kh);
-  const bool jl = j < dv;
   const int t_first = g.grp.tok[g.grp.start[gi]];
   float *st = g.state + (size_t)tok_slot(g.tok, t_first) * g.state_slot_stride + (size_t)h * dk * dv;
+  // dv is a multiple of 32, so every lane's column exists; a half holds 64
+  // key rows when dk = 128 (the loads and stores then take no branches)
+  const bool rows64 = i0 + 64 <= dk;
   float S[64];
+  if (rows64) {
 #pragma unroll
-  for (int m = 0; m < 64; m++) S[m] = (jl && i0 + m < dk) ? st[(size_t)(i0 + m) * dv + j] : 0.0f;
+    for (int m = 0; m < 64; m++) S[m] = st[(size_t)(i0 + m) * dv + j];
+  } else {
+#pragma unroll
+    for (int m = 0; m < 64; m++) S[m] = (i0 + m < dk) ? st[(size_t)(i0 + m) * dv + j] : 0.0f;
+  }
   const float invsqrt = 1.f / sqrtf((float)dk);
   const float Ah = expf(g.A_log[h]);
+  const float nj = g.norm[j];
   for (int gt = g.grp.start[gi]; gt < g.grp.start[gi + 1]; gt++) {
     const int t = g.grp.tok[gt];
     const float *mt = g.mix + (size_t)t * C;
     __syncthreads();
-    if (threadIdx.x < 128) {
-      const int i = threadIdx.x;
+    for (int i = lane; i < 128; i += 64) {
       sq[i] = i < dk ? mt[hk * dk + i] : 0.0f;
       sk[i] = i < dk ? mt[kd + hk * dk + i] : 0.0f;
     }
+    const float v = mt[2 * kd + h * dv + j];
+    const float zt = g.z[(size_t)t * vd + (size_t)h * dv + j];
     __syncthreads();
     float pq = 0.0f, pk = 0.0f;
     for (int i = lane; i < 128; i += 64) {
@@ -398,36 +426,39 @@ __global__ __launch_bounds__(512) void k_gdn_recur(GdnArgs g) {
     const float kn = 1.f / sqrtf(wave_sum_dpp(pk) + 1e-6f);
     const float beta = sigmoid_ref(g.b[(size_t)t * g.vh + h]);
     const float decay = expf(-Ah * softplus_ref(g.a[(size_t)t * g.vh + h] + g.dt_bias[h]));
-    float mem = 0.0f;
+    float mem0 = 0.0f, mem1 = 0.0f;
 #pragma unroll
-    for (int m = 0; m < 64; m++) {
+    for (int m = 0; m < 64; m += 2) {
       S[m] *= decay;
-      mem = __builtin_fmaf(S[m], sk[i0 + m] * kn, mem);
+      S[m + 1] *= decay;
+      mem0 = __builtin_fmaf(S[m], sk[i0 + m] * kn, mem0);
+      mem1 = __builtin_fmaf(S[m + 1], sk[i0 + m + 1] * kn, mem1);
     }
+    float mem = mem0 + mem1;
     mem += __shfl_xor(mem, 32);
-    const float v = jl ? mt[2 * kd + h * dv + j] : 0.0f;
     const float delta = (v - mem) * beta;
-    float o = 0.0f;
+    float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-    for (int m = 0; m < 64; m++) {
+    for (int m = 0; m < 64; m += 2) {
       S[m] = __builtin_fmaf(sk[i0 + m] * kn, delta, S[m]);
-      o = __builtin_fmaf(S[m], sq[i0 + m] * qn * invsqrt, o);
+      S[m + 1] = __builtin_fmaf(sk[i0 + m + 1] * kn, delta, S[m + 1]);
+      o0 = __builtin_fmaf(S[m], sq[i0 + m] * qn * invsqrt, o0);
+      o1 = __builtin_fmaf(S[m + 1], sq[i0 + m + 1] * qn * invsqrt, o1);
     }
+    float o = o0 + o1;
     o += __shfl_xor(o, 32);
-    const float p2 = wave_sum_dpp((half == 0 && jl) ? o * o : 0.0f);
-    if (lane == 0) sred[wave] = p2;
-    __syncthreads();
-    float ms = 0.0f;
-    for (int w = 0; w < nw; w++) ms += sred[w];
-    const float rinv = 1.f / sqrtf(ms / (float)dv + g.eps);
-    if (half == 0 && jl) {
-      const size_t at = (size_t)t * vd + (size_t)h * dv + j;
-      g.core[at] = o * rinv * g.norm[j] * silu_ref(g.z[at]);
-    }
+    const float p2 = wave_sum_dpp(half == 0 ? o * o : 0.0f);
+    if (half == 0) g.core[(size_t)t * vd + (size_t)h * dv + j] = o * nj * silu_ref(zt);
+    if (lane == 0) g.msp[((size_t)t * g.vh + h) * nsp + js] = p2;
   }
+  if (rows64) {
 #pragma unroll
-  for (int m = 0; m < 64; m++)
-    if (jl && i0 + m < dk) st[(size_t)(i0 + m) * dv + j] = S[m];
+    for (int m = 0; m < 64; m++) st[(size_t)(i0 + m) * dv + j] = S[m];
+  } else {
+#pragma unroll
+    for (int m = 0; m < 64; m++)
+      if (i0 + m < dk) st[(size_t)(i0 + m) * dv + j] = S[m];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -522,6 +553,7 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
   constexpr int KQ = HD / 4, NT16 = HD / 16, PSZ = 16 * HD + 32;
   __shared__ float s_m[4][16], s_l[4][16];
   __shared__ float s_o[16 * HD];
+  __shared__ float s_q[16 * 4 * (HD / 4 + 4)];
   const int t = blockIdx.y, kvh = blockIdx.x / a.S, s = blockIdx.x % a.S;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
   const int G = a.nh / a.nkv;
@@ -532,19 +564,17 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
   const size_t sbase = (size_t)tok_slot(a.tok, t) * a.slot_stride + (size_t)kvh * HD;
   const float *kc = a.k_cache + sbase, *vc = a.v_cache + sbase;
 
-  float qf[KQ];
-  {
-    const bool hv = n < G;
-    const float *qr = a.q + (size_t)t * a.nh * HD + (size_t)(kvh * G + (hv ? n : 0)) * HD + kg * KQ;
-#pragma unroll
-    for (int i = 0; i < KQ; i += 4) {
-      float4 v = hv ? *(const float4 *)(qr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-      qf[i] = v.x;
-      qf[i + 1] = v.y;
-      qf[i + 2] = v.z;
-      qf[i + 3] = v.w;
-    }
+  // the kv head's queries in LDS, [head n][lane group g][KQ + 4] (heads past
+  // G are zero); a lane reads its B operands from there, keeping registers
+  // for the K and V values of a whole block in flight
+  for (int u = threadIdx.x; u < 16 * HD / 4; u += 256) {
+    const int hn = u / (HD / 4), e4 = u % (HD / 4), g4 = e4 / (KQ / 4), i4 = e4 % (KQ / 4);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (hn < G) v = *(const float4 *)(a.q + (size_t)t * a.nh * HD + (size_t)(kvh * G + hn) * HD + 4 * e4);
+    *(float4 *)(s_q + (hn * 4 + g4) * (KQ + 4) + 4 * i4) = v;
   }
+  __syncthreads();
+  const float *qs = s_q + (n * 4 + kg) * (KQ + 4);
   v4f o[NT16];
 #pragma unroll
   for (int d = 0; d < NT16; d++) o[d] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -568,13 +598,16 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
 #pragma unroll
       for (int d = 0; d < NT16; d++) vv[s2][d] = vr[16 * d];
     }
+    // all of the block's K and V loads are in flight before the first MFMA
+    asm volatile("" ::: "memory");
     v4f c0 = v4f{0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0;
 #pragma unroll
     for (int i = 0; i < KQ / 4; i++) {
-      c0 = mfma_f32_16x16x4(kv[i].x, qf[4 * i], c0);
-      c1 = mfma_f32_16x16x4(kv[i].y, qf[4 * i + 1], c1);
-      c2 = mfma_f32_16x16x4(kv[i].z, qf[4 * i + 2], c2);
-      c3 = mfma_f32_16x16x4(kv[i].w, qf[4 * i + 3], c3);
+      const float4 qv = *(const float4 *)(qs + 4 * i);
+      c0 = mfma_f32_16x16x4(kv[i].x, qv.x, c0);
+      c1 = mfma_f32_16x16x4(kv[i].y, qv.y, c1);
+      c2 = mfma_f32_16x16x4(kv[i].z, qv.z, c2);
+      c3 = mfma_f32_16x16x4(kv[i].w, qv.w, c3);
     }
     const v4f sc = (c0 + c1) + (c2 + c3);
     float sv[4];
@@ -682,11 +715,18 @@ __global__ __launch_bounds__(256) void k_gqa_combine(CombArgs c) {
   const float *op = base + (size_t)n * hd + j;
   float O0 = 0.0f, O1 = 0.0f, O2 = 0.0f, O3 = 0.0f;
   int s = 0;
-  for (; s + 4 <= c.S; s += 4) {
-    O0 = __builtin_fmaf(op[(size_t)s * psz], s_w[s], O0);
-    O1 = __builtin_fmaf(op[(size_t)(s + 1) * psz], s_w[s + 1], O1);
-    O2 = __builtin_fmaf(op[(size_t)(s + 2) * psz], s_w[s + 2], O2);
-    O3 = __builtin_fmaf(op[(size_t)(s + 3) * psz], s_w[s + 3], O3);
+  for (; s + 16 <= c.S; s += 16) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = op[(size_t)(s + k) * psz];
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 16; k += 4) {
+      O0 = __builtin_fmaf(v[k], s_w[s + k], O0);
+      O1 = __builtin_fmaf(v[k + 1], s_w[s + k + 1], O1);
+      O2 = __builtin_fmaf(v[k + 2], s_w[s + k + 2], O2);
+      O3 = __builtin_fmaf(v[k + 3], s_w[s + k + 3], O3);
+    }
   }
   for (; s < c.S; s++) O0 = __builtin_fmaf(op[(size_t)s * psz], s_w[s], O0);
   const size_t at = (size_t)t * c.nh * hd + (size_t)h * hd + j;
@@ -707,17 +747,25 @@ bool q8_ok(const void *q, const float *s, int rows, int cols, int rb) {
   return q && s && rows > 0 && cols > 0 && cols % 16 == 0 && rb >= cols && rb % 16 == 0 && ((uintptr_t)q & 15) == 0;
 }
 
-// The one- and two-token form of k_mix_proj without LDS: a wave's lanes read
-// their own 32 (int4) or 16 (int8) activations of each chunk straight from
-// global memory (L2-resident, shared by the workgroups), so the weight and
-// activation loads of a chunk issue together and no barrier separates them.
-// One workgroup per 4 x RW rows (RW = 4 for one token, 2 for two); the
-// epilogue is k_mix_proj's.  grid ceil(rows_total / (4 RW)), 256 threads, no LDS.
+// The one- and two-token form of k_mix_proj: no activation staging, the
+// columns split over waves.  A workgroup owns 4 rows for every wk of its 4
+// waves (wk = 1, 2 or 4 waves along the columns, by the row's chunk count);
+// each wave loads 16 bytes of each of its 4 rows per 64-lane chunk of its
+// column share together with the lanes' own 32 (int4) or 16 (int8)
+// activations, straight from global memory (L2-resident), so a wave's loads
+// issue at once and many short waves keep HBM busy.  The waves' partial sums
+// meet in LDS in a fixed order; the first wave of each row group finishes
+// the rows (k_mix_proj's epilogue).  grid ceil(rows_total / (16 / wk)),
+// 256 threads.
 template <int FMT, int NT, bool CONV>
 __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
-  constexpr int CPL = FMT == 4 ? 32 : 16, CH = 64 * CPL, F4 = CPL / 4, RW = NT == 1 ? 4 : 2;
+  constexpr int CPL = FMT == 4 ? 32 : 16, CH = 64 * CPL, F4 = CPL / 4, RW = 4;
+  __shared__ float s_part[4][RW][NT];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = (blockIdx.x * 4 + wave) * RW;
+  const int nch = (a.cols + CH - 1) / CH;
+  const int wk = nch >= 4 ? 4 : (nch >= 2 ? 2 : 1);
+  const int rg = wave / wk, kw = wave % wk;
+  const int r0 = (blockIdx.x * (4 / wk) + rg) * RW;
   const unsigned char *qrow[RW];
   const float *srow[RW];
   int mi[RW], rr[RW];
@@ -746,34 +794,46 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
   for (int r = 0; r < RW; r++)
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
-#pragma unroll 2
-  for (int c0 = 0; c0 < a.cols; c0 += CH) {
-    const int col = c0 + lane * CPL;
+  for (int ci = kw; ci < nch; ci += wk) {
+    const int col = ci * CH + lane * CPL;
     const bool ok = col < a.cols;
     const int cc = ok ? col : 0;
-    uint4 w[RW];
-    float sc[RW];
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-      w[r] = *(const uint4 *)(qrow[r] + (FMT == 4 ? cc / 2 : cc));
-      sc[r] = (ok && live[r]) ? (FMT == 4 ? srow[r][cc / a.gs] : 1.0f) : 0.0f;
-    }
-    float xv[NT][CPL];
+    // every load of the chunk is issued before the first use (the empty
+    // asm with a memory clobber keeps the compiler from sinking loads to
+    // their uses, which would serialise their latencies)
+    float4 xl[NT][F4];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const int tc = t < a.B ? t : 0;
 #pragma unroll
+      for (int k = 0; k < F4; k++) xl[t][k] = *(const float4 *)(a.x + (size_t)tc * a.ldx + cc + 4 * k);
+    }
+    uint4 w[RW];
+    float sl[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      w[r] = *(const uint4 *)(qrow[r] + (FMT == 4 ? cc / 2 : cc));
+      sl[r] = FMT == 4 ? srow[r][cc / a.gs] : 1.0f;
+    }
+    asm volatile("" ::: "memory");
+    float sc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) sc[r] = (ok && live[r]) ? sl[r] : 0.0f;
+    float xv[NT][CPL];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const float xs = proj_xscale(a, t < a.B ? t : 0, cc);
+#pragma unroll
       for (int k = 0; k < F4; k++) {
-        const float4 v = *(const float4 *)(a.x + (size_t)tc * a.ldx + cc + 4 * k);
-        xv[t][4 * k] = v.x;
-        xv[t][4 * k + 1] = v.y;
-        xv[t][4 * k + 2] = v.z;
-        xv[t][4 * k + 3] = v.w;
+        xv[t][4 * k] = xl[t][k].x * xs;
+        xv[t][4 * k + 1] = xl[t][k].y * xs;
+        xv[t][4 * k + 2] = xl[t][k].z * xs;
+        xv[t][4 * k + 3] = xl[t][k].w * xs;
       }
     }
     // int4: sum (n - 8) x = sum n x - 8 sum x, the nibbles n converted from
-    // the bytes of (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) (one
-    // v_cvt_f32_ubyte each); the lane's sum of x serves every row
+    // the bytes of (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F); the lane's
+    // sum of x serves every row
     float sx[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -817,11 +877,24 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
     }
   }
 #pragma unroll
+  for (int r = 0; r < RW; r++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const float v = wave_sum_dpp(acc[r][t]);
+      if (lane == 0) s_part[wave][r][t] = v;
+    }
+  __syncthreads();
+  if (kw != 0 || lane != 0) return;
+#pragma unroll
   for (int r = 0; r < RW; r++) {
+    if (!live[r]) continue;
     float red[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) red[t] = wave_sum_dpp(acc[r][t]);
-    if (!live[r] || lane != 0) continue;
+    for (int t = 0; t < NT; t++) {
+      float v = s_part[wave][r][t];
+      for (int k = 1; k < wk; k++) v += s_part[wave + k][r][t];
+      red[t] = v;
+    }
     const ProjMat &pm = a.m[mi[r]];
     if (CONV && mi[r] == 0) {
       const int ch = rr[r], C = a.m[0].rows, K = a.K;
@@ -858,8 +931,10 @@ void launch_proj_nt(ColiCuda *ctx, const ProjArgs &a) {
 
 template <int FMT, int NT, bool CONV>
 void launch_proj_direct(ColiCuda *ctx, const ProjArgs &a) {
-  constexpr int RW = NT == 1 ? 4 : 2;
-  k_mix_proj_direct<FMT, NT, CONV><<<(a.rows_total + 4 * RW - 1) / (4 * RW), 256, 0, ctx->stream>>>(a);
+  constexpr int CH = 64 * (FMT == 4 ? 32 : 16);
+  const int nch = (a.cols + CH - 1) / CH;
+  const int rows_per_block = 16 / (nch >= 4 ? 4 : (nch >= 2 ? 2 : 1));
+  k_mix_proj_direct<FMT, NT, CONV><<<(a.rows_total + rows_per_block - 1) / rows_per_block, 256, 0, ctx->stream>>>(a);
 }
 
 template <int FMT, bool CONV>
@@ -909,14 +984,16 @@ int gdn_run(ColiCuda *ctx, const GdnCall &c) {
       !q4_ok(c.out_q, c.out_s, H, vd, c.gs, c.out_rb, c.out_ng))
     return fail_arg("%s: int4 projections need group sizes and widths that are multiples of 32 and 16-byte rows",
                     c.name);
-  if (c.dk > 128 || c.dv > 256)
-    return fail_arg("%s: key_dim above 128 or value_dim above 256 is not supported", c.name);
+  if (c.dk > 128 || c.dv > 256 || c.dv % 32)
+    return fail_arg("%s: key_dim above 128, or value_dim above 256 or not a multiple of 32, is not supported",
+                    c.name);
   if (((uintptr_t)c.x & 15) || (H % 4)) return fail_arg("%s: activations must be 16-byte aligned", c.name);
   // scratch: [x][a][b] (host I/O), mix, z, core, y
   const size_t ox = 0, oa = ox + align_up((size_t)B * H * 4), ob = oa + align_up((size_t)B * c.vh * 4),
                om = ob + align_up((size_t)B * c.vh * 4), oz = om + align_up((size_t)B * C * 4),
                oc = oz + align_up((size_t)B * vd * 4), oy = oc + align_up((size_t)B * vd * 4),
-               total = oy + align_up((size_t)B * H * 4);
+               oms = oy + align_up((size_t)B * H * 4),
+               total = oms + align_up((size_t)B * c.vh * ((c.dv + 31) / 32) * 4);
   if (ensure_scratch(ctx, kScrMixer, total, c.name)) return -1;
   char *w = (char *)ctx->scratch[kScrMixer];
   const float *x = c.x, *av = c.a, *bv = c.b;
@@ -931,7 +1008,7 @@ int gdn_run(ColiCuda *ctx, const GdnCall &c) {
     av = (const float *)(w + oa);
     bv = (const float *)(w + ob);
   }
-  float *mix = (float *)(w + om), *z = (float *)(w + oz), *core = (float *)(w + oc);
+  float *mix = (float *)(w + om), *z = (float *)(w + oz), *core = (float *)(w + oc), *msp = (float *)(w + oms);
   float *y = c.device_io ? c.out : (float *)(w + oy);
 
   ProjArgs p;
@@ -965,11 +1042,11 @@ int gdn_run(ColiCuda *ctx, const GdnCall &c) {
   g.state = c.state;
   g.state_slot_stride = (long long)c.vh * c.dk * c.dv;
   g.core = core;
+  g.msp = msp;
   g.kh = c.kh;
   g.vh = c.vh;
   g.dk = c.dk;
   g.dv = c.dv;
-  g.eps = c.eps;
   g.tok = c.tok;
   // groups of tokens sharing a slot, each in token order
   int gslot[kMixMaxTok];
@@ -992,8 +1069,8 @@ int gdn_run(ColiCuda *ctx, const GdnCall &c) {
     for (int i = 0; i < count[k]; i++) g.grp.tok[at++] = members[k][i];
   }
   g.grp.start[ng] = at;
-  const int waves = c.dv <= 64 ? 2 : (c.dv + 31) / 32;
-  k_gdn_recur<<<dim3(c.vh, ng), 64 * waves, 0, ctx->stream>>>(g);
+  const int nsp = (c.dv + 31) / 32;
+  k_gdn_recur<<<dim3(c.vh * nsp, ng), 64, 0, ctx->stream>>>(g);
 
   ProjArgs o;
   memset(&o, 0, sizeof(o));
@@ -1005,6 +1082,10 @@ int gdn_run(ColiCuda *ctx, const GdnCall &c) {
   o.cols = vd;
   o.gs = c.gs;
   o.B = B;
+  o.msp = msp;
+  o.nsp = nsp;
+  o.hw = c.dv;
+  o.eps = c.eps;
   launch_proj<4, false>(ctx, o);
   if (launch_status(c.name)) return -1;
   if (c.device_io) return 0;
