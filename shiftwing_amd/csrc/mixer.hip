@@ -885,6 +885,23 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
     }
   __syncthreads();
   if (kw != 0 || lane != 0) return;
+  // one token, K <= 4: the rows' ring slots and tap weights load together
+  // before any store (a conv row reads channel 0's words when it is not one)
+  float tv[RW][4], tw[RW][4];
+  const bool ring1 = CONV && NT == 1 && a.K <= 4;
+  if (ring1) {
+    const int C = a.m[0].rows, K = a.K;
+    const float *cs = a.conv_state + (size_t)tok_slot(a.tok, 0) * a.conv_slot_stride;
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+      const int ch = (live[r] && mi[r] == 0) ? rr[r] : 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        tv[r][k] = cs[(size_t)(k < K ? k : 0) * C + ch];
+        tw[r][k] = a.conv_w[(size_t)ch * K + (k < K ? k : 0)];
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < RW; r++) {
     if (!live[r]) continue;
@@ -896,7 +913,24 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
       red[t] = v;
     }
     const ProjMat &pm = a.m[mi[r]];
-    if (CONV && mi[r] == 0) {
+    if (CONV && mi[r] == 0 && ring1) {
+      const int ch = rr[r], C = a.m[0].rows, K = a.K;
+      const int pos = tok_pos(a.tok, 0);
+      float sconv = 0.0f;
+#pragma unroll
+      for (int tap = 0; tap < 4; tap++) {
+        const int src = pos - (K - 1 - tap);
+        if (tap >= K || src < 0) continue;
+        const int ks = src % K;
+        float v = red[0];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (src != pos && k == ks) v = tv[r][k];
+        sconv = __builtin_fmaf(tw[r][tap], v, sconv);
+      }
+      a.conv_state[(size_t)tok_slot(a.tok, 0) * a.conv_slot_stride + (size_t)(pos % K) * C + ch] = red[0];
+      a.mix[ch] = silu_ref(sconv);
+    } else if (CONV && mi[r] == 0) {
       const int ch = rr[r], C = a.m[0].rows, K = a.K;
       const float *cw = a.conv_w + (size_t)ch * K;
 #pragma unroll
