@@ -227,3 +227,51 @@ def test_gqa_rejects_bad_arguments(be):
         dev.slots_step(x, [0], [8])
     with pytest.raises(HipError, match="invalid argument"):
         dev.prefill(np.zeros((4, 512), np.float32), 6)
+
+
+@pytest.mark.parametrize("dk,dv,K", [(64, 64, 3), (128, 96, 5)], ids=["dk64_dv64_K3", "dk128_dv96_K5"])
+def test_gdn_other_shapes(be, oracle, dk, dv, K):
+    """Shapes off the Qwen3.5 ones: key_dim 64 (the upper lane half of the
+    recurrence holds no key rows), value_dim 96 (three 32-column waves), conv
+    kernels of 3 and 5 taps (5 takes the ring path through memory), decode
+    steps then a block of 3."""
+    from oracle import pyoracle as po
+    g = po.HostGdn(91, 512, 2, 4, dk, dv, K)
+    dev = _dev_gdn(be, g)
+    cs, st = [a[0] for a in g.new_state()]
+    rng = np.random.default_rng(92)
+    for pos in range(7):
+        x = _x(rng, 1, 512)[0]
+        a, b = po.oracle_gdn_gates(oracle, g, x)
+        want = po.oracle_gdn_step(oracle, g, x, a, b, pos, cs, st)
+        assert_close_rms(dev.decode(x, a, b, pos), want, 1e-3, f"gdn dk{dk} dv{dv} K{K} pos {pos}")
+    X = _x(rng, 3, 512)
+    AB = [po.oracle_gdn_gates(oracle, g, X[t]) for t in range(3)]
+    A = np.stack([ab[0] for ab in AB])
+    Bv = np.stack([ab[1] for ab in AB])
+    want = np.stack([po.oracle_gdn_step(oracle, g, X[t], A[t], Bv[t], 7 + t, cs, st) for t in range(3)])
+    assert_close_rms(dev.block(X, A, Bv, 7), want, 1e-3, f"gdn dk{dk} dv{dv} K{K} block")
+    dcs, dst = dev.read_state()
+    _close_state(dst[0], st, "recurrent state")
+    _close_state(dcs[0], cs, "conv state")
+
+
+@pytest.mark.parametrize("nh,nkv,hd,rd", [(8, 2, 128, 32), (4, 1, 64, 64)], ids=["hd128", "hd64"])
+def test_gqa_other_head_dims(be, oracle, nh, nkv, hd, rd):
+    """head_dim 128 and 64 (the other two attention instantiations), 4 query
+    heads on one kv head, a full-width rotation: decode 0..23 then a prefill of
+    10 rows."""
+    from oracle import pyoracle as po
+    at = po.HostAttn(93, 512, nh, nkv, hd, rd, o_fmt=4)
+    dev = _dev_attn(be, at, 40)
+    kc, vc = [a[0] for a in at.new_cache(40)]
+    rng = np.random.default_rng(94)
+    for pos in range(24):
+        x = _x(rng, 1, 512)[0]
+        want = po.oracle_attn_step(oracle, at, x, pos, kc, vc)
+        assert_close_rms(dev.decode(x, pos), want, 1e-3, f"gqa hd{hd} pos {pos}")
+    X = _x(rng, 10, 512)
+    want = np.stack([po.oracle_attn_step(oracle, at, X[r], 24 + r, kc, vc) for r in range(10)])
+    got = dev.prefill(X, 24)
+    for r in range(10):
+        assert_close_rms(got[r], want[r], 1e-3, f"gqa hd{hd} prefill row {24 + r}")
