@@ -55,6 +55,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // Per-token slot and position: a table (slot calls, blocks) or base + t.
 struct MixTok {
   int tab;
+  int distinct;  // tab: every token has a slot of its own
   int base;
   int slot[kMixMaxTok];
   int pos[kMixMaxTok];
@@ -96,6 +97,61 @@ __device__ __forceinline__ float proj_xscale(const ProjArgs &a, int t, int c) {
   float ms = 0.0f;
   for (int k = 0; k < a.nsp; k++) ms += m[k];
   return 1.f / sqrtf(ms / (float)a.hw + a.eps);
+}
+
+// The Gated DeltaNet causal convolution of qkv channel ch for the call's
+// tokens in order (c/qwen.c:3018-3023), red[t] its raw values; lane-0 code.
+// Tokens in slots of their own with K <= 4: every ring word and tap weight
+// loads before any store; otherwise each token writes its ring slot and reads
+// its taps in turn (a slot's later token sees the earlier one's word).
+template <int NT>
+__device__ __forceinline__ void conv_channel(const ProjArgs &a, int ch, const float (&red)[NT]) {
+  const int C = a.m[0].rows, K = a.K;
+  if (a.tok.tab && a.tok.distinct && K <= 4) {
+    float tw[4], tv[NT][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) tw[k] = a.conv_w[(size_t)ch * K + (k < K ? k : 0)];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const float *cs = a.conv_state + (size_t)tok_slot(a.tok, t < a.B ? t : 0) * a.conv_slot_stride;
+#pragma unroll
+      for (int k = 0; k < 4; k++) tv[t][k] = cs[(size_t)(k < K ? k : 0) * C + ch];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if (t >= a.B) continue;
+      const int pos = tok_pos(a.tok, t);
+      float sconv = 0.0f;
+#pragma unroll
+      for (int tap = 0; tap < 4; tap++) {
+        const int src = pos - (K - 1 - tap);
+        if (tap >= K || src < 0) continue;
+        const int ks = src % K;
+        float v = red[t];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (src != pos && k == ks) v = tv[t][k];
+        sconv = __builtin_fmaf(tw[tap], v, sconv);
+      }
+      a.mix[(size_t)t * C + ch] = silu_ref(sconv);
+      a.conv_state[(size_t)tok_slot(a.tok, t) * a.conv_slot_stride + (size_t)(pos % K) * C + ch] = red[t];
+    }
+    return;
+  }
+  const float *cw = a.conv_w + (size_t)ch * K;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    if (t >= a.B) continue;
+    const int pos = tok_pos(a.tok, t);
+    float *cs = a.conv_state + (size_t)tok_slot(a.tok, t) * a.conv_slot_stride;
+    cs[(size_t)(pos % K) * C + ch] = red[t];
+    float sconv = 0.0f;
+    for (int tap = 0; tap < K; tap++) {
+      const int src = pos - (K - 1 - tap);
+      if (src >= 0) sconv = __builtin_fmaf(cw[tap], src == pos ? red[t] : cs[(size_t)(src % K) * C + ch], sconv);
+    }
+    a.mix[(size_t)t * C + ch] = silu_ref(sconv);
+  }
 }
 
 // y[t][row] = sum_g s[row][g] * sum_{i in g} code(row, i) * x[t][i]
@@ -328,20 +384,7 @@ __global__ __launch_bounds__(256) void k_mix_proj(ProjArgs a) {
             a.conv_state[(size_t)slot_w * C + ch] = red[t];
           }
         } else {
-          const float *cw = a.conv_w + (size_t)ch * K;
-#pragma unroll
-          for (int t = 0; t < NT; t++) {
-            if (t >= a.B) continue;
-            const int pos = tok_pos(a.tok, t);
-            float *cs = a.conv_state + (size_t)tok_slot(a.tok, t) * a.conv_slot_stride;
-            cs[(size_t)(pos % K) * C + ch] = red[t];
-            float s = 0.0f;
-            for (int tap = 0; tap < K; tap++) {
-              const int src = pos - (K - 1 - tap);
-              if (src >= 0) s = __builtin_fmaf(cw[tap], src == pos ? red[t] : cs[(size_t)(src % K) * C + ch], s);
-            }
-            a.mix[(size_t)t * C + ch] = silu_ref(s);
-          }
+          conv_channel<NT>(a, ch, red);
         }
       } else {
 #pragma unroll
@@ -931,22 +974,7 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
       a.conv_state[(size_t)tok_slot(a.tok, 0) * a.conv_slot_stride + (size_t)(pos % K) * C + ch] = red[0];
       a.mix[ch] = silu_ref(sconv);
     } else if (CONV && mi[r] == 0) {
-      const int ch = rr[r], C = a.m[0].rows, K = a.K;
-      const float *cw = a.conv_w + (size_t)ch * K;
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        if (t >= a.B) continue;
-        const int pos = tok_pos(a.tok, t);
-        float *cs = a.conv_state + (size_t)tok_slot(a.tok, t) * a.conv_slot_stride;
-        cs[(size_t)(pos % K) * C + ch] = red[t];
-        float sconv = 0.0f;
-        for (int tap = 0; tap < K; tap++) {
-          const int src = pos - (K - 1 - tap);
-          if (src >= 0)
-            sconv = __builtin_fmaf(cw[tap], src == pos ? red[t] : cs[(size_t)(src % K) * C + ch], sconv);
-        }
-        a.mix[(size_t)t * C + ch] = silu_ref(sconv);
-      }
+      conv_channel<NT>(a, rr[r], red);
     } else {
 #pragma unroll
       for (int t = 0; t < NT; t++)
@@ -1381,10 +1409,13 @@ static int gdn_slots(const char *name, int device_io, ColiCuda *ctx, float *out,
   GdnCall c;
   memset(&c, 0, sizeof(c));
   c.tok.tab = 1;
+  c.tok.distinct = 1;
   for (int r = 0; r < batch; r++) {
     if (slot[r] < 0 || slot[r] >= slots || position[r] < 0) return fail_arg("%s: invalid slot", name);
     c.tok.slot[r] = slot[r];
     c.tok.pos[r] = position[r];
+    for (int q = 0; q < r; q++)
+      if (slot[q] == slot[r]) c.tok.distinct = 0;
   }
   c.name = name;
   c.out = out;
