@@ -43,12 +43,12 @@
 
 #include "sw_backend.h"
 #include "sw_device.h"
+#include "sw_lds_dma.h"
 
 namespace sw {
 namespace {
 
 constexpr int kMixMaxTok = 16;  // tokens of one projection / slot-table launch
-constexpr int kProjRW = 2;      // rows per wave in k_mix_proj
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -791,24 +791,55 @@ bool q8_ok(const void *q, const float *s, int rows, int cols, int rb) {
 }
 
 // The one- and two-token form of k_mix_proj: no activation staging, the
-// columns split over waves.  A workgroup owns 4 rows for every wk of its 4
-// waves (wk = 1, 2 or 4 waves along the columns, by the row's chunk count);
-// each wave loads 16 bytes of each of its 4 rows per 64-lane chunk of its
-// column share together with the lanes' own 32 (int4) or 16 (int8)
-// activations, straight from global memory (L2-resident), so a wave's loads
+// columns split over waves.  A workgroup owns RW rows for every wk of its 4
+// waves (wk = 1, 2 or 4 waves along the columns, by the row's chunk count).
+// Per 64-lane chunk of its column share a wave copies 16 bytes a lane of
+// each of its RW rows into its own LDS slice (global_load_lds: the bytes in
+// flight hold no registers) and loads the lanes' own 32 (int4) or 16 (int8)
+// activations straight from global memory (L2-resident), so a wave's loads
 // issue at once and many short waves keep HBM busy.  The waves' partial sums
-// meet in LDS in a fixed order; the first wave of each row group finishes
-// the rows (k_mix_proj's epilogue).  grid ceil(rows_total / (16 / wk)),
-// 256 threads.
-template <int FMT, int NT, bool CONV>
+// meet in LDS in a fixed order; lane r of the row group's first wave
+// finishes row r (k_mix_proj's epilogue, the rows in parallel, its loads
+// issued at the start).  grid ceil(rows_total / (4 RW / wk)), 256 threads,
+// 4 RW KB of dynamic LDS.
+constexpr int kDirectRows = 8;  // rows a wave of k_mix_proj_direct takes
+template <int FMT, int NT, bool CONV, int RW>
 __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
-  constexpr int CPL = FMT == 4 ? 32 : 16, CH = 64 * CPL, F4 = CPL / 4, RW = 4;
+  constexpr int CPL = FMT == 4 ? 32 : 16, CH = 64 * CPL, F4 = CPL / 4;
   __shared__ float s_part[4][RW][NT];
+  extern __shared__ __align__(16) unsigned char wlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = (a.cols + CH - 1) / CH;
   const int wk = nch >= 4 ? 4 : (nch >= 2 ? 2 : 1);
   const int rg = wave / wk, kw = wave % wk;
   const int r0 = (blockIdx.x * (4 / wk) + rg) * RW;
+  unsigned char *const wbuf = wlds + wave * (RW * 1024);
+  // Lane r < RW of the row group's first wave finishes row r0 + r; what its
+  // epilogue reads (the int8 row scale; one token's conv ring slots and tap
+  // weights, K <= 4) is loaded now, with the projection's own loads.
+  const bool ring1 = CONV && NT == 1 && a.K <= 4;
+  int err = r0 + lane, em = 0;
+  const bool elive = kw == 0 && lane < RW && err < a.rows_total;
+  if (err >= a.m[0].rows) {
+    err -= a.m[0].rows;
+    em = 1;
+    if (a.nm > 2 && err >= a.m[1].rows) {
+      err -= a.m[1].rows;
+      em = 2;
+    }
+  }
+  if (!elive) err = em = 0;
+  float tv[4] = {}, tw[4] = {}, escale = 1.0f;
+  if (ring1) {
+    const int C = a.m[0].rows, K = a.K, ch = em == 0 ? err : 0;
+    const float *cs = a.conv_state + (size_t)tok_slot(a.tok, 0) * a.conv_slot_stride;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      tv[k] = cs[(size_t)(k < K ? k : 0) * C + ch];
+      tw[k] = a.conv_w[(size_t)ch * K + (k < K ? k : 0)];
+    }
+  }
+  if (FMT == 8) escale = (em == 0 ? a.m[0].s : (em == 1 ? a.m[1].s : a.m[2].s))[err];
   const unsigned char *qrow[RW];
   const float *srow[RW];
   int mi[RW], rr[RW];
@@ -844,6 +875,13 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
     // every load of the chunk is issued before the first use (the empty
     // asm with a memory clobber keeps the compiler from sinking loads to
     // their uses, which would serialise their latencies)
+    // the rows' 16 bytes a lane go global -> LDS (the wave's own slice,
+    // 1 KB a row), so a wave has RW KB in flight without holding it in
+    // registers; the previous chunk's LDS reads are done before the copies
+    // overwrite them
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < RW; r++) dma_b128(qrow[r] + (FMT == 4 ? cc / 2 : cc), lds_addr(wbuf + r * 1024));
     float4 xl[NT][F4];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -851,14 +889,10 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
 #pragma unroll
       for (int k = 0; k < F4; k++) xl[t][k] = *(const float4 *)(a.x + (size_t)tc * a.ldx + cc + 4 * k);
     }
-    uint4 w[RW];
     float sl[RW];
 #pragma unroll
-    for (int r = 0; r < RW; r++) {
-      w[r] = *(const uint4 *)(qrow[r] + (FMT == 4 ? cc / 2 : cc));
-      sl[r] = FMT == 4 ? srow[r][cc / a.gs] : 1.0f;
-    }
-    asm volatile("" ::: "memory");
+    for (int r = 0; r < RW; r++) sl[r] = FMT == 4 ? srow[r][cc / a.gs] : 1.0f;
+    wait_dma();
     float sc[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) sc[r] = (ok && live[r]) ? sl[r] : 0.0f;
@@ -892,7 +926,8 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-      const unsigned wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+      const uint4 wr = *(const uint4 *)(wbuf + r * 1024 + 16 * lane);
+      const unsigned wd[4] = {wr.x, wr.y, wr.z, wr.w};
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         float p0 = 0.0f, p1 = 0.0f;
@@ -927,59 +962,39 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
       if (lane == 0) s_part[wave][r][t] = v;
     }
   __syncthreads();
-  if (kw != 0 || lane != 0) return;
-  // one token, K <= 4: the rows' ring slots and tap weights load together
-  // before any store (a conv row reads channel 0's words when it is not one)
-  float tv[RW][4], tw[RW][4];
-  const bool ring1 = CONV && NT == 1 && a.K <= 4;
-  if (ring1) {
-    const int C = a.m[0].rows, K = a.K;
-    const float *cs = a.conv_state + (size_t)tok_slot(a.tok, 0) * a.conv_slot_stride;
+  if (!elive) return;
+  float red[NT];
 #pragma unroll
-    for (int r = 0; r < RW; r++) {
-      const int ch = (live[r] && mi[r] == 0) ? rr[r] : 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        tv[r][k] = cs[(size_t)(k < K ? k : 0) * C + ch];
-        tw[r][k] = a.conv_w[(size_t)ch * K + (k < K ? k : 0)];
-      }
-    }
+  for (int t = 0; t < NT; t++) {
+    float v = s_part[wave][lane][t];
+    for (int k = 1; k < wk; k++) v += s_part[wave + k][lane][t];
+    red[t] = v;
   }
+  if (CONV && em == 0 && ring1) {
+    const int C = a.m[0].rows, K = a.K;
+    const int pos = tok_pos(a.tok, 0);
+    float sconv = 0.0f;
 #pragma unroll
-  for (int r = 0; r < RW; r++) {
-    if (!live[r]) continue;
-    float red[NT];
+    for (int tap = 0; tap < 4; tap++) {
+      const int src = pos - (K - 1 - tap);
+      if (tap >= K || src < 0) continue;
+      const int ks = src % K;
+      float v = red[0];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      float v = s_part[wave][r][t];
-      for (int k = 1; k < wk; k++) v += s_part[wave + k][r][t];
-      red[t] = v;
+      for (int k = 0; k < 4; k++)
+        if (src != pos && k == ks) v = tv[k];
+      sconv = __builtin_fmaf(tw[tap], v, sconv);
     }
-    const ProjMat &pm = a.m[mi[r]];
-    if (CONV && mi[r] == 0 && ring1) {
-      const int ch = rr[r], C = a.m[0].rows, K = a.K;
-      const int pos = tok_pos(a.tok, 0);
-      float sconv = 0.0f;
+    a.conv_state[(size_t)tok_slot(a.tok, 0) * a.conv_slot_stride + (size_t)(pos % K) * C + err] = red[0];
+    a.mix[err] = silu_ref(sconv);
+  } else if (CONV && em == 0) {
+    conv_channel<NT>(a, err, red);
+  } else {
+    float *const y = em == 0 ? a.m[0].y : (em == 1 ? a.m[1].y : a.m[2].y);
+    const int ldy = em == 0 ? a.m[0].ldy : (em == 1 ? a.m[1].ldy : a.m[2].ldy);
 #pragma unroll
-      for (int tap = 0; tap < 4; tap++) {
-        const int src = pos - (K - 1 - tap);
-        if (tap >= K || src < 0) continue;
-        const int ks = src % K;
-        float v = red[0];
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-          if (src != pos && k == ks) v = tv[r][k];
-        sconv = __builtin_fmaf(tw[r][tap], v, sconv);
-      }
-      a.conv_state[(size_t)tok_slot(a.tok, 0) * a.conv_slot_stride + (size_t)(pos % K) * C + ch] = red[0];
-      a.mix[ch] = silu_ref(sconv);
-    } else if (CONV && mi[r] == 0) {
-      conv_channel<NT>(a, rr[r], red);
-    } else {
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-        if (t < a.B) pm.y[(size_t)t * pm.ldy + rr[r]] = FMT == 8 ? red[t] * srow[r][0] : red[t];
-    }
+    for (int t = 0; t < NT; t++)
+      if (t < a.B) y[(size_t)t * ldy + err] = FMT == 8 ? red[t] * escale : red[t];
   }
 }
 
@@ -993,10 +1008,11 @@ void launch_proj_nt(ColiCuda *ctx, const ProjArgs &a) {
 
 template <int FMT, int NT, bool CONV>
 void launch_proj_direct(ColiCuda *ctx, const ProjArgs &a) {
-  constexpr int CH = 64 * (FMT == 4 ? 32 : 16);
+  constexpr int CH = 64 * (FMT == 4 ? 32 : 16), RW = kDirectRows;
   const int nch = (a.cols + CH - 1) / CH;
-  const int rows_per_block = 16 / (nch >= 4 ? 4 : (nch >= 2 ? 2 : 1));
-  k_mix_proj_direct<FMT, NT, CONV><<<(a.rows_total + rows_per_block - 1) / rows_per_block, 256, 0, ctx->stream>>>(a);
+  const int rows_per_block = 4 * RW / (nch >= 4 ? 4 : (nch >= 2 ? 2 : 1));
+  k_mix_proj_direct<FMT, NT, CONV, RW>
+      <<<(a.rows_total + rows_per_block - 1) / rows_per_block, 256, 4 * RW * 1024, ctx->stream>>>(a);
 }
 
 template <int FMT, bool CONV>
