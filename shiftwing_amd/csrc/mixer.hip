@@ -564,19 +564,20 @@ __global__ __launch_bounds__(256) void k_gqa_prep(PrepArgs p) {
 
 // ---------------------------------------------------------------------------
 // Flash decoding over fp32 caches on v_mfma_f32_16x16x4f32.  One workgroup
-// of four waves per (row, kv head, split); the split owns a run of 16-key
-// blocks of the row's T = pos + 1 keys and wave w takes every fourth of them.
+// of kAttnWaves (4) waves per (row, kv head, split); the split owns a run of
+// 16-key blocks of the row's T = pos + 1 keys and wave w takes every fourth.
 // Operand layouts of the 16x16x4 instruction: lane l gives A[l % 16][l / 16]
 // and B[l / 16][l % 16]; D lane l, register i holds D[4 (l / 16) + i][l % 16].
-//   scores S^T (keys x heads): A = K block rows, B = Q^T; the contraction
-//     index of lane group g = l / 16 at step s is dim g * HD/4 + s, so each
-//     lane's 64 query values and 64 key values per block are contiguous; four
+//   scores S^T (keys x heads): A = K block rows, B = Q^T; lane group
+//     g = l / 16 at step i, float4 component c, contracts dim 16 i + 4 g + c,
+//     so the four lane groups of a key read 64 contiguous bytes per load; four
 //     accumulators (one per float4 component) keep the MFMA chain short;
 //   O^T (dims x heads) += V^T P^T: step s takes keys 4g + s of the block, the
-//     probabilities lane l already holds for its head, and V[key][dim].  The
-//     block's V values are loaded before the score MFMAs, so their latency
-//     overlaps them.
-// The four waves' (m, l, O) merge in LDS in wave order; the workgroup writes
+//     probabilities lane l already holds for its head, and V[key][dim], the
+//     A row r of dim tile d being dim 64 (d / 4) + 4 r + d % 4, so a lane's
+//     values of four tiles are one float4.  The block's V values are loaded
+//     before the score MFMAs, so their latency overlaps them.
+// The waves' (m, l, O) merge in LDS in wave order; the workgroup writes
 // one partial record: O [16][HD] unnormalised, the max m [16], the sum l [16].
 struct AttnArgs {
   const float *q;  // [B][nh*hd]
@@ -591,11 +592,12 @@ __device__ __forceinline__ v4f mfma_f32_16x16x4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+constexpr int kAttnWaves = 4;  // waves of a k_gqa_attn workgroup
 template <int HD>
-__global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
+__global__ __launch_bounds__(64 * kAttnWaves) void k_gqa_attn(AttnArgs a) {
   constexpr int KQ = HD / 4, NT16 = HD / 16, PSZ = 16 * HD + 32;
-  __shared__ float s_m[4][16], s_l[4][16];
-  __shared__ float s_o[16 * HD];
+  __shared__ float s_m[kAttnWaves][16], s_l[kAttnWaves][16];
+  __shared__ float s_o[16 * (HD + 1)];  // [head][dim], rows padded
   __shared__ float s_q[16 * 4 * (HD / 4 + 4)];
   const int t = blockIdx.y, kvh = blockIdx.x / a.S, s = blockIdx.x % a.S;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
@@ -610,8 +612,8 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
   // the kv head's queries in LDS, [head n][lane group g][KQ + 4] (heads past
   // G are zero); a lane reads its B operands from there, keeping registers
   // for the K and V values of a whole block in flight
-  for (int u = threadIdx.x; u < 16 * HD / 4; u += 256) {
-    const int hn = u / (HD / 4), e4 = u % (HD / 4), g4 = e4 / (KQ / 4), i4 = e4 % (KQ / 4);
+  for (int u = threadIdx.x; u < 16 * HD / 4; u += 64 * kAttnWaves) {
+    const int hn = u / (HD / 4), e4 = u % (HD / 4), g4 = e4 % 4, i4 = e4 / 4;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (hn < G) v = *(const float4 *)(a.q + (size_t)t * a.nh * HD + (size_t)(kvh * G + hn) * HD + 4 * e4);
     *(float4 *)(s_q + (hn * 4 + g4) * (KQ + 4) + 4 * i4) = v;
@@ -624,22 +626,28 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.0f;
   const float scale = 1.f / sqrtf((float)HD);
 
-  for (int b = b0 + wave; b < b1; b += 4) {
+  for (int b = b0 + wave; b < b1; b += kAttnWaves) {
     const int key0 = b * 16;
     // this block's K rows (A operand) and V values (A operand of O^T); rows
     // past T read the block's first row and are masked below
     const int km = key0 + n;
-    const float *kr = kc + (size_t)(km < T ? km : key0) * kvrows + kg * KQ;
+    const float *kr = kc + (size_t)(km < T ? km : key0) * kvrows + 4 * kg;
     float4 kv[KQ / 4];
 #pragma unroll
-    for (int i = 0; i < KQ / 4; i++) kv[i] = *(const float4 *)(kr + 4 * i);
+    for (int i = 0; i < KQ / 4; i++) kv[i] = *(const float4 *)(kr + 16 * i);
     float vv[4][NT16];
 #pragma unroll
     for (int s2 = 0; s2 < 4; s2++) {
       const int key = key0 + 4 * kg + s2;
-      const float *vr = vc + (size_t)(key < T ? key : key0) * kvrows + n;
+      const float *vr = vc + (size_t)(key < T ? key : key0) * kvrows + 4 * n;
 #pragma unroll
-      for (int d = 0; d < NT16; d++) vv[s2][d] = vr[16 * d];
+      for (int q4 = 0; q4 < NT16 / 4; q4++) {
+        const float4 v4 = *(const float4 *)(vr + 64 * q4);
+        vv[s2][4 * q4] = v4.x;
+        vv[s2][4 * q4 + 1] = v4.y;
+        vv[s2][4 * q4 + 2] = v4.z;
+        vv[s2][4 * q4 + 3] = v4.w;
+      }
     }
     // all of the block's K and V loads are in flight before the first MFMA
     asm volatile("" ::: "memory");
@@ -683,7 +691,7 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
       for (int d = 0; d < NT16; d++) o[d] = mfma_f32_16x16x4(vv[s2][d], pr[s2], o[d]);
   }
 
-  // merge the four waves in wave order
+  // merge the waves in wave order
   if (kg == 0) {
     s_m[wave][n] = m_run;
     s_l[wave][n] = l_run;
@@ -691,27 +699,27 @@ __global__ __launch_bounds__(256) void k_gqa_attn(AttnArgs a) {
   __syncthreads();
   float M = s_m[0][n];
 #pragma unroll
-  for (int w = 1; w < 4; w++) M = fmaxf(M, s_m[w][n]);
+  for (int w = 1; w < kAttnWaves; w++) M = fmaxf(M, s_m[w][n]);
   const float f = m_run == -INFINITY ? 0.0f : expf(m_run - M);
-  for (int w = 0; w < 4; w++) {
+  for (int w = 0; w < kAttnWaves; w++) {
     if (wave == w) {
 #pragma unroll
       for (int d = 0; d < NT16; d++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          float *p = s_o + (size_t)n * HD + 16 * d + 4 * kg + i;
+          float *p = s_o + (size_t)n * (HD + 1) + 64 * (d / 4) + 16 * kg + 4 * i + (d % 4);
           *p = w == 0 ? o[d][i] * f : __builtin_fmaf(o[d][i], f, *p);
         }
     }
     __syncthreads();
   }
   float *rec = a.part + ((size_t)(t * a.nkv + kvh) * a.S + s) * PSZ;
-  for (int u = threadIdx.x; u < 16 * HD; u += 256) rec[u] = s_o[u];
+  for (int u = threadIdx.x; u < 16 * HD; u += 64 * kAttnWaves) rec[u] = s_o[(u / HD) * (HD + 1) + u % HD];
   if (threadIdx.x < 16) {
     const int h = threadIdx.x;
     float Mh = s_m[0][h], L = 0.0f;
-    for (int w = 1; w < 4; w++) Mh = fmaxf(Mh, s_m[w][h]);
-    for (int w = 0; w < 4; w++)
+    for (int w = 1; w < kAttnWaves; w++) Mh = fmaxf(Mh, s_m[w][h]);
+    for (int w = 0; w < kAttnWaves; w++)
       if (s_m[w][h] != -INFINITY) L = __builtin_fmaf(s_l[w][h], expf(s_m[w][h] - Mh), L);
     rec[16 * HD + h] = Mh;
     rec[16 * HD + 16 + h] = L;
@@ -1196,7 +1204,7 @@ struct GqaCall {
 
 template <int HD>
 void launch_attn(ColiCuda *ctx, const AttnArgs &a, int rows) {
-  k_gqa_attn<HD><<<dim3(a.nkv * a.S, rows), 256, 0, ctx->stream>>>(a);
+  k_gqa_attn<HD><<<dim3(a.nkv * a.S, rows), 64 * kAttnWaves, 0, ctx->stream>>>(a);
 }
 
 int gqa_run(ColiCuda *ctx, const GqaCall &c) {
@@ -1217,7 +1225,7 @@ int gqa_run(ColiCuda *ctx, const GqaCall &c) {
   const int T = c.max_pos + 1;
   const int nb = (T + 15) / 16;
   int S = (256 + c.nkv * R - 1) / (c.nkv * R);
-  const int smax = (nb + 3) / 4;
+  const int smax = (nb + kAttnWaves - 1) / kAttnWaves;
   S = S > smax ? smax : S;
   S = S > kMaxSplits ? kMaxSplits : S;
   S = S < 1 ? 1 : S;
