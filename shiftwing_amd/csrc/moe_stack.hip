@@ -1028,39 +1028,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         }
       }
     }
-    lds_barrier();  // xq complete
-    // shared gate/up task: exact int32 dots of 16 rows with xq (A operands in
-    // registers), added to the layer's counted sums (stage S reads each sum
-    // once all of its KQ parts are in)
-    const ShTask st = sh_task_lds(s_sht);
-    {
-      v4i cs = {0, 0, 0, 0};
-      if (st.valid) {
-        int k0, k1;
-        sh_wave_range(st, wave, k0, k1);
-#pragma unroll
-        for (int i = 0; i < kShMaxKc; i++)
-          if (k0 + i < k1) {
-            const int kc = k0 + i;
-            const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
-            cs = mfma_i8(sreg.sa[i], bv, cs);
-          }
-        if ((lane & 15) == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
-        }
-      }
-    }
-    lds_barrier();  // acc_i, Lp/Ap/Pp complete
+    lds_barrier();  // xq, Lp/Ap/Pp complete
     if (wave == 0) {
-      if (st.valid && lane >= 16 && lane < 32) {
-        const int r = lane - 16;
-        int v = 0;
-#pragma unroll
-        for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
-        atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], acc_term(v));
-      }
-      // Router records of this workgroup's rows, lanes 2s (logit) and 2s+1
+      // Router records of this workgroup's rows, published before the shared
+      // task below (every workgroup's selection waits for the last record),
+      // lanes 2s (logit) and 2s+1
       // (bound).  The bound of the reference's serial fp32 dot:
       //   |fl(x.w) - x.w| <= u (A + sum_k |s^_k|) (u = 2^-24, s^_k its own
       //   partial sums), sum_k |s^_k| <= (P* + n u A)(1 + 2 n u) with P* the
@@ -1087,6 +1059,38 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
                              with_tag((unsigned long long)__double_as_longlong(v), layer_tag(cs, l)), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
+    }
+    // shared gate/up task: exact int32 dots of 16 rows with xq (A operands in
+    // registers), added to the layer's counted sums (stage S reads each sum
+    // once all of its KQ parts are in)
+    const ShTask st = sh_task_lds(s_sht);
+    {
+      v4i cs = {0, 0, 0, 0};
+      if (st.valid) {
+        int k0, k1;
+        sh_wave_range(st, wave, k0, k1);
+#pragma unroll
+        for (int i = 0; i < kShMaxKc; i++)
+          if (k0 + i < k1) {
+            const int kc = k0 + i;
+            const v4i bv = (lane & 15) == 0 ? *(const v4i *)(S.xq + kc * 64 + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
+            cs = mfma_i8(sreg.sa[i], bv, cs);
+          }
+        if ((lane & 15) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) R.acc_i[wave][4 * (lane >> 4) + i] = cs[i];
+        }
+      }
+    }
+    lds_barrier();  // acc_i complete
+    if (wave == 0) {
+      if (st.valid && lane >= 16 && lane < 32) {
+        const int r = lane - 16;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < kW; w++) v += R.acc_i[w][r];
+        atomicAdd(&acc[st.m * a.Ish + st.rt * kTileRows + r], acc_term(v));
       }
     }
     stamp(a, l, 1);
@@ -1248,8 +1252,8 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
       } else if (wave == 1) {
         // This workgroup's values of the shared hidden vector, i = b + j*NB
         // (lane j), while wave 0 selects: the counted gate/up sums (complete
-        // once all KQ parts are in; the tagged records vouch that every
-        // workgroup has added its own), the IDOT epilogue
+        // once all KQ parts are in: the call started with the set cleared, so
+        // a count of KQ is this call's), the IDOT epilogue
         // ((float)dot * s_row) * sx (c/qwen.c:1766) and SwiGLU (c/qwen.c:3419),
         // published (tagged with the layer) for every workgroup's stage G.
         const int i = b + lane * a.NB;
@@ -1957,7 +1961,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
           out = __builtin_fmaf(shv, rt.sg, out);
           a.y[(size_t)l * a.ys + tile * kTileRows + t] = out;
         }
+        // the layer barrier's arrival follows the workgroup's output rows
+        // directly (their stores issued by this wave)
+        if (t == 0 && l + 1 < a.n) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
       } else if (l + 1 < a.n) {
+        if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
         static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sh_task_lds(s_sht), sreg, t);
       }
       // The next layer's stage R inputs, loaded while the layer barrier
@@ -1972,8 +1980,6 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
     // ======================= barrier y (next layer) =======================
     stamp(a, l, 6);
     if (l + 1 < a.n) {
-      lds_barrier();
-      if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
       if (t == 0) rt.flag = bar_wait(bar_of(a, cs, l, kBarY), a) ? 1 : 0;
       lds_barrier();
       if (__builtin_expect(!rt.flag, 0)) return;
@@ -2015,8 +2021,7 @@ static size_t stack_union_bytes(int E, int H, int K, int ngh, int ngi, int Ish, 
 }
 
 // shared gate/up tasks: 16-row tiles of both matrices, each split into KQ
-// k-ranges; every task's workgroup must also own a router record (its tagged
-// records vouch for its shared sums)
+// k-ranges (KQ at most NB / tiles, E / tiles and H / 64)
 static int stack_kq(int NB, int H, int E, int Ish) {
   const int nsh_rt = 2 * (Ish / kTileRows);
   if (nsh_rt == 0) return 1;
