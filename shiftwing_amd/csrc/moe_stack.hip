@@ -1968,12 +1968,11 @@ __global__ __launch_bounds__(kT, 1) void k_stack(StackArgs a0) {
         if (t == 0) bar_arrive(bar_of(a, cs, l, kBarY), a.NB);
         static_load(a, layer_ref_lds(s_lref[(l + 1) & 1]), sh_task_lds(s_sht), sreg, t);
       }
-      // The next layer's stage R inputs, loaded while the layer barrier
-      // completes (HBM is otherwise idle then), by waves 1..7; wave 0, whose
-      // barrier arrival and polls would wait behind them (a wave's loads
-      // complete in order), loads its part once it has passed the barrier.
-      // Issued after the combine: the compiler's wait for the combine's own
-      // loads would otherwise wait for these too.
+      // The next layer's stage R inputs are in flight (every wave's share,
+      // issued before the combine).  Wave 0's returning barrier arrival
+      // waits behind its share (a wave's loads complete in order); deferring
+      // that share past the barrier measured slower (it then delays the next
+      // layer's router pass).
       lds_barrier();
     }
 
