@@ -331,12 +331,16 @@ typedef struct {
     int topk;                /* K */
     int intermediate;        /* routed expert I */
     int shared_intermediate; /* shared expert I */
-    int expert_format;       /* 4 = grouped int4, 3 = packed int3 triplets */
+    int expert_format;       /* 4 = grouped int4, 3 = packed int3 triplets,
+                                2 = int2 (four codes a byte, value 2c - 3) */
     int group_size;          /* routed-expert quant group (128) */
 } ColiMoeShape;
 
 /* Allocate an HBM-resident layer (all experts).  Requires hidden % 64 == 0,
- * group_size 128, expert_format 3 or 4, topk <= 32 and experts <= 4096.
+ * group_size 128, expert_format 2, 3 or 4, topk <= 32 and experts <= 4096.
+ * int2 experts are held as int4 records (code c as the nibble 5 + 2c, the
+ * same value; c/qwen.c:567-575 widens them so for the reference's device
+ * path), so they stream as many bytes as int4.
  * Any intermediate and shared_intermediate: a ragged one is held rounded up
  * to the row tiles (16 and 64 rows) with zero rows, which add exact zeros
  * (the reference's tail groups, c/qwen.c:1706-1754, as in
@@ -400,10 +404,10 @@ int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int sidecar
                                   ColiMoeShape *shape);
 /* Create an HBM-resident layer and fill it from the container: router and
  * gate row (F32, BF16 or F16), the int8 shared expert (one scale per row),
- * every routed expert (int4, or int3 from the .q3 sidecar, in groups of 128),
- * repacked on the device.  int2 experts (.q2 sidecars, .qtype 2) and other
- * group sizes, which the reference's CPU path reads, return -1 with a message:
- * the device layer does not take them. */
+ * every routed expert (int4, int3 from the .q3 sidecar, or int2 from .q2
+ * sidecars / .qtype 2, in groups of 128), repacked on the device.  Other
+ * group sizes, which the reference's CPU path reads, return -1 with a
+ * message: the device layer does not take them. */
 int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer,
                              int topk, int sidecar, ColiMoeLayer **out);
 

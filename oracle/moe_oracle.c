@@ -5,7 +5,8 @@
  *
  * What it restates (all in /root/reference/c/qwen.c):
  *   dot 1674, parallel_work 1675-1682, dot_q8f 1687-1695, qrow_i8 1696,
- *   dot_i8i8 1697-1705, dot_q4_group 1706-1716, q3_value 1725-1729,
+ *   dot_i8i8 1697-1705, dot_q4_group 1706-1716, dot_q2_group 1717-1724,
+ *   q3_value 1725-1729,
  *   dot_q3_group 1730-1754 (+ q3_lut_init 416-429 / q3_word24 430-433),
  *   qmat_dot_row 1755-1760, qmat_mul_ex 1761-1773, qmat_mul_batch 3305-3329,
  *   sigmoidf_stable / siluf 307-308, mlp_batch 3407-3413, mlp_one 3415-3420,
@@ -167,6 +168,18 @@ float or_dot_q4_group(const uint8_t *w, const float *x, int n) {
     return or_tail_fma(sum, x + i, wf, r);
 }
 
+/* dot_q2_group, qwen.c:1717-1724: four 2-bit codes a byte, lowest bits
+ * first, value 2 code - 3; a scalar loop, which gcc keeps in order and
+ * contracts into an FMA chain. */
+float or_dot_q2_group(const uint8_t *w, const float *x, int n) {
+    float sum = 0.f;
+    for (int i = 0; i < n; i++) {
+        const int code = (w[i >> 2] >> (2 * (i & 3))) & 3;
+        sum = fmaf(x[i], (float)(2 * code - 3), sum);
+    }
+    return sum;
+}
+
 /* q3_value, qwen.c:1725-1729 */
 int or_q3_value(const uint8_t *w, int i) {
     int bit = 3 * i, byte = bit >> 3, shift = bit & 7;
@@ -197,7 +210,7 @@ float or_dot_q3_group(const uint8_t *w, const float *x, int n) {
     return or_tail_fma(sum, x + i, wf, r);
 }
 
-/* qmat_dot_row, qwen.c:1755-1760 (fmt 0, 1, 3, 4). */
+/* qmat_dot_row, qwen.c:1755-1760 (fmt 0, 1, 2, 3, 4). */
 float or_qmat_dot_row(const or_qmat *w, int row, const float *x) {
     if (w->fmt == 0) return or_dot_f32(x, w->f + (int64_t)row * w->I, w->I);
     if (w->fmt == 1)
@@ -210,8 +223,9 @@ float or_qmat_dot_row(const or_qmat *w, int row, const float *x) {
         int base = g * w->gs, n = w->gs;
         if (base + n > w->I) n = w->I - base;
         if (n > 0) {
-            float v = w->fmt == 3 ? or_dot_q3_group(q + (base * 3 / 8), x + base, n)
-                                  : or_dot_q4_group(q + (base >> 1), x + base, n);
+            float v = w->fmt == 2   ? or_dot_q2_group(q + (base >> 2), x + base, n)
+                      : w->fmt == 3 ? or_dot_q3_group(q + (base * 3 / 8), x + base, n)
+                                    : or_dot_q4_group(q + (base >> 1), x + base, n);
             out = fmaf(v, s[g], out);
         }
     }
@@ -577,7 +591,7 @@ void or_synth_shared_q8(uint64_t seed, int layer, int H, int I_sh, int8_t *gq,
 
 static int or_row_bytes(int fmt, int cols, int gs) {
     int ng = (cols + gs - 1) / gs;
-    return fmt == 4 ? ng * gs / 2 : ng * gs * 3 / 8;
+    return fmt == 4 ? ng * gs / 2 : fmt == 2 ? ng * gs / 4 : ng * gs * 3 / 8;
 }
 
 void or_synth_expert(uint64_t seed, int layer, int eid, int fmt, int H, int I,

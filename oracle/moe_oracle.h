@@ -18,8 +18,9 @@ extern "C" {
 #endif
 
 /* QMat, c/qwen.c:68-81 (host fields only).
- * fmt 0 = f32 (f), 1 = int8 (q, one scale per row), 3 = packed int3 triplets,
- * 4 = int4 low-nibble-first; fmt 3/4 carry one f32 scale per (row, group). */
+ * fmt 0 = f32 (f), 1 = int8 (q, one scale per row), 2 = int2 (four codes a
+ * byte, value 2 code - 3), 3 = packed int3 triplets, 4 = int4
+ * low-nibble-first; fmt 2/3/4 carry one f32 scale per (row, group). */
 typedef struct {
     int fmt, O, I, gs, rb, ng;
     const float *f;
@@ -59,6 +60,7 @@ int32_t or_dot_i8i8(const int8_t *w, const int8_t *x, int n);
 float or_dot_q4_group(const uint8_t *w, const float *x, int n);
 int or_q3_value(const uint8_t *w, int i);
 float or_dot_q3_group(const uint8_t *w, const float *x, int n);
+float or_dot_q2_group(const uint8_t *w, const float *x, int n);
 float or_qmat_dot_row(const or_qmat *w, int row, const float *x);
 void or_qmat_mul(float *y, const float *x, const or_qmat *w, int allow_idot);
 void or_qmat_mul_batch(float *y, const float *x, int B, int ldx,

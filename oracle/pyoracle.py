@@ -62,6 +62,7 @@ def _declare(lib, prefix: str):
         ("dot_i8i8", C.c_int32, [C.c_void_p, C.c_void_p, C.c_int]),
         ("dot_q4_group", C.c_float, [C.c_void_p, f32p, C.c_int]),
         ("dot_q3_group", C.c_float, [C.c_void_p, f32p, C.c_int]),
+        ("dot_q2_group", C.c_float, [C.c_void_p, f32p, C.c_int]),
         ("expf", C.c_float, [C.c_float]),
         ("siluf", C.c_float, [C.c_float]),
         ("qmat_mul", None, [f32p, f32p, C.POINTER(OrQMat), C.c_int]),
@@ -375,12 +376,12 @@ class RefLayer:
 # -- host-side layer containers ------------------------------------------------
 
 def row_bytes(fmt: int, cols: int, gs: int) -> int:
-    """Container row bytes: int4 ng*gs/2, int3 ng*gs*3/8, int8 cols
-    (c/qwen.c:2242-2254)."""
+    """Container row bytes: int4 ng*gs/2, int3 ng*gs*3/8, int2 ng*gs/4, int8
+    cols (c/qwen.c:2242-2254)."""
     if fmt == 1:
         return cols
     ng = (cols + gs - 1) // gs
-    return ng * gs // 2 if fmt == 4 else ng * gs * 3 // 8
+    return ng * gs // 2 if fmt == 4 else ng * gs // 4 if fmt == 2 else ng * gs * 3 // 8
 
 
 class HostQMat:
@@ -388,8 +389,8 @@ class HostQMat:
 
     def __init__(self, fmt: int, O: int, I: int, gs: int = 0, q=None, s=None, f=None):
         self.fmt, self.O, self.I, self.gs = fmt, O, I, gs
-        self.ng = (I + gs - 1) // gs if fmt in (3, 4) else 0
-        self.rb = row_bytes(fmt, I, gs) if fmt in (1, 3, 4) else 0
+        self.ng = (I + gs - 1) // gs if fmt in (2, 3, 4) else 0
+        self.rb = row_bytes(fmt, I, gs) if fmt in (1, 2, 3, 4) else 0
         self.q, self.s, self.f = q, s, f
         self.st = OrQMat(fmt, O, I, gs, self.rb, self.ng,
                          ptr(f, f32p) if f is not None else None,

@@ -27,7 +27,7 @@ static QMat ref_qmat_named(const or_qmat *w, const char *name) {
     /* the reference's device weight cache keys tensors by name (c/qwen.c:576) */
     if (name) {
         snprintf(q.cuda_key, sizeof(q.cuda_key), "%s", name);
-        q.cuda_eligible = w->fmt == 1 || w->fmt == 3 || w->fmt == 4;
+        q.cuda_eligible = w->fmt == 1 || w->fmt == 2 || w->fmt == 3 || w->fmt == 4;
     }
 #else
     (void)name;
@@ -38,7 +38,7 @@ static QMat ref_qmat_named(const or_qmat *w, const char *name) {
     q.gs = w->gs;
     q.rb = w->rb;
     q.ng = w->ng;
-    q.drb = w->fmt == 3 ? (w->rb / 3) * 4 : w->rb;
+    q.drb = w->fmt == 3 ? (w->rb / 3) * 4 : w->fmt == 2 ? w->rb * 2 : w->rb;
     q.f = (float *)w->f;
     q.s = (float *)w->s;
     if (w->fmt == 1)
@@ -56,6 +56,7 @@ float ref_qrow_i8(const float *x, int8_t *q, int n) { return qrow_i8(x, q, n); }
 int32_t ref_dot_i8i8(const int8_t *w, const int8_t *x, int n) { return dot_i8i8(w, x, n); }
 float ref_dot_q4_group(const uint8_t *w, const float *x, int n) { return dot_q4_group(w, x, n); }
 float ref_dot_q3_group(const uint8_t *w, const float *x, int n) { return dot_q3_group(w, x, n); }
+float ref_dot_q2_group(const uint8_t *w, const float *x, int n) { return dot_q2_group(w, x, n); }
 float ref_expf(float x) { return expf(x); }
 void ref_rmsnorm_zero(float *out, const float *x, const float *w, int n, float eps) {
     rmsnorm_zero(out, x, w, n, eps);

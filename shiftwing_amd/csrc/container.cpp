@@ -471,9 +471,9 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
   if (layer_shape(c, layer, sidecar, s)) return -1;
   s.topk = topk;
   const int H = s.hidden, E = s.experts, I = s.intermediate, Ish = s.shared_intermediate, fmt = s.expert_format;
-  if (fmt != 3 && fmt != 4)
+  if (fmt < 2 || fmt > 4)
     return fail_arg("coli_cuda_moe_layer_load: layer %d: routed experts are format %d; the device layer takes "
-                    "int4 or int3 (sidecar 1 for the .q3 sidecar)", layer, fmt);
+                    "int4, int3 (sidecar 1 for the .q3 sidecar) or int2 (widened to int4 records)", layer, fmt);
   if (s.group_size != 128)
     return fail_arg("coli_cuda_moe_layer_load: layer %d: routed experts in groups of %d; the device layer takes "
                     "groups of 128", layer, s.group_size);

@@ -2705,8 +2705,8 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   *out = nullptr;
   if (s->hidden <= 0 || s->experts <= 0 || s->topk <= 0 || s->intermediate <= 0 ||
       s->shared_intermediate <= 0 || s->hidden % 64 || s->topk > kMaxTopK || s->topk > s->experts ||
-      s->experts > 4096 || s->group_size != kGroup || (s->expert_format != 3 && s->expert_format != 4))
-    return fail_arg("coli_cuda_moe_layer_create: unsupported shape (H%%64, group_size 128, format 3|4, "
+      s->experts > 4096 || s->group_size != kGroup || s->expert_format < 2 || s->expert_format > 4)
+    return fail_arg("coli_cuda_moe_layer_create: unsupported shape (H%%64, group_size 128, format 2|3|4, "
                     "topk<=32, experts<=4096)");
   ColiMoeLayer *L = (ColiMoeLayer *)calloc(1, sizeof(ColiMoeLayer));
   if (!L) return fail_arg("out of memory creating MoE layer");
@@ -2715,6 +2715,11 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   // hidden values there are silu(0)*0 = 0, and the down columns they meet
   // hold zero values).
   L->sh = *s;
+  // int2 experts are held as int4 records: code c is the nibble 5 + 2c, the
+  // same value 2c - 3 (the reference widens them the same way for its device
+  // path, q2_expand_q4 at c/qwen.c:567-575)
+  L->src_fmt = s->expert_format;
+  if (L->src_fmt == 2) L->sh.expert_format = 4;
   L->I_src = s->intermediate;
   L->Ish_src = s->shared_intermediate;
   L->sh.intermediate = (s->intermediate + kTileRows - 1) / kTileRows * kTileRows;
@@ -2723,7 +2728,7 @@ extern "C" int coli_cuda_moe_layer_create(ColiCuda *ctx, ColiMoeLayer **out, con
   int H = s->hidden, I = L->sh.intermediate, E = s->experts, Ish = L->sh.shared_intermediate;
   L->ngh = (H + kGroup - 1) / kGroup;
   L->ngi = (I + kGroup - 1) / kGroup;
-  L->xl = expert_layout(nullptr, H, I, s->expert_format);
+  L->xl = expert_layout(nullptr, H, I, L->sh.expert_format);
   int rc = layer_alloc(L, (void **)&L->router, (size_t)E * H * 4, "router allocation") ||
            layer_alloc(L, (void **)&L->sgate_row, (size_t)H * 4, "shared gate allocation") ||
            layer_alloc(L, (void **)&L->sh_gq, (size_t)Ish * H, "shared gate allocation") ||
@@ -2798,6 +2803,16 @@ extern "C" int coli_cuda_moe_layer_set_shared_q8(ColiCuda *ctx, ColiMoeLayer *L,
   return launch_status("coli_cuda_moe_layer_set_shared_q8");
 }
 
+// int2 container bytes (four codes a byte, lowest bits first, value 2c - 3)
+// into int4 bytes (two nibbles a byte, low first, value n - 8): n = 5 + 2c
+__global__ void k_widen_q2(unsigned short *out, const unsigned char *in, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const unsigned b = in[i];
+  const unsigned c0 = 5 + 2 * (b & 3), c1 = 5 + 2 * ((b >> 2) & 3), c2 = 5 + 2 * ((b >> 4) & 3), c3 = 5 + 2 * (b >> 6);
+  out[i] = (unsigned short)((c0 | c1 << 4) | (c2 | c3 << 4) << 8);
+}
+
 // container rows [rows_src x cols] into tile records of `rows` (a multiple of
 // the tile rows) rows
 static int repack_matrix(ColiCuda *ctx, const TileMat &dst, const unsigned char *q, const float *s, int rows,
@@ -2821,6 +2836,22 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
   if (expert < 0 || expert >= L->sh.experts)
     return fail_arg("coli_cuda_moe_layer_set_expert: expert %d outside [0,%d)", expert, L->sh.experts);
   int H = L->sh.hidden, I = L->sh.intermediate, Is = L->I_src, fmt = L->sh.expert_format;
+  if (L->src_fmt == 2) {
+    // each matrix widened into scratch, then repacked as int4 (stream
+    // order keeps one matrix's repack ahead of the next one's widening)
+    const size_t bh = (size_t)Is * (L->ngh * kGroup / 4), bi = (size_t)H * (L->ngi * kGroup / 4);
+    if (ensure_scratch(ctx, kScrSetup, 2 * (bh > bi ? bh : bi), "int2 expert widening")) return -1;
+    unsigned char *w4 = (unsigned char *)ctx->scratch[kScrSetup];
+    const unsigned char *src[3] = {gq, uq, dq};
+    const float *sc[3] = {gs, us, ds};
+    for (int m = 0; m < 3; m++) {
+      const size_t nb = m < 2 ? bh : bi;
+      k_widen_q2<<<blocks_for(nb, 256), 256, 0, ctx->stream>>>((unsigned short *)w4, src[m], nb);
+      if (repack_matrix(ctx, L->xl.mat(expert, m), w4, sc[m], m < 2 ? I : H, m < 2 ? Is : H, m < 2 ? H : Is, 4))
+        return -1;
+    }
+    return 0;
+  }
   if (repack_matrix(ctx, L->xl.mat(expert, 0), gq, gs, I, Is, H, fmt) ||
       repack_matrix(ctx, L->xl.mat(expert, 1), uq, us, I, Is, H, fmt) ||
       repack_matrix(ctx, L->xl.mat(expert, 2), dq, ds, H, H, Is, fmt))
@@ -2849,11 +2880,14 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
   k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_gs, Ish, sw_key(seed, li, 0, SW_T_SH_GATE_S), 0.01f, 1);
   k_synth_normal<<<blocks_for(Ish, 256), 256, 0, st>>>(L->sh_us, Ish, sw_key(seed, li, 0, SW_T_SH_UP_S), 0.01f, 1);
   k_synth_normal<<<blocks_for(H, 256), 256, 0, st>>>(L->sh_ds, H, sw_key(seed, li, 0, SW_T_SH_DOWN_S), 0.01f, 1);
-  // routed experts: container bytes into scratch, repacked per matrix
-  int rbh = fmt == 4 ? L->ngh * kGroup / 2 : L->ngh * kGroup * 3 / 8;
-  int rbi = fmt == 4 ? L->ngi * kGroup / 2 : L->ngi * kGroup * 3 / 8;
+  // routed experts: container bytes into scratch, repacked per matrix (int2
+  // bytes widened to int4 first, behind them in the same scratch)
+  const bool q2 = L->src_fmt == 2;
+  auto row_b = [&](int ng) { return q2 ? ng * kGroup / 4 : fmt == 4 ? ng * kGroup / 2 : ng * kGroup * 3 / 8; };
+  int rbh = row_b(L->ngh), rbi = row_b(L->ngi);
   size_t need = (size_t)I * rbh > (size_t)H * rbi ? (size_t)I * rbh : (size_t)H * rbi;
-  if (ensure_scratch(ctx, kScrSetup, need, "synthesis scratch")) return -1;
+  const size_t wide_off = (need + 255) & ~(size_t)255;
+  if (ensure_scratch(ctx, kScrSetup, q2 ? wide_off + 2 * need : need, "synthesis scratch")) return -1;
   unsigned char *tmp = (unsigned char *)ctx->scratch[kScrSetup];
   for (int e = 0; e < E; e++) {
     const int tq[3] = {SW_T_GATE_Q, SW_T_UP_Q, SW_T_DOWN_Q}, ts[3] = {SW_T_GATE_S, SW_T_UP_S, SW_T_DOWN_S};
@@ -2862,10 +2896,17 @@ extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, un
       const int rows_dev = m < 2 ? Ip : H;
       size_t nb = (size_t)rows * rb;
       k_synth_bytes<<<blocks_for((nb + 7) / 8, 256), 256, 0, st>>>(tmp, nb, sw_key(seed, li, (uint32_t)e, tq[m]));
+      const unsigned char *codes = tmp;
+      int rbd = rb;
+      if (q2) {
+        k_widen_q2<<<blocks_for(nb, 256), 256, 0, st>>>((unsigned short *)(tmp + wide_off), tmp, nb);
+        codes = tmp + wide_off;
+        rbd = 2 * rb;
+      }
       const TileMat dst = L->xl.mat(e, m);
       unsigned char *base = const_cast<unsigned char *>(dst.base);
       size_t lanes = (size_t)(rows_dev / kTileRows) * ng * 64;
-      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(base, dst.rs, tmp, rows_dev, rows, cols, rb, ng, fmt);
+      k_repack_codes<<<blocks_for(lanes, 256), 256, 0, st>>>(base, dst.rs, codes, rows_dev, rows, cols, rbd, ng, fmt);
       k_synth_scales_tiled<<<blocks_for((size_t)rows_dev * ng, 256), 256, 0, st>>>(
           base, dst.rs, dst.so, rows_dev, rows, ng, sw_key(seed, li, (uint32_t)e, ts[m]));
     }

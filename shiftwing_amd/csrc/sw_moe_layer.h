@@ -11,6 +11,7 @@
 struct ColiMoeLayer {
   ColiMoeShape sh;               // the device shape: I and shared I rounded up to the tiles (16, 64)
   int I_src, Ish_src;            // the caller's I and shared I (rows past them hold zeros)
+  int src_fmt;                   // the caller's expert format: 2 (int2 rows, widened to the int4 records), 3, 4
   int ngh, ngi;                  // groups along H (gate/up cols) and I (down cols)
   float *router;                 // [E][H]
   float *sgate_row;              // [H]

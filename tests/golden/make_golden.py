@@ -36,6 +36,8 @@ LAYERS = [
     ("ragged_q3", 384, 32, 8, 257, 129, 3, 128, 14, 3, 5),
     ("s35_q4", 2048, 256, 8, 512, 512, 4, 128, 35, 0, 3),
     ("s397_q3", 4096, 512, 10, 1024, 1024, 3, 128, 397, 0, 2),
+    ("small_q2", 256, 16, 4, 128, 128, 2, 128, 15, 4, 7),
+    ("ragged_q2", 384, 32, 8, 257, 129, 2, 128, 16, 5, 5),
 ]
 
 
@@ -84,6 +86,7 @@ def main():
              K=np.array(ks), idx=np.stack(idxs), weight=np.stack(ws))
 
     # single-matrix GEMV rows, fmt 1 (int8, IDOT and fp32-activation) / 3 / 4
+    # (fmt 2 below)
     out = {}
     for fmt in (1, 3, 4):
         for I in (1, 31, 64, 128, 129, 257):
@@ -109,6 +112,23 @@ def main():
             out[key + "_X"] = X
             out[key + "_Y"] = ref.qmat_mul_batch(np.ascontiguousarray(X), m, 1)
     np.savez(os.path.join(HERE, "qmat.npz"), **out)
+
+    # int2 rows (dot_q2_group), from a generator of their own so that the
+    # fixtures above keep their bytes
+    rng2 = np.random.default_rng(20261202)
+    out2 = {}
+    for I in (1, 3, 31, 64, 128, 129, 257):
+        O, gs = 5, 128
+        q = rng2.integers(0, 256, (O, row_bytes(2, I, gs)), dtype=np.uint8)
+        s = np.abs(rng2.standard_normal((O, (I + gs - 1) // gs)) * 0.01).astype(np.float32)
+        x = rng2.standard_normal(I).astype(np.float32)
+        m = HostQMat(2, O, I, gs, q=np.ascontiguousarray(q), s=np.ascontiguousarray(s))
+        key = f"f2_I{I}"
+        out2[key + "_q"] = q
+        out2[key + "_s"] = s
+        out2[key + "_x"] = x
+        out2[key + "_y"] = ref.qmat_mul(x, m, 1)
+    np.savez(os.path.join(HERE, "qmat_q2.npz"), **out2)
 
     # whole layers: decode (moe_forward) per token and prefill (moe_prefill_grouped)
     for name, H, E, K, I, I_sh, fmt, gs, seed, layer, T in LAYERS:

@@ -54,12 +54,14 @@ def write(path: str, tensors: dict) -> None:
 
 
 def moe_layer_tensors(hl, layer: int, prefix: str = "", q3: "object | None" = None,
-                      router_bf16: bool = False, qtype_tags: bool = True) -> dict:
+                      router_bf16: bool = False, qtype_tags: bool = True, q2: "object | None" = None) -> dict:
     """The MoE tensors of one layer as c/tools/convert_qwen.py writes them
     (c/qwen.c:2443-2457, 2330-2346): router and gate row as float, the shared
     expert as int8 rows + .qs [rows] + .qtype 8, routed experts as packed
     codes + .qs [rows, groups] + .qtype 4 (or 3).  `q3`: a second host layer
-    whose int3 experts go into the .q3 sidecar (c/tools/requantize_expert_q2.py)."""
+    whose int3 experts go into the .q3 sidecar (c/tools/requantize_expert_q2.py);
+    `q2`: one whose int2 experts go into .q2 sidecars (the EXPERT_Q2=1 lookup,
+    c/qwen.c:2207-2212)."""
     p = f"{prefix}layers.{layer}.mlp."
     t = {}
     t[p + "gate.weight"] = bf16(hl.router_w) if router_bf16 else hl.router_w
@@ -78,14 +80,16 @@ def moe_layer_tensors(hl, layer: int, prefix: str = "", q3: "object | None" = No
             t[base + ".qs"] = s
             if qtype_tags:
                 t[base + ".qtype"] = np.array([tag], np.uint8)
-    if q3 is not None:
-        for e in range(q3.E):
-            for nm, q, s in (("gate", q3.gq[e], q3.gsc[e]), ("up", q3.uq[e], q3.usc[e]),
-                             ("down", q3.dq[e], q3.dsc[e])):
-                base = f"{p}experts.{e}.{nm}_proj.weight.q3"
+    for side, sfx, tg in ((q3, ".q3", 3), (q2, ".q2", 2)):
+        if side is None:
+            continue
+        for e in range(side.E):
+            for nm, q, s in (("gate", side.gq[e], side.gsc[e]), ("up", side.uq[e], side.usc[e]),
+                             ("down", side.dq[e], side.dsc[e])):
+                base = f"{p}experts.{e}.{nm}_proj.weight{sfx}"
                 t[base] = q
                 t[base + ".qs"] = s
-                t[base + ".qtype"] = np.array([3], np.uint8)
+                t[base + ".qtype"] = np.array([tg], np.uint8)
     return t
 
 

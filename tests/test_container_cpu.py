@@ -251,12 +251,13 @@ def test_container_matches_the_reference_loader(tmp_path, layers, oracle):
 
 
 def test_container_int2_and_group_sizes_as_the_reference_reads_them(tmp_path, oracle):
-    """Formats the reference's CPU path reads and the device layer does not
-    take are still classified as the reference classifies them, so that
-    coli_cuda_moe_layer_load can refuse them by name (its GPU test checks the
-    refusal): int2 experts from .qtype 2 main payloads and from .q2 sidecars
-    (EXPERT_Q2=1, which falls back to the main payload for an expert without
-    one, c/qwen.c:2207-2214), and int4 experts in groups of 64."""
+    """int2 experts and other group sizes are classified as the reference
+    classifies them: int2 experts from .qtype 2 main payloads and from .q2
+    sidecars (EXPERT_Q2=1, which falls back to the main payload for an expert
+    without one, c/qwen.c:2207-2214), which coli_cuda_moe_layer_load widens to
+    int4 records, and int4 experts in groups of 64, which it refuses by name
+    (the GPU container tests load the one and check the refusal of the
+    other)."""
     ref = _reference()
     H, E, K, I, Ish = SHAPE
     rng = np.random.default_rng(2)

@@ -2,7 +2,8 @@
 reference's conventions (tests/st_writer.py) from the CPU checker's synthetic
 layers is loaded into an HBM-resident layer (coli_cuda_moe_layer_load).  The
 loaded layer must equal the same layer synthesised on the device bit for bit
-(int4 experts from the main payloads, int3 from the .q3 sidecar), and match
+(int4 experts from the main payloads, int3 from the .q3 sidecar, int2 from
+.qtype 2 payloads or .q2 sidecars), and match
 moe_forward / moe_prefill_grouped (c/qwen.c:3717-3739, 4141-4206)."""
 import ctypes as C
 
@@ -17,11 +18,11 @@ pytestmark = pytest.mark.gpu
 SHAPE = (512, 16, 4, 256, 128)  # H, E, K, I, Ish
 
 
-def _load(be, d, layer, K, use_q3, H):
+def _load(be, d, layer, K, sidecar, H):
     from shiftwing_amd import Container, MoeLayer
     c = Container(d)
     try:
-        return MoeLayer.load(be, c, layer, K, bool(use_q3))
+        return MoeLayer.load(be, c, layer, K, int(sidecar))
     finally:
         c.close()
 
@@ -68,23 +69,58 @@ def test_container_bf16_router(be, oracle, tmp_path):
     Lc.close()
 
 
+def test_container_int2_loads(be, oracle, tmp_path):
+    """int2 routed experts as the reference reads them (c/qwen.c:2207-2212,
+    2244-2246): .qtype 2 main payloads (sidecar 0) and .q2 sidecars (sidecar
+    2, EXPERT_Q2=1).  Loaded, they equal the same int2 layer synthesised on the
+    device bit for bit, and match moe_forward / moe_prefill_grouped over the
+    int2 layer; the .q2 directory's main payloads (sidecar 0) are its int4
+    layer."""
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish = SHAPE
+    hl4 = oracle.host_layer(8, 1, H, E, K, I, Ish, 4)
+    hl2 = oracle.host_layer(8, 1, H, E, K, I, Ish, 2)
+    st_writer.write_split(str(tmp_path / "q2main"), st_writer.moe_layer_tensors(hl2, 1), parts=2)
+    st_writer.write_split(str(tmp_path / "q2side"), st_writer.moe_layer_tensors(hl4, 1, q2=hl2), parts=2)
+    x = np.stack([oracle.synth_x(8, 1, t, H) for t in range(5)])
+    Ls = MoeLayer(be, H, E, K, I, Ish, 2)
+    Ls.synthesize(8, 1)
+    want, tr = oracle.moe_prefill(hl2, x, trace=True)
+    want1, tr1 = oracle.moe_forward(hl2, x[0], trace=True)
+    for d, sidecar in (("q2main", 0), ("q2side", 2)):
+        print(f"[container int2] {d} sidecar {sidecar}", flush=True)
+        Lc = _load(be, str(tmp_path / d), 1, K, sidecar, H)
+        try:
+            for rows in (x[:1], x):
+                yc, ic, _ = Lc.forward_host(rows)
+                ys, is_, _ = Ls.forward_host(rows)
+                assert np.array_equal(ic, is_)
+                assert np.array_equal(yc.view(np.uint32), ys.view(np.uint32))
+            y, idx, _ = Lc.forward_host(x)
+            assert np.array_equal(idx, tr["idx"])
+            assert_close_rms(y, want, 1e-3, f"{d} int2 block")
+            y1, i1, _ = Lc.forward_host(x[0])
+            assert np.array_equal(i1[0], tr1["idx"])
+            assert_close_rms(y1[0], want1, 1e-3, f"{d} int2 token")
+        finally:
+            Lc.close()
+    Ls.close()
+    Lc = _load(be, str(tmp_path / "q2side"), 1, K, 0, H)
+    want4, tr4 = oracle.moe_forward(hl4, x[0], trace=True)
+    y, idx, _ = Lc.forward_host(x[0])
+    assert np.array_equal(idx[0], tr4["idx"])
+    assert_close_rms(y[0], want4, 1e-3, "q2side main payload")
+    Lc.close()
+
+
 def test_container_load_refusals(be, oracle, tmp_path):
     """Layers the device layer does not take return -1 with a message from
-    coli_cuda_moe_layer_load, and nothing is created: int2 experts (.qtype 2
-    payloads, .q2 sidecars), int4 experts in groups of 64 (both read by the
-    reference's CPU path, c/qwen.c:2244-2254), and a shared expert tagged int8
-    with two scales per row (more than the one per row an int8 matrix uses,
-    c/qwen.c:1765-1768)."""
-    from test_container_cpu import _int2_tensors
+    coli_cuda_moe_layer_load, and nothing is created: int4 experts in groups
+    of 64 (read by the reference's CPU path, c/qwen.c:2244-2254), and a shared
+    expert tagged int8 with two scales per row (more than the one per row an
+    int8 matrix uses, c/qwen.c:1765-1768)."""
     H, E, K, I, Ish = SHAPE
-    rng = np.random.default_rng(3)
     hl = oracle.host_layer(6, 1, H, E, K, I, Ish, 4)
-    t = st_writer.moe_layer_tensors(hl, 1)
-    t.update(_int2_tensors(rng, 1, E, H, I))
-    st_writer.write_split(str(tmp_path / "q2main"), t, parts=2)
-    t = st_writer.moe_layer_tensors(hl, 1)
-    t.update(_int2_tensors(rng, 1, E, H, I, suffix=".q2"))
-    st_writer.write_split(str(tmp_path / "q2side"), t, parts=2)
     hl64 = oracle.host_layer(6, 1, H, E, K, I, Ish, 4, gs=64)
     st_writer.write_split(str(tmp_path / "g64"), st_writer.moe_layer_tensors(hl64, 1), parts=1)
     t = st_writer.moe_layer_tensors(hl, 1)
@@ -92,8 +128,7 @@ def test_container_load_refusals(be, oracle, tmp_path):
         np.asarray(hl.shared_down.s, np.float32)[:, None], 2, axis=1)
     st_writer.write_split(str(tmp_path / "i8two"), t, parts=1)
     from shiftwing_amd import Container
-    for d, sidecar, msg in (("q2main", 0, "format 2"), ("q2side", 2, "format 2"), ("g64", 0, "groups of 64"),
-                            ("i8two", 0, "2 scales per row")):
+    for d, sidecar, msg in (("g64", 0, "groups of 64"), ("i8two", 0, "2 scales per row")):
         print(f"[container refusal] {d}", flush=True)
         c = Container(str(tmp_path / d))
         try:
@@ -104,11 +139,3 @@ def test_container_load_refusals(be, oracle, tmp_path):
             assert msg in err, (d, err)
         finally:
             c.close()
-    # the same directory's main int4 payloads still load (the .q2 sidecars unused)
-    Lc = _load(be, str(tmp_path / "q2side"), 1, K, 0, H)
-    x = oracle.synth_x(6, 1, 0, H)
-    want, tr = oracle.moe_forward(hl, x, trace=True)
-    y, idx, _ = Lc.forward_host(x)
-    assert np.array_equal(idx[0], tr["idx"])
-    assert_close_rms(y[0], want, 1e-3, "q2side main payload")
-    Lc.close()

@@ -13,7 +13,7 @@ from conftest import GOLDEN, assert_close_rms
 
 pytestmark = pytest.mark.gpu
 
-LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3"]
+LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3", "small_q2", "ragged_q2"]
 
 
 def _load(name):
@@ -96,8 +96,9 @@ def test_exact_router_mode_bitexact_weights(be, oracle):
     assert tok == c["T"] and fb == c["T"]
 
 
-@pytest.mark.parametrize("shape", [(256, 16, 4, 128, 128, 3), (384, 32, 8, 257, 129, 4), (384, 32, 8, 200, 100, 3)],
-                         ids=["small_q3", "ragged_q4", "ragged_q3"])
+@pytest.mark.parametrize("shape", [(256, 16, 4, 128, 128, 3), (384, 32, 8, 257, 129, 4), (384, 32, 8, 200, 100, 3),
+                                   (384, 32, 8, 257, 129, 2)],
+                         ids=["small_q3", "ragged_q4", "ragged_q3", "ragged_q2"])
 def test_upload_path_equals_device_synthesis(be, oracle, shape):
     """Weights uploaded in the container layout (set_router / set_shared_q8 /
     set_expert, repacked on device) give the same result as device synthesis,
@@ -133,6 +134,52 @@ def test_upload_path_equals_device_synthesis(be, oracle, shape):
     assert_close_rms(y1a[0], want1, 1e-3, "upload path vs oracle, one token")
     A.close()
     B.close()
+
+
+def test_int2_layer_equals_int4_layer_of_widened_codes(be, oracle):
+    """An int2 layer (expert_format 2) is an int4 layer whose codes are the
+    int2 codes widened as the reference's q2_expand_q4 does (c/qwen.c:567-575:
+    nibble 5 + 2c, the same value 2c - 3), widened here on the host: both
+    give the same bits for one token and for a block."""
+    from shiftwing_amd import MoeLayer
+    H, E, K, I, Ish = 512, 16, 4, 256, 128
+    hl = oracle.host_layer(31, 1, H, E, K, I, Ish, 2)
+
+    def widen(q):
+        c = [(q >> (2 * k)) & 3 for k in range(4)]
+        n = [(5 + 2 * ck).astype(np.uint8) for ck in c]
+        out = np.empty(q.shape[:-1] + (2 * q.shape[-1],), np.uint8)
+        out[..., 0::2] = n[0] | (n[1] << 4)
+        out[..., 1::2] = n[2] | (n[3] << 4)
+        return out
+
+    A = MoeLayer(be, H, E, K, I, Ish, 2)
+    A.synthesize(31, 1)
+    B = MoeLayer(be, H, E, K, I, Ish, 4)
+    keep = [be.upload(hl.router_w), be.upload(hl.shared_gate_row)]
+    B.set_router(*keep)
+    sh = [be.upload(a) for a in (hl.shared_gate.q, hl.shared_gate.s, hl.shared_up.q, hl.shared_up.s,
+                                 hl.shared_down.q, hl.shared_down.s)]
+    B.set_shared_q8(*sh)
+    for e in range(E):
+        bufs = [be.upload(np.ascontiguousarray(a)) for a in (widen(hl.gq[e]), hl.gsc[e], widen(hl.uq[e]),
+                                                               hl.usc[e], widen(hl.dq[e]), hl.dsc[e])]
+        B.set_expert(e, *bufs)
+        be.sync()
+    try:
+        x = np.stack([oracle.synth_x(31, 1, t, H) for t in range(6)])
+        for rows in (x[:1], x):
+            ya, ia, _ = A.forward_host(rows)
+            yb, ib, _ = B.forward_host(rows)
+            assert np.array_equal(ia, ib)
+            assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32))
+        want, tr = oracle.moe_prefill(hl, x, trace=True)
+        y, idx, _ = A.forward_host(x)
+        assert np.array_equal(idx, tr["idx"])
+        assert_close_rms(y, want, 1e-3, "int2 layer vs oracle")
+    finally:
+        A.close()
+        B.close()
 
 
 @pytest.mark.parametrize("seed", [101, 202, 303])

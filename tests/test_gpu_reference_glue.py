@@ -139,14 +139,16 @@ def glue():
     g.lib.ref_cuda_stop()
 
 
-@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397)],
-                         ids=["s35_q4", "s397_q3"])
+@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397),
+                                        ((2048, 256, 8, 512, 512, 2), 36)],
+                         ids=["s35_q4", "s397_q3", "s35_q2"])
 def test_reference_glue_moe_forward(glue, oracle, shape, seed):
     """moe_forward with the device backend active: the reference routes on the
     host and runs cuda_experts_try (c/qwen.c:1270) -> coli_cuda_grouped_q{4,3}_mlp_f16
     and the q8 shared expert via cuda_mlp_try (q8_gemv, silu_mul) on this
     library.  fp16 activations (CUDA_F16=1), then fp32 (per-expert q4/q3 gemv
-    + silu_mul + axpy)."""
+    + silu_mul + axpy).  int2 experts reach the q4 kernels widened by the
+    reference's own upload (q2_expand_q4, c/qwen.c:567-575)."""
     H, E, K, I, Ish, fmt = shape
     hl = oracle.host_layer(seed, 2, H, E, K, I, Ish, fmt)
     h = glue.lib.ref_layer_create(C.byref(hl.st))
@@ -197,8 +199,9 @@ def test_reference_glue_speculative_block(glue, oracle):
         glue.lib.ref_layer_destroy(h)
 
 
-@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397)],
-                         ids=["s35_q4", "s397_q3"])
+@pytest.mark.parametrize("shape,seed", [((2048, 256, 8, 512, 512, 4), 35), ((4096, 512, 10, 1024, 1024, 3), 397),
+                                        ((2048, 256, 8, 512, 512, 2), 36)],
+                         ids=["s35_q4", "s397_q3", "s35_q2"])
 def test_bridge_device_moe_step(glue, oracle, shape, seed):
     """shiftwing_amd/integration/sw_qwen_bridge.inc compiled into the reference
     engine: sw_moe_register copies a loaded MoeW (router, shared expert, every

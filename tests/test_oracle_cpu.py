@@ -22,7 +22,7 @@ import pytest
 
 from conftest import GOLDEN
 
-LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3"]
+LAYERS = ["small_q4", "small_q3", "ragged_q4", "ragged_q3", "s35_q4", "s397_q3", "small_q2", "ragged_q2"]
 
 
 def _bits(a):
@@ -94,6 +94,66 @@ def test_qmat_golden_bitexact(oracle):
         assert np.array_equal(_bits(oracle.qmat_mul_batch(g[k + "_X"], m)), _bits(g[k + "_Y"])), k
 
 
+def test_qmat_q2_golden_bitexact(oracle):
+    """int2 rows (dot_q2_group, c/qwen.c:1717-1724) bit for bit against the
+    compiled reference's qmat_mul, ragged widths included."""
+    from oracle.pyoracle import HostQMat
+    g = np.load(os.path.join(GOLDEN, "qmat_q2.npz"))
+    keys = sorted({k.rsplit("_", 1)[0] for k in g.files if k.endswith("_q")})
+    assert keys
+    for k in keys:
+        I = int(k.split("_")[1][1:])
+        q, s = g[k + "_q"], g[k + "_s"]
+        m = HostQMat(2, q.shape[0], I, 128, q=q, s=s)
+        assert np.array_equal(_bits(oracle.qmat_mul(g[k + "_x"], m, 1)), _bits(g[k + "_y"])), k
+        # and up to rounding the brute-force dequantisation
+        w = _dequant(2, q, s, I)
+        x = g[k + "_x"].astype(np.float64)
+        got = oracle.qmat_mul(g[k + "_x"], m, 0)
+        assert np.all(np.abs(got - w @ x) <= 1e-5 * (np.abs(w) @ np.abs(x) + 1e-30)), k
+
+
+def test_q2_group_known_answers_and_exact_sums(oracle):
+    """int2 layout: byte 0b11100100 holds codes 0, 1, 2, 3 (lowest bits
+    first), values 2c - 3 = -3, -1, 1, 3.  With small-integer activations
+    every partial sum is exact, so any order gives sum x_i (2 c_i - 3)
+    exactly: random codes pin the bit positions and the value map."""
+    import ctypes as C
+    L = oracle.lib
+    w = np.array([0b11100100], np.uint8)
+    x = np.array([1, 10, 100, 1000], np.float32)
+    assert L.or_dot_q2_group(w.ctypes.data, x.ctypes.data_as(C.POINTER(C.c_float)), 4) == 3087.0
+    rng = np.random.default_rng(4)
+    for n in (1, 5, 64, 128):
+        q = rng.integers(0, 256, (n + 3) // 4, dtype=np.uint8)
+        xi = rng.integers(-8, 9, n).astype(np.float32)
+        codes = (q[np.arange(n) >> 2] >> (2 * (np.arange(n) & 3))) & 3
+        want = float(np.sum(xi.astype(np.int64) * (2 * codes.astype(np.int64) - 3)))
+        got = L.or_dot_q2_group(q.ctypes.data, xi.ctypes.data_as(C.POINTER(C.c_float)), n)
+        assert got == want, n
+
+
+def test_q2_group_matches_compiled_reference(oracle):
+    """Random groups (lengths 1..128, activations of three magnitudes):
+    or_dot_q2_group equals the compiled dot_q2_group bit for bit (gcc keeps
+    the scalar loop in order and contracts it into an FMA chain)."""
+    import ctypes as C
+    from oracle.pyoracle import Reference
+    try:
+        ref = Reference()
+    except Exception as e:  # not built (no reference sources here)
+        pytest.skip(f"compiled reference not available: {e}")
+    rng = np.random.default_rng(6)
+    f32p = C.POINTER(C.c_float)
+    for n in (1, 3, 4, 31, 64, 127, 128):
+        for _ in range(100):
+            q = rng.integers(0, 256, (n + 3) // 4, dtype=np.uint8)
+            x = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 1e3])).astype(np.float32)
+            a = oracle.lib.or_dot_q2_group(q.ctypes.data, x.ctypes.data_as(f32p), n)
+            b = ref.lib.ref_dot_q2_group(q.ctypes.data, x.ctypes.data_as(f32p), n)
+            assert _bits(a) == _bits(b), n
+
+
 def _dequant(fmt, q, s, I, gs=128):
     """Brute-force dequantisation from the byte layouts (fp64)."""
     O = q.shape[0]
@@ -107,6 +167,8 @@ def _dequant(fmt, q, s, I, gs=128):
                 byte = int(q[o, i >> 1])
                 code = (byte & 15) if (i & 1) == 0 else (byte >> 4)
                 v = code - 8
+            elif fmt == 2:
+                v = 2 * ((int(q[o, i >> 2]) >> (2 * (i & 3))) & 3) - 3
             else:
                 j, k = i // 8, i % 8
                 word = int(q[o, 3 * j]) | int(q[o, 3 * j + 1]) << 8 | int(q[o, 3 * j + 2]) << 16
