@@ -309,12 +309,24 @@ __global__ __launch_bounds__(256) void k_mix_proj(ProjArgs a) {
             for (int q = 0; q < 2; q++) {
               const uint4 wq = w[ci][r2 + q];
               const unsigned wd[4] = {wq.x, wq.y, wq.z, wq.w};
+              if (FMT == 4) {
+                // nibble bytes through opaque masks, so that each value is
+                // one v_cvt_f32_ubyte0..3 (column 8d + 2b: low nibble of
+                // byte b, 8d + 2b + 1: its high nibble)
 #pragma unroll
-              for (int e = 0; e < CPL; e++) {
-                if (FMT == 4)
-                  wf[q][e] = (float)((int)((wd[e / 8] >> (4 * (e % 8))) & 15u) - 8);
-                else
-                  wf[q][e] = (float)(signed char)((wd[e / 4] >> (8 * (e % 4))) & 255u);
+                for (int d = 0; d < 4; d++) {
+                  unsigned lo, hi;
+                  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(wd[d]));
+                  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(wd[d] >> 4));
+#pragma unroll
+                  for (int b = 0; b < 4; b++) {
+                    wf[q][8 * d + 2 * b] = (float)((lo >> (8 * b)) & 255u) - 8.0f;
+                    wf[q][8 * d + 2 * b + 1] = (float)((hi >> (8 * b)) & 255u) - 8.0f;
+                  }
+                }
+              } else {
+#pragma unroll
+                for (int e = 0; e < CPL; e++) wf[q][e] = (float)(signed char)((wd[e / 4] >> (8 * (e % 4))) & 255u);
               }
             }
 #pragma unroll
@@ -942,7 +954,11 @@ __global__ __launch_bounds__(256) void k_mix_proj_direct(ProjArgs a) {
         if (FMT == 4) {
 #pragma unroll
           for (int q = 0; q < 4; q++) {
-            const unsigned lo = wd[q] & 0x0F0F0F0Fu, hi = (wd[q] >> 4) & 0x0F0F0F0Fu;
+            // the masks as opaque instructions: seen through, they become a
+            // bit-field extract per nibble instead of v_cvt_f32_ubyte1..3
+            unsigned lo, hi;
+            asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(wd[q]));
+            asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(wd[q] >> 4));
 #pragma unroll
             for (int b = 0; b < 4; b++) {
               p0 = __builtin_fmaf((float)((lo >> (8 * b)) & 255u), xv[t][8 * q + 2 * b], p0);
