@@ -863,7 +863,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding is a design only, see DESIGN.md)", file=sys.stderr)
+              "(the path's multi-GPU sharding is designed, not built)", file=sys.stderr)
         sys.exit(2)
     if args.copy_probe:
         copy_probe(args.copy_probe)
