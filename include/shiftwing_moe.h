@@ -405,7 +405,9 @@ int coli_cuda_container_moe_shape(const ColiContainer *c, int layer, int sidecar
 /* Create an HBM-resident layer and fill it from the container: router and
  * gate row (F32, BF16 or F16), the int8 shared expert (one scale per row),
  * every routed expert (int4, int3 from the .q3 sidecar, or int2 from .q2
- * sidecars / .qtype 2, in groups of 128), repacked on the device.  Other
+ * sidecars / .qtype 2, in groups of 128; with sidecar 2 an expert without a
+ * .q2 sidecar keeps its int4 payload, both held as int4 records), repacked
+ * on the device.  Other
  * group sizes, which the reference's CPU path reads, return -1 with a
  * message: the device layer does not take them. */
 int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, int layer,

@@ -36,6 +36,7 @@
 #include <vector>
 
 #include "sw_backend.h"
+#include "sw_moe_layer.h"
 
 using sw::fail_arg;
 using sw::fail_hip;
@@ -486,18 +487,29 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
     return -1;
   if (sgq.fmt != 1 || suq.fmt != 1 || sdq.fmt != 1 || gate_row.fmt != 0)
     return fail_arg("coli_cuda_moe_layer_load: layer %d: the shared expert must be int8 and its gate row float", layer);
-  // every routed expert: one format and geometry
+  // every routed expert: one format and geometry; int2 and int4 experts may
+  // mix (the .q2 sidecar where an expert has one, else its int4 payload), as
+  // both are held as int4 records
   std::vector<QInfo> xq((size_t)E * 3);
   static const char *proj[3] = {"gate_proj", "up_proj", "down_proj"};
+  const bool mix24 = fmt == 2 || fmt == 4;
+  bool any2 = false;
   for (int e = 0; e < E; e++)
     for (int k = 0; k < 3; k++) {
       QInfo &q = xq[(size_t)e * 3 + k];
       if (qinfo(c, expert_name(layer, e, proj[k]), k == 2 ? H : I, k == 2 ? I : H, sidecar, q)) return -1;
       const QInfo &ref = xq[k];
-      if (q.fmt != fmt || q.gs != s.group_size || q.rb != ref.rb || q.ng != ref.ng)
+      const bool fmt_ok = q.fmt == fmt || (mix24 && (q.fmt == 2 || q.fmt == 4));
+      if (!fmt_ok || q.gs != s.group_size || q.ng != ref.ng || (q.fmt == ref.fmt && q.rb != ref.rb))
         return fail_arg("coli_cuda_moe_layer_load: layer %d expert %d %s: format %d / group %d differs from expert 0",
                         layer, e, proj[k], q.fmt, q.gs);
+      const QInfo &g0 = xq[(size_t)e * 3];
+      if (k > 0 && q.fmt != g0.fmt)
+        return fail_arg("coli_cuda_moe_layer_load: layer %d expert %d: projections in formats %d and %d", layer, e,
+                        g0.fmt, q.fmt);
+      any2 = any2 || q.fmt == 2;
     }
+  if (any2) s.expert_format = 2;
   ColiMoeLayer *L = nullptr;
   if (coli_cuda_moe_layer_create(ctx, &L, &s)) return -1;
   auto bail = [&](int rc) {
@@ -506,9 +518,13 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
     return rc;
   };
   // staging: router + gate row, the shared expert, or one routed expert
-  const size_t gqb = xq[0].q->nbytes, gsb = (size_t)xq[0].s->numel * 4, dqb = xq[2].q->nbytes,
-               dsb = (size_t)xq[2].s->numel * 4;
-  const size_t expert_b = 2 * (gqb + gsb) + dqb + dsb;
+  // the largest expert (int4 and int2 experts differ in code bytes)
+  size_t expert_b = 0;
+  for (int e = 0; e < E; e++) {
+    const QInfo *q = &xq[(size_t)e * 3];
+    const size_t b = 2 * (q[0].q->nbytes + (size_t)q[0].s->numel * 4) + q[2].q->nbytes + (size_t)q[2].s->numel * 4;
+    expert_b = b > expert_b ? b : expert_b;
+  }
   const size_t shared_b = 3 * (size_t)Ish * H + (2 * (size_t)Ish + H) * 4;
   const size_t router_b = ((size_t)E + 1) * H * 4;
   const size_t slot = std::max(expert_b, std::max(shared_b, router_b));
@@ -576,6 +592,7 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
         });
   for (int e = 0; !rc && e < E; e++) {
     const QInfo *q = &xq[(size_t)e * 3];
+    const size_t gqb = q[0].q->nbytes, gsb = (size_t)q[0].s->numel * 4, dqb = q[2].q->nbytes;
     rc = stage(
         [&](char *h, size_t &n) {
           n = expert_b;
@@ -585,10 +602,10 @@ extern "C" int coli_cuda_moe_layer_load(ColiCuda *ctx, const ColiContainer *c, i
                  read_f32(c, *q[2].s, (float *)(p + 2 * (gqb + gsb) + dqb));
         },
         [&](char *d) {
-          return coli_cuda_moe_layer_set_expert(
-              ctx, L, e, (const unsigned char *)d, (const float *)(d + 2 * gqb), (const unsigned char *)(d + gqb),
-              (const float *)(d + 2 * gqb + gsb), (const unsigned char *)(d + 2 * (gqb + gsb)),
-              (const float *)(d + 2 * (gqb + gsb) + dqb));
+          return sw::set_expert_as(
+              ctx, L, e, q[0].fmt, (const unsigned char *)d, (const float *)(d + 2 * gqb),
+              (const unsigned char *)(d + gqb), (const float *)(d + 2 * gqb + gsb),
+              (const unsigned char *)(d + 2 * (gqb + gsb)), (const float *)(d + 2 * (gqb + gsb) + dqb));
         });
   }
   const hipError_t e = hipStreamSynchronize(ctx->stream);

@@ -2828,15 +2828,21 @@ static int repack_matrix(ColiCuda *ctx, const TileMat &dst, const unsigned char 
   return launch_status("expert repack");
 }
 
-extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, int expert,
-                                              const unsigned char *gq, const float *gs, const unsigned char *uq,
-                                              const float *us, const unsigned char *dq, const float *ds) {
+namespace sw {
+// One expert in container format `fmt`: the layer's own, or, for a layer held
+// as int4 records (int4 or int2 experts), 2 or 4 per expert (EXPERT_Q2=1 takes
+// an expert's .q2 sidecar where it has one, else its int4 payload,
+// c/qwen.c:2207-2214).
+int set_expert_as(ColiCuda *ctx, ColiMoeLayer *L, int expert, int src_fmt, const unsigned char *gq, const float *gs,
+                  const unsigned char *uq, const float *us, const unsigned char *dq, const float *ds) {
   if (!ctx || !L || !gq || !gs || !uq || !us || !dq || !ds)
     return fail_arg("coli_cuda_moe_layer_set_expert: null argument");
   if (expert < 0 || expert >= L->sh.experts)
     return fail_arg("coli_cuda_moe_layer_set_expert: expert %d outside [0,%d)", expert, L->sh.experts);
   int H = L->sh.hidden, I = L->sh.intermediate, Is = L->I_src, fmt = L->sh.expert_format;
-  if (L->src_fmt == 2) {
+  if (src_fmt != L->src_fmt && !(fmt == 4 && (src_fmt == 2 || src_fmt == 4)))
+    return fail_arg("coli_cuda_moe_layer_set_expert: format %d in a layer of format %d", src_fmt, L->src_fmt);
+  if (src_fmt == 2) {
     // each matrix widened into scratch, then repacked as int4 (stream
     // order keeps one matrix's repack ahead of the next one's widening)
     const size_t bh = (size_t)Is * (L->ngh * kGroup / 4), bi = (size_t)H * (L->ngi * kGroup / 4);
@@ -2857,6 +2863,14 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
       repack_matrix(ctx, L->xl.mat(expert, 2), dq, ds, H, H, Is, fmt))
     return -1;
   return 0;
+}
+}  // namespace sw
+
+extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, int expert,
+                                              const unsigned char *gq, const float *gs, const unsigned char *uq,
+                                              const float *us, const unsigned char *dq, const float *ds) {
+  if (!L) return fail_arg("coli_cuda_moe_layer_set_expert: null argument");
+  return sw::set_expert_as(ctx, L, expert, L->src_fmt, gq, gs, uq, us, dq, ds);
 }
 
 extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long seed,

@@ -34,6 +34,10 @@ struct ColiMoeLayer {
 namespace sw {
 // words of ColiMoeLayer::sync for a layer shape
 size_t decode_sync_words(const ColiMoeShape &s);
+// One routed expert given in container format src_fmt (the layer's own; 2 or
+// 4 in a layer held as int4 records)
+int set_expert_as(ColiCuda *ctx, ColiMoeLayer *L, int expert, int src_fmt, const unsigned char *gq, const float *gs,
+                  const unsigned char *uq, const float *us, const unsigned char *dq, const float *ds);
 // One decoded token through one layer (three kernels).  Returns 0 on success,
 // -1 on error, 1 when the layer shape is outside the decode kernels' limits.
 int decode_step(ColiCuda *ctx, ColiMoeLayer *L, float *y, const float *x, int *route_idx, float *route_weight);

@@ -113,6 +113,41 @@ def test_container_int2_loads(be, oracle, tmp_path):
     Lc.close()
 
 
+def test_container_int2_sidecars_with_an_int4_fallback(be, oracle, tmp_path):
+    """EXPERT_Q2=1 takes an expert's .q2 sidecar where it has one, else its
+    int4 payload (c/qwen.c:2207-2214): with the last expert's sidecar
+    missing, the loaded layer mixes int2 and int4 experts (both held as int4
+    records) and matches moe_forward / moe_prefill_grouped over the same
+    mixed layer."""
+    H, E, K, I, Ish = SHAPE
+    hl4 = oracle.host_layer(12, 1, H, E, K, I, Ish, 4)
+    mix = oracle.host_layer(12, 1, H, E, K, I, Ish, 2)
+    t = st_writer.moe_layer_tensors(hl4, 1, q2=mix)
+    for nm in ("gate", "up", "down"):
+        base = f"layers.1.mlp.experts.{E - 1}.{nm}_proj.weight.q2"
+        for sfx in ("", ".qs", ".qtype"):
+            del t[base + sfx]
+    st_writer.write_split(str(tmp_path), t, parts=2)
+    # the CPU checker's layer: int2 experts but the last, which is int4
+    mix._g[E - 1], mix._u[E - 1], mix._d[E - 1] = hl4.gate[E - 1].st, hl4.up[E - 1].st, hl4.down[E - 1].st
+    # tokens 1, 4 and 5 route to the last (int4) expert
+    x = np.stack([oracle.synth_x(12, 1, t_, H) for t_ in range(6)])
+    Lc = _load(be, str(tmp_path), 1, K, 2, H)
+    try:
+        want, tr = oracle.moe_prefill(mix, x, trace=True)
+        y, idx, _ = Lc.forward_host(x)
+        assert np.array_equal(idx, tr["idx"])
+        assert_close_rms(y, want, 1e-3, "int2 + int4 fallback block")
+        assert E - 1 in set(np.asarray(tr["idx"]).ravel().tolist())
+        for r in range(2):
+            w1, tr1 = oracle.moe_forward(mix, x[r], trace=True)
+            y1, i1, _ = Lc.forward_host(x[r])
+            assert np.array_equal(i1[0], tr1["idx"])
+            assert_close_rms(y1[0], w1, 1e-3, f"int2 + int4 fallback token {r}")
+    finally:
+        Lc.close()
+
+
 def test_container_load_refusals(be, oracle, tmp_path):
     """Layers the device layer does not take return -1 with a message from
     coli_cuda_moe_layer_load, and nothing is created: int4 experts in groups
