@@ -374,6 +374,19 @@ int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *layer,
                                    const float *up_s,
                                    const unsigned char *down_q,
                                    const float *down_s);
+/* The same for one expert in container format expert_format: the layer's
+ * own, or 2 or 4 in a layer created with format 2 or 4 (both held as int4
+ * records).  No counterpart in the reference backend: for loaders whose
+ * layers mix int2 and int4 experts, as EXPERT_Q2=1 reads a snapshot whose
+ * .q2 sidecars cover only some experts (c/qwen.c:2207-2214). */
+int coli_cuda_moe_layer_set_expert_format(ColiCuda *ctx, ColiMoeLayer *layer,
+                                          int expert, int expert_format,
+                                          const unsigned char *gate_q,
+                                          const float *gate_s,
+                                          const unsigned char *up_q,
+                                          const float *up_s,
+                                          const unsigned char *down_q,
+                                          const float *down_s);
 /* Generate the whole layer on the device from the counter hash of
  * shiftwing_amd/csrc/sw_synth.h (identical bytes to the host generator). */
 int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *layer,

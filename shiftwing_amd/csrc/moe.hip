@@ -2873,6 +2873,14 @@ extern "C" int coli_cuda_moe_layer_set_expert(ColiCuda *ctx, ColiMoeLayer *L, in
   return sw::set_expert_as(ctx, L, expert, L->src_fmt, gq, gs, uq, us, dq, ds);
 }
 
+extern "C" int coli_cuda_moe_layer_set_expert_format(ColiCuda *ctx, ColiMoeLayer *L, int expert, int expert_format,
+                                                     const unsigned char *gq, const float *gs,
+                                                     const unsigned char *uq, const float *us,
+                                                     const unsigned char *dq, const float *ds) {
+  if (!L) return fail_arg("coli_cuda_moe_layer_set_expert_format: null argument");
+  return sw::set_expert_as(ctx, L, expert, expert_format, gq, gs, uq, us, dq, ds);
+}
+
 extern "C" int coli_cuda_moe_layer_synthesize(ColiCuda *ctx, ColiMoeLayer *L, unsigned long long seed,
                                               int layer_index) {
   if (!ctx || !L) return fail_arg("coli_cuda_moe_layer_synthesize: null argument");

@@ -268,6 +268,39 @@ def test_bridge_device_activations_and_hooks(glue, oracle, shape, seed):
         glue.lib.ref_layer_destroy(h)
 
 
+def test_bridge_registers_layers_mixing_int2_and_int4_experts(glue, oracle):
+    """A reference layer as EXPERT_Q2=1 leaves it when only some experts have
+    .q2 sidecars (c/qwen.c:2207-2214): int2 experts with int4 ones (here the
+    first and the last, expert 0 deciding the layer's format).  sw_moe_register
+    takes it (both held as int4 records, each expert given in its own format),
+    and the device step matches moe_forward / moe_prefill_grouped over the
+    same mixed layer; the tokens route to both kinds."""
+    H, E, K, I, Ish = 2048, 64, 8, 512, 512
+    hl4 = oracle.host_layer(44, 2, H, E, K, I, Ish, 4)
+    mix = oracle.host_layer(44, 2, H, E, K, I, Ish, 2)
+    for e in (0, E - 1):
+        mix._g[e], mix._u[e], mix._d[e] = hl4.gate[e].st, hl4.up[e].st, hl4.down[e].st
+    h = glue.lib.ref_layer_create(C.byref(mix.st))
+    try:
+        assert glue.lib.ref_sw_register(h) == 1
+        x = np.stack([oracle.synth_x(44, 2, 400 + t, H) for t in range(5)])
+        for T in (1, 5):
+            print(f"[bridge int2+int4] T={T}", flush=True)
+            used, got, idx = glue.sw_forward(h, x[:T], K)
+            assert used == 1 and glue.counters()["failed"] == 0
+            if T == 1:
+                want, tr = oracle.moe_forward(mix, x[0], trace=True)
+                want, want_idx = want[None], tr["idx"][None]
+            else:
+                want, tr = oracle.moe_prefill(mix, x, trace=True)
+                want_idx = tr["idx"]
+                assert {0, E - 1} <= set(np.asarray(want_idx).ravel().tolist())
+            assert np.array_equal(idx, want_idx), (T, idx, want_idx)
+            assert_close_rms(got, want, 1e-3, f"bridge int2+int4 T={T}")
+    finally:
+        glue.lib.ref_layer_destroy(h)
+
+
 def test_bridge_declines_layers_it_does_not_take(glue, oracle):
     """A reference layer whose routed experts use groups of 64 (which the
     reference's CPU path computes, c/qwen.c:1706-1716 with gs = 64) is not
