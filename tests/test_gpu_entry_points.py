@@ -80,6 +80,31 @@ def test_q4_gemm_batch(be):
     assert np.max(np.abs(got - want)) < 2e-4
 
 
+@pytest.mark.parametrize("gs", [32, 64])
+def test_q4_gemm_other_group_sizes(be, gs):
+    """The Part 1 GEMMs take the group size as an argument, as the reference's
+    kernels do (c/backend_cuda.cu:485-496: sr[i / group_size]); the CPU path
+    derives it as rb*2/ng (c/qwen.c:2253).  A layer quantised in groups other
+    than 128 therefore runs on these entry points."""
+    ng = (COLS + gs - 1) // gs
+    rb = ng * (gs // 2)
+    q = np.zeros((ROWS, rb), np.uint8)
+    for r in range(ROWS):
+        codes = (r * 5 + np.arange(rb * 2) * 7) % 16
+        q[r] = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)
+    s = np.array([[np.ldexp(1.0, ((r + 2 * g) % 7) - 7) for g in range(ng)] for r in range(ROWS)], np.float32)
+    x = _x(2)
+    dq, ds, dx, dy = be.upload(q), be.upload(s), be.upload(x), be.alloc(2 * ROWS * 4)
+    be.check(be.lib.coli_cuda_q4_gemm(be.ctx, dy.p, dx.p, 2, dq.p, ds.p, ROWS, COLS, gs, rb, ng), "q4_gemm")
+    got = be.download(dy, (2, ROWS), np.float32)
+    codes = np.empty((ROWS, rb * 2), np.int64)
+    codes[:, 0::2] = q & 15
+    codes[:, 1::2] = q >> 4
+    w = (codes[:, :COLS] - 8).astype(np.float64) * np.repeat(s.astype(np.float64), gs, axis=1)[:, :COLS]
+    want = x.astype(np.float64) @ w.T
+    assert np.max(np.abs(got - want)) < 2e-4
+
+
 def test_sigmoid_axpy_copy_memset(be, oracle):
     i = np.arange(N, dtype=np.float32)
     y0 = (np.cos(i * 7 + 2) * 0.0625).astype(np.float32)
