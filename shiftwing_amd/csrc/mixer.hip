@@ -739,10 +739,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_gqa_attn(AttnArgs a) {
 }
 
 // Merge the splits of one (row, query head), divide by the softmax sum and
-// apply the sigmoid gate (c/qwen.c:3129-3134).  The split maxima and weights
-// go through LDS; each thread then sums one dim over the splits.
-// grid (nh, B), head_dim threads; S <= kMaxSplits.
-constexpr int kMaxSplits = 1024;
+// apply the sigmoid gate (c/qwen.c:3129-3134).  A workgroup takes 64 dims of
+// one head (one per lane), its 4 waves the splits w, w + 4, ...: lane i of
+// wave w loads split w + 4i's maximum and sum (one load each for the wave),
+// the wave's maximum and weights follow by lane reductions, and its lanes'
+// partial outputs of up to 32 splits a round issue before the first is used
+// (each split's weight read from the lane that holds it).  The waves meet in
+// LDS in wave order.  grid (nh * hd / 64, B), 256 threads; S <= kMaxSplits.
+constexpr int kMaxSplits = 256;
+constexpr int kCombWaves = 4, kCombBatch = 32;
 struct CombArgs {
   const float *part, *gate;
   float *ctx;  // [B][nh*hd]
@@ -750,50 +755,59 @@ struct CombArgs {
 };
 
 __global__ __launch_bounds__(256) void k_gqa_combine(CombArgs c) {
-  __shared__ float s_w[kMaxSplits], s_red[4];
-  const int h = blockIdx.x, t = blockIdx.y, j = threadIdx.x, hd = c.hd, nw = hd >> 6;
-  const int G = c.nh / c.nkv, kvh = h / G, n = h % G;
+  __shared__ float s_o[kCombWaves][64], s_m[kCombWaves], s_l[kCombWaves];
+  const int hd = c.hd, dq = hd >> 6, h = blockIdx.x / dq, t = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, j = 64 * (blockIdx.x % dq) + lane;
+  const int G = c.nh / c.nkv, kvh = h / G, n = h % G, S = c.S;
   const size_t psz = (size_t)16 * hd + 32;
-  const float *base = c.part + (size_t)(t * c.nkv + kvh) * c.S * psz;
-  float mx = -INFINITY;
-  for (int s = j; s < c.S; s += hd) mx = fmaxf(mx, base[s * psz + 16 * hd + n]);
-  mx = wave_max_dpp(mx);
-  if ((j & 63) == 0) s_red[j >> 6] = mx;
-  __syncthreads();
-  float M = s_red[0];
-  for (int w = 1; w < nw; w++) M = fmaxf(M, s_red[w]);
-  __syncthreads();
-  float lp = 0.0f;
-  for (int s = j; s < c.S; s += hd) {
-    const float ms = base[s * psz + 16 * hd + n];
-    const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
-    s_w[s] = w;
-    lp = __builtin_fmaf(base[s * psz + 16 * hd + 16 + n], w, lp);
+  const float *base = c.part + (size_t)(t * c.nkv + kvh) * S * psz;
+  const size_t at = (size_t)t * c.nh * hd + (size_t)h * hd + j;
+  const float g = w == 0 ? c.gate[at] : 0.0f;
+  const int sl = w + kCombWaves * lane;  // this lane's split for the maximum and sum
+  float m = -INFINITY, lv = 0.0f;
+  if (sl < S) {
+    m = base[(size_t)sl * psz + 16 * hd + n];
+    lv = base[(size_t)sl * psz + 16 * hd + 16 + n];
   }
-  lp = wave_sum_dpp(lp);
-  if ((j & 63) == 0) s_red[j >> 6] = lp;
-  __syncthreads();
-  float L = 0.0f;
-  for (int w = 0; w < nw; w++) L += s_red[w];
-  const float *op = base + (size_t)n * hd + j;
-  float O0 = 0.0f, O1 = 0.0f, O2 = 0.0f, O3 = 0.0f;
-  int s = 0;
-  for (; s + 16 <= c.S; s += 16) {
-    float v[16];
+  const int ns = S > w ? (S - w + kCombWaves - 1) / kCombWaves : 0;  // the wave's splits
+  float o = 0.0f, mb = -INFINITY, lsum = 0.0f;
+  if (ns > 0) {
+    float vo[kCombBatch];
+    const float *op = base + (size_t)n * hd + j;
 #pragma unroll
-    for (int k = 0; k < 16; k++) v[k] = op[(size_t)(s + k) * psz];
-    asm volatile("" ::: "memory");
+    for (int k = 0; k < kCombBatch; k++)
+      vo[k] = op[(size_t)(k < ns ? w + kCombWaves * k : w) * psz];
+    mb = wave_max_dpp(m);
+    const float wl = m == -INFINITY ? 0.0f : expf(m - mb);
+    lsum = wave_sum_dpp(lv * wl);
 #pragma unroll
-    for (int k = 0; k < 16; k += 4) {
-      O0 = __builtin_fmaf(v[k], s_w[s + k], O0);
-      O1 = __builtin_fmaf(v[k + 1], s_w[s + k + 1], O1);
-      O2 = __builtin_fmaf(v[k + 2], s_w[s + k + 2], O2);
-      O3 = __builtin_fmaf(v[k + 3], s_w[s + k + 3], O3);
+    for (int k = 0; k < kCombBatch; k++)
+      o = __builtin_fmaf(vo[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k)), o);
+    for (int k0 = kCombBatch; k0 < ns; k0 += kCombBatch) {
+#pragma unroll
+      for (int k = 0; k < kCombBatch; k++)
+        vo[k] = op[(size_t)(k0 + k < ns ? w + kCombWaves * (k0 + k) : w) * psz];
+#pragma unroll
+      for (int k = 0; k < kCombBatch; k++)
+        o = __builtin_fmaf(vo[k], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k0 + k)), o);
     }
   }
-  for (; s < c.S; s++) O0 = __builtin_fmaf(op[(size_t)s * psz], s_w[s], O0);
-  const size_t at = (size_t)t * c.nh * hd + (size_t)h * hd + j;
-  c.ctx[at] = (((O0 + O1) + (O2 + O3)) / L) * sigmoid_ref(c.gate[at]);
+  s_o[w][lane] = o;
+  if (lane == 0) {
+    s_m[w] = mb;
+    s_l[w] = lsum;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  float Mx = -INFINITY;
+  for (int q = 0; q < kCombWaves; q++) Mx = fmaxf(Mx, s_m[q]);
+  float O = 0.0f, L = 0.0f;
+  for (int q = 0; q < kCombWaves; q++) {
+    const float f = s_m[q] == -INFINITY ? 0.0f : expf(s_m[q] - Mx);
+    O = __builtin_fmaf(s_o[q][lane], f, O);
+    L = __builtin_fmaf(s_l[q], f, L);
+  }
+  c.ctx[at] = (O / L) * sigmoid_ref(g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1326,7 +1340,7 @@ int gqa_run(ColiCuda *ctx, const GqaCall &c) {
   cb.nkv = c.nkv;
   cb.hd = hd;
   cb.S = S;
-  k_gqa_combine<<<dim3(c.nh, R), hd, 0, ctx->stream>>>(cb);
+  k_gqa_combine<<<dim3(c.nh * (hd / 64), R), 256, 0, ctx->stream>>>(cb);
 
   for (int r0 = 0; r0 < R; r0 += kMixMaxTok) {
     const int n = R - r0 < kMixMaxTok ? R - r0 : kMixMaxTok;
