@@ -538,13 +538,27 @@ __global__ __launch_bounds__(256) void k_gqa_prep(PrepArgs p) {
   const int kvrows = p.nkv * hd, ctxn = p.nh * hd;
   const bool isq = hh < p.nh;
   const int kvh = hh - p.nh;
-  float v;
+  float v, vv = 0.0f;
   if (isq) {
     const float *src = p.qp + (size_t)t * 2 * ctxn + (size_t)hh * 2 * hd;
     v = src[j];
     p.gate[(size_t)t * ctxn + (size_t)hh * hd + j] = src[hd + j];
   } else {
     v = p.kr[(size_t)t * kvrows + (size_t)kvh * hd + j];
+    vv = p.vr[(size_t)t * kvrows + (size_t)kvh * hd + j];
+  }
+  const float nw1 = 1.f + (isq ? p.q_norm : p.k_norm)[j];
+  // the rotation's angle depends on the position only: formed while the
+  // row's loads are in flight
+  const int half = p.rd / 2, pos = tok_pos(p.tok, t);
+  float co = 1.0f, si = 0.0f;
+  if (j < p.rd) {
+    const int i = j < half ? j : j - half;
+    const float e = -2.f * (float)i / (float)p.rd;
+    const float fr = (float)pow((double)p.theta, (double)e);
+    const float ang = (float)pos * fr;
+    co = (float)cos((double)ang);
+    si = (float)sin((double)ang);
   }
   const float s2 = wave_sum_dpp(v * v);
   if (lane == 0) sred[wave] = s2;
@@ -552,16 +566,11 @@ __global__ __launch_bounds__(256) void k_gqa_prep(PrepArgs p) {
   float ms = 0.0f;
   for (int w = 0; w < nw; w++) ms += sred[w];
   const float r = 1.f / sqrtf(ms / (float)hd + p.eps);
-  row[j] = v * r * (1.f + (isq ? p.q_norm : p.k_norm)[j]);
+  row[j] = v * r * nw1;
   __syncthreads();
-  const int half = p.rd / 2, pos = tok_pos(p.tok, t);
   float y = row[j];
   if (j < p.rd) {
     const int i = j < half ? j : j - half;
-    const float e = -2.f * (float)i / (float)p.rd;
-    const float fr = (float)pow((double)p.theta, (double)e);
-    const float ang = (float)pos * fr;
-    const float co = (float)cos((double)ang), si = (float)sin((double)ang);
     const float a = row[i], b = row[i + half];
     y = j < half ? __builtin_fmaf(a, co, -(b * si)) : __builtin_fmaf(b, co, a * si);
   }
@@ -570,7 +579,7 @@ __global__ __launch_bounds__(256) void k_gqa_prep(PrepArgs p) {
   } else {
     const size_t at = (size_t)tok_slot(p.tok, t) * p.slot_stride + (size_t)pos * kvrows + (size_t)kvh * hd + j;
     p.k_cache[at] = y;
-    p.v_cache[at] = p.vr[(size_t)t * kvrows + (size_t)kvh * hd + j];
+    p.v_cache[at] = vv;
   }
 }
 
