@@ -461,16 +461,28 @@ __global__ __launch_bounds__(64) void k_gdn_recur(GdnArgs g) {
   const float invsqrt = 1.f / sqrtf((float)dk);
   const float Ah = expf(g.A_log[h]);
   const float nj = g.norm[j];
+  const float dtb = g.dt_bias[h];
   for (int gt = g.grp.start[gi]; gt < g.grp.start[gi + 1]; gt++) {
     const int t = g.grp.tok[gt];
     const float *mt = g.mix + (size_t)t * C;
-    __syncthreads();
-    for (int i = lane; i < 128; i += 64) {
-      sq[i] = i < dk ? mt[hk * dk + i] : 0.0f;
-      sk[i] = i < dk ? mt[kd + hk * dk + i] : 0.0f;
+    // every load of the token issues before the barrier (which waits for
+    // all of them, the state's included), so they share one round trip
+    float qa[2], ka[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int i = lane + 64 * u;
+      qa[u] = i < dk ? mt[hk * dk + i] : 0.0f;
+      ka[u] = i < dk ? mt[kd + hk * dk + i] : 0.0f;
     }
     const float v = mt[2 * kd + h * dv + j];
     const float zt = g.z[(size_t)t * vd + (size_t)h * dv + j];
+    const float bt = g.b[(size_t)t * g.vh + h], at = g.a[(size_t)t * g.vh + h];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      sq[lane + 64 * u] = qa[u];
+      sk[lane + 64 * u] = ka[u];
+    }
     __syncthreads();
     float pq = 0.0f, pk = 0.0f;
     for (int i = lane; i < 128; i += 64) {
@@ -479,8 +491,8 @@ __global__ __launch_bounds__(64) void k_gdn_recur(GdnArgs g) {
     }
     const float qn = 1.f / sqrtf(wave_sum_dpp(pq) + 1e-6f);
     const float kn = 1.f / sqrtf(wave_sum_dpp(pk) + 1e-6f);
-    const float beta = sigmoid_ref(g.b[(size_t)t * g.vh + h]);
-    const float decay = expf(-Ah * softplus_ref(g.a[(size_t)t * g.vh + h] + g.dt_bias[h]));
+    const float beta = sigmoid_ref(bt);
+    const float decay = expf(-Ah * softplus_ref(at + dtb));
     float mem0 = 0.0f, mem1 = 0.0f;
 #pragma unroll
     for (int m = 0; m < 64; m += 2) {
