@@ -642,6 +642,34 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_gqa_attn(AttnArgs a) {
   const size_t sbase = (size_t)tok_slot(a.tok, t) * a.slot_stride + (size_t)kvh * HD;
   const float *kc = a.k_cache + sbase, *vc = a.v_cache + sbase;
 
+  // a block's K rows (A operand) and V values (A operand of O^T); rows past
+  // T read the block's first row and are masked below
+  float4 kv[KQ / 4];
+  float vv[4][NT16];
+  auto load_block = [&](int blk) {
+    const int key0 = blk * 16, km = key0 + n;
+    const float *kr = kc + (size_t)(km < T ? km : key0) * kvrows + 4 * kg;
+#pragma unroll
+    for (int i = 0; i < KQ / 4; i++) kv[i] = *(const float4 *)(kr + 16 * i);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; s2++) {
+      const int key = key0 + 4 * kg + s2;
+      const float *vr = vc + (size_t)(key < T ? key : key0) * kvrows + 4 * n;
+#pragma unroll
+      for (int q4 = 0; q4 < NT16 / 4; q4++) {
+        const float4 v4 = *(const float4 *)(vr + 64 * q4);
+        vv[s2][4 * q4] = v4.x;
+        vv[s2][4 * q4 + 1] = v4.y;
+        vv[s2][4 * q4 + 2] = v4.z;
+        vv[s2][4 * q4 + 3] = v4.w;
+      }
+    }
+  };
+  // the wave's first block issues before the queries' staging barrier (which
+  // waits for every load in flight), so both share one round trip
+  const int bfirst = b0 + wave;
+  if (bfirst < b1) load_block(bfirst);
+
   // the kv head's queries in LDS, [head n][lane group g][KQ + 4] (heads past
   // G are zero); a lane reads its B operands from there, keeping registers
   // for the K and V values of a whole block in flight
@@ -659,29 +687,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_gqa_attn(AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.0f;
   const float scale = 1.f / sqrtf((float)HD);
 
-  for (int b = b0 + wave; b < b1; b += kAttnWaves) {
+  for (int b = bfirst; b < b1; b += kAttnWaves) {
     const int key0 = b * 16;
-    // this block's K rows (A operand) and V values (A operand of O^T); rows
-    // past T read the block's first row and are masked below
-    const int km = key0 + n;
-    const float *kr = kc + (size_t)(km < T ? km : key0) * kvrows + 4 * kg;
-    float4 kv[KQ / 4];
-#pragma unroll
-    for (int i = 0; i < KQ / 4; i++) kv[i] = *(const float4 *)(kr + 16 * i);
-    float vv[4][NT16];
-#pragma unroll
-    for (int s2 = 0; s2 < 4; s2++) {
-      const int key = key0 + 4 * kg + s2;
-      const float *vr = vc + (size_t)(key < T ? key : key0) * kvrows + 4 * n;
-#pragma unroll
-      for (int q4 = 0; q4 < NT16 / 4; q4++) {
-        const float4 v4 = *(const float4 *)(vr + 64 * q4);
-        vv[s2][4 * q4] = v4.x;
-        vv[s2][4 * q4 + 1] = v4.y;
-        vv[s2][4 * q4 + 2] = v4.z;
-        vv[s2][4 * q4 + 3] = v4.w;
-      }
-    }
+    if (b != bfirst) load_block(b);
     // all of the block's K and V loads are in flight before the first MFMA
     asm volatile("" ::: "memory");
     v4f c0 = v4f{0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0;
