@@ -53,7 +53,9 @@ def test_calibrated_beta_fits_exponent(H, E, K):
 
 def test_stage_model_matches_closed_form():
     """Per-stage bytes sum to U*expert + shared + router + gate row + T*H*8
-    and flops to T*(K*6HI + 6HI_sh + 2EH) (the survey's per-token figures)."""
+    and flops to T*(K*6HI + 6HI_sh + 2EH): per token, three H x I products
+    (2 flops a weight) for each of the K routed experts and the shared one,
+    and the E x H router."""
     import bench
     H, E, K, I, Ish, fmt = 4096, 512, 10, 1024, 1024, 3
     for T, U in [(1, 10), (8, 61.5), (512, 512)]:
