@@ -853,7 +853,7 @@ bool q8_ok(const void *q, const float *s, int rows, int cols, int rb) {
   return q && s && rows > 0 && cols > 0 && cols % 16 == 0 && rb >= cols && rb % 16 == 0 && ((uintptr_t)q & 15) == 0;
 }
 
-// The one- and two-token form of k_mix_proj: no activation staging, the
+// The one- to four-token form of k_mix_proj: no activation staging, the
 // columns split over waves.  A workgroup owns RW rows for every wk of its 4
 // waves (wk = 1, 2 or 4 waves along the columns, by the row's chunk count).
 // Per 64-lane chunk of its column share a wave copies 16 bytes a lane of
@@ -1087,7 +1087,7 @@ void launch_proj(ColiCuda *ctx, const ProjArgs &a) {
   switch (tok_bucket(a.B)) {
     case 1: launch_proj_direct<FMT, 1, CONV>(ctx, a); break;
     case 2: launch_proj_direct<FMT, 2, CONV>(ctx, a); break;
-    case 4: launch_proj_nt<FMT, 4, CONV>(ctx, a); break;
+    case 4: launch_proj_direct<FMT, 4, CONV>(ctx, a); break;
     case 8: launch_proj_nt<FMT, 8, CONV>(ctx, a); break;
     default: launch_proj_nt<FMT, 16, CONV>(ctx, a); break;
   }
